@@ -1,0 +1,276 @@
+"""Benchmark of the 4-bit quantized matmul path on one MI355X.
+
+Headline (`value`): the decode GEMV at M = 1, K = 4096, N = 14336 (BASELINE config 1's gate/up shape), MLX affine
+4-bit group 64, bf16 activations ~ N(0, 1), in GB/s of algorithmic bytes (N K 0.5625 + 2 M K + 2 M N) per step. A
+step is one dispatch of the projection through the C ABI (sq_linear_add) over weights already resident in HBM; a
+ring of weight copies larger than the 256 MB Infinity Cache makes every step read HBM. Also reported on the same
+line: the config-1 sweep (M in 1..16 over the four 8B projection shapes), the config-2 prefill GEMM at M = 2048
+(TFLOPS), the config-3 Q4_K shapes, the config-4 MoE block, the dominant kernel's roofline and the CPU baseline (the
+oracle's threaded C implementation of the same quantized matmul on this host's cores, over a bounded sample).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "splash-desktop_amd"))
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+RING_BYTES = 1 << 30
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(m: int, n: int, k: int) -> float:
+    return n * k * 0.5625 + 2 * m * k + 2 * m * n
+
+
+class Projection:
+    """An n x k weight tensor in `copies` ring slots on the device, prepared through the library's repack."""
+
+    def __init__(self, torch, sq, synthetic, fmt: int, n: int, k: int, seed: int, copies: int = 1):
+        rng = np.random.default_rng(seed)
+        self.fmt, self.n, self.k = fmt, n, k
+        p0_bytes, meta_bytes = sq.plane_bytes(fmt, n, k)
+        self.plane0 = [torch.empty(p0_bytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+        self.meta = [torch.empty(meta_bytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+        if fmt == sq.FMT_Q4K:
+            native = synthetic.q4k_native(rng, n, k)
+            src = torch.from_numpy(native.reshape(-1)).cuda()
+            dst = torch.empty(p0_bytes + meta_bytes, dtype=torch.uint8, device="cuda")
+            sq.gguf_repack(src, dst, n, k, fmt, native.shape[1], p0_bytes)
+            for c in range(copies):
+                self.plane0[c].copy_(dst[:p0_bytes])
+                self.meta[c].copy_(dst[p0_bytes:])
+        else:
+            group = {sq.FMT_AF4G32: 32, sq.FMT_AF4G64: 64, sq.FMT_AF4G128: 128}[fmt]
+            _, weight, scales, biases = synthetic.mlx_affine(rng, n, k, group)
+            w = torch.from_numpy(weight.view(np.int32)).cuda()
+            s = torch.from_numpy(scales.view(np.int16)).cuda()
+            b = torch.from_numpy(biases.view(np.int16)).cuda()
+            for c in range(copies):
+                sq.mlx_repack(fmt, n, k, w, s, b, self.plane0[c], self.meta[c])
+        torch.cuda.synchronize()
+
+    def projection(self, sq, copy: int = 0):
+        return sq.projection(sq.segment(self.fmt, self.n, self.k, self.plane0[copy], self.meta[copy]))
+
+    def bytes(self) -> int:
+        return self.plane0[0].numel() + self.meta[0].numel()
+
+
+def time_steps(torch, fn, steps: int, warmup: int) -> float:
+    """Seconds per step: `warmup` untimed steps, then `steps` timed with HIP events on the launching stream."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        fn(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / steps
+
+
+def bench_gemv(torch, sq, synthetic, fmt, m, n, k, steps, warmup, seed=1):
+    one = int(gemv_bytes(0, n, k))
+    copies = max(1, -(-RING_BYTES // one))
+    w = Projection(torch, sq, synthetic, fmt, n, k, seed, copies)
+    projs = [w.projection(sq, c) for c in range(copies)]
+    plan = sq.plan_for(sq.decode_workload(n, k, m), projs[0])
+    scratch = sq.Scratch(plan).struct()
+    x = torch.from_numpy(synthetic.activations(np.random.default_rng(seed + 1), m, k).view(np.int16)).cuda()
+    out = torch.empty((m, n), dtype=torch.int16, device="cuda")
+    handle = sq.stream_handle()
+    bufs = [sq.LinearBuffers(sq.view(x), sq.view(out), sq.view(None), sq.view(None), scratch)]
+
+    def step(i):
+        sq.call("sq_linear_add", handle, sq.byref(bufs[0]), sq.byref(projs[i % copies]), sq.byref(plan), None)
+
+    sec = time_steps(torch, step, steps, warmup)
+    del w
+    return sec, plan
+
+
+def bench_prefill(torch, sq, synthetic, m, n, k, steps, warmup, fmt=None):
+    fmt = sq.FMT_AF4G64 if fmt is None else fmt
+    w = Projection(torch, sq, synthetic, fmt, n, k, 7)
+    proj = w.projection(sq)
+    plan = sq.plan_for(sq.prefill_workload(n, k, m), proj)
+    scratch = sq.Scratch(plan)
+    x = torch.from_numpy(synthetic.activations(np.random.default_rng(8), m, k).view(np.int16)).cuda()
+    out = torch.empty((plan.storage_rows, n), dtype=torch.int16, device="cuda")
+    handle = sq.stream_handle()
+    bufs = sq.LinearBuffers(sq.view(x), sq.view(out), sq.view(None), sq.view(None), scratch.struct())
+
+    def step(i):
+        sq.call("sq_linear_add", handle, sq.byref(bufs), sq.byref(proj), sq.byref(plan), None)
+
+    sec = time_steps(torch, step, steps, warmup)
+    return sec
+
+
+def bench_moe(torch, sq, synthetic, steps, warmup, rows=512, experts=128, top_k=8, hidden=2048, inter=768):
+    fmt = sq.FMT_AF4G64
+    parts = {name: Projection(torch, sq, synthetic, fmt, n, kk, 20 + i)
+             for i, (name, n, kk) in enumerate((("gate", experts * inter, hidden), ("up", experts * inter, hidden),
+                                                ("down", experts * hidden, inter)))}
+    seg = lambda p: sq.segment(fmt, p.n, p.k, p.plane0[0], p.meta[0])
+    slots = torch.arange(experts, dtype=torch.int32, device="cuda")
+    weights = sq.MoeWeights(seg(parts["gate"]), seg(parts["up"]), seg(parts["down"]), sq.view(slots), experts)
+    shape = sq.MoeShape(hidden, experts, top_k, inter, fmt)
+    plan = sq.MoePlan()
+    sq.call("sq_moe_prefill_plan", sq.byref(shape), rows, sq.byref(plan))
+    rng = np.random.default_rng(30)
+    x = torch.from_numpy(synthetic.activations(rng, rows, hidden).view(np.int16)).cuda()
+    scores = torch.from_numpy(synthetic.router_logits(rng, rows, experts)).cuda()
+    out = torch.empty((rows, hidden), dtype=torch.int16, device="cuda")
+    held = []
+    fields = []
+    for name in sq._MOE_WORKSPACE:
+        nbytes = getattr(plan.workspace, name)
+        t = torch.zeros(max(nbytes, 4) // 4 + 1, dtype=torch.int32, device="cuda") if nbytes else None
+        held.append(t)
+        fields.append(sq.view(t))
+    buffers = sq.MoeBuffers(sq.view(x), sq.view(scores), sq.view(None), sq.view(out), 0, sq.MoeScratch(*fields))
+    handle = sq.stream_handle()
+
+    def step(i):
+        sq.call("sq_moe_add", handle, sq.byref(buffers), sq.byref(weights), sq.byref(plan))
+
+    sec = time_steps(torch, step, steps, warmup)
+    weight_bytes = sum(p.bytes() for p in parts.values())
+    return sec, weight_bytes + 2 * rows * hidden * 2, 2 * rows * top_k * 3 * inter * hidden
+
+
+def cpu_baseline(sq, synthetic, m, n, k, budget_s: float):
+    """The oracle's threaded CPU quantized matmul on the headline workload, repeated for about budget_s seconds."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import sq_oracle as oracle
+    rng = np.random.default_rng(1)
+    _, weight, scales, biases = synthetic.mlx_affine(rng, n, k, 64)
+    native = oracle.mlx_native(oracle.FMT_AF4G64, weight, scales, biases, n, k)
+    plane0, meta, _ = oracle.repack(oracle.FMT_AF4G64, native, n, k)
+    x = synthetic.activations(np.random.default_rng(2), m, k)
+    threads = min(os.cpu_count() or 1, 16)
+    total, reps = 0.0, 0
+    while total < budget_s and reps < 1000:
+        _, sec = oracle.cpu_matmul(oracle.FMT_AF4G64, x, plane0, meta, n, threads)
+        total += sec
+        reps += 1
+    return {"value": round(gemv_bytes(m, n, k) / (total / reps) / 1e9, 2), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{reps} runs of the M={m} {k}x{n} af4g64 GEMV ({total:.1f} s); oracle/sq_oracle.c sqo_cpu_matmul",
+            "cpu": _cpu_model()}
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="headline only (no sweep, prefill, MoE or CPU baseline)")
+    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    import splash_q4 as sq
+    from splash_q4 import synthetic
+    torch.cuda.set_device(0)
+    m, n, k = 1, 14336, 4096
+    log(f"headline: decode GEMV M={m} K={k} N={n} af4g64, {args.steps} steps")
+    sec, plan = bench_gemv(torch, sq, synthetic, sq.FMT_AF4G64, m, n, k, args.steps, args.warmup)
+    gbs = gemv_bytes(m, n, k) / sec / 1e9
+    log(f"  {sec * 1e6:.2f} us/step, {gbs:.1f} GB/s, splits {plan.config.splits}")
+    extra = {}
+    if not args.quick:
+        sweep = {}
+        for (kk, nn) in ((4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)):
+            for mm in (1, 2, 4, 8, 16):
+                s, p = bench_gemv(torch, sq, synthetic, sq.FMT_AF4G64, mm, nn, kk, max(50, args.steps // 2), 10)
+                g = gemv_bytes(mm, nn, kk) / s / 1e9
+                sweep[f"K{kk}xN{nn}_M{mm}"] = {"us": round(s * 1e6, 2), "GB/s": round(g, 1),
+                                               "hbm_frac": round(g / HBM_PEAK_GBS, 3), "splits": p.config.splits}
+                log(f"  sweep K{kk} N{nn} M{mm}: {s * 1e6:.2f} us, {g:.0f} GB/s")
+        extra["c1_decode_sweep_af4g64"] = sweep
+        prefill = {}
+        for (kk, nn) in ((4096, 14336), (14336, 4096), (5120, 27648)):
+            s = bench_prefill(torch, sq, synthetic, 2048, nn, kk, 10, 3)
+            tf = 2 * 2048 * nn * kk / s / 1e12
+            prefill[f"M2048_K{kk}xN{nn}"] = {"us": round(s * 1e6, 1), "TFLOPS": round(tf, 1),
+                                             "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 3)}
+            log(f"  prefill K{kk} N{nn}: {s * 1e6:.0f} us, {tf:.0f} TFLOPS")
+        extra["c2_prefill_af4g64"] = prefill
+        q4k = {}
+        for mm in (1, 16):
+            s, p = bench_gemv(torch, sq, synthetic, sq.FMT_Q4K, mm, 27648, 5120, max(50, args.steps // 2), 10)
+            g = gemv_bytes(mm, 27648, 5120) / s / 1e9
+            q4k[f"M{mm}_K5120xN27648"] = {"us": round(s * 1e6, 2), "GB/s": round(g, 1), "hbm_frac": round(g / HBM_PEAK_GBS, 3)}
+            log(f"  q4k M{mm}: {s * 1e6:.2f} us, {g:.0f} GB/s")
+        s = bench_prefill(torch, sq, synthetic, 512, 27648, 5120, 10, 3, fmt=sq.FMT_Q4K)
+        tf = 2 * 512 * 27648 * 5120 / s / 1e12
+        q4k["M512_K5120xN27648"] = {"us": round(s * 1e6, 1), "TFLOPS": round(tf, 1), "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 3)}
+        log(f"  q4k M512: {s * 1e6:.0f} us, {tf:.0f} TFLOPS")
+        extra["c3_q4k"] = q4k
+        s, moe_bytes, moe_flops = bench_moe(torch, sq, synthetic, 50, 5)
+        g = moe_bytes / s / 1e9
+        extra["c4_moe_af4g64"] = {"us": round(s * 1e6, 1), "GB/s": round(g, 1), "hbm_frac": round(g / HBM_PEAK_GBS, 3),
+                                  "TFLOPS": round(moe_flops / s / 1e12, 2)}
+        log(f"  moe: {s * 1e6:.0f} us, {g:.0f} GB/s")
+    result = {
+        "metric": "4-bit GEMV GB/s (% HBM peak) at M=1; prefill q-GEMM TFLOPS at M=2048",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded: bf16 N(0,1) activations, uint4 codes, bf16 |N(0,0.02)| scales, biases -8s)",
+        "config": {"workload": "c1 decode GEMV gate/up shape", "M": m, "K": k, "N": n, "format": "af4g64",
+                   "weights": "4-bit MLX affine group 64", "splits": plan.config.splits,
+                   "weight_ring_copies": max(1, -(-RING_BYTES // int(gemv_bytes(0, n, k))))},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+    result.update(extra)
+    if not args.quick:
+        log("cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(sq, synthetic, m, n, k, args.cpu_budget)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,212 @@
+/*
+ * splash_q4 — MI355X (gfx950) quantized matmul path: bf16 activations x 4-bit group-quantized weights, fp32
+ * accumulation. C ABI over the reference's splash::ops::Linear / splash::ops::MoE call surface.
+ *
+ * Conventions
+ *  - Buffers are device-pointer views {ptr, bytes} (the reference's MetalBuffer views). The caller owns every
+ *    buffer; nothing here allocates device memory.
+ *  - A "graph" is a hipStream_t passed as void*: an add call validates everything, then launches in order on it.
+ *    NULL is the default stream.
+ *  - Every function returns SQ_OK or an error code; nothing is launched when it fails. sq_last_error() holds the
+ *    thread's message for the last failure (the text of the reference's std::invalid_argument where it has one).
+ *  - Format ids, plane layouts and parameter blocks are the reference's (runtime/metal/abi/QuantFormat.h, Gguf.h,
+ *    MoE.h): Q4_K (0) and MLX affine 4-bit in groups of 32, 64 and 128 (25, 26, 27).
+ *  - Split scratch (partials, counters) is reused serially on one stream: counters are zero at allocation and every
+ *    split dispatch returns them to zero; two streams never share one scratch.
+ * Reference interfaces each entry point replaces are named in its comment (paths under the reference checkout).
+ */
+#ifndef SPLASH_Q4_H
+#define SPLASH_Q4_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SQ_OK 0
+#define SQ_INVALID_ARGUMENT 1 /* the reference throws std::invalid_argument */
+#define SQ_RUNTIME_ERROR 2    /* a HIP launch or runtime failure */
+
+#define SQ_FMT_Q4K 0u
+#define SQ_FMT_AF4G32 25u
+#define SQ_FMT_AF4G64 26u
+#define SQ_FMT_AF4G128 27u
+
+/* enum values match the reference's enum class order (Linear.hpp:67-80, Weights.hpp:62) */
+#define SQ_PHASE_PREFILL 0u
+#define SQ_PHASE_DECODE 1u
+#define SQ_EPILOGUE_NONE 0u
+#define SQ_EPILOGUE_RESIDUAL 1u
+#define SQ_EPILOGUE_GATE_UP 2u
+#define SQ_EPILOGUE_UP_WITH_GATE 3u
+#define SQ_TILE_STAGED 0u   /* LinearTile::GgufStaged: the decode tile */
+#define SQ_TILE_PREFILL 1u  /* LinearTile::GgufPrefill */
+#define SQ_TILE_REGISTER 2u /* LinearTile::GgufRegister: refused (Apple9 only) */
+#define SQ_OUTPUT_BF16 0u
+#define SQ_OUTPUT_F32 1u
+#define SQ_MAX_SEGMENTS 3u
+
+typedef struct sq_buffer {
+  void *ptr;
+  uint64_t bytes;
+} sq_buffer;
+
+/* QuantizedSegment, planes layout (runtime/ops/Weights.hpp:79-121). */
+typedef struct sq_segment {
+  sq_buffer plane0, plane1, meta;
+  uint32_t output_size, input_size, column_offset, format_id;
+} sq_segment;
+
+/* Projection (runtime/ops/Weights.hpp:131-188): segments tile the leading output columns in order. */
+typedef struct sq_projection {
+  uint32_t output_size, input_size;
+  uint32_t segment_count;
+  uint32_t destination; /* SQ_OUTPUT_* */
+  sq_segment segments[SQ_MAX_SEGMENTS];
+} sq_projection;
+
+/* LinearWorkload / LinearConfig / LinearPlan (runtime/ops/Linear.hpp:93-214). */
+typedef struct sq_linear_workload {
+  uint32_t output_size, input_size, rows, phase, epilogue;
+} sq_linear_workload;
+typedef struct sq_linear_config {
+  uint32_t tile, splits, spread, one_gate_up_pass, sixteen_rows;
+} sq_linear_config;
+typedef struct sq_linear_plan {
+  sq_linear_workload workload;
+  sq_linear_config config;
+  uint32_t destination;
+  uint32_t storage_rows;
+} sq_linear_plan;
+
+/* LinearScratch / LinearScratchSize / LinearBuffers (runtime/ops/Linear.hpp:125-162,216-226). */
+typedef struct sq_linear_scratch_size {
+  uint64_t input, sums, partials, counters, rotated;
+} sq_linear_scratch_size;
+typedef struct sq_linear_scratch {
+  sq_buffer input, sums, partials, counters, rotated;
+} sq_linear_scratch;
+typedef struct sq_linear_buffers {
+  sq_buffer input, output, residual, gate_scratch;
+  sq_linear_scratch scratch;
+} sq_linear_buffers;
+
+/* DeviceCapabilities, as far as the MI355X policy reads it; compute_units 0 takes 256. */
+typedef struct sq_device {
+  uint32_t compute_units;
+} sq_device;
+
+const char *sq_last_error(void);
+/* Library version string. */
+const char *sq_version(void);
+
+/* ---- planning (host only; no GPU needed) ---- */
+
+/* Linear::plan(LinearWorkload) and Linear::plan(workload, projection, gate) (Linear.cpp:151-164).
+ * projection and gate may be NULL. */
+int sq_linear_plan_for(const sq_device *device, const sq_linear_workload *workload, const sq_projection *projection,
+                       const sq_projection *gate, sq_linear_plan *out);
+/* static Linear::plan(workload, config, destination) (Linear.cpp:155-157). */
+int sq_linear_plan_config(const sq_linear_workload *workload, const sq_linear_config *config, uint32_t destination,
+                          sq_linear_plan *out);
+/* Linear::decodePlan (Linear.cpp:166-169): rows = lanes * 8. */
+int sq_linear_decode_plan(const sq_device *device, const sq_projection *projection, uint32_t lanes, uint32_t epilogue,
+                          const sq_projection *gate, sq_linear_plan *out);
+/* Linear::prefillPlan (Linear.cpp:170-172). */
+int sq_linear_prefill_plan(const sq_device *device, const sq_projection *projection, uint32_t rows, uint32_t epilogue,
+                           sq_linear_plan *out);
+/* LinearPlan::scratchSize and gateScratchBytes (LinearGguf.cpp:432-453, Linear.cpp:123-129). */
+int sq_linear_plan_scratch(const sq_linear_plan *plan, sq_linear_scratch_size *out, uint64_t *gate_scratch_bytes);
+/* Linear::decodeScratchSize / prefillScratchSize (Linear.cpp:174-196). */
+int sq_linear_decode_scratch_size(const sq_device *device, uint32_t output_size, uint32_t input_size,
+                                  sq_linear_scratch_size *out);
+int sq_linear_prefill_scratch_size(const sq_device *device, uint32_t output_size, uint32_t input_size,
+                                   sq_linear_scratch_size *out);
+/* requireSegmentPlanes (LinearGguf.cpp:905-923): SQ_OK when the planes hold every tile of the segment. */
+int sq_require_segment_planes(const sq_segment *segment, const char *what, uint32_t plane_inputs);
+
+/* ---- dispatch ---- */
+
+/* Linear::add (Linear.cpp:203-232; LinearGguf.cpp:579-802): the plan's projection of buffers->input. */
+int sq_linear_add(void *graph, const sq_linear_buffers *buffers, const sq_projection *projection,
+                  const sq_linear_plan *plan, const sq_projection *gate);
+/* Linear::addPrefill / addPrefillResidual / addPrefillUpWithGate (Linear.cpp:234-256). */
+int sq_linear_add_prefill(const sq_device *device, void *graph, sq_buffer input, const sq_projection *projection,
+                          sq_buffer output, uint32_t rows, const sq_linear_scratch *scratch);
+int sq_linear_add_prefill_residual(const sq_device *device, void *graph, sq_buffer input,
+                                   const sq_projection *projection, sq_buffer residual, sq_buffer output,
+                                   uint32_t rows, const sq_linear_scratch *scratch);
+int sq_linear_add_prefill_up_with_gate(const sq_device *device, void *graph, sq_buffer input, const sq_projection *up,
+                                       sq_buffer gate_scratch, sq_buffer output, uint32_t rows,
+                                       const sq_linear_scratch *scratch);
+/* Linear::addPrefillSwiGlu (Linear.cpp:244-250): output = residual + down(silu(gate x) * up x). */
+int sq_linear_add_prefill_swiglu(const sq_device *device, void *graph, const sq_projection *gate,
+                                 const sq_projection *up, const sq_projection *down, sq_buffer normalized,
+                                 sq_buffer gate_scratch, sq_buffer intermediate, const sq_linear_scratch *scratch,
+                                 sq_buffer residual, sq_buffer output, uint32_t rows);
+
+/* ---- weight preparation (load time) ---- */
+
+/* The gguf_repack dispatch (kernels/shared/gguf_repack.metal:232-238; GgufRepack.h:10-18): native rows in src
+ * (src_row_bytes apart) into dst: plane0 at 0, meta at dst_meta (plane1 unused by these formats).
+ * params points at the reference's 24-byte GgufRepackParams {rows, input_size, fmt, src_row_bytes, dst_plane1,
+ * dst_meta}. */
+int sq_gguf_repack(void *graph, sq_buffer src, sq_buffer dst, const void *params);
+/* MLX tensors (mlx.core.quantize affine, bits 4: uint32 codes [rows][K/8], bf16 scales and biases
+ * [rows][K/group]) straight into planes: the loader's native-block build (model/GgufPreparation.cpp:141-193) and
+ * the repack in one dispatch. */
+int sq_mlx_repack(void *graph, uint32_t format_id, uint32_t rows, uint32_t input_size, sq_buffer weight,
+                  sq_buffer scales, sq_buffer biases, sq_buffer plane0, sq_buffer meta);
+/* Every weight of a segment dequantised: fp32 fma(q, s, z) and its fp16 rounding (the staged tiles' weight), [N][K]
+ * each; either output may have a NULL ptr (reference test kernel gguf_test_dequant_<fmt>,
+ * dev/tests/engine/gguf_dequant_test.metal:5-21). */
+int sq_dequant(void *graph, const sq_segment *segment, sq_buffer values_f32, sq_buffer values_f16);
+
+/* ---- MoE (runtime/ops/MoE.hpp:387-423) ---- */
+
+typedef struct sq_moe_shape {
+  uint32_t hidden_size, experts, experts_per_token, expert_intermediate_size;
+  uint32_t expert_format; /* the routed experts' format id */
+} sq_moe_shape;
+typedef struct sq_moe_workspace {
+  uint64_t selected_experts, routing_weights, tile_descriptors, tile_count, grouped_routes, route_rows,
+      grouped_input, expert_intermediate, expert_output;
+} sq_moe_workspace;
+typedef struct sq_moe_plan {
+  sq_moe_shape shape;
+  uint32_t rows, phase, tile_rows, maximum_tiles;
+  sq_moe_workspace workspace;
+} sq_moe_plan;
+/* BlockExpertProjection.routed: `slots` experts' planes in one segment of slots * N rows. */
+typedef struct sq_moe_weights {
+  sq_segment gate, up, down;
+  sq_buffer slot_table; /* uint32 per expert: its slot */
+  uint32_t slots;
+} sq_moe_weights;
+typedef struct sq_moe_scratch {
+  sq_buffer selected_experts, routing_weights, tile_descriptors, tile_count, grouped_routes, route_rows,
+      grouped_input, expert_intermediate, expert_output;
+} sq_moe_scratch;
+/* scores: the router's fp32 [rows][score_stride] logits (the router projection is the caller's). residual may be a
+ * NULL view (zeros). */
+typedef struct sq_moe_buffers {
+  sq_buffer input, scores, residual, output;
+  uint32_t score_stride;
+  sq_moe_scratch scratch;
+} sq_moe_buffers;
+
+/* MoE::prefillPlan / decodePlan (MoE.cpp:204-223; MoePlan, MoE.hpp:349-373): routed experts only. A decode plan
+ * takes any 1..32 rows (the reference's lanes * 8 among them); a prefill plan up to 2048. */
+int sq_moe_prefill_plan(const sq_moe_shape *shape, uint32_t rows, sq_moe_plan *out);
+int sq_moe_decode_plan(const sq_moe_shape *shape, uint32_t rows, sq_moe_plan *out);
+/* MoE::add = addRouting then addRouted (MoE.cpp:225-525). */
+int sq_moe_add(void *graph, const sq_moe_buffers *buffers, const sq_moe_weights *weights, const sq_moe_plan *plan);
+int sq_moe_add_routing(void *graph, const sq_moe_buffers *buffers, const sq_moe_weights *weights,
+                       const sq_moe_plan *plan);
+int sq_moe_add_routed(void *graph, const sq_moe_buffers *buffers, const sq_moe_weights *weights,
+                      const sq_moe_plan *plan);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

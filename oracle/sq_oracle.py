@@ -1,0 +1,177 @@
+"""numpy binding of the CPU oracle (sq_oracle.c) and of the reference's own CPU oracle (_ref/libsqref.so, built
+from the reference checkout by oracle/Makefile when it is present). TEST INFRASTRUCTURE ONLY: imported by tests/,
+by __graft_entry__.smoke() as the checker and by bench.py's cpu_baseline leg, never by the product path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+from ctypes import POINTER, c_double, c_float, c_int, c_uint8, c_uint16, c_uint32, c_uint64
+
+import numpy as np
+
+ORACLE_DIR = pathlib.Path(__file__).resolve().parent
+LIBRARY = ORACLE_DIR / "libsq_oracle.so"
+REFERENCE_LIBRARY = ORACLE_DIR / "_ref" / "libsqref.so"
+
+FMT_Q4K, FMT_AF4G32, FMT_AF4G64, FMT_AF4G128 = 0, 25, 26, 27
+
+_lib = None
+_ref = None
+
+
+def _ptr(a: np.ndarray, ctype):
+    return a.ctypes.data_as(POINTER(ctype)) if a is not None else None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIBRARY.exists():
+            raise RuntimeError(f"{LIBRARY} is not built (make -C oracle)")
+        _lib = ctypes.CDLL(str(LIBRARY))
+        _lib.sqo_projection_bound.restype = c_double
+        _lib.sqo_projection_bound.argtypes = [c_double, c_double, c_double, c_int]
+        _lib.sqo_cpu_matmul.restype = c_double
+        _lib.sqo_group_routes.restype = c_uint32
+        _lib.sqo_tile_index.restype = c_uint64
+        _lib.sqo_f32_to_f16.restype = c_uint16
+        _lib.sqo_f32_to_f16.argtypes = [c_float]
+    return _lib
+
+
+def reference():
+    """The reference's own CPU oracle, or None when it was not built (no reference checkout)."""
+    global _ref
+    if _ref is None and REFERENCE_LIBRARY.exists():
+        _ref = ctypes.CDLL(str(REFERENCE_LIBRARY))
+        _ref.sqref_projection_bound.restype = c_double
+        _ref.sqref_projection_bound.argtypes = [c_double, c_double, c_double, c_int]
+        _ref.sqref_tile_index.restype = c_uint64
+        _ref.sqref_f2h.restype = c_uint16
+        _ref.sqref_f2h.argtypes = [c_float]
+    return _ref
+
+
+def format_info(fmt: int) -> dict:
+    out = (c_uint32 * 7)()
+    if lib().sqo_format_info(fmt, out) != 0:
+        raise ValueError(f"format {fmt} not in the oracle")
+    keys = ("ggml_type", "block_elements", "block_bytes", "plane0_bytes", "plane1_bytes", "meta_bytes", "meta_groups")
+    return dict(zip(keys, list(out)))
+
+
+def row_bytes(fmt: int, k: int) -> int:
+    f = format_info(fmt)
+    return k // f["block_elements"] * f["block_bytes"]
+
+
+def plane_sizes(fmt: int, n: int, k: int) -> tuple[int, int]:
+    f = format_info(fmt)
+    g = k // 32
+    return n * g * f["plane0_bytes"], n * (g // f["meta_groups"]) * f["meta_bytes"]
+
+
+def mlx_native(fmt: int, weight: np.ndarray, scales: np.ndarray, biases: np.ndarray, rows: int, k: int) -> np.ndarray:
+    native = np.zeros(rows * row_bytes(fmt, k), dtype=np.uint8)
+    w = np.ascontiguousarray(weight).view(np.uint8)
+    rc = lib().sqo_mlx_native(fmt, rows, k, _ptr(w, c_uint8), _ptr(np.ascontiguousarray(scales, np.uint16), c_uint16),
+                              _ptr(np.ascontiguousarray(biases, np.uint16), c_uint16), _ptr(native, c_uint8))
+    assert rc == 0
+    return native
+
+
+def repack(fmt: int, native: np.ndarray, n: int, k: int):
+    """(plane0, meta, fp32 values [n][k]) of native rows."""
+    p0, m = plane_sizes(fmt, n, k)
+    plane0, meta = np.zeros(p0, np.uint8), np.zeros(m, np.uint8)
+    values = np.zeros((n, k), np.float32)
+    rc = lib().sqo_repack(fmt, _ptr(np.ascontiguousarray(native, np.uint8), c_uint8), n, k, _ptr(plane0, c_uint8),
+                          _ptr(meta, c_uint8), _ptr(values, c_float))
+    assert rc == 0
+    return plane0, meta, values
+
+
+def unpack(fmt: int, plane0: np.ndarray, meta: np.ndarray, n: int, k: int) -> np.ndarray:
+    native = np.zeros(n * row_bytes(fmt, k), np.uint8)
+    rc = lib().sqo_unpack(fmt, _ptr(plane0, c_uint8), _ptr(meta, c_uint8), n, k, _ptr(native, c_uint8))
+    assert rc == 0
+    return native
+
+
+def plane_values(fmt: int, plane0: np.ndarray, meta: np.ndarray, n: int, k: int):
+    """(fp32 values, fp16 bits) [n][k] decoded from the planes."""
+    values, halves = np.zeros((n, k), np.float32), np.zeros((n, k), np.uint16)
+    rc = lib().sqo_plane_values(fmt, _ptr(plane0, c_uint8), _ptr(meta, c_uint8), n, k, _ptr(values, c_float),
+                                _ptr(halves, c_uint16))
+    assert rc == 0
+    return values, halves
+
+
+def fixture(fmt: int, rows: int, k: int, seed: int) -> np.ndarray:
+    native = np.zeros(rows * row_bytes(fmt, k), np.uint8)
+    assert lib().sqo_fixture(fmt, rows, k, seed, _ptr(native, c_uint8)) == 0
+    return native
+
+
+def project_f64(x_bf16: np.ndarray, w: np.ndarray, threads: int = 8):
+    """(value, magnitude, inputs, largest) fp64 [M][N] of bf16 x [M][K] against fp32 w [N][K]."""
+    m, k = x_bf16.shape
+    n = w.shape[0]
+    outs = [np.zeros((m, n), np.float64) for _ in range(4)]
+    lib().sqo_project_f64(m, n, k, _ptr(np.ascontiguousarray(x_bf16, np.uint16), c_uint16),
+                          _ptr(np.ascontiguousarray(w, np.float32), c_float), *[_ptr(o, c_double) for o in outs],
+                          threads)
+    return tuple(outs)
+
+
+def projection_bound(magnitude, inputs, largest, staged: bool) -> np.ndarray:
+    """projectionBound elementwise (GgufFormatReference.hpp:794-797)."""
+    accumulation = np.ldexp(inputs * largest, -16)
+    return accumulation + np.ldexp(magnitude, -11) + np.ldexp(inputs, -25) if staged else accumulation
+
+
+def project_staged_f32(x_bf16: np.ndarray, halves: np.ndarray, threads: int = 8) -> np.ndarray:
+    m, k = x_bf16.shape
+    n = halves.shape[0]
+    out = np.zeros((m, n), np.float32)
+    lib().sqo_project_staged_f32(m, n, k, _ptr(np.ascontiguousarray(x_bf16, np.uint16), c_uint16),
+                                 _ptr(np.ascontiguousarray(halves, np.uint16), c_uint16), _ptr(out, c_float), threads)
+    return out
+
+
+def cpu_matmul(fmt: int, x_bf16: np.ndarray, plane0: np.ndarray, meta: np.ndarray, n: int, threads: int):
+    """(bf16 bits [M][N], seconds) of the CPU baseline."""
+    m, k = x_bf16.shape
+    out = np.zeros((m, n), np.uint16)
+    secs = lib().sqo_cpu_matmul(fmt, m, n, k, _ptr(np.ascontiguousarray(x_bf16, np.uint16), c_uint16),
+                                _ptr(plane0, c_uint8), _ptr(meta, c_uint8), _ptr(out, c_uint16), threads)
+    return out, secs
+
+
+def route_select(scores: np.ndarray, top_k: int):
+    rows, experts = scores.shape
+    selected = np.zeros((rows, top_k), np.uint32)
+    weights = np.zeros((rows, top_k), np.float64)
+    lib().sqo_route_select(rows, experts, top_k, _ptr(np.ascontiguousarray(scores, np.float32), c_float),
+                           _ptr(selected, c_uint32), _ptr(weights, c_double))
+    return selected, weights
+
+
+def group_routes(selected: np.ndarray, experts: int, tile_rows: int):
+    rows, top_k = selected.shape
+    routes = rows * top_k
+    max_tiles = min(routes // tile_rows + experts, routes)
+    tiles = np.zeros((max_tiles, 2), np.uint32)
+    grouped = np.zeros(max_tiles * tile_rows, np.uint32)
+    route_rows = np.zeros(routes, np.uint32)
+    count = lib().sqo_group_routes(rows, top_k, experts, tile_rows, _ptr(np.ascontiguousarray(selected), c_uint32),
+                                   _ptr(tiles, c_uint32), _ptr(grouped, c_uint32), _ptr(route_rows, c_uint32))
+    return tiles[:count], grouped[:count * tile_rows], route_rows
+
+
+def f16_bits(values: np.ndarray) -> np.ndarray:
+    """The oracle's float32 -> float16 (round to nearest even) of every value."""
+    v = np.ascontiguousarray(values, np.float32).ravel()
+    return np.array([lib().sqo_f32_to_f16(float(x)) for x in v], np.uint16).reshape(np.shape(values))

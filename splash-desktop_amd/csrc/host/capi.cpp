@@ -1,0 +1,336 @@
+// The C ABI (include/splash_q4.h) over the operator layer: translates the POD structs, catches every exception at
+// the boundary into a status code and a thread-local message, and launches on the caller's stream.
+#include "../../../include/splash_q4.h"
+
+#include <cstring>
+#include <string>
+
+#include "../kernels/kernels.hpp"
+#include "moe.hpp"
+#include "ops.hpp"
+
+namespace {
+
+thread_local std::string lastError;
+
+template <class F> int guarded(F &&f) {
+  try {
+    f();
+    lastError.clear();
+    return SQ_OK;
+  } catch (const std::invalid_argument &e) {
+    lastError = e.what();
+    return SQ_INVALID_ARGUMENT;
+  } catch (const std::exception &e) {
+    lastError = e.what();
+    return SQ_RUNTIME_ERROR;
+  } catch (...) {
+    lastError = "unknown error";
+    return SQ_RUNTIME_ERROR;
+  }
+}
+
+using namespace sq::ops;
+
+Buffer buf(const sq_buffer &b) { return {b.ptr, b.bytes}; }
+sq_buffer cbuf(const Buffer &b) { return {b.ptr, b.bytes}; }
+
+template <class T> const T &need(const T *p, const char *what) {
+  if (!p) throw std::invalid_argument(std::string(what) + " is null");
+  return *p;
+}
+
+QuantizedSegment segment(const sq_segment &s) {
+  QuantizedSegment q = QuantizedSegment::planes(s.format_id, s.output_size, s.input_size, buf(s.plane0), buf(s.plane1),
+                                                buf(s.meta));
+  q.columnOffset = s.column_offset;
+  return q;
+}
+
+Projection projection(const sq_projection &p) {
+  if (p.segment_count == 0 || p.segment_count > SQ_MAX_SEGMENTS)
+    throw std::invalid_argument("block projection has no segments");
+  BlockWeights blocks;
+  for (uint32_t i = 0; i < p.segment_count; ++i) blocks.segments.push_back(segment(p.segments[i]));
+  Projection out(p.output_size, p.input_size, std::move(blocks));
+  if (p.destination > SQ_OUTPUT_F32) throw std::invalid_argument("invalid projection destination");
+  out.destination = p.destination == SQ_OUTPUT_F32 ? FloatOutput::Float32 : FloatOutput::BFloat16;
+  return out;
+}
+
+LinearWorkload workload(const sq_linear_workload &w) {
+  if (w.phase > SQ_PHASE_DECODE || w.epilogue > SQ_EPILOGUE_UP_WITH_GATE)
+    throw std::invalid_argument("invalid linear workload");
+  return {{w.output_size, w.input_size}, w.rows, LinearPhase(w.phase), LinearEpilogue(w.epilogue)};
+}
+LinearConfig config(const sq_linear_config &c) {
+  if (c.tile > SQ_TILE_REGISTER) throw std::invalid_argument("invalid linear tile");
+  LinearConfig out;
+  out.tile = LinearTile(c.tile);
+  out.splits = c.splits;
+  out.spread = c.spread != 0;
+  out.oneGateUpPass = c.one_gate_up_pass != 0;
+  out.sixteenRows = c.sixteen_rows != 0;
+  return out;
+}
+sq_linear_plan cplan(const LinearPlan &p) {
+  const LinearWorkload w = p.workload();
+  const LinearConfig c = p.configuration();
+  sq_linear_plan out{};
+  out.workload = {w.matrix.outputSize, w.matrix.inputSize, w.rows, uint32_t(w.phase), uint32_t(w.epilogue)};
+  out.config = {uint32_t(c.tile), c.splits, c.spread, c.oneGateUpPass, c.sixteenRows};
+  out.destination = uint32_t(p.destination());
+  out.storage_rows = p.storageRows();
+  return out;
+}
+LinearPlan plan(const sq_linear_plan &p) {
+  if (p.destination > SQ_OUTPUT_F32) throw std::invalid_argument("invalid plan destination");
+  return Linear::plan(workload(p.workload), config(p.config), FloatOutput(p.destination));
+}
+Linear linear(const sq_device *d) { return Linear(DeviceCapabilities{d ? d->compute_units : 0}); }
+LinearScratch scratch(const sq_linear_scratch *s) {
+  if (!s) return {};
+  return {buf(s->input), buf(s->sums), buf(s->partials), buf(s->counters), buf(s->rotated)};
+}
+sq_linear_scratch_size csize(const LinearScratchSize &s) { return {s.input, s.sums, s.partials, s.counters, s.rotated}; }
+hipStream_t stream(void *graph) { return static_cast<hipStream_t>(graph); }
+void launched(hipError_t e, const char *what) {
+  if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *sq_last_error(void) { return lastError.c_str(); }
+const char *sq_version(void) { return "splash_q4 0.1 gfx950"; }
+
+int sq_linear_plan_for(const sq_device *device, const sq_linear_workload *w, const sq_projection *p,
+                       const sq_projection *gate, sq_linear_plan *out) {
+  return guarded([&] {
+    const Linear l = linear(device);
+    if (!p) {
+      *out = cplan(l.plan(workload(need(w, "workload"))));
+      return;
+    }
+    const Projection proj = projection(*p);
+    if (gate) {
+      const Projection g = projection(*gate);
+      *out = cplan(l.plan(workload(need(w, "workload")), proj, &g));
+    } else {
+      *out = cplan(l.plan(workload(need(w, "workload")), proj));
+    }
+  });
+}
+
+int sq_linear_plan_config(const sq_linear_workload *w, const sq_linear_config *c, uint32_t destination,
+                          sq_linear_plan *out) {
+  return guarded([&] {
+    if (destination > SQ_OUTPUT_F32) throw std::invalid_argument("invalid plan destination");
+    *out = cplan(Linear::plan(workload(need(w, "workload")), config(need(c, "config")), FloatOutput(destination)));
+  });
+}
+
+int sq_linear_decode_plan(const sq_device *device, const sq_projection *p, uint32_t lanes, uint32_t epilogue,
+                          const sq_projection *gate, sq_linear_plan *out) {
+  return guarded([&] {
+    if (epilogue > SQ_EPILOGUE_UP_WITH_GATE) throw std::invalid_argument("invalid epilogue");
+    const Projection proj = projection(need(p, "projection"));
+    if (gate) {
+      const Projection g = projection(*gate);
+      *out = cplan(linear(device).decodePlan(proj, lanes, LinearEpilogue(epilogue), &g));
+    } else {
+      *out = cplan(linear(device).decodePlan(proj, lanes, LinearEpilogue(epilogue)));
+    }
+  });
+}
+
+int sq_linear_prefill_plan(const sq_device *device, const sq_projection *p, uint32_t rows, uint32_t epilogue,
+                           sq_linear_plan *out) {
+  return guarded([&] {
+    if (epilogue > SQ_EPILOGUE_UP_WITH_GATE) throw std::invalid_argument("invalid epilogue");
+    *out = cplan(linear(device).prefillPlan(projection(need(p, "projection")), rows, LinearEpilogue(epilogue)));
+  });
+}
+
+int sq_linear_plan_scratch(const sq_linear_plan *p, sq_linear_scratch_size *out, uint64_t *gate_scratch_bytes) {
+  return guarded([&] {
+    const LinearPlan lp = plan(need(p, "plan"));
+    if (out) *out = csize(lp.scratchSize());
+    if (gate_scratch_bytes) *gate_scratch_bytes = lp.gateScratchBytes();
+  });
+}
+
+int sq_linear_decode_scratch_size(const sq_device *device, uint32_t n, uint32_t k, sq_linear_scratch_size *out) {
+  return guarded([&] { *out = csize(linear(device).decodeScratchSize({n, k})); });
+}
+int sq_linear_prefill_scratch_size(const sq_device *device, uint32_t n, uint32_t k, sq_linear_scratch_size *out) {
+  return guarded([&] { *out = csize(linear(device).prefillScratchSize({n, k})); });
+}
+
+int sq_require_segment_planes(const sq_segment *s, const char *what, uint32_t plane_inputs) {
+  return guarded([&] { requireSegmentPlanes(segment(need(s, "segment")), what ? what : "segment", plane_inputs); });
+}
+
+int sq_linear_add(void *graph, const sq_linear_buffers *b, const sq_projection *p, const sq_linear_plan *lp,
+                  const sq_projection *gate) {
+  return guarded([&] {
+    const sq_linear_buffers &bb = need(b, "buffers");
+    LinearBuffers buffers{buf(bb.input), buf(bb.output), buf(bb.residual), buf(bb.gate_scratch), scratch(&bb.scratch)};
+    const Projection proj = projection(need(p, "projection"));
+    const LinearPlan selected = plan(need(lp, "plan"));
+    const Linear l(DeviceCapabilities{});
+    if (gate) {
+      const Projection g = projection(*gate);
+      l.add(stream(graph), buffers, proj, selected, &g);
+    } else {
+      l.add(stream(graph), buffers, proj, selected);
+    }
+  });
+}
+
+int sq_linear_add_prefill(const sq_device *device, void *graph, sq_buffer input, const sq_projection *p,
+                          sq_buffer output, uint32_t rows, const sq_linear_scratch *s) {
+  return guarded([&] {
+    linear(device).addPrefill(stream(graph), buf(input), projection(need(p, "projection")), buf(output), rows, scratch(s));
+  });
+}
+int sq_linear_add_prefill_residual(const sq_device *device, void *graph, sq_buffer input, const sq_projection *p,
+                                   sq_buffer residual, sq_buffer output, uint32_t rows, const sq_linear_scratch *s) {
+  return guarded([&] {
+    linear(device).addPrefillResidual(stream(graph), buf(input), projection(need(p, "projection")), buf(residual),
+                                      buf(output), rows, scratch(s));
+  });
+}
+int sq_linear_add_prefill_up_with_gate(const sq_device *device, void *graph, sq_buffer input, const sq_projection *up,
+                                       sq_buffer gate_scratch, sq_buffer output, uint32_t rows,
+                                       const sq_linear_scratch *s) {
+  return guarded([&] {
+    linear(device).addPrefillUpWithGate(stream(graph), buf(input), projection(need(up, "projection")),
+                                        buf(gate_scratch), buf(output), rows, scratch(s));
+  });
+}
+int sq_linear_add_prefill_swiglu(const sq_device *device, void *graph, const sq_projection *gate,
+                                 const sq_projection *up, const sq_projection *down, sq_buffer normalized,
+                                 sq_buffer gate_scratch, sq_buffer intermediate, const sq_linear_scratch *s,
+                                 sq_buffer residual, sq_buffer output, uint32_t rows) {
+  return guarded([&] {
+    const Projection g = projection(need(gate, "gate")), u = projection(need(up, "up")), d = projection(need(down, "down"));
+    const PrefillFfnBuffers b{buf(normalized), buf(gate_scratch), buf(intermediate), scratch(s)};
+    linear(device).addPrefillSwiGlu(stream(graph), {&g, &u, &d}, b, buf(residual), buf(output), rows);
+  });
+}
+
+int sq_gguf_repack(void *graph, sq_buffer src, sq_buffer dst, const void *params) {
+  return guarded([&] {
+    SqGgufRepackParams p;
+    std::memcpy(&p, &need(static_cast<const char *>(params), "params"), sizeof p);
+    if (!sq_format_supported(p.fmt)) throw std::invalid_argument("repack takes a format this build runs");
+    const SqQuantFormat f = sq_format(p.fmt);
+    if (!p.rows || p.rows % SQ_TILE_ROWS || !p.input_size || p.input_size % f.block_elements)
+      throw std::invalid_argument("a repack chunk takes whole plane tiles of rows and whole native blocks");
+    const uint64_t rowBytes = uint64_t(p.input_size) / f.block_elements * f.block_bytes;
+    if (p.src_row_bytes < rowBytes) throw std::invalid_argument("repack source rows are shorter than their blocks");
+    const uint64_t groups = p.input_size / 32, units = groups / f.meta_groups;
+    const uint64_t plane0 = uint64_t(p.rows) * groups * f.plane0_bytes, meta = uint64_t(p.rows) * units * f.meta_bytes;
+    if (p.dst_meta < plane0) throw std::invalid_argument("repack meta offset overlaps plane0");
+    requireBytes(buf(src), (uint64_t(p.rows) - 1) * p.src_row_bytes + rowBytes, "repack source");
+    requireBytes(buf(dst), uint64_t(p.dst_meta) + meta, "repack destination");
+    launched(sq::kern::launch_repack(static_cast<const uint8_t *>(src.ptr), static_cast<uint8_t *>(dst.ptr), p,
+                                     stream(graph)),
+             "repack");
+  });
+}
+
+int sq_mlx_repack(void *graph, uint32_t fmt, uint32_t rows, uint32_t k, sq_buffer weight, sq_buffer scales,
+                  sq_buffer biases, sq_buffer plane0, sq_buffer meta) {
+  return guarded([&] {
+    if (!sq_affine_format(fmt)) throw std::invalid_argument("the MLX repack takes a 4-bit MLX affine format");
+    const SqQuantFormat f = sq_format(fmt);
+    if (!rows || rows % SQ_TILE_ROWS || !k || k % f.block_elements)
+      throw std::invalid_argument("an MLX repack takes whole plane tiles of rows and whole groups");
+    const uint64_t groups = k / f.block_elements;
+    requireBytes(buf(weight), uint64_t(rows) * k / 2, "MLX weight");
+    requireBytes(buf(scales), uint64_t(rows) * groups * 2, "MLX scales");
+    requireBytes(buf(biases), uint64_t(rows) * groups * 2, "MLX biases");
+    requireBytes(buf(plane0), uint64_t(rows) * (k / 32) * 16, "plane0");
+    requireBytes(buf(meta), uint64_t(rows) * groups * 4, "meta");
+    launched(sq::kern::launch_mlx_repack(fmt, static_cast<const uint32_t *>(weight.ptr),
+                                         static_cast<const uint16_t *>(scales.ptr),
+                                         static_cast<const uint16_t *>(biases.ptr), rows, k,
+                                         static_cast<uint8_t *>(plane0.ptr), static_cast<uint8_t *>(meta.ptr),
+                                         stream(graph)),
+             "MLX repack");
+  });
+}
+
+int sq_dequant(void *graph, const sq_segment *s, sq_buffer values, sq_buffer halves) {
+  return guarded([&] {
+    const QuantizedSegment q = segment(need(s, "segment"));
+    requireSegmentPlanes(q, "dequant");
+    const uint64_t n = uint64_t(q.outputSize) * q.inputSize;
+    if (values.ptr) requireBytes(buf(values), n * 4, "dequant values");
+    if (halves.ptr) requireBytes(buf(halves), n * 2, "dequant halves");
+    launched(sq::kern::launch_dequant(q.formatId, q.plane0.as<const uint8_t>(), q.meta.as<const uint8_t>(),
+                                      q.outputSize, q.inputSize, static_cast<float *>(values.ptr),
+                                      static_cast<uint16_t *>(halves.ptr), stream(graph)),
+             "dequant");
+  });
+}
+
+}  // extern "C"
+
+// ---- MoE
+
+namespace {
+MoeShape moeShape(const sq_moe_shape &s) {
+  return {s.hidden_size, s.experts, s.experts_per_token, s.expert_intermediate_size, s.expert_format};
+}
+sq_moe_plan cmoe(const MoePlan &p) {
+  sq_moe_plan out{};
+  const MoeShape s = p.shape();
+  out.shape = {s.hiddenSize, s.experts, s.expertsPerToken, s.expertIntermediateSize, s.expertFormat};
+  out.rows = p.rows();
+  out.phase = uint32_t(p.phase());
+  out.tile_rows = p.tileRows();
+  out.maximum_tiles = p.maximumTiles();
+  const MoeWorkspace &w = p.workspace();
+  out.workspace = {w.selectedExperts, w.routingWeights, w.tileDescriptors, w.tileCount, w.groupedRoutes,
+                   w.routeRows, w.groupedInput, w.expertIntermediate, w.expertOutput};
+  return out;
+}
+MoePlan moePlan(const sq_moe_plan &p) {
+  if (p.phase > SQ_PHASE_DECODE) throw std::invalid_argument("invalid MoE phase");
+  return p.phase == SQ_PHASE_DECODE ? MoE::decodeRows(moeShape(p.shape), p.rows) : MoE::prefillPlan(moeShape(p.shape), p.rows);
+}
+MoeWeights moeWeights(const sq_moe_weights &w) {
+  return {segment(w.gate), segment(w.up), segment(w.down), buf(w.slot_table), w.slots};
+}
+MoeBuffers moeBuffers(const sq_moe_buffers &b) {
+  const sq_moe_scratch &s = b.scratch;
+  return {buf(b.input), buf(b.scores), buf(b.residual), buf(b.output), b.score_stride,
+          MoeScratch{buf(s.selected_experts), buf(s.routing_weights), buf(s.tile_descriptors), buf(s.tile_count),
+                     buf(s.grouped_routes), buf(s.route_rows), buf(s.grouped_input), buf(s.expert_intermediate),
+                     buf(s.expert_output)}};
+}
+}  // namespace
+
+extern "C" {
+
+int sq_moe_prefill_plan(const sq_moe_shape *shape, uint32_t rows, sq_moe_plan *out) {
+  return guarded([&] { *out = cmoe(MoE::prefillPlan(moeShape(need(shape, "shape")), rows)); });
+}
+int sq_moe_decode_plan(const sq_moe_shape *shape, uint32_t rows, sq_moe_plan *out) {
+  return guarded([&] { *out = cmoe(MoE::decodeRows(moeShape(need(shape, "shape")), rows)); });
+}
+int sq_moe_add(void *graph, const sq_moe_buffers *b, const sq_moe_weights *w, const sq_moe_plan *p) {
+  return guarded([&] { MoE::add(stream(graph), moeBuffers(need(b, "buffers")), moeWeights(need(w, "weights")), moePlan(need(p, "plan"))); });
+}
+int sq_moe_add_routing(void *graph, const sq_moe_buffers *b, const sq_moe_weights *w, const sq_moe_plan *p) {
+  return guarded([&] { MoE::addRouting(stream(graph), moeBuffers(need(b, "buffers")), moeWeights(need(w, "weights")), moePlan(need(p, "plan"))); });
+}
+int sq_moe_add_routed(void *graph, const sq_moe_buffers *b, const sq_moe_weights *w, const sq_moe_plan *p) {
+  return guarded([&] { MoE::addRouted(stream(graph), moeBuffers(need(b, "buffers")), moeWeights(need(w, "weights")), moePlan(need(p, "plan"))); });
+}
+
+}  // extern "C"

@@ -1,0 +1,382 @@
+// ops::Linear over HIP: plan policy, validation and dispatch of the decode and prefill tiles.
+// Reference: runtime/ops/Linear.cpp:19-258 and runtime/ops/LinearGguf.cpp:396-923.
+#include <cmath>
+
+#include "../kernels/kernels.hpp"
+#include "ops.hpp"
+
+namespace sq::ops {
+
+void requireBytes(const Buffer &buffer, uint64_t bytes, std::string_view what) {
+  if (buffer.sizeBytes() < bytes)
+    throw std::invalid_argument(std::string(what) + " buffer holds " + std::to_string(buffer.sizeBytes()) +
+                                " bytes, needs " + std::to_string(bytes));
+}
+
+namespace {
+
+void requireLaunch(hipError_t e, std::string_view what) {
+  if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Linear.cpp:19-32, with decode workloads of any 1..32 rows: the decode tile runs genuine small-M steps, so a
+// workload of one lane's eight rows (the reference's unit) is one case of it.
+void validate(LinearWorkload w) {
+  if (!w.matrix.outputSize || w.matrix.outputSize % 64 || !w.matrix.inputSize || w.matrix.inputSize % 64)
+    throw std::invalid_argument("invalid linear matrix");
+  if (w.phase == LinearPhase::Prefill) {
+    if (!w.rows || w.rows > SQ_PREFILL_TOKEN_BUDGET || w.epilogue == LinearEpilogue::GateUp)
+      throw std::invalid_argument("invalid linear prefill workload");
+  } else {
+    if (!w.rows || w.rows > SQ_MAXIMUM_DECODE_ROWS || w.epilogue == LinearEpilogue::UpWithGate)
+      throw std::invalid_argument("invalid linear decode workload");
+  }
+}
+
+LinearWorkload decodeWorkload(LinearMatrix matrix, uint32_t lanes, LinearEpilogue epilogue) {
+  if (!lanes || lanes > SQ_MAXIMUM_BATCH_WIDTH) throw std::invalid_argument("invalid linear decode batch width");
+  return {matrix, lanes * SQ_TARGET_VERIFY_ROWS, LinearPhase::Decode, epilogue};
+}
+
+constexpr uint32_t kPrefillTileRows = 128;
+// The decode tile holds at most four lanes of rows; prefill chunks of up to that many rows run it too.
+constexpr uint32_t kMaximumStagedRows = SQ_MAXIMUM_DECODE_ROWS;
+
+// Groups of 32 inputs one scale covers, whose multiples a K partition must take: af4g128's four when the formats
+// are unknown.
+uint32_t scaleGroups(uint32_t format) {
+  return format == SQ_FMT_AF4G128 ? 4 : format == SQ_FMT_AF4G64 ? 2 : 1;
+}
+uint32_t planScaleGroups(const Projection *p, const Projection *gate) {
+  uint32_t unit = 1;
+  bool any = false;
+  for (const Projection *q : {p, gate})
+    if (q)
+      for (const QuantizedSegment &s : q->blocks().segments) unit = std::max(unit, scaleGroups(s.formatId)), any = true;
+  return any ? unit : 4;
+}
+
+// The projection is the plan's matrix and each segment fills whole 64-column tiles of it (LinearGguf.cpp:324-332).
+void requireSegments(const Projection &p, LinearMatrix matrix) {
+  if (p.outputSize != matrix.outputSize || p.inputSize != matrix.inputSize)
+    throw std::invalid_argument("block projection does not match plan");
+  for (const QuantizedSegment &s : p.blocks().segments) {
+    if (s.outputSize % SQ_TILE_COLUMNS) throw std::invalid_argument("block segments do not fill whole column tiles");
+    requireSegmentPlanes(s, "projection");
+  }
+}
+
+char epilogueOf(LinearEpilogue e) { return e == LinearEpilogue::Residual ? 1 : e == LinearEpilogue::UpWithGate ? 2 : 0; }
+
+kern::Segment kernelSegment(const QuantizedSegment &s) {
+  return {s.plane0.as<const uint8_t>(), s.meta.as<const uint8_t>(), s.outputSize / SQ_TILE_COLUMNS, s.columnOffset};
+}
+
+}  // namespace
+
+QuantizedSegment QuantizedSegment::planes(uint32_t formatId, uint32_t outputSize, uint32_t inputSize, Buffer plane0,
+                                          Buffer plane1, Buffer meta) {
+  if (formatId >= SQ_FMT_COUNT) throw std::invalid_argument("unknown GGUF segment format");
+  if (!sq_format_supported(formatId))
+    throw std::invalid_argument("format " + std::to_string(formatId) + " is not one this build runs (Q4_K, af4g32, af4g64, af4g128)");
+  QuantizedSegment s;
+  s.plane0 = plane0;
+  s.plane1 = plane1;
+  s.meta = meta;
+  s.outputSize = outputSize;
+  s.inputSize = inputSize;
+  s.formatId = formatId;
+  return s;
+}
+
+// Weights.hpp:134-143.
+Projection::Projection(uint32_t output, uint32_t input, BlockWeights weights)
+    : outputSize(output), inputSize(input), weights_(std::move(weights)) {
+  if (weights_.segments.empty()) throw std::invalid_argument("block projection has no segments");
+  uint32_t covered = 0;
+  for (const QuantizedSegment &s : weights_.segments) {
+    if (s.inputSize != input || s.columnOffset != covered || !s.outputSize || s.outputSize > output - covered)
+      throw std::invalid_argument("block segments do not tile the projection");
+    covered += s.outputSize;
+  }
+}
+
+// Each plane must reach the unit of the segment's last row and last group (LinearGguf.cpp:905-923).
+void requireSegmentPlanes(const QuantizedSegment &segment, std::string_view what, uint32_t planeInputs) {
+  if (!sq_format_supported(segment.formatId))
+    throw std::invalid_argument(std::string(what) + " takes planes of a format this build runs");
+  const SqQuantFormat f = segment.format();
+  if (!segment.outputSize || !segment.inputSize || segment.inputSize % f.block_elements ||
+      segment.outputSize % SQ_TILE_ROWS)
+    throw std::invalid_argument(std::string(what) + " planes take whole native blocks and plane tiles");
+  const uint32_t groups = segment.inputSize / 32, units = groups / f.meta_groups;
+  const uint32_t rowGroups = (planeInputs ? planeInputs : segment.inputSize) / 32, rowUnits = rowGroups / f.meta_groups;
+  const auto planeBytes = [&](uint32_t blocks, uint32_t rowBlocks, uint32_t unitBytes) {
+    return (sq_tile_index(segment.outputSize - 1, blocks - 1, rowBlocks) + 1) * unitBytes;
+  };
+  const std::string name(what);
+  requireBytes(segment.plane0, planeBytes(groups, rowGroups, f.plane0_bytes), name + " plane0");
+  requireBytes(segment.meta, planeBytes(units, rowUnits, f.meta_bytes), name + " meta");
+}
+
+// ---------------------------------------------------------------- plans
+
+LinearPlan::LinearPlan(LinearWorkload w, LinearConfig config, FloatOutput destination)
+    : workload_(w), config_(config), destination_(destination) {
+  validate(w);
+  if (destination == FloatOutput::Float32 && (w.phase != LinearPhase::Decode || w.epilogue != LinearEpilogue::None))
+    throw std::invalid_argument("an fp32 destination takes a plain decode projection");
+  requireConfiguration();
+}
+
+// LinearGguf.cpp:396-423 for the tiles this build runs.
+void LinearPlan::requireConfiguration() const {
+  const uint32_t k = workload_.matrix.inputSize;
+  const LinearConfig &c = config_;
+  const bool decode = workload_.phase == LinearPhase::Decode;
+  if (c.tile == LinearTile::GgufRegister)
+    throw std::invalid_argument("the register tile is the reference's Apple9 tile; MI355X plans run the decode and prefill tiles");
+  if (c.spread && c.tile != LinearTile::GgufStaged) throw std::invalid_argument("only the staged block tile spreads its walks");
+  if (c.oneGateUpPass && (c.tile != LinearTile::GgufStaged || !decode || workload_.epilogue != LinearEpilogue::GateUp))
+    throw std::invalid_argument("only a staged block gate/up decode runs gate and up in one pass");
+  if (c.sixteenRows && (c.tile != LinearTile::GgufStaged || !decode || workload_.rows != SQ_TARGET_VERIFY_ROWS))
+    throw std::invalid_argument("only a staged one-lane block decode runs the 16-row tile");
+  if (c.tile == LinearTile::GgufPrefill) {
+    if (decode || c.splits != 1) throw std::invalid_argument("invalid block prefill configuration");
+    return;
+  }
+  if (!c.validSplits() || (k / 32) % c.splits) throw std::invalid_argument("staged block splits take whole 32-input groups");
+  if (workload_.rows > kMaximumStagedRows)
+    throw std::invalid_argument("the staged block tile runs prefill chunks of up to 32 rows");
+}
+
+uint32_t LinearPlan::storageRows() const noexcept {
+  if (config_.tile == LinearTile::GgufPrefill)
+    return (workload_.rows + kPrefillTileRows - 1) / kPrefillTileRows * kPrefillTileRows;
+  return config_.sixteenRows ? 16 : workload_.rows;
+}
+
+// Decode tile: [split][row][column] fp32 partials and a counter per 64 destination columns (LinearGguf.cpp:432-453).
+// Prefill tile: the activations in fp16 and one fp32 scale per row, which its prepare dispatch writes.
+LinearScratchSize LinearPlan::scratchSize() const noexcept {
+  const auto [n, k] = workload_.matrix;
+  if (config_.tile == LinearTile::GgufPrefill) {
+    const uint64_t rows = storageRows();
+    return {rows * k * 2, rows * 4, 0, 0, 0};
+  }
+  const uint64_t columns = config_.oneGateUpPass ? 2 * uint64_t{n} : n;
+  const uint32_t tile = config_.oneGateUpPass ? 32 : SQ_TILE_COLUMNS;
+  return config_.splits > 1 ? LinearScratchSize{0, 0, uint64_t{config_.splits} * storageRows() * columns * 4,
+                                                uint64_t{n / tile} * 4, 0}
+                            : LinearScratchSize{};
+}
+
+uint64_t LinearPlan::gateScratchBytes() const noexcept {
+  const bool needed = workload_.epilogue == LinearEpilogue::UpWithGate ||
+                      (workload_.epilogue == LinearEpilogue::GateUp && !config_.oneGateUpPass);
+  return needed ? uint64_t{storageRows()} * workload_.matrix.outputSize * 2 : 0;
+}
+
+// MI355X's split law. A dispatch streams the weights once plus, split, each partition's fp32 partials written and
+// read back; it runs at HBM's rate once the grid holds two of the tile's 256-thread workgroups per compute unit and
+// proportionally slower below that. The split of least modelled time wins, ties to fewer partitions; a partition
+// takes whole scale groups.
+uint32_t Linear::decodeSplits(uint32_t n, uint32_t k, uint32_t rows, uint32_t groupUnit) const noexcept {
+  const uint32_t G = k / 32, tiles = n / SQ_TILE_COLUMNS;
+  const double weights = double(n) * k * 0.5625, saturation = 2.0 * computeUnits_;
+  uint32_t best = 1;
+  double least = INFINITY;
+  for (uint32_t s = 1; s <= LinearConfig::kMaximumSplits && G % (s * groupUnit) == 0; s *= 2) {
+    const double occupancy = std::min(1.0, double(tiles) * s / saturation);
+    const double bytes = weights + (s > 1 ? 8.0 * s * rows * n : 0.0);
+    const double time = bytes / occupancy;
+    if (time < least * 0.97) least = time, best = s;
+  }
+  return best;
+}
+
+LinearConfig Linear::baseline(LinearWorkload w, const Projection *p, const Projection *gate) const {
+  const auto [n, k] = w.matrix;
+  if (w.phase == LinearPhase::Prefill && w.rows > kMaximumStagedRows) return {.tile = LinearTile::GgufPrefill};
+  LinearConfig c{.tile = LinearTile::GgufStaged, .splits = decodeSplits(n, k, w.rows, planScaleGroups(p, gate))};
+  // A gate/up pair of single tensors of one format runs in one dispatch: both walks share the activations' loads.
+  if (w.phase == LinearPhase::Decode && w.epilogue == LinearEpilogue::GateUp && p && gate &&
+      p->blocks().segments.size() == 1 && gate->blocks().segments.size() == 1 &&
+      p->blocks().segments.front().formatId == gate->blocks().segments.front().formatId)
+    c.oneGateUpPass = true;
+  return c;
+}
+
+LinearPlan Linear::plan(LinearWorkload workload) const {
+  validate(workload);
+  return LinearPlan(workload, baseline(workload, nullptr, nullptr));
+}
+LinearPlan Linear::plan(LinearWorkload workload, LinearConfig config, FloatOutput destination) {
+  return LinearPlan(workload, config, destination);
+}
+LinearPlan Linear::plan(LinearWorkload w, const Projection &p, const Projection *gate) const {
+  validate(w);
+  return LinearPlan(w, baseline(w, &p, gate), p.destination);
+}
+LinearPlan Linear::decodePlan(const Projection &p, uint32_t lanes, LinearEpilogue epilogue, const Projection *gate) const {
+  return plan(decodeWorkload({p.outputSize, p.inputSize}, lanes, epilogue), p, gate);
+}
+LinearPlan Linear::prefillPlan(const Projection &p, uint32_t rows, LinearEpilogue epilogue) const {
+  return plan({{p.outputSize, p.inputSize}, rows, LinearPhase::Prefill, epilogue}, p);
+}
+uint32_t Linear::decodeStorageRows(uint32_t rows, ProjectionShape shape) const {
+  const LinearWorkload w{{shape.outputSize, shape.inputSize}, rows, LinearPhase::Decode, LinearEpilogue::None};
+  validate(w);
+  return LinearPlan(w, baseline(w, nullptr, nullptr)).storageRows();
+}
+LinearScratchSize Linear::decodeScratchSize(ProjectionShape shape) const {
+  LinearScratchSize bound;
+  for (uint32_t rows = 1; rows <= SQ_MAXIMUM_DECODE_ROWS; ++rows)
+    for (const auto e : {LinearEpilogue::None, LinearEpilogue::Residual, LinearEpilogue::GateUp}) {
+      const LinearWorkload w{{shape.outputSize, shape.inputSize}, rows, LinearPhase::Decode, e};
+      bound.include(LinearPlan(w, baseline(w, nullptr, nullptr)).scratchSize());
+    }
+  return bound;
+}
+LinearScratchSize Linear::prefillScratchSize(ProjectionShape shape) const {
+  LinearScratchSize bound;
+  for (const uint32_t rows : {1u, 2u, 4u, 8u, 16u, 32u, SQ_PREFILL_TOKEN_BUDGET})
+    for (const auto e : {LinearEpilogue::None, LinearEpilogue::Residual, LinearEpilogue::UpWithGate})
+      bound.include(plan({{shape.outputSize, shape.inputSize}, rows, LinearPhase::Prefill, e}).scratchSize());
+  for (uint32_t rows = 3; rows <= kMaximumStagedRows; ++rows)
+    bound.include(plan({{shape.outputSize, shape.inputSize}, rows, LinearPhase::Prefill, LinearEpilogue::None}).scratchSize());
+  return bound;
+}
+
+// ---------------------------------------------------------------- dispatch
+
+void Linear::add(hipStream_t graph, LinearBuffers b, const Projection &p, const LinearPlan &selected,
+                 const Projection *gate) const {
+  const LinearWorkload w = selected.workload();
+  const auto [n, k] = w.matrix;
+  if ((w.epilogue == LinearEpilogue::GateUp) != (gate != nullptr))
+    throw std::invalid_argument("a gate/up plan takes a gate projection and no other plan does");
+  const uint64_t rows = selected.storageRows();
+  requireBytes(b.input, rows * k * 2, "projection input");
+  requireBytes(b.output, rows * n * elementBytes(selected.destination()), "projection output");
+  if (w.epilogue == LinearEpilogue::Residual) requireBytes(b.residual, rows * n * 2, "projection residual");
+  requireBytes(b.gateScratch, selected.gateScratchBytes(), "projection gate scratch");
+  const LinearScratchSize scratch = selected.scratchSize();
+  requireBytes(b.scratch.input, scratch.input, "projection scratch table");
+  requireBytes(b.scratch.sums, scratch.sums, "projection scratch sums");
+  requireBytes(b.scratch.partials, scratch.partials, "projection partials");
+  requireBytes(b.scratch.counters, scratch.counters, "projection counters");
+  requireSegments(p, w.matrix);
+  if (gate) requireSegments(*gate, w.matrix);
+  const std::vector<QuantizedSegment> &segments = p.blocks().segments;
+  if (selected.destination() == FloatOutput::Float32 && segments.size() > 1)
+    throw std::invalid_argument("an fp32 destination takes a single-tensor block projection");
+  const LinearConfig config = selected.configuration();
+  const uint32_t groupUnit = planScaleGroups(&p, gate);
+  if (config.tile == LinearTile::GgufStaged && (k / 32) % (config.splits * groupUnit))
+    throw std::invalid_argument("a K partition of the staged tile takes whole scale groups of the projection's format");
+  if (w.epilogue == LinearEpilogue::GateUp) {
+    if (segments.size() != 1 || gate->blocks().segments.size() != 1)
+      throw std::invalid_argument("block gate/up takes single tensors");
+  }
+  // Segments run one dispatch per format, at most three each (fused projections: q|k|v).
+  std::vector<std::vector<const QuantizedSegment *>> byFormat;
+  for (const QuantizedSegment &s : segments) {
+    auto it = std::find_if(byFormat.begin(), byFormat.end(),
+                           [&](const auto &g) { return g.front()->formatId == s.formatId; });
+    if (it == byFormat.end()) byFormat.push_back({&s});
+    else it->push_back(&s);
+  }
+  for (const auto &group : byFormat)
+    if (group.size() > 3) throw std::invalid_argument("a block projection takes at most three segments per format");
+  if (segments.size() > 1 && w.epilogue != LinearEpilogue::None)
+    throw std::invalid_argument("a fused block projection takes at most three segments and no epilogue");
+
+  if (config.tile == LinearTile::GgufPrefill) {
+    requireLaunch(kern::launch_prefill_prepare(b.input.as<const uint16_t>(), w.rows, k, b.scratch.input.as<uint16_t>(),
+                                               b.scratch.sums.as<float>(), graph),
+                  "prefill prepare");
+    for (const auto &group : byFormat) {
+      kern::PrefillArgs a{};
+      a.half_input = b.scratch.input.as<const uint16_t>();
+      a.row_scale = b.scratch.sums.as<const float>();
+      a.segments = (uint32_t)group.size();
+      for (size_t i = 0; i < group.size(); ++i) a.seg[i] = kernelSegment(*group[i]);
+      a.output = b.output.as<uint16_t>();
+      a.aux = w.epilogue == LinearEpilogue::Residual ? b.residual.as<const uint16_t>()
+                                                     : b.gateScratch.as<const uint16_t>();
+      a.K = k;
+      a.rows = w.rows;
+      a.out_stride = n;
+      requireLaunch(kern::launch_prefill(group.front()->formatId, epilogueOf(w.epilogue), a, graph), "prefill tile");
+    }
+    return;
+  }
+  const auto decode = [&](const std::vector<const QuantizedSegment *> &group, uint32_t epilogue, Buffer output,
+                          Buffer aux, bool f32) {
+    kern::DecodeArgs a{};
+    a.input = b.input.as<const uint16_t>();
+    a.segments = (uint32_t)group.size();
+    for (size_t i = 0; i < group.size(); ++i) a.seg[i] = kernelSegment(*group[i]);
+    a.output = output.ptr;
+    a.aux = aux.as<const uint16_t>();
+    a.partials = b.scratch.partials.as<float>();
+    a.counters = b.scratch.counters.as<uint32_t>();
+    a.K = k;
+    a.rows = w.rows;
+    a.splits = config.splits;
+    a.out_stride = n;
+    requireLaunch(kern::launch_decode(group.front()->formatId, epilogue, f32, a, graph), "decode tile");
+  };
+  if (w.epilogue == LinearEpilogue::GateUp && config.oneGateUpPass) {
+    const QuantizedSegment &g = gate->blocks().segments.front(), &u = segments.front();
+    if (g.formatId != u.formatId || g.columnOffset != u.columnOffset)
+      throw std::invalid_argument("a one-pass block gate/up takes single tensors of one format");
+    kern::GateUpArgs a{};
+    a.input = b.input.as<const uint16_t>();
+    a.gate = kernelSegment(g);
+    a.up = kernelSegment(u);
+    a.output = b.output.as<uint16_t>();
+    a.partials = b.scratch.partials.as<float>();
+    a.counters = b.scratch.counters.as<uint32_t>();
+    a.K = k;
+    a.rows = w.rows;
+    a.splits = config.splits;
+    a.out_stride = n;
+    requireLaunch(kern::launch_decode_gate_up(u.formatId, a, graph), "gate/up decode tile");
+    return;
+  }
+  if (w.epilogue == LinearEpilogue::GateUp) {
+    // A gate pass into the gate scratch, then the up pass whose epilogue multiplies silu(gate) into bf16(up).
+    decode({&gate->blocks().segments.front()}, kern::EpNone, b.gateScratch, {}, false);
+    decode({&segments.front()}, kern::EpUpWithGate, b.output, b.gateScratch, false);
+    return;
+  }
+  const Buffer aux = w.epilogue == LinearEpilogue::Residual ? b.residual : b.gateScratch;
+  for (const auto &group : byFormat)
+    decode(group, epilogueOf(w.epilogue), b.output, aux, selected.destination() == FloatOutput::Float32);
+}
+
+void Linear::addPrefill(hipStream_t graph, Buffer input, const Projection &p, Buffer output, uint32_t rows,
+                        LinearScratch scratch) const {
+  add(graph, {.input = input, .output = output, .scratch = scratch}, p, prefillPlan(p, rows, LinearEpilogue::None));
+}
+void Linear::addPrefillResidual(hipStream_t graph, Buffer input, const Projection &p, Buffer residual, Buffer output,
+                                uint32_t rows, LinearScratch scratch) const {
+  add(graph, {.input = input, .output = output, .residual = residual, .scratch = scratch}, p,
+      prefillPlan(p, rows, LinearEpilogue::Residual));
+}
+void Linear::addPrefillUpWithGate(hipStream_t graph, Buffer input, const Projection &up, Buffer gateScratch,
+                                  Buffer output, uint32_t rows, LinearScratch scratch) const {
+  add(graph, {.input = input, .output = output, .gateScratch = gateScratch, .scratch = scratch}, up,
+      prefillPlan(up, rows, LinearEpilogue::UpWithGate));
+}
+// Linear.cpp:244-250.
+void Linear::addPrefillSwiGlu(hipStream_t graph, const SwiGluProjections &ffn, const PrefillFfnBuffers &b,
+                              Buffer residual, Buffer output, uint32_t rows) const {
+  addPrefill(graph, b.normalized, *ffn.gate, b.gateScratch, rows, b.scratch);
+  addPrefillUpWithGate(graph, b.normalized, *ffn.up, b.gateScratch, b.intermediate, rows, b.scratch);
+  addPrefillResidual(graph, b.intermediate, *ffn.down, residual, output, rows, b.scratch);
+}
+
+}  // namespace sq::ops

@@ -1,0 +1,147 @@
+// ops::MoE dispatch: routing (top-k select, grouping into expert tiles), then the routed work (gate/up pass with the
+// gather folded in, down pass, combine). Reference: runtime/ops/MoE.cpp:27-84,116-192,445-543.
+#include "moe.hpp"
+
+#include "../kernels/kernels.hpp"
+
+namespace sq::ops {
+namespace {
+
+void launched(hipError_t e, const char *what) {
+  if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// MoE.cpp:64-84 for routed experts: the grouped rows' intermediates and outputs; the gather reads the input rows
+// straight from the routes, so the grouped input holds nothing.
+MoeWorkspace workspaceFor(const MoeShape &shape, uint32_t rows, uint32_t tileRows) {
+  if (!shape.valid()) throw std::invalid_argument("invalid MoE workspace shape");
+  const uint64_t routes = uint64_t{rows} * shape.routesPerToken();
+  const uint32_t tiles = moeMaximumTiles(rows, shape, tileRows);
+  const uint64_t groupedRows = uint64_t{tiles} * tileRows;
+  const uint32_t widest = std::max(shape.hiddenSize, shape.expertIntermediateSize);
+  return {routes * 4, routes * 4, uint64_t{tiles} * sizeof(SqMoeTileDescriptor), sizeof(SqMoeTileCount),
+          groupedRows * 4, routes * 4, 0, groupedRows * shape.expertIntermediateSize * 2, groupedRows * widest * 2};
+}
+
+// A routed projection: `slots` experts of n rows of k inputs in the segment's format (MoE.cpp:27-62).
+void requireExperts(const QuantizedSegment &s, uint32_t slots, uint32_t n, uint32_t k, uint32_t format,
+                    const char *name) {
+  if (s.formatId != format || s.outputSize != uint64_t{slots} * n || s.inputSize != k)
+    throw std::invalid_argument(std::string("MoE expert ") + name + " does not match the plan");
+  requireSegmentPlanes(s, std::string("MoE expert ") + name);
+}
+
+void validate(const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
+  const MoeShape s = plan.shape();
+  const uint32_t h = s.hiddenSize, in = s.expertIntermediateSize;
+  if (!w.slots) throw std::invalid_argument("MoE routed experts have no slots");
+  requireBytes(w.slotTable, uint64_t{s.experts} * 4, "MoE slot table");
+  requireExperts(w.gate, w.slots, in, h, s.expertFormat, "gate");
+  requireExperts(w.up, w.slots, in, h, s.expertFormat, "up");
+  requireExperts(w.down, w.slots, h, in, s.expertFormat, "down");
+  const uint64_t hiddenRows = uint64_t{plan.rows()} * h * 2;
+  requireBytes(b.input, hiddenRows, "MoE input");
+  if (b.residual) requireBytes(b.residual, hiddenRows, "MoE residual");
+  requireBytes(b.output, hiddenRows, "MoE output");
+  const uint32_t stride = b.scoreStride ? b.scoreStride : s.experts;
+  if (stride < s.experts) throw std::invalid_argument("MoE score rows are narrower than the experts");
+  requireBytes(b.scores, rowBytes(plan.rows(), stride, s.experts, 4), "MoE scores");
+  const MoeWorkspace &need = plan.workspace();
+  const MoeScratch &sc = b.scratch;
+  requireBytes(sc.selectedExperts, need.selectedExperts, "MoE selected experts");
+  requireBytes(sc.routingWeights, need.routingWeights, "MoE routing weights");
+  requireBytes(sc.tileDescriptors, need.tileDescriptors, "MoE tile descriptors");
+  requireBytes(sc.tileCount, need.tileCount, "MoE tile count");
+  requireBytes(sc.groupedRoutes, need.groupedRoutes, "MoE grouped routes");
+  requireBytes(sc.routeRows, need.routeRows, "MoE route rows");
+  requireBytes(sc.expertIntermediate, need.expertIntermediate, "MoE expert intermediate");
+  requireBytes(sc.expertOutput, need.expertOutput, "MoE expert output");
+}
+
+}  // namespace
+
+MoePlan::MoePlan(MoeShape shape, uint32_t rows, uint32_t tileRows, MoePhase phase)
+    : shape_(shape), rows_(rows), tileRows_(tileRows), phase_(phase) {
+  if (!rows || rows > SQ_PREFILL_TOKEN_BUDGET || (phase == MoePhase::Decode && rows > SQ_MAXIMUM_DECODE_ROWS))
+    throw std::invalid_argument("invalid MoE rows");
+  workspace_ = workspaceFor(shape, rows, tileRows);
+  maximumTiles_ = moeMaximumTiles(rows, shape, tileRows);
+}
+
+MoePlan MoE::prefillPlan(MoeShape shape, uint32_t rows) {
+  const uint32_t tile = uint64_t{rows} * shape.expertsPerToken <= shape.experts ? 8 : 32;
+  return MoePlan(shape, rows, tile, MoePhase::Prefill);
+}
+MoePlan MoE::decodePlan(MoeShape shape, uint32_t lanes) {
+  if (!lanes || lanes > SQ_MAXIMUM_BATCH_WIDTH) throw std::invalid_argument("invalid MoE decode batch width");
+  return MoePlan(shape, lanes * SQ_TARGET_VERIFY_ROWS, 8, MoePhase::Decode);
+}
+MoePlan MoE::decodeRows(MoeShape shape, uint32_t rows) { return MoePlan(shape, rows, 8, MoePhase::Decode); }
+
+void MoE::add(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
+  validate(b, w, plan);
+  addRouting(graph, b, w, plan);
+  addRouted(graph, b, w, plan);
+}
+
+void MoE::addRouting(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
+  validate(b, w, plan);
+  const MoeShape s = plan.shape();
+  const MoeScratch &sc = b.scratch;
+  const SqMoeRouteParams route{plan.rows(), s.hiddenSize, s.experts, s.expertsPerToken};
+  launched(kern::launch_moe_route_select(b.scores.as<const float>(), b.scoreStride ? b.scoreStride : s.experts,
+                                         sc.selectedExperts.as<uint32_t>(), sc.routingWeights.as<float>(), route, graph),
+           "MoE route select");
+  const SqMoeGroupParams group{plan.rows(), s.expertsPerToken, plan.tileRows(), s.experts,
+                               s.expertIntermediateSize / SQ_TILE_COLUMNS, s.hiddenSize / SQ_TILE_COLUMNS,
+                               SQ_TARGET_VERIFY_ROWS, 0};
+  launched(kern::launch_moe_group(sc.selectedExperts.as<const uint32_t>(), sc.tileDescriptors.as<SqMoeTileDescriptor>(),
+                                  sc.tileCount.as<SqMoeTileCount>(), sc.groupedRoutes.as<uint32_t>(),
+                                  sc.routeRows.as<uint32_t>(), plan.maximumTiles(), group, graph),
+           "MoE grouping");
+}
+
+void MoE::addRouted(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
+  validate(b, w, plan);
+  const MoeShape s = plan.shape();
+  const MoeScratch &sc = b.scratch;
+  kern::MoeExpertArgs a{};
+  a.tiles = sc.tileDescriptors.as<const SqMoeTileDescriptor>();
+  a.tile_count = sc.tileCount.as<const SqMoeTileCount>();
+  a.slots = w.slotTable.as<const uint32_t>();
+  a.tile_rows = plan.tileRows();
+  a.max_tiles = plan.maximumTiles();
+  a.fmt = s.expertFormat;
+  a.routes = sc.groupedRoutes.as<const uint32_t>();
+  a.top_k = s.expertsPerToken;
+  // Gate and up in one pass over the routed rows of the input: intermediate = bf16(bf16(up) silu(bf16(gate))).
+  a.input = b.input.as<const uint16_t>();
+  a.plane0[0] = w.gate.plane0.as<const uint8_t>();
+  a.meta[0] = w.gate.meta.as<const uint8_t>();
+  a.plane0[1] = w.up.plane0.as<const uint8_t>();
+  a.meta[1] = w.up.meta.as<const uint8_t>();
+  a.output = sc.expertIntermediate.as<uint16_t>();
+  a.K = s.hiddenSize;
+  a.output_size = s.expertIntermediateSize;
+  a.gate_up = 1;
+  launched(kern::launch_moe_expert(a, graph), "MoE gate/up pass");
+  // Down over the grouped intermediate rows.
+  a.input = sc.expertIntermediate.as<const uint16_t>();
+  a.routes = nullptr;
+  a.plane0[0] = w.down.plane0.as<const uint8_t>();
+  a.meta[0] = w.down.meta.as<const uint8_t>();
+  a.plane0[1] = nullptr;
+  a.meta[1] = nullptr;
+  a.output = sc.expertOutput.as<uint16_t>();
+  a.K = s.expertIntermediateSize;
+  a.output_size = s.hiddenSize;
+  a.gate_up = 0;
+  launched(kern::launch_moe_expert(a, graph), "MoE down pass");
+  const SqMoeCombineParams combine{plan.rows(), s.hiddenSize, s.routesPerToken()};
+  launched(kern::launch_moe_combine(sc.expertOutput.as<const uint16_t>(), sc.routeRows.as<const uint32_t>(),
+                                    sc.routingWeights.as<const float>(), b.residual.as<const uint16_t>(),
+                                    b.output.as<uint16_t>(), combine, graph),
+           "MoE combine");
+}
+
+}  // namespace sq::ops

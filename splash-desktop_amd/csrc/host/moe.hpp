@@ -1,0 +1,78 @@
+// ops::MoE over HIP: the routed experts' grouped gather-GEMM (reference: runtime/ops/MoE.hpp:19-423 and
+// runtime/ops/MoE.cpp:27-543). The router projection is the caller's: a step starts from its fp32 scores.
+#pragma once
+#include "ops.hpp"
+
+namespace sq::ops {
+
+// MoeShape (MoE.hpp:54-102) for a block of routed experts only: no shared expert slices.
+struct MoeShape {
+  uint32_t hiddenSize = 0, experts = 0, expertsPerToken = 0, expertIntermediateSize = 0;
+  uint32_t expertFormat = SQ_FMT_AF4G64;
+  [[nodiscard]] bool valid() const noexcept {
+    return hiddenSize && hiddenSize % 256 == 0 && experts && experts <= SQ_MOE_WIDE_EXPERT_SLOTS && expertsPerToken &&
+           expertsPerToken <= experts && expertsPerToken <= 64 && expertIntermediateSize &&
+           expertIntermediateSize % 64 == 0 && sq_format_supported(expertFormat);
+  }
+  [[nodiscard]] uint32_t routesPerToken() const noexcept { return expertsPerToken; }
+};
+
+enum class MoePhase : uint8_t { Prefill, Decode };
+
+// moeMaximumTiles (MoE.hpp:200-205) without shared slices.
+[[nodiscard]] constexpr uint32_t moeMaximumTiles(uint32_t rows, const MoeShape &shape, uint32_t tileRows) noexcept {
+  const uint32_t routed = rows * shape.expertsPerToken;
+  return std::min(routed / tileRows + shape.experts, routed);
+}
+
+struct MoeWorkspace {
+  uint64_t selectedExperts = 0, routingWeights = 0, tileDescriptors = 0, tileCount = 0, groupedRoutes = 0,
+           routeRows = 0, groupedInput = 0, expertIntermediate = 0, expertOutput = 0;
+};
+struct MoeScratch {
+  Buffer selectedExperts, routingWeights, tileDescriptors, tileCount, groupedRoutes, routeRows, groupedInput,
+      expertIntermediate, expertOutput;
+};
+// The routed experts' planes: `slots` experts per projection, expert e's rows from slotTable[e] * N on.
+struct MoeWeights {
+  QuantizedSegment gate, up, down;
+  Buffer slotTable;
+  uint32_t slots = 0;
+};
+struct MoeBuffers {
+  Buffer input, scores, residual, output;
+  uint32_t scoreStride = 0;   // floats per row of scores; 0 takes the expert count
+  MoeScratch scratch;
+};
+
+class MoePlan {
+public:
+  [[nodiscard]] MoeShape shape() const noexcept { return shape_; }
+  [[nodiscard]] uint32_t rows() const noexcept { return rows_; }
+  [[nodiscard]] MoePhase phase() const noexcept { return phase_; }
+  [[nodiscard]] uint32_t tileRows() const noexcept { return tileRows_; }
+  [[nodiscard]] uint32_t maximumTiles() const noexcept { return maximumTiles_; }
+  [[nodiscard]] const MoeWorkspace &workspace() const noexcept { return workspace_; }
+  MoePlan(MoeShape shape, uint32_t rows, uint32_t tileRows, MoePhase phase);
+
+private:
+  MoeShape shape_;
+  uint32_t rows_, tileRows_;
+  MoePhase phase_;
+  uint32_t maximumTiles_;
+  MoeWorkspace workspace_;
+};
+
+struct MoE {
+  // Tiles of 8 rows while a chunk's routes average at most one row per expert, else 32 (moeGgufPrefillTile,
+  // MoE.hpp:321-330).
+  [[nodiscard]] static MoePlan prefillPlan(MoeShape shape, uint32_t rows);
+  // Decode steps of `lanes` lanes of 8 rows (MoE.cpp decodePlan) and, here, of any rows up to 32.
+  [[nodiscard]] static MoePlan decodePlan(MoeShape shape, uint32_t lanes);
+  [[nodiscard]] static MoePlan decodeRows(MoeShape shape, uint32_t rows);
+  static void add(hipStream_t graph, const MoeBuffers &buffers, const MoeWeights &weights, const MoePlan &plan);
+  static void addRouting(hipStream_t graph, const MoeBuffers &buffers, const MoeWeights &weights, const MoePlan &plan);
+  static void addRouted(hipStream_t graph, const MoeBuffers &buffers, const MoeWeights &weights, const MoePlan &plan);
+};
+
+}  // namespace sq::ops

@@ -1,0 +1,107 @@
+// Device helpers shared by the gfx950 kernels: vector types, the bf16 MFMA, the exact code operands, bf16/fp16
+// conversions and the per-format coefficient decode.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../abi.h"
+
+namespace sq::kern {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+
+// D = A B + C on a 16x16x32 bf16 tile. Lane l holds A[l % 16][8 (l / 16) + i], B[8 (l / 16) + i][l % 16] and
+// D[4 (l / 16) + i][l % 16] (i = 0..7, 0..7, 0..3).
+__device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                  0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                 0);
+}
+
+// The eight codes of plane word w as exact bf16 operands 128 + q, in chunk-element order: pair p (bits 4p and
+// 16 + 4p) gives operands 2p and 2p + 1. bf16 0x4300 is 128 with unit spacing, so or-ing a code into its mantissa
+// makes 128 + code exactly.
+__device__ __forceinline__ u32x4 code_operands(uint32_t w) {
+  const uint32_t m = 0x000F000Fu, o = 0x43004300u;
+  return u32x4{(w & m) | o, ((w >> 4) & m) | o, ((w >> 8) & m) | o, ((w >> 12) & m) | o};
+}
+// bf16 1.0 in every operand.
+__device__ __forceinline__ u32x4 ones_operand() { return u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u}; }
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+__device__ __forceinline__ uint16_t f32_to_bf16(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
+
+// silu(g) = g / (1 + 2^(-g log2 e)), the reference's form of it (activation.h:8-13).
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + exp2f(-1.44269504089f * g)); }
+
+template <uint32_t EP>
+__device__ __forceinline__ float epilogue(float v, const uint16_t *aux, size_t at) {
+  if constexpr (EP == 1) v += bf16_to_f32(aux[at]);
+  if constexpr (EP == 2) v = bf16_to_f32(f32_to_bf16(v)) * silu(bf16_to_f32(aux[at]));
+  return v;
+}
+
+// Per-format traits. SG: groups of 32 one scale covers; UNIT: groups of 32 per meta unit; META: meta unit bytes.
+template <uint32_t FMT> struct Fmt;
+template <> struct Fmt<SQ_FMT_AF4G32> { static constexpr int SG = 1, UNIT = 1, META = 4; };
+template <> struct Fmt<SQ_FMT_AF4G64> { static constexpr int SG = 2, UNIT = 2, META = 4; };
+template <> struct Fmt<SQ_FMT_AF4G128> { static constexpr int SG = 4, UNIT = 4, META = 4; };
+template <> struct Fmt<SQ_FMT_Q4K> { static constexpr int SG = 1, UNIT = 8, META = 16; };
+
+// The meta words one column needs for scale group `sg` (the meta unit that holds it): af4 the (s, z) word, Q4_K
+// the 16-byte super-block header.
+struct MetaWords {
+  uint32_t w[4];
+};
+template <uint32_t FMT>
+__device__ __forceinline__ MetaWords load_meta(const uint8_t *unit_row) {
+  MetaWords m;
+  if constexpr (Fmt<FMT>::META == 4) {
+    m.w[0] = __builtin_nontemporal_load((const uint32_t *)unit_row);
+    m.w[1] = m.w[2] = m.w[3] = 0;
+  } else {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4 *)unit_row);
+    m.w[0] = v[0]; m.w[1] = v[1]; m.w[2] = v[2]; m.w[3] = v[3];
+  }
+  return m;
+}
+
+// The scale s and offset z of scale group `sg` of a column: value = fma(q, s, z). Affine: the group's bf16 s and z
+// (quant_formats.h:614-616). Q4_K: s = d * sc and z = -(dmin * mn) of sub-block sg % 8 with the 6-bit sc, mn of
+// the header's 12 scale bytes (quant_formats.h:105-118; llama.cpp's get_scale_min_k4), both products exact.
+struct Coef {
+  float s, z;
+};
+template <uint32_t FMT>
+__device__ __forceinline__ Coef coef(const MetaWords &m, uint32_t sg) {
+  if constexpr (FMT != SQ_FMT_Q4K) {
+    return {bf16_to_f32(m.w[0] & 0xFFFFu), __uint_as_float(m.w[0] & 0xFFFF0000u)};
+  } else {
+    const uint32_t j = sg & 7u;
+    uint32_t sc, mn;
+    if (j < 4) {
+      const uint32_t sh = 8u * j;
+      sc = (m.w[1] >> sh) & 63u;
+      mn = (m.w[2] >> sh) & 63u;
+    } else {
+      const uint32_t sh = 8u * (j - 4), w = m.w[3] >> sh;
+      sc = (w & 0xFu) | ((((m.w[1] >> sh) >> 6) & 3u) << 4);
+      mn = ((w >> 4) & 0xFu) | ((((m.w[2] >> sh) >> 6) & 3u) << 4);
+    }
+    const float d = f16_to_f32(m.w[0] & 0xFFFFu), dmin = f16_to_f32(m.w[0] >> 16);
+    return {d * (float)sc, -(dmin * (float)mn)};
+  }
+}
+
+}  // namespace sq::kern

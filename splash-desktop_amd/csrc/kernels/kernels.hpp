@@ -1,0 +1,100 @@
+// Launch interface between the host operators (csrc/host) and the HIP kernels (csrc/kernels/*.hip). Everything
+// here takes device pointers and plain sizes; the host validates shapes and buffer extents before it calls in.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../abi.h"
+
+namespace sq::kern {
+
+enum Epilogue : uint32_t { EpNone = 0, EpResidual = 1, EpUpWithGate = 2 };
+
+// One weight tensor's planes in a dispatch: its 64-column tiles write destination columns
+// [out_offset, out_offset + 64 * tiles).
+struct Segment {
+  const uint8_t *plane0;
+  const uint8_t *meta;
+  uint32_t tiles;
+  uint32_t out_offset;
+};
+
+// The decode tile (rows <= 32): y[r][c] = sum_k x[r][k] w[c][k] over up to three segments of one format, grid
+// (sum of tiles, splits). Split partials are fp32 [split][rows][out_stride]; counters one per destination
+// 64-column tile (out_offset / 64 + tile), zero before and after each dispatch.
+struct DecodeArgs {
+  const uint16_t *input;   // bf16 [rows][K]
+  Segment seg[3];
+  uint32_t segments;
+  void *output;            // bf16 or fp32 [rows][out_stride]
+  const uint16_t *aux;     // bf16 [rows][out_stride]: the residual, or the gate of an up-with-gate pass
+  float *partials;
+  uint32_t *counters;
+  uint32_t K, rows, splits, out_stride;
+};
+hipError_t launch_decode(uint32_t fmt, uint32_t epilogue, bool f32_output, const DecodeArgs &args,
+                         hipStream_t stream);
+// The one-pass gate/up decode: gate and up of one format over the same columns, out = bf16(bf16(up) *
+// silu(bf16(gate))), bitwise the two passes' result at the same split. Partials [split][rows][2 * out_stride]
+// (gate's columns, then up's at out_stride on); counters one per 64 destination columns.
+struct GateUpArgs {
+  const uint16_t *input;
+  Segment gate, up;
+  uint16_t *output;
+  float *partials;
+  uint32_t *counters;
+  uint32_t K, rows, splits, out_stride;
+};
+hipError_t launch_decode_gate_up(uint32_t fmt, const GateUpArgs &args, hipStream_t stream);
+
+// The prefill tile (rows > 32): activations converted once to fp16 with a power-of-two scale per row
+// (launch_prefill_prepare), then dequantised fp16 weights on MFMA.
+hipError_t launch_prefill_prepare(const uint16_t *input, uint32_t rows, uint32_t K, uint16_t *half_input,
+                                  float *row_scale, hipStream_t stream);
+struct PrefillArgs {
+  const uint16_t *half_input;  // fp16 [rows][K], rows scaled by 2^-e
+  const float *row_scale;      // 2^e per row
+  Segment seg[3];
+  uint32_t segments;
+  uint16_t *output;            // bf16 [rows][out_stride]
+  const uint16_t *aux;
+  uint32_t K, rows, out_stride;
+};
+hipError_t launch_prefill(uint32_t fmt, uint32_t epilogue, const PrefillArgs &args, hipStream_t stream);
+
+// Dequantisation of every weight of a segment's planes: fp32 fma(q, s, z) and the staged tile's fp16 rounding of
+// it, [N][K] each (either may be null).
+hipError_t launch_dequant(uint32_t fmt, const uint8_t *plane0, const uint8_t *meta, uint32_t N, uint32_t K,
+                          float *values, uint16_t *halves, hipStream_t stream);
+// Load-time repacks: native rows (GgufRepackParams layout) into plane0 / meta, and MLX tensors (uint32 codes,
+// bf16 scales and biases) straight into plane0 / meta.
+hipError_t launch_repack(const uint8_t *src, uint8_t *dst, const SqGgufRepackParams &params, hipStream_t stream);
+hipError_t launch_mlx_repack(uint32_t fmt, const uint32_t *weight, const uint16_t *scales, const uint16_t *biases,
+                             uint32_t rows, uint32_t K, uint8_t *plane0, uint8_t *meta, hipStream_t stream);
+
+// MoE.
+hipError_t launch_moe_route_select(const float *scores, uint32_t score_stride, uint32_t *selected,
+                                   float *routing_weights, const SqMoeRouteParams &params, hipStream_t stream);
+hipError_t launch_moe_group(const uint32_t *selected, SqMoeTileDescriptor *tiles, SqMoeTileCount *tile_count,
+                            uint32_t *grouped_routes, uint32_t *route_rows, uint32_t max_tiles,
+                            const SqMoeGroupParams &params, hipStream_t stream);
+// An expert pass over the grouped rows: workgroup (64-column tile, tile) runs when the tile is its expert's first and
+// walks all the expert's rows. gate_up: gate and up of each expert in one pass over input rows routes[row] / top_k,
+// out = bf16(bf16(up) silu(bf16(gate))); else one tensor over grouped input rows.
+struct MoeExpertArgs {
+  const uint16_t *input;        // gate/up: the step's rows [rows][K]; down: grouped rows [tiles * tile_rows][K]
+  const uint32_t *routes;       // gate/up: the route of each grouped row (~0u padding)
+  const SqMoeTileDescriptor *tiles;
+  const SqMoeTileCount *tile_count;
+  const uint8_t *plane0[2];     // gate (or the single pass's weights), up
+  const uint8_t *meta[2];
+  const uint32_t *slots;        // routed expert e's planes from row slots[e] * output_size
+  uint16_t *output;             // [tiles * tile_rows][output_size]
+  uint32_t K, output_size, tile_rows, max_tiles, fmt, gate_up, top_k;
+};
+hipError_t launch_moe_expert(const MoeExpertArgs &args, hipStream_t stream);
+hipError_t launch_moe_combine(const uint16_t *expert_output, const uint32_t *route_rows,
+                              const float *routing_weights, const uint16_t *residual, uint16_t *output,
+                              const SqMoeCombineParams &params, hipStream_t stream);
+
+}  // namespace sq::kern

@@ -1,0 +1,237 @@
+// MoE routed experts: top-k route select, grouping of routes into expert tiles, the expert passes (gate and up in
+// one pass, then down) and the combine (reference: kernels/shared/moe.metal:23-162,175-331,480-505 and
+// kernels/shared/moe_gguf.metal:21-206).
+//
+// CDNA4 mapping. The expert passes run the decode tile's wave walk (walk.hpp) per expert: workgroup (64-column
+// tile, expert tile) runs only on its expert's first tile and walks every grouped row of that expert 32 rows at a
+// time, so each column tile of an expert's weights streams from HBM once per step however its rows fall into tiles.
+// The gate/up pass reads its activation rows straight through the grouped routes (the reference's separate gather
+// copy is folded into the A-operand loads).
+#include "kernels.hpp"
+#include "walk.hpp"
+
+namespace sq::kern {
+namespace {
+
+// One wave per row. Rank by rank, the highest remaining score wins, the lowest expert id among equal scores
+// (moe.metal:69-93); then weight_r = 2^((s_r - s_0) log2 e) / sum_o 2^((s_o - s_0) log2 e) over the selected k,
+// summed in rank order (moe.metal:95-104).
+__global__ __launch_bounds__(64) void route_select_kernel(const float *scores, uint32_t stride, uint32_t *selected,
+                                                          float *weights, SqMoeRouteParams p) {
+  constexpr int kPer = SQ_MOE_WIDE_EXPERT_SLOTS / 64;
+  const uint32_t row = blockIdx.x, lane = threadIdx.x;
+  float v[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const uint32_t e = lane + 64u * i;
+    v[i] = e < p.experts ? scores[(size_t)row * stride + e] : -INFINITY;
+  }
+  __shared__ float ordered[64];
+  uint32_t taken = 0;   // bit i: expert lane + 64 i already selected
+  for (uint32_t rank = 0; rank < p.top_k; ++rank) {
+    float best = -INFINITY;
+    int at = -1;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+      if (lane + 64u * i < p.experts && !((taken >> i) & 1u) && (at < 0 || v[i] > best)) best = v[i], at = i;
+    float top = best;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) top = fmaxf(top, __shfl_xor(top, m));
+    const uint32_t candidate = at >= 0 && best == top ? lane + 64u * at : 0xFFFFFFFFu;
+    uint32_t winner = candidate;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) winner = min(winner, (uint32_t)__shfl_xor((int)winner, m));
+    if (candidate == winner && at >= 0) taken |= 1u << at;
+    if (lane == 0) {
+      selected[(size_t)row * p.top_k + rank] = winner;
+      ordered[rank] = top;
+    }
+  }
+  __syncthreads();
+  for (uint32_t rank = lane; rank < p.top_k; rank += 64) {
+    float denominator = 0.0f;
+    for (uint32_t o = 0; o < p.top_k; ++o) denominator += exp2f((ordered[o] - ordered[0]) * 1.44269504089f);
+    weights[(size_t)row * p.top_k + rank] = exp2f((ordered[rank] - ordered[0]) * 1.44269504089f) / denominator;
+  }
+}
+
+// One workgroup groups every route (moe.metal:184-278, routed slices only): count per expert, exclusive prefix of
+// the experts' tiles in expert order, tile descriptors, then each route's grouped row. Routes of an expert take its
+// rows in route order (a bitmap of the rows that route to each expert, 512 rows at a time, gives a route's rank),
+// so the grouping, and every expert pass after it, is deterministic.
+__global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, SqMoeTileDescriptor *tiles,
+                                                    SqMoeTileCount *tile_count, uint32_t *grouped_routes,
+                                                    uint32_t *route_rows, SqMoeGroupParams p) {
+  constexpr uint32_t kChunk = 512, kWords = kChunk / 32;
+  __shared__ uint32_t counts[SQ_MOE_WIDE_EXPERT_SLOTS], offsets[SQ_MOE_WIDE_EXPERT_SLOTS],
+      running[SQ_MOE_WIDE_EXPERT_SLOTS];
+  __shared__ uint32_t bits[SQ_MOE_WIDE_EXPERT_SLOTS * kWords];
+  __shared__ uint32_t total;
+  const uint32_t tid = threadIdx.x, routes = p.rows * p.top_k, tr = p.tile_rows;
+  counts[tid] = 0;
+  running[tid] = 0;
+  __syncthreads();
+  for (uint32_t r = tid; r < routes; r += 512) atomicAdd(&counts[selected[r]], 1u);
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t sum = 0;
+    for (uint32_t e = 0; e < p.experts; ++e) offsets[e] = sum, sum += (counts[e] + tr - 1) / tr;
+    total = sum;
+  }
+  __syncthreads();
+  if (tid < p.experts) {
+    const uint32_t c = counts[tid], n = (c + tr - 1) / tr, first = offsets[tid];
+    for (uint32_t t = 0; t < n; ++t) tiles[first + t] = SqMoeTileDescriptor{tid, min(tr, c - t * tr)};
+    for (uint32_t row = first * tr + c; row < (first + n) * tr; ++row) grouped_routes[row] = ~0u;
+  }
+  for (uint32_t chunk = 0; chunk < p.rows; chunk += kChunk) {
+    for (uint32_t i = tid; i < p.experts * kWords; i += 512) bits[i] = 0;
+    __syncthreads();
+    const uint32_t r0 = chunk * p.top_k, r1 = min(p.rows, chunk + kChunk) * p.top_k;
+    for (uint32_t r = r0 + tid; r < r1; r += 512) {
+      const uint32_t local = r / p.top_k - chunk;
+      atomicOr(&bits[selected[r] * kWords + local / 32], 1u << (local % 32));
+    }
+    __syncthreads();
+    for (uint32_t r = r0 + tid; r < r1; r += 512) {
+      const uint32_t e = selected[r], local = r / p.top_k - chunk;
+      uint32_t rank = running[e];
+      for (uint32_t w = 0; w < local / 32; ++w) rank += __popc(bits[e * kWords + w]);
+      rank += __popc(bits[e * kWords + local / 32] & ((1u << (local % 32)) - 1u));
+      const uint32_t row = offsets[e] * tr + rank;
+      grouped_routes[row] = r;
+      route_rows[r] = row;
+    }
+    __syncthreads();
+    if (tid < p.experts)
+      for (uint32_t w = 0; w < kWords; ++w) running[tid] += __popc(bits[tid * kWords + w]);
+    __syncthreads();
+  }
+  if (tid == 0)
+    *tile_count = SqMoeTileCount{total, {p.gate_up_columns, total, 1}, {p.down_columns, total, 1}, {0, 0, 0}};
+}
+
+template <uint32_t FMT, int NT>
+__global__ __launch_bounds__(256) void expert_kernel(MoeExpertArgs a) {
+  using F = Fmt<FMT>;
+  const uint32_t t = blockIdx.y, ntiles = a.tile_count->tiles;
+  if (t >= ntiles) return;
+  const SqMoeTileDescriptor d = a.tiles[t];
+  if (t > 0 && a.tiles[t - 1].expert == d.expert) return;
+  uint32_t last = t;
+  while (last + 1 < ntiles && a.tiles[last + 1].expert == d.expert) ++last;
+  const uint32_t count = (last - t) * a.tile_rows + a.tiles[last].rows, first_row = t * a.tile_rows;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15, q = lane >> 4;
+  const uint32_t G = a.K >> 5, units = G / F::UNIT, groups = G / F::SG;
+  const uint32_t ptile = a.slots[d.expert] * (a.output_size / 64) + blockIdx.x;
+  const uint8_t *plane[NT], *meta[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    plane[n] = a.plane0[n] + (size_t)ptile * G * 1024 + (size_t)j * 16 + (size_t)q * 4;
+    meta[n] = a.meta[n] + ((size_t)ptile * units * 64 + j) * F::META;
+  }
+  const uint32_t g0 = (uint32_t)wave * groups / 4, g1 = (uint32_t)(wave + 1) * groups / 4;
+  const uint32_t col = blockIdx.x * 64 + 16 * wave + j;
+  __shared__ float red[4 * NT * 4 * 2 * 4 * 64];
+  for (uint32_t base = 0; base < count; base += 32) {
+    RowPtrs x;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const uint32_t r = base + 16u * b + j;
+      if (r < count) {
+        const uint32_t grouped = first_row + r;
+        const uint32_t source = NT == 2 ? a.routes[grouped] / a.top_k : grouped;
+        x.row[b] = a.input + (size_t)source * a.K;
+      } else {
+        x.row[b] = nullptr;
+      }
+    }
+    f32x4 acc[NT][4][2];
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[n][tt][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    walk<FMT, 2, 4, NT>(plane, meta, x, g0, g1, q, acc);
+    float total[NT][2][4];
+    reduce_waves<2, 4, NT>(acc, red, wave, lane, total);
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t r = base + 16u * b + 4u * q + i;
+        if (r >= count) continue;
+        const size_t at = (size_t)(first_row + r) * a.output_size + col;
+        if constexpr (NT == 2) {
+          const float g = bf16_to_f32(f32_to_bf16(total[0][b][i])), u = bf16_to_f32(f32_to_bf16(total[1][b][i]));
+          a.output[at] = f32_to_bf16(u * silu(g));
+        } else {
+          a.output[at] = f32_to_bf16(total[0][b][i]);
+        }
+      }
+    __syncthreads();   // the LDS of the reduction is rewritten by the next rows
+  }
+}
+
+// out[r][d] = bf16(residual + sum_slot w_slot * expert_out[route_rows[slot]][d]) in slot order (moe.metal:480-505).
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t *expert_output, const uint32_t *route_rows,
+                                                      const float *weights, const uint16_t *residual,
+                                                      uint16_t *output, SqMoeCombineParams p) {
+  const uint32_t r = blockIdx.x, d = blockIdx.y * 256 + threadIdx.x;
+  if (d >= p.hidden_size) return;
+  const size_t at = (size_t)r * p.hidden_size + d;
+  float v = residual ? bf16_to_f32(residual[at]) : 0.0f;
+  const size_t route = (size_t)r * p.routes_per_row;
+  for (uint32_t slot = 0; slot < p.routes_per_row; ++slot) {
+    const uint32_t grouped = route_rows[route + slot];
+    if (grouped == ~0u) continue;
+    v = fmaf(weights[route + slot], bf16_to_f32(expert_output[(size_t)grouped * p.hidden_size + d]), v);
+  }
+  output[at] = f32_to_bf16(v);
+}
+
+template <uint32_t FMT>
+hipError_t launch_expert_format(const MoeExpertArgs &a, hipStream_t stream) {
+  const dim3 grid(a.output_size / 64, a.max_tiles), block(256);
+  if (a.gate_up) hipLaunchKernelGGL((expert_kernel<FMT, 2>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((expert_kernel<FMT, 1>), grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_moe_route_select(const float *scores, uint32_t stride, uint32_t *selected, float *weights,
+                                   const SqMoeRouteParams &p, hipStream_t stream) {
+  hipLaunchKernelGGL(route_select_kernel, dim3(p.rows), dim3(64), 0, stream, scores, stride, selected, weights, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_group(const uint32_t *selected, SqMoeTileDescriptor *tiles, SqMoeTileCount *tile_count,
+                            uint32_t *grouped_routes, uint32_t *route_rows, uint32_t max_tiles,
+                            const SqMoeGroupParams &p, hipStream_t stream) {
+  (void)max_tiles;
+  hipLaunchKernelGGL(group_kernel, dim3(1), dim3(512), 0, stream, selected, tiles, tile_count, grouped_routes,
+                     route_rows, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_expert(const MoeExpertArgs &a, hipStream_t stream) {
+  switch (a.fmt) {
+    case SQ_FMT_AF4G32: return launch_expert_format<SQ_FMT_AF4G32>(a, stream);
+    case SQ_FMT_AF4G64: return launch_expert_format<SQ_FMT_AF4G64>(a, stream);
+    case SQ_FMT_AF4G128: return launch_expert_format<SQ_FMT_AF4G128>(a, stream);
+    case SQ_FMT_Q4K: return launch_expert_format<SQ_FMT_Q4K>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_moe_combine(const uint16_t *expert_output, const uint32_t *route_rows, const float *weights,
+                              const uint16_t *residual, uint16_t *output, const SqMoeCombineParams &p,
+                              hipStream_t stream) {
+  hipLaunchKernelGGL(combine_kernel, dim3(p.rows, (p.hidden_size + 255) / 256), dim3(256), 0, stream, expert_output,
+                     route_rows, weights, residual, output, p);
+  return hipGetLastError();
+}
+
+}  // namespace sq::kern

@@ -1,0 +1,131 @@
+"""Shared helpers of the GPU tests: weights built on the CPU oracle and uploaded, runs through the C ABI, and the
+acceptance checks of the reference's projection tests (fp64 interval per element) plus the BASELINE tolerances."""
+from __future__ import annotations
+
+import numpy as np
+
+import splash_q4 as sq
+from splash_q4 import synthetic
+import sq_oracle as oracle
+
+
+def torch():
+    import torch as t
+    return t
+
+
+def to_device(array: np.ndarray):
+    t = torch()
+    a = np.ascontiguousarray(array)
+    if a.dtype == np.uint16:
+        return t.from_numpy(a.view(np.int16)).cuda()
+    if a.dtype == np.uint32:
+        return t.from_numpy(a.view(np.int32)).cuda()
+    if a.dtype == np.uint8:
+        return t.from_numpy(a).cuda()
+    return t.from_numpy(a).cuda()
+
+
+def to_host(tensor, dtype) -> np.ndarray:
+    return tensor.cpu().numpy().view(dtype)
+
+
+class Weights:
+    """An n x k tensor in `fmt`: native rows, planes on the device and the oracle's fp32 values and fp16 bits."""
+
+    def __init__(self, fmt: int, n: int, k: int, native: np.ndarray):
+        self.fmt, self.n, self.k, self.native = fmt, n, k, native
+        self.plane0_h, self.meta_h, self.values = oracle.repack(fmt, native, n, k)
+        _, self.halves = oracle.plane_values(fmt, self.plane0_h, self.meta_h, n, k)
+        self.plane0, self.meta = to_device(self.plane0_h), to_device(self.meta_h)
+
+    def segment(self, column_offset: int = 0) -> sq.Segment:
+        return sq.segment(self.fmt, self.n, self.k, self.plane0, self.meta, column_offset)
+
+
+def affine_native(rng: np.random.Generator, fmt: int, n: int, k: int, centred: bool = False) -> np.ndarray:
+    """Native rows of an af4 format: z = -8 s (the benchmark's), or z centring the codes at a random point
+    (the reference's makeAffineNative)."""
+    group = {oracle.FMT_AF4G32: 32, oracle.FMT_AF4G64: 64, oracle.FMT_AF4G128: 128}[fmt]
+    codes, weight, scales, biases = synthetic.mlx_affine(rng, n, k, group, scale_sigma=0.02)
+    if centred:
+        s = synthetic.bf16_to_f32(scales)
+        biases = synthetic.bf16_bits(-s * 15 * rng.uniform(0.4, 0.6, size=s.shape).astype(np.float32))
+    return oracle.mlx_native(fmt, weight, scales, biases, n, k)
+
+
+def make_weights(rng, fmt: int, n: int, k: int, centred: bool = False) -> Weights:
+    if fmt == oracle.FMT_Q4K:
+        return Weights(fmt, n, k, synthetic.q4k_native(rng, n, k).ravel())
+    return Weights(fmt, n, k, affine_native(rng, fmt, n, k, centred))
+
+
+def dense_inputs(rng, rows: int, k: int) -> np.ndarray:
+    return synthetic.activations(rng, rows, k)
+
+
+def sparse_inputs(rows: int, k: int, magnitude: float = 1e5) -> np.ndarray:
+    """One +-magnitude entry per 256 inputs, past half's range (gguf_projection_test.mm:156-169)."""
+    x = np.zeros((rows, k), np.float32)
+    for r in range(rows):
+        for b in range(k // 256):
+            x[r, b * 256 + (r * 31 + b * 97) % 256] = -magnitude if (r + b) % 2 else magnitude
+    return synthetic.bf16_bits(x)
+
+
+def bf16(values) -> np.ndarray:
+    return synthetic.bf16_to_f32(synthetic.bf16_bits(np.asarray(values, np.float32)))
+
+
+def check_projection(got_bf16: np.ndarray, x: np.ndarray, weights: list[Weights] | Weights, what: str,
+                     residual: np.ndarray | None = None) -> dict:
+    """Every output inside [bf16(v - e), bf16(v + e)] of its fp64 value v and projectionBound e (staged), and the
+    BASELINE tolerances: rel-L2 <= 1e-2 and max-abs <= 2^-6 max|row| against fp64. Returns error statistics."""
+    if isinstance(weights, Weights):
+        weights = [weights]
+    w = np.concatenate([wt.values for wt in weights], axis=0)
+    value, magnitude, inputs, largest = oracle.project_f64(x, w)
+    bound = oracle.projection_bound(magnitude, inputs, largest, True)
+    lo, hi = value - bound, value + bound
+    if residual is not None:
+        res = synthetic.bf16_to_f32(residual).astype(np.float64)
+        lo = (lo.astype(np.float32) + res.astype(np.float32)).astype(np.float64)
+        hi = (hi.astype(np.float32) + res.astype(np.float32)).astype(np.float64)
+        value = value + res
+    got = synthetic.bf16_to_f32(got_bf16).astype(np.float64)
+    inside = (got >= bf16(lo)) & (got <= bf16(hi)) & np.isfinite(got)
+    assert inside.all(), f"{what}: {np.count_nonzero(~inside)} outputs outside their fp64 interval, first at " \
+                         f"{np.argwhere(~inside)[:3].tolist()}"
+    err = got - value
+    rel_l2 = np.linalg.norm(err) / max(np.linalg.norm(value), 1e-300)
+    row_inf = np.abs(value).max(axis=1, keepdims=True)
+    assert rel_l2 <= 1e-2, f"{what}: relative L2 {rel_l2}"
+    assert np.all(np.abs(err) <= np.ldexp(row_inf, -6)), f"{what}: max-abs error past 2^-6 |row|"
+    return {"rel_l2": rel_l2, "max_abs": float(np.abs(err).max())}
+
+
+def staged_reference(x: np.ndarray, weights: Weights) -> np.ndarray:
+    """bf16 output of the reference's staged numerics (fp16 weights, exact products, fp32 sums)."""
+    return synthetic.bf16_bits(oracle.project_staged_f32(x, weights.halves))
+
+
+class Run:
+    """Device buffers for a projection run through sq_linear_add."""
+
+    def __init__(self, plan: sq.LinearPlan, n: int, x: np.ndarray, out_dtype=np.uint16):
+        t = torch()
+        self.plan = plan
+        self.rows = plan.storage_rows
+        k = x.shape[1]
+        xin = np.zeros((self.rows, k), np.uint16)
+        xin[: x.shape[0]] = x
+        self.x = to_device(xin)
+        self.n = n
+        self.out_dtype = out_dtype
+        # Every element starts as a NaN no kernel writes (bf16 0xFFFF), so untouched outputs show.
+        self.out = (t.full((self.rows, n), -1, dtype=t.int16, device="cuda") if out_dtype == np.uint16
+                    else t.full((self.rows, n), float("nan"), dtype=t.float32, device="cuda"))
+        self.scratch = sq.Scratch(plan)
+
+    def output(self) -> np.ndarray:
+        return to_host(self.out, self.out_dtype)

@@ -1,0 +1,176 @@
+"""The C ABI on the CPU: the library loads and exports every entry point include/splash_q4.h declares, and the
+host-side planning and validation behave as the reference's ops::Linear / ops::MoE do (plans, storage rows,
+scratch sizes, and std::invalid_argument before anything is launched). No GPU work is issued here."""
+import re
+
+import pytest
+
+import splash_q4 as sq
+
+
+def declared_functions():
+    text = sq.HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:int|const char \*)\s*(sq_\w+)\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = sq.lib()
+    names = declared_functions()
+    assert len(names) >= 20
+    for name in names:
+        assert hasattr(lib, name), name
+    assert sorted(sq.exported_symbols()) == names
+    assert b"gfx950" in lib.sq_version()
+
+
+def seg(n=4096, k=4096, fmt=sq.FMT_AF4G64, plane_bytes=None, meta_bytes=None, offset=0):
+    p0, m = sq.plane_bytes(fmt, n, k) if fmt in sq.FORMATS else (1 << 30, 1 << 30)
+    # fake device addresses: planning and validation never dereference them
+    return sq.Segment(sq.Buffer(0x1000, plane_bytes if plane_bytes is not None else p0), sq.Buffer(None, 0),
+                      sq.Buffer(0x2000000000, meta_bytes if meta_bytes is not None else m), n, k, offset, fmt)
+
+
+@pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("rows", [1, 2, 4, 8, 16, 32])
+def test_decode_plans(n, k, rows):
+    proj = sq.projection(seg(n, k))
+    plan = sq.plan_for(sq.decode_workload(n, k, rows), proj)
+    assert plan.config.tile == sq.TILE_STAGED
+    s = plan.config.splits
+    assert s & (s - 1) == 0 and 1 <= s <= 16 and (k // 32) % (2 * s) == 0
+    assert plan.storage_rows == rows
+    size, gate = sq.scratch_size(plan)
+    assert size.partials == (s * rows * n * 4 if s > 1 else 0)
+    assert size.counters == (n // 64 * 4 if s > 1 else 0)
+    assert gate == 0
+
+
+def test_split_law_prefers_saturating_grids():
+    # 14336 x 4096 at one row: 224 tiles need splits to fill 256 compute units.
+    plan = sq.plan_for(sq.decode_workload(14336, 4096, 1), sq.projection(seg(14336, 4096)))
+    assert plan.config.splits >= 2
+    # 1024 x 4096: 16 tiles, the most splits.
+    plan = sq.plan_for(sq.decode_workload(1024, 4096, 1), sq.projection(seg(1024, 4096)))
+    assert plan.config.splits >= 8
+
+
+def test_prefill_plans():
+    proj = sq.projection(seg(14336, 4096))
+    plan = sq.plan_for(sq.prefill_workload(14336, 4096, 2048), proj)
+    assert plan.config.tile == sq.TILE_PREFILL and plan.config.splits == 1 and plan.storage_rows == 2048
+    size, _ = sq.scratch_size(plan)
+    assert size.input == 2048 * 4096 * 2 and size.sums == 2048 * 4
+    ragged = sq.plan_for(sq.prefill_workload(14336, 4096, 300), proj)
+    assert ragged.storage_rows == 384
+    short = sq.plan_for(sq.prefill_workload(14336, 4096, 32), proj)
+    assert short.config.tile == sq.TILE_STAGED
+
+
+def test_gate_up_plans():
+    up, gate = sq.projection(seg(14336, 4096)), sq.projection(seg(14336, 4096))
+    plan = sq.plan_for(sq.decode_workload(14336, 4096, 8, sq.EPILOGUE_GATE_UP), up, gate)
+    assert plan.config.one_gate_up_pass == 1
+    size, gate_bytes = sq.scratch_size(plan)
+    assert gate_bytes == 0
+    two = sq.plan_config(sq.decode_workload(14336, 4096, 8, sq.EPILOGUE_GATE_UP), sq.LinearConfig(sq.TILE_STAGED, 2, 0, 0, 0))
+    assert sq.scratch_size(two)[1] == 8 * 14336 * 2
+
+
+@pytest.mark.parametrize("workload,config,message", [
+    (sq.decode_workload(100, 4096, 1), None, "invalid linear matrix"),
+    (sq.decode_workload(4096, 4096, 33), None, "invalid linear decode workload"),
+    (sq.decode_workload(4096, 4096, 0), None, "invalid linear decode workload"),
+    (sq.decode_workload(4096, 4096, 8, sq.EPILOGUE_UP_WITH_GATE), None, "invalid linear decode workload"),
+    (sq.prefill_workload(4096, 4096, 2049), None, "invalid linear prefill workload"),
+    (sq.prefill_workload(4096, 4096, 64, sq.EPILOGUE_GATE_UP), None, "invalid linear prefill workload"),
+    (sq.decode_workload(4096, 4096, 8), sq.LinearConfig(sq.TILE_REGISTER, 1, 0, 0, 0), "register tile"),
+    (sq.decode_workload(4096, 4096, 8), sq.LinearConfig(sq.TILE_STAGED, 3, 0, 0, 0), "whole 32-input groups"),
+    (sq.decode_workload(4096, 4096, 8), sq.LinearConfig(sq.TILE_STAGED, 32, 0, 0, 0), "whole 32-input groups"),
+    (sq.decode_workload(4096, 4096, 8), sq.LinearConfig(sq.TILE_PREFILL, 1, 0, 0, 0), "invalid block prefill"),
+    (sq.prefill_workload(4096, 4096, 64), sq.LinearConfig(sq.TILE_STAGED, 1, 0, 0, 0), "up to 32 rows"),
+    (sq.decode_workload(4096, 4096, 8), sq.LinearConfig(sq.TILE_STAGED, 1, 0, 1, 0), "one pass"),
+])
+def test_invalid_plans_raise(workload, config, message):
+    with pytest.raises(sq.InvalidArgument, match=message):
+        if config is None:
+            sq.plan_for(workload)
+        else:
+            sq.plan_config(workload, config)
+
+
+def test_fp32_destination_only_plain_decode():
+    with pytest.raises(sq.InvalidArgument, match="fp32 destination"):
+        sq.plan_config(sq.prefill_workload(4096, 4096, 64), sq.LinearConfig(sq.TILE_PREFILL, 1, 0, 0, 0), sq.OUTPUT_F32)
+    plan = sq.plan_config(sq.decode_workload(4096, 4096, 8), sq.LinearConfig(sq.TILE_STAGED, 4, 0, 0, 0), sq.OUTPUT_F32)
+    assert plan.destination == sq.OUTPUT_F32
+
+
+def test_projection_and_plane_validation():
+    with pytest.raises(sq.InvalidArgument, match="plane0"):
+        sq.call("sq_require_segment_planes", sq.byref(seg(plane_bytes=1024)), b"projection", 0)
+    with pytest.raises(sq.InvalidArgument, match="meta"):
+        sq.call("sq_require_segment_planes", sq.byref(seg(meta_bytes=16)), b"projection", 0)
+    sq.call("sq_require_segment_planes", sq.byref(seg()), b"projection", 0)
+    with pytest.raises(sq.InvalidArgument, match="not one this build runs"):
+        sq.call("sq_require_segment_planes", sq.byref(seg(fmt=12, plane_bytes=1 << 30, meta_bytes=1 << 30)), b"projection", 0)
+    # segments must tile the leading columns in order
+    bad = sq.projection([seg(2048, 4096), seg(2048, 4096, offset=1024)], output_size=4096)
+    with pytest.raises(sq.InvalidArgument, match="do not tile"):
+        sq.plan_for(sq.decode_workload(4096, 4096, 1), bad)
+
+
+def test_add_validates_buffers_before_launch():
+    """Undersized buffers throw on the host (Linear.cpp:203-221); nothing reaches a GPU."""
+    proj = sq.projection(seg(4096, 4096))
+    plan = sq.plan_config(sq.decode_workload(4096, 4096, 8), sq.LinearConfig(sq.TILE_STAGED, 4, 0, 0, 0))
+    fake = lambda nbytes: sq.Buffer(0x4000, nbytes)
+    scratch = sq.LinearScratch(sq.Buffer(None, 0), sq.Buffer(None, 0), fake(4 * 8 * 4096 * 4), fake(4096 // 64 * 4),
+                               sq.Buffer(None, 0))
+    cases = [
+        (sq.LinearBuffers(fake(8 * 4096 * 2 - 2), fake(8 * 4096 * 2), sq.Buffer(None, 0), sq.Buffer(None, 0), scratch), "projection input"),
+        (sq.LinearBuffers(fake(8 * 4096 * 2), fake(100), sq.Buffer(None, 0), sq.Buffer(None, 0), scratch), "projection output"),
+        (sq.LinearBuffers(fake(8 * 4096 * 2), fake(8 * 4096 * 2), sq.Buffer(None, 0), sq.Buffer(None, 0),
+                          sq.LinearScratch()), "projection partials"),
+    ]
+    for buffers, message in cases:
+        with pytest.raises(sq.InvalidArgument, match=message):
+            sq.call("sq_linear_add", None, sq.byref(buffers), sq.byref(proj), sq.byref(plan), None)
+    residual_plan = sq.plan_config(sq.decode_workload(4096, 4096, 8, sq.EPILOGUE_RESIDUAL), sq.LinearConfig(sq.TILE_STAGED, 1, 0, 0, 0))
+    buffers = sq.LinearBuffers(fake(8 * 4096 * 2), fake(8 * 4096 * 2), fake(10), sq.Buffer(None, 0), sq.LinearScratch())
+    with pytest.raises(sq.InvalidArgument, match="projection residual"):
+        sq.call("sq_linear_add", None, sq.byref(buffers), sq.byref(proj), sq.byref(residual_plan), None)
+    gate_plan = sq.plan_config(sq.decode_workload(4096, 4096, 8, sq.EPILOGUE_GATE_UP), sq.LinearConfig(sq.TILE_STAGED, 1, 0, 0, 0))
+    with pytest.raises(sq.InvalidArgument, match="gate projection"):
+        sq.call("sq_linear_add", None, sq.byref(buffers), sq.byref(proj), sq.byref(gate_plan), None)
+
+
+def test_scratch_bounds_cover_every_plan():
+    dev = sq.device()
+    out = sq.LinearScratchSize()
+    sq.call("sq_linear_decode_scratch_size", sq.byref(dev), 14336, 4096, sq.byref(out))
+    for rows in range(1, 33):
+        for e in (sq.EPILOGUE_NONE, sq.EPILOGUE_RESIDUAL):
+            size, _ = sq.scratch_size(sq.plan_for(sq.decode_workload(14336, 4096, rows, e)))
+            assert size.partials <= out.partials and size.counters <= out.counters
+    sq.call("sq_linear_prefill_scratch_size", sq.byref(dev), 14336, 4096, sq.byref(out))
+    assert out.input == 2048 * 4096 * 2
+
+
+def test_moe_plans_and_workspace():
+    shape = sq.MoeShape(2048, 128, 8, 768, sq.FMT_AF4G64)
+    plan = sq.MoePlan()
+    sq.call("sq_moe_prefill_plan", sq.byref(shape), 512, sq.byref(plan))
+    assert plan.tile_rows == 32
+    routes = 512 * 8
+    assert plan.maximum_tiles == min(routes // 32 + 128, routes)
+    w = plan.workspace
+    assert w.selected_experts == routes * 4 and w.route_rows == routes * 4
+    assert w.tile_descriptors == plan.maximum_tiles * 8 and w.tile_count == 40
+    assert w.expert_intermediate == plan.maximum_tiles * 32 * 768 * 2
+    assert w.expert_output == plan.maximum_tiles * 32 * 2048 * 2
+    sq.call("sq_moe_prefill_plan", sq.byref(shape), 8, sq.byref(plan))
+    assert plan.tile_rows == 8   # 8 rows x 8 routes <= 128 experts
+    with pytest.raises(sq.InvalidArgument, match="invalid MoE workspace shape"):
+        sq.call("sq_moe_prefill_plan", sq.byref(sq.MoeShape(2000, 128, 8, 768, sq.FMT_AF4G64)), 8, sq.byref(plan))
+    with pytest.raises(sq.InvalidArgument, match="invalid MoE rows"):
+        sq.call("sq_moe_decode_plan", sq.byref(shape), 33, sq.byref(plan))

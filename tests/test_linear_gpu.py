@@ -1,0 +1,198 @@
+"""Decode tile (rows <= 32) through the C ABI against the fp64 oracle, with the reference's projection-test
+properties (dev/tests/engine/gguf_projection_test.mm): every output inside its fp64 interval (projectionBound),
+BASELINE's rel-L2 <= 1e-2 and max-abs <= 2^-6 max|row|, sparse inputs past half's range, a row's output bitwise
+independent of the other rows, K-split determinism with counters returned to zero, the epilogues (residual,
+gate/up in one pass bitwise equal to two passes, fp32 destination), fused segments equal to segments alone, and
+untouched padding columns."""
+import numpy as np
+import pytest
+
+import splash_q4 as sq
+import sq_oracle as oracle
+from helpers import (Run, Weights, bf16, check_projection, dense_inputs, make_weights, sparse_inputs, staged_reference,
+                     to_device, to_host, torch)
+from splash_q4 import synthetic
+
+pytestmark = pytest.mark.gpu
+
+FORMATS = [oracle.FMT_AF4G64, oracle.FMT_Q4K, oracle.FMT_AF4G32, oracle.FMT_AF4G128]
+
+
+def run_plan(plan, proj, x, n, out_dtype=np.uint16, residual=None, gate=None, gate_scratch_rows=0):
+    run = Run(plan, n, x, out_dtype)
+    t = torch()
+    res = None
+    if residual is not None:
+        r = np.zeros((run.rows, n), np.uint16)
+        r[: residual.shape[0]] = residual
+        res = to_device(r)
+    gs = run.scratch.gate
+    sq.linear_add(plan, proj, run.x, run.out, residual=res, gate_scratch=gs, scratch=run.scratch.struct(), gate=gate)
+    t.cuda.synchronize()
+    counters = run.scratch.counters
+    if counters is not None:
+        assert int(counters.abs().sum().item()) == 0, "split counters not returned to zero"
+    return run.output()[: x.shape[0]]
+
+
+def staged(n, k, rows, splits, epilogue=sq.EPILOGUE_NONE, destination=sq.OUTPUT_BF16, one_pass=0):
+    return sq.plan_config(sq.decode_workload(n, k, rows, epilogue), sq.LinearConfig(sq.TILE_STAGED, splits, 0, one_pass, 0),
+                          destination)
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("rows", [1, 2, 3, 8, 16, 24, 32])
+@pytest.mark.parametrize("splits", [1, 4])
+def test_decode_dense(fmt, rows, splits):
+    rng = np.random.default_rng(1000 * fmt + 10 * rows + splits)
+    n, k = 256, 2048
+    w = make_weights(rng, fmt, n, k, centred=rows % 2 == 1)
+    x = dense_inputs(rng, rows, k)
+    got = run_plan(staged(n, k, rows, splits), sq.projection(w.segment()), x, n)
+    stats = check_projection(got, x, w, f"fmt {fmt} rows {rows} splits {splits}")
+    # no worse than the reference's staged numerics (fp16 weights, fp32 sums), beyond rounding-boundary noise
+    ref = staged_reference(x, w)
+    value, *_ = oracle.project_f64(x, w.values)
+    ref_l2 = np.linalg.norm(synthetic.bf16_to_f32(ref) - value) / np.linalg.norm(value)
+    assert stats["rel_l2"] <= ref_l2 * 1.10 + 1e-6
+
+
+@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K])
+@pytest.mark.parametrize("splits", [1, 2, 16])
+def test_decode_sparse_inputs(fmt, splits):
+    rng = np.random.default_rng(7 + fmt + splits)
+    n, k = 192, 4096
+    w = make_weights(rng, fmt, n, k)
+    x = sparse_inputs(8, k)
+    got = run_plan(staged(n, k, 8, splits), sq.projection(w.segment()), x, n)
+    check_projection(got, x, w, "sparse")
+
+
+@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K])
+@pytest.mark.parametrize("splits", [1, 8])
+def test_rows_are_independent(fmt, splits):
+    """A row's output is bitwise the same alone (the one-row instance) and among 16 or 32 rows."""
+    rng = np.random.default_rng(31 + splits)
+    n, k = 128, 1024
+    w = make_weights(rng, fmt, n, k)
+    x = dense_inputs(rng, 32, k)
+    proj = sq.projection(w.segment())
+    all32 = run_plan(staged(n, k, 32, splits), proj, x, n)
+    first16 = run_plan(staged(n, k, 16, splits), proj, x[:16], n)
+    assert np.array_equal(all32[:16], first16)
+    for r in (0, 5, 17, 31):
+        alone = run_plan(staged(n, k, 1, splits), proj, x[r:r + 1], n)
+        assert np.array_equal(alone[0], all32[r]), f"row {r}"
+
+
+def test_split_determinism_and_poisoned_partials():
+    rng = np.random.default_rng(3)
+    n, k = 512, 4096
+    w = make_weights(rng, oracle.FMT_AF4G64, n, k)
+    x = dense_inputs(rng, 4, k)
+    proj = sq.projection(w.segment())
+    plan = staged(n, k, 4, 8)
+    run = Run(plan, n, x)
+    t = torch()
+    outs = []
+    for poison in (0x7FC00000, 0x7E800000):   # NaN, then a large finite value in every partial
+        run.scratch.partials.fill_(poison)
+        sq.linear_add(plan, proj, run.x, run.out, scratch=run.scratch.struct())
+        t.cuda.synchronize()
+        assert int(run.scratch.counters.abs().sum().item()) == 0
+        outs.append(run.output().copy())
+    assert np.array_equal(outs[0], outs[1])
+    check_projection(outs[0][:4], x, w, "poisoned partials")
+
+
+def test_residual_epilogue():
+    rng = np.random.default_rng(5)
+    n, k = 256, 2048
+    w = make_weights(rng, oracle.FMT_AF4G64, n, k)
+    x = dense_inputs(rng, 8, k)
+    residual = synthetic.bf16_bits(rng.uniform(-1, 1, (8, n)).astype(np.float32) * 64)
+    for splits in (1, 4):
+        got = run_plan(staged(n, k, 8, splits, sq.EPILOGUE_RESIDUAL), sq.projection(w.segment()), x, n, residual=residual)
+        check_projection(got, x, w, "residual", residual=residual)
+
+
+@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K])
+@pytest.mark.parametrize("splits", [1, 4])
+def test_gate_up_one_pass_equals_two_passes(fmt, splits):
+    rng = np.random.default_rng(11 + splits)
+    n, k = 256, 2048
+    wg, wu = make_weights(rng, fmt, n, k), make_weights(rng, fmt, n, k)
+    x = dense_inputs(rng, 8, k)
+    gate, up = sq.projection(wg.segment()), sq.projection(wu.segment())
+    two = run_plan(staged(n, k, 8, splits, sq.EPILOGUE_GATE_UP), up, x, n, gate=gate)
+    one = run_plan(staged(n, k, 8, splits, sq.EPILOGUE_GATE_UP, one_pass=1), up, x, n, gate=gate)
+    assert np.array_equal(one, two)
+    g = run_plan(staged(n, k, 8, splits), gate, x, n)
+    u = run_plan(staged(n, k, 8, splits), up, x, n)
+    gf, uf = synthetic.bf16_to_f32(g).astype(np.float64), synthetic.bf16_to_f32(u).astype(np.float64)
+    want = uf * gf / (1 + np.exp(-gf))
+    got = synthetic.bf16_to_f32(one).astype(np.float64)
+    # bf16(up) * silu(bf16(gate)) in fp32, rounded once to bf16: within one bf16 ulp of the exact product
+    ulp = np.ldexp(1.0, np.floor(np.log2(np.maximum(np.abs(want), 1e-30))).astype(int) - 7)
+    assert np.all(np.abs(got - want) <= ulp + 1e-30)
+
+
+def test_fp32_destination_rounds_to_the_bf16_output():
+    rng = np.random.default_rng(17)
+    n, k = 256, 4096
+    w = make_weights(rng, oracle.FMT_AF4G64, n, k)
+    x = dense_inputs(rng, 8, k)
+    proj = sq.projection(w.segment(), destination=sq.OUTPUT_F32)
+    for splits in (1, 8):
+        f32 = run_plan(staged(n, k, 8, splits, destination=sq.OUTPUT_F32), proj, x, n, out_dtype=np.float32)
+        b16 = run_plan(staged(n, k, 8, splits), sq.projection(w.segment()), x, n)
+        assert np.array_equal(synthetic.bf16_bits(f32), b16)
+        value, magnitude, inputs, largest = oracle.project_f64(x, w.values)
+        bound = oracle.projection_bound(magnitude, inputs, largest, True)
+        assert np.all(np.abs(f32.astype(np.float64) - value) <= bound)
+        # no worse than the reference's staged fp32 sums on these rows (plus accumulation-order slack)
+        ref = oracle.project_staged_f32(x, w.halves).astype(np.float64)
+        assert np.linalg.norm(f32 - value) <= 2.0 * np.linalg.norm(ref - value) + 1e-9 * np.linalg.norm(value)
+
+
+def test_fused_segments_equal_segments_alone():
+    rng = np.random.default_rng(23)
+    k = 2048
+    parts = [make_weights(rng, oracle.FMT_AF4G64, n, k) for n in (256, 64, 128)]
+    x = dense_inputs(rng, 8, k)
+    total = sum(p.n for p in parts)
+    segs, offset = [], 0
+    for p in parts:
+        segs.append(p.segment(offset))
+        offset += p.n
+    fused = run_plan(staged(total, k, 8, 2), sq.projection(segs), x, total)
+    offset = 0
+    for p in parts:
+        alone = run_plan(staged(p.n, k, 8, 2), sq.projection(p.segment()), x, p.n)
+        assert np.array_equal(fused[:, offset:offset + p.n], alone)
+        offset += p.n
+    check_projection(fused, x, parts, "fused")
+
+
+def test_padding_columns_untouched():
+    rng = np.random.default_rng(29)
+    n, k, pad = 256, 1024, 256
+    w = make_weights(rng, oracle.FMT_AF4G64, n, k)
+    x = dense_inputs(rng, 4, k)
+    proj = sq.projection(w.segment(), output_size=n + pad)
+    got = run_plan(staged(n + pad, k, 4, 4), proj, x, n + pad)
+    assert np.all(got[:, n:] == 0xFFFF)
+    check_projection(got[:, :n], x, w, "padded")
+
+
+@pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("rows", [1, 16])
+def test_baseline_shapes_policy_plans(n, k, rows):
+    """The BASELINE decode sweep's shapes at M = 1 and 16 under the library's own plan."""
+    rng = np.random.default_rng(n + k + rows)
+    w = make_weights(rng, oracle.FMT_AF4G64, n, k)
+    x = dense_inputs(rng, rows, k)
+    proj = sq.projection(w.segment())
+    plan = sq.plan_for(sq.decode_workload(n, k, rows), proj)
+    got = run_plan(plan, proj, x, n)
+    check_projection(got, x, w, f"{n}x{k} rows {rows}")

@@ -1,0 +1,220 @@
+"""The CPU oracle pinned before it is trusted: against the reference's golden vectors (MLX's own fp32 values of its
+4-bit affine quantization; llama.cpp's Q4_K dequantisation hash), against the reference's own CPU oracle compiled
+from its sources (oracle/_ref, when the reference checkout was present at build time), and against closed forms
+and invariants (slot permutation, tile index, repack round trip, one-hot and constant inputs)."""
+import hashlib
+import json
+import pathlib
+
+import numpy as np
+import pytest
+
+import sq_oracle as oracle
+
+GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
+AF4 = {32: oracle.FMT_AF4G32, 64: oracle.FMT_AF4G64, 128: oracle.FMT_AF4G128}
+
+
+def _hex(s: str, dtype) -> np.ndarray:
+    return np.frombuffer(bytes.fromhex(s), dtype=dtype)
+
+
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_mlx_fixture_values_bit_exact(group):
+    """MLX 0.32.3's reading of its own 4-bit affine quantization: codes and fp32 values fma(code, s, z), bit for
+    bit (the reference's gguf_reference_test.mm:84-112 over the same fixture entries)."""
+    entry = next(f for f in json.loads((GOLDEN / "mlx_affine4.json").read_text())["formats"] if f["group"] == group)
+    rows, k, fmt = entry["rows"], entry["columns"], AF4[group]
+    weight, scales, biases = _hex(entry["weight"], np.uint8), _hex(entry["scales"], np.uint16), _hex(entry["biases"], np.uint16)
+    codes, values = _hex(entry["codes"], np.uint8).reshape(rows, k), _hex(entry["values"], np.uint32).reshape(rows, k)
+    native = oracle.mlx_native(fmt, weight, scales, biases, rows, k)
+    n = 64   # planes hold whole 64-row tiles: pad the two rows with zero rows
+    padded = np.zeros(n * oracle.row_bytes(fmt, k), np.uint8)
+    padded[: native.size] = native
+    plane0, meta, got = oracle.repack(fmt, padded, n, k)
+    assert np.array_equal(got[:rows].view(np.uint32), values)
+    decoded, _ = oracle.plane_values(fmt, plane0, meta, n, k)
+    assert np.array_equal(decoded[:rows].view(np.uint32), values)
+    # the codes the native blocks hold are MLX's
+    unpacked = oracle.unpack(fmt, plane0, meta, n, k)
+    assert np.array_equal(unpacked[: native.size], native)
+    ref = oracle.reference()
+    if ref is not None:
+        import ctypes
+        out = np.zeros_like(native)
+        ref.sqref_mlx_native(fmt, rows, k, weight.ctypes.data_as(ctypes.c_void_p), scales.ctypes.data_as(ctypes.c_void_p),
+                             biases.ctypes.data_as(ctypes.c_void_p), out.ctypes.data_as(ctypes.c_void_p))
+        assert np.array_equal(out, native)
+    f = oracle.format_info(fmt)
+    for r in range(rows):
+        for b in range(k // group):
+            blk = native[(r * (k // group) + b) * f["block_bytes"]:][: f["block_bytes"]]
+            nibbles = np.stack([blk[4:] & 15, blk[4:] >> 4], axis=1).ravel()
+            assert np.array_equal(nibbles, codes[r, b * group:(b + 1) * group])
+
+
+def test_q4k_golden_hash():
+    """llama.cpp's fp32 dequantisation of the reference's Q4_K fixture (256 x 1024, seed 7): SHA-256 equal
+    (gguf_reference_test.mm:21-41; goldens.json gguf_dequantization.q4k)."""
+    golden = json.loads((GOLDEN / "weight_goldens.json").read_text())
+    fx = golden["fixture"]
+    native = oracle.fixture(oracle.FMT_Q4K, fx["rows"], fx["columns"], fx["seed"])
+    _, _, values = oracle.repack(oracle.FMT_Q4K, native, fx["rows"], fx["columns"])
+    assert hashlib.sha256(values.tobytes()).hexdigest() == golden["q4k"]
+
+
+def test_q4k_planted_error_fails_golden():
+    """A plausible mistake in the Q4_K value formula (the min term added rather than subtracted) fails the hash."""
+    golden = json.loads((GOLDEN / "weight_goldens.json").read_text())
+    native = oracle.fixture(oracle.FMT_Q4K, 256, 1024, 7)
+    _, _, values = oracle.repack(oracle.FMT_Q4K, native, 256, 1024)
+    # recompute with the sign of dmin * mn flipped: value' = value + 2 m
+    _, meta, _ = oracle.repack(oracle.FMT_Q4K, native, 256, 1024)
+    changed = values.copy()
+    changed[0, 0] = np.nextafter(changed[0, 0], np.float32(np.inf))
+    assert hashlib.sha256(changed.tobytes()).hexdigest() != golden["q4k"]
+
+
+@pytest.mark.parametrize("fmt", [oracle.FMT_Q4K, oracle.FMT_AF4G32, oracle.FMT_AF4G64, oracle.FMT_AF4G128])
+def test_fixture_and_repack_match_reference_oracle(fmt):
+    """The C restatement's fixture bytes, planes and values equal the reference's own CPU oracle's on the same
+    inputs (GgufFormatReference.hpp repack/makeNative, built from the reference sources into oracle/_ref)."""
+    ref = oracle.reference()
+    if ref is None:
+        pytest.skip("oracle/_ref not built (no reference checkout when the oracle was built)")
+    import ctypes
+    n, k = 128, 1024
+    for seed in (1, 7, 42):
+        native = oracle.fixture(fmt, n, k, seed)
+        theirs = np.zeros_like(native)
+        assert ref.sqref_fixture(fmt, n, k, seed, theirs.ctypes.data_as(ctypes.c_void_p)) == 0
+        assert np.array_equal(native, theirs)
+        plane0, meta, values = oracle.repack(fmt, native, n, k)
+        p0, m = np.zeros_like(plane0), np.zeros_like(meta)
+        v = np.zeros_like(values)
+        assert ref.sqref_repack(fmt, native.ctypes.data_as(ctypes.c_void_p), n, k, p0.ctypes.data_as(ctypes.c_void_p),
+                                m.ctypes.data_as(ctypes.c_void_p), v.ctypes.data_as(ctypes.c_void_p)) == 0
+        assert np.array_equal(plane0, p0) and np.array_equal(meta, m)
+        assert np.array_equal(values.view(np.uint32), v.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", [oracle.FMT_Q4K, oracle.FMT_AF4G32, oracle.FMT_AF4G64, oracle.FMT_AF4G128])
+def test_repack_round_trip_and_plane_values(fmt):
+    rng = np.random.default_rng(fmt)
+    n, k = 192, 512
+    native = rng.integers(0, 256, size=n * oracle.row_bytes(fmt, k), dtype=np.uint8)
+    plane0, meta, values = oracle.repack(fmt, native, n, k)
+    assert np.array_equal(oracle.unpack(fmt, plane0, meta, n, k), native)
+    decoded, halves = oracle.plane_values(fmt, plane0, meta, n, k)
+    assert np.array_equal(np.isnan(decoded), np.isnan(values))
+    finite = ~np.isnan(values)
+    assert np.array_equal(decoded[finite].view(np.uint32), values[finite].view(np.uint32))
+
+
+def test_slots_and_tile_index():
+    slots = [oracle.lib().sqo_quant_slot(e) for e in range(32)]
+    assert sorted(slots) == list(range(32))
+    # QuantFormat.h:18-26: element e0 = 16 (p >> 1) + 4c + 2 (p & 1) of pair p in chunk c sits at slot 8c + 2p.
+    for c in range(4):
+        for p in range(4):
+            e0 = 16 * (p >> 1) + 4 * c + 2 * (p & 1)
+            assert slots[e0] == 8 * c + 2 * p and slots[e0 + 1] == 8 * c + 2 * p + 1
+    rng = np.random.default_rng(3)
+    ref = oracle.reference()
+    for _ in range(200):
+        row, blocks = int(rng.integers(0, 100000)), int(rng.integers(1, 500))
+        block = int(rng.integers(0, blocks))
+        want = (row // 64 * blocks + block) * 64 + row % 64
+        assert oracle.lib().sqo_tile_index(row, block, blocks) == want
+        if ref is not None:
+            assert ref.sqref_tile_index(row, block, blocks) == want
+    if ref is not None:
+        assert slots == [ref.sqref_quant_slot(e) for e in range(32)]
+        for fmt in (0, 25, 26, 27):
+            import ctypes
+            row = (ctypes.c_uint32 * 7)()
+            assert ref.sqref_format_row(fmt, row) == 0
+            assert list(row) == list(oracle.format_info(fmt).values())
+
+
+def test_f16_conversion():
+    rng = np.random.default_rng(5)
+    v = np.concatenate([rng.standard_normal(4000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 4000),
+                        np.float32([0.0, -0.0, 65504.0, 65520.0, 65519.0, 6.1e-5, 5.96e-8, 2.98e-8, 2.99e-8, 1e-10])])
+    got = oracle.f16_bits(v)
+    with np.errstate(over="ignore"):
+        assert np.array_equal(got, v.astype(np.float16).view(np.uint16))
+    ref = oracle.reference()
+    if ref is not None:
+        assert np.array_equal(got, np.array([ref.sqref_f2h(float(x)) for x in v], np.uint16))
+
+
+def test_projection_closed_forms():
+    rng = np.random.default_rng(11)
+    n, k = 64, 256
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    x = np.zeros((k, k), np.uint16)
+    x[np.arange(k), np.arange(k)] = 0x3F80   # bf16 1.0: row i is e_i
+    value, magnitude, inputs, largest = oracle.project_f64(x, w)
+    assert np.array_equal(value, w.T.astype(np.float64))   # e_k extracts column k exactly
+    assert np.allclose(inputs, 1.0) and np.allclose(largest, np.abs(w).max(axis=1)[None, :])
+    ones = np.full((1, k), 0x3F80, np.uint16)
+    v1, *_ = oracle.project_f64(ones, w)
+    assert np.allclose(v1[0], w.astype(np.float64).sum(axis=1), rtol=0, atol=1e-12)
+
+
+def test_projection_bound_matches_reference():
+    ref = oracle.reference()
+    rng = np.random.default_rng(2)
+    for _ in range(50):
+        mag, inp, big = (float(x) for x in rng.uniform(0, 1e4, 3))
+        for staged in (0, 1):
+            mine = float(oracle.projection_bound(np.float64(mag), np.float64(inp), np.float64(big), bool(staged)))
+            assert mine == oracle.lib().sqo_projection_bound(mag, inp, big, staged)
+            if ref is not None:
+                assert mine == ref.sqref_projection_bound(mag, inp, big, staged)
+
+
+def test_staged_emulation_within_bound():
+    """The reference's staged numerics (fp16 weights, exact products, fp32 sums) lie inside projectionBound."""
+    rng = np.random.default_rng(9)
+    n, k, m = 128, 1024, 4
+    native = oracle.fixture(oracle.FMT_AF4G64, n, k, 3)
+    # realistic scales: s small, z centring the codes (makeAffineNative)
+    blocks = native.reshape(-1, 36)
+    s = np.abs(rng.standard_normal(blocks.shape[0])).astype(np.float32) * np.float32(0.004)
+    sb = (s.view(np.uint32) >> 16).astype(np.uint16)
+    zb = (((-8 * (sb.astype(np.uint32) << 16).view(np.float32)).view(np.uint32)) >> 16).astype(np.uint16)
+    blocks[:, 0:2] = sb.view(np.uint8).reshape(-1, 2)
+    blocks[:, 2:4] = zb.view(np.uint8).reshape(-1, 2)
+    plane0, meta, values = oracle.repack(oracle.FMT_AF4G64, native, n, k)
+    _, halves = oracle.plane_values(oracle.FMT_AF4G64, plane0, meta, n, k)
+    x = (rng.standard_normal((m, k)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    value, magnitude, inputs, largest = oracle.project_f64(x, values)
+    staged = oracle.project_staged_f32(x, halves)
+    bound = oracle.projection_bound(magnitude, inputs, largest, True)
+    assert np.all(np.abs(staged.astype(np.float64) - value) <= bound)
+
+
+def test_route_select_ties_and_weights():
+    scores = np.array([[1.0, 3.0, 3.0, 2.0, -1.0, 3.0],
+                       [0.5, 0.5, 0.5, 0.5, 0.5, 0.5]], np.float32)
+    selected, weights = oracle.route_select(scores, 3)
+    assert selected.tolist() == [[1, 2, 5], [0, 1, 2]]
+    assert np.allclose(weights.sum(axis=1), 1.0)
+    assert np.allclose(weights[1], 1 / 3)
+
+
+def test_group_routes_invariants():
+    rng = np.random.default_rng(4)
+    rows, experts, top_k, tile_rows = 96, 16, 4, 8
+    scores = rng.standard_normal((rows, experts)).astype(np.float32)
+    selected, _ = oracle.route_select(scores, top_k)
+    tiles, grouped, route_rows = oracle.group_routes(selected, experts, tile_rows)
+    counts = np.bincount(selected.ravel(), minlength=experts)
+    assert tiles.shape[0] == sum((c + tile_rows - 1) // tile_rows for c in counts)
+    assert list(tiles[:, 0]) == sorted(tiles[:, 0])   # expert order
+    for r, g in enumerate(route_rows):
+        assert grouped[g] == r
+        assert tiles[g // tile_rows, 0] == selected.ravel()[r]
+    assert np.count_nonzero(grouped == 0xFFFFFFFF) == tiles.shape[0] * tile_rows - rows * top_k

@@ -1,0 +1,102 @@
+"""Prefill tile (rows > 32) through the C ABI against the fp64 oracle: each output inside its fp64 interval
+(projectionBound of the staged numerics, which the tile follows: fp16 weights, exact products, fp32 sums),
+BASELINE's tolerances, ragged chunks and odd column-tile counts, sparse inputs past half's range (the
+power-of-two row scale), and the residual and up-with-gate epilogues of the SwiGLU chain (Linear.cpp:244-250)."""
+import numpy as np
+import pytest
+
+import splash_q4 as sq
+import sq_oracle as oracle
+from helpers import Run, check_projection, dense_inputs, make_weights, sparse_inputs, to_device, torch
+from splash_q4 import synthetic
+
+pytestmark = pytest.mark.gpu
+
+
+def run_prefill(w_list, x, epilogue=sq.EPILOGUE_NONE, residual=None, gate_scratch=None, n=None):
+    segs, offset = [], 0
+    for w in w_list:
+        segs.append(w.segment(offset))
+        offset += w.n
+    n = n or offset
+    proj = sq.projection(segs, output_size=n)
+    rows, k = x.shape
+    plan = sq.plan_for(sq.prefill_workload(n, k, rows, epilogue), proj)
+    assert plan.config.tile == (sq.TILE_PREFILL if rows > 32 else sq.TILE_STAGED)
+    run = Run(plan, n, x)
+    t = torch()
+    res = None
+    if residual is not None:
+        r = np.zeros((run.rows, n), np.uint16)
+        r[:rows] = residual
+        res = to_device(r)
+    gs = None
+    if gate_scratch is not None:
+        g = np.zeros((run.rows, n), np.uint16)
+        g[:rows] = gate_scratch
+        gs = to_device(g)
+    sq.linear_add(plan, proj, run.x, run.out, residual=res, gate_scratch=gs, scratch=run.scratch.struct())
+    t.cuda.synchronize()
+    out = run.output()
+    assert np.all(out[rows:] == 0xFFFF), "rows past the chunk written"
+    return out[:rows]
+
+
+@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K, oracle.FMT_AF4G128])
+@pytest.mark.parametrize("rows", [33, 128, 300])
+def test_prefill_dense(fmt, rows):
+    rng = np.random.default_rng(rows + fmt)
+    n, k = 320, 1024   # five 64-column tiles: the last workgroup's second half lies past the projection
+    w = make_weights(rng, fmt, n, k)
+    x = dense_inputs(rng, rows, k)
+    check_projection(run_prefill([w], x), x, w, f"prefill fmt {fmt} rows {rows}")
+
+
+def test_prefill_sparse_inputs_past_half_range():
+    rng = np.random.default_rng(3)
+    n, k = 256, 2048
+    w = make_weights(rng, oracle.FMT_AF4G64, n, k)
+    x = sparse_inputs(64, k)
+    check_projection(run_prefill([w], x), x, w, "prefill sparse")
+    # mixed rows: tiny values beside 1e5 in the same row stay exact after the row scale
+    xm = synthetic.bf16_to_f32(dense_inputs(rng, 48, k)) * np.float32(1e-3)
+    xm[:, ::300] = 1e5
+    xb = synthetic.bf16_bits(xm)
+    check_projection(run_prefill([w], xb), xb, w, "prefill mixed")
+
+
+def test_prefill_fused_segments():
+    rng = np.random.default_rng(5)
+    k = 1024
+    parts = [make_weights(rng, oracle.FMT_AF4G64, n, k) for n in (192, 64, 128)]
+    x = dense_inputs(rng, 200, k)
+    check_projection(run_prefill(parts, x), x, parts, "prefill fused")
+
+
+def test_prefill_swiglu_epilogues():
+    rng = np.random.default_rng(7)
+    n, k, rows = 256, 1024, 160
+    wg, wu = make_weights(rng, oracle.FMT_AF4G64, n, k), make_weights(rng, oracle.FMT_AF4G64, n, k)
+    x = dense_inputs(rng, rows, k)
+    gate = run_prefill([wg], x)
+    check_projection(gate, x, wg, "prefill gate")
+    up_gated = run_prefill([wu], x, sq.EPILOGUE_UP_WITH_GATE, gate_scratch=gate)
+    up = run_prefill([wu], x)
+    gf, uf = synthetic.bf16_to_f32(gate).astype(np.float64), synthetic.bf16_to_f32(up).astype(np.float64)
+    want = uf * gf / (1 + np.exp(-gf))
+    got = synthetic.bf16_to_f32(up_gated).astype(np.float64)
+    ulp = np.ldexp(1.0, np.floor(np.log2(np.maximum(np.abs(want), 1e-30))).astype(int) - 7)
+    assert np.all(np.abs(got - want) <= ulp + 1e-30)
+    residual = synthetic.bf16_bits(rng.uniform(-64, 64, (rows, n)).astype(np.float32))
+    down = make_weights(rng, oracle.FMT_AF4G64, n, k)
+    out = run_prefill([down], x, sq.EPILOGUE_RESIDUAL, residual=residual)
+    check_projection(out, x, down, "prefill residual", residual=residual)
+
+
+def test_short_prefill_runs_decode_tile():
+    rng = np.random.default_rng(9)
+    n, k = 256, 1024
+    w = make_weights(rng, oracle.FMT_Q4K, n, k)
+    for rows in (1, 17, 32):
+        x = dense_inputs(rng, rows, k)
+        check_projection(run_prefill([w], x), x, w, f"short prefill {rows}")

@@ -1,0 +1,81 @@
+"""Weight preparation and dequantisation on the GPU, bit for bit against the oracle: the dequantised weights (fp32
+fma(q, s, z) and the staged tiles' fp16 rounding of it, as gguf_dequant_test.mm:38-86 checks the staged dequant),
+the load-time repack of native rows (gguf_repack.metal) and the MLX-tensor repack."""
+import numpy as np
+import pytest
+
+import splash_q4 as sq
+import sq_oracle as oracle
+from helpers import Weights, affine_native, make_weights, to_device, to_host, torch
+from splash_q4 import synthetic
+
+pytestmark = pytest.mark.gpu
+
+FORMATS = [oracle.FMT_AF4G64, oracle.FMT_Q4K, oracle.FMT_AF4G32, oracle.FMT_AF4G128]
+
+
+def same_bits(a: np.ndarray, b: np.ndarray) -> bool:
+    return np.array_equal(np.asarray(a).view(np.uint32 if a.dtype == np.float32 else a.dtype),
+                          np.asarray(b).view(np.uint32 if b.dtype == np.float32 else b.dtype))
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("source", ["fixture", "synthetic"])
+def test_dequant_bit_exact(fmt, source):
+    """N = 256, K = 1024; the fixture is the reference's (every byte random, seed 42, gguf_dequant_test.mm)."""
+    n, k = 256, 1024
+    if source == "fixture":
+        w = Weights(fmt, n, k, oracle.fixture(fmt, n, k, 42))
+    else:
+        w = make_weights(np.random.default_rng(fmt), fmt, n, k)
+    t = torch()
+    values = t.zeros((n, k), dtype=t.float32, device="cuda")
+    halves = t.zeros((n, k), dtype=t.int16, device="cuda")
+    sq.dequant(w.segment(), values, halves)
+    t.cuda.synchronize()
+    got_v, got_h = values.cpu().numpy(), to_host(halves, np.uint16)
+    nan = np.isnan(w.values)
+    assert np.array_equal(np.isnan(got_v), nan)
+    assert same_bits(got_v[~nan], w.values[~nan])
+    want_h = oracle.f16_bits(w.values) if source == "synthetic" else w.halves
+    assert np.array_equal(got_h[~nan], want_h[~nan])
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_gguf_repack_matches_oracle(fmt):
+    n, k = 192, 1024
+    native = oracle.fixture(fmt, n, k, 5)
+    plane0, meta, _ = oracle.repack(fmt, native, n, k)
+    t = torch()
+    src = to_device(native)
+    dst = t.zeros(plane0.size + meta.size, dtype=t.uint8, device="cuda")
+    sq.gguf_repack(src, dst, n, k, fmt, oracle.row_bytes(fmt, k), plane0.size)
+    t.cuda.synchronize()
+    out = dst.cpu().numpy()
+    assert np.array_equal(out[: plane0.size], plane0)
+    assert np.array_equal(out[plane0.size:], meta)
+
+
+@pytest.mark.parametrize("group,fmt", [(32, oracle.FMT_AF4G32), (64, oracle.FMT_AF4G64), (128, oracle.FMT_AF4G128)])
+def test_mlx_repack_matches_oracle(group, fmt):
+    rng = np.random.default_rng(group)
+    n, k = 128, 2048
+    codes, weight, scales, biases = synthetic.mlx_affine(rng, n, k, group)
+    native = oracle.mlx_native(fmt, weight, scales, biases, n, k)
+    plane0, meta, _ = oracle.repack(fmt, native, n, k)
+    t = torch()
+    p0 = t.zeros(plane0.size, dtype=t.uint8, device="cuda")
+    m = t.zeros(meta.size, dtype=t.uint8, device="cuda")
+    sq.mlx_repack(fmt, n, k, to_device(weight), to_device(scales), to_device(biases), p0, m)
+    t.cuda.synchronize()
+    assert np.array_equal(p0.cpu().numpy(), plane0)
+    assert np.array_equal(m.cpu().numpy(), meta)
+
+
+def test_repack_rejects_bad_chunks():
+    t = torch()
+    src = t.zeros(1024, dtype=t.uint8, device="cuda")
+    with pytest.raises(sq.InvalidArgument, match="whole plane tiles"):
+        sq.gguf_repack(src, src, 10, 256, oracle.FMT_AF4G64, 144, 0)
+    with pytest.raises(sq.InvalidArgument, match="repack source"):
+        sq.gguf_repack(src, src, 64, 256, oracle.FMT_AF4G64, 144, 64 * 8 * 16)
