@@ -42,18 +42,15 @@ constexpr uint32_t kPrefillTileRows = 128;
 // The decode tile holds at most four lanes of rows; prefill chunks of up to that many rows run it too.
 constexpr uint32_t kMaximumStagedRows = SQ_MAXIMUM_DECODE_ROWS;
 
-// Groups of 32 inputs one scale covers, whose multiples a K partition must take: af4g128's four when the formats
-// are unknown.
-uint32_t scaleGroups(uint32_t format) {
-  return format == SQ_FMT_AF4G128 ? 4 : format == SQ_FMT_AF4G64 ? 2 : 1;
-}
+// Groups of 32 inputs per meta unit, whose multiples a K partition of the decode tile takes: Q4_K's eight (a
+// super-block) when the formats are unknown.
 uint32_t planScaleGroups(const Projection *p, const Projection *gate) {
   uint32_t unit = 1;
   bool any = false;
   for (const Projection *q : {p, gate})
     if (q)
-      for (const QuantizedSegment &s : q->blocks().segments) unit = std::max(unit, scaleGroups(s.formatId)), any = true;
-  return any ? unit : 4;
+      for (const QuantizedSegment &s : q->blocks().segments) unit = std::max(unit, s.format().meta_groups), any = true;
+  return any ? unit : 8;
 }
 
 // The projection is the plan's matrix and each segment fills whole 64-column tiles of it (LinearGguf.cpp:324-332).
@@ -164,10 +161,10 @@ LinearScratchSize LinearPlan::scratchSize() const noexcept {
     const uint64_t rows = storageRows();
     return {rows * k * 2, rows * 4, 0, 0, 0};
   }
+  // Counters: one per workgroup column of the decode tile, at most one per 16 destination columns.
   const uint64_t columns = config_.oneGateUpPass ? 2 * uint64_t{n} : n;
-  const uint32_t tile = config_.oneGateUpPass ? 32 : SQ_TILE_COLUMNS;
   return config_.splits > 1 ? LinearScratchSize{0, 0, uint64_t{config_.splits} * storageRows() * columns * 4,
-                                                uint64_t{n / tile} * 4, 0}
+                                                uint64_t{n / 16} * 4, 0}
                             : LinearScratchSize{};
 }
 
@@ -177,33 +174,52 @@ uint64_t LinearPlan::gateScratchBytes() const noexcept {
   return needed ? uint64_t{storageRows()} * workload_.matrix.outputSize * 2 : 0;
 }
 
-// MI355X's split law. A dispatch streams the weights once plus, split, each partition's fp32 partials written and
-// read back; it runs at HBM's rate once the grid holds two of the tile's 256-thread workgroups per compute unit and
-// proportionally slower below that. The split of least modelled time wins, ties to fewer partitions; a partition
-// takes whole scale groups.
-uint32_t Linear::decodeSplits(uint32_t n, uint32_t k, uint32_t rows, uint32_t groupUnit) const noexcept {
-  const uint32_t G = k / 32, tiles = n / SQ_TILE_COLUMNS;
-  const double weights = double(n) * k * 0.5625, saturation = 2.0 * computeUnits_;
-  uint32_t best = 1;
-  double least = INFINITY;
+// MI355X's split law. The decode tiles are HBM-bound and a split adds a reduction tail (partials stored, a counter,
+// partials read back: three device-scope round trips after the workgroup's last load). A partition takes whole
+// meta units. The split depends on the shape and the tile kind the rows run, never on the rows themselves, so a
+// row's result is the same in any batch of its kind.
+//  - Column tile: one workgroup per 64-column tile and split streams its K slices; the split with the least
+//    estimated time, where a workgroup streams at most kWorkgroupBandwidth (one compute unit's load rate), the
+//    device kHbmBandwidth, and each split past the first adds kSplitTail (fewest splits on a tie).
+//  - Row tile: the fewest splits whose layout holds each wave's slice in registers and whose grid has a workgroup
+//    for each compute unit.
+namespace {
+constexpr double kWorkgroupBandwidth = 55e9, kHbmBandwidth = 6.5e12, kSplitTail = 2.5e-6;   // measured on MI355X
+}  // namespace
+
+uint32_t Linear::decodeSplits(uint32_t n, uint32_t k, uint32_t rows, uint32_t groupUnit, bool pair) const noexcept {
+  const uint32_t G = k / 32, blocks = n / 16;
+  const uint32_t format = groupUnit == 8 ? SQ_FMT_Q4K : groupUnit == 4 ? SQ_FMT_AF4G128
+                        : groupUnit == 2 ? SQ_FMT_AF4G64 : SQ_FMT_AF4G32;
+  const bool column = rows <= kern::kColumnTileRows;
+  const double bytes = (pair ? 2.0 : 1.0) * n * (k * 0.5 + G * 4.0 / groupUnit);
+  uint32_t best = 0;
+  double bestTime = 0;
   for (uint32_t s = 1; s <= LinearConfig::kMaximumSplits && G % (s * groupUnit) == 0; s *= 2) {
-    const double occupancy = std::min(1.0, double(tiles) * s / saturation);
-    const double bytes = weights + (s > 1 ? 8.0 * s * rows * n : 0.0);
-    const double time = bytes / occupancy;
-    if (time < least * 0.97) least = time, best = s;
+    const kern::DecodeLayout layout = kern::decode_layout(format, blocks, k, s, pair, rows);
+    if (!layout.nb) continue;
+    if (column) {
+      const double workgroups = std::min<double>(uint64_t{n / 64} * s, computeUnits_);
+      const double t = std::max(bytes / (workgroups * kWorkgroupBandwidth), bytes / kHbmBandwidth) +
+                       (s > 1 ? kSplitTail : 0.0);
+      if (!best || t < bestTime) best = s, bestTime = t;
+      continue;
+    }
+    best = s;
+    if (uint64_t{blocks / layout.nb} * s >= computeUnits_) break;
   }
-  return best;
+  return best ? best : 1;
 }
 
 LinearConfig Linear::baseline(LinearWorkload w, const Projection *p, const Projection *gate) const {
   const auto [n, k] = w.matrix;
   if (w.phase == LinearPhase::Prefill && w.rows > kMaximumStagedRows) return {.tile = LinearTile::GgufPrefill};
-  LinearConfig c{.tile = LinearTile::GgufStaged, .splits = decodeSplits(n, k, w.rows, planScaleGroups(p, gate))};
   // A gate/up pair of single tensors of one format runs in one dispatch: both walks share the activations' loads.
-  if (w.phase == LinearPhase::Decode && w.epilogue == LinearEpilogue::GateUp && p && gate &&
-      p->blocks().segments.size() == 1 && gate->blocks().segments.size() == 1 &&
-      p->blocks().segments.front().formatId == gate->blocks().segments.front().formatId)
-    c.oneGateUpPass = true;
+  const bool pair = w.phase == LinearPhase::Decode && w.epilogue == LinearEpilogue::GateUp && p && gate &&
+                    p->blocks().segments.size() == 1 && gate->blocks().segments.size() == 1 &&
+                    p->blocks().segments.front().formatId == gate->blocks().segments.front().formatId;
+  LinearConfig c{.tile = LinearTile::GgufStaged, .splits = decodeSplits(n, k, w.rows, planScaleGroups(p, gate), pair)};
+  c.oneGateUpPass = pair;
   return c;
 }
 
@@ -273,8 +289,14 @@ void Linear::add(hipStream_t graph, LinearBuffers b, const Projection &p, const 
     throw std::invalid_argument("an fp32 destination takes a single-tensor block projection");
   const LinearConfig config = selected.configuration();
   const uint32_t groupUnit = planScaleGroups(&p, gate);
-  if (config.tile == LinearTile::GgufStaged && (k / 32) % (config.splits * groupUnit))
-    throw std::invalid_argument("a K partition of the staged tile takes whole scale groups of the projection's format");
+  if (config.tile == LinearTile::GgufStaged) {
+    if ((k / 32) % (config.splits * groupUnit))
+      throw std::invalid_argument("a K partition of the staged tile takes whole scale groups of the projection's format");
+    for (const QuantizedSegment &s : segments)
+      if (!kern::decode_layout(s.formatId, n / 16, k, config.splits, config.oneGateUpPass, w.rows).nb)
+        throw std::invalid_argument("the staged tile holds at most 256 groups of 32 inputs per K partition (64 for a "
+                                    "one-pass gate/up): take more splits");
+  }
   if (w.epilogue == LinearEpilogue::GateUp) {
     if (segments.size() != 1 || gate->blocks().segments.size() != 1)
       throw std::invalid_argument("block gate/up takes single tensors");
@@ -332,18 +354,19 @@ void Linear::add(hipStream_t graph, LinearBuffers b, const Projection &p, const 
     const QuantizedSegment &g = gate->blocks().segments.front(), &u = segments.front();
     if (g.formatId != u.formatId || g.columnOffset != u.columnOffset)
       throw std::invalid_argument("a one-pass block gate/up takes single tensors of one format");
-    kern::GateUpArgs a{};
+    kern::DecodeArgs a{};
     a.input = b.input.as<const uint16_t>();
+    a.seg[0] = kernelSegment(u);
+    a.segments = 1;
     a.gate = kernelSegment(g);
-    a.up = kernelSegment(u);
-    a.output = b.output.as<uint16_t>();
+    a.output = b.output.ptr;
     a.partials = b.scratch.partials.as<float>();
     a.counters = b.scratch.counters.as<uint32_t>();
     a.K = k;
     a.rows = w.rows;
     a.splits = config.splits;
     a.out_stride = n;
-    requireLaunch(kern::launch_decode_gate_up(u.formatId, a, graph), "gate/up decode tile");
+    requireLaunch(kern::launch_decode(u.formatId, kern::EpNone, false, a, graph), "gate/up decode tile");
     return;
   }
   if (w.epilogue == LinearEpilogue::GateUp) {

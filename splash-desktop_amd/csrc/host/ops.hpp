@@ -173,7 +173,8 @@ public:
   void addPrefillSwiGlu(hipStream_t graph, const SwiGluProjections &ffn, const PrefillFfnBuffers &buffers,
                         Buffer residual, Buffer output, uint32_t rows) const;
   // The K partitions the decode tile splits an n x k projection of `rows` rows into on this device.
-  [[nodiscard]] uint32_t decodeSplits(uint32_t n, uint32_t k, uint32_t rows, uint32_t groupUnit) const noexcept;
+  [[nodiscard]] uint32_t decodeSplits(uint32_t n, uint32_t k, uint32_t rows, uint32_t groupUnit,
+                                      bool pair = false) const noexcept;
 
 private:
   [[nodiscard]] LinearConfig baseline(LinearWorkload workload, const Projection *projection,

@@ -1,0 +1,243 @@
+// The column tile of the decode GEMV: y[r][c] = sum_k x[r][k] w[c][k] for one to four rows of bf16 activations
+// against 4-bit plane weights, fp32 accumulation (reference: gguf_decode / gguf_decode_tile,
+// kernels/shared/gguf_linear.metal:71-192, with its K-split reduction, kernels/shared/split_reduce.h:14-45).
+//
+// CDNA4 mapping. The GEMV is HBM-bound at 0.5625 bytes per weight, so every lane owns one output column of a
+// 64-column plane tile and the wave reads the tile's codes as they lie in the plane: per group of 32 inputs, one
+// 16-byte load per lane (the column's 32 codes) and 1 KiB per wave, fully coalesced.
+//  - The 32 codes become 32 exact bf16 operands 128 + q (one v_and_or_b32 per operand pair, code_pairs) and
+//    meet the activations in eight 4x4x4 bf16 MFMAs whose B is the lane's own column (two accumulation chains); the
+//    activations (A) of the MFMA's sixteen blocks are broadcast from one block (cbsz 4, abid): lane (b, i) holds row
+//    i's inputs 4b..4b+3 of a pair of groups, so one 8-byte load per lane covers 64 inputs of up to four rows, and D
+//    gives each lane its own column for the four rows.
+//  - Each scale group closes in fp32: acc += s * sum x (128 + q) + (z - 128 s) * sum x, every product exact; the
+//    rows' input sums come from a wave butterfly over the same activation registers, read out into scalars.
+//  - A workgroup of W waves takes one tile and W K slices of GW groups each (the split's last slice may be
+//    shorter; slices start on meta units). Each wave streams its slice with P groups in flight: codes, meta and
+//    activations are issued in the order they are consumed, every load unconditional (addresses past the slice
+//    repeat its last group and are not computed on), so the wait counts stay exact and every wave draws bandwidth
+//    for the whole dispatch instead of in one burst. The slices meet in LDS in slice order.
+//  - One workgroup covers a tile's whole K unless the launcher's layout splits it: a split across workgroups adds
+//    three device-scope round trips at the end of the dispatch (split_reduce), which only pays when the tiles alone
+//    leave most compute units idle.
+// A row's result depends only on its own activations and the layout (split, GW), never on the other rows.
+#include "device.hpp"
+#include "kernels.hpp"
+#include "split.hpp"
+
+namespace sq::kern {
+namespace {
+
+constexpr int kPipe = 4;   // groups in flight per wave
+
+// Row i's inputs 4b..4b+3 of the pair, as fp32, summed in a fixed order.
+__device__ __forceinline__ float quad_sum(u32x2 v) {
+  const float x0 = __uint_as_float(v[0] << 16), x1 = __uint_as_float(v[0] & 0xFFFF0000u);
+  const float x2 = __uint_as_float(v[1] << 16), x3 = __uint_as_float(v[1] & 0xFFFF0000u);
+  return (x0 + x1) + (x2 + x3);
+}
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+template <uint32_t FMT, int MR, int GW, int NT, uint32_t EP, bool F32OUT>
+__global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs a) {
+  using F = Fmt<FMT>;
+  constexpr int SG = F::SG, UNIT = F::UNIT, P = GW < kPipe ? GW : kPipe;
+  static_assert(GW % UNIT == 0 && GW % 2 == 0 && GW % SG == 0, "a slice holds whole meta units and group pairs");
+  const int lane = threadIdx.x & 63, b = lane >> 2, i = lane & 3;
+  const uint32_t slice = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), waves = blockDim.x >> 6;
+  const uint32_t split = blockIdx.y;
+  uint32_t tile = blockIdx.x, s = 0;
+  while (s + 1 < a.segments && tile >= a.seg[s].tiles) tile -= a.seg[s++].tiles;
+  const Segment seg = a.seg[s];
+  const uint32_t G = a.K >> 5, units = G / UNIT, gs = G / a.splits;
+  const uint32_t gb = split * gs + slice * GW, live = min((uint32_t)GW, gs - min(gs, slice * GW));
+  const uint32_t last = live ? live - 1 : 0;
+
+  const uint8_t *plane[NT], *meta[NT];
+  {
+    const size_t pbase = ((size_t)tile * G * 64 + lane) * 16 + (size_t)gb * 1024;
+    const size_t mbase = ((size_t)tile * units * 64 + lane) * F::META + (size_t)(gb / UNIT) * 64 * F::META;
+    plane[0] = (NT == 2 ? a.gate.plane0 : seg.plane0) + pbase;
+    meta[0] = (NT == 2 ? a.gate.meta : seg.meta) + mbase;
+    if constexpr (NT == 2) {
+      plane[1] = seg.plane0 + pbase;
+      meta[1] = seg.meta + mbase;
+    }
+  }
+  // Lane (b, i) reads row i's inputs 4 (b % 8)..+3 of the pair's group b / 8; rows past the live ones read row 0,
+  // whose MFMA rows nothing reads.
+  const uint16_t *xrow = a.input + (size_t)(i < MR && (uint32_t)i < a.rows ? i : 0) * a.K + 4 * (b & 7) + (size_t)gb * 32;
+  const CodeConstants cc = make_code_constants();
+
+  float acc[NT][MR];
+#pragma unroll
+  for (int n = 0; n < NT; ++n)
+#pragma unroll
+    for (int r = 0; r < MR; ++r) acc[n][r] = 0.0f;
+
+  u32x2 xp[GW / 2];
+  u32x4 codes[NT][GW];
+  MetaWords mw[NT][GW / UNIT];
+  const auto issue = [&](int u) __attribute__((always_inline)) {
+    if (u % 2 == 0) xp[u / 2] = *(const u32x2 *)(xrow + (size_t)min((uint32_t)(u + (b >> 3)), last) * 32);
+    if (u % UNIT == 0) {
+      const uint32_t v = min((uint32_t)(u / UNIT), last / UNIT);
+#pragma unroll
+      for (int n = 0; n < NT; ++n) mw[n][u / UNIT] = load_meta<FMT>(meta[n] + (size_t)v * 64 * F::META);
+    }
+    const uint32_t g = min((uint32_t)u, last);
+#pragma unroll
+    for (int n = 0; n < NT; ++n) codes[n][u] = __builtin_nontemporal_load((const u32x4 *)(plane[n] + (size_t)g * 1024));
+  };
+#pragma unroll
+  for (int u = 0; u < P; ++u) issue(u);
+
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 C0[NT], C1[NT];
+  float pair_sum = 0.0f;   // lane's butterfly value of the current pair
+  float sx[MR];            // the rows' input sums over the current scale group
+#pragma unroll
+  for (int u = 0; u < GW; ++u) {
+    if (u + P < GW) issue(u + P);
+    __builtin_amdgcn_sched_barrier(0);
+    if ((uint32_t)u < live) {
+      const int p = u >> 1, h = u & 1;
+      if (h == 0) {
+        float t = quad_sum(xp[p]);
+        t += __shfl_xor(t, 4);
+        t += __shfl_xor(t, 8);
+        t += __shfl_xor(t, 16);   // lanes b < 8: group 2p's sum; b >= 8: group 2p + 1's
+        if constexpr (SG > 1) t += __shfl_xor(t, 32);
+        pair_sum = t;
+      }
+      if constexpr (SG == 1) {
+#pragma unroll
+        for (int r = 0; r < MR; ++r) sx[r] = lane_value(pair_sum, 32 * h + r);
+      } else if (h == 0) {
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+          const float v = lane_value(pair_sum, r);
+          sx[r] = u % SG == 0 ? v : sx[r] + v;
+        }
+      }
+      const bool first = u % SG == 0;
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const u32x4 w = code_pairs(codes[n][u][d], cc);
+          C0[n] = mfma_bcast(8 * h + d, xp[p], u32x2{w[0], w[1]}, first && d == 0 ? zero : C0[n]);
+          C1[n] = mfma_bcast(8 * h + 4 + d, xp[p], u32x2{w[2], w[3]}, first && d == 0 ? zero : C1[n]);
+        }
+      if ((u + 1) % SG == 0) {
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+          const Coef k = coef<FMT>(mw[n][u / UNIT], u);
+          const float zc = fmaf(-128.0f, k.s, k.z);
+#pragma unroll
+          for (int r = 0; r < MR; ++r) {
+            acc[n][r] = fmaf(k.s, C0[n][r] + C1[n][r], acc[n][r]);
+            acc[n][r] = fmaf(zc, sx[r], acc[n][r]);
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // Slices meet in LDS; the slice-0 wave adds them in slice order.
+  __shared__ float red[kColumnMaxWaves][NT][MR][64];
+#pragma unroll
+  for (int n = 0; n < NT; ++n)
+#pragma unroll
+    for (int r = 0; r < MR; ++r) red[slice][n][r][lane] = acc[n][r];
+  __syncthreads();
+  const bool owner = slice == 0;
+  const uint32_t col = seg.out_offset + tile * 64 + lane;
+  const uint32_t cstride = NT == 2 ? 2 * a.out_stride : a.out_stride;
+  float total[NT][MR];
+  bool rlive[NT][MR];
+  size_t index[NT][MR];
+#pragma unroll
+  for (int n = 0; n < NT; ++n)
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+      float v = 0.0f;
+      if (owner)
+        for (uint32_t w = 0; w < waves; ++w) v += red[w][n][r][lane];
+      total[n][r] = v;
+      rlive[n][r] = (uint32_t)r < a.rows;
+      index[n][r] = (size_t)r * cstride + n * a.out_stride + col;
+    }
+  if (a.splits > 1 && !split_reduce<NT, MR>(total, rlive, index, a.partials, (size_t)a.rows * cstride, split,
+                                            a.splits, a.counters + blockIdx.x, owner))
+    return;
+  if (!owner) return;
+#pragma unroll
+  for (int r = 0; r < MR; ++r) {
+    if ((uint32_t)r >= a.rows) continue;
+    const size_t o = (size_t)r * a.out_stride + col;
+    if constexpr (NT == 2) {
+      const float g = bf16_to_f32(f32_to_bf16(total[0][r])), up = bf16_to_f32(f32_to_bf16(total[1][r]));
+      ((uint16_t *)a.output)[o] = f32_to_bf16(up * silu(g));
+    } else {
+      const float v = epilogue<EP>(total[0][r], a.aux, o);
+      if constexpr (F32OUT) ((float *)a.output)[o] = v;
+      else ((uint16_t *)a.output)[o] = f32_to_bf16(v);
+    }
+  }
+}
+
+template <uint32_t FMT, int MR, int NT, uint32_t EP, bool F32OUT>
+hipError_t launch_mr(const DecodeArgs &a, uint32_t tiles, DecodeLayout layout, hipStream_t stream) {
+  const dim3 grid(tiles, a.splits), block(64 * layout.nb);
+  switch (layout.ks) {
+    case 8: hipLaunchKernelGGL((column_kernel<FMT, MR, 8, NT, EP, F32OUT>), grid, block, 0, stream, a); break;
+    case 16: hipLaunchKernelGGL((column_kernel<FMT, MR, 16, NT, EP, F32OUT>), grid, block, 0, stream, a); break;
+    default:
+      if constexpr (NT == 1) hipLaunchKernelGGL((column_kernel<FMT, MR, 32, NT, EP, F32OUT>), grid, block, 0, stream, a);
+      break;
+  }
+  return hipGetLastError();
+}
+
+template <uint32_t FMT, int NT, uint32_t EP, bool F32OUT>
+hipError_t launch_rows(const DecodeArgs &a, uint32_t tiles, DecodeLayout layout, hipStream_t stream) {
+  return a.rows <= 1 ? launch_mr<FMT, 1, NT, EP, F32OUT>(a, tiles, layout, stream)
+                     : launch_mr<FMT, 4, NT, EP, F32OUT>(a, tiles, layout, stream);
+}
+
+template <uint32_t FMT>
+hipError_t launch_format(uint32_t epilogue, bool f32_output, bool pair, const DecodeArgs &a, uint32_t tiles,
+                         DecodeLayout layout, hipStream_t stream) {
+  if (pair) return launch_rows<FMT, 2, EpNone, false>(a, tiles, layout, stream);
+  if (f32_output) return launch_rows<FMT, 1, EpNone, true>(a, tiles, layout, stream);
+  switch (epilogue) {
+    case EpNone: return launch_rows<FMT, 1, EpNone, false>(a, tiles, layout, stream);
+    case EpResidual: return launch_rows<FMT, 1, EpResidual, false>(a, tiles, layout, stream);
+    default: return launch_rows<FMT, 1, EpUpWithGate, false>(a, tiles, layout, stream);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_decode_column(uint32_t fmt, uint32_t epilogue, bool f32_output, const DecodeArgs &a,
+                                hipStream_t stream) {
+  uint32_t tiles = 0;
+  for (uint32_t s = 0; s < a.segments; ++s) tiles += a.seg[s].tiles;
+  const bool pair = a.gate.plane0 != nullptr;
+  // nb: the workgroup's waves (K slices), ks: a slice's groups of 32 inputs.
+  const DecodeLayout layout = decode_layout(fmt, tiles * 4, a.K, a.splits, pair, a.rows);
+  if (!a.rows || a.rows > kColumnTileRows || !layout.nb) return hipErrorInvalidValue;
+  switch (fmt) {
+    case SQ_FMT_AF4G32: return launch_format<SQ_FMT_AF4G32>(epilogue, f32_output, pair, a, tiles, layout, stream);
+    case SQ_FMT_AF4G64: return launch_format<SQ_FMT_AF4G64>(epilogue, f32_output, pair, a, tiles, layout, stream);
+    case SQ_FMT_AF4G128: return launch_format<SQ_FMT_AF4G128>(epilogue, f32_output, pair, a, tiles, layout, stream);
+    case SQ_FMT_Q4K: return launch_format<SQ_FMT_Q4K>(epilogue, f32_output, pair, a, tiles, layout, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace sq::kern

@@ -13,6 +13,7 @@ typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
 typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short i16x4;
 
 // D = A B + C on a 16x16x32 bf16 tile. Lane l holds A[l % 16][8 (l / 16) + i], B[8 (l / 16) + i][l % 16] and
 // D[4 (l / 16) + i][l % 16] (i = 0..7, 0..7, 0..3).
@@ -25,12 +26,47 @@ __device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
                                                  0);
 }
 
+// D = A B + C on sixteen 4x4x4 bf16 blocks with block `abid`'s A broadcast to all sixteen (cbsz 4). Lane 4b + i holds
+// A[b][i][0..3] and B[b][0..3][i] (block b = lane / 4) and D[b][0..3][i]: with the broadcast, lane l's D is the four
+// A rows of block abid against the lane's own four B values. abid folds to a constant once the caller's loop is
+// unrolled (the instruction takes it as an immediate).
+__device__ __forceinline__ f32x4 mfma_bcast(int abid, u32x2 a, u32x2 b, f32x4 c) {
+  const i16x4 av = __builtin_bit_cast(i16x4, a), bv = __builtin_bit_cast(i16x4, b);
+#define SQ_MFMA_BCAST(k) \
+  case k: return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(av, bv, c, 4, k, 0);
+  switch (abid) {
+    SQ_MFMA_BCAST(0) SQ_MFMA_BCAST(1) SQ_MFMA_BCAST(2) SQ_MFMA_BCAST(3)
+    SQ_MFMA_BCAST(4) SQ_MFMA_BCAST(5) SQ_MFMA_BCAST(6) SQ_MFMA_BCAST(7)
+    SQ_MFMA_BCAST(8) SQ_MFMA_BCAST(9) SQ_MFMA_BCAST(10) SQ_MFMA_BCAST(11)
+    SQ_MFMA_BCAST(12) SQ_MFMA_BCAST(13) SQ_MFMA_BCAST(14) default: break;
+  }
+  return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(av, bv, c, 4, 15, 0);
+#undef SQ_MFMA_BCAST
+}
+
 // The eight codes of plane word w as exact bf16 operands 128 + q, in chunk-element order: pair p (bits 4p and
 // 16 + 4p) gives operands 2p and 2p + 1. bf16 0x4300 is 128 with unit spacing, so or-ing a code into its mantissa
 // makes 128 + code exactly.
 __device__ __forceinline__ u32x4 code_operands(uint32_t w) {
   const uint32_t m = 0x000F000Fu, o = 0x43004300u;
   return u32x4{(w & m) | o, ((w >> 4) & m) | o, ((w >> 8) & m) | o, ((w >> 12) & m) | o};
+}
+// code_operands with each operand pair formed by one v_and_or_b32: the mask arrives in a scalar register and the
+// exponent 0x43004300 in a vector register (make_code_constants pins them there), so the compiler selects the
+// three-operand form itself; with literal constants gfx9 spends two instructions per pair (its three-operand
+// encoding takes no literal).
+struct CodeConstants {
+  uint32_t mask, exponent;
+};
+__device__ __forceinline__ CodeConstants make_code_constants() {
+  uint32_t mask = 0x000F000Fu, exponent = 0x43004300u;
+  asm volatile("" : "+s"(mask));
+  asm volatile("" : "+v"(exponent));
+  return {mask, exponent};
+}
+__device__ __forceinline__ u32x4 code_pairs(uint32_t w, CodeConstants c) {
+  return u32x4{(w & c.mask) | c.exponent, ((w >> 4) & c.mask) | c.exponent, ((w >> 8) & c.mask) | c.exponent,
+               ((w >> 12) & c.mask) | c.exponent};
 }
 // bf16 1.0 in every operand.
 __device__ __forceinline__ u32x4 ones_operand() { return u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u}; }

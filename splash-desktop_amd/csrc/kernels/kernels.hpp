@@ -19,33 +19,40 @@ struct Segment {
   uint32_t out_offset;
 };
 
-// The decode tile (rows <= 32): y[r][c] = sum_k x[r][k] w[c][k] over up to three segments of one format, grid
-// (sum of tiles, splits). Split partials are fp32 [split][rows][out_stride]; counters one per destination
-// 64-column tile (out_offset / 64 + tile), zero before and after each dispatch.
+// The decode tiles: y[r][c] = sum_k x[r][k] w[c][k] over up to three segments of one format. With gate.plane0 set,
+// gate (gate) and up (seg[0]) run in one pass and the output is bf16(bf16(up) silu(bf16(gate))). Split partials
+// are fp32 [split][rows][out_stride] (a gate/up pair's [split][rows][2 out_stride], gate's columns then up's);
+// counters one per workgroup column (grid.x, at most one per 16 destination columns), zero before and after each
+// dispatch.
+//  - The column tile (rows <= kColumnTileRows): grid (64-column tiles, splits) of up to kColumnMaxWaves waves, each
+//    lane one destination column.
+//  - The row tile (more rows): grid (16-column blocks / nb, splits), rows on the MFMA's 16-row side.
+constexpr uint32_t kColumnTileRows = 4;
+// The column tile's most waves (K slices) per workgroup, and the most groups of 32 inputs one wave streams.
+constexpr uint32_t kColumnMaxWaves = 16, kColumnMaxGroups = 32;
 struct DecodeArgs {
   const uint16_t *input;   // bf16 [rows][K]
   Segment seg[3];
   uint32_t segments;
+  Segment gate;            // a one-pass gate/up pair's gate (plane0 null otherwise)
   void *output;            // bf16 or fp32 [rows][out_stride]
   const uint16_t *aux;     // bf16 [rows][out_stride]: the residual, or the gate of an up-with-gate pass
   float *partials;
   uint32_t *counters;
   uint32_t K, rows, splits, out_stride;
+  uint32_t nb;             // the row tile's 16-column blocks per workgroup (the launcher's layout)
 };
+// A decode dispatch's layout. Row tile: nb 16-column blocks per workgroup, each over 4 / nb K slices of ks groups of
+// 32 inputs. Column tile: nb waves per workgroup, each a K slice of ks groups (8, 16 or 32) of the split. {0, 0} when the split is not one the tile
+// runs (a K partition takes whole meta units; the row tile also holds its slice in registers).
+struct DecodeLayout {
+  uint32_t nb, ks;
+};
+DecodeLayout decode_layout(uint32_t fmt, uint32_t blocks, uint32_t K, uint32_t splits, bool pair, uint32_t rows);
 hipError_t launch_decode(uint32_t fmt, uint32_t epilogue, bool f32_output, const DecodeArgs &args,
                          hipStream_t stream);
-// The one-pass gate/up decode: gate and up of one format over the same columns, out = bf16(bf16(up) *
-// silu(bf16(gate))), bitwise the two passes' result at the same split. Partials [split][rows][2 * out_stride]
-// (gate's columns, then up's at out_stride on); counters one per 64 destination columns.
-struct GateUpArgs {
-  const uint16_t *input;
-  Segment gate, up;
-  uint16_t *output;
-  float *partials;
-  uint32_t *counters;
-  uint32_t K, rows, splits, out_stride;
-};
-hipError_t launch_decode_gate_up(uint32_t fmt, const GateUpArgs &args, hipStream_t stream);
+hipError_t launch_decode_column(uint32_t fmt, uint32_t epilogue, bool f32_output, const DecodeArgs &args,
+                                hipStream_t stream);
 
 // The prefill tile (rows > 32): activations converted once to fp16 with a power-of-two scale per row
 // (launch_prefill_prepare), then dequantised fp16 weights on MFMA.

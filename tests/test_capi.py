@@ -41,17 +41,46 @@ def test_decode_plans(n, k, rows):
     assert plan.storage_rows == rows
     size, gate = sq.scratch_size(plan)
     assert size.partials == (s * rows * n * 4 if s > 1 else 0)
-    assert size.counters == (n // 64 * 4 if s > 1 else 0)
+    assert size.counters == (n // 16 * 4 if s > 1 else 0)
+    # the split depends on the tile kind the rows run, never on the rows: a row's result is the same in any batch
+    # of its kind
+    assert s == sq.plan_for(sq.decode_workload(n, k, 1 if rows <= 4 else 32), proj).config.splits
     assert gate == 0
 
 
-def test_split_law_prefers_saturating_grids():
-    # 14336 x 4096 at one row: 224 tiles need splits to fill 256 compute units.
-    plan = sq.plan_for(sq.decode_workload(14336, 4096, 1), sq.projection(seg(14336, 4096)))
+def column_time(n, k, s, pair=False):
+    """The column tile's split cost model: a workgroup streams at most 55 GB/s, HBM 6.5 TB/s, 2.5 us per split."""
+    bytes_ = (2 if pair else 1) * n * (k * 0.5 + k // 32 * 2.0)
+    return max(bytes_ / (min(n // 64 * s, 256) * 55e9), bytes_ / 6.5e12) + (2.5e-6 if s > 1 else 0.0)
+
+
+def column_layout_fits(k, s):
+    """A split's groups fit one workgroup: at most 16 waves of at most 32 groups each."""
+    return k // 32 // s <= 16 * 32
+
+
+@pytest.mark.parametrize("n,k,want", [(4096, 4096, 1), (1024, 4096, 1), (14336, 4096, 1), (4096, 14336, 2),
+                                      (27648, 5120, 1), (4096, 16384, 2), (4096, 32768, 2)])
+def test_split_law_column_tile(n, k, want):
+    """Rows <= 4: the split of least estimated time, the fewest on a tie."""
+    s = sq.plan_for(sq.decode_workload(n, k, 1), sq.projection(seg(n, k))).config.splits
+    assert s == want
+    valid = [c for c in (1, 2, 4, 8, 16) if column_layout_fits(k, c)]
+    times = {c: column_time(n, k, c) for c in valid}
+    assert times[s] == min(times.values())
+    assert all(times[c] > times[s] for c in valid if c < s)
+
+
+def test_split_law_row_tile():
+    # 14336 x 4096: 896 16-column blocks fill 256 compute units without a split.
+    plan = sq.plan_for(sq.decode_workload(14336, 4096, 16), sq.projection(seg(14336, 4096)))
+    assert plan.config.splits == 1
+    # 1024 x 4096: 64 blocks need K partitions to fill the device.
+    plan = sq.plan_for(sq.decode_workload(1024, 4096, 16), sq.projection(seg(1024, 4096)))
+    assert plan.config.splits >= 4
+    # 4096 x 14336: a K slice of 448 groups does not fit one workgroup's registers unsplit.
+    plan = sq.plan_for(sq.decode_workload(4096, 14336, 16), sq.projection(seg(4096, 14336)))
     assert plan.config.splits >= 2
-    # 1024 x 4096: 16 tiles, the most splits.
-    plan = sq.plan_for(sq.decode_workload(1024, 4096, 1), sq.projection(seg(1024, 4096)))
-    assert plan.config.splits >= 8
 
 
 def test_prefill_plans():

@@ -1,9 +1,10 @@
 """Decode tile (rows <= 32) through the C ABI against the fp64 oracle, with the reference's projection-test
 properties (dev/tests/engine/gguf_projection_test.mm): every output inside its fp64 interval (projectionBound),
 BASELINE's rel-L2 <= 1e-2 and max-abs <= 2^-6 max|row|, sparse inputs past half's range, a row's output bitwise
-independent of the other rows, K-split determinism with counters returned to zero, the epilogues (residual,
-gate/up in one pass bitwise equal to two passes, fp32 destination), fused segments equal to segments alone, and
-untouched padding columns."""
+independent of the other rows of its tile kind (the column tile runs 1..4 rows, the row tile more), K-split
+determinism with counters returned to zero, the epilogues (residual, gate/up in one pass bitwise equal to two
+passes, fp32 destination), fused segments equal to segments alone, and untouched padding columns. Both tile kinds
+run every case that has rows to choose."""
 import numpy as np
 import pytest
 
@@ -71,18 +72,23 @@ def test_decode_sparse_inputs(fmt, splits):
 @pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K])
 @pytest.mark.parametrize("splits", [1, 8])
 def test_rows_are_independent(fmt, splits):
-    """A row's output is bitwise the same alone (the one-row instance) and among 16 or 32 rows."""
+    """A row's output is bitwise the same in any batch of its tile kind: alone (the one-row instance) or among four
+    rows on the column tile, among 16 or 32 rows on the row tile; across the kinds both are inside the oracle's
+    interval (check_projection)."""
     rng = np.random.default_rng(31 + splits)
-    n, k = 128, 1024
+    n, k = 128, 2048   # K partitions take whole meta units: Q4_K's 256-input super-blocks
     w = make_weights(rng, fmt, n, k)
     x = dense_inputs(rng, 32, k)
     proj = sq.projection(w.segment())
     all32 = run_plan(staged(n, k, 32, splits), proj, x, n)
     first16 = run_plan(staged(n, k, 16, splits), proj, x[:16], n)
     assert np.array_equal(all32[:16], first16)
-    for r in (0, 5, 17, 31):
+    four = run_plan(staged(n, k, 4, splits), proj, x[:4], n)
+    for r in range(4):
         alone = run_plan(staged(n, k, 1, splits), proj, x[r:r + 1], n)
-        assert np.array_equal(alone[0], all32[r]), f"row {r}"
+        assert np.array_equal(alone[0], four[r]), f"row {r}"
+    check_projection(four, x[:4], w, "column tile")
+    check_projection(all32, x, w, "row tile")
 
 
 def test_split_determinism_and_poisoned_partials():
@@ -105,30 +111,32 @@ def test_split_determinism_and_poisoned_partials():
     check_projection(outs[0][:4], x, w, "poisoned partials")
 
 
-def test_residual_epilogue():
-    rng = np.random.default_rng(5)
+@pytest.mark.parametrize("rows", [2, 8])
+def test_residual_epilogue(rows):
+    rng = np.random.default_rng(5 + rows)
     n, k = 256, 2048
     w = make_weights(rng, oracle.FMT_AF4G64, n, k)
-    x = dense_inputs(rng, 8, k)
-    residual = synthetic.bf16_bits(rng.uniform(-1, 1, (8, n)).astype(np.float32) * 64)
-    for splits in (1, 4):
-        got = run_plan(staged(n, k, 8, splits, sq.EPILOGUE_RESIDUAL), sq.projection(w.segment()), x, n, residual=residual)
+    x = dense_inputs(rng, rows, k)
+    residual = synthetic.bf16_bits(rng.uniform(-1, 1, (rows, n)).astype(np.float32) * 64)
+    for splits in (2, 4):
+        got = run_plan(staged(n, k, rows, splits, sq.EPILOGUE_RESIDUAL), sq.projection(w.segment()), x, n,
+                       residual=residual)
         check_projection(got, x, w, "residual", residual=residual)
 
 
 @pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K])
-@pytest.mark.parametrize("splits", [1, 4])
-def test_gate_up_one_pass_equals_two_passes(fmt, splits):
-    rng = np.random.default_rng(11 + splits)
+@pytest.mark.parametrize("rows,splits", [(8, 1), (8, 4), (2, 2), (2, 4), (1, 8)])
+def test_gate_up_one_pass_equals_two_passes(fmt, rows, splits):
+    rng = np.random.default_rng(11 + splits + rows)
     n, k = 256, 2048
     wg, wu = make_weights(rng, fmt, n, k), make_weights(rng, fmt, n, k)
-    x = dense_inputs(rng, 8, k)
+    x = dense_inputs(rng, rows, k)
     gate, up = sq.projection(wg.segment()), sq.projection(wu.segment())
-    two = run_plan(staged(n, k, 8, splits, sq.EPILOGUE_GATE_UP), up, x, n, gate=gate)
-    one = run_plan(staged(n, k, 8, splits, sq.EPILOGUE_GATE_UP, one_pass=1), up, x, n, gate=gate)
+    two = run_plan(staged(n, k, rows, splits, sq.EPILOGUE_GATE_UP), up, x, n, gate=gate)
+    one = run_plan(staged(n, k, rows, splits, sq.EPILOGUE_GATE_UP, one_pass=1), up, x, n, gate=gate)
     assert np.array_equal(one, two)
-    g = run_plan(staged(n, k, 8, splits), gate, x, n)
-    u = run_plan(staged(n, k, 8, splits), up, x, n)
+    g = run_plan(staged(n, k, rows, splits), gate, x, n)
+    u = run_plan(staged(n, k, rows, splits), up, x, n)
     gf, uf = synthetic.bf16_to_f32(g).astype(np.float64), synthetic.bf16_to_f32(u).astype(np.float64)
     want = uf * gf / (1 + np.exp(-gf))
     got = synthetic.bf16_to_f32(one).astype(np.float64)
@@ -137,15 +145,16 @@ def test_gate_up_one_pass_equals_two_passes(fmt, splits):
     assert np.all(np.abs(got - want) <= ulp + 1e-30)
 
 
-def test_fp32_destination_rounds_to_the_bf16_output():
-    rng = np.random.default_rng(17)
+@pytest.mark.parametrize("rows", [1, 8])
+def test_fp32_destination_rounds_to_the_bf16_output(rows):
+    rng = np.random.default_rng(17 + rows)
     n, k = 256, 4096
     w = make_weights(rng, oracle.FMT_AF4G64, n, k)
-    x = dense_inputs(rng, 8, k)
+    x = dense_inputs(rng, rows, k)
     proj = sq.projection(w.segment(), destination=sq.OUTPUT_F32)
-    for splits in (1, 8):
-        f32 = run_plan(staged(n, k, 8, splits, destination=sq.OUTPUT_F32), proj, x, n, out_dtype=np.float32)
-        b16 = run_plan(staged(n, k, 8, splits), sq.projection(w.segment()), x, n)
+    for splits in (2, 8):
+        f32 = run_plan(staged(n, k, rows, splits, destination=sq.OUTPUT_F32), proj, x, n, out_dtype=np.float32)
+        b16 = run_plan(staged(n, k, rows, splits), sq.projection(w.segment()), x, n)
         assert np.array_equal(synthetic.bf16_bits(f32), b16)
         value, magnitude, inputs, largest = oracle.project_f64(x, w.values)
         bound = oracle.projection_bound(magnitude, inputs, largest, True)
@@ -155,20 +164,21 @@ def test_fp32_destination_rounds_to_the_bf16_output():
         assert np.linalg.norm(f32 - value) <= 2.0 * np.linalg.norm(ref - value) + 1e-9 * np.linalg.norm(value)
 
 
-def test_fused_segments_equal_segments_alone():
-    rng = np.random.default_rng(23)
+@pytest.mark.parametrize("rows", [3, 8])
+def test_fused_segments_equal_segments_alone(rows):
+    rng = np.random.default_rng(23 + rows)
     k = 2048
     parts = [make_weights(rng, oracle.FMT_AF4G64, n, k) for n in (256, 64, 128)]
-    x = dense_inputs(rng, 8, k)
+    x = dense_inputs(rng, rows, k)
     total = sum(p.n for p in parts)
     segs, offset = [], 0
     for p in parts:
         segs.append(p.segment(offset))
         offset += p.n
-    fused = run_plan(staged(total, k, 8, 2), sq.projection(segs), x, total)
+    fused = run_plan(staged(total, k, rows, 2), sq.projection(segs), x, total)
     offset = 0
     for p in parts:
-        alone = run_plan(staged(p.n, k, 8, 2), sq.projection(p.segment()), x, p.n)
+        alone = run_plan(staged(p.n, k, rows, 2), sq.projection(p.segment()), x, p.n)
         assert np.array_equal(fused[:, offset:offset + p.n], alone)
         offset += p.n
     check_projection(fused, x, parts, "fused")
@@ -186,7 +196,7 @@ def test_padding_columns_untouched():
 
 
 @pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
-@pytest.mark.parametrize("rows", [1, 16])
+@pytest.mark.parametrize("rows", [1, 4, 16])
 def test_baseline_shapes_policy_plans(n, k, rows):
     """The BASELINE decode sweep's shapes at M = 1 and 16 under the library's own plan."""
     rng = np.random.default_rng(n + k + rows)
