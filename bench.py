@@ -3,12 +3,21 @@
 Headline (`value`): the decode GEMV at M = 1, K = 4096, N = 14336 (BASELINE config 1's gate/up shape), MLX affine
 4-bit group 64, bf16 activations ~ N(0, 1), in GB/s of algorithmic bytes (N K 0.5625 + 2 M K + 2 M N) per step. A
 step is one dispatch of the projection through the C ABI (sq_linear_add) over weights already resident in HBM; a
-ring of weight copies larger than the 256 MB Infinity Cache makes every step read HBM. Also reported on the same
-line: the config-1 sweep (M in 1..16 over the four 8B projection shapes), the config-2 prefill GEMM at M = 2048
-(TFLOPS), the config-3 Q4_K shapes, the config-4 MoE block, the dominant kernel's roofline and the CPU baseline (the
+ring of weight copies larger than the 256 MB Infinity Cache makes every step read HBM. The K timed steps are
+captured once in a HIP graph and replayed (a serving loop's form: no host work between dispatches), bracketed by
+HIP events on the launching stream.
+
+`roofline.achieved`: the same bytes over the column tile's average launch duration, the HIP-event timed region
+on the launching stream divided by its K launches (one dispatch per step; rocprofv3's kernel trace of the same
+command, profiles/decode_column_gemv_m1_4096x14336.txt, agrees to within the dispatch gaps); `roofline.traffic`:
+HBM bytes per launch from rocprofv3's FETCH_SIZE and WRITE_SIZE counters (profiles/decode_column_traffic.txt), scaled
+by the counters' reading for a plain copy of known size (`--calibrate-copy` runs one).
+
+Also reported on the same line: the config-1 sweep (M in 1..16 over the four 8B projection shapes), the config-2
+prefill GEMM at M = 2048 (TFLOPS), the config-3 Q4_K shapes, the config-4 MoE block and the CPU baseline (the
 oracle's threaded C implementation of the same quantized matmul on this host's cores, over a bounded sample).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--calibrate-copy]
 """
 from __future__ import annotations
 
@@ -27,6 +36,19 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 RING_BYTES = 1 << 30
+
+
+COPY_BYTES = 1 << 29
+TRAFFIC_FILE = ROOT / "profiles" / "decode_column_traffic.txt"
+
+
+def traffic_bytes():
+    """HBM bytes per launch of the headline kernel, from the committed counter summary (None when absent)."""
+    try:
+        fields = dict(line.split(":", 1) for line in TRAFFIC_FILE.read_text().splitlines() if ":" in line)
+        return int(fields["fetch_bytes_per_launch"]) + int(fields["write_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def log(msg: str) -> None:
@@ -86,23 +108,57 @@ def time_steps(torch, fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / 1e3 / steps
 
 
+def time_graph(torch, launch, steps: int, warmup: int) -> float:
+    """Seconds per step: `warmup` untimed eager steps, then `steps` launches captured in one HIP graph, replayed once
+    untimed and once between HIP events on the replaying stream. launch(i, stream_handle) issues step i."""
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        launch(i, stream.cuda_stream)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        handle = torch.cuda.current_stream().cuda_stream
+        for i in range(steps):
+            launch(i, handle)
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    del graph
+    return start.elapsed_time(end) / 1e3 / steps
+
+
+class Gemv:
+    """A decode projection over a weight ring; launch(i, stream) dispatches step i on ring copy i % copies."""
+
+    def __init__(self, torch, sq, synthetic, fmt, m, n, k, seed=1):
+        one = int(gemv_bytes(0, n, k))
+        self.copies = max(1, -(-RING_BYTES // one))
+        self.weights = Projection(torch, sq, synthetic, fmt, n, k, seed, self.copies)
+        self.projs = [self.weights.projection(sq, c) for c in range(self.copies)]
+        self.plan = sq.plan_for(sq.decode_workload(n, k, m), self.projs[0])
+        self.scratch = sq.Scratch(self.plan)
+        self.x = torch.from_numpy(synthetic.activations(np.random.default_rng(seed + 1), m, k).view(np.int16)).cuda()
+        self.out = torch.empty((m, n), dtype=torch.int16, device="cuda")
+        self.bufs = sq.LinearBuffers(sq.view(self.x), sq.view(self.out), sq.view(None), sq.view(None),
+                                     self.scratch.struct())
+        self.sq = sq
+
+    def launch(self, i, stream):
+        sq = self.sq
+        sq.call("sq_linear_add", sq.c_void_p(stream), sq.byref(self.bufs), sq.byref(self.projs[i % self.copies]),
+                sq.byref(self.plan), None)
+
+
 def bench_gemv(torch, sq, synthetic, fmt, m, n, k, steps, warmup, seed=1):
-    one = int(gemv_bytes(0, n, k))
-    copies = max(1, -(-RING_BYTES // one))
-    w = Projection(torch, sq, synthetic, fmt, n, k, seed, copies)
-    projs = [w.projection(sq, c) for c in range(copies)]
-    plan = sq.plan_for(sq.decode_workload(n, k, m), projs[0])
-    scratch = sq.Scratch(plan).struct()
-    x = torch.from_numpy(synthetic.activations(np.random.default_rng(seed + 1), m, k).view(np.int16)).cuda()
-    out = torch.empty((m, n), dtype=torch.int16, device="cuda")
-    handle = sq.stream_handle()
-    bufs = [sq.LinearBuffers(sq.view(x), sq.view(out), sq.view(None), sq.view(None), scratch)]
-
-    def step(i):
-        sq.call("sq_linear_add", handle, sq.byref(bufs[0]), sq.byref(projs[i % copies]), sq.byref(plan), None)
-
-    sec = time_steps(torch, step, steps, warmup)
-    del w
+    g = Gemv(torch, sq, synthetic, fmt, m, n, k, seed)
+    sec = time_graph(torch, g.launch, steps, warmup)
+    plan = g.plan
+    del g
     return sec, plan
 
 
@@ -195,6 +251,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only (no sweep, prefill, MoE or CPU baseline)")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--calibrate-copy", action="store_true", help="also run a plain copy of known size (counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -207,9 +264,23 @@ def main() -> int:
     torch.cuda.set_device(0)
     m, n, k = 1, 14336, 4096
     log(f"headline: decode GEMV M={m} K={k} N={n} af4g64, {args.steps} steps")
-    sec, plan = bench_gemv(torch, sq, synthetic, sq.FMT_AF4G64, m, n, k, args.steps, args.warmup)
+    headline = Gemv(torch, sq, synthetic, sq.FMT_AF4G64, m, n, k)
+    plan = headline.plan
+    sec = time_graph(torch, headline.launch, args.steps, args.warmup)
     gbs = gemv_bytes(m, n, k) / sec / 1e9
     log(f"  {sec * 1e6:.2f} us/step, {gbs:.1f} GB/s, splits {plan.config.splits}")
+    ring_copies = headline.copies
+    del headline
+    torch.cuda.empty_cache()
+    if args.calibrate_copy:
+        # A plain device copy of known size for scaling the FETCH_SIZE / WRITE_SIZE counters.
+        src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"  calibration copy: 5 x {COPY_BYTES} bytes")
+        del src, dst
     extra = {}
     if not args.quick:
         sweep = {}
@@ -258,11 +329,13 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded: bf16 N(0,1) activations, uint4 codes, bf16 |N(0,0.02)| scales, biases -8s)",
-        "config": {"workload": "c1 decode GEMV gate/up shape", "M": m, "K": k, "N": n, "format": "af4g64",
-                   "weights": "4-bit MLX affine group 64", "splits": plan.config.splits,
-                   "weight_ring_copies": max(1, -(-RING_BYTES // int(gemv_bytes(0, n, k))))},
+        "config": {"workload": "decode GEMV M=1 K=4096 N=14336 (BASELINE config 1, gate/up shape)", "M": m, "K": k,
+                   "N": n, "format": "af4g64", "weights": "4-bit MLX affine group 64", "tile": "column",
+                   "splits": plan.config.splits, "weight_ring_copies": ring_copies, "timing": "HIP graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(),
+                     "kernel": "column_kernel<af4g64, 1 row>", "launch_us": round(sec * 1e6, 3),
+                     "algorithmic_bytes": int(gemv_bytes(m, n, k))},
     }
     result.update(extra)
     if not args.quick:

@@ -174,39 +174,34 @@ uint64_t LinearPlan::gateScratchBytes() const noexcept {
   return needed ? uint64_t{storageRows()} * workload_.matrix.outputSize * 2 : 0;
 }
 
-// MI355X's split law. The decode tiles are HBM-bound and a split adds a reduction tail (partials stored, a counter,
-// partials read back: three device-scope round trips after the workgroup's last load). A partition takes whole
-// meta units. The split depends on the shape and the tile kind the rows run, never on the rows themselves, so a
-// row's result is the same in any batch of its kind.
-//  - Column tile: one workgroup per 64-column tile and split streams its K slices; the split with the least
-//    estimated time, where a workgroup streams at most kWorkgroupBandwidth (one compute unit's load rate), the
-//    device kHbmBandwidth, and each split past the first adds kSplitTail (fewest splits on a tie).
-//  - Row tile: the fewest splits whose layout holds each wave's slice in registers and whose grid has a workgroup
-//    for each compute unit.
+// MI355X's split law. Both decode tiles stream a 64-column tile's K slices through one workgroup; a split adds a
+// reduction tail (partials stored, a counter, partials read back: device-scope round trips after the workgroup's
+// last load) and spreads the tile over more compute units. Measured on MI355X, a workgroup streams its bytes fastest
+// up to about kColumnBytes (column tile) or kRowBytes (row tile, whose MFMA and close work per byte grows with the
+// rows) per dispatch, and a grid larger than the device queues workgroups. The split is the fewest K partitions
+// whose workgroups stream at most that many bytes, without growing the grid past the compute units, among those
+// whose slices fit one workgroup of the tile the rows run (a partition takes whole meta units). It depends on the
+// shape and the tile kind, never on the rows themselves, so a row's result is the same in any batch of its kind.
 namespace {
-constexpr double kWorkgroupBandwidth = 55e9, kHbmBandwidth = 6.5e12, kSplitTail = 2.5e-6;   // measured on MI355X
+constexpr double kColumnBytes = 160e3, kRowBytes = 80e3;
 }  // namespace
 
 uint32_t Linear::decodeSplits(uint32_t n, uint32_t k, uint32_t rows, uint32_t groupUnit, bool pair) const noexcept {
-  const uint32_t G = k / 32, blocks = n / 16;
+  const uint32_t G = k / 32, blocks = n / 16, tiles = n / 64;
   const uint32_t format = groupUnit == 8 ? SQ_FMT_Q4K : groupUnit == 4 ? SQ_FMT_AF4G128
                         : groupUnit == 2 ? SQ_FMT_AF4G64 : SQ_FMT_AF4G32;
+  // The split law sees the tile kind only: one row stands for the column tile, sixteen or thirty-two for the row
+  // tile's register budgets.
   const bool column = rows <= kern::kColumnTileRows;
-  const double bytes = (pair ? 2.0 : 1.0) * n * (k * 0.5 + G * 4.0 / groupUnit);
+  const uint32_t kind = column ? 1 : rows <= 16 ? 16 : SQ_MAXIMUM_DECODE_ROWS;
+  const double tileBytes = (pair ? 2.0 : 1.0) * 64 * (k * 0.5 + G * 4.0 / groupUnit);
+  const double budget = column ? kColumnBytes : kRowBytes;
   uint32_t best = 0;
-  double bestTime = 0;
   for (uint32_t s = 1; s <= LinearConfig::kMaximumSplits && G % (s * groupUnit) == 0; s *= 2) {
-    const kern::DecodeLayout layout = kern::decode_layout(format, blocks, k, s, pair, rows);
-    if (!layout.nb) continue;
-    if (column) {
-      const double workgroups = std::min<double>(uint64_t{n / 64} * s, computeUnits_);
-      const double t = std::max(bytes / (workgroups * kWorkgroupBandwidth), bytes / kHbmBandwidth) +
-                       (s > 1 ? kSplitTail : 0.0);
-      if (!best || t < bestTime) best = s, bestTime = t;
-      continue;
-    }
+    if (!kern::decode_layout(format, blocks, k, s, pair, kind).nb) continue;
+    if (best && uint64_t{tiles} * s > computeUnits_) break;
     best = s;
-    if (uint64_t{blocks / layout.nb} * s >= computeUnits_) break;
+    if (tileBytes / s <= budget) break;
   }
   return best ? best : 1;
 }

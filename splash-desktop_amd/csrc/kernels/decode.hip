@@ -1,233 +1,241 @@
-// The decode tile: y[r][c] = sum_k x[r][k] w[c][k] for up to 32 rows of bf16 activations against 4-bit plane
-// weights, fp32 accumulation (reference: gguf_decode / gguf_decode_tile and gguf_decode_gate_up,
+// The row tile of the decode GEMV: y[r][c] = sum_k x[r][k] w[c][k] for 5 to 32 rows of bf16 activations against
+// 4-bit plane weights, fp32 accumulation (reference: gguf_decode / gguf_decode_tile and gguf_decode_gate_up,
 // kernels/shared/gguf_linear.metal:71-192, and the exact-operand register tile of
-// kernels/decode/linear_gguf_sgmatrix.metal).
+// kernels/decode/linear_gguf_sgmatrix.metal), and the decode tiles' layout and dispatch.
 //
-// CDNA4 mapping. The tile is HBM-bound, so the design maximises bytes in flight and minimises serial phases:
-//  - a wave owns one 16-column block and one K slice of up to KS groups of 32 inputs, and issues every code and
-//    meta load of its slice before its first MFMA (up to 16 KiB of codes per wave in flight);
-//  - per group the 16 columns' 256 bytes of codes arrive as one dword per lane (lane (j, q): word q of column j's
-//    16-byte unit), become eight exact bf16 operands 128 + q each, and meet the activations in one 16x16x32 bf16
-//    MFMA; a second MFMA against bf16 ones gives the rows' input sums. Each scale group closes in fp32:
-//      acc += s * sum x (128 + q) + (z - 128 s) * sum x  =  sum x (s q + z);
-//  - the activation fragments (L2-resident, shared by every workgroup) stream through a ring of registers kPipe
-//    groups ahead of the MFMAs;
-//  - a workgroup of four waves holds NB column blocks x (4 / NB) K slices; slices meet in LDS in slice order;
-//  - K partitions across workgroups (splits) reduce as the reference's split_reduce.h:14-45 does: fp32 partials
-//    [split][rows][stride] and the last workgroup to arrive at the column block's counter adds them in split order
-//    and returns the counter to zero, so results do not depend on scheduling. A row's result depends only on its
-//    own activations, the split and the layout (NB, KS), which the launcher derives from the shape alone.
-#include "kernels.hpp"
+// CDNA4 mapping. The tile streams a 64-column plane tile exactly as the column tile does (decode_column.hip): per
+// group of 32 inputs one 16-byte load per lane (lane l: column l's 32 codes), 1 KiB per wave, P groups in flight,
+// every load unconditional. The rows go on the 16-row side of the 16x16x32 bf16 MFMA:
+//  - a 4x4 transpose of the four code dwords across the wave's four 16-lane rows (v_permlane32_swap, then
+//    v_permlane16_swap) gives lane (j, q) word q of column 16t + j in register t, the MFMA's B layout for column
+//    block t; each word becomes eight exact bf16 operands 128 + q (code_pairs);
+//  - per group and 16-row block, four MFMAs (one per 16-column block) plus one against bf16 ones, which leaves
+//    each lane its own rows' input sums: no cross-lane reduction;
+//  - each scale group closes in fp32: acc += s * sum x (128 + q) + (z - 128 s) * sum x, every product exact;
+//  - a workgroup of W waves takes the tile and W K slices; the slices meet in LDS in slice order, every wave
+//    adding a share of the accumulators, and K partitions across workgroups reduce through split_reduce.
+// A row's result depends only on its own activations and the layout, never on the other rows.
 #include "device.hpp"
+#include "kernels.hpp"
 #include "split.hpp"
 
 namespace sq::kern {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kPipe = 8;   // activation fragments in flight ahead of the MFMAs
+constexpr int kPipe = 4;   // groups in flight per wave
 
-// Where a 16-column block of the dispatch lies: its segment, plane tile and 16-column sub-block t of the tile.
-struct BlockPlace {
-  const uint8_t *plane0, *meta;
-  uint32_t tile, t, out_offset, live;
-};
-__device__ __forceinline__ BlockPlace place(const Segment (&seg)[3], uint32_t segments, uint32_t block) {
-  uint32_t s = 0;
-  while (s + 1 < segments && block >= seg[s].tiles * 4) block -= seg[s++].tiles * 4;
-  return {seg[s].plane0, seg[s].meta, block / 4, block % 4, seg[s].out_offset, block < seg[s].tiles * 4 ? 1u : 0u};
+// The most waves a row-tile workgroup holds, so that a wave's registers fit without spilling: 16 (128 registers) for
+// one tensor of 16 rows, 4 (512) for a gate/up pair of 32 rows, else 8 (256).
+constexpr uint32_t row_max_waves(int mb, int nt) { return mb == 1 && nt == 1 ? 16 : mb == 2 && nt == 2 ? 4 : 8; }
+
+// Lane (j, q) register t <- lane (j + 16 t) register q: the 4x4 transpose of words across the 16-lane rows.
+__device__ __forceinline__ void transpose4(uint32_t (&r)[4]) {
+  const auto a = __builtin_amdgcn_permlane32_swap(r[0], r[2], false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(r[1], r[3], false, false);
+  const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  r[0] = c[0];
+  r[1] = c[1];
+  r[2] = d[0];
+  r[3] = d[1];
 }
 
-// One wave's K slice of one 16-column block, NT tensors (gate, up): acc[n][b] over row blocks b.
-template <uint32_t FMT, int MB, int R, int KS, int NT>
-__device__ __forceinline__ void slice_walk(const uint8_t *const (&plane)[NT], const uint8_t *const (&meta)[NT],
-                                           const uint16_t *const (&xrow)[2], uint32_t g_begin, uint32_t count,
-                                           int q, f32x4 (&acc)[NT][MB]) {
+template <uint32_t FMT, int MB, int GW, int NT, uint32_t EP, bool F32OUT>
+__global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeArgs a) {
   using F = Fmt<FMT>;
-  constexpr int SG = F::SG;
-  constexpr int NU = (KS + F::UNIT - 1) / F::UNIT + 1;   // meta units a slice can touch
-  uint32_t codes[NT][KS];
-  MetaWords units[NT][NU];
-  u32x4 x[kPipe][MB];
-  const uint32_t unit0 = g_begin / F::UNIT;
-  const auto load_x = [&](int slot, uint32_t u) __attribute__((always_inline)) {
+  constexpr int SG = F::SG, UNIT = F::UNIT, P = GW < kPipe ? GW : kPipe;
+  constexpr int A = NT * 4 * MB * 4;   // accumulators per lane: tensor n, column block t, row block b, row i
+  static_assert(GW % UNIT == 0 && GW % SG == 0, "a slice holds whole meta units");
+  const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
+  const uint32_t slice = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), waves = blockDim.x >> 6;
+  const uint32_t split = blockIdx.y;
+  uint32_t tile = blockIdx.x, s = 0;
+  while (s + 1 < a.segments && tile >= a.seg[s].tiles) tile -= a.seg[s++].tiles;
+  const Segment seg = a.seg[s];
+  const uint32_t G = a.K >> 5, units = G / UNIT, gs = G / a.splits;
+  const uint32_t gb = split * gs + slice * GW, live = min((uint32_t)GW, gs - min(gs, slice * GW));
+  const uint32_t last = live ? live - 1 : 0;
+
+  const uint8_t *plane[NT], *meta[NT];
+  {
+    const size_t pbase = ((size_t)tile * G * 64 + lane) * 16 + (size_t)gb * 1024;
+    const size_t mbase = ((size_t)tile * units * 64 + j) * F::META + (size_t)(gb / UNIT) * 64 * F::META;
+    plane[0] = (NT == 2 ? a.gate.plane0 : seg.plane0) + pbase;
+    meta[0] = (NT == 2 ? a.gate.meta : seg.meta) + mbase;
+    if constexpr (NT == 2) {
+      plane[1] = seg.plane0 + pbase;
+      meta[1] = seg.meta + mbase;
+    }
+  }
+  // Lane (j, q) of row block b reads row 16 b + j's inputs 4q..4q+3 and 16+4q..19+4q of each group (the MFMA's A
+  // layout); rows past the live ones read row 0, whose results nothing stores.
+  const uint16_t *xrow[MB];
+#pragma unroll
+  for (int b = 0; b < MB; ++b) {
+    const uint32_t r = 16u * b + j;
+    xrow[b] = a.input + (size_t)(r < a.rows ? r : 0) * a.K + 4 * q + (size_t)gb * 32;
+  }
+  const CodeConstants cc = make_code_constants();
+
+  float acc[NT][4][MB][4];
+#pragma unroll
+  for (int n = 0; n < NT; ++n)
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[n][t][b][i] = 0.0f;
+
+  u32x4 xv[MB][GW];
+  u32x4 codes[NT][GW];
+  MetaWords mw[NT][4][GW / UNIT];
+  const auto issue = [&](int u) __attribute__((always_inline)) {
+    const uint32_t g = min((uint32_t)u, last);
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
-      if (xrow[b] && u < count) {
-        const uint16_t *p = xrow[b] + (g_begin + u) * 32 + 4 * q;
-        const u32x2 lo = *(const u32x2 *)p, hi = *(const u32x2 *)(p + 16);
-        x[slot][b] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-      } else {
-        x[slot][b] = u32x4{0u, 0u, 0u, 0u};
-      }
+      const u32x2 lo = *(const u32x2 *)(xrow[b] + (size_t)g * 32), hi = *(const u32x2 *)(xrow[b] + (size_t)g * 32 + 16);
+      xv[b][u] = u32x4{lo[0], lo[1], hi[0], hi[1]};
     }
+    if (u % UNIT == 0) {
+      const uint32_t v = min((uint32_t)(u / UNIT), last / UNIT);
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          mw[n][t][u / UNIT] = load_meta<FMT>(meta[n] + ((size_t)v * 64 + 16 * t) * F::META);
+    }
+#pragma unroll
+    for (int n = 0; n < NT; ++n) codes[n][u] = __builtin_nontemporal_load((const u32x4 *)(plane[n] + (size_t)g * 1024));
   };
-  // The first activation fragments, then every code and meta load of the slice.
 #pragma unroll
-  for (int u = 0; u < kPipe && u < KS; ++u) load_x(u, u);
-#pragma unroll
-  for (int u = 0; u < KS; ++u)
-#pragma unroll
-    for (int n = 0; n < NT; ++n)
-      codes[n][u] = (uint32_t)u < count ? __builtin_nontemporal_load((const uint32_t *)(plane[n] + (size_t)(g_begin + u) * 1024))
-                                        : 0u;
-  const uint32_t last_unit = (g_begin + count - 1) / F::UNIT;
-#pragma unroll
-  for (int v = 0; v < NU; ++v)
-#pragma unroll
-    for (int n = 0; n < NT; ++n)
-      units[n][v] = unit0 + v <= last_unit ? load_meta<FMT>(meta[n] + (size_t)(unit0 + v) * 64 * F::META)
-                                           : MetaWords{{0u, 0u, 0u, 0u}};
+  for (int u = 0; u < P; ++u) issue(u);
+
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4 c[NT][MB], sx[MB];
+  f32x4 C[NT][4][MB], S[MB];
 #pragma unroll
-  for (int u = 0; u < KS; ++u) {
-    if ((uint32_t)u >= count) continue;
-    const int slot = u % kPipe;
-    const uint32_t g = g_begin + u;
-    const bool first = u % SG == 0;   // slices start on meta units, so on scale groups
+  for (int u = 0; u < GW; ++u) {
+    if (u + P < GW) issue(u + P);
+    __builtin_amdgcn_sched_barrier(0);
+    if ((uint32_t)u < live) {
+      const bool first = u % SG == 0;
 #pragma unroll
-    for (int b = 0; b < MB; ++b) sx[b] = mfma_bf16(x[slot][b], ones_operand(), first ? zero : sx[b]);
-#pragma unroll
-    for (int n = 0; n < NT; ++n) {
-      const u32x4 w = code_operands(codes[n][u]);
-#pragma unroll
-      for (int b = 0; b < MB; ++b) c[n][b] = mfma_bf16(x[slot][b], w, first ? zero : c[n][b]);
-    }
-    if (u + kPipe < KS) load_x(slot, u + kPipe);
-    if ((u + 1) % SG == 0) {
-      constexpr int kUnitStride = F::UNIT;
-      const int v = u / kUnitStride;   // the slice starts on a meta unit
+      for (int b = 0; b < MB; ++b) S[b] = mfma_bf16(xv[b][u], ones_operand(), first ? zero : S[b]);
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
-        const Coef k = coef<FMT>(units[n][v], g / SG);
-        const float zc = fmaf(-128.0f, k.s, k.z);
+        uint32_t r[4] = {codes[n][u][0], codes[n][u][1], codes[n][u][2], codes[n][u][3]};
+        transpose4(r);
 #pragma unroll
-        for (int b = 0; b < MB; ++b)
+        for (int t = 0; t < 4; ++t) {
+          const u32x4 w = code_pairs(r[t], cc);
 #pragma unroll
-          for (int i = 0; i < R; ++i) {
-            acc[n][b][i] = fmaf(k.s, c[n][b][i], acc[n][b][i]);
-            acc[n][b][i] = fmaf(zc, sx[b][i], acc[n][b][i]);
+          for (int b = 0; b < MB; ++b) C[n][t][b] = mfma_bf16(xv[b][u], w, first ? zero : C[n][t][b]);
+        }
+      }
+      if ((u + 1) % SG == 0) {
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const Coef k = coef<FMT>(mw[n][t][u / UNIT], u);
+            const float zc = fmaf(-128.0f, k.s, k.z);
+#pragma unroll
+            for (int b = 0; b < MB; ++b)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                acc[n][t][b][i] = fmaf(k.s, C[n][t][b][i], acc[n][t][b][i]);
+                acc[n][t][b][i] = fmaf(zc, S[b][i], acc[n][t][b][i]);
+              }
           }
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
-}
 
-template <uint32_t FMT, int MT, int KS, int NT, uint32_t EP, bool F32OUT>
-__global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
-  using F = Fmt<FMT>;
-  constexpr int MB = MT > 16 ? 2 : 1;   // 16-row A blocks
-  constexpr int R = MT >= 4 ? 4 : MT;   // accumulator rows each lane group keeps
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15, q = lane >> 4;
-  const uint32_t nb = a.nb, slices = kWaves / nb, wnb = (uint32_t)wave % nb, slice = (uint32_t)wave / nb;
-  const uint32_t block = blockIdx.x * nb + wnb, split = blockIdx.y;
-  const BlockPlace at = place(a.seg, a.segments, block);
-  const uint32_t G = a.K >> 5, units = G / F::UNIT;
-  // Meta units of this split and this slice of it: slices start on meta units, so a group's unit is at a
-  // compile-time offset from the slice's first.
-  const uint32_t per = units / a.splits;
-  const uint32_t s0 = split * per + slice * per / slices, s1 = split * per + (slice + 1) * per / slices;
-  const uint32_t g_begin = s0 * F::UNIT, count = at.live ? (s1 - s0) * F::UNIT : 0;
-
-  const uint8_t *plane[NT], *meta[NT];
-  const size_t pbase = ((size_t)at.tile * G * 64 + 16 * at.t + j) * 16 + 4 * q;
-  const size_t mbase = ((size_t)at.tile * units * 64 + 16 * at.t + j) * F::META;
-  plane[0] = (NT == 2 ? a.gate.plane0 : at.plane0) + pbase;
-  meta[0] = (NT == 2 ? a.gate.meta : at.meta) + mbase;
-  if constexpr (NT == 2) {
-    plane[NT - 1] = at.plane0 + pbase;
-    meta[NT - 1] = at.meta + mbase;
-  }
-  const uint16_t *xrow[2];
-#pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    const uint32_t r = 16u * b + j;
-    xrow[b] = b < MB && r < a.rows ? a.input + (size_t)r * a.K : nullptr;
-  }
-  f32x4 acc[NT][MB];
+  // Slices meet in LDS; accumulator (t, b, i) of both tensors is added, in slice order, by wave (t, b, i) % waves.
+  __shared__ float red[row_max_waves(MB, NT) * A * 64];
 #pragma unroll
   for (int n = 0; n < NT; ++n)
 #pragma unroll
-    for (int b = 0; b < MB; ++b) acc[n][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-  slice_walk<FMT, MB, R, KS, NT>(plane, meta, xrow, g_begin, count, q, acc);
-
-  // Slices meet in LDS; the slice-0 wave of each column block adds them in slice order.
-  __shared__ float red[kWaves * NT * MB * R * 64];
-  const auto at_red = [&](uint32_t w, int n, int b, int i) { return (((w * NT + n) * MB + b) * R + i) * 64 + lane; };
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-  for (int n = 0; n < NT; ++n)
+      for (int b = 0; b < MB; ++b)
 #pragma unroll
-    for (int b = 0; b < MB; ++b)
-#pragma unroll
-      for (int i = 0; i < R; ++i) red[at_red(wave, n, b, i)] = acc[n][b][i];
+        for (int i = 0; i < 4; ++i) red[((slice * A) + ((n * 4 + t) * MB + b) * 4 + i) * 64 + lane] = acc[n][t][b][i];
   __syncthreads();
-  const bool owner = slice == 0 && at.live;
-  float total[NT * MB][R];
-  bool live[NT * MB][R];
-  size_t index[NT * MB][R];
-  const uint32_t col = at.out_offset + at.tile * 64 + 16 * at.t + j;
   const uint32_t cstride = NT == 2 ? 2 * a.out_stride : a.out_stride;
+  float total[A][1];
+  bool rlive[A][1];
+  size_t index[A][1];
 #pragma unroll
   for (int n = 0; n < NT; ++n)
 #pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int e = ((n * 4 + t) * MB + b) * 4 + i;
+          const uint32_t own = (uint32_t)((t * MB + b) * 4 + i) % waves;
+          const uint32_t row = 16u * b + 4u * q + i;
+          float v = 0.0f;
+          if (own == slice)
+            for (uint32_t w = 0; w < waves; ++w) v += red[(w * A + e) * 64 + lane];
+          total[e][0] = v;
+          rlive[e][0] = own == slice && row < a.rows;
+          index[e][0] = (size_t)row * cstride + n * a.out_stride + seg.out_offset + tile * 64 + 16 * t + j;
+        }
+  if (a.splits > 1 && !split_reduce<A, 1>(total, rlive, index, a.partials, (size_t)a.rows * cstride, split, a.splits,
+                                          a.counters + blockIdx.x, true))
+    return;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
     for (int b = 0; b < MB; ++b)
 #pragma unroll
-      for (int i = 0; i < R; ++i) {
-        float v = 0.0f;
-        for (uint32_t s = 0; s < slices; ++s) v += red[at_red(s * nb + wnb, n, b, i)];
-        const uint32_t r = 16u * b + 4u * q + i;
-        total[n * MB + b][i] = v;
-        live[n * MB + b][i] = r < a.rows;
-        index[n * MB + b][i] = (size_t)r * cstride + n * a.out_stride + col;
+      for (int i = 0; i < 4; ++i) {
+        const int e = (t * MB + b) * 4 + i;
+        if (!rlive[e][0]) continue;
+        const size_t o = (size_t)(16u * b + 4u * q + i) * a.out_stride + seg.out_offset + tile * 64 + 16 * t + j;
+        if constexpr (NT == 2) {
+          const float g = bf16_to_f32(f32_to_bf16(total[e][0])), up = bf16_to_f32(f32_to_bf16(total[4 * MB * 4 + e][0]));
+          ((uint16_t *)a.output)[o] = f32_to_bf16(up * silu(g));
+        } else {
+          const float v = epilogue<EP>(total[e][0], a.aux, o);
+          if constexpr (F32OUT) ((float *)a.output)[o] = v;
+          else ((uint16_t *)a.output)[o] = f32_to_bf16(v);
+        }
       }
-  if (a.splits > 1 &&
-      !split_reduce<NT * MB, R>(total, live, index, a.partials, (size_t)a.rows * cstride, split, a.splits,
-                                a.counters + blockIdx.x, owner))
-    return;
-  if (!owner) return;
-#pragma unroll
-  for (int b = 0; b < MB; ++b)
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      if (!live[b][i]) continue;
-      const size_t o = (size_t)(16u * b + 4u * q + i) * a.out_stride + col;
-      if constexpr (NT == 2) {
-        const float g = bf16_to_f32(f32_to_bf16(total[b][i])), u = bf16_to_f32(f32_to_bf16(total[MB + b][i]));
-        ((uint16_t *)a.output)[o] = f32_to_bf16(u * silu(g));
-      } else {
-        const float v = epilogue<EP>(total[b][i], a.aux, o);
-        if constexpr (F32OUT) ((float *)a.output)[o] = v;
-        else ((uint16_t *)a.output)[o] = f32_to_bf16(v);
-      }
-    }
 }
 
-template <uint32_t FMT, int MT, int NT, uint32_t EP, bool F32OUT>
-hipError_t launch_ks(const DecodeArgs &a, uint32_t blocks, uint32_t ks, hipStream_t stream) {
-  const dim3 grid(blocks / a.nb, a.splits), block(256);
-  if (NT == 2 || ks <= 32) hipLaunchKernelGGL((decode_kernel<FMT, MT, 32, NT, EP, F32OUT>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((decode_kernel<FMT, MT, 64, NT, EP, F32OUT>), grid, block, 0, stream, a);
+template <uint32_t FMT, int MB, int NT, uint32_t EP, bool F32OUT>
+hipError_t launch_mb(const DecodeArgs &a, uint32_t tiles, DecodeLayout layout, hipStream_t stream) {
+  const dim3 grid(tiles, a.splits), block(64 * layout.nb);
+  switch (layout.ks) {
+    case 8: hipLaunchKernelGGL((row_kernel<FMT, MB, 8, NT, EP, F32OUT>), grid, block, 0, stream, a); break;
+    case 16: hipLaunchKernelGGL((row_kernel<FMT, MB, 16, NT, EP, F32OUT>), grid, block, 0, stream, a); break;
+    default:
+      if constexpr (NT == 1) hipLaunchKernelGGL((row_kernel<FMT, MB, 32, NT, EP, F32OUT>), grid, block, 0, stream, a);
+      break;
+  }
   return hipGetLastError();
 }
 
 template <uint32_t FMT, int NT, uint32_t EP, bool F32OUT>
-hipError_t launch_rows(const DecodeArgs &a, uint32_t blocks, uint32_t ks, hipStream_t stream) {
-  if (a.rows <= 1) return launch_ks<FMT, 1, NT, EP, F32OUT>(a, blocks, ks, stream);
-  if (a.rows <= 4) return launch_ks<FMT, 4, NT, EP, F32OUT>(a, blocks, ks, stream);
-  if (a.rows <= 16) return launch_ks<FMT, 16, NT, EP, F32OUT>(a, blocks, ks, stream);
-  return launch_ks<FMT, 32, NT, EP, F32OUT>(a, blocks, ks, stream);
+hipError_t launch_rows(const DecodeArgs &a, uint32_t tiles, DecodeLayout layout, hipStream_t stream) {
+  return a.rows <= 16 ? launch_mb<FMT, 1, NT, EP, F32OUT>(a, tiles, layout, stream)
+                      : launch_mb<FMT, 2, NT, EP, F32OUT>(a, tiles, layout, stream);
 }
 
 template <uint32_t FMT>
-hipError_t launch_format(uint32_t epilogue, bool f32_output, bool pair, const DecodeArgs &a, uint32_t blocks,
-                         uint32_t ks, hipStream_t stream) {
-  if (pair) return launch_rows<FMT, 2, EpNone, false>(a, blocks, ks, stream);
-  if (f32_output) return launch_rows<FMT, 1, EpNone, true>(a, blocks, ks, stream);
+hipError_t launch_format(uint32_t epilogue, bool f32_output, bool pair, const DecodeArgs &a, uint32_t tiles,
+                         DecodeLayout layout, hipStream_t stream) {
+  if (pair) return launch_rows<FMT, 2, EpNone, false>(a, tiles, layout, stream);
+  if (f32_output) return launch_rows<FMT, 1, EpNone, true>(a, tiles, layout, stream);
   switch (epilogue) {
-    case EpNone: return launch_rows<FMT, 1, EpNone, false>(a, blocks, ks, stream);
-    case EpResidual: return launch_rows<FMT, 1, EpResidual, false>(a, blocks, ks, stream);
-    default: return launch_rows<FMT, 1, EpUpWithGate, false>(a, blocks, ks, stream);
+    case EpNone: return launch_rows<FMT, 1, EpNone, false>(a, tiles, layout, stream);
+    case EpResidual: return launch_rows<FMT, 1, EpResidual, false>(a, tiles, layout, stream);
+    default: return launch_rows<FMT, 1, EpUpWithGate, false>(a, tiles, layout, stream);
   }
 }
 
@@ -235,46 +243,31 @@ hipError_t launch_format(uint32_t epilogue, bool f32_output, bool pair, const De
 
 DecodeLayout decode_layout(uint32_t fmt, uint32_t blocks, uint32_t K, uint32_t splits, bool pair, uint32_t rows) {
   const uint32_t sg = sq_format(fmt).meta_groups;   // groups of 32 per meta unit
-  const uint32_t per = K / 32 / sg / (splits ? splits : 1);   // meta units per split
-  if (!sq_format_supported(fmt) || !splits || (K / 32 / sg) % splits || !per || blocks % 4) return {0, 0};
-  if (rows <= kColumnTileRows) {
-    // The shortest slices (8, 16 or 32 groups; a gate/up pair streams two tensors, at most 16) whose waves fit one
-    // workgroup.
-    const uint32_t gs = per * sg;
-    for (uint32_t ks = 8; ks <= (pair ? kColumnMaxGroups / 2 : kColumnMaxGroups); ks *= 2)
-      if ((gs + ks - 1) / ks <= kColumnMaxWaves) return {(gs + ks - 1) / ks, ks};
-    return {0, 0};
-  }
-  const uint32_t most = pair ? 32 : 64;        // groups of 32 a wave holds in registers
-  // The fewest slices per column block whose waves hold their slice (widest column blocks per workgroup), among
-  // those whose grid fills the device's 256 compute units.
-  DecodeLayout best{0, 0};
-  for (uint32_t nb = 4; nb >= 1; nb /= 2) {
-    const uint32_t slices = kWaves / nb;
-    if (blocks % nb) continue;
-    const uint32_t ks = (per + slices - 1) / slices * sg;
-    if (ks > most) continue;
-    best = {nb, ks};
-    if (uint64_t{blocks / nb} * splits >= 256) break;
-  }
-  return best;
+  if (!sq_format_supported(fmt) || !splits || !rows || rows > SQ_MAXIMUM_DECODE_ROWS || blocks % 4) return {0, 0};
+  const uint32_t units = K / 32 / sg;
+  if (units % splits || !(units / splits)) return {0, 0};
+  // The shortest slices (8, 16 or 32 groups; a gate/up pair streams two tensors, at most 16) whose waves fit one
+  // workgroup of the tile the rows run.
+  const uint32_t gs = units / splits * sg;
+  const uint32_t most = rows <= kColumnTileRows ? kColumnMaxWaves : row_max_waves(rows <= 16 ? 1 : 2, pair ? 2 : 1);
+  for (uint32_t ks = 8; ks <= (pair ? kColumnMaxGroups / 2 : kColumnMaxGroups); ks *= 2)
+    if ((gs + ks - 1) / ks <= most) return {(gs + ks - 1) / ks, ks};
+  return {0, 0};
 }
 
 hipError_t launch_decode(uint32_t fmt, uint32_t epilogue, bool f32_output, const DecodeArgs &args,
                          hipStream_t stream) {
   if (args.rows <= kColumnTileRows) return launch_decode_column(fmt, epilogue, f32_output, args, stream);
-  DecodeArgs a = args;
-  uint32_t blocks = 0;
-  for (uint32_t s = 0; s < a.segments; ++s) blocks += a.seg[s].tiles * 4;
-  const bool pair = a.gate.plane0 != nullptr;
-  const DecodeLayout layout = decode_layout(fmt, blocks, a.K, a.splits, pair, a.rows);
+  uint32_t tiles = 0;
+  for (uint32_t s = 0; s < args.segments; ++s) tiles += args.seg[s].tiles;
+  const bool pair = args.gate.plane0 != nullptr;
+  const DecodeLayout layout = decode_layout(fmt, tiles * 4, args.K, args.splits, pair, args.rows);
   if (!layout.nb) return hipErrorInvalidValue;
-  a.nb = layout.nb;
   switch (fmt) {
-    case SQ_FMT_AF4G32: return launch_format<SQ_FMT_AF4G32>(epilogue, f32_output, pair, a, blocks, layout.ks, stream);
-    case SQ_FMT_AF4G64: return launch_format<SQ_FMT_AF4G64>(epilogue, f32_output, pair, a, blocks, layout.ks, stream);
-    case SQ_FMT_AF4G128: return launch_format<SQ_FMT_AF4G128>(epilogue, f32_output, pair, a, blocks, layout.ks, stream);
-    case SQ_FMT_Q4K: return launch_format<SQ_FMT_Q4K>(epilogue, f32_output, pair, a, blocks, layout.ks, stream);
+    case SQ_FMT_AF4G32: return launch_format<SQ_FMT_AF4G32>(epilogue, f32_output, pair, args, tiles, layout, stream);
+    case SQ_FMT_AF4G64: return launch_format<SQ_FMT_AF4G64>(epilogue, f32_output, pair, args, tiles, layout, stream);
+    case SQ_FMT_AF4G128: return launch_format<SQ_FMT_AF4G128>(epilogue, f32_output, pair, args, tiles, layout, stream);
+    case SQ_FMT_Q4K: return launch_format<SQ_FMT_Q4K>(epilogue, f32_output, pair, args, tiles, layout, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -26,7 +26,8 @@ struct Segment {
 // dispatch.
 //  - The column tile (rows <= kColumnTileRows): grid (64-column tiles, splits) of up to kColumnMaxWaves waves, each
 //    lane one destination column.
-//  - The row tile (more rows): grid (16-column blocks / nb, splits), rows on the MFMA's 16-row side.
+//  - The row tile (more rows): grid (64-column tiles, splits) of up to 16 waves (fewer for more than 16 rows or a
+//    gate/up pair), rows on the MFMA's 16-row side.
 constexpr uint32_t kColumnTileRows = 4;
 // The column tile's most waves (K slices) per workgroup, and the most groups of 32 inputs one wave streams.
 constexpr uint32_t kColumnMaxWaves = 16, kColumnMaxGroups = 32;
@@ -40,11 +41,10 @@ struct DecodeArgs {
   float *partials;
   uint32_t *counters;
   uint32_t K, rows, splits, out_stride;
-  uint32_t nb;             // the row tile's 16-column blocks per workgroup (the launcher's layout)
 };
-// A decode dispatch's layout. Row tile: nb 16-column blocks per workgroup, each over 4 / nb K slices of ks groups of
-// 32 inputs. Column tile: nb waves per workgroup, each a K slice of ks groups (8, 16 or 32) of the split. {0, 0} when the split is not one the tile
-// runs (a K partition takes whole meta units; the row tile also holds its slice in registers).
+// A decode dispatch's layout: nb waves per workgroup, each a K slice of ks groups of 32 inputs (8, 16 or 32) of the
+// split. {0, 0} when the split is not one the tile runs (a K partition takes whole meta units, and the split's
+// slices must fit one workgroup).
 struct DecodeLayout {
   uint32_t nb, ks;
 };

@@ -48,39 +48,37 @@ def test_decode_plans(n, k, rows):
     assert gate == 0
 
 
-def column_time(n, k, s, pair=False):
-    """The column tile's split cost model: a workgroup streams at most 55 GB/s, HBM 6.5 TB/s, 2.5 us per split."""
-    bytes_ = (2 if pair else 1) * n * (k * 0.5 + k // 32 * 2.0)
-    return max(bytes_ / (min(n // 64 * s, 256) * 55e9), bytes_ / 6.5e12) + (2.5e-6 if s > 1 else 0.0)
+def split_law(n, k, budget, max_waves=16, pair=False):
+    """The fewest splits whose workgroups stream at most `budget` bytes, the grid kept within 256 compute units,
+    among splits whose K slices fit one workgroup (at most `max_waves` waves of at most 32 groups)."""
+    tiles, groups = n // 64, k // 32
+    tile_bytes = (2 if pair else 1) * 64 * (k * 0.5 + groups * 2.0)
+    best = None
+    for s in (1, 2, 4, 8, 16):
+        if groups % (2 * s) or groups // s > max_waves * 32:
+            continue
+        if best is not None and tiles * s > 256:
+            break
+        best = s
+        if tile_bytes / s <= budget:
+            break
+    return best
 
 
-def column_layout_fits(k, s):
-    """A split's groups fit one workgroup: at most 16 waves of at most 32 groups each."""
-    return k // 32 // s <= 16 * 32
-
-
-@pytest.mark.parametrize("n,k,want", [(4096, 4096, 1), (1024, 4096, 1), (14336, 4096, 1), (4096, 14336, 2),
-                                      (27648, 5120, 1), (4096, 16384, 2), (4096, 32768, 2)])
+@pytest.mark.parametrize("n,k,want", [(4096, 4096, 1), (1024, 4096, 1), (14336, 4096, 1), (4096, 14336, 4),
+                                      (27648, 5120, 1), (4096, 16384, 4), (4096, 32768, 4)])
 def test_split_law_column_tile(n, k, want):
-    """Rows <= 4: the split of least estimated time, the fewest on a tie."""
+    """Rows <= 4: workgroups of at most 160 KB."""
     s = sq.plan_for(sq.decode_workload(n, k, 1), sq.projection(seg(n, k))).config.splits
-    assert s == want
-    valid = [c for c in (1, 2, 4, 8, 16) if column_layout_fits(k, c)]
-    times = {c: column_time(n, k, c) for c in valid}
-    assert times[s] == min(times.values())
-    assert all(times[c] > times[s] for c in valid if c < s)
+    assert s == want == split_law(n, k, 160e3)
 
 
-def test_split_law_row_tile():
-    # 14336 x 4096: 896 16-column blocks fill 256 compute units without a split.
-    plan = sq.plan_for(sq.decode_workload(14336, 4096, 16), sq.projection(seg(14336, 4096)))
-    assert plan.config.splits == 1
-    # 1024 x 4096: 64 blocks need K partitions to fill the device.
-    plan = sq.plan_for(sq.decode_workload(1024, 4096, 16), sq.projection(seg(1024, 4096)))
-    assert plan.config.splits >= 4
-    # 4096 x 14336: a K slice of 448 groups does not fit one workgroup's registers unsplit.
-    plan = sq.plan_for(sq.decode_workload(4096, 14336, 16), sq.projection(seg(4096, 14336)))
-    assert plan.config.splits >= 2
+@pytest.mark.parametrize("rows", [8, 16])
+@pytest.mark.parametrize("n,k,want", [(14336, 4096, 1), (1024, 4096, 2), (4096, 4096, 2), (4096, 14336, 4)])
+def test_split_law_row_tile(rows, n, k, want):
+    """5..32 rows: workgroups of at most 80 KB."""
+    s = sq.plan_for(sq.decode_workload(n, k, rows), sq.projection(seg(n, k))).config.splits
+    assert s == want == split_law(n, k, 80e3)
 
 
 def test_prefill_plans():
