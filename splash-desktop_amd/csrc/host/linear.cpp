@@ -159,7 +159,8 @@ LinearScratchSize LinearPlan::scratchSize() const noexcept {
   const auto [n, k] = workload_.matrix;
   if (config_.tile == LinearTile::GgufPrefill) {
     const uint64_t rows = storageRows();
-    return {rows * k * 2, rows * 4, 0, 0, 0};
+    const uint64_t block = kern::kPrefillRowBlock, halfRows = (workload_.rows + block - 1) / block * block;
+    return {halfRows * k * 2, rows * 4, 0, 0, 0};
   }
   // Counters: one per workgroup column of the decode tile, at most one per 16 destination columns.
   const uint64_t columns = config_.oneGateUpPass ? 2 * uint64_t{n} : n;

@@ -55,7 +55,9 @@ hipError_t launch_decode_column(uint32_t fmt, uint32_t epilogue, bool f32_output
                                 hipStream_t stream);
 
 // The prefill tile (rows > 32): activations converted once to fp16 with a power-of-two scale per row
-// (launch_prefill_prepare), then dequantised fp16 weights on MFMA.
+// (launch_prefill_prepare), then dequantised fp16 weights on MFMA. The fp16 copy holds kPrefillRowBlock-row
+// blocks: rows past the live ones are read and never stored.
+constexpr uint32_t kPrefillRowBlock = 256;
 hipError_t launch_prefill_prepare(const uint16_t *input, uint32_t rows, uint32_t K, uint16_t *half_input,
                                   float *row_scale, hipStream_t stream);
 struct PrefillArgs {

@@ -42,7 +42,7 @@ def run_prefill(w_list, x, epilogue=sq.EPILOGUE_NONE, residual=None, gate_scratc
     return out[:rows]
 
 
-@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K, oracle.FMT_AF4G128])
+@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K, oracle.FMT_AF4G128, oracle.FMT_AF4G32])
 @pytest.mark.parametrize("rows", [33, 128, 300])
 def test_prefill_dense(fmt, rows):
     rng = np.random.default_rng(rows + fmt)
