@@ -60,27 +60,39 @@ __device__ __forceinline__ uint32_t chunk_at(uint32_t r, uint32_t c) { return r 
 
 // ---------------------------------------------------------------- prepare
 
+// One workgroup per row: the row's bf16 inputs in 16-byte vectors (K is a multiple of 64), the largest magnitude
+// from a wave reduction and LDS, then the fp16 row scaled by 2^-e where 2^e brings the largest below 2^16.
 __global__ __launch_bounds__(256) void prepare_kernel(const uint16_t *input, uint32_t K, uint16_t *half_input,
                                                       float *row_scale) {
-  const uint32_t r = blockIdx.x;
-  const uint16_t *x = input + (size_t)r * K;
-  uint32_t largest = 0;   // magnitude bits of the largest |x| (bf16 bits order like the values)
-  for (uint32_t k = threadIdx.x; k < K; k += 256) largest = max(largest, (uint32_t)(x[k] & 0x7FFFu));
-  __shared__ uint32_t part[256];
-  part[threadIdx.x] = largest;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) part[threadIdx.x] = max(part[threadIdx.x], part[threadIdx.x + s]);
-    __syncthreads();
+  const uint32_t r = blockIdx.x, vectors = K / 8;
+  const u32x4 *x = (const u32x4 *)(input + (size_t)r * K);
+  u32x4 *h = (u32x4 *)(half_input + (size_t)r * K);
+  uint32_t largest = 0;   // magnitude bits of the largest |x| (bf16 bit patterns order like the magnitudes)
+  for (uint32_t v = threadIdx.x; v < vectors; v += 256) {
+    const u32x4 w = x[v];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) largest = max(largest, max(w[e] & 0x7FFFu, (w[e] >> 16) & 0x7FFFu));
   }
-  largest = part[0];
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) largest = max(largest, (uint32_t)__shfl_xor((int)largest, d));
+  __shared__ uint32_t part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = largest;
+  __syncthreads();
+  largest = max(max(part[0], part[1]), max(part[2], part[3]));
   // Exponent field of the largest magnitude: scale by 2^-(e - 15) when it is 2^16 or more, so it ends below 2^16.
   const int exponent = (int)(min(largest, 0x7F80u) >> 7) - 127;
   const int shift = exponent >= 16 ? exponent - 15 : 0;
   const float down = ldexpf(1.0f, -shift);
   if (threadIdx.x == 0) row_scale[r] = ldexpf(1.0f, shift);
-  uint16_t *h = half_input + (size_t)r * K;
-  for (uint32_t k = threadIdx.x; k < K; k += 256) h[k] = f32_to_f16(bf16_to_f32(x[k]) * down);
+  for (uint32_t v = threadIdx.x; v < vectors; v += 256) {
+    const u32x4 w = x[v];
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = (uint32_t)f32_to_f16(bf16_to_f32(w[e] & 0xFFFFu) * down) |
+             ((uint32_t)f32_to_f16(bf16_to_f32(w[e] >> 16) * down) << 16);
+    h[v] = o;
+  }
 }
 
 // ---------------------------------------------------------------- GEMM
@@ -209,25 +221,25 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
     read_codes(stage ^ 1);
     const uint8_t *sa = lds + stage * kStageBytes, *sb = sa + BM * kRowBytes;
     // Sixteen groups g = (kk, mi): four MFMAs of A block mi against the four B blocks of input half kk. Each
-    // group's A fragment (and half 1's B fragments) is read one group ahead; after every fourth group, one of the
-    // wave's four 16-byte chunks of the next step's weights.
+    // group's A fragment is read two groups ahead (half 1's B fragments during half 0); after every fourth group,
+    // one of the wave's four 16-byte chunks of the next step's weights.
     const auto read_a = [&](int g) __attribute__((always_inline)) {
       return *(const u32x4 *)(sa + chunk_at(wm * 128 + (g & 7) * 16 + j, 4 * (g >> 3) + q));
     };
     u32x4 fb[2][4];
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) fb[0][ni] = *(const u32x4 *)(sb + chunk_at(wn * 64 + ni * 16 + j, q));
-    u32x4 fa = read_a(0);
+    u32x4 fa[3];
+    fa[0] = read_a(0);
+    fa[1] = read_a(1);
 #pragma unroll
     for (int g = 0; g < 16; ++g) {
       const int kk = g >> 3, mi = g & 7;
-      u32x4 fa_next = fa;
-      if (g + 1 < 16) fa_next = read_a(g + 1);
+      if (g + 2 < 16) fa[(g + 2) % 3] = read_a(g + 2);
       if (g < 4) fb[1][g] = *(const u32x4 *)(sb + chunk_at(wn * 64 + g * 16 + j, 4 + q));
 #pragma unroll
-      for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma_f16(fa, fb[kk][ni], acc[mi][ni]);
+      for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma_f16(fa[g % 3], fb[kk][ni], acc[mi][ni]);
       if (g % 4 == 3) write_chunk(next, stage ^ 1, g / 4);
-      fa = fa_next;
     }
     // This step's activation copies (issued first) and chunk writes are done; its code and meta copies, read by
     // this wave only, may still be in flight.
