@@ -1,0 +1,35 @@
+// Host-only use of the C++ face (include/splash_q4.hpp): plans, scratch sizes and the reference's exceptions.
+// Nothing here touches a GPU. Built and run by tests/test_capi.py.
+#include <cstdio>
+#include <stdexcept>
+
+#include "splash_q4.hpp"
+
+using namespace splash_q4::ops;
+
+int main() {
+  const Linear linear({256});
+  Projection p{};
+  p.output_size = 14336;
+  p.input_size = 4096;
+  p.segment_count = 1;
+  p.destination = SQ_OUTPUT_BF16;
+  p.segments[0].output_size = 14336;
+  p.segments[0].input_size = 4096;
+  p.segments[0].format_id = SQ_FMT_AF4G64;
+  p.segments[0].plane0.bytes = 14336ull * 4096 / 2;
+  p.segments[0].meta.bytes = 14336ull * 4096 / 64 * 4;
+  const LinearPlan decode = linear.decodePlan(p, 1);
+  const LinearPlan prefill = linear.prefillPlan(p, 2048, LinearEpilogue::None);
+  const LinearScratchSize s = linear.decodeScratchSize({14336, 4096});
+  std::printf("decode rows %u tile %u splits %u; prefill tile %u; decode partials %llu\n", decode.storage_rows,
+              decode.config.tile, decode.config.splits, prefill.config.tile, (unsigned long long)s.partials);
+  try {
+    (void)linear.decodePlan(p, 0);
+    std::printf("no exception\n");
+    return 1;
+  } catch (const std::invalid_argument &e) {
+    std::printf("invalid_argument: %s\n", e.what());
+  }
+  return 0;
+}

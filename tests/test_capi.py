@@ -1,11 +1,14 @@
 """The C ABI on the CPU: the library loads and exports every entry point include/splash_q4.h declares, and the
 host-side planning and validation behave as the reference's ops::Linear / ops::MoE do (plans, storage rows,
 scratch sizes, and std::invalid_argument before anything is launched). No GPU work is issued here."""
+import pathlib
 import re
 
 import pytest
 
 import splash_q4 as sq
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
 
 
 def declared_functions():
@@ -201,3 +204,19 @@ def test_moe_plans_and_workspace():
         sq.call("sq_moe_prefill_plan", sq.byref(sq.MoeShape(2000, 128, 8, 768, sq.FMT_AF4G64)), 8, sq.byref(plan))
     with pytest.raises(sq.InvalidArgument, match="invalid MoE rows"):
         sq.call("sq_moe_decode_plan", sq.byref(shape), 33, sq.byref(plan))
+
+
+def test_cxx_face_plans_and_throws(tmp_path):
+    """include/splash_q4.hpp compiles as C++17, plans through the library and turns a refused plan back into the
+    reference's std::invalid_argument (host only)."""
+    import shutil
+    import subprocess
+    if shutil.which("g++") is None:
+        pytest.skip("no g++")
+    exe = tmp_path / "wrapper_check"
+    lib_dir = sq.LIBRARY.parent
+    subprocess.run(["g++", "-std=c++17", "-O1", "-I", str(sq.HEADER.parent), str(ROOT / "tests" / "cxx_wrapper_check.cpp"),
+                    "-L", str(lib_dir), "-lsplash_q4", f"-Wl,-rpath,{lib_dir}", "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    assert "decode rows 8 tile 0" in out and "prefill tile 1" in out
+    assert "invalid_argument:" in out

@@ -218,3 +218,35 @@ def test_group_routes_invariants():
         assert grouped[g] == r
         assert tiles[g // tile_rows, 0] == selected.ravel()[r]
     assert np.count_nonzero(grouped == 0xFFFFFFFF) == tiles.shape[0] * tile_rows - rows * top_k
+
+
+def test_route_weights_closed_form():
+    """Scores ln 4, ln 2, 0 (and losers) give weights 4/7, 2/7, 1/7 in rank order: a sign or index slip in the
+    renormalised softmax moves them."""
+    scores = np.array([[0.0, np.log(2.0), -5.0, np.log(4.0), -6.0]], np.float32)
+    selected, weights = oracle.route_select(scores, 3)
+    assert selected.tolist() == [[3, 1, 0]]
+    assert np.allclose(weights[0], [4 / 7, 2 / 7, 1 / 7], rtol=1e-6)
+
+
+@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K])
+def test_cpu_baseline_matches_fp64(fmt):
+    """The CPU baseline (threaded fp32 sums of the dequantised weights) agrees with the fp64 projection within the
+    accumulation bound plus one bf16 rounding of the output."""
+    rng = np.random.default_rng(13)
+    n, k, m = 128, 1024, 3
+    native = oracle.fixture(fmt, n, k, 17)
+    if fmt == oracle.FMT_AF4G64:   # the fixture's raw meta bytes span bf16's range: give the groups real scales
+        blocks = native.reshape(-1, 36)
+        sb = ((np.abs(rng.standard_normal(blocks.shape[0])).astype(np.float32) * np.float32(0.02)).view(np.uint32)
+              >> 16).astype(np.uint16)
+        zb = (((np.float32(-8) * (sb.astype(np.uint32) << 16).view(np.float32)).view(np.uint32)) >> 16).astype(np.uint16)
+        blocks[:, 0:2] = sb.view(np.uint8).reshape(-1, 2)
+        blocks[:, 2:4] = zb.view(np.uint8).reshape(-1, 2)
+    plane0, meta, values = oracle.repack(fmt, native, n, k)
+    x = (rng.standard_normal((m, k)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    out, secs = oracle.cpu_matmul(fmt, x, plane0, meta, n, 4)
+    got = (out.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    value, magnitude, inputs, largest = oracle.project_f64(x, values)
+    bound = oracle.projection_bound(magnitude, inputs, largest, False) + np.abs(value) * 2.0 ** -8
+    assert secs > 0 and np.all(np.abs(got - value) <= bound)
