@@ -159,8 +159,7 @@ LinearScratchSize LinearPlan::scratchSize() const noexcept {
   const auto [n, k] = workload_.matrix;
   if (config_.tile == LinearTile::GgufPrefill) {
     const uint64_t rows = storageRows();
-    const uint64_t block = kern::kPrefillRowBlock, halfRows = (workload_.rows + block - 1) / block * block;
-    return {halfRows * k * 2, rows * 4, 0, 0, 0};
+    return {uint64_t{workload_.rows} * k * 2, rows * 4, 0, 0, 0};
   }
   // Counters: one per workgroup column of the decode tile, at most one per 16 destination columns.
   const uint64_t columns = config_.oneGateUpPass ? 2 * uint64_t{n} : n;
@@ -280,6 +279,13 @@ void Linear::add(hipStream_t graph, LinearBuffers b, const Projection &p, const 
   requireBytes(b.scratch.counters, scratch.counters, "projection counters");
   requireSegments(p, w.matrix);
   if (gate) requireSegments(*gate, w.matrix);
+  if (selected.configuration().tile == LinearTile::GgufPrefill) {
+    // The prefill tile moves activations, outputs and epilogue operands in 16-byte vectors.
+    const auto aligned = [](const Buffer &buffer) { return (reinterpret_cast<uintptr_t>(buffer.ptr) & 15u) == 0; };
+    if (!aligned(b.input) || !aligned(b.output) || !aligned(b.residual) || !aligned(b.gateScratch) ||
+        !aligned(b.scratch.input))
+      throw std::invalid_argument("prefill projection buffers are 16-byte aligned");
+  }
   const std::vector<QuantizedSegment> &segments = p.blocks().segments;
   if (selected.destination() == FloatOutput::Float32 && segments.size() > 1)
     throw std::invalid_argument("an fp32 destination takes a single-tensor block projection");
@@ -326,6 +332,7 @@ void Linear::add(hipStream_t graph, LinearBuffers b, const Projection &p, const 
       a.K = k;
       a.rows = w.rows;
       a.out_stride = n;
+      a.compute_units = computeUnits_;
       requireLaunch(kern::launch_prefill(group.front()->formatId, epilogueOf(w.epilogue), a, graph), "prefill tile");
     }
     return;

@@ -81,11 +81,18 @@ __device__ __forceinline__ uint16_t f32_to_f16(float v) { return __builtin_bit_c
 // silu(g) = g / (1 + 2^(-g log2 e)), the reference's form of it (activation.h:8-13).
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + exp2f(-1.44269504089f * g)); }
 
+// Epilogue of one output before its bf16 rounding, given the bf16 bits of its aux element: Residual adds it,
+// UpWithGate rounds the up value to bf16 and multiplies by silu of the gate (gguf_tile.h:6-14).
+template <uint32_t EP>
+__device__ __forceinline__ float epilogue_bits(float v, uint32_t aux_bits) {
+  if constexpr (EP == 1) v += bf16_to_f32(aux_bits);
+  if constexpr (EP == 2) v = bf16_to_f32(f32_to_bf16(v)) * silu(bf16_to_f32(aux_bits));
+  return v;
+}
 template <uint32_t EP>
 __device__ __forceinline__ float epilogue(float v, const uint16_t *aux, size_t at) {
-  if constexpr (EP == 1) v += bf16_to_f32(aux[at]);
-  if constexpr (EP == 2) v = bf16_to_f32(f32_to_bf16(v)) * silu(bf16_to_f32(aux[at]));
-  return v;
+  if constexpr (EP == 0) return v;
+  else return epilogue_bits<EP>(v, aux[at]);
 }
 
 // Per-format traits. SG: groups of 32 one scale covers; UNIT: groups of 32 per meta unit; META: meta unit bytes.

@@ -55,9 +55,7 @@ hipError_t launch_decode_column(uint32_t fmt, uint32_t epilogue, bool f32_output
                                 hipStream_t stream);
 
 // The prefill tile (rows > 32): activations converted once to fp16 with a power-of-two scale per row
-// (launch_prefill_prepare), then dequantised fp16 weights on MFMA. The fp16 copy holds kPrefillRowBlock-row
-// blocks: rows past the live ones are read and never stored.
-constexpr uint32_t kPrefillRowBlock = 256;
+// (launch_prefill_prepare, [rows][K] fp16 in the order the tile reads), then dequantised fp16 weights on MFMA.
 hipError_t launch_prefill_prepare(const uint16_t *input, uint32_t rows, uint32_t K, uint16_t *half_input,
                                   float *row_scale, hipStream_t stream);
 struct PrefillArgs {
@@ -68,6 +66,7 @@ struct PrefillArgs {
   uint16_t *output;            // bf16 [rows][out_stride]
   const uint16_t *aux;
   uint32_t K, rows, out_stride;
+  uint32_t compute_units;      // the device's, for the tile choice
 };
 hipError_t launch_prefill(uint32_t fmt, uint32_t epilogue, const PrefillArgs &args, hipStream_t stream);
 

@@ -8,18 +8,22 @@
 // rows, stay finite) and converts the row to fp16, which is exact for every bf16 input in half's normal range; the
 // epilogue multiplies the row's sums back by the same power of two.
 //
-// CDNA4 mapping. A 512-thread workgroup computes a 256-row x 256-column tile, its eight waves 128 x 64 each as 8 x 4
-// 16x16x32 f16 MFMAs per 32 inputs (128 fp32 accumulators per lane, two waves per SIMD, so one wave's VALU and LDS
-// work runs under the other's MFMAs). Per 64-input step, double buffered in LDS (2 x 64 KiB):
-//  - the activations (fp16, 256 x 64) go global -> LDS with global_load_lds_dwordx4, no registers on the way;
-//  - the codes and meta of the tile's columns go global -> LDS the same way, one step ahead of their use, and lane
-//    l of wave w dequantises group w / 4 of column l of plane tile w % 4 into fp16 in natural input order, written as
-//    four 16-byte chunks;
-//  - both tiles keep 128-byte rows whose 16-byte chunk c sits in slot c ^ (row % 8), so the MFMA fragment reads
-//    (16 lanes, 16 rows, one chunk) and the chunk writes (8 lanes a pass, one row each) spread over all banks.
-// Step s + 1's activation copies and step s + 2's code loads are issued before step s's MFMAs, and step s + 1's
-// weights are dequantised into the other buffer between them, a 16-byte chunk after each 16-row block's MFMAs (one
-// wave per SIMD has no other wave to hide the VALU and LDS work behind); one barrier a step.
+// CDNA4 mapping. A workgroup of four waves (one per SIMD) computes BM rows x 256 columns; wave w owns one 64-column
+// plane tile and all BM rows of it, as BM/16 x 4 16x16x32 f16 MFMAs per 32 inputs (BM fp32 accumulators per lane,
+// held in the accumulation registers). The product runs weights x activations, so each lane ends holding eight
+// consecutive outputs of a row twice over and stores them as 16-byte vectors. Per 64-input step:
+//  - the activations (fp16, BM x 64) go global -> LDS with global_load_lds_dwordx4, no registers on the way, two
+//    steps ahead into a ring of three stages; all four waves read them as MFMA B fragments, four blocks at a time;
+//  - each wave's plane tile codes and meta go global -> LDS the same way, three steps ahead into a ring of four
+//    slots only that wave reads, and the wave dequantises its own A fragments from them straight into registers:
+//    lane (j, q) takes plane word q of one column, whose eight codes are inputs 4q..4q+3 and 16+4q..19+4q of the
+//    group. The prepare dispatch stores each group of 32 fp16 inputs in that order (16-byte chunk q = inputs
+//    4q..4q+3 then 16+4q..19+4q), so one 16-byte activation read pairs with one plane word: the dot product over
+//    the group is the same sum in another order of its terms;
+//  - group 1's weights are dequantised during the step's first half of MFMAs, the next step's group 0 during the
+//    second half, in pieces of four weights between MFMAs.
+// LDS rows are 128 bytes whose 16-byte chunk c sits in slot c ^ (row % 8), so fragment reads (16 rows x one chunk
+// per 16 lanes) and the copies spread over all banks. One barrier a step.
 #include <type_traits>
 
 #include "device.hpp"
@@ -28,13 +32,14 @@
 namespace sq::kern {
 namespace {
 
-constexpr int BM = 256, BN = 256, BK = 64, kThreads = 512;
-constexpr int kRowBytes = BK * 2;                            // one LDS row: 64 fp16
-constexpr int kStageBytes = (BM + BN) * kRowBytes;           // A rows then B rows
-constexpr int kCodeBytes = BN * 32;                          // a step's raw codes: [4 tiles][2 groups][64 columns][16 B]
-constexpr int kMetaBytes = BN * 16;                          // a step's meta: [4 tiles][up to 2 units][64 columns][META]
-constexpr int kCodeBase = 2 * kStageBytes, kMetaBase = kCodeBase + 2 * kCodeBytes;
-constexpr int kLdsBytes = kMetaBase + 2 * kMetaBytes;
+constexpr int BK = 64, kWaves = 4, kThreads = 64 * kWaves, kStages = 3, kSlots = 4;
+constexpr int kRowBytes = BK * 2;                  // one LDS activation row: 64 fp16
+constexpr int kWaveSlotBytes = 2048 + 1024;        // a wave's codes of one step (2 groups x 64 columns x 16 B) + meta
+constexpr int kSlotBytes = kWaves * kWaveSlotBytes;
+template <int BM> constexpr int stage_bytes() { return BM * kRowBytes; }
+template <int BM> constexpr int code_base() { return kStages * stage_bytes<BM>(); }
+template <int BM> constexpr int lds_bytes() { return code_base<BM>() + kSlots * kSlotBytes; }
+
 // global -> LDS copy of SIZE bytes per lane (global_load_lds): lane l's bytes land at lds + SIZE l.
 // (The size is spelled as a literal: the host pass of hipcc does not take a template argument there.)
 template <int SIZE>
@@ -44,29 +49,28 @@ __device__ __forceinline__ void copy_to_lds(const void *src, uint8_t *lds) {
   if constexpr (SIZE == 16) __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
   else __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
 }
-// s_waitcnt immediates (gfx9: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8): a vmcnt below 16 with
-// lgkmcnt(0) (kWaitLgkm), or without an lgkm wait (kWaitVm).
-constexpr int kWaitLgkm = 0x0070, kWaitVm = 0x0F70;
 // The workgroup barrier between steps: the waits before it are explicit (a __syncthreads() fence would also wait for
-// the code copies still in flight); LDS writes complete under lgkmcnt are visible to every wave of the workgroup.
+// copies still in flight); LDS writes complete under vmcnt / lgkmcnt are visible to every wave of the workgroup.
 // The empty asm statements keep the compiler from moving memory accesses across it.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }
+// s_waitcnt immediate for vmcnt(n) alone (gfx9: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0070 | 0x0F00; }
 // Byte offset of 16-byte chunk c of LDS row r (the XOR swizzle).
 __device__ __forceinline__ uint32_t chunk_at(uint32_t r, uint32_t c) { return r * kRowBytes + ((c ^ (r & 7)) << 4); }
 
 // ---------------------------------------------------------------- prepare
 
-// One workgroup per row: the row's bf16 inputs in 16-byte vectors (K is a multiple of 64), the largest magnitude
-// from a wave reduction and LDS, then the fp16 row scaled by 2^-e where 2^e brings the largest below 2^16.
+// One workgroup per row: the largest magnitude of the row's bf16 inputs (16-byte vectors, a wave reduction and
+// LDS), then the fp16 row scaled by 2^-e where 2^e brings the largest below 2^16, each group of 32 stored with its
+// 16-byte chunk q holding inputs 4q..4q+3 and 16+4q..19+4q.
 __global__ __launch_bounds__(256) void prepare_kernel(const uint16_t *input, uint32_t K, uint16_t *half_input,
                                                       float *row_scale) {
   const uint32_t r = blockIdx.x, vectors = K / 8;
   const u32x4 *x = (const u32x4 *)(input + (size_t)r * K);
-  u32x4 *h = (u32x4 *)(half_input + (size_t)r * K);
   uint32_t largest = 0;   // magnitude bits of the largest |x| (bf16 bit patterns order like the magnitudes)
   for (uint32_t v = threadIdx.x; v < vectors; v += 256) {
     const u32x4 w = x[v];
@@ -84,8 +88,12 @@ __global__ __launch_bounds__(256) void prepare_kernel(const uint16_t *input, uin
   const int shift = exponent >= 16 ? exponent - 15 : 0;
   const float down = ldexpf(1.0f, -shift);
   if (threadIdx.x == 0) row_scale[r] = ldexpf(1.0f, shift);
+  const u32x2 *units = (const u32x2 *)(input + (size_t)r * K);   // 4-input units
+  u32x4 *h = (u32x4 *)(half_input + (size_t)r * K);
   for (uint32_t v = threadIdx.x; v < vectors; v += 256) {
-    const u32x4 w = x[v];
+    const uint32_t g = v >> 2, c = v & 3;   // output chunk c of group g: units 8 g + c and 8 g + c + 4
+    const u32x2 lo = units[8 * g + c], hi = units[8 * g + c + 4];
+    const uint32_t w[4] = {lo[0], lo[1], hi[0], hi[1]};
     u32x4 o;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
@@ -97,19 +105,10 @@ __global__ __launch_bounds__(256) void prepare_kernel(const uint16_t *input, uin
 
 // ---------------------------------------------------------------- GEMM
 
-// Eight codes of one plane word as floats in natural input order: word q holds inputs 4q..4q+3 at bits 0, 16, 4,
-// 20 (part 0) and 16+4q..19+4q at bits 8, 24, 12, 28 (part 1).
-// The codes of one plane word's part (inputs 4q..4q+3 at bits 0, 16, 4, 20, or 16+4q..19+4q at bits 8, 24, 12, 28)
-// as floats: each byte of lo and hi holds one code (v_cvt_f32_ubyte0..3). The mask arrives in a register the
-// compiler cannot see through, so each code costs one conversion instead of an extract and a conversion.
+// One code of a masked plane word as a float: after masking every other nibble each byte holds one code
+// (v_cvt_f32_ubyte0..3). The mask arrives in a register the compiler cannot see through, so each code costs one
+// conversion instead of an extract and a conversion.
 __device__ __forceinline__ float byte_float(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xFFu); }
-__device__ __forceinline__ void word_codes(uint32_t w, uint32_t mask, int part, float (&v)[4]) {
-  const uint32_t lo = w & mask, hi = (w >> 4) & mask;
-  v[0] = byte_float(lo, part);
-  v[1] = byte_float(lo, part + 2);
-  v[2] = byte_float(hi, part);
-  v[3] = byte_float(hi, part + 2);
-}
 typedef _Float16 half2 __attribute__((ext_vector_type(2)));
 typedef float float2v __attribute__((ext_vector_type(2)));
 // fp16(fma(q, s, z)) of two codes, rounded as the reference rounds: to fp32 by the fma, then to fp16 (the empty asm
@@ -119,165 +118,244 @@ __device__ __forceinline__ uint32_t dequant_pair(float q0, float q1, Coef k) {
   asm volatile("" : "+v"(v0), "+v"(v1));
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{v0, v1}, half2));
 }
+// Four of the eight fp16 weights of plane word q of a group, in A-chunk order: the word holds inputs 4q..4q+3 at
+// bits 0, 16, 4, 20 (part 0: fragment words 0, 1) and 16+4q..19+4q at bits 8, 24, 12, 28 (part 1: words 2, 3);
+// lo and hi are the word masked and shifted down a nibble and masked.
+__device__ __forceinline__ u32x2 dequant_part(uint32_t lo, uint32_t hi, int part, Coef k) {
+  return u32x2{dequant_pair(byte_float(lo, part), byte_float(lo, part + 2), k),
+               dequant_pair(byte_float(hi, part), byte_float(hi, part + 2), k)};
+}
 
-template <uint32_t FMT, uint32_t EP>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
+// The plane tile column whose weights lane j of the MFMA's A operand carries in column block t. The product runs
+// weights x activations (D = W X^T), so lane (j', q) of D holds column column_of(4q + i, t) for i = 0..3: with
+// this order those are columns 8q + 4(t % 2) + i (blocks 0, 1) and 32 + 8q + 4(t % 2) + i (blocks 2, 3), eight
+// consecutive outputs of one row twice over.
+__device__ __forceinline__ uint32_t column_of(uint32_t j, int t) {
+  return (t >> 1) * 32 + 8 * (j >> 2) + 4 * (t & 1) + (j & 3);
+}
+
+// The meta of column c for one step out of the wave's LDS slot: af4g32 the words of its two groups, af4g64 and
+// af4g128 the one word covering the step, Q4_K the 16-byte header of its 256-input unit.
+template <uint32_t FMT>
+__device__ __forceinline__ MetaWords slot_meta(const uint8_t *meta, uint32_t c) {
+  if constexpr (FMT == SQ_FMT_Q4K) {
+    const u32x4 v = *(const u32x4 *)(meta + c * 16);
+    return MetaWords{{v[0], v[1], v[2], v[3]}};
+  } else if constexpr (FMT == SQ_FMT_AF4G32) {
+    return MetaWords{{*(const uint32_t *)(meta + c * 4), *(const uint32_t *)(meta + 256 + c * 4), 0u, 0u}};
+  } else {
+    return MetaWords{{*(const uint32_t *)(meta + c * 4), 0u, 0u, 0u}};
+  }
+}
+// The coefficients of group h (0, 1) of the step, the step's group `group` of the tile.
+template <uint32_t FMT>
+__device__ __forceinline__ Coef group_coef(const MetaWords &m, uint32_t group, int h) {
+  if constexpr (FMT == SQ_FMT_AF4G32) return coef<FMT>(MetaWords{{m.w[h], 0u, 0u, 0u}}, group);
+  else return coef<FMT>(m, group);
+}
+
+template <uint32_t FMT, uint32_t EP, int BM>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_kernel(PrefillArgs a) {
   using F = Fmt<FMT>;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes];
+  constexpr int MI = BM / 16;                         // 16-row blocks of the wave
+  static_assert(MI == 8 || MI == 16, "128- or 256-row tiles");
+  constexpr int kStage = stage_bytes<BM>(), kCodeBase = code_base<BM>();
+  constexpr int kMetaCopies = FMT == SQ_FMT_AF4G32 ? 2 : 1;
+  constexpr int kCopies = BM / 32 + 2 + kMetaCopies;  // copy instructions a wave issues per step
+  static_assert(kCopies < 64, "vmcnt counts to 63");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes<BM>()];
   const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, q = lane >> 4;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t wm = wave >> 2, wn = wave & 3;   // the wave's 128-row and 64-column block
   const uint32_t row0 = blockIdx.x * BM;
   const uint32_t G = a.K >> 5, units = G / F::UNIT, steps = a.K / BK;
 
-  // Weights: wave w brings group h = w / 4 of each step of plane tile 4 blockIdx.y + w % 4 and its meta unit into
-  // LDS (both groups' waves copy a shared unit: the same bytes to the same place), and lane l dequantises the group
-  // for column l of the tile. A grid of a
-  // tile count not a multiple of 4 ends short: its spare waves dequantise tile 0 into columns nothing stores.
-  const uint32_t bt = wave & 3, bh = wave >> 2;
-  uint32_t ptile = blockIdx.y * 4 + bt, s = 0;
+  // The wave's plane tile. A grid whose tile count is not a multiple of 4 ends short: a spare wave runs tile 0 of
+  // its segment and stores nothing.
+  uint32_t ptile = blockIdx.y * 4 + wave, s = 0;
   while (s + 1 < a.segments && ptile >= a.seg[s].tiles) ptile -= a.seg[s++].tiles;
-  const bool blive = ptile < a.seg[s].tiles;
+  const bool live = ptile < a.seg[s].tiles;
   const Segment seg = a.seg[s];
-  const uint8_t *bplane = seg.plane0 + ((size_t)(blive ? ptile : 0) * G * 64 + lane) * 16 + (size_t)bh * 1024;
-  const uint8_t *bmeta = seg.meta + ((size_t)(blive ? ptile : 0) * units * 64 + lane) * F::META;
-  const uint32_t bcol = 64 * bt + lane;
-  // LDS offsets of this wave's codes and of the meta its group reads: [tile][group][64 columns][16 B] and
-  // [tile][unit][64 columns][META], one unit per tile and step unless 32-input scale groups give each group its own
-  // (at most 4 KiB either way: 16-byte meta comes in 256-input units).
-  constexpr uint32_t MU = F::UNIT == 1 ? 2 : 1;
-  static_assert(4 * MU * 64 * F::META <= kMetaBytes, "a step's meta fits its stage");
-  const uint32_t code_at = (bt * 2 + bh) * 1024;
-  const uint32_t meta_at = (bt * MU + (MU == 2 ? bh : 0)) * 64 * F::META;
+  const uint8_t *bplane = seg.plane0 + ((size_t)(live ? ptile : 0) * G * 64 + lane) * 16;
+  const uint8_t *bmeta = seg.meta + (size_t)(live ? ptile : 0) * units * 64 * F::META + lane * F::META;
+  uint8_t *const wave_slot = lds + kCodeBase + wave * kWaveSlotBytes;
   uint32_t mask = 0x0F0F0F0Fu;
   asm volatile("" : "+s"(mask));
 
-  // Activations: wave w copies LDS rows 32 w .. 32 w + 31, eight per instruction: lane l fills chunk slot l % 8 of
-  // row 8 i + l / 8, i.e. input chunk (l % 8) ^ (row % 8) (row % 8 = l / 8, the same for every i). The fp16 copy
-  // holds whole 256-row tiles (rows past the live ones are never stored).
-  const uint16_t *asrc = a.half_input + (size_t)(row0 + 32 * wave + (lane >> 3)) * a.K + 8 * ((lane & 7) ^ (lane >> 3));
-  // Step `step`'s activations into stage `stage`; its codes and meta into code stage `cstage`.
-  const auto copy_a = [&](uint32_t step, uint32_t stage) __attribute__((always_inline)) {
+  // Activations: wave w copies LDS rows BM/4 w .. BM/4 (w + 1) - 1, eight per instruction: lane l fills chunk slot
+  // l % 8 of row 8 i + l / 8, i.e. input chunk (l % 8) ^ (row % 8) (row % 8 = l / 8, the same for every i).
+  constexpr int kRowsPerWave = BM / kWaves;
+  // Byte offsets of the lane's copy sources, rows clamped to the last live one (a tile past the rows reads it again).
+  uint32_t aoff[BM / 32];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      copy_to_lds<16>(asrc + (size_t)8 * i * a.K + (size_t)step * BK,
-                      lds + stage * kStageBytes + (32 * wave + 8 * i) * kRowBytes);
+  for (int i = 0; i < BM / 32; ++i) {
+    const uint32_t r = min(row0 + kRowsPerWave * wave + 8 * i + (lane >> 3), a.rows - 1);
+    aoff[i] = (r * a.K + 8 * ((lane & 7) ^ (lane >> 3))) * 2;
+  }
+  // Step `step`'s activations into stage `stage` (sources clamped to the last step: every step issues as many
+  // copies, which the vmcnt waits count on).
+  const auto copy_a = [&](uint32_t step, uint32_t stage) __attribute__((always_inline)) {
+    const uint8_t *from = (const uint8_t *)a.half_input + (size_t)min(step, steps - 1) * BK * 2;
+#pragma unroll
+    for (int i = 0; i < BM / 32; ++i)
+      copy_to_lds<16>(from + aoff[i], lds + stage * kStage + (kRowsPerWave * wave + 8 * i) * kRowBytes);
   };
-  const auto copy_b = [&](uint32_t step, uint32_t cstage) __attribute__((always_inline)) {
-    copy_to_lds<16>(bplane + (size_t)(2 * step) * 1024, lds + kCodeBase + cstage * kCodeBytes + code_at);
-    copy_to_lds<F::META>(bmeta + (size_t)((2 * step + bh) / F::UNIT) * 64 * F::META,
-                         lds + kMetaBase + cstage * kMetaBytes + meta_at);
-  };
-  u32x4 code;
-  MetaWords mw;
-  const auto read_codes = [&](uint32_t cstage) __attribute__((always_inline)) {
-    code = *(const u32x4 *)(lds + kCodeBase + cstage * kCodeBytes + code_at + lane * 16);
-    const uint8_t *m = lds + kMetaBase + cstage * kMetaBytes + meta_at + lane * F::META;
-    if constexpr (F::META == 4) {
-      mw = MetaWords{{*(const uint32_t *)m, 0u, 0u, 0u}};
+  // Step `step`'s codes (two 1 KiB groups) and meta into slot `slot` of this wave.
+  const auto copy_b = [&](uint32_t step, uint32_t slot) __attribute__((always_inline)) {
+    const uint32_t from = min(step, steps - 1);
+    uint8_t *dst = wave_slot + slot * kSlotBytes;
+    copy_to_lds<16>(bplane + (size_t)(2 * from) * 1024, dst);
+    copy_to_lds<16>(bplane + (size_t)(2 * from + 1) * 1024, dst + 1024);
+    if constexpr (FMT == SQ_FMT_AF4G32) {
+      copy_to_lds<4>(bmeta + (size_t)(2 * from) * 256, dst + 2048);
+      copy_to_lds<4>(bmeta + (size_t)(2 * from + 1) * 256, dst + 2048 + 256);
     } else {
-      const u32x4 v = *(const u32x4 *)m;
-      mw = MetaWords{{v[0], v[1], v[2], v[3]}};
+      copy_to_lds<F::META>(bmeta + (size_t)(2 * from / F::UNIT) * 64 * F::META, dst + 2048);
     }
   };
-  // Chunk mm = 0..3 (inputs 8 mm .. 8 mm + 7 of the wave's group of the step) into weight stage `stage`.
-  const auto write_chunk = [&](uint32_t step, uint32_t stage, int mm) __attribute__((always_inline)) {
-    const Coef k = coef<FMT>(mw, 2 * step + bh);
-    float v0[4], v1[4];
-    word_codes(code[(2 * mm) & 3], mask, mm >> 1, v0);
-    word_codes(code[(2 * mm + 1) & 3], mask, mm >> 1, v1);
-    const u32x4 out = {dequant_pair(v0[0], v0[1], k), dequant_pair(v0[2], v0[3], k), dequant_pair(v1[0], v1[1], k),
-                       dequant_pair(v1[2], v1[3], k)};
-    *(u32x4 *)(lds + stage * kStageBytes + BM * kRowBytes + chunk_at(bcol, 4 * bh + mm)) = out;
-  };
 
-  f32x4 acc[8][4];
+  f32x4 acc[MI][4];
 #pragma unroll
-  for (int mi = 0; mi < 8; ++mi)
+  for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // Prologue: step 0's activations, codes and meta, then step 1's codes and meta; step 0's weights dequantised.
-  copy_a(0, 0);
-  copy_b(0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
-  copy_b(min(1u, steps - 1), 1);
-  read_codes(0);
+  // B fragments: bq[h][t] = group h of the step, column block t. Group 0 serves the first half of a step's MFMAs
+  // while group 1 is dequantised into bq[1], then group 1 serves the second half while the next step's group 0 is
+  // dequantised into bq[0]; each register set has one role, so the step loop needs no unrolling.
+  u32x4 bq[2][4];
+  // The plane words and meta of group h of a step for the lane's four columns 16 t + j, out of the step's slot,
+  // into register set h; and the B fragment of column block t from them, in two parts.
+  uint32_t cw[2][4];
+  MetaWords mw[2][4];
+  const auto read_b = [&](uint32_t slot, int h) __attribute__((always_inline)) {
+    const uint8_t *src = wave_slot + slot * kSlotBytes;
 #pragma unroll
-  for (int mm = 0; mm < 4; ++mm) write_chunk(0, 0, mm);
-  __builtin_amdgcn_s_waitcnt(0);
-  lds_barrier();
-  // Step s: stage s % 2 holds its activations and weights, code stage (s + 1) % 2 step s + 1's codes. The step
-  // copies step s + 1's activations (stage (s + 1) % 2) and step s + 2's codes (code stage s % 2), and between its
-  // MFMAs dequantises step s + 1's weights into stage (s + 1) % 2.
-  constexpr int kCopies = 4 + 1 + 1;   // a step's copy instructions per wave: activations, codes, meta
-  for (uint32_t step = 0; step < steps; ++step) {
-    const uint32_t stage = step & 1, next = min(step + 1, steps - 1), ahead = min(step + 2, steps - 1);
-    copy_a(next, stage ^ 1);
-    copy_b(ahead, stage);
-    // The codes and meta of step s + 1 (copied by this wave one step ago) are in: everything but this step's
-    // copies has completed.
-    __builtin_amdgcn_s_waitcnt(kWaitVm | kCopies);
-    read_codes(stage ^ 1);
-    const uint8_t *sa = lds + stage * kStageBytes, *sb = sa + BM * kRowBytes;
-    // Sixteen groups g = (kk, mi): four MFMAs of A block mi against the four B blocks of input half kk. Each
-    // group's A fragment is read two groups ahead (half 1's B fragments during half 0); after every fourth group,
-    // one of the wave's four 16-byte chunks of the next step's weights.
-    const auto read_a = [&](int g) __attribute__((always_inline)) {
-      return *(const u32x4 *)(sa + chunk_at(wm * 128 + (g & 7) * 16 + j, 4 * (g >> 3) + q));
-    };
-    u32x4 fb[2][4];
-#pragma unroll
-    for (int ni = 0; ni < 4; ++ni) fb[0][ni] = *(const u32x4 *)(sb + chunk_at(wn * 64 + ni * 16 + j, q));
-    u32x4 fa[3];
-    fa[0] = read_a(0);
-    fa[1] = read_a(1);
-#pragma unroll
-    for (int g = 0; g < 16; ++g) {
-      const int kk = g >> 3, mi = g & 7;
-      if (g + 2 < 16) fa[(g + 2) % 3] = read_a(g + 2);
-      if (g < 4) fb[1][g] = *(const u32x4 *)(sb + chunk_at(wn * 64 + g * 16 + j, 4 + q));
-#pragma unroll
-      for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma_f16(fa[g % 3], fb[kk][ni], acc[mi][ni]);
-      if (g % 4 == 3) write_chunk(next, stage ^ 1, g / 4);
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t c = column_of(j, t);
+      cw[h][t] = *(const uint32_t *)(src + h * 1024 + c * 16 + q * 4);
+      mw[h][t] = slot_meta<FMT>(src + 2048, c);
     }
-    // This step's activation copies (issued first) and chunk writes are done; its code and meta copies, read by
-    // this wave only, may still be in flight.
-    __builtin_amdgcn_s_waitcnt(kWaitLgkm | 2);
+  };
+  const auto dequant = [&](uint32_t step, int h, int t, int part) __attribute__((always_inline)) {
+    const Coef k = group_coef<FMT>(mw[h][t], 2 * step + h, h);
+    const uint32_t lo = cw[h][t] & mask, hi = (cw[h][t] >> 4) & mask;
+    const u32x2 v = dequant_part(lo, hi, part, k);
+    bq[h][t][2 * part] = v[0];
+    bq[h][t][2 * part + 1] = v[1];
+  };
+
+  // Prologue: steps 0 and 1's activations, steps 0..2's codes; step 0's group-0 fragments.
+  copy_b(0, 0);
+  copy_b(1, 1);
+  copy_b(2, 2);
+  copy_a(0, 0);
+  copy_a(1, 1);
+  __builtin_amdgcn_s_waitcnt(wait_vm(0));
+  lds_barrier();
+  read_b(0, 0);
+  read_b(0, 1);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    dequant(0, 0, t, 0);
+    dequant(0, 0, t, 1);
+  }
+
+  // Step s copies step s + 2's activations into stage (s + 2) % 3 and step s + 3's codes into slot (s + 3) % 4. It
+  // dequantises its own group 1 during its first half and step s + 1's group 0 during its second half, from words
+  // read half a step earlier (each half reads the words the next half dequantises: step s + 1's slot has been in
+  // LDS since the last barrier). Before the barrier it waits for everything but its own copies, so step s + 1's
+  // activations and step s + 2's codes are in.
+  // The A fragments go through registers in batches of four blocks (16 MFMAs), two batches in flight: with the
+  // copies to LDS outstanding the compiler can only wait for all LDS reads at once, so each batch's reads are issued
+  // a whole batch before their MFMAs.
+  constexpr int kGroups = 2 * MI, kBatch = 4, kBatches = kGroups / kBatch;
+  for (uint32_t step = 0; step < steps; ++step) {
+    const uint32_t stage = step % 3;
+    copy_a(step + 2, (step + 2) % 3);
+    copy_b(step + 3, (step + 3) % kSlots);
+    const uint8_t *sa = lds + stage * kStage;
+    u32x4 fa[2][kBatch];
+    const auto read_batch = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int g = b * kBatch + i;
+        fa[b & 1][i] = *(const u32x4 *)(sa + chunk_at((g % MI) * 16 + j, 4 * (g / MI) + q));
+      }
+    };
+    read_batch(0);
+#pragma unroll
+    for (int b = 0; b < kBatches; ++b) {
+      if (b + 1 < kBatches) read_batch(b + 1);
+      if (b == 0) read_b((step + 1) % kSlots, 0);
+      if (b == kBatches / 2) read_b((step + 1) % kSlots, 1);
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int g = b * kBatch + i, kk = g / MI, mi = g % MI;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[mi][t] = mfma_f16(bq[kk][t], fa[b & 1][i], acc[mi][t]);
+        // Part p % 2 of column block p / 2 of the other group at block p MI / 8 of the half.
+        if (mi % (MI / 8) == 0) {
+          const int p = mi / (MI / 8);
+          dequant(kk == 0 ? step : step + 1, kk ^ 1, p >> 1, p & 1);
+        }
+        // One MFMA, then up to three VALU instructions, four times: the dequantisation issues in the MFMAs' shadow.
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(wait_vm(kCopies));
     lds_barrier();
   }
 
-  // Epilogue: lane (j, q) holds rows 4q + i and column j of each 16 x 16 block.
+  // Epilogue: lane (j, q) holds row 16 mi + j of each row block at columns 8q..8q+7 (blocks 0, 1) and
+  // 32+8q..32+8q+7 (blocks 2, 3) of the plane tile: two 16-byte stores a row block.
+  if (!live) return;
+  const uint32_t col0 = seg.out_offset + ptile * 64 + 8 * q;
 #pragma unroll
-  for (int ni = 0; ni < 4; ++ni) {
-    const uint32_t lc = wn * 64 + ni * 16 + j;   // column within the workgroup's 256
-    uint32_t ct = blockIdx.y * 4 + (lc >> 6), cs = 0;
-    while (cs + 1 < a.segments && ct >= a.seg[cs].tiles) ct -= a.seg[cs++].tiles;
-    if (ct >= a.seg[cs].tiles) continue;
-    const uint32_t col = a.seg[cs].out_offset + ct * 64 + (lc & 63);
+  for (int mi = 0; mi < MI; ++mi) {
+    const uint32_t r = row0 + mi * 16 + j;
+    if (r >= a.rows) continue;
+    const float scale = a.row_scale[r];
 #pragma unroll
-    for (int mi = 0; mi < 8; ++mi)
+    for (int half = 0; half < 2; ++half) {
+      const size_t at = (size_t)r * a.out_stride + col0 + 32 * half;
+      u32x4 aux = {0u, 0u, 0u, 0u};
+      if constexpr (EP != EpNone) aux = *(const u32x4 *)(a.aux + at);
+      u32x4 out;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t r = row0 + wm * 128 + mi * 16 + 4 * q + i;
-        if (r >= a.rows) continue;
-        const size_t at = (size_t)r * a.out_stride + col;
-        a.output[at] = f32_to_bf16(epilogue<EP>(acc[mi][ni][i] * a.row_scale[r], a.aux, at));
+      for (int e = 0; e < 4; ++e) {
+        const f32x4 &v = acc[mi][2 * half + (e >> 1)];
+        const float lo = epilogue_bits<EP>(v[2 * (e & 1)] * scale, aux[e] & 0xFFFFu);
+        const float hi = epilogue_bits<EP>(v[2 * (e & 1) + 1] * scale, aux[e] >> 16);
+        out[e] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
       }
+      *(u32x4 *)(a.output + at) = out;
+    }
   }
 }
 
+template <uint32_t FMT, int BM>
+hipError_t launch_tile(uint32_t epilogue, const PrefillArgs &a, uint32_t tiles, hipStream_t stream) {
+  const dim3 grid((a.rows + BM - 1) / BM, (tiles + 3) / 4), block(kThreads);
+  switch (epilogue) {
+    case EpNone: hipLaunchKernelGGL((prefill_kernel<FMT, EpNone, BM>), grid, block, 0, stream, a); break;
+    case EpResidual: hipLaunchKernelGGL((prefill_kernel<FMT, EpResidual, BM>), grid, block, 0, stream, a); break;
+    default: hipLaunchKernelGGL((prefill_kernel<FMT, EpUpWithGate, BM>), grid, block, 0, stream, a); break;
+  }
+  return hipGetLastError();
+}
+
+// 256-row tiles, unless fewer of them than compute units would leave units idle that 128-row tiles fill.
 template <uint32_t FMT>
 hipError_t launch_format(uint32_t epilogue, const PrefillArgs &a, hipStream_t stream) {
   uint32_t tiles = 0;
   for (uint32_t s = 0; s < a.segments; ++s) tiles += a.seg[s].tiles;
-  const dim3 grid((a.rows + BM - 1) / BM, (tiles + 3) / 4), block(kThreads);
-  switch (epilogue) {
-    case EpNone: hipLaunchKernelGGL((prefill_kernel<FMT, EpNone>), grid, block, 0, stream, a); break;
-    case EpResidual: hipLaunchKernelGGL((prefill_kernel<FMT, EpResidual>), grid, block, 0, stream, a); break;
-    default: hipLaunchKernelGGL((prefill_kernel<FMT, EpUpWithGate>), grid, block, 0, stream, a); break;
-  }
-  return hipGetLastError();
+  const uint32_t large = (a.rows + 255) / 256 * ((tiles + 3) / 4);
+  if (large < a.compute_units) return launch_tile<FMT, 128>(epilogue, a, tiles, stream);
+  return launch_tile<FMT, 256>(epilogue, a, tiles, stream);
 }
 
 }  // namespace

@@ -220,3 +220,16 @@ def test_cxx_face_plans_and_throws(tmp_path):
     out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
     assert "decode rows 8 tile 0" in out and "prefill tile 1" in out
     assert "invalid_argument:" in out
+
+
+def test_prefill_buffers_are_aligned():
+    """The prefill tile moves 16-byte vectors: a buffer off 16-byte alignment is refused on the host."""
+    proj = sq.projection(seg(4096, 4096))
+    plan = sq.plan_for(sq.prefill_workload(4096, 4096, 256), proj)
+    size, _ = sq.scratch_size(plan)
+    scratch = sq.LinearScratch(sq.Buffer(0x10000, size.input), sq.Buffer(0x20000, size.sums), sq.Buffer(None, 0),
+                               sq.Buffer(None, 0), sq.Buffer(None, 0))
+    buffers = sq.LinearBuffers(sq.Buffer(0x40000, 256 * 4096 * 2), sq.Buffer(0x80002, 256 * 4096 * 2),
+                               sq.Buffer(None, 0), sq.Buffer(None, 0), scratch)
+    with pytest.raises(sq.InvalidArgument, match="16-byte aligned"):
+        sq.call("sq_linear_add", None, sq.byref(buffers), sq.byref(proj), sq.byref(plan), None)
