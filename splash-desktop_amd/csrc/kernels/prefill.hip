@@ -118,14 +118,6 @@ __device__ __forceinline__ uint32_t dequant_pair(float q0, float q1, Coef k) {
   asm volatile("" : "+v"(v0), "+v"(v1));
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{v0, v1}, half2));
 }
-// Four of the eight fp16 weights of plane word q of a group, in A-chunk order: the word holds inputs 4q..4q+3 at
-// bits 0, 16, 4, 20 (part 0: fragment words 0, 1) and 16+4q..19+4q at bits 8, 24, 12, 28 (part 1: words 2, 3);
-// lo and hi are the word masked and shifted down a nibble and masked.
-__device__ __forceinline__ u32x2 dequant_part(uint32_t lo, uint32_t hi, int part, Coef k) {
-  return u32x2{dequant_pair(byte_float(lo, part), byte_float(lo, part + 2), k),
-               dequant_pair(byte_float(hi, part), byte_float(hi, part + 2), k)};
-}
-
 // The plane tile column whose weights lane j of the MFMA's A operand carries in column block t. The product runs
 // weights x activations (D = W X^T), so lane (j', q) of D holds column column_of(4q + i, t) for i = 0..3: with
 // this order those are columns 8q + 4(t % 2) + i (blocks 0, 1) and 32 + 8q + 4(t % 2) + i (blocks 2, 3), eight
@@ -153,6 +145,30 @@ __device__ __forceinline__ Coef group_coef(const MetaWords &m, uint32_t group, i
   if constexpr (FMT == SQ_FMT_AF4G32) return coef<FMT>(MetaWords{{m.w[h], 0u, 0u, 0u}}, group);
   else return coef<FMT>(m, group);
 }
+
+// The dequantisation of one group's four plane words as a sequence of micro-operations: kind 0 prepares word arg
+// (masks, coefficients), kinds 1, 2, 3 convert, multiply-add and pack weight pair arg (word arg / 4). Pairs are
+// software pipelined: pair i's conversion comes after pair i - 1's multiply-add and pair i - 2's pack.
+struct Micro {
+  int kind, arg;
+};
+constexpr int kMicro = 4 + 3 * 16;
+struct MicroTable {
+  Micro op[kMicro];
+};
+constexpr MicroTable make_micro_table() {
+  MicroTable t{};
+  int n = 0;
+  for (int i = 0; i < 18; ++i) {
+    if (i < 16 && i % 4 == 0) t.op[n++] = {0, i / 4};
+    if (i < 16) t.op[n++] = {1, i};
+    if (i >= 1 && i <= 16) t.op[n++] = {2, i - 1};
+    if (i >= 2) t.op[n++] = {3, i - 2};
+  }
+  return t;
+}
+constexpr MicroTable kMicroTable = make_micro_table();
+static_assert(kMicroTable.op[kMicro - 1].kind == 3 && kMicroTable.op[kMicro - 1].arg == 15, "52 micro-operations");
 
 template <uint32_t FMT, uint32_t EP, int BM>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_kernel(PrefillArgs a) {
@@ -218,12 +234,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // B fragments: bq[h][t] = group h of the step, column block t. Group 0 serves the first half of a step's MFMAs
-  // while group 1 is dequantised into bq[1], then group 1 serves the second half while the next step's group 0 is
-  // dequantised into bq[0]; each register set has one role, so the step loop needs no unrolling.
-  u32x4 bq[2][4];
-  // The plane words and meta of group h of a step for the lane's four columns 16 t + j, out of the step's slot,
-  // into register set h; and the B fragment of column block t from them, in two parts.
+  // Weight fragments (the MFMA's A operand): wq[h][t] = group h of the step, column block t. Group 0 serves the first
+  // half of a step's MFMAs while group 1 is dequantised into wq[1], then group 1 serves the second half while the
+  // next step's group 0 is dequantised into wq[0]; each register set has one role, so the step loop needs no
+  // unrolling.
+  u32x4 wq[2][4];
+  // The plane words and meta of group h of a step for the lane's four columns, out of the step's slot.
   uint32_t cw[2][4];
   MetaWords mw[2][4];
   const auto read_b = [&](uint32_t slot, int h) __attribute__((always_inline)) {
@@ -235,12 +251,39 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       mw[h][t] = slot_meta<FMT>(src + 2048, c);
     }
   };
-  const auto dequant = [&](uint32_t step, int h, int t, int part) __attribute__((always_inline)) {
-    const Coef k = group_coef<FMT>(mw[h][t], 2 * step + h, h);
-    const uint32_t lo = cw[h][t] & mask, hi = (cw[h][t] >> 4) & mask;
-    const u32x2 v = dequant_part(lo, hi, part, k);
-    bq[h][t][2 * part] = v[0];
-    bq[h][t][2 * part + 1] = v[1];
+  // The dequantisation of one group's four words runs as 52 micro-operations (see micro_op) spread one or two
+  // after each MFMA: prep(t) masks word t and derives its coefficients, then every pair of weights p (word p / 4,
+  // fragment register p % 4) is converted (C), multiplied and added (F) and packed to fp16 (P), software
+  // pipelined so that no micro-operation waits on the one just before it.
+  uint32_t lo[4], hi[4];
+  Coef kw[4];
+  float cf[4][2], vf[4][2];
+  const auto micro = [&](int u, uint32_t step, int h) __attribute__((always_inline)) {
+    const Micro m = kMicroTable.op[u];
+    if (m.kind == 0) {
+      const int t = m.arg;
+      lo[t] = cw[h][t] & mask;
+      hi[t] = (cw[h][t] >> 4) & mask;
+      kw[t] = group_coef<FMT>(mw[h][t], 2 * step + h, h);
+    } else {
+      const int p = m.arg, t = p >> 2, r = p & 3, slot = p & 3;
+      if (m.kind == 1) {
+        const uint32_t src = (r & 1) ? hi[t] : lo[t];
+        cf[slot][0] = byte_float(src, r >> 1);
+        cf[slot][1] = byte_float(src, (r >> 1) + 2);
+      } else if (m.kind == 2) {
+        vf[slot][0] = fmaf(cf[slot][0], kw[t].s, kw[t].z);
+        vf[slot][1] = fmaf(cf[slot][1], kw[t].s, kw[t].z);
+      } else {
+        // fp32 by the fma, then fp16: the empty asm keeps the two roundings apart (no fused mixed-precision fma).
+        asm volatile("" : "+v"(vf[slot][0]), "+v"(vf[slot][1]));
+        wq[h][t][r] = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{vf[slot][0], vf[slot][1]}, half2));
+      }
+    }
+  };
+  const auto dequant_group = [&](uint32_t step, int h) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < kMicro; ++u) micro(u, step, h);
   };
 
   // Prologue: steps 0 and 1's activations, steps 0..2's codes; step 0's group-0 fragments.
@@ -253,21 +296,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   lds_barrier();
   read_b(0, 0);
   read_b(0, 1);
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    dequant(0, 0, t, 0);
-    dequant(0, 0, t, 1);
-  }
+  dequant_group(0, 0);
 
   // Step s copies step s + 2's activations into stage (s + 2) % 3 and step s + 3's codes into slot (s + 3) % 4. It
   // dequantises its own group 1 during its first half and step s + 1's group 0 during its second half, from words
   // read half a step earlier (each half reads the words the next half dequantises: step s + 1's slot has been in
   // LDS since the last barrier). Before the barrier it waits for everything but its own copies, so step s + 1's
   // activations and step s + 2's codes are in.
-  // The A fragments go through registers in batches of four blocks (16 MFMAs), two batches in flight: with the
-  // copies to LDS outstanding the compiler can only wait for all LDS reads at once, so each batch's reads are issued
-  // a whole batch before their MFMAs.
-  constexpr int kGroups = 2 * MI, kBatch = 4, kBatches = kGroups / kBatch;
+  // The activation fragments go through registers in batches of four blocks (16 MFMAs), two batches in flight:
+  // with the copies to LDS outstanding the compiler can only wait for all LDS reads at once, so each batch's reads
+  // are issued a whole batch before their MFMAs.
+  constexpr int kGroups = 2 * MI, kBatch = 4, kBatches = kGroups / kBatch, kSlotsHalf = 4 * MI;
   for (uint32_t step = 0; step < steps; ++step) {
     const uint32_t stage = step % 3;
     copy_a(step + 2, (step + 2) % 3);
@@ -291,19 +330,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       for (int i = 0; i < kBatch; ++i) {
         const int g = b * kBatch + i, kk = g / MI, mi = g % MI;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[mi][t] = mfma_f16(bq[kk][t], fa[b & 1][i], acc[mi][t]);
-        // Part p % 2 of column block p / 2 of the other group at block p MI / 8 of the half.
-        if (mi % (MI / 8) == 0) {
-          const int p = mi / (MI / 8);
-          dequant(kk == 0 ? step : step + 1, kk ^ 1, p >> 1, p & 1);
-        }
-        // One MFMA, then up to three VALU instructions, four times: the dequantisation issues in the MFMAs' shadow.
-#pragma unroll
         for (int t = 0; t < 4; ++t) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+          acc[mi][t] = mfma_f16(wq[kk][t], fa[b & 1][i], acc[mi][t]);
+          // This MFMA's share of the other group's micro-operations: slot s of the half runs micro-operations
+          // [s kMicro / S, (s + 1) kMicro / S).
+          const int slot = mi * 4 + t, u0 = slot * kMicro / kSlotsHalf, u1 = (slot + 1) * kMicro / kSlotsHalf;
+          static_assert(kMicro <= 2 * kSlotsHalf, "at most two micro-operations a slot");
+          if (u0 < u1) micro(u0, kk == 0 ? step : step + 1, kk ^ 1);
+          if (u0 + 1 < u1) micro(u0 + 1, kk == 0 ? step : step + 1, kk ^ 1);
+          __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
     __builtin_amdgcn_s_waitcnt(wait_vm(kCopies));
