@@ -3,63 +3,40 @@
 // kernels/shared/gguf_linear.metal:71-192, and the exact-operand register tile of
 // kernels/decode/linear_gguf_sgmatrix.metal), and the decode tiles' layout and dispatch.
 //
-// CDNA4 mapping. The tile streams a 64-column plane tile exactly as the column tile does (decode_column.hip): per
-// group of 32 inputs one 16-byte load per lane (lane l: column l's 32 codes), 1 KiB per wave, P groups in flight,
-// every load unconditional. The rows go on the 16-row side of the 16x16x32 bf16 MFMA:
-//  - a 4x4 transpose of the four code dwords across the wave's four 16-lane rows (v_permlane32_swap, then
-//    v_permlane16_swap) gives lane (j, q) word q of column 16t + j in register t, the MFMA's B layout for column
-//    block t; each word becomes eight exact bf16 operands 128 + q (code_pairs);
-//  - per group and 16-row block, four MFMAs (one per 16-column block) plus one against bf16 ones, which leaves
-//    each lane its own rows' input sums: no cross-lane reduction;
-//  - each scale group closes in fp32: acc += s * sum x (128 + q) + (z - 128 s) * sum x, every product exact;
-//  - a workgroup of W waves takes the tile and W K slices; the slices meet in LDS in slice order, every wave
-//    adding a share of the accumulators, and K partitions across workgroups reduce through split_reduce.
-// A row's result depends only on its own activations and the layout, never on the other rows.
+// CDNA4 mapping. A workgroup of W waves takes a 64-column plane tile and W K slices; each wave streams its slice
+// with the row tile's inner loop (rowtile.hpp: exact bf16 operands on the 16x16x32 MFMA, rows on its 16-row side,
+// per-group closes in fp32); the slices meet in LDS in slice order, every wave adding a share of the accumulators,
+// and K partitions across workgroups reduce through split_reduce. A row's result depends only on its own
+// activations and the layout, never on the other rows.
 #include "device.hpp"
 #include "kernels.hpp"
+#include "rowtile.hpp"
 #include "split.hpp"
 
 namespace sq::kern {
 namespace {
 
-constexpr int kPipe = 4;   // groups in flight per wave
-
 // The most waves a row-tile workgroup holds, so that a wave's registers fit without spilling: 16 (128 registers) for
 // one tensor of 16 rows, 4 (512) for a gate/up pair of 32 rows, else 8 (256).
 constexpr uint32_t row_max_waves(int mb, int nt) { return mb == 1 && nt == 1 ? 16 : mb == 2 && nt == 2 ? 4 : 8; }
 
-// Lane (j, q) register t <- lane (j + 16 t) register q: the 4x4 transpose of words across the 16-lane rows.
-__device__ __forceinline__ void transpose4(uint32_t (&r)[4]) {
-  const auto a = __builtin_amdgcn_permlane32_swap(r[0], r[2], false, false);
-  const auto b = __builtin_amdgcn_permlane32_swap(r[1], r[3], false, false);
-  const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
-  const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
-  r[0] = c[0];
-  r[1] = c[1];
-  r[2] = d[0];
-  r[3] = d[1];
-}
-
 template <uint32_t FMT, int MB, int GW, int NT, uint32_t EP, bool F32OUT>
 __global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeArgs a) {
   using F = Fmt<FMT>;
-  constexpr int SG = F::SG, UNIT = F::UNIT, P = GW < kPipe ? GW : kPipe;
   constexpr int A = NT * 4 * MB * 4;   // accumulators per lane: tensor n, column block t, row block b, row i
-  static_assert(GW % UNIT == 0 && GW % SG == 0, "a slice holds whole meta units");
   const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
   const uint32_t slice = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), waves = blockDim.x >> 6;
   const uint32_t split = blockIdx.y;
   uint32_t tile = blockIdx.x, s = 0;
   while (s + 1 < a.segments && tile >= a.seg[s].tiles) tile -= a.seg[s++].tiles;
   const Segment seg = a.seg[s];
-  const uint32_t G = a.K >> 5, units = G / UNIT, gs = G / a.splits;
+  const uint32_t G = a.K >> 5, units = G / F::UNIT, gs = G / a.splits;
   const uint32_t gb = split * gs + slice * GW, live = min((uint32_t)GW, gs - min(gs, slice * GW));
-  const uint32_t last = live ? live - 1 : 0;
 
   const uint8_t *plane[NT], *meta[NT];
   {
     const size_t pbase = ((size_t)tile * G * 64 + lane) * 16 + (size_t)gb * 1024;
-    const size_t mbase = ((size_t)tile * units * 64 + j) * F::META + (size_t)(gb / UNIT) * 64 * F::META;
+    const size_t mbase = ((size_t)tile * units * 64 + j) * F::META + (size_t)(gb / F::UNIT) * 64 * F::META;
     plane[0] = (NT == 2 ? a.gate.plane0 : seg.plane0) + pbase;
     meta[0] = (NT == 2 ? a.gate.meta : seg.meta) + mbase;
     if constexpr (NT == 2) {
@@ -75,94 +52,14 @@ __global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeA
     const uint32_t r = 16u * b + j;
     xrow[b] = a.input + (size_t)(r < a.rows ? r : 0) * a.K + 4 * q + (size_t)gb * 32;
   }
-  const CodeConstants cc = make_code_constants();
-
   float acc[NT][4][MB][4];
-#pragma unroll
-  for (int n = 0; n < NT; ++n)
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int b = 0; b < MB; ++b)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[n][t][b][i] = 0.0f;
+  clear(acc);
+  row_slice<FMT, MB, GW, NT>(plane, meta, xrow, live, acc);
 
-  u32x4 xv[MB][GW];
-  u32x4 codes[NT][GW];
-  MetaWords mw[NT][4][GW / UNIT];
-  const auto issue = [&](int u) __attribute__((always_inline)) {
-    const uint32_t g = min((uint32_t)u, last);
-#pragma unroll
-    for (int b = 0; b < MB; ++b) {
-      const u32x2 lo = *(const u32x2 *)(xrow[b] + (size_t)g * 32), hi = *(const u32x2 *)(xrow[b] + (size_t)g * 32 + 16);
-      xv[b][u] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-    }
-    if (u % UNIT == 0) {
-      const uint32_t v = min((uint32_t)(u / UNIT), last / UNIT);
-#pragma unroll
-      for (int n = 0; n < NT; ++n)
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          mw[n][t][u / UNIT] = load_meta<FMT>(meta[n] + ((size_t)v * 64 + 16 * t) * F::META);
-    }
-#pragma unroll
-    for (int n = 0; n < NT; ++n) codes[n][u] = __builtin_nontemporal_load((const u32x4 *)(plane[n] + (size_t)g * 1024));
-  };
-#pragma unroll
-  for (int u = 0; u < P; ++u) issue(u);
-
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4 C[NT][4][MB], S[MB];
-#pragma unroll
-  for (int u = 0; u < GW; ++u) {
-    if (u + P < GW) issue(u + P);
-    __builtin_amdgcn_sched_barrier(0);
-    if ((uint32_t)u < live) {
-      const bool first = u % SG == 0;
-#pragma unroll
-      for (int b = 0; b < MB; ++b) S[b] = mfma_bf16(xv[b][u], ones_operand(), first ? zero : S[b]);
-#pragma unroll
-      for (int n = 0; n < NT; ++n) {
-        uint32_t r[4] = {codes[n][u][0], codes[n][u][1], codes[n][u][2], codes[n][u][3]};
-        transpose4(r);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const u32x4 w = code_pairs(r[t], cc);
-#pragma unroll
-          for (int b = 0; b < MB; ++b) C[n][t][b] = mfma_bf16(xv[b][u], w, first ? zero : C[n][t][b]);
-        }
-      }
-      if ((u + 1) % SG == 0) {
-#pragma unroll
-        for (int n = 0; n < NT; ++n)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const Coef k = coef<FMT>(mw[n][t][u / UNIT], u);
-            const float zc = fmaf(-128.0f, k.s, k.z);
-#pragma unroll
-            for (int b = 0; b < MB; ++b)
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                acc[n][t][b][i] = fmaf(k.s, C[n][t][b][i], acc[n][t][b][i]);
-                acc[n][t][b][i] = fmaf(zc, S[b][i], acc[n][t][b][i]);
-              }
-          }
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
-  // Slices meet in LDS; accumulator (t, b, i) of both tensors is added, in slice order, by wave (t, b, i) % waves.
   __shared__ float red[row_max_waves(MB, NT) * A * 64];
-#pragma unroll
-  for (int n = 0; n < NT; ++n)
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int b = 0; b < MB; ++b)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) red[((slice * A) + ((n * 4 + t) * MB + b) * 4 + i) * 64 + lane] = acc[n][t][b][i];
-  __syncthreads();
+  float sum[A];
+  bool owned[A];
+  row_reduce<MB, NT>(acc, red, slice, waves, lane, sum, owned);
   const uint32_t cstride = NT == 2 ? 2 * a.out_stride : a.out_stride;
   float total[A][1];
   bool rlive[A][1];
@@ -176,13 +73,9 @@ __global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeA
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int e = ((n * 4 + t) * MB + b) * 4 + i;
-          const uint32_t own = (uint32_t)((t * MB + b) * 4 + i) % waves;
           const uint32_t row = 16u * b + 4u * q + i;
-          float v = 0.0f;
-          if (own == slice)
-            for (uint32_t w = 0; w < waves; ++w) v += red[(w * A + e) * 64 + lane];
-          total[e][0] = v;
-          rlive[e][0] = own == slice && row < a.rows;
+          total[e][0] = sum[e];
+          rlive[e][0] = owned[e] && row < a.rows;
           index[e][0] = (size_t)row * cstride + n * a.out_stride + seg.out_offset + tile * 64 + 16 * t + j;
         }
   if (a.splits > 1 && !split_reduce<A, 1>(total, rlive, index, a.partials, (size_t)a.rows * cstride, split, a.splits,

@@ -2,13 +2,11 @@
 // one pass, then down) and the combine (reference: kernels/shared/moe.metal:23-162,175-331,480-505 and
 // kernels/shared/moe_gguf.metal:21-206).
 //
-// CDNA4 mapping. The expert passes run the decode tile's wave walk (walk.hpp) per expert: workgroup (64-column
-// tile, expert tile) runs only on its expert's first tile and walks every grouped row of that expert 32 rows at a
-// time, so each column tile of an expert's weights streams from HBM once per step however its rows fall into tiles.
-// The gate/up pass reads its activation rows straight through the grouped routes (the reference's separate gather
-// copy is folded into the A-operand loads).
+// CDNA4 mapping. Each expert pass is the decode row tile's exact-operand inner loop (rowtile.hpp) per expert tile:
+// a wave streams one 64-column plane tile of its expert over all of K against the tile's (at most 32) grouped
+// rows; an expert's other tiles read the same weights while they are still in L2.
 #include "kernels.hpp"
-#include "walk.hpp"
+#include "rowtile.hpp"
 
 namespace sq::kern {
 namespace {
@@ -111,67 +109,69 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
     *tile_count = SqMoeTileCount{total, {p.gate_up_columns, total, 1}, {p.down_columns, total, 1}, {0, 0, 0}};
 }
 
-template <uint32_t FMT, int NT>
-__global__ __launch_bounds__(256) void expert_kernel(MoeExpertArgs a) {
+// Workgroup (four 64-column tiles, expert tile): wave w streams column tile 4 blockIdx.x + w of the tile's expert
+// over all of K against the tile's rows (at most 32: the expert's grouped rows from tile * tile_rows), so each
+// wave owns its outputs and no wave waits on another. The gate/up pass reads its rows through the grouped routes
+// (row r of the tile is input row routes[r] / top_k: the reference's gather copy folds into these loads) and
+// writes bf16(bf16(up) silu(bf16(gate))); the down pass reads the grouped intermediate rows
+// (moe_gguf.metal:121-206, moe_expert_slab.h:13-99).
+template <uint32_t FMT, int MB, int NT>
+__device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDescriptor d, uint32_t tile,
+                                            uint32_t ct) {
   using F = Fmt<FMT>;
-  const uint32_t t = blockIdx.y, ntiles = a.tile_count->tiles;
-  if (t >= ntiles) return;
-  const SqMoeTileDescriptor d = a.tiles[t];
-  if (t > 0 && a.tiles[t - 1].expert == d.expert) return;
-  uint32_t last = t;
-  while (last + 1 < ntiles && a.tiles[last + 1].expert == d.expert) ++last;
-  const uint32_t count = (last - t) * a.tile_rows + a.tiles[last].rows, first_row = t * a.tile_rows;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane & 15, q = lane >> 4;
-  const uint32_t G = a.K >> 5, units = G / F::UNIT, groups = G / F::SG;
-  const uint32_t ptile = a.slots[d.expert] * (a.output_size / 64) + blockIdx.x;
+  const uint32_t column_tiles = a.output_size / 64;
+  const uint32_t rows = d.rows, first_row = tile * a.tile_rows;
+  const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
+  const uint32_t G = a.K >> 5, units = G / F::UNIT;
+  const uint32_t ptile = a.slots[d.expert] * column_tiles + ct;
   const uint8_t *plane[NT], *meta[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
-    plane[n] = a.plane0[n] + (size_t)ptile * G * 1024 + (size_t)j * 16 + (size_t)q * 4;
+    plane[n] = a.plane0[n] + ((size_t)ptile * G * 64 + lane) * 16;
     meta[n] = a.meta[n] + ((size_t)ptile * units * 64 + j) * F::META;
   }
-  const uint32_t g0 = (uint32_t)wave * groups / 4, g1 = (uint32_t)(wave + 1) * groups / 4;
-  const uint32_t col = blockIdx.x * 64 + 16 * wave + j;
-  __shared__ float red[4 * NT * 4 * 2 * 4 * 64];
-  for (uint32_t base = 0; base < count; base += 32) {
-    RowPtrs x;
+  // Lane (j, q) of row block b reads row 16 b + j (row 0 past the tile's rows: nothing stores those results).
+  const uint16_t *xrow[MB];
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const uint32_t r = base + 16u * b + j;
-      if (r < count) {
-        const uint32_t grouped = first_row + r;
-        const uint32_t source = NT == 2 ? a.routes[grouped] / a.top_k : grouped;
-        x.row[b] = a.input + (size_t)source * a.K;
-      } else {
-        x.row[b] = nullptr;
-      }
-    }
-    f32x4 acc[NT][4][2];
+  for (int b = 0; b < MB; ++b) {
+    const uint32_t r = 16u * b + j < rows ? 16u * b + j : 0u;
+    const uint32_t source = NT == 2 ? a.routes[first_row + r] / a.top_k : first_row + r;
+    xrow[b] = a.input + (size_t)source * a.K + 4 * q;
+  }
+  float acc[NT][4][MB][4];
+  clear(acc);
+  // A gate/up pair runs one wave a SIMD anyway: it takes a third register set to look further ahead (Q4_K's
+  // headers leave no room for it).
+  constexpr int kSets = NT == 2 && FMT != SQ_FMT_Q4K ? 3 : 2;
+  row_stream<FMT, MB, NT, kSets>(plane, meta, xrow, G, acc);
 #pragma unroll
-    for (int n = 0; n < NT; ++n)
+  for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-        for (int b = 0; b < 2; ++b) acc[n][tt][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-    walk<FMT, 2, 4, NT>(plane, meta, x, g0, g1, q, acc);
-    float total[NT][2][4];
-    reduce_waves<2, 4, NT>(acc, red, wave, lane, total);
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < MB; ++b)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t r = base + 16u * b + 4u * q + i;
-        if (r >= count) continue;
-        const size_t at = (size_t)(first_row + r) * a.output_size + col;
+        const uint32_t r = 16u * b + 4u * q + i;
+        if (r >= rows) continue;
+        const size_t at = (size_t)(first_row + r) * a.output_size + ct * 64 + 16 * t + j;
         if constexpr (NT == 2) {
-          const float g = bf16_to_f32(f32_to_bf16(total[0][b][i])), u = bf16_to_f32(f32_to_bf16(total[1][b][i]));
+          const float g = bf16_to_f32(f32_to_bf16(acc[0][t][b][i])), u = bf16_to_f32(f32_to_bf16(acc[1][t][b][i]));
           a.output[at] = f32_to_bf16(u * silu(g));
         } else {
-          a.output[at] = f32_to_bf16(total[0][b][i]);
+          a.output[at] = f32_to_bf16(acc[0][t][b][i]);
         }
       }
-    __syncthreads();   // the LDS of the reduction is rewritten by the next rows
-  }
+}
+
+// Tiles of at most 16 rows (most of an expert's last tiles) take the one-block path.
+template <uint32_t FMT, int MB, int NT>
+__global__ __launch_bounds__(256) void expert_kernel(MoeExpertArgs a) {
+  const uint32_t tile = blockIdx.y;
+  if (tile >= a.tile_count->tiles) return;
+  const uint32_t ct = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (ct >= a.output_size / 64) return;
+  const SqMoeTileDescriptor d = a.tiles[tile];
+  if (MB == 1 || d.rows <= 16) expert_tile<FMT, 1, NT>(a, d, tile, ct);
+  else expert_tile<FMT, MB, NT>(a, d, tile, ct);
 }
 
 // out[r][d] = bf16(residual + sum_slot w_slot * expert_out[route_rows[slot]][d]) in slot order (moe.metal:480-505).
@@ -191,12 +191,18 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *expert_out
   output[at] = f32_to_bf16(v);
 }
 
+template <uint32_t FMT, int MB, int NT>
+hipError_t launch_expert_rows(const MoeExpertArgs &a, hipStream_t stream) {
+  const dim3 grid((a.output_size / 64 + 3) / 4, a.max_tiles), block(256);
+  hipLaunchKernelGGL((expert_kernel<FMT, MB, NT>), grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
 template <uint32_t FMT>
 hipError_t launch_expert_format(const MoeExpertArgs &a, hipStream_t stream) {
-  const dim3 grid(a.output_size / 64, a.max_tiles), block(256);
-  if (a.gate_up) hipLaunchKernelGGL((expert_kernel<FMT, 2>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((expert_kernel<FMT, 1>), grid, block, 0, stream, a);
-  return hipGetLastError();
+  if (a.tile_rows <= 16)
+    return a.gate_up ? launch_expert_rows<FMT, 1, 2>(a, stream) : launch_expert_rows<FMT, 1, 1>(a, stream);
+  return a.gate_up ? launch_expert_rows<FMT, 2, 2>(a, stream) : launch_expert_rows<FMT, 2, 1>(a, stream);
 }
 
 }  // namespace
