@@ -56,6 +56,10 @@ void validate(const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
   requireBytes(sc.routeRows, need.routeRows, "MoE route rows");
   requireBytes(sc.expertIntermediate, need.expertIntermediate, "MoE expert intermediate");
   requireBytes(sc.expertOutput, need.expertOutput, "MoE expert output");
+  // The combine moves eight bf16 a lane.
+  const auto aligned = [](const Buffer &buffer) { return (reinterpret_cast<uintptr_t>(buffer.ptr) & 15u) == 0; };
+  if (!aligned(b.residual) || !aligned(b.output) || !aligned(sc.expertOutput))
+    throw std::invalid_argument("MoE output, residual and expert output buffers are 16-byte aligned");
 }
 
 }  // namespace

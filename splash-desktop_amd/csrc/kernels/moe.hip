@@ -63,7 +63,7 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
   constexpr uint32_t kChunk = 512, kWords = kChunk / 32;
   __shared__ uint32_t counts[SQ_MOE_WIDE_EXPERT_SLOTS], offsets[SQ_MOE_WIDE_EXPERT_SLOTS],
       running[SQ_MOE_WIDE_EXPERT_SLOTS];
-  __shared__ uint32_t bits[SQ_MOE_WIDE_EXPERT_SLOTS * kWords];
+  __shared__ uint32_t bits[SQ_MOE_WIDE_EXPERT_SLOTS * kWords], prefix[SQ_MOE_WIDE_EXPERT_SLOTS * kWords];
   __shared__ uint32_t total;
   const uint32_t tid = threadIdx.x, routes = p.rows * p.top_k, tr = p.tile_rows;
   counts[tid] = 0;
@@ -71,10 +71,22 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
   __syncthreads();
   for (uint32_t r = tid; r < routes; r += 512) atomicAdd(&counts[selected[r]], 1u);
   __syncthreads();
-  if (tid == 0) {
-    uint32_t sum = 0;
-    for (uint32_t e = 0; e < p.experts; ++e) offsets[e] = sum, sum += (counts[e] + tr - 1) / tr;
-    total = sum;
+  {
+    // Exclusive prefix of the experts' tile counts: a scan within each wave, then over the eight wave totals.
+    __shared__ uint32_t wave_sum[8];
+    const uint32_t mine = tid < p.experts ? (counts[tid] + tr - 1) / tr : 0u, lane = tid & 63, wave = tid >> 6;
+    uint32_t inclusive = mine;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t up = (uint32_t)__shfl_up((int)inclusive, d);
+      if (lane >= (uint32_t)d) inclusive += up;
+    }
+    if (lane == 63) wave_sum[wave] = inclusive;
+    __syncthreads();
+    uint32_t before = 0;
+    for (uint32_t w = 0; w < wave; ++w) before += wave_sum[w];
+    offsets[tid] = before + inclusive - mine;
+    if (tid == 511) total = before + inclusive;
   }
   __syncthreads();
   if (tid < p.experts) {
@@ -91,10 +103,19 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
       atomicOr(&bits[selected[r] * kWords + local / 32], 1u << (local % 32));
     }
     __syncthreads();
+    // Rows of the chunk before word w that route to expert e: one pass per expert, then each route's rank is a
+    // table read and one population count.
+    if (tid < p.experts) {
+      uint32_t before = 0;
+      for (uint32_t w = 0; w < kWords; ++w) {
+        prefix[tid * kWords + w] = before;
+        before += __popc(bits[tid * kWords + w]);
+      }
+    }
+    __syncthreads();
     for (uint32_t r = r0 + tid; r < r1; r += 512) {
       const uint32_t e = selected[r], local = r / p.top_k - chunk;
-      uint32_t rank = running[e];
-      for (uint32_t w = 0; w < local / 32; ++w) rank += __popc(bits[e * kWords + w]);
+      uint32_t rank = running[e] + prefix[e * kWords + local / 32];
       rank += __popc(bits[e * kWords + local / 32] & ((1u << (local % 32)) - 1u));
       const uint32_t row = offsets[e] * tr + rank;
       grouped_routes[row] = r;
@@ -178,17 +199,30 @@ __global__ __launch_bounds__(256) void expert_kernel(MoeExpertArgs a) {
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *expert_output, const uint32_t *route_rows,
                                                       const float *weights, const uint16_t *residual,
                                                       uint16_t *output, SqMoeCombineParams p) {
-  const uint32_t r = blockIdx.x, d = blockIdx.y * 256 + threadIdx.x;
+  // Thread: eight consecutive outputs of row blockIdx.x (the hidden size is a multiple of 64).
+  const uint32_t r = blockIdx.x, d = (blockIdx.y * 256 + threadIdx.x) * 8;
   if (d >= p.hidden_size) return;
   const size_t at = (size_t)r * p.hidden_size + d;
-  float v = residual ? bf16_to_f32(residual[at]) : 0.0f;
+  float v[8];
+  const u32x4 res = residual ? *(const u32x4 *)(residual + at) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[2 * e] = bf16_to_f32(res[e] & 0xFFFFu), v[2 * e + 1] = bf16_to_f32(res[e] >> 16);
   const size_t route = (size_t)r * p.routes_per_row;
   for (uint32_t slot = 0; slot < p.routes_per_row; ++slot) {
     const uint32_t grouped = route_rows[route + slot];
     if (grouped == ~0u) continue;
-    v = fmaf(weights[route + slot], bf16_to_f32(expert_output[(size_t)grouped * p.hidden_size + d]), v);
+    const float w = weights[route + slot];
+    const u32x4 x = *(const u32x4 *)(expert_output + (size_t)grouped * p.hidden_size + d);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = fmaf(w, bf16_to_f32(x[e] & 0xFFFFu), v[2 * e]);
+      v[2 * e + 1] = fmaf(w, bf16_to_f32(x[e] >> 16), v[2 * e + 1]);
+    }
   }
-  output[at] = f32_to_bf16(v);
+  u32x4 out;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) out[e] = (uint32_t)f32_to_bf16(v[2 * e]) | ((uint32_t)f32_to_bf16(v[2 * e + 1]) << 16);
+  *(u32x4 *)(output + at) = out;
 }
 
 template <uint32_t FMT, int MB, int NT>
@@ -235,7 +269,7 @@ hipError_t launch_moe_expert(const MoeExpertArgs &a, hipStream_t stream) {
 hipError_t launch_moe_combine(const uint16_t *expert_output, const uint32_t *route_rows, const float *weights,
                               const uint16_t *residual, uint16_t *output, const SqMoeCombineParams &p,
                               hipStream_t stream) {
-  hipLaunchKernelGGL(combine_kernel, dim3(p.rows, (p.hidden_size + 255) / 256), dim3(256), 0, stream, expert_output,
+  hipLaunchKernelGGL(combine_kernel, dim3(p.rows, (p.hidden_size / 8 + 255) / 256), dim3(256), 0, stream, expert_output,
                      route_rows, weights, residual, output, p);
   return hipGetLastError();
 }
