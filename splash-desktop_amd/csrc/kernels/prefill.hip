@@ -64,18 +64,39 @@ __device__ __forceinline__ uint32_t chunk_at(uint32_t r, uint32_t c) { return r 
 
 // ---------------------------------------------------------------- prepare
 
-// One workgroup per row: the largest magnitude of the row's bf16 inputs (16-byte vectors, a wave reduction and
-// LDS), then the fp16 row scaled by 2^-e where 2^e brings the largest below 2^16, each group of 32 stored with its
-// 16-byte chunk q holding inputs 4q..4q+3 and 16+4q..19+4q.
+// One workgroup per row: the largest magnitude of the row's bf16 inputs (a wave reduction and LDS), then the fp16 row
+// scaled by 2^-e where 2^e brings the largest below 2^16, each group of 32 stored with its 16-byte chunk q holding
+// inputs 4q..4q+3 and 16+4q..19+4q. Rows of at most 256 NV output chunks are read once, into registers (NV > 0);
+// longer ones are read twice.
+template <int NV>
 __global__ __launch_bounds__(256) void prepare_kernel(const uint16_t *input, uint32_t K, uint16_t *half_input,
                                                       float *row_scale) {
   const uint32_t r = blockIdx.x, vectors = K / 8;
-  const u32x4 *x = (const u32x4 *)(input + (size_t)r * K);
-  uint32_t largest = 0;   // magnitude bits of the largest |x| (bf16 bit patterns order like the magnitudes)
-  for (uint32_t v = threadIdx.x; v < vectors; v += 256) {
-    const u32x4 w = x[v];
+  const u32x2 *units = (const u32x2 *)(input + (size_t)r * K);   // 4-input units
+  u32x4 *h = (u32x4 *)(half_input + (size_t)r * K);
+  // Output chunk v = 4 g + c (group g) takes units 8 g + c and 8 g + c + 4.
+  const auto chunk = [&](uint32_t v) __attribute__((always_inline)) {
+    const uint32_t g = v >> 2, c = v & 3;
+    const u32x2 lo = units[8 * g + c], hi = units[8 * g + c + 4];
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  };
+  const auto magnitude = [](u32x4 w) __attribute__((always_inline)) {
+    uint32_t m = 0;   // bf16 bit patterns order like their magnitudes
 #pragma unroll
-    for (int e = 0; e < 4; ++e) largest = max(largest, max(w[e] & 0x7FFFu, (w[e] >> 16) & 0x7FFFu));
+    for (int e = 0; e < 4; ++e) m = max(m, max(w[e] & 0x7FFFu, (w[e] >> 16) & 0x7FFFu));
+    return m;
+  };
+  uint32_t largest = 0;
+  u32x4 held[NV > 0 ? NV : 1];
+  if constexpr (NV > 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t v = threadIdx.x + 256u * i;
+      held[i] = v < vectors ? chunk(v) : u32x4{0u, 0u, 0u, 0u};
+      largest = max(largest, magnitude(held[i]));
+    }
+  } else {
+    for (uint32_t v = threadIdx.x; v < vectors; v += 256) largest = max(largest, magnitude(chunk(v)));
   }
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) largest = max(largest, (uint32_t)__shfl_xor((int)largest, d));
@@ -88,18 +109,22 @@ __global__ __launch_bounds__(256) void prepare_kernel(const uint16_t *input, uin
   const int shift = exponent >= 16 ? exponent - 15 : 0;
   const float down = ldexpf(1.0f, -shift);
   if (threadIdx.x == 0) row_scale[r] = ldexpf(1.0f, shift);
-  const u32x2 *units = (const u32x2 *)(input + (size_t)r * K);   // 4-input units
-  u32x4 *h = (u32x4 *)(half_input + (size_t)r * K);
-  for (uint32_t v = threadIdx.x; v < vectors; v += 256) {
-    const uint32_t g = v >> 2, c = v & 3;   // output chunk c of group g: units 8 g + c and 8 g + c + 4
-    const u32x2 lo = units[8 * g + c], hi = units[8 * g + c + 4];
-    const uint32_t w[4] = {lo[0], lo[1], hi[0], hi[1]};
+  const auto convert = [&](u32x4 w) __attribute__((always_inline)) {
     u32x4 o;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       o[e] = (uint32_t)f32_to_f16(bf16_to_f32(w[e] & 0xFFFFu) * down) |
              ((uint32_t)f32_to_f16(bf16_to_f32(w[e] >> 16) * down) << 16);
-    h[v] = o;
+    return o;
+  };
+  if constexpr (NV > 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t v = threadIdx.x + 256u * i;
+      if (v < vectors) h[v] = convert(held[i]);
+    }
+  } else {
+    for (uint32_t v = threadIdx.x; v < vectors; v += 256) h[v] = convert(chunk(v));
   }
 }
 
@@ -398,7 +423,13 @@ hipError_t launch_format(uint32_t epilogue, const PrefillArgs &a, hipStream_t st
 
 hipError_t launch_prefill_prepare(const uint16_t *input, uint32_t rows, uint32_t K, uint16_t *half_input,
                                   float *row_scale, hipStream_t stream) {
-  hipLaunchKernelGGL(prepare_kernel, dim3(rows), dim3(256), 0, stream, input, K, half_input, row_scale);
+  const uint32_t chunks = K / 8;
+  const dim3 grid(rows), block(256);
+  if (chunks <= 256) hipLaunchKernelGGL(prepare_kernel<1>, grid, block, 0, stream, input, K, half_input, row_scale);
+  else if (chunks <= 512) hipLaunchKernelGGL(prepare_kernel<2>, grid, block, 0, stream, input, K, half_input, row_scale);
+  else if (chunks <= 1024) hipLaunchKernelGGL(prepare_kernel<4>, grid, block, 0, stream, input, K, half_input, row_scale);
+  else if (chunks <= 2048) hipLaunchKernelGGL(prepare_kernel<8>, grid, block, 0, stream, input, K, half_input, row_scale);
+  else hipLaunchKernelGGL(prepare_kernel<0>, grid, block, 0, stream, input, K, half_input, row_scale);
   return hipGetLastError();
 }
 
