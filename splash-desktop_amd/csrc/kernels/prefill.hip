@@ -151,13 +151,14 @@ __device__ __forceinline__ uint32_t column_of(uint32_t j, int t) {
   return (t >> 1) * 32 + 8 * (j >> 2) + 4 * (t & 1) + (j & 3);
 }
 
-// The meta of column c for one step out of the wave's LDS slot: af4g32 the words of its two groups, af4g64 and
-// af4g128 the one word covering the step, Q4_K the 16-byte header of its 256-input unit.
+// The meta of column c for group h of one step out of the wave's LDS slot: af4g32 the words of its two groups,
+// af4g64 and af4g128 the one word covering the step, Q4_K the fp32 (s, z) of group h that q4k_coefficients left
+// in place of the column's header.
 template <uint32_t FMT>
-__device__ __forceinline__ MetaWords slot_meta(const uint8_t *meta, uint32_t c) {
+__device__ __forceinline__ MetaWords slot_meta(const uint8_t *meta, uint32_t c, int h) {
   if constexpr (FMT == SQ_FMT_Q4K) {
-    const u32x4 v = *(const u32x4 *)(meta + c * 16);
-    return MetaWords{{v[0], v[1], v[2], v[3]}};
+    const u32x2 v = *(const u32x2 *)(meta + c * 16 + h * 8);
+    return MetaWords{{v[0], v[1], 0u, 0u}};
   } else if constexpr (FMT == SQ_FMT_AF4G32) {
     return MetaWords{{*(const uint32_t *)(meta + c * 4), *(const uint32_t *)(meta + 256 + c * 4), 0u, 0u}};
   } else {
@@ -167,8 +168,20 @@ __device__ __forceinline__ MetaWords slot_meta(const uint8_t *meta, uint32_t c) 
 // The coefficients of group h (0, 1) of the step, the step's group `group` of the tile.
 template <uint32_t FMT>
 __device__ __forceinline__ Coef group_coef(const MetaWords &m, uint32_t group, int h) {
-  if constexpr (FMT == SQ_FMT_AF4G32) return coef<FMT>(MetaWords{{m.w[h], 0u, 0u, 0u}}, group);
+  if constexpr (FMT == SQ_FMT_Q4K) return Coef{__uint_as_float(m.w[0]), __uint_as_float(m.w[1])};
+  else if constexpr (FMT == SQ_FMT_AF4G32) return coef<FMT>(MetaWords{{m.w[h], 0u, 0u, 0u}}, group);
   else return coef<FMT>(m, group);
+}
+// Q4_K: lane l turns column l's 16-byte header in the slot into the fp32 (s, z) of the step's two groups, in place,
+// so each lane derives one column's coefficients instead of four (the wave's reads precede its writes).
+template <uint32_t FMT>
+__device__ __forceinline__ void q4k_coefficients(uint8_t *meta, uint32_t step, int lane) {
+  if constexpr (FMT == SQ_FMT_Q4K) {
+    const u32x4 v = *(const u32x4 *)(meta + lane * 16);
+    const MetaWords m{{v[0], v[1], v[2], v[3]}};
+    const Coef c0 = coef<FMT>(m, 2 * step), c1 = coef<FMT>(m, 2 * step + 1);
+    *(f32x4 *)(meta + lane * 16) = f32x4{c0.s, c0.z, c1.s, c1.z};
+  }
 }
 
 // The dequantisation of one group's four plane words as a sequence of micro-operations: kind 0 prepares word arg
@@ -273,7 +286,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     for (int t = 0; t < 4; ++t) {
       const uint32_t c = column_of(j, t);
       cw[h][t] = *(const uint32_t *)(src + h * 1024 + c * 16 + q * 4);
-      mw[h][t] = slot_meta<FMT>(src + 2048, c);
+      mw[h][t] = slot_meta<FMT>(src + 2048, c, h);
     }
   };
   // The dequantisation of one group's four words runs as 52 micro-operations (see micro_op) spread one or two
@@ -319,6 +332,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   copy_a(1, 1);
   __builtin_amdgcn_s_waitcnt(wait_vm(0));
   lds_barrier();
+  q4k_coefficients<FMT>(wave_slot + 2048, 0, lane);
   read_b(0, 0);
   read_b(0, 1);
   dequant_group(0, 0);
@@ -349,7 +363,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
     for (int b = 0; b < kBatches; ++b) {
       if (b + 1 < kBatches) read_batch(b + 1);
-      if (b == 0) read_b((step + 1) % kSlots, 0);
+      if (b == 0) {
+        q4k_coefficients<FMT>(wave_slot + ((step + 1) % kSlots) * kSlotBytes + 2048, step + 1, lane);
+        read_b((step + 1) % kSlots, 0);
+      }
       if (b == kBatches / 2) read_b((step + 1) % kSlots, 1);
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
@@ -409,13 +426,16 @@ hipError_t launch_tile(uint32_t epilogue, const PrefillArgs &a, uint32_t tiles, 
   return hipGetLastError();
 }
 
-// 256-row tiles, unless fewer of them than compute units would leave units idle that 128-row tiles fill.
+// The tile height with fewer rounds of workgroups over the compute units (one workgroup a unit), a 128-row tile
+// costing 0.7 of a 256-row one (measured: the dequantisation and the step's fixed work are shared by half the rows).
 template <uint32_t FMT>
 hipError_t launch_format(uint32_t epilogue, const PrefillArgs &a, hipStream_t stream) {
   uint32_t tiles = 0;
   for (uint32_t s = 0; s < a.segments; ++s) tiles += a.seg[s].tiles;
-  const uint32_t large = (a.rows + 255) / 256 * ((tiles + 3) / 4);
-  if (large < a.compute_units) return launch_tile<FMT, 128>(epilogue, a, tiles, stream);
+  const uint32_t columns = (tiles + 3) / 4, units = a.compute_units ? a.compute_units : 256;
+  const uint32_t rounds256 = ((a.rows + 255) / 256 * columns + units - 1) / units;
+  const uint32_t rounds128 = ((a.rows + 127) / 128 * columns + units - 1) / units;
+  if (7 * rounds128 < 10 * rounds256) return launch_tile<FMT, 128>(epilogue, a, tiles, stream);
   return launch_tile<FMT, 256>(epilogue, a, tiles, stream);
 }
 
