@@ -150,25 +150,36 @@ __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], co
   };
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   f32x4 C[NT][4][MB], S[MB];
-  const auto compute = [&](uint32_t c, int set) __attribute__((always_inline)) {
+  // Each group's exact operands (transposed words as bf16 128 + q) are built one group ahead, into the other of
+  // two operand sets, so that building them interleaves with the previous group's MFMAs.
+  u32x4 wop[2][NT][4];
+  const auto prepare = [&](int set, int u, int os) __attribute__((always_inline)) {
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      uint32_t r[4] = {codes[set][n][u][0], codes[set][n][u][1], codes[set][n][u][2], codes[set][n][u][3]};
+      transpose4(r);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) wop[os][n][t] = code_pairs(r[t], cc);
+    }
+  };
+  const auto compute = [&](uint32_t c, int set, int next_set) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const uint32_t g = c * CH + u;
+      const int os = u & 1;   // CH is even: group g's operands sit in set g % 2
       if (g < G) {
         const bool first = u % SG == 0;
 #pragma unroll
         for (int b = 0; b < MB; ++b) S[b] = mfma_bf16(xv[set][b][u], ones_operand(), first ? zero : S[b]);
 #pragma unroll
-        for (int n = 0; n < NT; ++n) {
-          uint32_t r[4] = {codes[set][n][u][0], codes[set][n][u][1], codes[set][n][u][2], codes[set][n][u][3]};
-          transpose4(r);
+        for (int n = 0; n < NT; ++n)
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const u32x4 w = code_pairs(r[t], cc);
+          for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int b = 0; b < MB; ++b) C[n][t][b] = mfma_bf16(xv[set][b][u], w, first ? zero : C[n][t][b]);
-          }
-        }
+            for (int b = 0; b < MB; ++b) C[n][t][b] = mfma_bf16(xv[set][b][u], wop[os][n][t], first ? zero : C[n][t][b]);
+        // The next group's operands (the last group of a chunk takes the next chunk's first).
+        if (u + 1 < CH) prepare(set, u + 1, os ^ 1);
+        else prepare(next_set, 0, os ^ 1);
         if ((u + 1) % SG == 0) {
 #pragma unroll
           for (int n = 0; n < NT; ++n)
@@ -191,12 +202,13 @@ __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], co
   };
 #pragma unroll
   for (int c = 0; c < SETS - 1; ++c) issue(c, c);
+  prepare(0, 0, 0);
   for (uint32_t c = 0; c < chunks; c += SETS) {
 #pragma unroll
     for (int k = 0; k < SETS; ++k) {
       issue(c + k + SETS - 1, (k + SETS - 1) % SETS);
       __builtin_amdgcn_sched_barrier(0);
-      compute(c + k, k);
+      compute(c + k, k, (k + 1) % SETS);
     }
   }
 }
