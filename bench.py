@@ -7,6 +7,9 @@ ring of weight copies larger than the 256 MB Infinity Cache makes every step rea
 captured once in a HIP graph and replayed (a serving loop's form: no host work between dispatches), bracketed by
 HIP events on the launching stream.
 
+`stream_floor`: a read-only streaming kernel (sq_diag_stream_read, several launch shapes) over the same number of
+bytes from a ring of copies, timed the same way: what one dispatch of that size reaches on this machine's HBM.
+
 `roofline.achieved`: the same bytes over the column tile's average launch duration, the HIP-event timed region
 on the launching stream divided by its K launches (one dispatch per step; rocprofv3's kernel trace of the same
 command, profiles/decode_column_gemv_m1_4096x14336.txt, agrees to within the dispatch gaps); `roofline.traffic`:
@@ -130,6 +133,26 @@ def time_graph(torch, launch, steps: int, warmup: int) -> float:
     torch.cuda.synchronize()
     del graph
     return start.elapsed_time(end) / 1e3 / steps
+
+
+def stream_floor(torch, sq, nbytes: int, steps: int, warmup: int) -> dict:
+    """The read-only streaming kernel (sq_diag_stream_read) over `nbytes` from a ring of copies larger than the
+    Infinity Cache, timed like the headline GEMV: the HBM read rate one dispatch of that size reaches here."""
+    span = (nbytes + 4095) // 4096 * 4096
+    copies = max(2, -(-RING_BYTES // span))
+    ring = torch.empty(copies * span, dtype=torch.uint8, device="cuda").fill_(1)
+    sink = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    results = {}
+    for workgroups, threads in ((224, 1024), (256, 1024), (512, 512), (1024, 256), (2048, 256)):
+        def launch(i, stream, workgroups=workgroups, threads=threads):
+            copy = ring[(i % copies) * span:]
+            sq.stream_read(copy, sink, workgroups, threads, nbytes=nbytes, stream=sq.c_void_p(stream))
+        sec = time_graph(torch, launch, steps, warmup)
+        results[f"{workgroups}x{threads}"] = round(nbytes / sec / 1e9, 1)
+    best = max(results, key=results.get)
+    del ring, sink
+    torch.cuda.empty_cache()
+    return {"GB/s": results[best], "launch": best, "bytes": nbytes, "by_launch": results}
 
 
 class Gemv:
@@ -272,6 +295,8 @@ def main() -> int:
     ring_copies = headline.copies
     del headline
     torch.cuda.empty_cache()
+    floor = stream_floor(torch, sq, int(gemv_bytes(m, n, k)), args.steps, args.warmup)
+    log(f"  stream floor over the same bytes: {floor['GB/s']} GB/s ({floor['launch']})")
     if args.calibrate_copy:
         # A plain device copy of known size for scaling the FETCH_SIZE / WRITE_SIZE counters.
         src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
@@ -336,6 +361,7 @@ def main() -> int:
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(),
                      "kernel": "column_kernel<af4g64, 1 row>", "launch_us": round(sec * 1e6, 3),
                      "algorithmic_bytes": int(gemv_bytes(m, n, k))},
+        "stream_floor": dict(floor, frac_of_floor=round(gbs / floor["GB/s"], 3)),
     }
     result.update(extra)
     if not args.quick:

@@ -162,6 +162,13 @@ int sq_mlx_repack(void *graph, uint32_t format_id, uint32_t rows, uint32_t input
  * dev/tests/engine/gguf_dequant_test.metal:5-21). */
 int sq_dequant(void *graph, const sq_segment *segment, sq_buffer values_f32, sq_buffer values_f16);
 
+/* ---- measurement ---- */
+
+/* No counterpart in the reference: a read-only stream of src (whole 16-byte vectors) by `workgroups` workgroups of
+ * `threads` threads, each folding what it reads into its word of sink. The HBM floor the GEMV is measured against
+ * (bench.py). */
+int sq_diag_stream_read(void *graph, sq_buffer src, sq_buffer sink, uint32_t workgroups, uint32_t threads);
+
 /* ---- MoE (runtime/ops/MoE.hpp:387-423) ---- */
 
 typedef struct sq_moe_shape {

@@ -264,6 +264,18 @@ int sq_mlx_repack(void *graph, uint32_t fmt, uint32_t rows, uint32_t k, sq_buffe
   });
 }
 
+int sq_diag_stream_read(void *graph, sq_buffer src, sq_buffer sink, uint32_t workgroups, uint32_t threads) {
+  return guarded([&] {
+    if (!src.ptr || !src.bytes || src.bytes % 16) throw std::invalid_argument("stream source is whole 16-byte vectors");
+    if (!workgroups || !threads || threads > 1024 || threads % 64)
+      throw std::invalid_argument("stream launch takes workgroups of 64..1024 threads, whole waves");
+    requireBytes(buf(sink), uint64_t{workgroups} * 4, "stream sink");
+    launched(sq::kern::launch_stream_read(src.ptr, src.bytes, static_cast<uint32_t *>(sink.ptr), workgroups, threads,
+                                          stream(graph)),
+             "stream read");
+  });
+}
+
 int sq_dequant(void *graph, const sq_segment *s, sq_buffer values, sq_buffer halves) {
   return guarded([&] {
     const QuantizedSegment q = segment(need(s, "segment"));

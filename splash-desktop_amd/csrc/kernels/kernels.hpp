@@ -77,6 +77,9 @@ hipError_t launch_dequant(uint32_t fmt, const uint8_t *plane0, const uint8_t *me
 // Load-time repacks: native rows (GgufRepackParams layout) into plane0 / meta, and MLX tensors (uint32 codes,
 // bf16 scales and biases) straight into plane0 / meta.
 hipError_t launch_repack(const uint8_t *src, uint8_t *dst, const SqGgufRepackParams &params, hipStream_t stream);
+// Measurement aid (diag.hip): a read-only stream of `bytes` (a multiple of 16) over `workgroups` workgroups.
+hipError_t launch_stream_read(const void *src, uint64_t bytes, uint32_t *sink, uint32_t workgroups, uint32_t threads,
+                              hipStream_t stream);
 hipError_t launch_mlx_repack(uint32_t fmt, const uint32_t *weight, const uint16_t *scales, const uint16_t *biases,
                              uint32_t rows, uint32_t K, uint8_t *plane0, uint8_t *meta, hipStream_t stream);
 

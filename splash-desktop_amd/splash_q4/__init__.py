@@ -147,6 +147,7 @@ _SIGNATURES = {
     "sq_gguf_repack": [c_void_p, Buffer, Buffer, c_void_p],
     "sq_mlx_repack": [c_void_p, c_uint32, c_uint32, c_uint32, Buffer, Buffer, Buffer, Buffer, Buffer],
     "sq_dequant": [c_void_p, POINTER(Segment), Buffer, Buffer],
+    "sq_diag_stream_read": [c_void_p, Buffer, Buffer, c_uint32, c_uint32],
     "sq_moe_prefill_plan": [POINTER(MoeShape), c_uint32, POINTER(MoePlan)],
     "sq_moe_decode_plan": [POINTER(MoeShape), c_uint32, POINTER(MoePlan)],
     "sq_moe_add": [c_void_p, POINTER(MoeBuffers), POINTER(MoeWeights), POINTER(MoePlan)],
@@ -289,3 +290,9 @@ def gguf_repack(src, dst, rows: int, k: int, fmt: int, src_row_bytes: int, dst_m
 
 def dequant(seg: Segment, values=None, halves=None, stream=None) -> None:
     call("sq_dequant", stream if stream is not None else stream_handle(), byref(seg), view(values), view(halves))
+
+
+def stream_read(src, sink, workgroups: int, threads: int, nbytes: int | None = None, stream=None) -> None:
+    """The read-only streaming kernel over `nbytes` of src (measurement aid, sq_diag_stream_read)."""
+    call("sq_diag_stream_read", stream if stream is not None else stream_handle(), view(src, nbytes), view(sink),
+         workgroups, threads)

@@ -79,3 +79,19 @@ def test_repack_rejects_bad_chunks():
         sq.gguf_repack(src, src, 10, 256, oracle.FMT_AF4G64, 144, 0)
     with pytest.raises(sq.InvalidArgument, match="repack source"):
         sq.gguf_repack(src, src, 64, 256, oracle.FMT_AF4G64, 144, 64 * 8 * 16)
+
+
+def test_stream_read_folds_every_word():
+    """The measurement stream reads every 16-byte vector of its source: each workgroup's word is the xor of its
+    share (4 workgroups, a share not a multiple of the launch width)."""
+    t = torch()
+    rng = np.random.default_rng(21)
+    words = rng.integers(0, 2**32, size=4 * 5000, dtype=np.uint32)
+    src = to_device(words.view(np.uint8))
+    sink = t.zeros(4, dtype=t.int32, device="cuda")
+    sq.stream_read(src, sink, 4, 256)
+    got = to_host(sink, np.int32).view(np.uint32)
+    vectors = words.reshape(-1, 4)
+    share = -(-len(vectors) // 4)
+    want = [np.bitwise_xor.reduce(vectors[w * share:(w + 1) * share].ravel()) for w in range(4)]
+    assert got.tolist() == [int(v) for v in want]
