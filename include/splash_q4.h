@@ -171,9 +171,22 @@ int sq_diag_stream_read(void *graph, sq_buffer src, sq_buffer sink, uint32_t wor
 
 /* ---- MoE (runtime/ops/MoE.hpp:387-423) ---- */
 
+/* MoeRouter (MoE.hpp:22-28): Softmax weights the top_k routes by the softmax of their scores, SigmoidNormalized by
+ * each one's sigmoid over the sum of theirs. */
+#define SQ_MOE_ROUTER_SOFTMAX 0u
+#define SQ_MOE_ROUTER_SIGMOID_NORMALIZED 1u
+
+/* MoeShape (MoE.hpp:54-102). The reference compiles two routings, (Softmax, 1 shared slice, gated) and
+ * (SigmoidNormalized, 2 shared slices, ungated) (kCompiledMoeRoutings, MoE.hpp:34-46); this build also takes
+ * (Softmax, no shared expert). The shared expert is shared_slices experts every row visits after its routed ones,
+ * each of the routed experts' intermediate width; gated, slice weights are sigmoid(x . g) of the block's fp32
+ * scalar gate g, else 1. */
 typedef struct sq_moe_shape {
   uint32_t hidden_size, experts, experts_per_token, expert_intermediate_size;
   uint32_t expert_format; /* the routed experts' format id */
+  uint32_t router;        /* SQ_MOE_ROUTER_* */
+  uint32_t shared_slices; /* 0, 1 or 2 */
+  uint32_t shared_gated;  /* 1: slice weights sigmoid(x . g); 0: 1 */
 } sq_moe_shape;
 typedef struct sq_moe_workspace {
   uint64_t selected_experts, routing_weights, tile_descriptors, tile_count, grouped_routes, route_rows,
@@ -184,11 +197,17 @@ typedef struct sq_moe_plan {
   uint32_t rows, phase, tile_rows, maximum_tiles;
   sq_moe_workspace workspace;
 } sq_moe_plan;
-/* BlockExpertProjection.routed: `slots` experts' planes in one segment of slots * N rows. */
+/* BlockExpertProjection (MoE.hpp:111-148). routed: `slots` experts' planes in one segment of slots * N rows.
+ * shared: the shared slices' planes in their order, slice s's rows s * N on (a shared down of shared_slices * I
+ * inputs laid out as shared_slices column windows of I inputs, window s rows s * H on); their format may differ
+ * from the routed one, gate and up alike. shared_scalar_gate: the block's fp32 gate [hidden] for a gated shared
+ * expert. The shared views are ignored without shared slices. */
 typedef struct sq_moe_weights {
   sq_segment gate, up, down;
   sq_buffer slot_table; /* uint32 per expert: its slot */
   uint32_t slots;
+  sq_segment shared_gate, shared_up, shared_down;
+  sq_buffer shared_scalar_gate;
 } sq_moe_weights;
 typedef struct sq_moe_scratch {
   sq_buffer selected_experts, routing_weights, tile_descriptors, tile_count, grouped_routes, route_rows,
@@ -202,7 +221,7 @@ typedef struct sq_moe_buffers {
   sq_moe_scratch scratch;
 } sq_moe_buffers;
 
-/* MoE::prefillPlan / decodePlan (MoE.cpp:204-223; MoePlan, MoE.hpp:349-373): routed experts only. A decode plan
+/* MoE::prefillPlan / decodePlan (MoE.cpp:204-223; MoePlan, MoE.hpp:349-373). A decode plan
  * takes any 1..32 rows (the reference's lanes * 8 among them); a prefill plan up to 2048. */
 int sq_moe_prefill_plan(const sq_moe_shape *shape, uint32_t rows, sq_moe_plan *out);
 int sq_moe_decode_plan(const sq_moe_shape *shape, uint32_t rows, sq_moe_plan *out);

@@ -497,39 +497,49 @@ double sqo_cpu_matmul(uint32_t fmt, uint32_t M, uint32_t N, uint32_t K, const ui
 
 /* ------------------------------------------------------------------ MoE */
 
-/* moe_route_select (moe.metal:69-104): ranks by descending score, the lower expert id among equal scores; weight of
- * rank r = exp(s_r - s_0) / sum_j exp(s_j - s_0) over the selected k (here in fp64). */
-void sqo_route_select(uint32_t rows, uint32_t experts, uint32_t top_k, const float *scores, uint32_t *selected,
-                      double *weights) {
+static double sqo_sigmoid(double x) { return 1.0 / (1.0 + exp(-x)); }
+
+/* moe_route_select (moe.metal:23-104): ranks by descending score, the lower expert id among equal scores. Softmax
+ * (router 0): weight of rank r = exp(s_r - s_0) / sum_j exp(s_j - s_0) over the selected k; SigmoidNormalized
+ * (router 1): sigmoid(s_r) / (sum_j sigmoid(s_j) + 1e-20). In fp64. Rows of `per_row` routes, the routed top_k
+ * first (the caller fills the shared slices' routes after them). */
+void sqo_route_select(uint32_t rows, uint32_t experts, uint32_t top_k, uint32_t router, uint32_t per_row,
+                      const float *scores, uint32_t *selected, double *weights) {
   unsigned char *taken = (unsigned char *)malloc(experts);
   for (uint32_t r = 0; r < rows; ++r) {
     const float *s = scores + (size_t)r * experts;
+    uint32_t *sel = selected + (size_t)r * per_row;
+    double *w = weights + (size_t)r * per_row;
     memset(taken, 0, experts);
     for (uint32_t rank = 0; rank < top_k; ++rank) {
       uint32_t best = experts;
       for (uint32_t e = 0; e < experts; ++e)
         if (!taken[e] && (best == experts || s[e] > s[best])) best = e;
       taken[best] = 1;
-      selected[(size_t)r * top_k + rank] = best;
+      sel[rank] = best;
     }
-    const double top = s[selected[(size_t)r * top_k]];
+    const double top = s[sel[0]];
     double denominator = 0;
-    for (uint32_t rank = 0; rank < top_k; ++rank) denominator += exp((double)s[selected[(size_t)r * top_k + rank]] - top);
     for (uint32_t rank = 0; rank < top_k; ++rank)
-      weights[(size_t)r * top_k + rank] = exp((double)s[selected[(size_t)r * top_k + rank]] - top) / denominator;
+      denominator += router ? sqo_sigmoid(s[sel[rank]]) : exp((double)s[sel[rank]] - top);
+    if (router) denominator += 1e-20;
+    for (uint32_t rank = 0; rank < top_k; ++rank)
+      w[rank] = (router ? sqo_sigmoid(s[sel[rank]]) : exp((double)s[sel[rank]] - top)) / denominator;
   }
   free(taken);
 }
 
-/* moe_group_routes_phase (moe.metal:184-278) without shared slices: count per expert, exclusive prefix of the
- * experts' tiles in expert order, then each expert's routes in route order over its tiles. */
-uint32_t sqo_group_routes(uint32_t rows, uint32_t top_k, uint32_t experts, uint32_t tile_rows,
+/* moe_group_routes_phase (moe.metal:184-278): count per expert, exclusive prefix of the experts' tiles in expert
+ * order, then each expert's routes in route order over its tiles; the `shared` slices' tiles follow, slice after
+ * slice, each holding every row in order. Rows hold top_k + shared routes, the routed ones first. */
+uint32_t sqo_group_routes(uint32_t rows, uint32_t top_k, uint32_t shared, uint32_t experts, uint32_t tile_rows,
                           const uint32_t *selected, uint32_t *tiles, uint32_t *grouped_routes, uint32_t *route_rows) {
-  const uint32_t routes = rows * top_k;
+  const uint32_t per_row = top_k + shared, routes = rows * per_row;
   uint32_t *count = (uint32_t *)calloc(experts, sizeof(uint32_t));
   uint32_t *offset = (uint32_t *)calloc(experts, sizeof(uint32_t));
   uint32_t *cursor = (uint32_t *)calloc(experts, sizeof(uint32_t));
-  for (uint32_t r = 0; r < routes; ++r) ++count[selected[r]];
+  for (uint32_t r = 0; r < routes; ++r)
+    if (r % per_row < top_k) ++count[selected[r]];
   uint32_t total = 0;
   for (uint32_t e = 0; e < experts; ++e) {
     offset[e] = total;
@@ -540,12 +550,27 @@ uint32_t sqo_group_routes(uint32_t rows, uint32_t top_k, uint32_t experts, uint3
     }
     total += t;
   }
-  for (uint32_t i = 0; i < total * tile_rows; ++i) grouped_routes[i] = ~0u;
+  const uint32_t shared_tiles = (rows + tile_rows - 1) / tile_rows;
+  for (uint32_t i = 0; i < (total + shared * shared_tiles) * tile_rows; ++i) grouped_routes[i] = ~0u;
   for (uint32_t r = 0; r < routes; ++r) {
+    if (r % per_row >= top_k) continue;
     const uint32_t e = selected[r], row = offset[e] * tile_rows + cursor[e]++;
     grouped_routes[row] = r;
     route_rows[r] = row;
   }
+  for (uint32_t slice = 0; slice < shared; ++slice) {
+    for (uint32_t t = 0; t < shared_tiles; ++t) {
+      const uint32_t at = total + slice * shared_tiles + t;
+      tiles[2 * at] = experts + slice;
+      tiles[2 * at + 1] = rows - t * tile_rows < tile_rows ? rows - t * tile_rows : tile_rows;
+    }
+    for (uint32_t row = 0; row < rows; ++row) {
+      const uint32_t r = row * per_row + top_k + slice, g = (total + slice * shared_tiles) * tile_rows + row;
+      grouped_routes[g] = r;
+      route_rows[r] = g;
+    }
+  }
+  total += shared * shared_tiles;
   free(count);
   free(offset);
   free(cursor);

@@ -75,14 +75,14 @@ void sqo_project_staged_f32(uint32_t M, uint32_t N, uint32_t K, const uint16_t *
 double sqo_cpu_matmul(uint32_t fmt, uint32_t M, uint32_t N, uint32_t K, const uint16_t *x, const uint8_t *plane0,
                       const uint8_t *meta, uint16_t *out, int threads);
 
-/* MoE (moe.metal): top-k of fp32 scores [rows][experts] (descending, ties to the lower id) with their renormalised
- * softmax weights (fp64 here), [rows][top_k] each. */
-void sqo_route_select(uint32_t rows, uint32_t experts, uint32_t top_k, const float *scores, uint32_t *selected,
-                      double *weights);
-/* Grouping into tiles of tile_rows rows: routes by expert (stable in route order), returns the tile count.
- * tiles: 2 uint32 per tile (expert, live rows); grouped_routes [tiles * tile_rows] (~0u padding);
- * route_rows [rows * top_k]. */
-uint32_t sqo_group_routes(uint32_t rows, uint32_t top_k, uint32_t experts, uint32_t tile_rows,
+/* MoE (moe.metal): top-k of fp32 scores [rows][experts] (descending, ties to the lower id) with their weights
+ * (router 0: renormalised softmax; 1: sigmoids over their sum), fp64 here, into rows of per_row routes. */
+void sqo_route_select(uint32_t rows, uint32_t experts, uint32_t top_k, uint32_t router, uint32_t per_row,
+                      const float *scores, uint32_t *selected, double *weights);
+/* Grouping into tiles of tile_rows rows: routed routes by expert (stable in route order), then `shared` slices'
+ * tiles of every row; returns the tile count. tiles: 2 uint32 per tile (expert, live rows); grouped_routes
+ * [tiles * tile_rows] (~0u padding); route_rows [rows * (top_k + shared)]. */
+uint32_t sqo_group_routes(uint32_t rows, uint32_t top_k, uint32_t shared, uint32_t experts, uint32_t tile_rows,
                           const uint32_t *selected, uint32_t *tiles, uint32_t *grouped_routes, uint32_t *route_rows);
 
 #ifdef __cplusplus

@@ -150,23 +150,43 @@ def cpu_matmul(fmt: int, x_bf16: np.ndarray, plane0: np.ndarray, meta: np.ndarra
     return out, secs
 
 
-def route_select(scores: np.ndarray, top_k: int):
+ROUTER_SOFTMAX, ROUTER_SIGMOID_NORMALIZED = 0, 1
+
+
+def route_select(scores: np.ndarray, top_k: int, router: int = ROUTER_SOFTMAX, shared: int = 0,
+                 x_bf16: np.ndarray | None = None, scalar_gate: np.ndarray | None = None):
+    """moe_route_select (moe.metal:23-104): [rows][top_k + shared] experts and fp64 weights. The shared slices'
+    routes (ids experts..experts + shared - 1) follow the routed ones, weighted sigmoid(x . g) of the fp32 scalar
+    gate g when one is given (moe.metal:43-67), else 1."""
     rows, experts = scores.shape
-    selected = np.zeros((rows, top_k), np.uint32)
-    weights = np.zeros((rows, top_k), np.float64)
-    lib().sqo_route_select(rows, experts, top_k, _ptr(np.ascontiguousarray(scores, np.float32), c_float),
+    per_row = top_k + shared
+    selected = np.zeros((rows, per_row), np.uint32)
+    weights = np.zeros((rows, per_row), np.float64)
+    lib().sqo_route_select(rows, experts, top_k, router, per_row,
+                           _ptr(np.ascontiguousarray(scores, np.float32), c_float),
                            _ptr(selected, c_uint32), _ptr(weights, c_double))
+    if shared:
+        selected[:, top_k:] = experts + np.arange(shared, dtype=np.uint32)
+        if scalar_gate is not None:
+            x = (x_bf16.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+            gate = 1.0 / (1.0 + np.exp(-(x @ scalar_gate.astype(np.float64))))
+            weights[:, top_k:] = gate[:, None]
+        else:
+            weights[:, top_k:] = 1.0
     return selected, weights
 
 
-def group_routes(selected: np.ndarray, experts: int, tile_rows: int):
-    rows, top_k = selected.shape
-    routes = rows * top_k
-    max_tiles = min(routes // tile_rows + experts, routes)
+def group_routes(selected: np.ndarray, experts: int, tile_rows: int, shared: int = 0):
+    """moe_group_routes_phase (moe.metal:184-278) over rows of top_k routed then `shared` shared routes."""
+    rows, per_row = selected.shape
+    top_k = per_row - shared
+    routed = rows * top_k
+    max_tiles = min(routed // tile_rows + experts, routed) + shared * (-(-rows // tile_rows))
     tiles = np.zeros((max_tiles, 2), np.uint32)
     grouped = np.zeros(max_tiles * tile_rows, np.uint32)
-    route_rows = np.zeros(routes, np.uint32)
-    count = lib().sqo_group_routes(rows, top_k, experts, tile_rows, _ptr(np.ascontiguousarray(selected), c_uint32),
+    route_rows = np.zeros(rows * per_row, np.uint32)
+    count = lib().sqo_group_routes(rows, top_k, shared, experts, tile_rows,
+                                   _ptr(np.ascontiguousarray(selected), c_uint32),
                                    _ptr(tiles, c_uint32), _ptr(grouped, c_uint32), _ptr(route_rows, c_uint32))
     return tiles[:count], grouped[:count * tile_rows], route_rows
 

@@ -126,6 +126,9 @@ struct SqGgufRepackParams {
 static_assert(sizeof(SqGgufRepackParams) == 24, "GgufRepackParams is 24 bytes");
 
 // ---------------------------------------------------------------- MoE (MoE.h:19-181)
+// ops::MoeRouter (MoE.hpp:22-28): how the top_k routes are weighted.
+#define SQ_MOE_ROUTER_SOFTMAX 0u
+#define SQ_MOE_ROUTER_SIGMOID_NORMALIZED 1u
 #define SQ_MOE_EXPERT_SLOTS 256u
 #define SQ_MOE_WIDE_EXPERT_SLOTS 512u
 struct SqMoeRouteParams {

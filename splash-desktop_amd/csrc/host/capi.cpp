@@ -296,12 +296,15 @@ int sq_dequant(void *graph, const sq_segment *s, sq_buffer values, sq_buffer hal
 
 namespace {
 MoeShape moeShape(const sq_moe_shape &s) {
-  return {s.hidden_size, s.experts, s.experts_per_token, s.expert_intermediate_size, s.expert_format};
+  if (s.router > SQ_MOE_ROUTER_SIGMOID_NORMALIZED) throw std::invalid_argument("unknown MoE router");
+  return {s.hidden_size, s.experts, s.experts_per_token, s.expert_intermediate_size, s.expert_format,
+          MoeRouter(s.router), s.shared_slices, s.shared_gated != 0};
 }
 sq_moe_plan cmoe(const MoePlan &p) {
   sq_moe_plan out{};
   const MoeShape s = p.shape();
-  out.shape = {s.hiddenSize, s.experts, s.expertsPerToken, s.expertIntermediateSize, s.expertFormat};
+  out.shape = {s.hiddenSize, s.experts, s.expertsPerToken, s.expertIntermediateSize, s.expertFormat,
+               uint32_t(s.router), s.sharedSlices, uint32_t(s.sharedGate)};
   out.rows = p.rows();
   out.phase = uint32_t(p.phase());
   out.tile_rows = p.tileRows();
@@ -315,8 +318,16 @@ MoePlan moePlan(const sq_moe_plan &p) {
   if (p.phase > SQ_PHASE_DECODE) throw std::invalid_argument("invalid MoE phase");
   return p.phase == SQ_PHASE_DECODE ? MoE::decodeRows(moeShape(p.shape), p.rows) : MoE::prefillPlan(moeShape(p.shape), p.rows);
 }
-MoeWeights moeWeights(const sq_moe_weights &w) {
-  return {segment(w.gate), segment(w.up), segment(w.down), buf(w.slot_table), w.slots};
+// The shared views are read only when the plan has shared slices.
+MoeWeights moeWeights(const sq_moe_weights &w, const sq_moe_plan &p) {
+  MoeWeights out{segment(w.gate), segment(w.up), segment(w.down), buf(w.slot_table), w.slots, {}, {}, {}, {}};
+  if (p.shape.shared_slices) {
+    out.sharedGate = segment(w.shared_gate);
+    out.sharedUp = segment(w.shared_up);
+    out.sharedDown = segment(w.shared_down);
+    if (p.shape.shared_gated) out.sharedScalarGate = buf(w.shared_scalar_gate);
+  }
+  return out;
 }
 MoeBuffers moeBuffers(const sq_moe_buffers &b) {
   const sq_moe_scratch &s = b.scratch;
@@ -336,13 +347,13 @@ int sq_moe_decode_plan(const sq_moe_shape *shape, uint32_t rows, sq_moe_plan *ou
   return guarded([&] { *out = cmoe(MoE::decodeRows(moeShape(need(shape, "shape")), rows)); });
 }
 int sq_moe_add(void *graph, const sq_moe_buffers *b, const sq_moe_weights *w, const sq_moe_plan *p) {
-  return guarded([&] { MoE::add(stream(graph), moeBuffers(need(b, "buffers")), moeWeights(need(w, "weights")), moePlan(need(p, "plan"))); });
+  return guarded([&] { MoE::add(stream(graph), moeBuffers(need(b, "buffers")), moeWeights(need(w, "weights"), need(p, "plan")), moePlan(need(p, "plan"))); });
 }
 int sq_moe_add_routing(void *graph, const sq_moe_buffers *b, const sq_moe_weights *w, const sq_moe_plan *p) {
-  return guarded([&] { MoE::addRouting(stream(graph), moeBuffers(need(b, "buffers")), moeWeights(need(w, "weights")), moePlan(need(p, "plan"))); });
+  return guarded([&] { MoE::addRouting(stream(graph), moeBuffers(need(b, "buffers")), moeWeights(need(w, "weights"), need(p, "plan")), moePlan(need(p, "plan"))); });
 }
 int sq_moe_add_routed(void *graph, const sq_moe_buffers *b, const sq_moe_weights *w, const sq_moe_plan *p) {
-  return guarded([&] { MoE::addRouted(stream(graph), moeBuffers(need(b, "buffers")), moeWeights(need(w, "weights")), moePlan(need(p, "plan"))); });
+  return guarded([&] { MoE::addRouted(stream(graph), moeBuffers(need(b, "buffers")), moeWeights(need(w, "weights"), need(p, "plan")), moePlan(need(p, "plan"))); });
 }
 
 }  // extern "C"

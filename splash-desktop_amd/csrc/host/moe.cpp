@@ -11,7 +11,7 @@ void launched(hipError_t e, const char *what) {
   if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
 
-// MoE.cpp:64-84 for routed experts: the grouped rows' intermediates and outputs; the gather reads the input rows
+// MoE.cpp:64-84: the grouped rows' intermediates and outputs; the gather reads the input rows
 // straight from the routes, so the grouped input holds nothing.
 MoeWorkspace workspaceFor(const MoeShape &shape, uint32_t rows, uint32_t tileRows) {
   if (!shape.valid()) throw std::invalid_argument("invalid MoE workspace shape");
@@ -39,6 +39,15 @@ void validate(const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
   requireExperts(w.gate, w.slots, in, h, s.expertFormat, "gate");
   requireExperts(w.up, w.slots, in, h, s.expertFormat, "up");
   requireExperts(w.down, w.slots, h, in, s.expertFormat, "down");
+  if (s.sharedSlices) {
+    // The shared slices (MoE.cpp:40-60). The gate/up pass runs gate and up in one format.
+    if (!sq_format_supported(w.sharedGate.formatId) || !sq_format_supported(w.sharedDown.formatId))
+      throw std::invalid_argument("MoE shared expert format is not supported");
+    requireExperts(w.sharedGate, s.sharedSlices, in, h, w.sharedGate.formatId, "shared gate");
+    requireExperts(w.sharedUp, s.sharedSlices, in, h, w.sharedGate.formatId, "shared up");
+    requireExperts(w.sharedDown, s.sharedSlices, h, in, w.sharedDown.formatId, "shared down");
+    if (s.sharedGate) requireBytes(w.sharedScalarGate, uint64_t{h} * 4, "MoE shared scalar gate weight");
+  }
   const uint64_t hiddenRows = uint64_t{plan.rows()} * h * 2;
   requireBytes(b.input, hiddenRows, "MoE input");
   if (b.residual) requireBytes(b.residual, hiddenRows, "MoE residual");
@@ -94,14 +103,17 @@ void MoE::addRouting(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w
   const MoeScratch &sc = b.scratch;
   const SqMoeRouteParams route{plan.rows(), s.hiddenSize, s.experts, s.expertsPerToken};
   launched(kern::launch_moe_route_select(b.scores.as<const float>(), b.scoreStride ? b.scoreStride : s.experts,
-                                         sc.selectedExperts.as<uint32_t>(), sc.routingWeights.as<float>(), route, graph),
+                                         sc.selectedExperts.as<uint32_t>(), sc.routingWeights.as<float>(), route,
+                                         b.input.as<const uint16_t>(),
+                                         s.sharedGate ? w.sharedScalarGate.as<const float>() : nullptr,
+                                         uint32_t(s.router), s.sharedSlices, graph),
            "MoE route select");
   const SqMoeGroupParams group{plan.rows(), s.expertsPerToken, plan.tileRows(), s.experts,
                                s.expertIntermediateSize / SQ_TILE_COLUMNS, s.hiddenSize / SQ_TILE_COLUMNS,
                                SQ_TARGET_VERIFY_ROWS, 0};
   launched(kern::launch_moe_group(sc.selectedExperts.as<const uint32_t>(), sc.tileDescriptors.as<SqMoeTileDescriptor>(),
                                   sc.tileCount.as<SqMoeTileCount>(), sc.groupedRoutes.as<uint32_t>(),
-                                  sc.routeRows.as<uint32_t>(), plan.maximumTiles(), group, graph),
+                                  sc.routeRows.as<uint32_t>(), group, s.sharedSlices, graph),
            "MoE grouping");
 }
 
@@ -115,32 +127,53 @@ void MoE::addRouted(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w,
   a.slots = w.slotTable.as<const uint32_t>();
   a.tile_rows = plan.tileRows();
   a.max_tiles = plan.maximumTiles();
-  a.fmt = s.expertFormat;
   a.routes = sc.groupedRoutes.as<const uint32_t>();
-  a.top_k = s.expertsPerToken;
-  // Gate and up in one pass over the routed rows of the input: intermediate = bf16(bf16(up) silu(bf16(gate))).
+  a.routes_per_row = s.routesPerToken();
+  a.experts = s.experts;
+  // A pass runs the routed and the shared tiles in one launch when their formats agree, else one launch each.
+  const auto pass = [&](uint32_t routedFormat, uint32_t sharedFormat, const char *what) {
+    if (!s.sharedSlices || routedFormat == sharedFormat) {
+      a.fmt = routedFormat;
+      a.mode = s.sharedSlices ? 2 : 0;
+      launched(kern::launch_moe_expert(a, graph), what);
+      return;
+    }
+    a.fmt = routedFormat;
+    a.mode = 0;
+    launched(kern::launch_moe_expert(a, graph), what);
+    a.fmt = sharedFormat;
+    a.mode = 1;
+    launched(kern::launch_moe_expert(a, graph), what);
+  };
+  // Gate and up in one pass over the input rows of the routes: intermediate = bf16(bf16(up) silu(bf16(gate))).
   a.input = b.input.as<const uint16_t>();
   a.plane0[0] = w.gate.plane0.as<const uint8_t>();
   a.meta[0] = w.gate.meta.as<const uint8_t>();
   a.plane0[1] = w.up.plane0.as<const uint8_t>();
   a.meta[1] = w.up.meta.as<const uint8_t>();
+  a.shared_plane0[0] = w.sharedGate.plane0.as<const uint8_t>();
+  a.shared_meta[0] = w.sharedGate.meta.as<const uint8_t>();
+  a.shared_plane0[1] = w.sharedUp.plane0.as<const uint8_t>();
+  a.shared_meta[1] = w.sharedUp.meta.as<const uint8_t>();
   a.output = sc.expertIntermediate.as<uint16_t>();
   a.K = s.hiddenSize;
   a.output_size = s.expertIntermediateSize;
   a.gate_up = 1;
-  launched(kern::launch_moe_expert(a, graph), "MoE gate/up pass");
+  pass(s.expertFormat, w.sharedGate.formatId, "MoE gate/up pass");
   // Down over the grouped intermediate rows.
   a.input = sc.expertIntermediate.as<const uint16_t>();
   a.routes = nullptr;
   a.plane0[0] = w.down.plane0.as<const uint8_t>();
   a.meta[0] = w.down.meta.as<const uint8_t>();
-  a.plane0[1] = nullptr;
-  a.meta[1] = nullptr;
+  a.plane0[1] = a.meta[1] = nullptr;
+  a.shared_plane0[0] = w.sharedDown.plane0.as<const uint8_t>();
+  a.shared_meta[0] = w.sharedDown.meta.as<const uint8_t>();
+  a.shared_plane0[1] = a.shared_meta[1] = nullptr;
   a.output = sc.expertOutput.as<uint16_t>();
   a.K = s.expertIntermediateSize;
   a.output_size = s.hiddenSize;
   a.gate_up = 0;
-  launched(kern::launch_moe_expert(a, graph), "MoE down pass");
+  pass(s.expertFormat, w.sharedDown.formatId, "MoE down pass");
   const SqMoeCombineParams combine{plan.rows(), s.hiddenSize, s.routesPerToken()};
   launched(kern::launch_moe_combine(sc.expertOutput.as<const uint16_t>(), sc.routeRows.as<const uint32_t>(),
                                     sc.routingWeights.as<const float>(), b.residual.as<const uint16_t>(),

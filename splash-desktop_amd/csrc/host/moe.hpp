@@ -1,28 +1,43 @@
-// ops::MoE over HIP: the routed experts' grouped gather-GEMM (reference: runtime/ops/MoE.hpp:19-423 and
+// ops::MoE over HIP: the routed and shared experts' grouped gather-GEMM (reference: runtime/ops/MoE.hpp:19-423 and
 // runtime/ops/MoE.cpp:27-543). The router projection is the caller's: a step starts from its fp32 scores.
 #pragma once
 #include "ops.hpp"
 
 namespace sq::ops {
 
-// MoeShape (MoE.hpp:54-102) for a block of routed experts only: no shared expert slices.
+// MoeRouter (MoE.hpp:22-28).
+enum class MoeRouter : uint32_t { Softmax = SQ_MOE_ROUTER_SOFTMAX, SigmoidNormalized = SQ_MOE_ROUTER_SIGMOID_NORMALIZED };
+
+// MoeShape (MoE.hpp:54-102). The shared expert is sharedSlices experts (ids experts on) every row visits after its
+// routed ones, each of the routed experts' intermediate width; with sharedGate each slice's weight is the sigmoid
+// of the row's product with the block's fp32 scalar gate, else 1. The routings kernels run are the reference's
+// compiled ones (kCompiledMoeRoutings, MoE.hpp:34-46) and, here, routed experts alone (Softmax, no slices).
 struct MoeShape {
   uint32_t hiddenSize = 0, experts = 0, expertsPerToken = 0, expertIntermediateSize = 0;
   uint32_t expertFormat = SQ_FMT_AF4G64;
+  MoeRouter router = MoeRouter::Softmax;
+  uint32_t sharedSlices = 0;
+  bool sharedGate = false;
+  [[nodiscard]] bool compiledRouting() const noexcept {
+    return (router == MoeRouter::Softmax && sharedSlices == 1 && sharedGate) ||
+           (router == MoeRouter::SigmoidNormalized && sharedSlices == 2 && !sharedGate) ||
+           (router == MoeRouter::Softmax && sharedSlices == 0 && !sharedGate);
+  }
   [[nodiscard]] bool valid() const noexcept {
     return hiddenSize && hiddenSize % 256 == 0 && experts && experts <= SQ_MOE_WIDE_EXPERT_SLOTS && expertsPerToken &&
            expertsPerToken <= experts && expertsPerToken <= 64 && expertIntermediateSize &&
-           expertIntermediateSize % 64 == 0 && sq_format_supported(expertFormat);
+           expertIntermediateSize % 64 == 0 && sq_format_supported(expertFormat) && compiledRouting();
   }
-  [[nodiscard]] uint32_t routesPerToken() const noexcept { return expertsPerToken; }
+  [[nodiscard]] uint32_t routesPerToken() const noexcept { return expertsPerToken + sharedSlices; }
 };
 
 enum class MoePhase : uint8_t { Prefill, Decode };
 
-// moeMaximumTiles (MoE.hpp:200-205) without shared slices.
+// moeMaximumTiles (MoE.hpp:200-205): every routed expert may leave one partial tile and no tile is empty; each shared
+// slice fills one tile per tileRows rows.
 [[nodiscard]] constexpr uint32_t moeMaximumTiles(uint32_t rows, const MoeShape &shape, uint32_t tileRows) noexcept {
   const uint32_t routed = rows * shape.expertsPerToken;
-  return std::min(routed / tileRows + shape.experts, routed);
+  return std::min(routed / tileRows + shape.experts, routed) + shape.sharedSlices * ((rows + tileRows - 1) / tileRows);
 }
 
 struct MoeWorkspace {
@@ -33,11 +48,15 @@ struct MoeScratch {
   Buffer selectedExperts, routingWeights, tileDescriptors, tileCount, groupedRoutes, routeRows, groupedInput,
       expertIntermediate, expertOutput;
 };
-// The routed experts' planes: `slots` experts per projection, expert e's rows from slotTable[e] * N on.
+// BlockExpertProjection (MoE.hpp:111-148): the routed experts' planes, `slots` experts per projection, expert e's
+// rows from slotTable[e] * N on; the shared slices' planes, slice s's rows s * N on, in a format of their own (the
+// shared down's slices are the column windows of a shared_slices * I wide down); the block's fp32 scalar gate.
 struct MoeWeights {
   QuantizedSegment gate, up, down;
   Buffer slotTable;
   uint32_t slots = 0;
+  QuantizedSegment sharedGate, sharedUp, sharedDown;
+  Buffer sharedScalarGate;
 };
 struct MoeBuffers {
   Buffer input, scores, residual, output;

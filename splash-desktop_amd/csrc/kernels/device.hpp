@@ -78,8 +78,10 @@ __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
 }
 __device__ __forceinline__ uint16_t f32_to_f16(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
 
-// silu(g) = g / (1 + 2^(-g log2 e)), the reference's form of it (activation.h:8-13).
+// silu(g) = g / (1 + 2^(-g log2 e)) and sigmoid(x) = 1 / (1 + 2^(-x log2 e)), the reference's forms of them
+// (activation.h:8-16).
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + exp2f(-1.44269504089f * g)); }
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + exp2f(-1.44269504089f * x)); }
 
 // Epilogue of one output before its bf16 rounding, given the bf16 bits of its aux element: Residual adds it,
 // UpWithGate rounds the up value to bf16 and multiplies by silu of the gate (gguf_tile.h:6-14).

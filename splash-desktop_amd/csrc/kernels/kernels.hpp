@@ -85,13 +85,16 @@ hipError_t launch_mlx_repack(uint32_t fmt, const uint32_t *weight, const uint16_
 
 // MoE.
 hipError_t launch_moe_route_select(const float *scores, uint32_t score_stride, uint32_t *selected,
-                                   float *routing_weights, const SqMoeRouteParams &params, hipStream_t stream);
+                                   float *routing_weights, const SqMoeRouteParams &params, const uint16_t *input,
+                                   const float *shared_gate, uint32_t router, uint32_t shared, hipStream_t stream);
 hipError_t launch_moe_group(const uint32_t *selected, SqMoeTileDescriptor *tiles, SqMoeTileCount *tile_count,
-                            uint32_t *grouped_routes, uint32_t *route_rows, uint32_t max_tiles,
-                            const SqMoeGroupParams &params, hipStream_t stream);
-// An expert pass over the grouped rows: workgroup (64-column tile, tile) runs when the tile is its expert's first and
-// walks all the expert's rows. gate_up: gate and up of each expert in one pass over input rows routes[row] / top_k,
-// out = bf16(bf16(up) silu(bf16(gate))); else one tensor over grouped input rows.
+                            uint32_t *grouped_routes, uint32_t *route_rows, const SqMoeGroupParams &params,
+                            uint32_t shared, hipStream_t stream);
+// An expert pass over the grouped rows, tile by tile: gate_up: gate and up of each tile's expert in one pass over
+// input rows routes[row] / routes_per_row, out = bf16(bf16(up) silu(bf16(gate))); else one tensor over the grouped
+// input rows. Routed tiles (expert < experts) read the routed planes, expert e's rows from slots[e] * output_size
+// on; shared tiles (expert experts + s) the shared planes, slice s's rows s * output_size on. `mode` picks the
+// tiles a launch runs: 0 routed, 1 shared, 2 both (one format).
 struct MoeExpertArgs {
   const uint16_t *input;        // gate/up: the step's rows [rows][K]; down: grouped rows [tiles * tile_rows][K]
   const uint32_t *routes;       // gate/up: the route of each grouped row (~0u padding)
@@ -99,9 +102,11 @@ struct MoeExpertArgs {
   const SqMoeTileCount *tile_count;
   const uint8_t *plane0[2];     // gate (or the single pass's weights), up
   const uint8_t *meta[2];
-  const uint32_t *slots;        // routed expert e's planes from row slots[e] * output_size
+  const uint8_t *shared_plane0[2];
+  const uint8_t *shared_meta[2];
+  const uint32_t *slots;
   uint16_t *output;             // [tiles * tile_rows][output_size]
-  uint32_t K, output_size, tile_rows, max_tiles, fmt, gate_up, top_k;
+  uint32_t K, output_size, tile_rows, max_tiles, fmt, gate_up, routes_per_row, experts, mode;
 };
 hipError_t launch_moe_expert(const MoeExpertArgs &args, hipStream_t stream);
 hipError_t launch_moe_combine(const uint16_t *expert_output, const uint32_t *route_rows,

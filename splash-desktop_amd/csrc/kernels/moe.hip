@@ -1,4 +1,4 @@
-// MoE routed experts: top-k route select, grouping of routes into expert tiles, the expert passes (gate and up in
+// MoE block: top-k route select and shared-slice weights, grouping of routes into expert tiles, the expert passes (gate and up in
 // one pass, then down) and the combine (reference: kernels/shared/moe.metal:23-162,175-331,480-505 and
 // kernels/shared/moe_gguf.metal:21-206).
 //
@@ -11,13 +11,32 @@
 namespace sq::kern {
 namespace {
 
-// One wave per row. Rank by rank, the highest remaining score wins, the lowest expert id among equal scores
-// (moe.metal:69-93); then weight_r = 2^((s_r - s_0) log2 e) / sum_o 2^((s_o - s_0) log2 e) over the selected k,
-// summed in rank order (moe.metal:95-104).
+// One wave per row (moe.metal:23-112). Rank by rank, the highest remaining score wins, the lowest expert id among
+// equal scores; the router then weights the top_k routes in rank order: Softmax weight_r =
+// 2^((s_r - s_0) log2 e) / sum_o 2^((s_o - s_0) log2 e), SigmoidNormalized weight_r = sigmoid(s_r) /
+// (sum_o sigmoid(s_o) + 1e-20). The row's routes top_k .. top_k + shared - 1 are the shared expert's slices (ids
+// experts on), each weighted by sigmoid(x . g) of the block's fp32 scalar gate g (gated) or by 1.
 __global__ __launch_bounds__(64) void route_select_kernel(const float *scores, uint32_t stride, uint32_t *selected,
-                                                          float *weights, SqMoeRouteParams p) {
+                                                          float *weights, SqMoeRouteParams p, const uint16_t *input,
+                                                          const float *shared_gate, uint32_t router, uint32_t shared) {
   constexpr int kPer = SQ_MOE_WIDE_EXPERT_SLOTS / 64;
-  const uint32_t row = blockIdx.x, lane = threadIdx.x;
+  const uint32_t row = blockIdx.x, lane = threadIdx.x, per_row = p.top_k + shared;
+  const size_t base = (size_t)row * per_row;
+  if (shared) {
+    float gate = 1.0f;
+    if (shared_gate) {
+      float dot = 0.0f;
+      for (uint32_t d = lane; d < p.input_size; d += 64)
+        dot = fmaf(bf16_to_f32(input[(size_t)row * p.input_size + d]), shared_gate[d], dot);
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) dot += __shfl_xor(dot, m);
+      gate = sigmoid(dot);
+    }
+    if (lane < shared) {
+      selected[base + p.top_k + lane] = p.experts + lane;
+      weights[base + p.top_k + lane] = gate;
+    }
+  }
   float v[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
@@ -41,35 +60,43 @@ __global__ __launch_bounds__(64) void route_select_kernel(const float *scores, u
     for (int m = 32; m >= 1; m >>= 1) winner = min(winner, (uint32_t)__shfl_xor((int)winner, m));
     if (candidate == winner && at >= 0) taken |= 1u << at;
     if (lane == 0) {
-      selected[(size_t)row * p.top_k + rank] = winner;
+      selected[base + rank] = winner;
       ordered[rank] = top;
     }
   }
   __syncthreads();
   for (uint32_t rank = lane; rank < p.top_k; rank += 64) {
     float denominator = 0.0f;
-    for (uint32_t o = 0; o < p.top_k; ++o) denominator += exp2f((ordered[o] - ordered[0]) * 1.44269504089f);
-    weights[(size_t)row * p.top_k + rank] = exp2f((ordered[rank] - ordered[0]) * 1.44269504089f) / denominator;
+    if (router == SQ_MOE_ROUTER_SOFTMAX) {
+      for (uint32_t o = 0; o < p.top_k; ++o) denominator += exp2f((ordered[o] - ordered[0]) * 1.44269504089f);
+      weights[base + rank] = exp2f((ordered[rank] - ordered[0]) * 1.44269504089f) / denominator;
+    } else {
+      for (uint32_t o = 0; o < p.top_k; ++o) denominator += sigmoid(ordered[o]);
+      weights[base + rank] = sigmoid(ordered[rank]) / (denominator + 1e-20f);
+    }
   }
 }
 
-// One workgroup groups every route (moe.metal:184-278, routed slices only): count per expert, exclusive prefix of
-// the experts' tiles in expert order, tile descriptors, then each route's grouped row. Routes of an expert take its
-// rows in route order (a bitmap of the rows that route to each expert, 512 rows at a time, gives a route's rank),
-// so the grouping, and every expert pass after it, is deterministic.
+// One workgroup groups every route (moe.metal:184-278): count per expert, exclusive prefix of the experts' tiles in
+// expert order, tile descriptors, then each routed route's grouped row. Routes of an expert take its rows in route
+// order (a bitmap of the rows that route to each expert, 512 rows at a time, gives a route's rank), so the
+// grouping, and every expert pass after it, is deterministic. The `shared` slices' tiles follow the routed tiles,
+// slice after slice, each slice's holding every row in order (route row * (top_k + shared) + top_k + slice).
 __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, SqMoeTileDescriptor *tiles,
                                                     SqMoeTileCount *tile_count, uint32_t *grouped_routes,
-                                                    uint32_t *route_rows, SqMoeGroupParams p) {
+                                                    uint32_t *route_rows, SqMoeGroupParams p, uint32_t shared) {
   constexpr uint32_t kChunk = 512, kWords = kChunk / 32;
   __shared__ uint32_t counts[SQ_MOE_WIDE_EXPERT_SLOTS], offsets[SQ_MOE_WIDE_EXPERT_SLOTS],
       running[SQ_MOE_WIDE_EXPERT_SLOTS];
   __shared__ uint32_t bits[SQ_MOE_WIDE_EXPERT_SLOTS * kWords], prefix[SQ_MOE_WIDE_EXPERT_SLOTS * kWords];
   __shared__ uint32_t total;
-  const uint32_t tid = threadIdx.x, routes = p.rows * p.top_k, tr = p.tile_rows;
+  const uint32_t tid = threadIdx.x, per_row = p.top_k + shared, tr = p.tile_rows;
+  // Routed route k of row r: selected[r * per_row + k].
+  const auto route_of = [&](uint32_t i) { return i / p.top_k * per_row + i % p.top_k; };
   counts[tid] = 0;
   running[tid] = 0;
   __syncthreads();
-  for (uint32_t r = tid; r < routes; r += 512) atomicAdd(&counts[selected[r]], 1u);
+  for (uint32_t i = tid; i < p.rows * p.top_k; i += 512) atomicAdd(&counts[selected[route_of(i)]], 1u);
   __syncthreads();
   {
     // Exclusive prefix of the experts' tile counts: a scan within each wave, then over the eight wave totals.
@@ -97,10 +124,10 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
   for (uint32_t chunk = 0; chunk < p.rows; chunk += kChunk) {
     for (uint32_t i = tid; i < p.experts * kWords; i += 512) bits[i] = 0;
     __syncthreads();
-    const uint32_t r0 = chunk * p.top_k, r1 = min(p.rows, chunk + kChunk) * p.top_k;
-    for (uint32_t r = r0 + tid; r < r1; r += 512) {
-      const uint32_t local = r / p.top_k - chunk;
-      atomicOr(&bits[selected[r] * kWords + local / 32], 1u << (local % 32));
+    const uint32_t i0 = chunk * p.top_k, i1 = min(p.rows, chunk + kChunk) * p.top_k;
+    for (uint32_t i = i0 + tid; i < i1; i += 512) {
+      const uint32_t local = i / p.top_k - chunk;
+      atomicOr(&bits[selected[route_of(i)] * kWords + local / 32], 1u << (local % 32));
     }
     __syncthreads();
     // Rows of the chunk before word w that route to expert e: one pass per expert, then each route's rank is a
@@ -113,8 +140,8 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
       }
     }
     __syncthreads();
-    for (uint32_t r = r0 + tid; r < r1; r += 512) {
-      const uint32_t e = selected[r], local = r / p.top_k - chunk;
+    for (uint32_t i = i0 + tid; i < i1; i += 512) {
+      const uint32_t r = route_of(i), e = selected[r], local = i / p.top_k - chunk;
       uint32_t rank = running[e] + prefix[e * kWords + local / 32];
       rank += __popc(bits[e * kWords + local / 32] & ((1u << (local % 32)) - 1u));
       const uint32_t row = offsets[e] * tr + rank;
@@ -126,8 +153,26 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
       for (uint32_t w = 0; w < kWords; ++w) running[tid] += __popc(bits[tid * kWords + w]);
     __syncthreads();
   }
-  if (tid == 0)
-    *tile_count = SqMoeTileCount{total, {p.gate_up_columns, total, 1}, {p.down_columns, total, 1}, {0, 0, 0}};
+  // Shared slices (moe.metal:245-270): slice s's tiles after slice s - 1's, each of every row in order.
+  const uint32_t shared_tiles = (p.rows + tr - 1) / tr, shared_base = total * tr;
+  for (uint32_t i = tid; i < shared * shared_tiles; i += 512) {
+    const uint32_t slice = i / shared_tiles, t = i % shared_tiles;
+    tiles[total + i] = SqMoeTileDescriptor{p.experts + slice, min(tr, p.rows - t * tr)};
+  }
+  for (uint32_t i = tid; i < shared * shared_tiles * tr; i += 512) {
+    const uint32_t slice = i / (shared_tiles * tr), row = i % (shared_tiles * tr);
+    if (row < p.rows) {
+      const uint32_t r = row * per_row + p.top_k + slice;
+      grouped_routes[shared_base + i] = r;
+      route_rows[r] = shared_base + i;
+    } else {
+      grouped_routes[shared_base + i] = ~0u;
+    }
+  }
+  if (tid == 0) {
+    const uint32_t live = total + shared * shared_tiles;
+    *tile_count = SqMoeTileCount{live, {p.gate_up_columns, live, 1}, {p.down_columns, live, 1}, {0, 0, 0}};
+  }
 }
 
 // Workgroup (four 64-column tiles, expert tile): wave w streams column tile 4 blockIdx.x + w of the tile's expert
@@ -143,20 +188,23 @@ __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDes
   const uint32_t column_tiles = a.output_size / 64;
   const uint32_t rows = d.rows, first_row = tile * a.tile_rows;
   const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
-  const uint32_t G = a.K >> 5, units = G / F::UNIT;
-  const uint32_t ptile = a.slots[d.expert] * column_tiles + ct;
+  const uint32_t G = a.K >> 5;
+  // The plane tile: routed expert e's from tile slots[e] of its projection on, shared slice s's from tile s of the
+  // shared segment on.
+  const bool shared = d.expert >= a.experts;
+  const uint32_t ptile = (shared ? d.expert - a.experts : a.slots[d.expert]) * column_tiles + ct;
   const uint8_t *plane[NT], *meta[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
-    plane[n] = a.plane0[n] + ((size_t)ptile * G * 64 + lane) * 16;
-    meta[n] = a.meta[n] + ((size_t)ptile * units * 64 + j) * F::META;
+    plane[n] = (shared ? a.shared_plane0[n] : a.plane0[n]) + ((size_t)ptile * G * 64 + lane) * 16;
+    meta[n] = (shared ? a.shared_meta[n] : a.meta[n]) + ((size_t)ptile * (G / F::UNIT) * 64 + j) * F::META;
   }
   // Lane (j, q) of row block b reads row 16 b + j (row 0 past the tile's rows: nothing stores those results).
   const uint16_t *xrow[MB];
 #pragma unroll
   for (int b = 0; b < MB; ++b) {
     const uint32_t r = 16u * b + j < rows ? 16u * b + j : 0u;
-    const uint32_t source = NT == 2 ? a.routes[first_row + r] / a.top_k : first_row + r;
+    const uint32_t source = NT == 2 ? a.routes[first_row + r] / a.routes_per_row : first_row + r;
     xrow[b] = a.input + (size_t)source * a.K + 4 * q;
   }
   float acc[NT][4][MB][4];
@@ -191,6 +239,7 @@ __global__ __launch_bounds__(256) void expert_kernel(MoeExpertArgs a) {
   const uint32_t ct = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (ct >= a.output_size / 64) return;
   const SqMoeTileDescriptor d = a.tiles[tile];
+  if (a.mode != 2 && (d.expert >= a.experts) != (a.mode == 1)) return;
   if (MB == 1 || d.rows <= 16) expert_tile<FMT, 1, NT>(a, d, tile, ct);
   else expert_tile<FMT, MB, NT>(a, d, tile, ct);
 }
@@ -242,17 +291,18 @@ hipError_t launch_expert_format(const MoeExpertArgs &a, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_moe_route_select(const float *scores, uint32_t stride, uint32_t *selected, float *weights,
-                                   const SqMoeRouteParams &p, hipStream_t stream) {
-  hipLaunchKernelGGL(route_select_kernel, dim3(p.rows), dim3(64), 0, stream, scores, stride, selected, weights, p);
+                                   const SqMoeRouteParams &p, const uint16_t *input, const float *shared_gate,
+                                   uint32_t router, uint32_t shared, hipStream_t stream) {
+  hipLaunchKernelGGL(route_select_kernel, dim3(p.rows), dim3(64), 0, stream, scores, stride, selected, weights, p,
+                     input, shared_gate, router, shared);
   return hipGetLastError();
 }
 
 hipError_t launch_moe_group(const uint32_t *selected, SqMoeTileDescriptor *tiles, SqMoeTileCount *tile_count,
-                            uint32_t *grouped_routes, uint32_t *route_rows, uint32_t max_tiles,
-                            const SqMoeGroupParams &p, hipStream_t stream) {
-  (void)max_tiles;
+                            uint32_t *grouped_routes, uint32_t *route_rows, const SqMoeGroupParams &p,
+                            uint32_t shared, hipStream_t stream) {
   hipLaunchKernelGGL(group_kernel, dim3(1), dim3(512), 0, stream, selected, tiles, tile_count, grouped_routes,
-                     route_rows, p);
+                     route_rows, p, shared);
   return hipGetLastError();
 }
 

@@ -77,9 +77,12 @@ class Device(Structure):
     _fields_ = [("compute_units", c_uint32)]
 
 
+ROUTER_SOFTMAX, ROUTER_SIGMOID_NORMALIZED = 0, 1
+
+
 class MoeShape(Structure):
     _fields_ = [(n, c_uint32) for n in ("hidden_size", "experts", "experts_per_token", "expert_intermediate_size",
-                                        "expert_format")]
+                                        "expert_format", "router", "shared_slices", "shared_gated")]
 
 
 _MOE_WORKSPACE = ("selected_experts", "routing_weights", "tile_descriptors", "tile_count", "grouped_routes",
@@ -96,7 +99,9 @@ class MoePlan(Structure):
 
 
 class MoeWeights(Structure):
-    _fields_ = [("gate", Segment), ("up", Segment), ("down", Segment), ("slot_table", Buffer), ("slots", c_uint32)]
+    _fields_ = [("gate", Segment), ("up", Segment), ("down", Segment), ("slot_table", Buffer), ("slots", c_uint32),
+                ("shared_gate", Segment), ("shared_up", Segment), ("shared_down", Segment),
+                ("shared_scalar_gate", Buffer)]
 
 
 class MoeScratch(Structure):

@@ -206,6 +206,28 @@ def test_moe_plans_and_workspace():
         sq.call("sq_moe_decode_plan", sq.byref(shape), 33, sq.byref(plan))
 
 
+def test_moe_shared_slice_plans():
+    """Shared slices add their routes to every row and one tile per tile_rows rows each (MoE.hpp:200-205); only the
+    compiled routings plan (kCompiledMoeRoutings, MoE.hpp:34-46)."""
+    plan = sq.MoePlan()
+    gated = sq.MoeShape(2048, 128, 8, 768, sq.FMT_AF4G64, sq.ROUTER_SOFTMAX, 1, 1)
+    sq.call("sq_moe_prefill_plan", sq.byref(gated), 500, sq.byref(plan))
+    assert plan.maximum_tiles == min(500 * 8 // 32 + 128, 500 * 8) + 16
+    assert plan.workspace.selected_experts == 500 * 9 * 4 and plan.workspace.route_rows == 500 * 9 * 4
+    assert plan.workspace.expert_output == plan.maximum_tiles * 32 * 2048 * 2
+    two = sq.MoeShape(2048, 64, 6, 512, sq.FMT_AF4G64, sq.ROUTER_SIGMOID_NORMALIZED, 2, 0)
+    sq.call("sq_moe_decode_plan", sq.byref(two), 3, sq.byref(plan))
+    assert plan.tile_rows == 8 and plan.maximum_tiles == min(3 * 6 // 8 + 64, 18) + 2
+    for router, slices, gate in ((sq.ROUTER_SOFTMAX, 2, 0), (sq.ROUTER_SOFTMAX, 1, 0),
+                                 (sq.ROUTER_SIGMOID_NORMALIZED, 2, 1), (sq.ROUTER_SIGMOID_NORMALIZED, 0, 0)):
+        with pytest.raises(sq.InvalidArgument, match="invalid MoE workspace shape"):
+            sq.call("sq_moe_prefill_plan", sq.byref(sq.MoeShape(2048, 64, 6, 512, sq.FMT_AF4G64, router, slices, gate)),
+                    8, sq.byref(plan))
+    with pytest.raises(sq.InvalidArgument, match="unknown MoE router"):
+        sq.call("sq_moe_prefill_plan", sq.byref(sq.MoeShape(2048, 64, 6, 512, sq.FMT_AF4G64, 2, 0, 0)), 8,
+                sq.byref(plan))
+
+
 def test_cxx_face_plans_and_throws(tmp_path):
     """include/splash_q4.hpp compiles as C++17, plans through the library and turns a refused plan back into the
     reference's std::invalid_argument (host only)."""

@@ -1,7 +1,8 @@
-"""MoE routed experts through the C ABI against the oracle (kernels/shared/moe.metal, moe_gguf.metal): the top-k
-selection bit for bit (ties to the lower expert id), the renormalised softmax weights, the grouping (tiles in expert
-order, each expert's routes in route order, padding marked ~0u), and the combined output against an fp64 SwiGLU of
-every route with the kernels' bf16 rounding points, within BASELINE's tolerances."""
+"""MoE blocks through the C ABI against the oracle (kernels/shared/moe.metal, moe_gguf.metal): the top-k selection
+bit for bit (ties to the lower expert id), the router's weights (renormalised softmax, or sigmoids over their sum)
+and the shared slices' (sigmoid of the scalar gate's product, or 1), the grouping (tiles in expert order, each
+expert's routes in route order, then the shared slices' tiles, padding marked ~0u), and the combined output against
+an fp64 SwiGLU of every route with the kernels' bf16 rounding points, within BASELINE's tolerances."""
 import numpy as np
 import pytest
 
@@ -13,34 +14,65 @@ from splash_q4 import synthetic
 pytestmark = pytest.mark.gpu
 
 
+def native_rows(rng, fmt, n, k):
+    if fmt == oracle.FMT_Q4K:
+        return synthetic.q4k_native(rng, n, k).ravel()
+    return affine_native(rng, fmt, n, k)
+
+
 class Block:
-    def __init__(self, rng, experts, hidden, intermediate, fmt=oracle.FMT_AF4G64):
+    """Routed experts in `fmt`; `shared` shared slices with gate and up in shared_fmt and down in down_fmt, laid out
+    as the reference's BlockExpertProjection (slice s's rows s * N on); a scalar gate when `gated`."""
+
+    def __init__(self, rng, experts, hidden, intermediate, fmt=oracle.FMT_AF4G64, shared=0, gated=False,
+                 router=oracle.ROUTER_SOFTMAX, shared_fmt=None, down_fmt=None):
         self.e, self.h, self.i, self.fmt = experts, hidden, intermediate, fmt
+        self.shared, self.gated, self.router = shared, gated, router
         self.parts = {}
-        for name, n, k in (("gate", experts * intermediate, hidden), ("up", experts * intermediate, hidden),
-                           ("down", experts * hidden, intermediate)):
-            native = affine_native(rng, fmt, n, k)
-            p0, meta, values = oracle.repack(fmt, native, n, k)
-            self.parts[name] = (to_device(p0), to_device(meta), values, n, k)
+        plan = [("gate", experts * intermediate, hidden, fmt), ("up", experts * intermediate, hidden, fmt),
+                ("down", experts * hidden, intermediate, fmt)]
+        if shared:
+            sf = fmt if shared_fmt is None else shared_fmt
+            df = sf if down_fmt is None else down_fmt
+            plan += [("shared_gate", shared * intermediate, hidden, sf), ("shared_up", shared * intermediate, hidden, sf),
+                     ("shared_down", shared * hidden, intermediate, df)]
+        for name, n, k, f in plan:
+            p0, meta, values = oracle.repack(f, native_rows(rng, f, n, k), n, k)
+            self.parts[name] = (to_device(p0), to_device(meta), values, n, k, f)
         self.slots = to_device(np.arange(experts, dtype=np.uint32))
+        self.scalar_gate = rng.normal(0, 0.05, hidden).astype(np.float32) if gated else None
 
     def segment(self, name):
-        p0, meta, _, n, k = self.parts[name]
-        return sq.segment(self.fmt, n, k, p0, meta)
+        if name not in self.parts:
+            return sq.Segment()
+        p0, meta, _, n, k, f = self.parts[name]
+        return sq.segment(f, n, k, p0, meta)
 
     def weights(self):
-        return sq.MoeWeights(self.segment("gate"), self.segment("up"), self.segment("down"), sq.view(self.slots), self.e)
+        self._gate = to_device(self.scalar_gate) if self.gated else None
+        return sq.MoeWeights(self.segment("gate"), self.segment("up"), self.segment("down"), sq.view(self.slots), self.e,
+                             self.segment("shared_gate"), self.segment("shared_up"), self.segment("shared_down"),
+                             sq.view(self._gate))
 
     def values(self, name, expert):
-        _, _, v, n, k = self.parts[name]
-        rows = self.i if name != "down" else self.h
+        """Expert `expert`'s rows of projection `name`; ids from the expert count on are the shared slices."""
+        if expert >= self.e:
+            name, expert = "shared_" + name, expert - self.e
+        v = self.parts[name][2]
+        rows = self.i if name.endswith("gate") or name.endswith("up") else self.h
         return v[expert * rows:(expert + 1) * rows]
+
+    def shape(self, top_k):
+        return sq.MoeShape(self.h, self.e, top_k, self.i, self.fmt, self.router, self.shared, int(self.gated))
+
+    def route(self, x, scores, top_k):
+        return oracle.route_select(scores, top_k, self.router, self.shared, x, self.scalar_gate)
 
 
 def run_moe(block, x, scores, top_k, residual=None, phase="prefill"):
     t = torch()
     rows = x.shape[0]
-    shape = sq.MoeShape(block.h, block.e, top_k, block.i, block.fmt)
+    shape = block.shape(top_k)
     plan = sq.MoePlan()
     sq.call("sq_moe_prefill_plan" if phase == "prefill" else "sq_moe_decode_plan", sq.byref(shape), rows, sq.byref(plan))
     scratch = {}
@@ -84,17 +116,24 @@ def test_moe_routed_experts(rows, experts, top_k):
     scores = synthetic.router_logits(rng, rows, experts)
     scores[0, 3] = scores[0, 5] = scores[0].max() + 1   # a tie: the lower id ranks first
     residual = synthetic.bf16_bits(rng.uniform(-4, 4, (rows, hidden)).astype(np.float32))
-    plan, scratch, got = run_moe(block, x, scores, top_k, residual)
-    routes = rows * top_k
-    sel_gpu = to_host(scratch["selected_experts"], np.uint32)[:routes].reshape(rows, top_k)
-    w_gpu = scratch["routing_weights"].cpu().numpy().view(np.float32)[:routes].reshape(rows, top_k)
-    selected, weights = oracle.route_select(scores, top_k)
+    selected = check_block(block, x, scores, top_k, residual)
+    assert selected[0, 0] == 3 and selected[0, 1] == 5
+
+
+def check_block(block, x, scores, top_k, residual, phase="prefill", weight_rtol=2e-6):
+    """Runs the block and checks selection, weights, grouping and output against the oracle; returns the selection."""
+    rows = x.shape[0]
+    plan, scratch, got = run_moe(block, x, scores, top_k, residual, phase)
+    per_row = top_k + block.shared
+    routes = rows * per_row
+    sel_gpu = to_host(scratch["selected_experts"], np.uint32)[:routes].reshape(rows, per_row)
+    w_gpu = scratch["routing_weights"].cpu().numpy().view(np.float32)[:routes].reshape(rows, per_row)
+    selected, weights = block.route(x, scores, top_k)
     assert np.array_equal(sel_gpu, selected)
-    assert sel_gpu[0, 0] == 3 and sel_gpu[0, 1] == 5
-    assert np.allclose(w_gpu, weights, rtol=2e-6, atol=1e-7)
-    tiles, grouped, route_rows = oracle.group_routes(selected, experts, plan.tile_rows)
+    assert np.allclose(w_gpu, weights, rtol=weight_rtol, atol=1e-7)
+    tiles, grouped, route_rows = oracle.group_routes(selected, block.e, plan.tile_rows, block.shared)
     count = to_host(scratch["tile_count"], np.uint32)
-    assert count[0] == tiles.shape[0]
+    assert count[0] == tiles.shape[0] <= plan.maximum_tiles
     assert np.array_equal(to_host(scratch["tile_descriptors"], np.uint32)[: 2 * count[0]].reshape(-1, 2), tiles)
     assert np.array_equal(to_host(scratch["grouped_routes"], np.uint32)[: grouped.size], grouped)
     assert np.array_equal(to_host(scratch["route_rows"], np.uint32)[:routes], route_rows)
@@ -103,6 +142,46 @@ def test_moe_routed_experts(rows, experts, top_k):
     err = gotf - want
     assert np.linalg.norm(err) / np.linalg.norm(want) <= 1e-2
     assert np.all(np.abs(err) <= np.ldexp(np.abs(want).max(axis=1, keepdims=True), -6))
+    return sel_gpu
+
+
+@pytest.mark.parametrize("fmt", [oracle.FMT_Q4K, oracle.FMT_AF4G32])
+def test_moe_routed_formats(fmt):
+    rng = np.random.default_rng(900 + fmt)
+    block = Block(rng, 16, 512, 256, fmt=fmt)
+    x = synthetic.activations(rng, 40, 512)
+    scores = synthetic.router_logits(rng, 40, 16)
+    check_block(block, x, scores, 4, None)
+
+
+@pytest.mark.parametrize("rows,phase", [(48, "prefill"), (5, "decode")])
+def test_moe_gated_shared_slice(rows, phase):
+    """The reference's default routing: softmax over the top 4, one shared slice weighted sigmoid(x . g)."""
+    rng = np.random.default_rng(500 + rows)
+    block = Block(rng, 32, 512, 128, shared=1, gated=True)
+    x = synthetic.activations(rng, rows, 512)
+    scores = synthetic.router_logits(rng, rows, 32)
+    residual = synthetic.bf16_bits(rng.uniform(-2, 2, (rows, 512)).astype(np.float32))
+    check_block(block, x, scores, 4, residual, phase)
+
+
+def test_moe_sigmoid_router_two_ungated_slices():
+    """A sigmoid-normalised router with two ungated shared slices (weight 1 each), the second compiled routing."""
+    rng = np.random.default_rng(600)
+    block = Block(rng, 64, 512, 128, shared=2, router=oracle.ROUTER_SIGMOID_NORMALIZED)
+    x = synthetic.activations(rng, 40, 512)
+    scores = synthetic.router_logits(rng, 40, 64)
+    check_block(block, x, scores, 6, None)
+
+
+@pytest.mark.parametrize("shared_fmt,down_fmt", [(oracle.FMT_Q4K, oracle.FMT_Q4K), (oracle.FMT_AF4G128, oracle.FMT_AF4G32)])
+def test_moe_shared_slices_in_their_own_formats(shared_fmt, down_fmt):
+    """Shared gate/up and down in formats other than the routed experts' take launches of their own."""
+    rng = np.random.default_rng(700 + shared_fmt + down_fmt)
+    block = Block(rng, 16, 512, 256, shared=1, gated=True, shared_fmt=shared_fmt, down_fmt=down_fmt)
+    x = synthetic.activations(rng, 70, 512)
+    scores = synthetic.router_logits(rng, 70, 16)
+    check_block(block, x, scores, 2, None)
 
 
 def test_moe_decode_rows():

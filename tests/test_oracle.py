@@ -229,6 +229,57 @@ def test_route_weights_closed_form():
     assert np.allclose(weights[0], [4 / 7, 2 / 7, 1 / 7], rtol=1e-6)
 
 
+def test_sigmoid_router_closed_form():
+    """SigmoidNormalized: scores ln 3, 0, -ln 3 have sigmoids 3/4, 1/2, 1/4, so weights 1/2, 1/3, 1/6 in rank order;
+    equal scores give 1/k each."""
+    scores = np.array([[-np.log(3.0), -9.0, np.log(3.0), 0.0],
+                       [0.7, 0.7, 0.7, 0.7]], np.float32)
+    selected, weights = oracle.route_select(scores, 3, oracle.ROUTER_SIGMOID_NORMALIZED)
+    assert selected.tolist() == [[2, 3, 0], [0, 1, 2]]
+    assert np.allclose(weights[0], [1 / 2, 1 / 3, 1 / 6], rtol=1e-6)
+    assert np.allclose(weights[1], 1 / 3, rtol=1e-12)
+
+
+def test_shared_slice_weights():
+    """Shared slices follow the routed routes with ids experts.. and weight sigmoid(x . g): x . g = 0 gives 1/2 and
+    x . g = ln 3 gives 3/4; ungated slices weigh 1."""
+    scores = np.array([[0.0, 1.0, 2.0], [2.0, 1.0, 0.0]], np.float32)
+    x = (np.array([[1.0, -1.0, 0.0, 0.0], [0.5, 0.0, 0.0, 0.0]], np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    g = np.array([2.0, 2.0, 0.0, 0.0], np.float32)
+    g[0] = np.float32(2 * np.log(3.0))   # row 1: 0.5 * 2 ln 3 = ln 3
+    g[1] = g[0]                           # row 0: 1 * g0 - 1 * g1 = 0
+    selected, weights = oracle.route_select(scores, 2, oracle.ROUTER_SOFTMAX, 1, x, g)
+    assert selected.tolist() == [[2, 1, 3], [0, 1, 3]]
+    assert np.allclose(weights[:, 2], [0.5, 0.75], rtol=1e-6)
+    assert np.allclose(weights[:, :2].sum(axis=1), 1.0)
+    selected, weights = oracle.route_select(scores, 1, oracle.ROUTER_SIGMOID_NORMALIZED, 2)
+    assert selected.tolist() == [[2, 3, 4], [0, 3, 4]]
+    assert np.all(weights[:, 1:] == 1.0)
+
+
+def test_group_routes_with_shared_slices():
+    """The shared slices' tiles follow the routed tiles, slice after slice, each of every row in order; every route
+    (routed and shared) owns exactly one grouped row."""
+    rng = np.random.default_rng(9)
+    rows, experts, top_k, shared, tile_rows = 21, 8, 2, 2, 8
+    scores = rng.standard_normal((rows, experts)).astype(np.float32)
+    selected, _ = oracle.route_select(scores, top_k, oracle.ROUTER_SIGMOID_NORMALIZED, shared)
+    tiles, grouped, route_rows = oracle.group_routes(selected, experts, tile_rows, shared)
+    routed = sum((c + tile_rows - 1) // tile_rows
+                 for c in np.bincount(selected[:, :top_k].ravel(), minlength=experts))
+    shared_tiles = -(-rows // tile_rows)
+    assert tiles.shape[0] == routed + shared * shared_tiles
+    assert tiles[routed:, 0].tolist() == [experts + s for s in range(shared) for _ in range(shared_tiles)]
+    assert tiles[routed:, 1].tolist() == [8, 8, 5] * shared
+    for r, g in enumerate(route_rows):
+        assert grouped[g] == r
+        assert tiles[g // tile_rows, 0] == selected.ravel()[r]
+    for s in range(shared):
+        base = (routed + s * shared_tiles) * tile_rows
+        assert grouped[base:base + rows].tolist() == [row * (top_k + shared) + top_k + s for row in range(rows)]
+    assert np.count_nonzero(grouped == 0xFFFFFFFF) == tiles.shape[0] * tile_rows - rows * (top_k + shared)
+
+
 @pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K])
 def test_cpu_baseline_matches_fp64(fmt):
     """The CPU baseline (threaded fp32 sums of the dequantised weights) agrees with the fp64 projection within the
