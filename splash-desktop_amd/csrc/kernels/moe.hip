@@ -1,6 +1,6 @@
-// MoE block: top-k route select and shared-slice weights, grouping of routes into expert tiles, the expert passes (gate and up in
-// one pass, then down) and the combine (reference: kernels/shared/moe.metal:23-162,175-331,480-505 and
-// kernels/shared/moe_gguf.metal:21-206).
+// MoE block: top-k route select and shared-slice weights, grouping of routes into expert tiles, the expert passes
+// (gate and up in one pass, then down) and the combine (reference: kernels/shared/moe.metal:23-162,175-331,480-505
+// and kernels/shared/moe_gguf.metal:21-206).
 //
 // CDNA4 mapping. Each expert pass is the decode row tile's exact-operand inner loop (rowtile.hpp) per expert tile:
 // a wave streams one 64-column plane tile of its expert over all of K against the tile's (at most 32) grouped
