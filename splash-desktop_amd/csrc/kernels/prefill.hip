@@ -267,6 +267,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     }
   };
 
+  // Copy c of step `step`'s copies: c < BM / 32 the activation rows of step + 2, then step + 3's two code groups
+  // and its meta.
+  const auto copy_one = [&](uint32_t step, int c) __attribute__((always_inline)) {
+    if (c < BM / 32) {
+      const uint8_t *from = (const uint8_t *)a.half_input + (size_t)min(step + 2, steps - 1) * BK * 2;
+      uint8_t *stage = lds + ((step + 2) % kStages) * kStage;
+      copy_to_lds<16>(from + aoff[c], stage + (kRowsPerWave * wave + 8 * c) * kRowBytes);
+      return;
+    }
+    const uint32_t from = min(step + 3, steps - 1), k = c - BM / 32;
+    uint8_t *dst = wave_slot + ((step + 3) % kSlots) * kSlotBytes;
+    if (k < 2) copy_to_lds<16>(bplane + (size_t)(2 * from + k) * 1024, dst + k * 1024);
+    else if constexpr (FMT == SQ_FMT_AF4G32)
+      copy_to_lds<4>(bmeta + (size_t)(2 * from + k - 2) * 256, dst + 2048 + (k - 2) * 256);
+    else
+      copy_to_lds<F::META>(bmeta + (size_t)(2 * from / F::UNIT) * 64 * F::META, dst + 2048);
+  };
+
   f32x4 acc[MI][4];
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi)
@@ -337,56 +355,66 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   read_b(0, 1);
   dequant_group(0, 0);
 
-  // Step s copies step s + 2's activations into stage (s + 2) % 3 and step s + 3's codes into slot (s + 3) % 4. It
-  // dequantises its own group 1 during its first half and step s + 1's group 0 during its second half, from words
-  // read half a step earlier (each half reads the words the next half dequantises: step s + 1's slot has been in
-  // LDS since the last barrier). Before the barrier it waits for everything but its own copies, so step s + 1's
-  // activations and step s + 2's codes are in.
-  // The activation fragments go through registers in batches of four blocks (16 MFMAs), two batches in flight:
-  // with the copies to LDS outstanding the compiler can only wait for all LDS reads at once, so each batch's reads
-  // are issued a whole batch before their MFMAs.
+  // Step s copies step s + 2's activations into stage (s + 2) % 3 and step s + 3's codes into slot (s + 3) % 4,
+  // one copy instruction before each of its batches in turn (a burst of them at the top of the step stalls the wave
+  // on the address unit). It dequantises its own group 1 during its first half and step s + 1's group 0 during its
+  // second half, from words read half a step earlier (each half reads the words the next half dequantises: step
+  // s + 1's slot has been in LDS since the last barrier). Before the barrier it waits for everything but its own
+  // copies, so step s + 1's activations and step s + 2's codes are in.
+  // The activation fragments go through registers in batches of four blocks (16 MFMAs), two batches in flight.
+  // With copies to LDS outstanding the compiler can only wait for all LDS reads at once, so each batch waits for
+  // its own reads (issued a batch earlier) before it issues the next batch's. A step's last batch runs after the
+  // barrier, while the next step's first reads are in flight.
   constexpr int kGroups = 2 * MI, kBatch = 4, kBatches = kGroups / kBatch, kSlotsHalf = 4 * MI;
-  for (uint32_t step = 0; step < steps; ++step) {
-    const uint32_t stage = step % 3;
-    copy_a(step + 2, (step + 2) % 3);
-    copy_b(step + 3, (step + 3) % kSlots);
-    const uint8_t *sa = lds + stage * kStage;
-    u32x4 fa[2][kBatch];
-    const auto read_batch = [&](int b) __attribute__((always_inline)) {
+  constexpr int kWaitLds = 0xC07F;   // s_waitcnt lgkmcnt(0), the other counters at their maximum
+  u32x4 fa[2][kBatch];
+  const auto read_batch = [&](uint32_t step, int b) __attribute__((always_inline)) {
+    const uint8_t *sa = lds + (step % kStages) * kStage;
 #pragma unroll
-      for (int i = 0; i < kBatch; ++i) {
-        const int g = b * kBatch + i;
-        fa[b & 1][i] = *(const u32x4 *)(sa + chunk_at((g % MI) * 16 + j, 4 * (g / MI) + q));
+    for (int i = 0; i < kBatch; ++i) {
+      const int g = b * kBatch + i;
+      fa[b & 1][i] = *(const u32x4 *)(sa + chunk_at((g % MI) * 16 + j, 4 * (g / MI) + q));
+    }
+  };
+  const auto mfma_batch = [&](uint32_t step, int b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int g = b * kBatch + i, kk = g / MI, mi = g % MI;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        acc[mi][t] = mfma_f16(wq[kk][t], fa[b & 1][i], acc[mi][t]);
+        // This MFMA's share of the other group's micro-operations: slot s of the half runs micro-operations
+        // [s kMicro / S, (s + 1) kMicro / S).
+        const int slot = mi * 4 + t, u0 = slot * kMicro / kSlotsHalf, u1 = (slot + 1) * kMicro / kSlotsHalf;
+        static_assert(kMicro <= 2 * kSlotsHalf, "at most two micro-operations a slot");
+        if (u0 < u1) micro(u0, kk == 0 ? step : step + 1, kk ^ 1);
+        if (u0 + 1 < u1) micro(u0 + 1, kk == 0 ? step : step + 1, kk ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
       }
-    };
-    read_batch(0);
+    }
+  };
+  read_batch(0, 0);
+  for (uint32_t step = 0; step < steps; ++step) {
+    if (step > 0) mfma_batch(step - 1, kBatches - 1);
 #pragma unroll
     for (int b = 0; b < kBatches; ++b) {
-      if (b + 1 < kBatches) read_batch(b + 1);
+#pragma unroll
+      for (int c = 0; c < kCopies; ++c)
+        if (c * kBatches / kCopies == b) copy_one(step, c);
+      __builtin_amdgcn_s_waitcnt(kWaitLds);
+      if (b + 1 < kBatches) read_batch(step, b + 1);
       if (b == 0) {
         q4k_coefficients<FMT>(wave_slot + ((step + 1) % kSlots) * kSlotBytes + 2048, step + 1, lane);
         read_b((step + 1) % kSlots, 0);
       }
       if (b == kBatches / 2) read_b((step + 1) % kSlots, 1);
-#pragma unroll
-      for (int i = 0; i < kBatch; ++i) {
-        const int g = b * kBatch + i, kk = g / MI, mi = g % MI;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          acc[mi][t] = mfma_f16(wq[kk][t], fa[b & 1][i], acc[mi][t]);
-          // This MFMA's share of the other group's micro-operations: slot s of the half runs micro-operations
-          // [s kMicro / S, (s + 1) kMicro / S).
-          const int slot = mi * 4 + t, u0 = slot * kMicro / kSlotsHalf, u1 = (slot + 1) * kMicro / kSlotsHalf;
-          static_assert(kMicro <= 2 * kSlotsHalf, "at most two micro-operations a slot");
-          if (u0 < u1) micro(u0, kk == 0 ? step : step + 1, kk ^ 1);
-          if (u0 + 1 < u1) micro(u0 + 1, kk == 0 ? step : step + 1, kk ^ 1);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
+      if (b + 1 < kBatches) mfma_batch(step, b);
     }
     __builtin_amdgcn_s_waitcnt(wait_vm(kCopies));
     lds_barrier();
+    if (step + 1 < steps) read_batch(step + 1, 0);
   }
+  mfma_batch(steps - 1, kBatches - 1);
 
   // Epilogue: lane (j, q) holds row 16 mi + j of each row block at columns 8q..8q+7 (blocks 0, 1) and
   // 32+8q..32+8q+7 (blocks 2, 3) of the plane tile: two 16-byte stores a row block.
