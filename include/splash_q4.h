@@ -31,6 +31,10 @@ extern "C" {
 #define SQ_FMT_AF4G32 25u
 #define SQ_FMT_AF4G64 26u
 #define SQ_FMT_AF4G128 27u
+/* Float rows (QuantizedSegment::rows, Weights.hpp:67-81): F32 rows carry the format id kFloat32, BF16 rows
+ * GGUF_FMT_BF16; the float projection multiplies them unrounded in fp32. */
+#define SQ_FMT_BF16 41u
+#define SQ_FLOAT32_ROWS 0xFFFFFFFFu
 
 /* enum values match the reference's enum class order (Linear.hpp:67-80, Weights.hpp:62) */
 #define SQ_PHASE_PREFILL 0u
@@ -86,9 +90,24 @@ typedef struct sq_linear_scratch_size {
 typedef struct sq_linear_scratch {
   sq_buffer input, sums, partials, counters, rotated;
 } sq_linear_scratch;
+/* LinearInput (Linear.hpp:166-169): the activation layout a plan reads. TABLE16 is the reference's Apple9 register
+ * tile table, which no plan here reads (a producer asked for it is refused); HALF_ROWS is this build's prefill
+ * table: the rows in fp16, scaled by a power of two per row and stored group by group in the prefill tile's read
+ * order, in scratch.input, with the powers (fp32) in scratch.sums. */
+#define SQ_LINEAR_INPUT_PLAIN 0u
+#define SQ_LINEAR_INPUT_TABLE16 1u
+#define SQ_LINEAR_INPUT_HALF_ROWS 2u
+/* PreparedInput (Linear.hpp:184-190): the scratch table currently holds `source` in `layout`. */
+typedef struct sq_prepared_input {
+  sq_buffer source;
+  uint32_t layout;
+} sq_prepared_input;
 typedef struct sq_linear_buffers {
   sq_buffer input, output, residual, gate_scratch;
   sq_linear_scratch scratch;
+  /* What the scratch table holds (LinearBuffers::prepared, Linear.hpp:216-226): a plan that reads a table prepares
+   * one unless this describes its input (same pointer and bytes). All zero: nothing. */
+  sq_prepared_input prepared;
 } sq_linear_buffers;
 
 /* DeviceCapabilities, as far as the MI355X policy reads it; compute_units 0 takes 256. */
@@ -130,6 +149,33 @@ int sq_require_segment_planes(const sq_segment *segment, const char *what, uint3
 /* Linear::add (Linear.cpp:203-232; LinearGguf.cpp:579-802): the plan's projection of buffers->input. */
 int sq_linear_add(void *graph, const sq_linear_buffers *buffers, const sq_projection *projection,
                   const sq_linear_plan *plan, const sq_projection *gate);
+/* Linear::add with its result: *prepared (may be NULL) receives what the scratch table describes after the
+ * dispatch (the PreparedInput Linear::add returns, Linear.cpp:222-231). */
+int sq_linear_add_prepared(void *graph, const sq_linear_buffers *buffers, const sq_projection *projection,
+                           const sq_linear_plan *plan, const sq_projection *gate, sq_prepared_input *prepared);
+/* LinearPlan::input (Linear.hpp:199-202): the layout the producer of the plan's input may write (SQ_LINEAR_INPUT_*):
+ * HALF_ROWS for a prefill plan, PLAIN otherwise. */
+int sq_linear_plan_input(const sq_linear_plan *plan, uint32_t *layout);
+
+/* ---- producers either side of the path ---- */
+
+/* NormWeights (Normalization.hpp:14-23): the per-channel multipliers of an RMS norm, bf16 (float32 0) or F32. */
+typedef struct sq_norm_weights {
+  sq_buffer buffer;
+  uint32_t float32;
+} sq_norm_weights;
+/* Normalization::addRms (Normalization.hpp:35-39; Normalization.cpp:16-38): output = bf16((x rsqrt(sum x^2 / width +
+ * 1e-6)) w) for `rows` rows of `width` bf16 inputs. With layout SQ_LINEAR_INPUT_HALF_ROWS it also writes the prefill
+ * table of `output` into *scratch (input: rows * width * 2 bytes, sums: rows * 4), the bits the prefill's own
+ * preparation would write; *prepared (may be NULL) receives what the scratch then describes. scratch may be NULL
+ * for PLAIN. width % 64 == 0; input, output, weights and the table 16-byte aligned. */
+int sq_norm_add_rms(void *graph, sq_buffer input, const sq_norm_weights *weight, sq_buffer output, uint32_t width,
+                    uint32_t rows, const sq_linear_scratch *scratch, uint32_t layout, sq_prepared_input *prepared);
+/* addGgufFloat (Linear.hpp:29-40; LinearGguf.cpp:806-818) for a float segment (format SQ_FLOAT32_ROWS or SQ_FMT_BF16,
+ * its rows in plane0): output[r][out_offset + n] = sum_k input[r][k] W[n][k] for r < rows, products and sums in
+ * fp32, into an fp32 or bf16 (destination SQ_OUTPUT_*) destination of out_stride columns. input_size % 4 == 0. */
+int sq_float_add(void *graph, sq_buffer input, const sq_segment *weights, sq_buffer output, uint32_t rows,
+                 uint32_t out_stride, uint32_t out_offset, uint32_t destination);
 /* Linear::addPrefill / addPrefillResidual / addPrefillUpWithGate (Linear.cpp:234-256). */
 int sq_linear_add_prefill(const sq_device *device, void *graph, sq_buffer input, const sq_projection *projection,
                           sq_buffer output, uint32_t rows, const sq_linear_scratch *scratch);
@@ -208,6 +254,10 @@ typedef struct sq_moe_weights {
   uint32_t slots;
   sq_segment shared_gate, shared_up, shared_down;
   sq_buffer shared_scalar_gate;
+  /* BlockMoeWeights::router (MoE.hpp:133): F32 (SQ_FLOAT32_ROWS) or BF16 rows [experts][hidden] in plane0. With
+   * plane0 set the routing first projects the input onto it into buffers->scores (MoE::addRoutes,
+   * MoE.cpp:527-543); with plane0 NULL the scores are the caller's. */
+  sq_segment router;
 } sq_moe_weights;
 typedef struct sq_moe_scratch {
   sq_buffer selected_experts, routing_weights, tile_descriptors, tile_count, grouped_routes, route_rows,

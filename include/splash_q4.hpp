@@ -25,6 +25,9 @@ using MoeShape = sq_moe_shape;
 using MoePlan = sq_moe_plan;
 using MoeWeights = sq_moe_weights;
 using MoeBuffers = sq_moe_buffers;
+using PreparedInput = sq_prepared_input;
+using NormWeights = sq_norm_weights;
+using QuantizedSegment = sq_segment;
 using Graph = void *;   // a hipStream_t; nullptr is the default stream
 
 enum class LinearEpilogue : uint32_t {
@@ -109,9 +112,18 @@ class Linear final {
     return out;
   }
 
-  void add(Graph graph, LinearBuffers buffers, const Projection &projection, const LinearPlan &plan,
-           const Projection *gate = nullptr) const {
-    check(sq_linear_add(graph, &buffers, &projection, &plan, gate));
+  // Returns what the scratch table describes after the dispatch (Linear.cpp:222-231).
+  PreparedInput add(Graph graph, LinearBuffers buffers, const Projection &projection, const LinearPlan &plan,
+                    const Projection *gate = nullptr) const {
+    PreparedInput out{};
+    check(sq_linear_add_prepared(graph, &buffers, &projection, &plan, gate, &out));
+    return out;
+  }
+  // LinearPlan::input (Linear.hpp:199-202).
+  [[nodiscard]] static uint32_t input(const LinearPlan &plan) {
+    uint32_t layout = 0;
+    check(sq_linear_plan_input(&plan, &layout));
+    return layout;
   }
   void addPrefill(Graph graph, Buffer input, const Projection &projection, Buffer output, uint32_t rows,
                   LinearScratch scratch = {}) const {
@@ -135,6 +147,23 @@ class Linear final {
  private:
   sq_device device_;
 };
+
+// Normalization (Normalization.hpp:29-40).
+class Normalization final {
+ public:
+  static PreparedInput addRms(Graph graph, Buffer input, const NormWeights &weight, Buffer output, uint32_t width,
+                              uint32_t rows, LinearScratch scratch = {}, uint32_t layout = SQ_LINEAR_INPUT_PLAIN) {
+    PreparedInput out{};
+    check(sq_norm_add_rms(graph, input, &weight, output, width, rows, &scratch, layout, &out));
+    return out;
+  }
+};
+
+// addGgufFloat (Linear.hpp:29-40) for F32 or BF16 rows.
+inline void addGgufFloat(Graph graph, Buffer input, const QuantizedSegment &weights, Buffer output, uint32_t rows,
+                         uint32_t outStride, uint32_t outOffset, uint32_t destination = SQ_OUTPUT_F32) {
+  check(sq_float_add(graph, input, &weights, output, rows, outStride, outOffset, destination));
+}
 
 class MoE final {
  public:

@@ -195,3 +195,62 @@ def f16_bits(values: np.ndarray) -> np.ndarray:
     """The oracle's float32 -> float16 (round to nearest even) of every value."""
     v = np.ascontiguousarray(values, np.float32).ravel()
     return np.array([lib().sqo_f32_to_f16(float(x)) for x in v], np.uint16).reshape(np.shape(values))
+
+
+# ---------------------------------------------------------------- producers either side of the path
+
+RMS_EPSILON = 1e-6   # SPLASH_RMS_EPSILON (runtime/metal/abi/ExecutionGeometry.h:59)
+
+
+def bf16_values(bits: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns as fp64 values (exact)."""
+    return (np.asarray(bits, np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def rms_norm_f64(x_bf16: np.ndarray, weights: np.ndarray) -> np.ndarray:
+    """The fp64 RMS norm of bf16 rows with the kernels' epsilon, scaled by the weights as read (fp32 values of the
+    stored bf16 or F32 weights): x / sqrt(mean(x^2) + eps) * w (dev/tests/engine/NormReference.hpp:44-57)."""
+    x = bf16_values(x_bf16)
+    inverse = 1.0 / np.sqrt((x * x).sum(axis=1, keepdims=True) / x.shape[1] + RMS_EPSILON)
+    return x * inverse * np.asarray(weights, np.float64)[None, :]
+
+
+def ulp_bf16(values: np.ndarray) -> np.ndarray:
+    """The spacing of bf16 at each |value| (the smallest normal's for zero and subnormals)."""
+    v = np.abs(np.asarray(values, np.float64))
+    exponent = np.floor(np.log2(np.maximum(v, 2.0 ** -126)))
+    return np.ldexp(1.0, (exponent - 7).astype(np.int64))
+
+
+def rounded_once_to_bf16(got_bits: np.ndarray, exact: np.ndarray) -> np.ndarray:
+    """Whether each bf16 result is the exact value rounded once to bf16, up to fp32 noise well below 2^-8 of half
+    an ulp (dev/tests/engine/NormReference.hpp:59-66)."""
+    return np.abs(bf16_values(got_bits) - exact) <= 0.5 * ulp_bf16(exact) * (1 + 1.0 / 256)
+
+
+def half_rows(x_bf16: np.ndarray):
+    """The prefill tile's prepared input of bf16 rows [rows][K] (K % 32 == 0): each row times 2^-shift, shift the
+    smallest that brings its largest magnitude below 2^16 (0 when it already is), as fp16 bits, chunk v = 4 g + c
+    of a row holding inputs 32 g + 4 c .. +3 then 32 g + 16 + 4 c .. +3; and the fp32 scales 2^shift."""
+    bits = np.ascontiguousarray(x_bf16, np.uint16)
+    rows, k = bits.shape
+    largest = (bits & 0x7FFF).max(axis=1).astype(np.int64)
+    exponent = (np.minimum(largest, 0x7F80) >> 7) - 127
+    shift = np.where(exponent >= 16, exponent - 15, 0)
+    scaled = bf16_values(bits) * np.ldexp(1.0, -shift)[:, None]
+    half = scaled.astype(np.float32).astype(np.float16).view(np.uint16)   # exact in fp32; one rounding to fp16
+    order = np.empty(k, np.int64)
+    for v in range(k // 8):
+        g, c = divmod(v, 4)
+        base = 32 * g + 4 * c
+        order[8 * v:8 * v + 4] = np.arange(base, base + 4)
+        order[8 * v + 4:8 * v + 8] = np.arange(base + 16, base + 20)
+    return half[:, order], np.ldexp(1.0, shift).astype(np.float32)
+
+
+def float_rows_f64(x_bf16: np.ndarray, w: np.ndarray):
+    """The fp64 projection of bf16 rows onto float rows w [N][K] as read (fp32 values), and sum_k |x w| per output
+    (the scale of the fp32 accumulation bound)."""
+    x = bf16_values(x_bf16)
+    wf = np.asarray(w, np.float64)
+    return x @ wf.T, np.abs(x) @ np.abs(wf).T

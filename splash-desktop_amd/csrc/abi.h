@@ -23,7 +23,14 @@
 #define SQ_FMT_AF4G32 25u
 #define SQ_FMT_AF4G64 26u
 #define SQ_FMT_AF4G128 27u
+#define SQ_FMT_BF16 41u   // as float rows only (QuantizedSegment::rows)
 #define SQ_FMT_COUNT 48u
+// QuantizedSegment::kFloat32 (Weights.hpp:81): the format id of F32 rows, which no format row names.
+#define SQ_FLOAT32_ROWS 0xFFFFFFFFu
+// LinearInput (Linear.hpp:166-169) and this build's prefill table (the prefill tile's prepared input).
+#define SQ_LINEAR_INPUT_PLAIN 0u
+#define SQ_LINEAR_INPUT_TABLE16 1u
+#define SQ_LINEAR_INPUT_HALF_ROWS 2u
 
 // A format row (QuantFormat.h:147-156): the bytes of a native block and of the planes' units.
 struct SqQuantFormat {

@@ -93,6 +93,11 @@ LinearScratch scratch(const sq_linear_scratch *s) {
   return {buf(s->input), buf(s->sums), buf(s->partials), buf(s->counters), buf(s->rotated)};
 }
 sq_linear_scratch_size csize(const LinearScratchSize &s) { return {s.input, s.sums, s.partials, s.counters, s.rotated}; }
+PreparedInput prepared(const sq_prepared_input &p) {
+  if (p.layout > SQ_LINEAR_INPUT_HALF_ROWS) throw std::invalid_argument("unknown linear input layout");
+  return {buf(p.source), LinearInput(p.layout)};
+}
+sq_prepared_input cprepared(const PreparedInput &p) { return {cbuf(p.source), uint32_t(p.layout)}; }
 hipStream_t stream(void *graph) { return static_cast<hipStream_t>(graph); }
 void launched(hipError_t e, const char *what) {
   if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
@@ -172,20 +177,54 @@ int sq_require_segment_planes(const sq_segment *s, const char *what, uint32_t pl
   return guarded([&] { requireSegmentPlanes(segment(need(s, "segment")), what ? what : "segment", plane_inputs); });
 }
 
-int sq_linear_add(void *graph, const sq_linear_buffers *b, const sq_projection *p, const sq_linear_plan *lp,
-                  const sq_projection *gate) {
+int sq_linear_add_prepared(void *graph, const sq_linear_buffers *b, const sq_projection *p, const sq_linear_plan *lp,
+                           const sq_projection *gate, sq_prepared_input *result) {
   return guarded([&] {
     const sq_linear_buffers &bb = need(b, "buffers");
-    LinearBuffers buffers{buf(bb.input), buf(bb.output), buf(bb.residual), buf(bb.gate_scratch), scratch(&bb.scratch)};
+    LinearBuffers buffers{buf(bb.input), buf(bb.output), buf(bb.residual), buf(bb.gate_scratch), scratch(&bb.scratch),
+                          prepared(bb.prepared)};
     const Projection proj = projection(need(p, "projection"));
     const LinearPlan selected = plan(need(lp, "plan"));
     const Linear l(DeviceCapabilities{});
+    PreparedInput after;
     if (gate) {
       const Projection g = projection(*gate);
-      l.add(stream(graph), buffers, proj, selected, &g);
+      after = l.add(stream(graph), buffers, proj, selected, &g);
     } else {
-      l.add(stream(graph), buffers, proj, selected);
+      after = l.add(stream(graph), buffers, proj, selected);
     }
+    if (result) *result = cprepared(after);
+  });
+}
+int sq_linear_add(void *graph, const sq_linear_buffers *b, const sq_projection *p, const sq_linear_plan *lp,
+                  const sq_projection *gate) {
+  return sq_linear_add_prepared(graph, b, p, lp, gate, nullptr);
+}
+int sq_linear_plan_input(const sq_linear_plan *lp, uint32_t *layout) {
+  return guarded([&] {
+    if (!layout) throw std::invalid_argument("layout is null");
+    *layout = uint32_t(plan(need(lp, "plan")).input());
+  });
+}
+
+int sq_norm_add_rms(void *graph, sq_buffer input, const sq_norm_weights *weight, sq_buffer output, uint32_t width,
+                    uint32_t rows, const sq_linear_scratch *s, uint32_t layout, sq_prepared_input *result) {
+  return guarded([&] {
+    if (layout > SQ_LINEAR_INPUT_HALF_ROWS) throw std::invalid_argument("unknown linear input layout");
+    const sq_norm_weights &w = need(weight, "norm weights");
+    const PreparedInput after = Normalization::addRms(stream(graph), buf(input), NormWeights{buf(w.buffer), w.float32 != 0},
+                                                      buf(output), width, rows, scratch(s), LinearInput(layout));
+    if (result) *result = cprepared(after);
+  });
+}
+
+int sq_float_add(void *graph, sq_buffer input, const sq_segment *weights, sq_buffer output, uint32_t rows,
+                 uint32_t out_stride, uint32_t out_offset, uint32_t destination) {
+  return guarded([&] {
+    if (destination > SQ_OUTPUT_F32) throw std::invalid_argument("unknown float destination");
+    const sq_segment &w = need(weights, "float rows");
+    addGgufFloat(stream(graph), buf(input), QuantizedSegment::rows(w.format_id, w.output_size, w.input_size, buf(w.plane0)),
+                 buf(output), rows, out_stride, out_offset, FloatOutput(destination));
   });
 }
 
@@ -320,7 +359,10 @@ MoePlan moePlan(const sq_moe_plan &p) {
 }
 // The shared views are read only when the plan has shared slices.
 MoeWeights moeWeights(const sq_moe_weights &w, const sq_moe_plan &p) {
-  MoeWeights out{segment(w.gate), segment(w.up), segment(w.down), buf(w.slot_table), w.slots, {}, {}, {}, {}};
+  MoeWeights out{segment(w.gate), segment(w.up), segment(w.down), buf(w.slot_table), w.slots, {}, {}, {}, {}, {}};
+  if (w.router.plane0.ptr)
+    out.router = QuantizedSegment::rows(w.router.format_id, w.router.output_size, w.router.input_size,
+                                        buf(w.router.plane0));
   if (p.shape.shared_slices) {
     out.sharedGate = segment(w.shared_gate);
     out.sharedUp = segment(w.shared_up);

@@ -86,6 +86,29 @@ QuantizedSegment QuantizedSegment::planes(uint32_t formatId, uint32_t outputSize
   return s;
 }
 
+// QuantizedSegment::rows (Weights.hpp:88-99): F32 or BF16 rows, `outputSize` rows of `inputSize` values in plane0.
+QuantizedSegment QuantizedSegment::rows(uint32_t formatId, uint32_t outputSize, uint32_t inputSize, Buffer values) {
+  if (formatId != kFloat32 && formatId != SQ_FMT_BF16)
+    throw std::invalid_argument("float rows are F32 or BF16 (other formats' native rows are not taken here)");
+  QuantizedSegment s;
+  s.plane0 = values;
+  s.outputSize = outputSize;
+  s.inputSize = inputSize;
+  s.formatId = formatId;
+  return s;
+}
+
+void requireTableScratch(const LinearScratch &scratch, LinearInput layout, uint32_t width, uint32_t rows) {
+  if (layout == LinearInput::Table16)
+    throw std::invalid_argument("the Table16 layout is the Apple9 register tile's, which this device does not run");
+  if (layout != LinearInput::HalfRows) throw std::invalid_argument("a table producer takes a table layout");
+  if (!rows || width % 64) throw std::invalid_argument("a prefill table takes whole 64-input spans");
+  requireBytes(scratch.input, tableBytes(width, rows), "norm table scratch");
+  requireBytes(scratch.sums, tableSumsBytes(rows), "norm table sums");
+  if (reinterpret_cast<uintptr_t>(scratch.input.ptr) & 15u)
+    throw std::invalid_argument("the prefill table is 16-byte aligned");
+}
+
 // Weights.hpp:134-143.
 Projection::Projection(uint32_t output, uint32_t input, BlockWeights weights)
     : outputSize(output), inputSize(input), weights_(std::move(weights)) {
@@ -166,6 +189,10 @@ LinearScratchSize LinearPlan::scratchSize() const noexcept {
   return config_.splits > 1 ? LinearScratchSize{0, 0, uint64_t{config_.splits} * storageRows() * columns * 4,
                                                 uint64_t{n / 16} * 4, 0}
                             : LinearScratchSize{};
+}
+
+LinearInput LinearPlan::input() const noexcept {
+  return config_.tile == LinearTile::GgufPrefill ? LinearInput::HalfRows : LinearInput::Plain;
 }
 
 uint64_t LinearPlan::gateScratchBytes() const noexcept {
@@ -261,8 +288,8 @@ LinearScratchSize Linear::prefillScratchSize(ProjectionShape shape) const {
 
 // ---------------------------------------------------------------- dispatch
 
-void Linear::add(hipStream_t graph, LinearBuffers b, const Projection &p, const LinearPlan &selected,
-                 const Projection *gate) const {
+PreparedInput Linear::add(hipStream_t graph, LinearBuffers b, const Projection &p, const LinearPlan &selected,
+                          const Projection *gate) const {
   const LinearWorkload w = selected.workload();
   const auto [n, k] = w.matrix;
   if ((w.epilogue == LinearEpilogue::GateUp) != (gate != nullptr))
@@ -317,9 +344,12 @@ void Linear::add(hipStream_t graph, LinearBuffers b, const Projection &p, const 
     throw std::invalid_argument("a fused block projection takes at most three segments and no epilogue");
 
   if (config.tile == LinearTile::GgufPrefill) {
-    requireLaunch(kern::launch_prefill_prepare(b.input.as<const uint16_t>(), w.rows, k, b.scratch.input.as<uint16_t>(),
-                                               b.scratch.sums.as<float>(), graph),
-                  "prefill prepare");
+    // The table is prepared unless the scratch already holds this input's (a fused RMS norm, or a projection of the
+    // same input before).
+    if (!b.prepared.describes(b.input, LinearInput::HalfRows))
+      requireLaunch(kern::launch_prefill_prepare(b.input.as<const uint16_t>(), w.rows, k,
+                                                 b.scratch.input.as<uint16_t>(), b.scratch.sums.as<float>(), graph),
+                    "prefill prepare");
     for (const auto &group : byFormat) {
       kern::PrefillArgs a{};
       a.half_input = b.scratch.input.as<const uint16_t>();
@@ -335,7 +365,7 @@ void Linear::add(hipStream_t graph, LinearBuffers b, const Projection &p, const 
       a.compute_units = computeUnits_;
       requireLaunch(kern::launch_prefill(group.front()->formatId, epilogueOf(w.epilogue), a, graph), "prefill tile");
     }
-    return;
+    return {b.input, LinearInput::HalfRows};
   }
   const auto decode = [&](const std::vector<const QuantizedSegment *> &group, uint32_t epilogue, Buffer output,
                           Buffer aux, bool f32) {
@@ -370,17 +400,19 @@ void Linear::add(hipStream_t graph, LinearBuffers b, const Projection &p, const 
     a.splits = config.splits;
     a.out_stride = n;
     requireLaunch(kern::launch_decode(u.formatId, kern::EpNone, false, a, graph), "gate/up decode tile");
-    return;
+    return b.prepared;
   }
+  // The decode tiles read the plain rows and leave the scratch table as it was.
   if (w.epilogue == LinearEpilogue::GateUp) {
     // A gate pass into the gate scratch, then the up pass whose epilogue multiplies silu(gate) into bf16(up).
     decode({&gate->blocks().segments.front()}, kern::EpNone, b.gateScratch, {}, false);
     decode({&segments.front()}, kern::EpUpWithGate, b.output, b.gateScratch, false);
-    return;
+    return b.prepared;
   }
   const Buffer aux = w.epilogue == LinearEpilogue::Residual ? b.residual : b.gateScratch;
   for (const auto &group : byFormat)
     decode(group, epilogueOf(w.epilogue), b.output, aux, selected.destination() == FloatOutput::Float32);
+  return b.prepared;
 }
 
 void Linear::addPrefill(hipStream_t graph, Buffer input, const Projection &p, Buffer output, uint32_t rows,
@@ -400,8 +432,13 @@ void Linear::addPrefillUpWithGate(hipStream_t graph, Buffer input, const Project
 // Linear.cpp:244-250.
 void Linear::addPrefillSwiGlu(hipStream_t graph, const SwiGluProjections &ffn, const PrefillFfnBuffers &b,
                               Buffer residual, Buffer output, uint32_t rows) const {
-  addPrefill(graph, b.normalized, *ffn.gate, b.gateScratch, rows, b.scratch);
-  addPrefillUpWithGate(graph, b.normalized, *ffn.up, b.gateScratch, b.intermediate, rows, b.scratch);
+  // Gate and up read the same rows: up takes the table gate's dispatch prepared.
+  const PreparedInput normalized =
+      add(graph, {.input = b.normalized, .output = b.gateScratch, .scratch = b.scratch}, *ffn.gate,
+          prefillPlan(*ffn.gate, rows, LinearEpilogue::None));
+  add(graph, {.input = b.normalized, .output = b.intermediate, .gateScratch = b.gateScratch, .scratch = b.scratch,
+              .prepared = normalized},
+      *ffn.up, prefillPlan(*ffn.up, rows, LinearEpilogue::UpWithGate));
   addPrefillResidual(graph, b.intermediate, *ffn.down, residual, output, rows, b.scratch);
 }
 

@@ -48,6 +48,8 @@ void validate(const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
     requireExperts(w.sharedDown, s.sharedSlices, h, in, w.sharedDown.formatId, "shared down");
     if (s.sharedGate) requireBytes(w.sharedScalarGate, uint64_t{h} * 4, "MoE shared scalar gate weight");
   }
+  if (w.router.plane0 && (!w.router.isFloat() || w.router.outputSize != s.experts || w.router.inputSize != h))
+    throw std::invalid_argument("MoE router does not match the plan");
   const uint64_t hiddenRows = uint64_t{plan.rows()} * h * 2;
   requireBytes(b.input, hiddenRows, "MoE input");
   if (b.residual) requireBytes(b.residual, hiddenRows, "MoE residual");
@@ -101,8 +103,12 @@ void MoE::addRouting(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w
   validate(b, w, plan);
   const MoeShape s = plan.shape();
   const MoeScratch &sc = b.scratch;
+  const uint32_t stride = b.scoreStride ? b.scoreStride : s.experts;
+  // The router's fp32 scores (MoE.cpp:527-543), when the block carries its rows.
+  if (w.router.plane0)
+    addGgufFloat(graph, b.input, w.router, b.scores, plan.rows(), stride, 0, FloatOutput::Float32);
   const SqMoeRouteParams route{plan.rows(), s.hiddenSize, s.experts, s.expertsPerToken};
-  launched(kern::launch_moe_route_select(b.scores.as<const float>(), b.scoreStride ? b.scoreStride : s.experts,
+  launched(kern::launch_moe_route_select(b.scores.as<const float>(), stride,
                                          sc.selectedExperts.as<uint32_t>(), sc.routingWeights.as<float>(), route,
                                          b.input.as<const uint16_t>(),
                                          s.sharedGate ? w.sharedScalarGate.as<const float>() : nullptr,

@@ -1,5 +1,6 @@
 // ops::MoE over HIP: the routed and shared experts' grouped gather-GEMM (reference: runtime/ops/MoE.hpp:19-423 and
-// runtime/ops/MoE.cpp:27-543). The router projection is the caller's: a step starts from its fp32 scores.
+// runtime/ops/MoE.cpp:27-543). A step starts from fp32 router scores: the block's router rows projected by the
+// routing itself (MoeWeights::router), or the caller's.
 #pragma once
 #include "ops.hpp"
 
@@ -57,6 +58,10 @@ struct MoeWeights {
   uint32_t slots = 0;
   QuantizedSegment sharedGate, sharedUp, sharedDown;
   Buffer sharedScalarGate;
+  // The router (BlockMoeWeights::router, MoE.hpp:133): F32 or BF16 rows [experts][hidden]. With it the routing
+  // projects the input onto it into the scores buffer first (MoE::addRoutes, MoE.cpp:527-543); without it the
+  // scores are the caller's.
+  QuantizedSegment router;
 };
 struct MoeBuffers {
   Buffer input, scores, residual, output;

@@ -36,12 +36,17 @@ enum class FloatOutput : uint8_t { BFloat16, Float32 };
   return type == FloatOutput::Float32 ? 4 : 2;
 }
 
-// Weights.hpp:79-121, planes layout (the float-rows layout is the router's, outside this path).
+// Weights.hpp:79-121. Planes: repacked planes in format formatId, which the block tiles read. Rows: the tensor's
+// rows as stored, inputSize values per output column in plane0, F32 (formatId kFloat32) or BF16 (SQ_FMT_BF16),
+// which the float projection multiplies unrounded in fp32 (the MoE router is one).
 struct QuantizedSegment {
+  static constexpr uint32_t kFloat32 = SQ_FLOAT32_ROWS;
   Buffer plane0, plane1, meta;
   uint32_t outputSize = 0, inputSize = 0, columnOffset = 0, formatId = SQ_FMT_COUNT;
   [[nodiscard]] static QuantizedSegment planes(uint32_t formatId, uint32_t outputSize, uint32_t inputSize,
                                                Buffer plane0, Buffer plane1, Buffer meta);
+  [[nodiscard]] static QuantizedSegment rows(uint32_t formatId, uint32_t outputSize, uint32_t inputSize, Buffer values);
+  [[nodiscard]] bool isFloat() const noexcept { return formatId == kFloat32 || formatId == SQ_FMT_BF16; }
   [[nodiscard]] SqQuantFormat format() const noexcept { return sq_format(formatId); }
   [[nodiscard]] const char *name() const noexcept { return sq_format_name(formatId); }
 };
@@ -121,6 +126,27 @@ struct PrefillFfnBuffers {
   LinearScratch scratch;
 };
 
+// LinearInput (Linear.hpp:166-169): the activation layout a plan reads. Table16 is the reference's Apple9 register
+// tile table, which no MI355X plan reads; HalfRows is the prefill tile's prepared input (the rows in fp16 scaled by
+// a power of two per row, in the tile's group order, in scratch.input, and the powers in scratch.sums), which the
+// prefill's own prepare dispatch or a fused RMS norm writes.
+enum class LinearInput : uint8_t { Plain = SQ_LINEAR_INPUT_PLAIN, Table16 = SQ_LINEAR_INPUT_TABLE16,
+                                   HalfRows = SQ_LINEAR_INPUT_HALF_ROWS };
+// PreparedInput (Linear.hpp:184-190): the scratch table currently holds `source` in `layout`. Producers return it,
+// consumers accept it and return what the scratch describes after their dispatch.
+struct PreparedInput {
+  Buffer source;
+  LinearInput layout = LinearInput::Plain;
+  [[nodiscard]] bool describes(const Buffer &input, LinearInput want) const noexcept {
+    return layout == want && source.ptr == input.ptr && source.bytes == input.bytes;
+  }
+};
+// The table bytes a producer writes for `rows` rows of `width` inputs (Linear.hpp:172-174), and its row scales.
+[[nodiscard]] constexpr uint64_t tableBytes(uint32_t width, uint64_t rows) noexcept { return uint64_t{width} * rows * 2; }
+[[nodiscard]] constexpr uint64_t tableSumsBytes(uint64_t rows) noexcept { return rows * 4; }
+// Throws unless `scratch` holds the `layout` table of `rows` rows of `width` inputs (Linear.hpp:175-179).
+void requireTableScratch(const LinearScratch &scratch, LinearInput layout, uint32_t width, uint32_t rows);
+
 class LinearPlan {
 public:
   [[nodiscard]] LinearWorkload workload() const noexcept { return workload_; }
@@ -129,6 +155,8 @@ public:
   [[nodiscard]] uint32_t storageRows() const noexcept;
   [[nodiscard]] LinearScratchSize scratchSize() const noexcept;
   [[nodiscard]] uint64_t gateScratchBytes() const noexcept;
+  // The layout the producer of this plan's input may write: HalfRows for the prefill tile, Plain otherwise.
+  [[nodiscard]] LinearInput input() const noexcept;
   LinearPlan(LinearWorkload workload, LinearConfig config, FloatOutput destination = FloatOutput::BFloat16);
 
 private:
@@ -141,6 +169,9 @@ private:
 struct LinearBuffers {
   Buffer input, output, residual, gateScratch;
   LinearScratch scratch{};
+  // What the scratch table holds (after a fused RMS norm, say). A plan that reads a table prepares one unless this
+  // describes its input.
+  PreparedInput prepared{};
 };
 
 // The device the policy plans for (the reference's DeviceCapabilities, reduced to what the MI355X policy reads).
@@ -162,8 +193,9 @@ public:
   [[nodiscard]] LinearScratchSize decodeScratchSize(ProjectionShape shape) const;
   [[nodiscard]] LinearScratchSize prefillScratchSize(ProjectionShape shape) const;
   [[nodiscard]] static LinearPlan plan(LinearWorkload workload, LinearConfig config, FloatOutput destination);
-  void add(hipStream_t graph, LinearBuffers buffers, const Projection &projection, const LinearPlan &plan,
-           const Projection *gate = nullptr) const;
+  // Returns what the scratch table describes after the dispatch (Linear.cpp:203-231).
+  PreparedInput add(hipStream_t graph, LinearBuffers buffers, const Projection &projection, const LinearPlan &plan,
+                    const Projection *gate = nullptr) const;
   void addPrefill(hipStream_t graph, Buffer input, const Projection &projection, Buffer output, uint32_t rows,
                   LinearScratch scratch = {}) const;
   void addPrefillUpWithGate(hipStream_t graph, Buffer input, const Projection &up, Buffer gateScratch, Buffer output,
@@ -181,5 +213,26 @@ private:
                                       const Projection *gate) const;
   uint32_t computeUnits_;
 };
+
+// NormWeights (Normalization.hpp:14-23): the per-channel multipliers of an RMS norm, bf16 or F32 as stored.
+struct NormWeights {
+  Buffer buffer;
+  bool float32 = false;
+  [[nodiscard]] constexpr uint64_t bytes(uint32_t width) const noexcept { return uint64_t{width} * (float32 ? 4 : 2); }
+};
+
+// Normalization (Normalization.hpp:29-40).
+struct Normalization {
+  // out = bf16((x * rsqrt(sum x^2 / width + 1e-6)) * w) per row; also writes the consumer's `layout` table into
+  // `scratch` when it is not Plain, and throws when `scratch` cannot hold it; returns what the scratch describes.
+  static PreparedInput addRms(hipStream_t graph, Buffer input, const NormWeights &weight, Buffer output,
+                              uint32_t width, uint32_t rows, LinearScratch scratch = {},
+                              LinearInput layout = LinearInput::Plain);
+};
+
+// addGgufFloat (Linear.hpp:29-40) for a float segment: out[r][outOffset + n] = sum_k input[r][k] W[n][k] for rows
+// r < `rows`, in fp32, into a `type` destination of `outStride` columns.
+void addGgufFloat(hipStream_t graph, Buffer input, const QuantizedSegment &weights, Buffer output, uint32_t rows,
+                  uint32_t outStride, uint32_t outOffset, FloatOutput type);
 
 }  // namespace sq::ops

@@ -78,6 +78,16 @@ hipError_t launch_dequant(uint32_t fmt, const uint8_t *plane0, const uint8_t *me
 // bf16 scales and biases) straight into plane0 / meta.
 hipError_t launch_repack(const uint8_t *src, uint8_t *dst, const SqGgufRepackParams &params, hipStream_t stream);
 // Measurement aid (diag.hip): a read-only stream of `bytes` (a multiple of 16) over `workgroups` workgroups.
+// The RMS norm producer: out = bf16((x * rsqrt(sum x^2 / width + 1e-6)) * w) per row, w bf16 or fp32; with
+// half_input set it also writes the prefill tile's prepared input of `out` (half_input [rows][width], row_scale
+// [rows]), the bits launch_prefill_prepare would write from it. width % 64 == 0; buffers 16-byte aligned.
+hipError_t launch_rms_norm(const uint16_t *input, const void *weight, bool f32_weights, uint16_t *output,
+                           uint32_t width, uint32_t rows, uint16_t *half_input, float *row_scale, hipStream_t stream);
+// A float projection: out[r][out_offset + n] = sum_k x[r][k] W[n][k] for W's N rows of K values stored fp32 or bf16,
+// fp32 products and sums, into fp32 or bf16 [rows][out_stride]. K % 4 == 0.
+hipError_t launch_float_rows(const uint16_t *input, const void *weights, bool f32_weights, void *output,
+                             bool f32_output, uint32_t rows, uint32_t N, uint32_t K, uint32_t out_stride,
+                             uint32_t out_offset, hipStream_t stream);
 hipError_t launch_stream_read(const void *src, uint64_t bytes, uint32_t *sink, uint32_t workgroups, uint32_t threads,
                               hipStream_t stream);
 hipError_t launch_mlx_repack(uint32_t fmt, const uint32_t *weight, const uint16_t *scales, const uint16_t *biases,

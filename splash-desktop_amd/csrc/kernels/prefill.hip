@@ -27,6 +27,7 @@
 #include <type_traits>
 
 #include "device.hpp"
+#include "half_rows.hpp"
 #include "kernels.hpp"
 
 namespace sq::kern {
@@ -64,27 +65,19 @@ __device__ __forceinline__ uint32_t chunk_at(uint32_t r, uint32_t c) { return r 
 
 // ---------------------------------------------------------------- prepare
 
-// One workgroup per row: the largest magnitude of the row's bf16 inputs (a wave reduction and LDS), then the fp16 row
-// scaled by 2^-e where 2^e brings the largest below 2^16, each group of 32 stored with its 16-byte chunk q holding
-// inputs 4q..4q+3 and 16+4q..19+4q. Rows of at most 256 NV output chunks are read once, into registers (NV > 0);
-// longer ones are read twice.
+// One workgroup per row: the largest magnitude of the row's bf16 inputs (a wave reduction and LDS), then the half
+// rows table of the row (half_rows.hpp). Rows of at most 256 NV output chunks are read once, into registers
+// (NV > 0); longer ones are read twice.
 template <int NV>
 __global__ __launch_bounds__(256) void prepare_kernel(const uint16_t *input, uint32_t K, uint16_t *half_input,
                                                       float *row_scale) {
   const uint32_t r = blockIdx.x, vectors = K / 8;
   const u32x2 *units = (const u32x2 *)(input + (size_t)r * K);   // 4-input units
   u32x4 *h = (u32x4 *)(half_input + (size_t)r * K);
-  // Output chunk v = 4 g + c (group g) takes units 8 g + c and 8 g + c + 4.
   const auto chunk = [&](uint32_t v) __attribute__((always_inline)) {
-    const uint32_t g = v >> 2, c = v & 3;
-    const u32x2 lo = units[8 * g + c], hi = units[8 * g + c + 4];
+    const uint32_t u = half_rows_unit(v);
+    const u32x2 lo = units[u], hi = units[u + 4];
     return u32x4{lo[0], lo[1], hi[0], hi[1]};
-  };
-  const auto magnitude = [](u32x4 w) __attribute__((always_inline)) {
-    uint32_t m = 0;   // bf16 bit patterns order like their magnitudes
-#pragma unroll
-    for (int e = 0; e < 4; ++e) m = max(m, max(w[e] & 0x7FFFu, (w[e] >> 16) & 0x7FFFu));
-    return m;
   };
   uint32_t largest = 0;
   u32x4 held[NV > 0 ? NV : 1];
@@ -93,10 +86,10 @@ __global__ __launch_bounds__(256) void prepare_kernel(const uint16_t *input, uin
     for (int i = 0; i < NV; ++i) {
       const uint32_t v = threadIdx.x + 256u * i;
       held[i] = v < vectors ? chunk(v) : u32x4{0u, 0u, 0u, 0u};
-      largest = max(largest, magnitude(held[i]));
+      largest = max(largest, bf16_largest(held[i]));
     }
   } else {
-    for (uint32_t v = threadIdx.x; v < vectors; v += 256) largest = max(largest, magnitude(chunk(v)));
+    for (uint32_t v = threadIdx.x; v < vectors; v += 256) largest = max(largest, bf16_largest(chunk(v)));
   }
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) largest = max(largest, (uint32_t)__shfl_xor((int)largest, d));
@@ -104,27 +97,17 @@ __global__ __launch_bounds__(256) void prepare_kernel(const uint16_t *input, uin
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = largest;
   __syncthreads();
   largest = max(max(part[0], part[1]), max(part[2], part[3]));
-  // Exponent field of the largest magnitude: scale by 2^-(e - 15) when it is 2^16 or more, so it ends below 2^16.
-  const int exponent = (int)(min(largest, 0x7F80u) >> 7) - 127;
-  const int shift = exponent >= 16 ? exponent - 15 : 0;
+  const int shift = half_rows_shift(largest);
   const float down = ldexpf(1.0f, -shift);
   if (threadIdx.x == 0) row_scale[r] = ldexpf(1.0f, shift);
-  const auto convert = [&](u32x4 w) __attribute__((always_inline)) {
-    u32x4 o;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      o[e] = (uint32_t)f32_to_f16(bf16_to_f32(w[e] & 0xFFFFu) * down) |
-             ((uint32_t)f32_to_f16(bf16_to_f32(w[e] >> 16) * down) << 16);
-    return o;
-  };
   if constexpr (NV > 0) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const uint32_t v = threadIdx.x + 256u * i;
-      if (v < vectors) h[v] = convert(held[i]);
+      if (v < vectors) h[v] = half_rows_chunk(held[i], down);
     }
   } else {
-    for (uint32_t v = threadIdx.x; v < vectors; v += 256) h[v] = convert(chunk(v));
+    for (uint32_t v = threadIdx.x; v < vectors; v += 256) h[v] = half_rows_chunk(chunk(v), down);
   }
 }
 

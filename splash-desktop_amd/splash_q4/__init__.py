@@ -21,6 +21,8 @@ PHASE_PREFILL, PHASE_DECODE = 0, 1
 EPILOGUE_NONE, EPILOGUE_RESIDUAL, EPILOGUE_GATE_UP, EPILOGUE_UP_WITH_GATE = 0, 1, 2, 3
 TILE_STAGED, TILE_PREFILL, TILE_REGISTER = 0, 1, 2
 OUTPUT_BF16, OUTPUT_F32 = 0, 1
+FMT_BF16, FLOAT32_ROWS = 41, 0xFFFFFFFF
+LINEAR_INPUT_PLAIN, LINEAR_INPUT_TABLE16, LINEAR_INPUT_HALF_ROWS = 0, 1, 2
 
 # (block_elements, block_bytes, plane0_bytes, meta_bytes, meta_groups) of QuantFormat.h:159,185-187.
 FORMATS = {
@@ -68,9 +70,17 @@ class LinearScratch(Structure):
     _fields_ = [(n, Buffer) for n in ("input", "sums", "partials", "counters", "rotated")]
 
 
+class PreparedInput(Structure):
+    _fields_ = [("source", Buffer), ("layout", c_uint32)]
+
+
 class LinearBuffers(Structure):
     _fields_ = [("input", Buffer), ("output", Buffer), ("residual", Buffer), ("gate_scratch", Buffer),
-                ("scratch", LinearScratch)]
+                ("scratch", LinearScratch), ("prepared", PreparedInput)]
+
+
+class NormWeights(Structure):
+    _fields_ = [("buffer", Buffer), ("float32", c_uint32)]
 
 
 class Device(Structure):
@@ -101,7 +111,7 @@ class MoePlan(Structure):
 class MoeWeights(Structure):
     _fields_ = [("gate", Segment), ("up", Segment), ("down", Segment), ("slot_table", Buffer), ("slots", c_uint32),
                 ("shared_gate", Segment), ("shared_up", Segment), ("shared_down", Segment),
-                ("shared_scalar_gate", Buffer)]
+                ("shared_scalar_gate", Buffer), ("router", Segment)]
 
 
 class MoeScratch(Structure):
@@ -140,6 +150,12 @@ _SIGNATURES = {
     "sq_linear_prefill_scratch_size": [POINTER(Device), c_uint32, c_uint32, POINTER(LinearScratchSize)],
     "sq_require_segment_planes": [POINTER(Segment), c_char_p, c_uint32],
     "sq_linear_add": [c_void_p, POINTER(LinearBuffers), POINTER(Projection), POINTER(LinearPlan), POINTER(Projection)],
+    "sq_linear_add_prepared": [c_void_p, POINTER(LinearBuffers), POINTER(Projection), POINTER(LinearPlan),
+                               POINTER(Projection), POINTER(PreparedInput)],
+    "sq_linear_plan_input": [POINTER(LinearPlan), POINTER(c_uint32)],
+    "sq_norm_add_rms": [c_void_p, Buffer, POINTER(NormWeights), Buffer, c_uint32, c_uint32, POINTER(LinearScratch),
+                        c_uint32, POINTER(PreparedInput)],
+    "sq_float_add": [c_void_p, Buffer, POINTER(Segment), Buffer, c_uint32, c_uint32, c_uint32, c_uint32],
     "sq_linear_add_prefill": [POINTER(Device), c_void_p, Buffer, POINTER(Projection), Buffer, c_uint32,
                               POINTER(LinearScratch)],
     "sq_linear_add_prefill_residual": [POINTER(Device), c_void_p, Buffer, POINTER(Projection), Buffer, Buffer,

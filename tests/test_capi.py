@@ -255,3 +255,45 @@ def test_prefill_buffers_are_aligned():
                                sq.Buffer(None, 0), sq.Buffer(None, 0), scratch)
     with pytest.raises(sq.InvalidArgument, match="16-byte aligned"):
         sq.call("sq_linear_add", None, sq.byref(buffers), sq.byref(proj), sq.byref(plan), None)
+
+
+def _fake(nbytes, at=1 << 20):
+    """A buffer view the host validates but nothing dereferences (every call below is refused before a launch)."""
+    return sq.Buffer(at, nbytes)
+
+
+def test_plan_input_layouts():
+    """LinearPlan::input: the prefill tile reads the half-rows table, the decode tiles plain rows."""
+    layout = sq.c_uint32()
+    for workload, want in ((sq.prefill_workload(1024, 2048, 512), sq.LINEAR_INPUT_HALF_ROWS),
+                           (sq.decode_workload(1024, 2048, 4), sq.LINEAR_INPUT_PLAIN)):
+        sq.call("sq_linear_plan_input", sq.byref(sq.plan_for(workload)), sq.byref(layout))
+        assert layout.value == want
+
+
+def test_norm_and_float_rows_refusals():
+    """The producers' validation (host only): whole 64-input spans, the Apple9 table refused, a table scratch that
+    holds the rows, float rows F32 or BF16 only, destination columns inside the stride."""
+    rows, width = 8, 2048
+    io = _fake(rows * width * 2)
+    weights = sq.NormWeights(_fake(width * 2), 0)
+    table = sq.LinearScratch(_fake(rows * width * 2, 1 << 24), _fake(rows * 4, 1 << 25), sq.Buffer(), sq.Buffer(),
+                             sq.Buffer())
+    with pytest.raises(sq.InvalidArgument, match="64-input spans"):
+        sq.call("sq_norm_add_rms", None, io, sq.byref(weights), io, 100, 1, None, sq.LINEAR_INPUT_PLAIN, None)
+    with pytest.raises(sq.InvalidArgument, match="register tile"):
+        sq.call("sq_norm_add_rms", None, io, sq.byref(weights), io, width, rows, sq.byref(table),
+                sq.LINEAR_INPUT_TABLE16, None)
+    small = sq.LinearScratch(_fake(rows * width, 1 << 24), _fake(rows * 4, 1 << 25), sq.Buffer(), sq.Buffer(),
+                             sq.Buffer())
+    with pytest.raises(sq.InvalidArgument, match="norm table scratch"):
+        sq.call("sq_norm_add_rms", None, io, sq.byref(weights), io, width, rows, sq.byref(small),
+                sq.LINEAR_INPUT_HALF_ROWS, None)
+    with pytest.raises(sq.InvalidArgument, match="unknown linear input layout"):
+        sq.call("sq_norm_add_rms", None, io, sq.byref(weights), io, width, rows, None, 7, None)
+    q4k = sq.Segment(_fake(64 * 2048), sq.Buffer(), sq.Buffer(), 64, 2048, 0, sq.FMT_Q4K)
+    with pytest.raises(sq.InvalidArgument, match="F32 or BF16"):
+        sq.call("sq_float_add", None, io, sq.byref(q4k), io, rows, 64, 0, sq.OUTPUT_F32)
+    f32 = sq.Segment(_fake(64 * 2048 * 4), sq.Buffer(), sq.Buffer(), 64, 2048, 0, sq.FLOAT32_ROWS)
+    with pytest.raises(sq.InvalidArgument, match="outside its destination"):
+        sq.call("sq_float_add", None, io, sq.byref(f32), _fake(rows * 64 * 4), rows, 64, 8, sq.OUTPUT_F32)

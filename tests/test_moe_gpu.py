@@ -50,9 +50,14 @@ class Block:
 
     def weights(self):
         self._gate = to_device(self.scalar_gate) if self.gated else None
+        router = sq.Segment()
+        if getattr(self, "router_rows", None) is not None:
+            self._router = to_device(self.router_rows)
+            router = sq.Segment(sq.view(self._router), sq.view(None), sq.view(None), self.e, self.h, 0,
+                                sq.FLOAT32_ROWS)
         return sq.MoeWeights(self.segment("gate"), self.segment("up"), self.segment("down"), sq.view(self.slots), self.e,
                              self.segment("shared_gate"), self.segment("shared_up"), self.segment("shared_down"),
-                             sq.view(self._gate))
+                             sq.view(self._gate), router)
 
     def values(self, name, expert):
         """Expert `expert`'s rows of projection `name`; ids from the expert count on are the shared slices."""
@@ -82,6 +87,7 @@ def run_moe(block, x, scores, top_k, residual=None, phase="prefill"):
     ms = sq.MoeScratch(*[sq.view(scratch[n]) if getattr(plan.workspace, n) else sq.Buffer(None, 0)
                          for n in sq._MOE_WORKSPACE])
     xin, sc = to_device(x), t.from_numpy(np.ascontiguousarray(scores)).cuda()
+    scratch["scores"] = sc
     res = to_device(residual) if residual is not None else None
     out = t.full((rows, block.h), -1, dtype=t.int16, device="cuda")
     buffers = sq.MoeBuffers(sq.view(xin), sq.view(sc), sq.view(res), sq.view(out), 0, ms)
@@ -194,4 +200,29 @@ def test_moe_decode_rows():
     selected, weights = oracle.route_select(scores, 8)
     want = expected(block, x, selected, weights, None)
     err = synthetic.bf16_to_f32(got) - want
+    assert np.linalg.norm(err) / np.linalg.norm(want) <= 1e-2
+
+
+def test_moe_router_projection():
+    """A block that carries its router's F32 rows projects the input onto them first (MoE::addRoutes): the scores
+    lie within the fp32 accumulation bound of fp64, the selection and grouping follow from them as the oracle says,
+    and the output is the one the same scores give when the caller supplies them."""
+    rng = np.random.default_rng(808)
+    block = Block(rng, 32, 512, 128, shared=1, gated=True)
+    block.router_rows = rng.normal(0, 0.05, (32, 512)).astype(np.float32)
+    rows = 44
+    x = synthetic.activations(rng, rows, 512)
+    plan, scratch, got = run_moe(block, x, np.zeros((rows, 32), np.float32), 4)
+    scores = scratch["scores"].cpu().numpy()
+    exact, magnitude = oracle.float_rows_f64(x, block.router_rows)
+    assert np.all(np.abs(scores - exact) <= (512 / 64 + 8) * 2.0 ** -24 * magnitude)
+    per_row = 4 + 1
+    sel_gpu = to_host(scratch["selected_experts"], np.uint32)[:rows * per_row].reshape(rows, per_row)
+    selected, weights = block.route(x, scores, 4)
+    assert np.array_equal(sel_gpu, selected)
+    block.router_rows = None
+    _, _, again = run_moe(block, x, scores, 4)
+    assert np.array_equal(got, again)
+    want = expected(block, x, selected, weights, None)
+    err = synthetic.bf16_to_f32(got).astype(np.float64) - want
     assert np.linalg.norm(err) / np.linalg.norm(want) <= 1e-2

@@ -1,0 +1,140 @@
+"""The producers either side of the projections through the C ABI: the RMS norm (Normalization::addRms) against the
+reference's own acceptance (every output the fp64 norm rounded once to bf16, dev/tests/engine/NormReference.hpp),
+its prefill table bit for bit against the oracle's and as the prefill tile's prepared input, and the float
+projection of F32 and BF16 rows (addGgufFloat, the MoE router's) against fp64 within its accumulation bound."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import splash_q4 as sq
+import sq_oracle as oracle
+from helpers import make_weights, to_device, to_host, torch
+from splash_q4 import synthetic
+
+pytestmark = pytest.mark.gpu
+
+
+def norm_weights(rng, width, f32):
+    values = rng.uniform(0.25, 2.0, width).astype(np.float32)
+    if f32:
+        return to_device(values), values.astype(np.float64)
+    bits = synthetic.bf16_bits(values)
+    return to_device(bits), synthetic.bf16_to_f32(bits).astype(np.float64)
+
+
+def run_norm(x_bits, w_dev, f32, width, layout=sq.LINEAR_INPUT_PLAIN, storage_rows=None):
+    """The norm of x_bits' rows into an output of storage_rows rows (a prefill plan's input holds its storage rows)."""
+    t = torch()
+    rows = x_bits.shape[0]
+    x = to_device(x_bits)
+    out = t.zeros((storage_rows or rows, width), dtype=t.int16, device="cuda")
+    table = t.zeros((storage_rows or rows, width), dtype=t.int16, device="cuda")
+    sums = t.zeros(storage_rows or rows, dtype=t.float32, device="cuda")
+    scratch = sq.LinearScratch(sq.view(table), sq.view(sums), sq.view(None), sq.view(None), sq.view(None))
+    prepared = sq.PreparedInput()
+    sq.call("sq_norm_add_rms", sq.stream_handle(), sq.view(x), ctypes.byref(sq.NormWeights(sq.view(w_dev), int(f32))),
+            sq.view(out), width, rows, ctypes.byref(scratch), layout, ctypes.byref(prepared))
+    t.cuda.synchronize()
+    return out, table, sums, prepared
+
+
+@pytest.mark.parametrize("width,f32", [(2048, False), (5120, True), (4096, False), (17408, True)])
+def test_rms_norm_rounded_once(width, f32):
+    rng = np.random.default_rng(width + f32)
+    rows = 9
+    x = rng.standard_normal((rows, width)).astype(np.float32)
+    x[1] *= 3e4                     # a row past half's range
+    x[2] *= 1e-3                    # a small one
+    x[3, ::7] = 0.0
+    bits = synthetic.bf16_bits(x)
+    w_dev, w = norm_weights(rng, width, f32)
+    out, _, _, prepared = run_norm(bits, w_dev, f32, width)
+    assert prepared.layout == sq.LINEAR_INPUT_PLAIN
+    got = to_host(out, np.uint16)
+    exact = oracle.rms_norm_f64(bits, w)
+    ok = oracle.rounded_once_to_bf16(got, exact)
+    assert ok.all(), f"{(~ok).sum()} outputs not the fp64 norm rounded once"
+
+
+@pytest.mark.parametrize("width,rows", [(4096, 300), (2048, 5)])
+def test_rms_norm_writes_prefill_table(width, rows):
+    """With the half-rows layout the norm also writes the prefill table of its own output: the oracle's table of
+    the output bits, bit for bit, and the row scales."""
+    rng = np.random.default_rng(31 + rows)
+    x = rng.standard_normal((rows, width)).astype(np.float32)
+    x[0] *= 5e4
+    bits = synthetic.bf16_bits(x)
+    w_dev, _ = norm_weights(rng, width, False)
+    out, table, sums, prepared = run_norm(bits, w_dev, False, width, sq.LINEAR_INPUT_HALF_ROWS)
+    assert prepared.layout == sq.LINEAR_INPUT_HALF_ROWS and prepared.source.ptr == out.data_ptr()
+    want_table, want_scale = oracle.half_rows(to_host(out, np.uint16))
+    assert table.shape[0] == rows
+    assert np.array_equal(to_host(table, np.uint16), want_table)
+    assert np.array_equal(sums.cpu().numpy(), want_scale)
+
+
+def test_prefill_takes_the_norm_table():
+    """A prefill plan whose buffers say the scratch holds its input's table skips its own preparation: it gives the
+    same bits as a prefill that prepares, even after the input rows are overwritten, and reports the table."""
+    t = torch()
+    rng = np.random.default_rng(41)
+    rows, k, n = 300, 2048, 512
+    w = make_weights(rng, sq.FMT_AF4G64, n, k)
+    proj = sq.projection(w.segment())
+    plan = sq.plan_for(sq.prefill_workload(n, k, rows), proj)
+    layout = ctypes.c_uint32()
+    sq.call("sq_linear_plan_input", ctypes.byref(plan), ctypes.byref(layout))
+    assert layout.value == sq.LINEAR_INPUT_HALF_ROWS
+    bits = synthetic.activations(rng, rows, k)
+    w_dev, _ = norm_weights(rng, k, False)
+    normalized, table, sums, prepared = run_norm(bits, w_dev, False, k, sq.LINEAR_INPUT_HALF_ROWS, plan.storage_rows)
+    scratch = sq.LinearScratch(sq.view(table), sq.view(sums), sq.view(None), sq.view(None), sq.view(None))
+    want = t.zeros((plan.storage_rows, n), dtype=t.int16, device="cuda")
+    sq.linear_add(plan, proj, normalized, want, scratch=scratch)            # prepares its own table
+    t.cuda.synchronize()
+    normalized2, table, sums, prepared = run_norm(bits, w_dev, False, k, sq.LINEAR_INPUT_HALF_ROWS, plan.storage_rows)
+    assert t.equal(normalized2, normalized)
+    scratch = sq.LinearScratch(sq.view(table), sq.view(sums), sq.view(None), sq.view(None), sq.view(None))
+    normalized2.fill_(0x7F00)       # the table still holds the rows; the rows themselves are gone
+    got = t.zeros_like(want)
+    after = sq.PreparedInput()
+    buffers = sq.LinearBuffers(sq.view(normalized2), sq.view(got), sq.view(None), sq.view(None), scratch, prepared)
+    sq.call("sq_linear_add_prepared", sq.stream_handle(), ctypes.byref(buffers), ctypes.byref(proj),
+            ctypes.byref(plan), None, ctypes.byref(after))
+    t.cuda.synchronize()
+    assert t.equal(got[:rows], want[:rows])
+    assert after.layout == sq.LINEAR_INPUT_HALF_ROWS and after.source.ptr == normalized2.data_ptr()
+
+
+@pytest.mark.parametrize("f32_rows,f32_out", [(True, True), (False, True), (True, False)])
+def test_float_rows(f32_rows, f32_out):
+    t = torch()
+    rng = np.random.default_rng(51 + 2 * f32_rows + f32_out)
+    rows, n, k, stride, offset = 37, 128, 2048, 136, 5
+    x = synthetic.activations(rng, rows, k)
+    values = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    if f32_rows:
+        w_dev, w = to_device(values), values
+        seg = sq.Segment(sq.view(w_dev), sq.view(None), sq.view(None), n, k, 0, sq.FLOAT32_ROWS)
+    else:
+        wb = synthetic.bf16_bits(values)
+        w_dev, w = to_device(wb), synthetic.bf16_to_f32(wb)
+        seg = sq.Segment(sq.view(w_dev), sq.view(None), sq.view(None), n, k, 0, sq.FMT_BF16)
+    out = t.zeros((rows, stride), dtype=t.float32 if f32_out else t.int16, device="cuda")
+    x_dev = to_device(x)
+    sq.call("sq_float_add", sq.stream_handle(), sq.view(x_dev), ctypes.byref(seg), sq.view(out), rows, stride,
+            offset, sq.OUTPUT_F32 if f32_out else sq.OUTPUT_BF16)
+    t.cuda.synchronize()
+    exact, magnitude = oracle.float_rows_f64(x, w)
+    host = out.cpu().numpy()
+    got = host[:, offset:offset + n].astype(np.float64) if f32_out else \
+        synthetic.bf16_to_f32(host.view(np.uint16)[:, offset:offset + n]).astype(np.float64)
+    # Each lane sums k / 64 products in a chain, then a 6-level butterfly: (k / 64 + 8) roundings of sum |x w| at
+    # most, plus half a bf16 ulp of the result for a bf16 destination.
+    bound = (k / 64 + 8) * 2.0 ** -24 * magnitude
+    if not f32_out:
+        bound = bound + 0.5 * oracle.ulp_bf16(exact)
+    assert np.all(np.abs(got - exact) <= bound)
+    untouched = np.delete(host, np.s_[offset:offset + n], axis=1)
+    assert not untouched.any()

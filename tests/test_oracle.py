@@ -301,3 +301,57 @@ def test_cpu_baseline_matches_fp64(fmt):
     value, magnitude, inputs, largest = oracle.project_f64(x, values)
     bound = oracle.projection_bound(magnitude, inputs, largest, False) + np.abs(value) * 2.0 ** -8
     assert secs > 0 and np.all(np.abs(got - value) <= bound)
+
+
+def _bf16(values):
+    return (np.asarray(values, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def test_rms_norm_oracle_invariants():
+    """rms_norm_f64 is scale-free (a missing square root or mean breaks it) and, with unit weights, leaves each row
+    with mean square ms / (ms + eps) (a dropped epsilon or a sum in place of the mean breaks that)."""
+    rng = np.random.default_rng(21)
+    x = _bf16(rng.standard_normal((4, 256)))
+    x4 = _bf16(4 * oracle.bf16_values(x))          # exact: a power of two
+    ones = np.ones(256)
+    a, b = oracle.rms_norm_f64(x, ones), oracle.rms_norm_f64(x4, ones)
+    assert np.allclose(a, b, rtol=1e-6)
+    ms = (oracle.bf16_values(x) ** 2).mean(axis=1)
+    assert np.allclose((a * a).mean(axis=1), ms / (ms + oracle.RMS_EPSILON), rtol=1e-12)
+    w = rng.uniform(0.5, 2.0, 256)
+    assert np.allclose(oracle.rms_norm_f64(x, w), a * w[None, :], rtol=1e-15)
+
+
+def test_rounded_once_to_bf16():
+    """The reference's acceptance of a norm output: the exact value rounded once to bf16 passes, one ulp off fails."""
+    exact = np.array([1.0 + 2 ** -9 + 2 ** -12, -3.3, 1e-3, 65.0])
+    rounded = _bf16(exact)
+    assert oracle.rounded_once_to_bf16(rounded, exact).all()
+    assert not oracle.rounded_once_to_bf16(rounded + 1, exact).any()
+
+
+def test_half_rows_round_trip():
+    """The prefill table holds each row exactly: undoing the chunk order and the power of two gives the bf16 row
+    back; a row past half's range takes the smallest shift that brings it below 2^16."""
+    rng = np.random.default_rng(22)
+    x = rng.standard_normal((3, 128)).astype(np.float32)
+    x[2, 5] = 1.0e5
+    bits = _bf16(x)
+    table, scale = oracle.half_rows(bits)
+    assert scale.tolist() == [1.0, 1.0, 2.0]
+    back = np.empty((3, 128))
+    for v in range(16):
+        g, c = divmod(v, 4)
+        back[:, 32 * g + 4 * c:32 * g + 4 * c + 4] = table[:, 8 * v:8 * v + 4].view(np.float16)
+        back[:, 32 * g + 16 + 4 * c:32 * g + 20 + 4 * c] = table[:, 8 * v + 4:8 * v + 8].view(np.float16)
+    assert np.array_equal(back * scale[:, None], oracle.bf16_values(bits))
+
+
+def test_float_rows_exact_on_integers():
+    """Small integers multiply and sum exactly: the projection equals integer arithmetic, its magnitude too."""
+    rng = np.random.default_rng(23)
+    xi = rng.integers(-8, 9, (5, 64))
+    wi = rng.integers(-8, 9, (7, 64))
+    exact, magnitude = oracle.float_rows_f64(_bf16(xi), wi.astype(np.float32))
+    assert np.array_equal(exact, (xi @ wi.T).astype(np.float64))
+    assert np.array_equal(magnitude, (np.abs(xi) @ np.abs(wi).T).astype(np.float64))
