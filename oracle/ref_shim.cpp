@@ -28,6 +28,23 @@ int sqref_repack(uint32_t fmt, const uint8_t *native, uint32_t N, uint32_t K, ui
   }
 }
 
+// repack with plane1 as well (formats with high bits: Q5_K, Q6_K).
+int sqref_repack_planes(uint32_t fmt, const uint8_t *native, uint32_t N, uint32_t K, uint8_t *plane0,
+                        uint8_t *plane1, uint8_t *meta, float *values) {
+  try {
+    const std::vector<uint8_t> in(native, native + size_t(N) * rowBytes(Fmt(fmt), K));
+    std::vector<float> v;
+    const Packed p = repack(Fmt(fmt), in, N, K, &v);
+    std::memcpy(plane0, p.w0.data(), p.w0.size());
+    if (plane1 && kQuantFormats[fmt].plane1_bytes) std::memcpy(plane1, p.w1.data(), p.w1.size());
+    std::memcpy(meta, p.meta.data(), p.meta.size());
+    std::memcpy(values, v.data(), v.size() * sizeof(float));
+    return 0;
+  } catch (...) {
+    return -1;
+  }
+}
+
 // The test fixture of GgufFixtures.hpp:148-165 through the reference's makeNative (GgufFixtures.hpp itself needs
 // Foundation, so its three-line scale draw is restated here and handed to makeNative).
 int sqref_fixture(uint32_t fmt, uint32_t rows, uint32_t K, uint32_t seed, uint8_t *native) {

@@ -15,17 +15,28 @@
 
 int sqo_format_info(uint32_t fmt, sqo_format *out) {
   /* {ggml_type, block_elements, block_bytes, plane0_bytes, plane1_bytes, meta_bytes, meta_groups}:
-   * q4k QuantFormat.h:159; af4g32/64/128 QuantFormat.h:185-187 (ggml_type QUANT_AFFINE_TYPE(4, g)). */
+   * q4k QuantFormat.h:159, q5k :162, q6k :163, q80 :165; af4g32/64/128 :185-187 and af8g64 :192 (ggml_type
+   * QUANT_AFFINE_TYPE(bits, g)). */
   switch (fmt) {
     case SQO_FMT_Q4K: *out = (sqo_format){12, 256, 144, 16, 0, 16, 8}; return 0;
+    case SQO_FMT_Q5K: *out = (sqo_format){13, 256, 176, 16, 4, 16, 8}; return 0;
+    case SQO_FMT_Q6K: *out = (sqo_format){14, 256, 210, 16, 8, 20, 8}; return 0;
+    case SQO_FMT_Q80: *out = (sqo_format){8, 32, 34, 32, 0, 2, 1}; return 0;
     case SQO_FMT_AF4G32: *out = (sqo_format){0x4D4C0000u | (4u << 8) | 32u, 32, 20, 16, 0, 4, 1}; return 0;
     case SQO_FMT_AF4G64: *out = (sqo_format){0x4D4C0000u | (4u << 8) | 64u, 64, 36, 16, 0, 4, 2}; return 0;
     case SQO_FMT_AF4G128: *out = (sqo_format){0x4D4C0000u | (4u << 8) | 128u, 128, 68, 16, 0, 4, 4}; return 0;
+    case SQO_FMT_AF8G64: *out = (sqo_format){0x4D4C0000u | (8u << 8) | 64u, 64, 68, 32, 0, 4, 2}; return 0;
     default: return -1;
   }
 }
 
-static int affine(uint32_t fmt) { return fmt == SQO_FMT_AF4G32 || fmt == SQO_FMT_AF4G64 || fmt == SQO_FMT_AF4G128; }
+static int affine(uint32_t fmt) {
+  return fmt == SQO_FMT_AF4G32 || fmt == SQO_FMT_AF4G64 || fmt == SQO_FMT_AF4G128 || fmt == SQO_FMT_AF8G64;
+}
+static uint32_t affine_bits(uint32_t fmt) { return fmt == SQO_FMT_AF8G64 ? 8 : 4; }
+/* Byte offsets in block_q6_K (GgufFormatReference.hpp kQ6KScales, kQ6KD; llama.cpp's ql[128] qh[64] scales[16] d). */
+#define SQO_Q6K_SCALES 192u
+#define SQO_Q6K_D 208u
 
 /* quant_slot (QuantFormat.h:254): element e of a group of 32 sits at slot 8c + 2p + (e & 1). */
 uint32_t sqo_quant_slot(uint32_t e) { return 8 * ((e >> 2) & 3) + 4 * (e >> 4) + (e & 3); }
@@ -86,7 +97,8 @@ int sqo_mlx_native(uint32_t fmt, uint32_t rows, uint32_t K, const uint8_t *weigh
                    const uint16_t *biases, uint8_t *native) {
   sqo_format f;
   if (!affine(fmt) || sqo_format_info(fmt, &f) || K % f.block_elements) return -1;
-  const uint32_t group = f.block_elements, group_bytes = group / 2, groups = K / group, row_codes = K / 2;
+  const uint32_t bits = affine_bits(fmt), group = f.block_elements, group_bytes = group * bits / 8, groups = K / group,
+                 row_codes = K * bits / 8;
   uint8_t *out = native;
   for (uint32_t r = 0; r < rows; ++r)
     for (uint32_t g = 0; g < groups; ++g) {
@@ -116,6 +128,27 @@ static void unpack_pairs(const uint8_t src[16], uint8_t slots[32]) {
   }
 }
 
+/* packBits (GgufFormatReference.hpp:331-337): the slots as a little-endian string of `bits`-bit fields. */
+static void pack_bits(const uint8_t slots[32], uint32_t bits, uint8_t *dst) {
+  const uint32_t per = 32 / bits;
+  for (uint32_t w = 0; w < bits; ++w) {
+    uint32_t v = 0;
+    for (uint32_t i = 0; i < per; ++i) v |= (uint32_t)slots[w * per + i] << (bits * i);
+    memcpy(dst + 4 * w, &v, 4);
+  }
+}
+static void unpack_bits(const uint8_t *src, uint32_t bits, uint8_t slots[32]) {
+  const uint32_t per = 32 / bits, mask = bits == 8 ? 0xFFu : (1u << bits) - 1;
+  for (uint32_t w = 0; w < bits; ++w) {
+    uint32_t v;
+    memcpy(&v, src + 4 * w, 4);
+    for (uint32_t i = 0; i < per; ++i) slots[w * per + i] = (uint8_t)((v >> (bits * i)) & mask);
+  }
+}
+/* The widths of a format's low codes (plane0) and high bits (plane1). */
+static uint32_t low_bits(uint32_t fmt) { return fmt == SQO_FMT_Q80 || fmt == SQO_FMT_AF8G64 ? 8 : 4; }
+static uint32_t high_bits(uint32_t fmt) { return fmt == SQO_FMT_Q5K ? 1 : fmt == SQO_FMT_Q6K ? 2 : 0; }
+
 /* scale_min_k4 (GgufFormatReference.hpp:323-326), llama.cpp's get_scale_min_k4. */
 static void scale_min_k4(const uint8_t *sc, uint32_t j, uint8_t *s, uint8_t *m) {
   if (j < 4) {
@@ -127,12 +160,15 @@ static void scale_min_k4(const uint8_t *sc, uint32_t j, uint8_t *s, uint8_t *m) 
   }
 }
 
-/* The codes (by element) and fp32 values of group g of a native row: groupPack affine and Q4_K branches
- * (GgufFormatReference.hpp:345-374). Affine value = fma(code, s, z); Q4_K value = d*sc*q - dmin*mn. */
+/* The low codes, high bits (by element) and fp32 values of group g of a native row: groupPack
+ * (GgufFormatReference.hpp:349-440), llama.cpp's dequantize_row_* for the GGUF formats. Affine value =
+ * fma(code, s, z); Q4_K d*sc*q - dmin*mn; Q5_K the same of the 5-bit q; Q6_K d*sc*(q - 32) with a scale per 16;
+ * Q8_0 d*q. Every product before the last rounding is exact in fp32. */
 static void group_codes(uint32_t fmt, const sqo_format *f, const uint8_t *row, uint32_t g, uint8_t codes[32],
-                        float vals[32]) {
+                        uint8_t highs[32], float vals[32]) {
   const uint8_t *blk = row + (size_t)(g * 32 / f->block_elements) * f->block_bytes;
   const uint32_t j = (g * 32 % f->block_elements) / 32;
+  memset(highs, 0, 32);
   if (affine(fmt)) {
     uint16_t sb, zb;
     memcpy(&sb, blk, 2);
@@ -140,13 +176,36 @@ static void group_codes(uint32_t fmt, const sqo_format *f, const uint8_t *row, u
     const float s = sqo_bf16_to_f32(sb), z = sqo_bf16_to_f32(zb);
     for (uint32_t e = 0; e < 32; ++e) {
       const uint32_t l = 32 * j + e;
-      codes[e] = (uint8_t)((blk[4 + l / 2] >> (4 * (l % 2))) & 15u);
+      codes[e] = affine_bits(fmt) == 8 ? blk[4 + l] : (uint8_t)((blk[4 + l / 2] >> (4 * (l % 2))) & 15u);
       vals[e] = fmaf((float)codes[e], s, z);
     }
     return;
   }
-  /* Q4_K */
-  const uint8_t *q = blk + 16 + (j / 2) * 32;
+  if (fmt == SQO_FMT_Q80) {
+    uint16_t d16;
+    memcpy(&d16, blk, 2);
+    for (uint32_t e = 0; e < 32; ++e) {
+      codes[e] = blk[2 + e];
+      vals[e] = sqo_f16_to_f32(d16) * (float)(int8_t)blk[2 + e];
+    }
+    return;
+  }
+  if (fmt == SQO_FMT_Q6K) {
+    const uint32_t n = j / 4, r = j % 4;
+    const uint8_t *ql = blk + 64 * n, *qh = blk + 128 + 32 * n;
+    const int8_t *sc = (const int8_t *)(blk + SQO_Q6K_SCALES) + 8 * n;
+    uint16_t d16;
+    memcpy(&d16, blk + SQO_Q6K_D, 2);
+    const float d = sqo_f16_to_f32(d16);
+    for (uint32_t k = 0; k < 32; ++k) {
+      codes[k] = (uint8_t)((ql[k + 32 * (r & 1)] >> (4 * (r >> 1))) & 15u);
+      highs[k] = (uint8_t)((qh[k] >> (2 * r)) & 3u);
+      vals[k] = d * (float)sc[2 * r + k / 16] * (float)((int)(codes[k] | (highs[k] << 4)) - 32);
+    }
+    return;
+  }
+  /* Q4_K and Q5_K */
+  const uint8_t *q = blk + (fmt == SQO_FMT_Q5K ? 48 : 16) + (j / 2) * 32, *qh = blk + 16;
   const uint32_t sh = (j % 2) * 4;
   uint16_t d16, m16;
   memcpy(&d16, blk, 2);
@@ -157,60 +216,103 @@ static void group_codes(uint32_t fmt, const sqo_format *f, const uint8_t *row, u
   const float s = sqo_f16_to_f32(d16) * (float)sc, m = sqo_f16_to_f32(m16) * (float)mn;
   for (uint32_t k = 0; k < 32; ++k) {
     codes[k] = (uint8_t)((q[k] >> sh) & 15u);
-    vals[k] = s * (float)codes[k] - m;
+    if (fmt == SQO_FMT_Q5K) highs[k] = (uint8_t)((qh[k] >> j) & 1u);
+    vals[k] = s * (float)(codes[k] | (highs[k] << 4)) - m;
   }
 }
 
-/* repack (GgufFormatReference.hpp:701-725) restating gguf_repack_group's affine and Q4_K branches
- * (gguf_repack.metal:42-74): plane0 [N/64][G][64][16 B], meta [N/64][units][64][meta_bytes]. */
-int sqo_repack(uint32_t fmt, const uint8_t *native, uint32_t N, uint32_t K, uint8_t *plane0, uint8_t *meta,
-               float *values) {
+/* metaPack (GgufFormatReference.hpp:675-690): the block's leading meta_bytes (affine s, z; the K-quant headers;
+ * Q8_0's d), but Q6_K's scales, d and two zero bytes. */
+static void meta_pack(uint32_t fmt, const sqo_format *f, const uint8_t *blk, uint8_t *dst) {
+  if (fmt == SQO_FMT_Q6K) {
+    memcpy(dst, blk + SQO_Q6K_SCALES, 16);
+    memcpy(dst + 16, blk + SQO_Q6K_D, 2);
+    dst[18] = dst[19] = 0;
+    return;
+  }
+  memcpy(dst, blk, f->meta_bytes);
+}
+
+/* repack (GgufFormatReference.hpp:701-725) restating gguf_repack_group (gguf_repack.metal:42-74): plane0
+ * [N/64][G][64][plane0_bytes] (4-bit low codes pair-interleaved, 8-bit codes as bytes), plane1 [N/64][G][64]
+ * [plane1_bytes] (Q5_K's fifth bits, Q6_K's high two, as bit strings over the slots), meta
+ * [N/64][units][64][meta_bytes]. plane1 may be NULL for a format without one. */
+int sqo_repack(uint32_t fmt, const uint8_t *native, uint32_t N, uint32_t K, uint8_t *plane0, uint8_t *plane1,
+               uint8_t *meta, float *values) {
   sqo_format f;
-  if (sqo_format_info(fmt, &f) || K % f.block_elements || N % 64) return -1;
+  if (sqo_format_info(fmt, &f) || K % f.block_elements || N % 64 || (f.plane1_bytes && !plane1)) return -1;
   const uint32_t G = K / 32, units = G / f.meta_groups;
   const size_t row_bytes = (size_t)K / f.block_elements * f.block_bytes;
   for (uint32_t n = 0; n < N; ++n) {
     const uint8_t *row = native + (size_t)n * row_bytes;
     for (uint32_t g = 0; g < G; ++g) {
-      uint8_t codes[32], slots[32];
+      uint8_t codes[32], highs[32], slots[32], hslots[32];
       float vals[32];
-      group_codes(fmt, &f, row, g, codes, vals);
-      for (uint32_t e = 0; e < 32; ++e) slots[sqo_quant_slot(e)] = codes[e];
-      pack_pairs(slots, plane0 + sqo_tile_index(n, g, G) * 16);
+      group_codes(fmt, &f, row, g, codes, highs, vals);
+      for (uint32_t e = 0; e < 32; ++e) {
+        slots[sqo_quant_slot(e)] = codes[e];
+        hslots[sqo_quant_slot(e)] = highs[e];
+      }
+      if (low_bits(fmt) == 4) pack_pairs(slots, plane0 + sqo_tile_index(n, g, G) * 16);
+      else pack_bits(slots, 8, plane0 + sqo_tile_index(n, g, G) * f.plane0_bytes);
+      if (f.plane1_bytes) pack_bits(hslots, high_bits(fmt), plane1 + sqo_tile_index(n, g, G) * f.plane1_bytes);
       if (values)
         for (uint32_t e = 0; e < 32; ++e) values[(size_t)n * K + (size_t)g * 32 + e] = vals[e];
     }
-    /* metaPack (GgufFormatReference.hpp:680-684): the block's leading meta_bytes (affine s, z; Q4_K header). */
     for (uint32_t u = 0; u < units; ++u)
-      memcpy(meta + sqo_tile_index(n, u, units) * f.meta_bytes, row + (size_t)u * f.block_bytes, f.meta_bytes);
+      meta_pack(fmt, &f, row + (size_t)u * f.block_bytes, meta + sqo_tile_index(n, u, units) * f.meta_bytes);
   }
   return 0;
 }
 
-int sqo_unpack(uint32_t fmt, const uint8_t *plane0, const uint8_t *meta, uint32_t N, uint32_t K, uint8_t *native) {
+/* Inverse of sqo_repack: native rows rebuilt from the planes (for the round-trip invariant). */
+int sqo_unpack(uint32_t fmt, const uint8_t *plane0, const uint8_t *plane1, const uint8_t *meta, uint32_t N,
+               uint32_t K, uint8_t *native) {
   sqo_format f;
-  if (sqo_format_info(fmt, &f) || K % f.block_elements || N % 64) return -1;
+  if (sqo_format_info(fmt, &f) || K % f.block_elements || N % 64 || (f.plane1_bytes && !plane1)) return -1;
   const uint32_t G = K / 32, units = G / f.meta_groups;
   const size_t row_bytes = (size_t)K / f.block_elements * f.block_bytes;
+  memset(native, 0, (size_t)N * row_bytes);
   for (uint32_t n = 0; n < N; ++n) {
     uint8_t *row = native + (size_t)n * row_bytes;
-    for (uint32_t u = 0; u < units; ++u)
-      memcpy(row + (size_t)u * f.block_bytes, meta + sqo_tile_index(n, u, units) * f.meta_bytes, f.meta_bytes);
+    for (uint32_t u = 0; u < units; ++u) {
+      const uint8_t *m = meta + sqo_tile_index(n, u, units) * f.meta_bytes;
+      uint8_t *blk = row + (size_t)u * f.block_bytes;
+      if (fmt == SQO_FMT_Q6K) {
+        memcpy(blk + SQO_Q6K_SCALES, m, 16);
+        memcpy(blk + SQO_Q6K_D, m + 16, 2);
+      } else {
+        memcpy(blk, m, f.meta_bytes);
+      }
+    }
     for (uint32_t g = 0; g < G; ++g) {
-      uint8_t slots[32];
-      unpack_pairs(plane0 + sqo_tile_index(n, g, G) * 16, slots);
+      uint8_t slots[32], hslots[32] = {0};
+      if (low_bits(fmt) == 4) unpack_pairs(plane0 + sqo_tile_index(n, g, G) * 16, slots);
+      else unpack_bits(plane0 + sqo_tile_index(n, g, G) * f.plane0_bytes, 8, slots);
+      if (f.plane1_bytes) unpack_bits(plane1 + sqo_tile_index(n, g, G) * f.plane1_bytes, high_bits(fmt), hslots);
       uint8_t *blk = row + (size_t)(g * 32 / f.block_elements) * f.block_bytes;
       const uint32_t j = (g * 32 % f.block_elements) / 32;
       for (uint32_t e = 0; e < 32; ++e) {
-        const uint8_t code = slots[sqo_quant_slot(e)];
-        if (affine(fmt)) {
+        const uint8_t code = slots[sqo_quant_slot(e)], high = hslots[sqo_quant_slot(e)];
+        if (affine(fmt) && affine_bits(fmt) == 8) {
+          blk[4 + 32 * j + e] = code;
+        } else if (affine(fmt)) {
           const uint32_t l = 32 * j + e;
           uint8_t *byte = blk + 4 + l / 2;
           *byte = (uint8_t)((*byte & ~(0xFu << (4 * (l % 2)))) | (code << (4 * (l % 2))));
+        } else if (fmt == SQO_FMT_Q80) {
+          blk[2 + e] = code;
+        } else if (fmt == SQO_FMT_Q6K) {
+          const uint32_t nn = j / 4, r = j % 4;
+          uint8_t *ql = blk + 64 * nn + e + 32 * (r & 1), *qh = blk + 128 + 32 * nn + e;
+          const uint32_t sh = 4 * (r >> 1);
+          *ql = (uint8_t)((*ql & ~(0xFu << sh)) | (code << sh));
+          *qh = (uint8_t)((*qh & ~(3u << (2 * r))) | (high << (2 * r)));
         } else {
-          uint8_t *byte = blk + 16 + (j / 2) * 32 + e;
+          uint8_t *byte = blk + (fmt == SQO_FMT_Q5K ? 48 : 16) + (j / 2) * 32 + e;
           const uint32_t sh = (j % 2) * 4;
           *byte = (uint8_t)((*byte & ~(0xFu << sh)) | (code << sh));
+          if (fmt == SQO_FMT_Q5K) blk[16 + e] = (uint8_t)((blk[16 + e] & ~(1u << j)) | (high << j));
         }
       }
     }
@@ -218,36 +320,55 @@ int sqo_unpack(uint32_t fmt, const uint8_t *plane0, const uint8_t *meta, uint32_
   return 0;
 }
 
-/* Values read from the planes alone: the chunk decode of quant_formats.h (codes by quant_nibble_pairs :94, coef
- * FmtAffine :614-616 and quant_k4_coef :105-118) and the staged fp16 rounding of gguf_staged.h:11-16. */
-int sqo_plane_values(uint32_t fmt, const uint8_t *plane0, const uint8_t *meta, uint32_t N, uint32_t K,
-                     float *values, uint16_t *halves) {
+/* Values read from the planes alone: the chunk decode of quant_formats.h (codes by quant_nibble_pairs :94 and the
+ * bit strings of FmtQ5K/FmtQ6K/FmtQ80 :138-235, coefficients FmtAffine :614-616, quant_k4_coef :105-118 and the Q6_K
+ * and Q8_0 scales) as value = fma(q, s, z), with Q6_K's z = -32 s and Q8_0's q the signed byte; and the staged
+ * fp16 rounding of gguf_staged.h:11-16. */
+int sqo_plane_values(uint32_t fmt, const uint8_t *plane0, const uint8_t *plane1, const uint8_t *meta, uint32_t N,
+                     uint32_t K, float *values, uint16_t *halves) {
   sqo_format f;
-  if (sqo_format_info(fmt, &f) || K % f.block_elements || N % 64) return -1;
+  if (sqo_format_info(fmt, &f) || K % f.block_elements || N % 64 || (f.plane1_bytes && !plane1)) return -1;
   const uint32_t G = K / 32, units = G / f.meta_groups;
   for (uint32_t n = 0; n < N; ++n)
     for (uint32_t g = 0; g < G; ++g) {
-      uint8_t slots[32];
-      unpack_pairs(plane0 + sqo_tile_index(n, g, G) * 16, slots);
+      uint8_t slots[32], hslots[32] = {0};
+      if (low_bits(fmt) == 4) unpack_pairs(plane0 + sqo_tile_index(n, g, G) * 16, slots);
+      else unpack_bits(plane0 + sqo_tile_index(n, g, G) * f.plane0_bytes, 8, slots);
+      if (f.plane1_bytes) unpack_bits(plane1 + sqo_tile_index(n, g, G) * f.plane1_bytes, high_bits(fmt), hslots);
       const uint8_t *m = meta + sqo_tile_index(n, g / f.meta_groups, units) * f.meta_bytes;
-      float s, z;
-      if (affine(fmt)) {
-        uint16_t sb, zb;
-        memcpy(&sb, m, 2);
-        memcpy(&zb, m + 2, 2);
-        s = sqo_bf16_to_f32(sb);
-        z = sqo_bf16_to_f32(zb);
-      } else {
-        uint16_t d16, m16;
-        memcpy(&d16, m, 2);
-        memcpy(&m16, m + 2, 2);
-        uint8_t sc, mn;
-        scale_min_k4(m + 4, g % 8, &sc, &mn);
-        s = sqo_f16_to_f32(d16) * (float)sc;
-        z = -(sqo_f16_to_f32(m16) * (float)mn);
-      }
       for (uint32_t e = 0; e < 32; ++e) {
-        const float v = fmaf((float)slots[sqo_quant_slot(e)], s, z);
+        const uint32_t slot = sqo_quant_slot(e);
+        float s, z, q = (float)(slots[slot] | (hslots[slot] << 4));
+        if (affine(fmt)) {
+          uint16_t sb, zb;
+          memcpy(&sb, m, 2);
+          memcpy(&zb, m + 2, 2);
+          s = sqo_bf16_to_f32(sb);
+          z = sqo_bf16_to_f32(zb);
+        } else if (fmt == SQO_FMT_Q80) {
+          uint16_t d16;
+          memcpy(&d16, m, 2);
+          s = sqo_f16_to_f32(d16);
+          z = 0.0f;
+          q = (float)(int8_t)slots[slot];
+        } else if (fmt == SQO_FMT_Q6K) {
+          uint16_t d16;
+          memcpy(&d16, m + 16, 2);
+          s = sqo_f16_to_f32(d16) * (float)(int8_t)m[2 * (g % 8) + e / 16];
+          z = -32.0f * s;
+        } else {
+          uint16_t d16, m16;
+          memcpy(&d16, m, 2);
+          memcpy(&m16, m + 2, 2);
+          uint8_t sc, mn;
+          scale_min_k4(m + 4, g % 8, &sc, &mn);
+          s = sqo_f16_to_f32(d16) * (float)sc;
+          z = -(sqo_f16_to_f32(m16) * (float)mn);
+        }
+        /* staged_linear (gguf_staged.h:11-16): a format with a code offset multiplies the exact q - Zero by s
+         * (so -0.0 where q = Zero and s < 0, as GGML's d * sc * (q - 32)); the rest take fma(q, s, z). Q8_0
+         * multiplies its signed value by d (QuantInt8, :40-44). */
+        const float v = fmt == SQO_FMT_Q6K ? (q - 32.0f) * s : fmt == SQO_FMT_Q80 ? q * s : fmaf(q, s, z);
         const size_t at = (size_t)n * K + (size_t)g * 32 + e;
         if (values) values[at] = v;
         if (halves) halves[at] = sqo_f32_to_f16(v);
@@ -307,10 +428,13 @@ int sqo_fixture(uint32_t fmt, uint32_t rows, uint32_t K, uint32_t seed, uint8_t 
       for (uint32_t field = 0; field < 4; field += 2)
         if ((blk[field + 1] & 0x7F) == 0x7F && (blk[field] & 0x80)) blk[field + 1] ^= 1;
     } else {
+      /* makeNative: the half d (Q6_K's at its end), and Q4_K's and Q5_K's dmin after it. */
       const uint16_t d = finite_half(&rng);
-      memcpy(blk, &d, 2);
-      const uint16_t m = finite_half(&rng);
-      memcpy(blk + 2, &m, 2);
+      memcpy(blk + (fmt == SQO_FMT_Q6K ? SQO_Q6K_D : 0), &d, 2);
+      if (fmt == SQO_FMT_Q4K || fmt == SQO_FMT_Q5K) {
+        const uint16_t m = finite_half(&rng);
+        memcpy(blk + 2, &m, 2);
+      }
     }
   }
   return 0;
@@ -474,6 +598,8 @@ static void *cpu_worker(void *arg) {
 
 double sqo_cpu_matmul(uint32_t fmt, uint32_t M, uint32_t N, uint32_t K, const uint16_t *x, const uint8_t *plane0,
                       const uint8_t *meta, uint16_t *out, int threads) {
+  /* The CPU baseline runs the 4-bit formats of the headline workloads. */
+  if (fmt != SQO_FMT_Q4K && fmt != SQO_FMT_AF4G32 && fmt != SQO_FMT_AF4G64 && fmt != SQO_FMT_AF4G128) return -1.0;
   struct timespec t0, t1;
   clock_gettime(CLOCK_MONOTONIC, &t0);
   float *xf = (float *)malloc(sizeof(float) * (size_t)M * K);

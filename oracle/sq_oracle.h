@@ -26,9 +26,13 @@ extern "C" {
 
 /* Format ids of the reference's kQuantFormats table (QuantFormat.h:83-133). */
 #define SQO_FMT_Q4K 0u
+#define SQO_FMT_Q5K 3u
+#define SQO_FMT_Q6K 4u
+#define SQO_FMT_Q80 6u
 #define SQO_FMT_AF4G32 25u
 #define SQO_FMT_AF4G64 26u
 #define SQO_FMT_AF4G128 27u
+#define SQO_FMT_AF8G64 35u
 
 typedef struct {
   uint32_t ggml_type, block_elements, block_bytes, plane0_bytes, plane1_bytes, meta_bytes, meta_groups;
@@ -45,17 +49,19 @@ float sqo_f16_to_f32(uint16_t h);
 uint16_t sqo_f32_to_bf16(float f);
 float sqo_bf16_to_f32(uint16_t b);
 
-/* MLX tensors of an af4 format -> the loader's native rows {bf16 s, bf16 z, codes} per group. */
+/* MLX tensors of an affine format -> the loader's native rows {bf16 s, bf16 z, codes} per group. */
 int sqo_mlx_native(uint32_t fmt, uint32_t rows, uint32_t K, const uint8_t *weight, const uint16_t *scales,
                    const uint16_t *biases, uint8_t *native);
-/* Native rows -> plane0 and meta (layout of QuantFormat.h:3-9); values (fp32, [N][K]) may be NULL. */
-int sqo_repack(uint32_t fmt, const uint8_t *native, uint32_t N, uint32_t K, uint8_t *plane0, uint8_t *meta,
-               float *values);
+/* Native rows -> plane0, plane1 (NULL for a format without one) and meta (layout of QuantFormat.h:3-9); values
+ * (fp32, [N][K]) may be NULL. */
+int sqo_repack(uint32_t fmt, const uint8_t *native, uint32_t N, uint32_t K, uint8_t *plane0, uint8_t *plane1,
+               uint8_t *meta, float *values);
 /* Inverse of sqo_repack (for the round-trip invariant). */
-int sqo_unpack(uint32_t fmt, const uint8_t *plane0, const uint8_t *meta, uint32_t N, uint32_t K, uint8_t *native);
+int sqo_unpack(uint32_t fmt, const uint8_t *plane0, const uint8_t *plane1, const uint8_t *meta, uint32_t N,
+               uint32_t K, uint8_t *native);
 /* The fp32 values and the staged tile's fp16 bits of every weight of the planes ([N][K] each, either may be NULL). */
-int sqo_plane_values(uint32_t fmt, const uint8_t *plane0, const uint8_t *meta, uint32_t N, uint32_t K,
-                     float *values, uint16_t *halves);
+int sqo_plane_values(uint32_t fmt, const uint8_t *plane0, const uint8_t *plane1, const uint8_t *meta, uint32_t N,
+                     uint32_t K, float *values, uint16_t *halves);
 /* The reference test fixture: native rows of random bytes, mt19937(seed), finite random half scales. */
 int sqo_fixture(uint32_t fmt, uint32_t rows, uint32_t K, uint32_t seed, uint8_t *native);
 

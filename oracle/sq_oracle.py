@@ -16,6 +16,7 @@ LIBRARY = ORACLE_DIR / "libsq_oracle.so"
 REFERENCE_LIBRARY = ORACLE_DIR / "_ref" / "libsqref.so"
 
 FMT_Q4K, FMT_AF4G32, FMT_AF4G64, FMT_AF4G128 = 0, 25, 26, 27
+FMT_Q5K, FMT_Q6K, FMT_Q80, FMT_AF8G64 = 3, 4, 6, 35
 
 _lib = None
 _ref = None
@@ -73,6 +74,10 @@ def plane_sizes(fmt: int, n: int, k: int) -> tuple[int, int]:
     return n * g * f["plane0_bytes"], n * (g // f["meta_groups"]) * f["meta_bytes"]
 
 
+def plane1_size(fmt: int, n: int, k: int) -> int:
+    return n * (k // 32) * format_info(fmt)["plane1_bytes"]
+
+
 def mlx_native(fmt: int, weight: np.ndarray, scales: np.ndarray, biases: np.ndarray, rows: int, k: int) -> np.ndarray:
     native = np.zeros(rows * row_bytes(fmt, k), dtype=np.uint8)
     w = np.ascontiguousarray(weight).view(np.uint8)
@@ -82,29 +87,39 @@ def mlx_native(fmt: int, weight: np.ndarray, scales: np.ndarray, biases: np.ndar
     return native
 
 
-def repack(fmt: int, native: np.ndarray, n: int, k: int):
-    """(plane0, meta, fp32 values [n][k]) of native rows."""
+def repack_planes(fmt: int, native: np.ndarray, n: int, k: int):
+    """(plane0, plane1 (None for a format without one), meta, fp32 values [n][k]) of native rows."""
     p0, m = plane_sizes(fmt, n, k)
     plane0, meta = np.zeros(p0, np.uint8), np.zeros(m, np.uint8)
+    p1 = plane1_size(fmt, n, k)
+    plane1 = np.zeros(p1, np.uint8) if p1 else None
     values = np.zeros((n, k), np.float32)
     rc = lib().sqo_repack(fmt, _ptr(np.ascontiguousarray(native, np.uint8), c_uint8), n, k, _ptr(plane0, c_uint8),
-                          _ptr(meta, c_uint8), _ptr(values, c_float))
+                          _ptr(plane1, c_uint8) if p1 else None, _ptr(meta, c_uint8), _ptr(values, c_float))
     assert rc == 0
+    return plane0, plane1, meta, values
+
+
+def repack(fmt: int, native: np.ndarray, n: int, k: int):
+    """(plane0, meta, fp32 values [n][k]) of native rows of a format without a plane1."""
+    plane0, plane1, meta, values = repack_planes(fmt, native, n, k)
+    assert plane1 is None, "this format has a plane1: use repack_planes"
     return plane0, meta, values
 
 
-def unpack(fmt: int, plane0: np.ndarray, meta: np.ndarray, n: int, k: int) -> np.ndarray:
+def unpack(fmt: int, plane0: np.ndarray, meta: np.ndarray, n: int, k: int, plane1: np.ndarray | None = None):
     native = np.zeros(n * row_bytes(fmt, k), np.uint8)
-    rc = lib().sqo_unpack(fmt, _ptr(plane0, c_uint8), _ptr(meta, c_uint8), n, k, _ptr(native, c_uint8))
+    rc = lib().sqo_unpack(fmt, _ptr(plane0, c_uint8), _ptr(plane1, c_uint8) if plane1 is not None else None,
+                          _ptr(meta, c_uint8), n, k, _ptr(native, c_uint8))
     assert rc == 0
     return native
 
 
-def plane_values(fmt: int, plane0: np.ndarray, meta: np.ndarray, n: int, k: int):
+def plane_values(fmt: int, plane0: np.ndarray, meta: np.ndarray, n: int, k: int, plane1: np.ndarray | None = None):
     """(fp32 values, fp16 bits) [n][k] decoded from the planes."""
     values, halves = np.zeros((n, k), np.float32), np.zeros((n, k), np.uint16)
-    rc = lib().sqo_plane_values(fmt, _ptr(plane0, c_uint8), _ptr(meta, c_uint8), n, k, _ptr(values, c_float),
-                                _ptr(halves, c_uint16))
+    rc = lib().sqo_plane_values(fmt, _ptr(plane0, c_uint8), _ptr(plane1, c_uint8) if plane1 is not None else None,
+                                _ptr(meta, c_uint8), n, k, _ptr(values, c_float), _ptr(halves, c_uint16))
     assert rc == 0
     return values, halves
 

@@ -355,3 +355,83 @@ def test_float_rows_exact_on_integers():
     exact, magnitude = oracle.float_rows_f64(_bf16(xi), wi.astype(np.float32))
     assert np.array_equal(exact, (xi @ wi.T).astype(np.float64))
     assert np.array_equal(magnitude, (np.abs(xi) @ np.abs(wi).T).astype(np.float64))
+
+
+NEW_FORMATS = [oracle.FMT_Q5K, oracle.FMT_Q6K, oracle.FMT_Q80, oracle.FMT_AF8G64]
+
+
+@pytest.mark.parametrize("name", ["q4k", "q5k", "q6k", "q80"])
+def test_gguf_golden_hashes(name):
+    """llama.cpp 7ab4ee7's fp32 dequantisation of the reference's fixture of each GGUF format (256 x 1024, seed
+    7 + format id): SHA-256 equal (gguf_reference_test.mm:20-41; goldens.json gguf_dequantization)."""
+    entry = json.loads((GOLDEN / "weight_goldens.json").read_text())["formats"][name]
+    native = oracle.fixture(entry["id"], 256, 1024, entry["seed"])
+    _, _, _, values = oracle.repack_planes(entry["id"], native, 256, 1024)
+    assert hashlib.sha256(values.tobytes()).hexdigest() == entry["sha256"]
+
+
+@pytest.mark.parametrize("fmt", NEW_FORMATS)
+def test_new_formats_match_reference_oracle(fmt):
+    """Q5_K, Q6_K, Q8_0 and af8g64: the fixture bytes, plane0, plane1, meta and values equal the reference's own
+    CPU oracle's (GgufFormatReference.hpp groupPack/metaPack/repack, built into oracle/_ref)."""
+    ref = oracle.reference()
+    if ref is None:
+        pytest.skip("oracle/_ref not built (no reference checkout when the oracle was built)")
+    import ctypes
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+    n, k = 128, 1024
+    for seed in (3, 7):
+        native = oracle.fixture(fmt, n, k, seed)
+        theirs = np.zeros_like(native)
+        assert ref.sqref_fixture(fmt, n, k, seed, ptr(theirs)) == 0
+        assert np.array_equal(native, theirs)
+        plane0, plane1, meta, values = oracle.repack_planes(fmt, native, n, k)
+        p0, m, v = np.zeros_like(plane0), np.zeros_like(meta), np.zeros_like(values)
+        p1 = np.zeros_like(plane1) if plane1 is not None else None
+        assert ref.sqref_repack_planes(fmt, ptr(native), n, k, ptr(p0), ptr(p1), ptr(m), ptr(v)) == 0
+        assert np.array_equal(plane0, p0) and np.array_equal(meta, m)
+        assert plane1 is None or np.array_equal(plane1, p1)
+        assert np.array_equal(values.view(np.uint32), v.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", NEW_FORMATS)
+def test_new_formats_round_trip_and_plane_values(fmt):
+    """Planes and meta hold every byte of the native blocks, and the values decoded from the planes alone equal
+    the native decode's bit for bit."""
+    rng = np.random.default_rng(100 + fmt)
+    n, k = 128, 512
+    native = oracle.fixture(fmt, n, k, 5)
+    if fmt == oracle.FMT_AF8G64:
+        native = rng.integers(0, 256, size=native.size, dtype=np.uint8)
+    plane0, plane1, meta, values = oracle.repack_planes(fmt, native, n, k)
+    assert np.array_equal(oracle.unpack(fmt, plane0, meta, n, k, plane1), native)
+    decoded, halves = oracle.plane_values(fmt, plane0, meta, n, k, plane1)
+    finite = ~np.isnan(values)
+    assert np.array_equal(np.isnan(decoded), ~finite)
+    assert np.array_equal(decoded[finite].view(np.uint32), values[finite].view(np.uint32))
+    with np.errstate(over="ignore"):   # fixture values past half's range round to infinity on both sides
+        assert np.array_equal(halves[finite], values[finite].astype(np.float16).view(np.uint16))
+
+
+@pytest.mark.parametrize("group", [64])
+def test_mlx_fixture_values_bit_exact_8bit(group):
+    """MLX 0.32.3's reading of its own 8-bit affine quantization (group 64): fp32 values fma(code, s, z) bit for
+    bit from the loader's native blocks and from the planes."""
+    entry = next(f for f in json.loads((GOLDEN / "mlx_affine8.json").read_text())["formats"] if f["group"] == group)
+    rows, k, fmt = entry["rows"], entry["columns"], oracle.FMT_AF8G64
+    weight, scales, biases = _hex(entry["weight"], np.uint8), _hex(entry["scales"], np.uint16), _hex(entry["biases"], np.uint16)
+    codes, values = _hex(entry["codes"], np.uint8).reshape(rows, k), _hex(entry["values"], np.uint32).reshape(rows, k)
+    native = oracle.mlx_native(fmt, weight, scales, biases, rows, k)
+    n = 64
+    padded = np.zeros(n * oracle.row_bytes(fmt, k), np.uint8)
+    padded[: native.size] = native
+    plane0, plane1, meta, got = oracle.repack_planes(fmt, padded, n, k)
+    assert plane1 is None
+    assert np.array_equal(got[:rows].view(np.uint32), values)
+    decoded, _ = oracle.plane_values(fmt, plane0, meta, n, k)
+    assert np.array_equal(decoded[:rows].view(np.uint32), values)
+    f = oracle.format_info(fmt)
+    for r in range(rows):
+        for b in range(k // group):
+            blk = native[(r * (k // group) + b) * f["block_bytes"]:][: f["block_bytes"]]
+            assert np.array_equal(blk[4:], codes[r, b * group:(b + 1) * group])
