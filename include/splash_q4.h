@@ -28,9 +28,13 @@ extern "C" {
 #define SQ_RUNTIME_ERROR 2    /* a HIP launch or runtime failure */
 
 #define SQ_FMT_Q4K 0u
+#define SQ_FMT_Q5K 3u
+#define SQ_FMT_Q6K 4u
+#define SQ_FMT_Q80 6u
 #define SQ_FMT_AF4G32 25u
 #define SQ_FMT_AF4G64 26u
 #define SQ_FMT_AF4G128 27u
+#define SQ_FMT_AF8G64 35u
 /* Float rows (QuantizedSegment::rows, Weights.hpp:67-81): F32 rows carry the format id kFloat32, BF16 rows
  * GGUF_FMT_BF16; the float projection multiplies them unrounded in fp32. */
 #define SQ_FMT_BF16 41u

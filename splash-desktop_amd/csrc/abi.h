@@ -20,9 +20,13 @@
 // ---------------------------------------------------------------- format ids (QuantFormat.h:83-133)
 // The ids keep the reference's numbering, so a caller's format ids mean the same formats here.
 #define SQ_FMT_Q4K 0u
+#define SQ_FMT_Q5K 3u
+#define SQ_FMT_Q6K 4u
+#define SQ_FMT_Q80 6u
 #define SQ_FMT_AF4G32 25u
 #define SQ_FMT_AF4G64 26u
 #define SQ_FMT_AF4G128 27u
+#define SQ_FMT_AF8G64 35u
 #define SQ_FMT_BF16 41u   // as float rows only (QuantizedSegment::rows)
 #define SQ_FMT_COUNT 48u
 // QuantizedSegment::kFloat32 (Weights.hpp:81): the format id of F32 rows, which no format row names.
@@ -43,25 +47,48 @@ struct SqQuantFormat {
   uint32_t meta_groups;    // groups of 32 per meta unit
 };
 
-// The formats this build runs: Q4_K (QuantFormat.h:159) and the 4-bit MLX affine ones (QuantFormat.h:185-187).
-// Every other id is a format of the reference this build does not take; the host rejects it before any launch.
+// The formats this build runs: Q4_K, Q5_K, Q6_K and Q8_0 (QuantFormat.h:159,162,163,165), the 4-bit MLX affine
+// ones (QuantFormat.h:185-187) and af8g64 (QuantFormat.h:192). Every other id is a format of the reference this
+// build does not take; the host rejects it before any launch.
 SQ_HD inline bool sq_format_supported(uint32_t f) {
+  return f == SQ_FMT_Q4K || f == SQ_FMT_Q5K || f == SQ_FMT_Q6K || f == SQ_FMT_Q80 || f == SQ_FMT_AF4G32 ||
+         f == SQ_FMT_AF4G64 || f == SQ_FMT_AF4G128 || f == SQ_FMT_AF8G64;
+}
+// The formats the decode, prefill and MoE tiles run (the load-time repack and the dequantisation take every
+// supported one).
+SQ_HD inline bool sq_tile_format(uint32_t f) {
   return f == SQ_FMT_Q4K || f == SQ_FMT_AF4G32 || f == SQ_FMT_AF4G64 || f == SQ_FMT_AF4G128;
 }
 SQ_HD inline SqQuantFormat sq_format(uint32_t f) {
   switch (f) {
     case SQ_FMT_Q4K: return {12u, 256u, 144u, 16u, 0u, 16u, 8u};
+    case SQ_FMT_Q5K: return {13u, 256u, 176u, 16u, 4u, 16u, 8u};
+    case SQ_FMT_Q6K: return {14u, 256u, 210u, 16u, 8u, 20u, 8u};
+    case SQ_FMT_Q80: return {8u, 32u, 34u, 32u, 0u, 2u, 1u};
     case SQ_FMT_AF4G32: return {0x4D4C0000u | (4u << 8) | 32u, 32u, 20u, 16u, 0u, 4u, 1u};
     case SQ_FMT_AF4G64: return {0x4D4C0000u | (4u << 8) | 64u, 64u, 36u, 16u, 0u, 4u, 2u};
     case SQ_FMT_AF4G128: return {0x4D4C0000u | (4u << 8) | 128u, 128u, 68u, 16u, 0u, 4u, 4u};
+    case SQ_FMT_AF8G64: return {0x4D4C0000u | (8u << 8) | 64u, 64u, 68u, 32u, 0u, 4u, 2u};
     default: return {0u, 0u, 0u, 0u, 0u, 0u, 0u};
   }
 }
 SQ_HD inline const char *sq_format_name(uint32_t f) {
-  return f == SQ_FMT_Q4K ? "q4k" : f == SQ_FMT_AF4G32 ? "af4g32" : f == SQ_FMT_AF4G64 ? "af4g64"
-       : f == SQ_FMT_AF4G128 ? "af4g128" : "unsupported";
+  switch (f) {
+    case SQ_FMT_Q4K: return "q4k";
+    case SQ_FMT_Q5K: return "q5k";
+    case SQ_FMT_Q6K: return "q6k";
+    case SQ_FMT_Q80: return "q80";
+    case SQ_FMT_AF4G32: return "af4g32";
+    case SQ_FMT_AF4G64: return "af4g64";
+    case SQ_FMT_AF4G128: return "af4g128";
+    case SQ_FMT_AF8G64: return "af8g64";
+    default: return "unsupported";
+  }
 }
-SQ_HD inline bool sq_affine_format(uint32_t f) { return f >= SQ_FMT_AF4G32 && f <= SQ_FMT_AF4G128; }
+SQ_HD inline bool sq_affine_format(uint32_t f) { return (f >= SQ_FMT_AF4G32 && f <= SQ_FMT_AF4G128) || f == SQ_FMT_AF8G64; }
+// Byte offsets in block_q6_K (llama.cpp: ql[128], qh[64], int8 scales[16], half d).
+#define SQ_Q6K_SCALES 192u
+#define SQ_Q6K_D 208u
 
 // Element e (0..31) of a group sits at slot 8c + 2p + (e & 1): chunk c = (e >> 2) & 3, pair p = 2 (e >> 4) +
 // ((e >> 1) & 1) (QuantFormat.h:18-26,254). Word c of a 4-bit plane unit holds slots 8c..8c+7, pair p's first

@@ -272,7 +272,11 @@ int sq_gguf_repack(void *graph, sq_buffer src, sq_buffer dst, const void *params
     if (p.src_row_bytes < rowBytes) throw std::invalid_argument("repack source rows are shorter than their blocks");
     const uint64_t groups = p.input_size / 32, units = groups / f.meta_groups;
     const uint64_t plane0 = uint64_t(p.rows) * groups * f.plane0_bytes, meta = uint64_t(p.rows) * units * f.meta_bytes;
+    const uint64_t plane1 = uint64_t(p.rows) * groups * f.plane1_bytes;
     if (p.dst_meta < plane0) throw std::invalid_argument("repack meta offset overlaps plane0");
+    if (plane1 && (p.dst_plane1 < plane0 || (p.dst_plane1 < p.dst_meta + meta && p.dst_meta < p.dst_plane1 + plane1)))
+      throw std::invalid_argument("repack plane1 overlaps plane0 or meta");
+    if (plane1) requireBytes(buf(dst), uint64_t(p.dst_plane1) + plane1, "repack destination");
     requireBytes(buf(src), (uint64_t(p.rows) - 1) * p.src_row_bytes + rowBytes, "repack source");
     requireBytes(buf(dst), uint64_t(p.dst_meta) + meta, "repack destination");
     launched(sq::kern::launch_repack(static_cast<const uint8_t *>(src.ptr), static_cast<uint8_t *>(dst.ptr), p,
@@ -284,15 +288,15 @@ int sq_gguf_repack(void *graph, sq_buffer src, sq_buffer dst, const void *params
 int sq_mlx_repack(void *graph, uint32_t fmt, uint32_t rows, uint32_t k, sq_buffer weight, sq_buffer scales,
                   sq_buffer biases, sq_buffer plane0, sq_buffer meta) {
   return guarded([&] {
-    if (!sq_affine_format(fmt)) throw std::invalid_argument("the MLX repack takes a 4-bit MLX affine format");
+    if (!sq_affine_format(fmt)) throw std::invalid_argument("the MLX repack takes a 4-bit or 8-bit MLX affine format");
     const SqQuantFormat f = sq_format(fmt);
     if (!rows || rows % SQ_TILE_ROWS || !k || k % f.block_elements)
       throw std::invalid_argument("an MLX repack takes whole plane tiles of rows and whole groups");
-    const uint64_t groups = k / f.block_elements;
-    requireBytes(buf(weight), uint64_t(rows) * k / 2, "MLX weight");
+    const uint64_t groups = k / f.block_elements, bits = fmt == SQ_FMT_AF8G64 ? 8 : 4;
+    requireBytes(buf(weight), uint64_t(rows) * k * bits / 8, "MLX weight");
     requireBytes(buf(scales), uint64_t(rows) * groups * 2, "MLX scales");
     requireBytes(buf(biases), uint64_t(rows) * groups * 2, "MLX biases");
-    requireBytes(buf(plane0), uint64_t(rows) * (k / 32) * 16, "plane0");
+    requireBytes(buf(plane0), uint64_t(rows) * (k / 32) * f.plane0_bytes, "plane0");
     requireBytes(buf(meta), uint64_t(rows) * groups * 4, "meta");
     launched(sq::kern::launch_mlx_repack(fmt, static_cast<const uint32_t *>(weight.ptr),
                                          static_cast<const uint16_t *>(scales.ptr),
@@ -322,7 +326,8 @@ int sq_dequant(void *graph, const sq_segment *s, sq_buffer values, sq_buffer hal
     const uint64_t n = uint64_t(q.outputSize) * q.inputSize;
     if (values.ptr) requireBytes(buf(values), n * 4, "dequant values");
     if (halves.ptr) requireBytes(buf(halves), n * 2, "dequant halves");
-    launched(sq::kern::launch_dequant(q.formatId, q.plane0.as<const uint8_t>(), q.meta.as<const uint8_t>(),
+    launched(sq::kern::launch_dequant(q.formatId, q.plane0.as<const uint8_t>(), q.plane1.as<const uint8_t>(),
+                                      q.meta.as<const uint8_t>(),
                                       q.outputSize, q.inputSize, static_cast<float *>(values.ptr),
                                       static_cast<uint16_t *>(halves.ptr), stream(graph)),
              "dequant");

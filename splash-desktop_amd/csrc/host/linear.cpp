@@ -59,6 +59,8 @@ void requireSegments(const Projection &p, LinearMatrix matrix) {
     throw std::invalid_argument("block projection does not match plan");
   for (const QuantizedSegment &s : p.blocks().segments) {
     if (s.outputSize % SQ_TILE_COLUMNS) throw std::invalid_argument("block segments do not fill whole column tiles");
+    if (!sq_tile_format(s.formatId))
+      throw std::invalid_argument(std::string("the decode and prefill tiles do not run ") + s.name() + " weights");
     requireSegmentPlanes(s, "projection");
   }
 }
@@ -66,7 +68,8 @@ void requireSegments(const Projection &p, LinearMatrix matrix) {
 char epilogueOf(LinearEpilogue e) { return e == LinearEpilogue::Residual ? 1 : e == LinearEpilogue::UpWithGate ? 2 : 0; }
 
 kern::Segment kernelSegment(const QuantizedSegment &s) {
-  return {s.plane0.as<const uint8_t>(), s.meta.as<const uint8_t>(), s.outputSize / SQ_TILE_COLUMNS, s.columnOffset};
+  return {s.plane0.as<const uint8_t>(), s.meta.as<const uint8_t>(), s.outputSize / SQ_TILE_COLUMNS, s.columnOffset,
+          s.plane1.as<const uint8_t>()};
 }
 
 }  // namespace
@@ -75,7 +78,8 @@ QuantizedSegment QuantizedSegment::planes(uint32_t formatId, uint32_t outputSize
                                           Buffer plane1, Buffer meta) {
   if (formatId >= SQ_FMT_COUNT) throw std::invalid_argument("unknown GGUF segment format");
   if (!sq_format_supported(formatId))
-    throw std::invalid_argument("format " + std::to_string(formatId) + " is not one this build runs (Q4_K, af4g32, af4g64, af4g128)");
+    throw std::invalid_argument("format " + std::to_string(formatId) +
+                                " is not one this build runs (Q4_K, Q5_K, Q6_K, Q8_0, af4g32, af4g64, af4g128, af8g64)");
   QuantizedSegment s;
   s.plane0 = plane0;
   s.plane1 = plane1;
@@ -137,6 +141,7 @@ void requireSegmentPlanes(const QuantizedSegment &segment, std::string_view what
   const std::string name(what);
   requireBytes(segment.plane0, planeBytes(groups, rowGroups, f.plane0_bytes), name + " plane0");
   requireBytes(segment.meta, planeBytes(units, rowUnits, f.meta_bytes), name + " meta");
+  if (f.plane1_bytes) requireBytes(segment.plane1, planeBytes(groups, rowGroups, f.plane1_bytes), name + " plane1");
 }
 
 // ---------------------------------------------------------------- plans

@@ -28,6 +28,8 @@ void requireExperts(const QuantizedSegment &s, uint32_t slots, uint32_t n, uint3
                     const char *name) {
   if (s.formatId != format || s.outputSize != uint64_t{slots} * n || s.inputSize != k)
     throw std::invalid_argument(std::string("MoE expert ") + name + " does not match the plan");
+  if (!sq_tile_format(format))
+    throw std::invalid_argument(std::string("the MoE expert passes do not run ") + s.name() + " weights");
   requireSegmentPlanes(s, std::string("MoE expert ") + name);
 }
 

@@ -97,24 +97,34 @@ __device__ __forceinline__ float epilogue(float v, const uint16_t *aux, size_t a
   else return epilogue_bits<EP>(v, aux[at]);
 }
 
-// Per-format traits. SG: groups of 32 one scale covers; UNIT: groups of 32 per meta unit; META: meta unit bytes.
+// Per-format traits (QuantFormat.h:147-216). SG: groups of 32 one scale covers; UNIT: groups of 32 per meta unit;
+// META: meta unit bytes; P0, P1: plane0 and plane1 bytes per group of 32; ZERO: the code offset of a format whose
+// value is s (q - ZERO) (quant_formats.h QUANT_FORMAT); HALVES: one scale per 16 elements (Q6_K).
 template <uint32_t FMT> struct Fmt;
-template <> struct Fmt<SQ_FMT_AF4G32> { static constexpr int SG = 1, UNIT = 1, META = 4; };
-template <> struct Fmt<SQ_FMT_AF4G64> { static constexpr int SG = 2, UNIT = 2, META = 4; };
-template <> struct Fmt<SQ_FMT_AF4G128> { static constexpr int SG = 4, UNIT = 4, META = 4; };
-template <> struct Fmt<SQ_FMT_Q4K> { static constexpr int SG = 1, UNIT = 8, META = 16; };
+template <> struct Fmt<SQ_FMT_AF4G32> { static constexpr int SG = 1, UNIT = 1, META = 4, P0 = 16, P1 = 0, ZERO = 0, HALVES = 0; };
+template <> struct Fmt<SQ_FMT_AF4G64> { static constexpr int SG = 2, UNIT = 2, META = 4, P0 = 16, P1 = 0, ZERO = 0, HALVES = 0; };
+template <> struct Fmt<SQ_FMT_AF4G128> { static constexpr int SG = 4, UNIT = 4, META = 4, P0 = 16, P1 = 0, ZERO = 0, HALVES = 0; };
+template <> struct Fmt<SQ_FMT_AF8G64> { static constexpr int SG = 2, UNIT = 2, META = 4, P0 = 32, P1 = 0, ZERO = 0, HALVES = 0; };
+template <> struct Fmt<SQ_FMT_Q4K> { static constexpr int SG = 1, UNIT = 8, META = 16, P0 = 16, P1 = 0, ZERO = 0, HALVES = 0; };
+template <> struct Fmt<SQ_FMT_Q5K> { static constexpr int SG = 1, UNIT = 8, META = 16, P0 = 16, P1 = 4, ZERO = 0, HALVES = 0; };
+template <> struct Fmt<SQ_FMT_Q6K> { static constexpr int SG = 1, UNIT = 8, META = 20, P0 = 16, P1 = 8, ZERO = 32, HALVES = 1; };
+template <> struct Fmt<SQ_FMT_Q80> { static constexpr int SG = 1, UNIT = 1, META = 2, P0 = 32, P1 = 0, ZERO = 0, HALVES = 0; };
 
-// The meta words one column needs for scale group `sg` (the meta unit that holds it): af4 the (s, z) word, Q4_K
-// the 16-byte super-block header.
+// The meta words one column needs for scale group `sg` (the meta unit that holds it): affine the (s, z) word,
+// Q4_K and Q5_K the 16-byte super-block header, Q6_K its 16 int8 scales and d, Q8_0 its half d.
 struct MetaWords {
-  uint32_t w[4];
+  uint32_t w[5];
 };
 template <uint32_t FMT>
 __device__ __forceinline__ MetaWords load_meta(const uint8_t *unit_row) {
-  MetaWords m;
+  MetaWords m{};
   if constexpr (Fmt<FMT>::META == 4) {
     m.w[0] = __builtin_nontemporal_load((const uint32_t *)unit_row);
-    m.w[1] = m.w[2] = m.w[3] = 0;
+  } else if constexpr (Fmt<FMT>::META == 2) {
+    m.w[0] = __builtin_nontemporal_load((const uint16_t *)unit_row);
+  } else if constexpr (Fmt<FMT>::META == 20) {   // 4-byte aligned only
+#pragma unroll
+    for (int i = 0; i < 5; ++i) m.w[i] = __builtin_nontemporal_load((const uint32_t *)unit_row + i);
   } else {
     const u32x4 v = __builtin_nontemporal_load((const u32x4 *)unit_row);
     m.w[0] = v[0]; m.w[1] = v[1]; m.w[2] = v[2]; m.w[3] = v[3];
@@ -130,7 +140,14 @@ struct Coef {
 };
 template <uint32_t FMT>
 __device__ __forceinline__ Coef coef(const MetaWords &m, uint32_t sg) {
-  if constexpr (FMT != SQ_FMT_Q4K) {
+  if constexpr (FMT == SQ_FMT_Q80) {
+    return {f16_to_f32(m.w[0] & 0xFFFFu), 0.0f};
+  } else if constexpr (FMT == SQ_FMT_Q6K) {
+    // Scale 2 (sg % 8) of the super-block's 16 (the group's first half; coef_half gives either).
+    const uint32_t i = 2 * (sg & 7u);
+    const float d = f16_to_f32(m.w[4] & 0xFFFFu);
+    return {d * (float)(int8_t)(m.w[i >> 2] >> (8 * (i & 3))), 0.0f};
+  } else if constexpr (FMT != SQ_FMT_Q4K && FMT != SQ_FMT_Q5K) {
     return {bf16_to_f32(m.w[0] & 0xFFFFu), __uint_as_float(m.w[0] & 0xFFFF0000u)};
   } else {
     const uint32_t j = sg & 7u;
@@ -147,6 +164,11 @@ __device__ __forceinline__ Coef coef(const MetaWords &m, uint32_t sg) {
     const float d = f16_to_f32(m.w[0] & 0xFFFFu), dmin = f16_to_f32(m.w[0] >> 16);
     return {d * (float)sc, -(dmin * (float)mn)};
   }
+}
+// Q6_K's scale of half h (elements 16 h .. 16 h + 15) of group sg: d * int8 scale 2 (sg % 8) + h, exact in fp32.
+__device__ __forceinline__ float q6k_scale(const MetaWords &m, uint32_t sg, uint32_t h) {
+  const uint32_t i = 2 * (sg & 7u) + h;
+  return f16_to_f32(m.w[4] & 0xFFFFu) * (float)(int8_t)(m.w[i >> 2] >> (8 * (i & 3)));
 }
 
 }  // namespace sq::kern

@@ -17,6 +17,7 @@ struct Segment {
   const uint8_t *meta;
   uint32_t tiles;
   uint32_t out_offset;
+  const uint8_t *plane1;   // the high bits of Q5_K and Q6_K (null for the other formats)
 };
 
 // The decode tiles: y[r][c] = sum_k x[r][k] w[c][k] over up to three segments of one format. With gate.plane0 set,
@@ -72,8 +73,8 @@ hipError_t launch_prefill(uint32_t fmt, uint32_t epilogue, const PrefillArgs &ar
 
 // Dequantisation of every weight of a segment's planes: fp32 fma(q, s, z) and the staged tile's fp16 rounding of
 // it, [N][K] each (either may be null).
-hipError_t launch_dequant(uint32_t fmt, const uint8_t *plane0, const uint8_t *meta, uint32_t N, uint32_t K,
-                          float *values, uint16_t *halves, hipStream_t stream);
+hipError_t launch_dequant(uint32_t fmt, const uint8_t *plane0, const uint8_t *plane1, const uint8_t *meta, uint32_t N,
+                          uint32_t K, float *values, uint16_t *halves, hipStream_t stream);
 // Load-time repacks: native rows (GgufRepackParams layout) into plane0 / meta, and MLX tensors (uint32 codes,
 // bf16 scales and biases) straight into plane0 / meta.
 hipError_t launch_repack(const uint8_t *src, uint8_t *dst, const SqGgufRepackParams &params, hipStream_t stream);

@@ -1,8 +1,8 @@
 // Load-time repack into the plane layout and the dequantisation kernel the tests read the weights through.
 //
-// Repack (reference: gguf_repack_group's affine and Q4_K branches, kernels/shared/gguf_repack.metal:24-74, and
-// kernel gguf_repack :232-238): one thread per (row, group of 32) writes the group's 16-byte plane unit, element e's
-// code at slot quant_slot(e), and the first group of each meta unit copies the unit's meta bytes. The MLX repack
+// Repack (reference: gguf_repack_group's affine, Q4_K, Q5_K, Q6_K and Q8_0 branches, kernels/shared/gguf_repack.metal
+// :24-74, and kernel gguf_repack :232-238): one thread per (row, group of 32) writes the group's plane units, element
+// e's code at slot quant_slot(e), and the first group of each meta unit copies the unit's meta bytes. The MLX repack
 // reads MLX's own tensors (uint32 codes, bf16 scales and biases, model/GgufPreparation.cpp:141-193 builds the native
 // block from them) and writes the same planes without the staging copy.
 //
@@ -14,7 +14,7 @@
 namespace sq::kern {
 namespace {
 
-// Word c of a plane unit holds slots 8c..8c+7, slot 8c + i at bit (i & 1) * 16 + 4 (i >> 1).
+// Word c of a 4-bit plane unit holds slots 8c..8c+7, slot 8c + i at bit (i & 1) * 16 + 4 (i >> 1).
 __device__ __forceinline__ void store_pairs(const uint8_t codes[32], uint8_t *dst) {
   uint32_t word[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -24,7 +24,23 @@ __device__ __forceinline__ void store_pairs(const uint8_t codes[32], uint8_t *ds
   }
   *(u32x4 *)dst = u32x4{word[0], word[1], word[2], word[3]};
 }
+// Every other field is a little-endian string of BITS-bit fields over the slots (QuantFormat.h:27-31): 8-bit codes
+// one byte a slot, Q5_K's fifth bits one bit a slot, Q6_K's high bits two bits a slot.
+template <uint32_t BITS>
+__device__ __forceinline__ void store_bits(const uint8_t codes[32], uint8_t *dst) {
+  uint32_t word[BITS] = {};
+#pragma unroll
+  for (uint32_t e = 0; e < 32; ++e) {
+    const uint32_t slot = sq_quant_slot(e);
+    word[slot * BITS / 32] |= (uint32_t)codes[e] << ((slot * BITS) % 32);
+  }
+#pragma unroll
+  for (uint32_t w = 0; w < BITS; ++w) ((uint32_t *)dst)[w] = word[w];
+}
 
+// One thread a (row, group of 32): the group's low codes into its plane0 unit, its high bits into its plane1 unit,
+// and the first group of each meta unit copies the unit's meta (gguf_repack_group, gguf_repack.metal:42-74, and
+// metaPack's Q6_K arrangement: its 16 int8 scales, d and two zero bytes).
 __global__ void repack_kernel(const uint8_t *src, uint8_t *dst, SqGgufRepackParams p) {
   const uint32_t G = p.input_size / 32;
   const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -33,24 +49,59 @@ __global__ void repack_kernel(const uint8_t *src, uint8_t *dst, SqGgufRepackPara
   const SqQuantFormat f = sq_format(p.fmt);
   const uint32_t b = g / f.meta_groups, jj = g % f.meta_groups;
   const uint8_t *blk = src + (size_t)n * p.src_row_bytes + (size_t)b * f.block_bytes;
-  uint8_t codes[32];
-  if (sq_affine_format(p.fmt)) {
+  uint8_t codes[32], highs[32];
+  uint8_t *unit0 = dst + sq_tile_index(n, g, G) * f.plane0_bytes;
+  uint8_t *unit1 = dst + p.dst_plane1 + sq_tile_index(n, g, G) * f.plane1_bytes;
+  if (p.fmt == SQ_FMT_AF8G64) {
+#pragma unroll
+    for (uint32_t e = 0; e < 32; ++e) codes[e] = blk[4 + 32u * jj + e];
+    store_bits<8>(codes, unit0);
+  } else if (sq_affine_format(p.fmt)) {
 #pragma unroll
     for (uint32_t e = 0; e < 32; ++e) {
       const uint32_t l = 32u * jj + e;
       codes[e] = (blk[4 + l / 2] >> (4u * (l & 1u))) & 15u;
     }
-  } else {
+    store_pairs(codes, unit0);
+  } else if (p.fmt == SQ_FMT_Q80) {
 #pragma unroll
-    for (uint32_t e = 0; e < 32; ++e) codes[e] = (blk[16 + (jj / 2) * 32 + e] >> (4u * (jj & 1u))) & 15u;
+    for (uint32_t e = 0; e < 32; ++e) codes[e] = blk[2 + e];
+    store_bits<8>(codes, unit0);
+  } else if (p.fmt == SQ_FMT_Q6K) {
+    const uint32_t h = jj / 4, r = jj % 4;
+#pragma unroll
+    for (uint32_t e = 0; e < 32; ++e) {
+      codes[e] = (blk[64 * h + e + 32 * (r & 1u)] >> (4u * (r >> 1))) & 15u;
+      highs[e] = (blk[128 + 32 * h + e] >> (2u * r)) & 3u;
+    }
+    store_pairs(codes, unit0);
+    store_bits<2>(highs, unit1);
+  } else {   // Q4_K, Q5_K
+    const uint32_t q = p.fmt == SQ_FMT_Q5K ? 48u : 16u;
+#pragma unroll
+    for (uint32_t e = 0; e < 32; ++e) codes[e] = (blk[q + (jj / 2) * 32 + e] >> (4u * (jj & 1u))) & 15u;
+    store_pairs(codes, unit0);
+    if (p.fmt == SQ_FMT_Q5K) {
+#pragma unroll
+      for (uint32_t e = 0; e < 32; ++e) highs[e] = (blk[16 + e] >> jj) & 1u;
+      store_bits<1>(highs, unit1);
+    }
   }
-  store_pairs(codes, dst + sq_tile_index(n, g, G) * 16);
   if (jj == 0) {
     uint8_t *meta = dst + p.dst_meta + sq_tile_index(n, b, G / f.meta_groups) * f.meta_bytes;
-    for (uint32_t i = 0; i < f.meta_bytes; ++i) meta[i] = blk[i];
+    if (p.fmt == SQ_FMT_Q6K) {
+      for (uint32_t i = 0; i < 16; ++i) meta[i] = blk[SQ_Q6K_SCALES + i];
+      meta[16] = blk[SQ_Q6K_D];
+      meta[17] = blk[SQ_Q6K_D + 1];
+      meta[18] = meta[19] = 0;
+    } else {
+      for (uint32_t i = 0; i < f.meta_bytes; ++i) meta[i] = blk[i];
+    }
   }
 }
 
+// MLX's own tensors: row n's codes a little-endian string of BITS-bit codes (group g of 32 is BITS words of the
+// row), bf16 scales and biases per group of the format.
 __global__ void mlx_repack_kernel(uint32_t fmt, const uint32_t *weight, const uint16_t *scales,
                                   const uint16_t *biases, uint32_t rows, uint32_t K, uint8_t *plane0, uint8_t *meta) {
   const uint32_t G = K / 32;
@@ -58,12 +109,19 @@ __global__ void mlx_repack_kernel(uint32_t fmt, const uint32_t *weight, const ui
   if (t >= (uint64_t)rows * G) return;
   const uint32_t n = (uint32_t)(t / G), g = (uint32_t)(t % G);
   const SqQuantFormat f = sq_format(fmt);
-  // Row n's codes are a little-endian string of 4-bit codes: group g is words 4g..4g+3 of the row.
-  const u32x4 w = *(const u32x4 *)(weight + (size_t)n * (K / 8) + (size_t)g * 4);
   uint8_t codes[32];
+  if (fmt == SQ_FMT_AF8G64) {
+    const u32x4 *w = (const u32x4 *)(weight + (size_t)n * (K / 4) + (size_t)g * 8);
+    const u32x4 lo = w[0], hi = w[1];
 #pragma unroll
-  for (uint32_t e = 0; e < 32; ++e) codes[e] = (w[e >> 3] >> (4u * (e & 7u))) & 15u;
-  store_pairs(codes, plane0 + sq_tile_index(n, g, G) * 16);
+    for (uint32_t e = 0; e < 32; ++e) codes[e] = ((e < 16 ? lo[e >> 2] : hi[(e - 16) >> 2]) >> (8u * (e & 3u))) & 0xFFu;
+    store_bits<8>(codes, plane0 + sq_tile_index(n, g, G) * 32);
+  } else {
+    const u32x4 w = *(const u32x4 *)(weight + (size_t)n * (K / 8) + (size_t)g * 4);
+#pragma unroll
+    for (uint32_t e = 0; e < 32; ++e) codes[e] = (w[e >> 3] >> (4u * (e & 7u))) & 15u;
+    store_pairs(codes, plane0 + sq_tile_index(n, g, G) * 16);
+  }
   if (g % f.meta_groups == 0) {
     const uint32_t groups = K / f.block_elements, b = g / f.meta_groups;
     const size_t parameter = (size_t)n * groups + b;
@@ -72,34 +130,49 @@ __global__ void mlx_repack_kernel(uint32_t fmt, const uint32_t *weight, const ui
   }
 }
 
+// Element e's code (low bits from plane0, high bits from plane1) of a group's units.
 template <uint32_t FMT>
-__global__ void dequant_kernel(const uint8_t *plane0, const uint8_t *meta, uint32_t N, uint32_t K, float *values,
-                               uint16_t *halves) {
+__device__ __forceinline__ uint32_t group_code(const uint8_t *unit0, const uint8_t *unit1, uint32_t e) {
+  using F = Fmt<FMT>;
+  const uint32_t slot = sq_quant_slot(e);
+  uint32_t q;
+  if constexpr (F::P0 == 32) {
+    q = unit0[slot];
+  } else {
+    const uint32_t word = ((const uint32_t *)unit0)[slot >> 3], i = slot & 7u;
+    q = (word >> ((i & 1u) * 16u + 4u * (i >> 1))) & 15u;
+  }
+  if constexpr (F::P1 == 4) q |= ((((const uint32_t *)unit1)[0] >> slot) & 1u) << 4;
+  if constexpr (F::P1 == 8) q |= ((((const uint32_t *)unit1)[slot >> 4] >> (2 * (slot & 15u))) & 3u) << 4;
+  return q;
+}
+
+// Every weight's fp32 value and its fp16 rounding, as the staged tile decodes it (staged_linear,
+// gguf_staged.h:11-16, and QuantInt8 :40-44): fma(q, s, z), but s (q - 32) for Q6_K and s q of the signed byte for
+// Q8_0, so signed zeros come out as the reference's.
+template <uint32_t FMT>
+__global__ void dequant_kernel(const uint8_t *plane0, const uint8_t *plane1, const uint8_t *meta, uint32_t N,
+                               uint32_t K, float *values, uint16_t *halves) {
   using F = Fmt<FMT>;
   const uint32_t G = K / 32, units = G / F::UNIT;
   const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (uint64_t)N * G) return;
   const uint32_t n = (uint32_t)(t / G), g = (uint32_t)(t % G);
-  const u32x4 w = *(const u32x4 *)(plane0 + sq_tile_index(n, g, G) * 16);
+  const uint8_t *unit0 = plane0 + sq_tile_index(n, g, G) * F::P0;
+  const uint8_t *unit1 = F::P1 ? plane1 + sq_tile_index(n, g, G) * F::P1 : nullptr;
   const MetaWords m = load_meta<FMT>(meta + sq_tile_index(n, g / F::UNIT, units) * F::META);
   const Coef k = coef<FMT>(m, g / F::SG);
   const size_t base = (size_t)n * K + (size_t)g * 32;
-#pragma unroll
-  for (uint32_t c = 0; c < 4; ++c)
-#pragma unroll
-    for (uint32_t p = 0; p < 4; ++p) {
-      const uint32_t e0 = 16u * (p >> 1) + 4u * c + 2u * (p & 1u);
-      const float v0 = fmaf((float)((w[c] >> (4u * p)) & 15u), k.s, k.z);
-      const float v1 = fmaf((float)((w[c] >> (16u + 4u * p)) & 15u), k.s, k.z);
-      if (values) {
-        values[base + e0] = v0;
-        values[base + e0 + 1] = v1;
-      }
-      if (halves) {
-        halves[base + e0] = f32_to_f16(v0);
-        halves[base + e0 + 1] = f32_to_f16(v1);
-      }
-    }
+#pragma unroll 4
+  for (uint32_t e = 0; e < 32; ++e) {
+    const uint32_t q = group_code<FMT>(unit0, unit1, e);
+    float v;
+    if constexpr (FMT == SQ_FMT_Q6K) v = ((float)q - 32.0f) * q6k_scale(m, g, e >> 4);
+    else if constexpr (FMT == SQ_FMT_Q80) v = (float)(int8_t)q * k.s;
+    else v = fmaf((float)q, k.s, k.z);
+    if (values) values[base + e] = v;
+    if (halves) halves[base + e] = f32_to_f16(v);
+  }
 }
 
 }  // namespace
@@ -118,17 +191,18 @@ hipError_t launch_mlx_repack(uint32_t fmt, const uint32_t *weight, const uint16_
   return hipGetLastError();
 }
 
-hipError_t launch_dequant(uint32_t fmt, const uint8_t *plane0, const uint8_t *meta, uint32_t N, uint32_t K,
-                          float *values, uint16_t *halves, hipStream_t stream) {
+hipError_t launch_dequant(uint32_t fmt, const uint8_t *plane0, const uint8_t *plane1, const uint8_t *meta, uint32_t N,
+                          uint32_t K, float *values, uint16_t *halves, hipStream_t stream) {
   const uint64_t threads = (uint64_t)N * (K / 32);
   const dim3 grid((uint32_t)((threads + 255) / 256)), block(256);
+#define SQ_DEQUANT(F) \
+  case F: hipLaunchKernelGGL(dequant_kernel<F>, grid, block, 0, stream, plane0, plane1, meta, N, K, values, halves); break;
   switch (fmt) {
-    case SQ_FMT_AF4G32: hipLaunchKernelGGL(dequant_kernel<SQ_FMT_AF4G32>, grid, block, 0, stream, plane0, meta, N, K, values, halves); break;
-    case SQ_FMT_AF4G64: hipLaunchKernelGGL(dequant_kernel<SQ_FMT_AF4G64>, grid, block, 0, stream, plane0, meta, N, K, values, halves); break;
-    case SQ_FMT_AF4G128: hipLaunchKernelGGL(dequant_kernel<SQ_FMT_AF4G128>, grid, block, 0, stream, plane0, meta, N, K, values, halves); break;
-    case SQ_FMT_Q4K: hipLaunchKernelGGL(dequant_kernel<SQ_FMT_Q4K>, grid, block, 0, stream, plane0, meta, N, K, values, halves); break;
+    SQ_DEQUANT(SQ_FMT_AF4G32) SQ_DEQUANT(SQ_FMT_AF4G64) SQ_DEQUANT(SQ_FMT_AF4G128) SQ_DEQUANT(SQ_FMT_AF8G64)
+    SQ_DEQUANT(SQ_FMT_Q4K) SQ_DEQUANT(SQ_FMT_Q5K) SQ_DEQUANT(SQ_FMT_Q6K) SQ_DEQUANT(SQ_FMT_Q80)
     default: return hipErrorInvalidValue;
   }
+#undef SQ_DEQUANT
   return hipGetLastError();
 }
 

@@ -17,6 +17,7 @@ HEADER = PACKAGE_ROOT.parent / "include" / "splash_q4.h"
 
 SQ_OK, SQ_INVALID_ARGUMENT, SQ_RUNTIME_ERROR = 0, 1, 2
 FMT_Q4K, FMT_AF4G32, FMT_AF4G64, FMT_AF4G128 = 0, 25, 26, 27
+FMT_Q5K, FMT_Q6K, FMT_Q80, FMT_AF8G64 = 3, 4, 6, 35
 PHASE_PREFILL, PHASE_DECODE = 0, 1
 EPILOGUE_NONE, EPILOGUE_RESIDUAL, EPILOGUE_GATE_UP, EPILOGUE_UP_WITH_GATE = 0, 1, 2, 3
 TILE_STAGED, TILE_PREFILL, TILE_REGISTER = 0, 1, 2
@@ -24,12 +25,16 @@ OUTPUT_BF16, OUTPUT_F32 = 0, 1
 FMT_BF16, FLOAT32_ROWS = 41, 0xFFFFFFFF
 LINEAR_INPUT_PLAIN, LINEAR_INPUT_TABLE16, LINEAR_INPUT_HALF_ROWS = 0, 1, 2
 
-# (block_elements, block_bytes, plane0_bytes, meta_bytes, meta_groups) of QuantFormat.h:159,185-187.
+# (block_elements, block_bytes, plane0_bytes, meta_bytes, meta_groups, plane1_bytes) of QuantFormat.h:159-192.
 FORMATS = {
-    FMT_Q4K: (256, 144, 16, 16, 8),
-    FMT_AF4G32: (32, 20, 16, 4, 1),
-    FMT_AF4G64: (64, 36, 16, 4, 2),
-    FMT_AF4G128: (128, 68, 16, 4, 4),
+    FMT_Q4K: (256, 144, 16, 16, 8, 0),
+    FMT_Q5K: (256, 176, 16, 16, 8, 4),
+    FMT_Q6K: (256, 210, 16, 20, 8, 8),
+    FMT_Q80: (32, 34, 32, 2, 1, 0),
+    FMT_AF4G32: (32, 20, 16, 4, 1, 0),
+    FMT_AF4G64: (64, 36, 16, 4, 2, 0),
+    FMT_AF4G128: (128, 68, 16, 4, 4, 0),
+    FMT_AF8G64: (64, 68, 32, 4, 2, 0),
 }
 
 
@@ -220,13 +225,13 @@ def stream_handle():
 
 def plane_bytes(fmt: int, n: int, k: int) -> tuple[int, int]:
     """Bytes of plane0 and meta for an n x k tensor."""
-    _, _, p0, meta_bytes, meta_groups = FORMATS[fmt]
+    _, _, p0, meta_bytes, meta_groups, _ = FORMATS[fmt]
     groups = k // 32
     return n * groups * p0, n * (groups // meta_groups) * meta_bytes
 
 
-def segment(fmt: int, n: int, k: int, plane0, meta, column_offset: int = 0) -> Segment:
-    return Segment(view(plane0), view(None), view(meta), n, k, column_offset, fmt)
+def segment(fmt: int, n: int, k: int, plane0, meta, column_offset: int = 0, plane1=None) -> Segment:
+    return Segment(view(plane0), view(plane1), view(meta), n, k, column_offset, fmt)
 
 
 def projection(segments, output_size: int | None = None, destination: int = OUTPUT_BF16) -> Projection:
@@ -304,8 +309,9 @@ def mlx_repack(fmt: int, rows: int, k: int, weight, scales, biases, plane0, meta
          view(biases), view(plane0), view(meta))
 
 
-def gguf_repack(src, dst, rows: int, k: int, fmt: int, src_row_bytes: int, dst_meta: int, stream=None) -> None:
-    params = (c_uint32 * 6)(rows, k, fmt, src_row_bytes, 0, dst_meta)
+def gguf_repack(src, dst, rows: int, k: int, fmt: int, src_row_bytes: int, dst_meta: int, stream=None,
+                dst_plane1: int = 0) -> None:
+    params = (c_uint32 * 6)(rows, k, fmt, src_row_bytes, dst_plane1, dst_meta)
     call("sq_gguf_repack", stream if stream is not None else stream_handle(), view(src), view(dst), params)
 
 

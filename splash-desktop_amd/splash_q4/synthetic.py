@@ -33,12 +33,14 @@ def pack_codes(codes: np.ndarray) -> np.ndarray:
     return np.bitwise_or.reduce(c << shifts, axis=2).astype(np.uint32)
 
 
-def mlx_affine(rng: np.random.Generator, n: int, k: int, group: int = 64, scale_sigma: float = 0.02):
-    """(codes uint8 [n][k], weight uint32 [n][k/8], scales bf16 bits [n][k/group], biases bf16 bits)."""
-    codes = rng.integers(0, 16, size=(n, k), dtype=np.uint8)
+def mlx_affine(rng: np.random.Generator, n: int, k: int, group: int = 64, scale_sigma: float = 0.02, bits: int = 4):
+    """(codes uint8 [n][k], weight uint32 [n][k * bits / 32], scales bf16 bits [n][k/group], biases bf16 bits):
+    bits 4 or 8, z = -2^(bits-1) s."""
+    codes = rng.integers(0, 1 << bits, size=(n, k), dtype=np.uint8)
     scales = bf16_bits(np.abs(rng.standard_normal((n, k // group), dtype=np.float32)) * np.float32(scale_sigma))
-    biases = bf16_bits(-8.0 * bf16_to_f32(scales))
-    return codes, pack_codes(codes), scales, biases
+    biases = bf16_bits(-float(1 << (bits - 1)) * bf16_to_f32(scales))
+    weight = pack_codes(codes) if bits == 4 else np.ascontiguousarray(codes).view(np.uint32)
+    return codes, weight, scales, biases
 
 
 def fp16_bits(values: np.ndarray) -> np.ndarray:
@@ -54,6 +56,26 @@ def q4k_native(rng: np.random.Generator, n: int, k: int, sigma: float = 0.01) ->
     raw[:, 0:2] = d.view(np.uint8).reshape(blocks, 2)
     raw[:, 2:4] = dmin.view(np.uint8).reshape(blocks, 2)
     return raw.reshape(n, (k // 256) * 144)
+
+
+# (block bytes, offset of d, offset of dmin or None) of the GGUF K-quant and Q8_0 blocks (llama.cpp's layouts).
+_GGUF_BLOCKS = {3: (176, 0, 2), 4: (210, 208, None), 6: (34, 0, None)}
+# The reference's realistic half scales per format (GgufFormatReference.hpp scaleRange).
+_GGUF_SCALES = {3: (0.0005, 0.004), 4: (0.00002, 0.0001), 6: (0.0005, 0.004)}
+
+
+def gguf_native(rng: np.random.Generator, fmt: int, n: int, k: int) -> np.ndarray:
+    """Native rows of Q5_K (3), Q6_K (4) or Q8_0 (6): random bytes with half scales d (and Q5_K's dmin) drawn from
+    the format's realistic range, as the reference's makeNative (GgufFormatReference.hpp:190-216) builds them."""
+    size, d_at, m_at = _GGUF_BLOCKS[fmt]
+    elements = 32 if fmt == 6 else 256
+    blocks = n * (k // elements)
+    raw = rng.integers(0, 256, size=(blocks, size), dtype=np.uint8)
+    lo, hi = _GGUF_SCALES[fmt]
+    raw[:, d_at:d_at + 2] = fp16_bits(rng.uniform(lo, hi, blocks).astype(np.float32)).view(np.uint8).reshape(blocks, 2)
+    if m_at is not None:
+        raw[:, m_at:m_at + 2] = fp16_bits(rng.uniform(lo, hi, blocks).astype(np.float32)).view(np.uint8).reshape(blocks, 2)
+    return raw.reshape(n, (k // elements) * size)
 
 
 def router_logits(rng: np.random.Generator, rows: int, experts: int) -> np.ndarray:

@@ -35,12 +35,13 @@ class Weights:
 
     def __init__(self, fmt: int, n: int, k: int, native: np.ndarray):
         self.fmt, self.n, self.k, self.native = fmt, n, k, native
-        self.plane0_h, self.meta_h, self.values = oracle.repack(fmt, native, n, k)
-        _, self.halves = oracle.plane_values(fmt, self.plane0_h, self.meta_h, n, k)
+        self.plane0_h, self.plane1_h, self.meta_h, self.values = oracle.repack_planes(fmt, native, n, k)
+        _, self.halves = oracle.plane_values(fmt, self.plane0_h, self.meta_h, n, k, self.plane1_h)
         self.plane0, self.meta = to_device(self.plane0_h), to_device(self.meta_h)
+        self.plane1 = to_device(self.plane1_h) if self.plane1_h is not None else None
 
     def segment(self, column_offset: int = 0) -> sq.Segment:
-        return sq.segment(self.fmt, self.n, self.k, self.plane0, self.meta, column_offset)
+        return sq.segment(self.fmt, self.n, self.k, self.plane0, self.meta, column_offset, self.plane1)
 
 
 def affine_native(rng: np.random.Generator, fmt: int, n: int, k: int, centred: bool = False) -> np.ndarray:
@@ -57,6 +58,11 @@ def affine_native(rng: np.random.Generator, fmt: int, n: int, k: int, centred: b
 def make_weights(rng, fmt: int, n: int, k: int, centred: bool = False) -> Weights:
     if fmt == oracle.FMT_Q4K:
         return Weights(fmt, n, k, synthetic.q4k_native(rng, n, k).ravel())
+    if fmt in (oracle.FMT_Q5K, oracle.FMT_Q6K, oracle.FMT_Q80):
+        return Weights(fmt, n, k, synthetic.gguf_native(rng, fmt, n, k).ravel())
+    if fmt == oracle.FMT_AF8G64:
+        codes, weight, scales, biases = synthetic.mlx_affine(rng, n, k, 64, scale_sigma=0.02 / 16, bits=8)
+        return Weights(fmt, n, k, oracle.mlx_native(fmt, weight, scales, biases, n, k))
     return Weights(fmt, n, k, affine_native(rng, fmt, n, k, centred))
 
 

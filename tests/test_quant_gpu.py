@@ -95,3 +95,71 @@ def test_stream_read_folds_every_word():
     share = -(-len(vectors) // 4)
     want = [np.bitwise_xor.reduce(vectors[w * share:(w + 1) * share].ravel()) for w in range(4)]
     assert got.tolist() == [int(v) for v in want]
+
+
+NEW_FORMATS = [oracle.FMT_Q5K, oracle.FMT_Q6K, oracle.FMT_Q80, oracle.FMT_AF8G64]
+
+
+@pytest.mark.parametrize("fmt", NEW_FORMATS)
+@pytest.mark.parametrize("source", ["fixture", "synthetic"])
+def test_dequant_bit_exact_new_formats(fmt, source):
+    """Q5_K, Q6_K, Q8_0 and af8g64 dequantised on the GPU: fp32 values and fp16 bits equal the oracle's (signed
+    zeros included: Q6_K multiplies the exact q - 32, Q8_0 its signed byte, as the reference's staged tile does)."""
+    n, k = 128, 1024
+    if source == "fixture":
+        native = oracle.fixture(fmt, n, k, 42)
+        if fmt == oracle.FMT_AF8G64:
+            native = np.random.default_rng(42).integers(0, 256, size=native.size, dtype=np.uint8)
+            native = native.reshape(-1, 68)
+            native[:, 1] &= 0x3F   # finite scales and biases
+            native[:, 3] &= 0x3F
+            native = native.ravel()
+        w = Weights(fmt, n, k, native)
+    else:
+        w = make_weights(np.random.default_rng(fmt), fmt, n, k)
+    t = torch()
+    values = t.zeros((n, k), dtype=t.float32, device="cuda")
+    halves = t.zeros((n, k), dtype=t.int16, device="cuda")
+    sq.dequant(w.segment(), values, halves)
+    t.cuda.synchronize()
+    got_v, got_h = values.cpu().numpy(), to_host(halves, np.uint16)
+    nan = np.isnan(w.values)
+    assert np.array_equal(np.isnan(got_v), nan)
+    assert same_bits(got_v[~nan], w.values[~nan])
+    assert np.array_equal(got_h[~nan], w.halves[~nan])
+
+
+@pytest.mark.parametrize("fmt", NEW_FORMATS)
+def test_gguf_repack_new_formats(fmt):
+    """The load-time repack of native rows into plane0, plane1 and meta equals the oracle's (and so the reference
+    CPU oracle's) bytes."""
+    n, k = 192, 1024
+    native = oracle.fixture(fmt, n, k, 5)
+    plane0, plane1, meta, _ = oracle.repack_planes(fmt, native, n, k)
+    t = torch()
+    src = to_device(native)
+    p1 = plane1.size if plane1 is not None else 0
+    dst = t.zeros(plane0.size + p1 + meta.size, dtype=t.uint8, device="cuda")
+    sq.gguf_repack(src, dst, n, k, fmt, oracle.row_bytes(fmt, k), plane0.size + p1, dst_plane1=plane0.size)
+    t.cuda.synchronize()
+    out = dst.cpu().numpy()
+    assert np.array_equal(out[: plane0.size], plane0)
+    if plane1 is not None:
+        assert np.array_equal(out[plane0.size:plane0.size + p1], plane1)
+    assert np.array_equal(out[plane0.size + p1:], meta)
+
+
+def test_mlx_repack_8bit():
+    rng = np.random.default_rng(8)
+    n, k, fmt = 128, 2048, oracle.FMT_AF8G64
+    codes, weight, scales, biases = synthetic.mlx_affine(rng, n, k, 64, bits=8)
+    native = oracle.mlx_native(fmt, weight, scales, biases, n, k)
+    plane0, plane1, meta, _ = oracle.repack_planes(fmt, native, n, k)
+    assert plane1 is None
+    t = torch()
+    p0 = t.zeros(plane0.size, dtype=t.uint8, device="cuda")
+    m = t.zeros(meta.size, dtype=t.uint8, device="cuda")
+    sq.mlx_repack(fmt, n, k, to_device(weight), to_device(scales), to_device(biases), p0, m)
+    t.cuda.synchronize()
+    assert np.array_equal(p0.cpu().numpy(), plane0)
+    assert np.array_equal(m.cpu().numpy(), meta)
