@@ -59,8 +59,6 @@ void requireSegments(const Projection &p, LinearMatrix matrix) {
     throw std::invalid_argument("block projection does not match plan");
   for (const QuantizedSegment &s : p.blocks().segments) {
     if (s.outputSize % SQ_TILE_COLUMNS) throw std::invalid_argument("block segments do not fill whole column tiles");
-    if (!sq_tile_format(s.formatId))
-      throw std::invalid_argument(std::string("the decode and prefill tiles do not run ") + s.name() + " weights");
     requireSegmentPlanes(s, "projection");
   }
 }
@@ -322,6 +320,14 @@ PreparedInput Linear::add(hipStream_t graph, LinearBuffers b, const Projection &
   if (selected.destination() == FloatOutput::Float32 && segments.size() > 1)
     throw std::invalid_argument("an fp32 destination takes a single-tensor block projection");
   const LinearConfig config = selected.configuration();
+  // The column tile (decode, at most four rows) runs every format; the row and prefill tiles the 4-bit ones.
+  const bool column = config.tile == LinearTile::GgufStaged && w.rows <= kern::kColumnTileRows;
+  for (const Projection *q : {&p, gate})
+    if (q)
+      for (const QuantizedSegment &s : q->blocks().segments)
+        if (!(column ? kern::column_tile_format(s.formatId) : sq_tile_format(s.formatId)))
+          throw std::invalid_argument(std::string(column ? "the decode tile" : "this tile") + " does not run " +
+                                      s.name() + " weights" + (column ? "" : " (decode rows of at most four do)"));
   const uint32_t groupUnit = planScaleGroups(&p, gate);
   if (config.tile == LinearTile::GgufStaged) {
     if ((k / 32) % (config.splits * groupUnit))

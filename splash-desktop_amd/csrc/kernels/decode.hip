@@ -136,7 +136,8 @@ hipError_t launch_format(uint32_t epilogue, bool f32_output, bool pair, const De
 
 DecodeLayout decode_layout(uint32_t fmt, uint32_t blocks, uint32_t K, uint32_t splits, bool pair, uint32_t rows) {
   const uint32_t sg = sq_format(fmt).meta_groups;   // groups of 32 per meta unit
-  if (!sq_tile_format(fmt) || !splits || !rows || rows > SQ_MAXIMUM_DECODE_ROWS || blocks % 4) return {0, 0};
+  const bool runs = rows <= kColumnTileRows ? column_tile_format(fmt) : sq_tile_format(fmt);
+  if (!runs || !splits || !rows || rows > SQ_MAXIMUM_DECODE_ROWS || blocks % 4) return {0, 0};
   const uint32_t units = K / 32 / sg;
   if (units % splits || !(units / splits)) return {0, 0};
   // The shortest slices (8, 16 or 32 groups; a gate/up pair streams two tensors, at most 16) whose waves fit one

@@ -43,7 +43,10 @@ __device__ __forceinline__ float lane_value(float v, int lane) {
 template <uint32_t FMT, int MR, int GW, int NT, uint32_t EP, bool F32OUT>
 __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs a) {
   using F = Fmt<FMT>;
-  constexpr int SG = F::SG, UNIT = F::UNIT, P = GW < kPipe ? GW : kPipe;
+  // Groups in flight: 8-bit codes of a gate/up pair (four 16-byte loads a group) keep two, to fit the registers of
+  // a full workgroup.
+  constexpr int kDepth = F::P0 == 32 && NT == 2 ? 2 : kPipe;
+  constexpr int SG = F::SG, UNIT = F::UNIT, P = GW < kDepth ? GW : kDepth;
   static_assert(GW % UNIT == 0 && GW % 2 == 0 && GW % SG == 0, "a slice holds whole meta units and group pairs");
   const int lane = threadIdx.x & 63, b = lane >> 2, i = lane & 3;
   const uint32_t slice = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), waves = blockDim.x >> 6;
@@ -55,15 +58,19 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
   const uint32_t gb = split * gs + slice * GW, live = min((uint32_t)GW, gs - min(gs, slice * GW));
   const uint32_t last = live ? live - 1 : 0;
 
-  const uint8_t *plane[NT], *meta[NT];
+  const uint8_t *plane[NT], *meta[NT], *high[NT];
   {
-    const size_t pbase = ((size_t)tile * G * 64 + lane) * 16 + (size_t)gb * 1024;
+    const size_t pbase = ((size_t)tile * G * 64 + lane) * F::P0 + (size_t)gb * 64 * F::P0;
+    const size_t hbase = ((size_t)tile * G * 64 + lane) * F::P1 + (size_t)gb * 64 * F::P1;
     const size_t mbase = ((size_t)tile * units * 64 + lane) * F::META + (size_t)(gb / UNIT) * 64 * F::META;
-    plane[0] = (NT == 2 ? a.gate.plane0 : seg.plane0) + pbase;
-    meta[0] = (NT == 2 ? a.gate.meta : seg.meta) + mbase;
+    const Segment &first = NT == 2 ? a.gate : seg;
+    plane[0] = first.plane0 + pbase;
+    meta[0] = first.meta + mbase;
+    high[0] = F::P1 ? first.plane1 + hbase : nullptr;
     if constexpr (NT == 2) {
       plane[1] = seg.plane0 + pbase;
       meta[1] = seg.meta + mbase;
+      high[1] = F::P1 ? seg.plane1 + hbase : nullptr;
     }
   }
   // Lane (b, i) reads row i's inputs 4 (b % 8)..+3 of the pair's group b / 8; rows past the live ones read row 0,
@@ -77,8 +84,11 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
 #pragma unroll
     for (int r = 0; r < MR; ++r) acc[n][r] = 0.0f;
 
+  constexpr bool kWide = F::P0 == 32;   // 8-bit codes: two 16-byte loads and two operand sets a group
   u32x2 xp[GW / 2];
   u32x4 codes[NT][GW];
+  u32x4 codes_hi[NT][kWide ? GW : 1];
+  u32x2 highs[NT][F::P1 ? GW : 1];
   MetaWords mw[NT][GW / UNIT];
   const auto issue = [&](int u) __attribute__((always_inline)) {
     if (u % 2 == 0) xp[u / 2] = *(const u32x2 *)(xrow + (size_t)min((uint32_t)(u + (b >> 3)), last) * 32);
@@ -89,15 +99,24 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
     }
     const uint32_t g = min((uint32_t)u, last);
 #pragma unroll
-    for (int n = 0; n < NT; ++n) codes[n][u] = __builtin_nontemporal_load((const u32x4 *)(plane[n] + (size_t)g * 1024));
+    for (int n = 0; n < NT; ++n) {
+      const uint8_t *unit = plane[n] + (size_t)g * 64 * F::P0;
+      codes[n][u] = __builtin_nontemporal_load((const u32x4 *)unit);
+      if constexpr (kWide) codes_hi[n][u] = __builtin_nontemporal_load((const u32x4 *)(unit + 16));
+      if constexpr (F::P1 == 4)
+        highs[n][u][0] = __builtin_nontemporal_load((const uint32_t *)(high[n] + (size_t)g * 64 * F::P1));
+      if constexpr (F::P1 == 8) highs[n][u] = __builtin_nontemporal_load((const u32x2 *)(high[n] + (size_t)g * 64 * F::P1));
+    }
   };
 #pragma unroll
   for (int u = 0; u < P; ++u) issue(u);
 
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4 C0[NT], C1[NT];
+  f32x4 C0[NT], C1[NT], H0[NT], H1[NT];   // H: the high nibbles' chains of 8-bit codes
   float pair_sum = 0.0f;   // lane's butterfly value of the current pair
+  float half_sum = 0.0f;   // the same over 16 inputs (Q6_K's scales cover halves of a group)
   float sx[MR];            // the rows' input sums over the current scale group
+  float sh[2][MR];         // Q6_K: the rows' input sums over each half of the group
 #pragma unroll
   for (int u = 0; u < GW; ++u) {
     if (u + P < GW) issue(u + P);
@@ -108,11 +127,18 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
         float t = quad_sum(xp[p]);
         t += __shfl_xor(t, 4);
         t += __shfl_xor(t, 8);
+        half_sum = t;             // lanes b % 8 < 4: the first half's sum; b % 8 >= 4: the second's
         t += __shfl_xor(t, 16);   // lanes b < 8: group 2p's sum; b >= 8: group 2p + 1's
         if constexpr (SG > 1) t += __shfl_xor(t, 32);
         pair_sum = t;
       }
-      if constexpr (SG == 1) {
+      if constexpr (F::HALVES) {
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+          sh[0][r] = lane_value(half_sum, 32 * h + r);
+          sh[1][r] = lane_value(half_sum, 32 * h + 16 + r);
+        }
+      } else if constexpr (SG == 1) {
 #pragma unroll
         for (int r = 0; r < MR; ++r) sx[r] = lane_value(pair_sum, 32 * h + r);
       } else if (h == 0) {
@@ -127,19 +153,48 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
       for (int n = 0; n < NT; ++n)
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-          const u32x4 w = code_pairs(codes[n][u][d], cc);
-          C0[n] = mfma_bcast(8 * h + d, xp[p], u32x2{w[0], w[1]}, first && d == 0 ? zero : C0[n]);
-          C1[n] = mfma_bcast(8 * h + 4 + d, xp[p], u32x2{w[2], w[3]}, first && d == 0 ? zero : C1[n]);
+          // Chunk d: plane word d (8-bit codes: words 2d and 2d + 1 of the 32-byte unit) and its plane1 bits.
+          uint32_t w0 = codes[n][u][d], w1 = 0u, hb = 0u;
+          if constexpr (kWide) {
+            w0 = d < 2 ? codes[n][u][2 * d] : codes_hi[n][u][2 * d - 4];
+            w1 = d < 2 ? codes[n][u][2 * d + 1] : codes_hi[n][u][2 * d - 3];
+          }
+          if constexpr (F::P1 == 4) hb = (highs[n][u][0] >> (8 * d)) & 0xFFu;
+          if constexpr (F::P1 == 8) hb = (highs[n][u][d >> 1] >> (16 * (d & 1))) & 0xFFFFu;
+          u32x4 lo, hi;
+          chunk_operands<FMT>(w0, w1, hb, cc, lo, hi);
+          C0[n] = mfma_bcast(8 * h + d, xp[p], u32x2{lo[0], lo[1]}, first && d == 0 ? zero : C0[n]);
+          C1[n] = mfma_bcast(8 * h + 4 + d, xp[p], u32x2{lo[2], lo[3]}, first && d == 0 ? zero : C1[n]);
+          if constexpr (kWide) {
+            H0[n] = mfma_bcast(8 * h + d, xp[p], u32x2{hi[0], hi[1]}, first && d == 0 ? zero : H0[n]);
+            H1[n] = mfma_bcast(8 * h + 4 + d, xp[p], u32x2{hi[2], hi[3]}, first && d == 0 ? zero : H1[n]);
+          }
         }
       if ((u + 1) % SG == 0) {
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
-          const Coef k = coef<FMT>(mw[n][u / UNIT], u);
-          const float zc = fmaf(-128.0f, k.s, k.z);
+          if constexpr (F::HALVES) {
+            // Q6_K: value = s_h (q - 32) = s_h (128 + q) - 160 s_h, a scale per half.
+            const float s0 = q6k_scale(mw[n][u / UNIT], u, 0), s1 = q6k_scale(mw[n][u / UNIT], u, 1);
 #pragma unroll
-          for (int r = 0; r < MR; ++r) {
-            acc[n][r] = fmaf(k.s, C0[n][r] + C1[n][r], acc[n][r]);
-            acc[n][r] = fmaf(zc, sx[r], acc[n][r]);
+            for (int r = 0; r < MR; ++r) {
+              acc[n][r] = fmaf(s0, C0[n][r], acc[n][r]);
+              acc[n][r] = fmaf(s1, C1[n][r], acc[n][r]);
+              acc[n][r] = fmaf(-160.0f * s0, sh[0][r], acc[n][r]);
+              acc[n][r] = fmaf(-160.0f * s1, sh[1][r], acc[n][r]);
+            }
+          } else {
+            const Coef k = coef<FMT>(mw[n][u / UNIT], u);
+            // 8-bit codes: sum x u = C_lo + 16 C_hi - 2176 sum x (Q8_0's value d (u - 128): z = -128 d).
+            const float zc = kWide ? fmaf(-2176.0f, k.s, FMT == SQ_FMT_Q80 ? -128.0f * k.s : k.z)
+                                   : fmaf(-128.0f, k.s, k.z);
+#pragma unroll
+            for (int r = 0; r < MR; ++r) {
+              float c = C0[n][r] + C1[n][r];
+              if constexpr (kWide) c = fmaf(16.0f, H0[n][r] + H1[n][r], c);
+              acc[n][r] = fmaf(k.s, c, acc[n][r]);
+              acc[n][r] = fmaf(zc, sx[r], acc[n][r]);
+            }
           }
         }
       }
@@ -236,6 +291,10 @@ hipError_t launch_decode_column(uint32_t fmt, uint32_t epilogue, bool f32_output
     case SQ_FMT_AF4G64: return launch_format<SQ_FMT_AF4G64>(epilogue, f32_output, pair, a, tiles, layout, stream);
     case SQ_FMT_AF4G128: return launch_format<SQ_FMT_AF4G128>(epilogue, f32_output, pair, a, tiles, layout, stream);
     case SQ_FMT_Q4K: return launch_format<SQ_FMT_Q4K>(epilogue, f32_output, pair, a, tiles, layout, stream);
+    case SQ_FMT_Q5K: return launch_format<SQ_FMT_Q5K>(epilogue, f32_output, pair, a, tiles, layout, stream);
+    case SQ_FMT_Q6K: return launch_format<SQ_FMT_Q6K>(epilogue, f32_output, pair, a, tiles, layout, stream);
+    case SQ_FMT_Q80: return launch_format<SQ_FMT_Q80>(epilogue, f32_output, pair, a, tiles, layout, stream);
+    case SQ_FMT_AF8G64: return launch_format<SQ_FMT_AF8G64>(epilogue, f32_output, pair, a, tiles, layout, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -171,4 +171,40 @@ __device__ __forceinline__ float q6k_scale(const MetaWords &m, uint32_t sg, uint
   return f16_to_f32(m.w[4] & 0xFFFFu) * (float)(int8_t)(m.w[i >> 2] >> (8 * (i & 3)));
 }
 
+// The exact bf16 operands of chunk c of a group (elements 4c..4c+3 and 16+4c..19+4c, pairs 0..3), for every
+// format: `w0` the chunk's plane0 word (8-bit formats: its first word, pairs 0 and 1, and `w1` its second, pairs 2
+// and 3), `high` the chunk's plane1 bits (Q5_K: byte c, bit 2p + i for element i of pair p; Q6_K: halfword c, bits
+// 4p + 2i). Codes of at most 7 bits make one operand 128 + q each, in `lo`; 8-bit codes u (Q8_0's signed byte
+// + 128) make two, 128 + (u & 15) in `lo` and 128 + (u >> 4) in `hi`, so sum x u = C_lo + 16 C_hi - 2176 sum x.
+template <uint32_t FMT>
+__device__ __forceinline__ void chunk_operands(uint32_t w0, uint32_t w1, uint32_t high, CodeConstants cc, u32x4 &lo,
+                                               u32x4 &hi) {
+  if constexpr (Fmt<FMT>::P0 == 32) {
+    const uint32_t flip = FMT == SQ_FMT_Q80 ? 0x80808080u : 0u;   // the signed byte v as u = v + 128
+    const uint32_t a = w0 ^ flip, b = w1 ^ flip, nib = 0x0F0F0F0Fu, e = 0x43434343u;
+    const uint32_t al = a & nib, bl = b & nib, ah = (a >> 4) & nib, bh = (b >> 4) & nib;
+    // Byte pair (2p', 2p' + 1) of a word into the two halves of an operand, exponent byte 0x43 above each.
+    lo = u32x4{__builtin_amdgcn_perm(e, al, 0x04010400u), __builtin_amdgcn_perm(e, al, 0x04030402u),
+               __builtin_amdgcn_perm(e, bl, 0x04010400u), __builtin_amdgcn_perm(e, bl, 0x04030402u)};
+    hi = u32x4{__builtin_amdgcn_perm(e, ah, 0x04010400u), __builtin_amdgcn_perm(e, ah, 0x04030402u),
+               __builtin_amdgcn_perm(e, bh, 0x04010400u), __builtin_amdgcn_perm(e, bh, 0x04030402u)};
+  } else {
+    lo = code_pairs(w0, cc);
+    if constexpr (Fmt<FMT>::P1 == 4) {
+      // Fifth bits: bit 2p + i of the byte to bit 4 of half i of operand p.
+      const uint32_t s = ((high & 0x55u) | ((high & 0xAAu) << 15)) << 4;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) lo[p] |= (s >> (2 * p)) & 0x00100010u;
+    } else if constexpr (Fmt<FMT>::P1 == 8) {
+      // High two bits: bits 4p + 2i of the halfword to bits 4..5 of half i of operand p. The spread word holds
+      // half i of pair p at bits 16 i + 4p (pair 3's second half at 28..29, so it is moved into place per pair).
+      const uint32_t s = (high & 0x3333u) | ((high & 0xCCCCu) << 14);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) lo[p] |= ((s >> (4 * p)) & 0x00030003u) << 4;
+    }
+    (void)w1;
+    (void)hi;
+  }
+}
+
 }  // namespace sq::kern

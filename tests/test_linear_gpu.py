@@ -206,3 +206,55 @@ def test_baseline_shapes_policy_plans(n, k, rows):
     plan = sq.plan_for(sq.decode_workload(n, k, rows), proj)
     got = run_plan(plan, proj, x, n)
     check_projection(got, x, w, f"{n}x{k} rows {rows}")
+
+
+NEW_FORMATS = [oracle.FMT_Q5K, oracle.FMT_Q6K, oracle.FMT_Q80, oracle.FMT_AF8G64]
+
+
+@pytest.mark.parametrize("fmt", NEW_FORMATS)
+@pytest.mark.parametrize("rows", [1, 2, 4])
+@pytest.mark.parametrize("splits", [1, 4])
+def test_decode_new_formats(fmt, rows, splits):
+    """Q5_K, Q6_K, Q8_0 and af8g64 through the decode column tile (rows <= 4): every output inside its fp64
+    interval, the BASELINE tolerances, and no worse than the reference's staged numerics."""
+    rng = np.random.default_rng(2000 * fmt + 10 * rows + splits)
+    n, k = 256, 2048
+    w = make_weights(rng, fmt, n, k)
+    x = dense_inputs(rng, rows, k)
+    got = run_plan(staged(n, k, rows, splits), sq.projection(w.segment()), x, n)
+    stats = check_projection(got, x, w, f"fmt {fmt} rows {rows} splits {splits}")
+    ref = staged_reference(x, w)
+    value, *_ = oracle.project_f64(x, w.values)
+    ref_l2 = np.linalg.norm(synthetic.bf16_to_f32(ref) - value) / np.linalg.norm(value)
+    assert stats["rel_l2"] <= ref_l2 * 1.10 + 1e-6
+
+
+@pytest.mark.parametrize("fmt", NEW_FORMATS)
+def test_decode_new_formats_fixture_and_pairs(fmt):
+    """The reference's fixture weights (every byte random, finite half scales) through the column tile, sparse
+    +-1e5 inputs, and a one-pass gate/up pair bitwise equal to two passes."""
+    rng = np.random.default_rng(77 + fmt)
+    n, k = 128, 1024
+    native = oracle.fixture(fmt, n, k, 9)
+    if fmt == oracle.FMT_AF8G64:
+        native = make_weights(rng, fmt, n, k).native
+    w = Weights(fmt, n, k, native)
+    if np.isfinite(w.values).all() and np.abs(w.values).max() < 1e30:
+        x = sparse_inputs(3, k, 1.0)
+        got = run_plan(staged(n, k, 3, 1), sq.projection(w.segment()), x, n)
+        check_projection(got, x, w, f"fixture fmt {fmt}")
+    wg, wu = make_weights(rng, fmt, 256, 2048), make_weights(rng, fmt, 256, 2048)
+    x = dense_inputs(rng, 2, 2048)
+    gate, up = sq.projection(wg.segment()), sq.projection(wu.segment())
+    two = run_plan(staged(256, 2048, 2, 2, sq.EPILOGUE_GATE_UP), up, x, 256, gate=gate)
+    one = run_plan(staged(256, 2048, 2, 2, sq.EPILOGUE_GATE_UP, one_pass=1), up, x, 256, gate=gate)
+    assert np.array_equal(one, two)
+
+
+@pytest.mark.parametrize("fmt", NEW_FORMATS)
+def test_new_formats_refused_past_the_column_tile(fmt):
+    """The row tile (more than four rows) does not run these formats yet: refused before any launch."""
+    rng = np.random.default_rng(5)
+    w = make_weights(rng, fmt, 128, 1024)
+    with pytest.raises(sq.InvalidArgument, match="does not run"):
+        run_plan(staged(128, 1024, 8, 1), sq.projection(w.segment()), dense_inputs(rng, 8, 1024), 128)
