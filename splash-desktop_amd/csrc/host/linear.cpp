@@ -320,14 +320,17 @@ PreparedInput Linear::add(hipStream_t graph, LinearBuffers b, const Projection &
   if (selected.destination() == FloatOutput::Float32 && segments.size() > 1)
     throw std::invalid_argument("an fp32 destination takes a single-tensor block projection");
   const LinearConfig config = selected.configuration();
-  // The column tile (decode, at most four rows) runs every format; the row and prefill tiles the 4-bit ones.
-  const bool column = config.tile == LinearTile::GgufStaged && w.rows <= kern::kColumnTileRows;
+  // The decode tiles (the column tile to four rows, the row tile past it) run every format; the prefill tile the
+  // 4-bit ones.
+  const bool staged = config.tile == LinearTile::GgufStaged;
+  const bool column = staged && w.rows <= kern::kColumnTileRows;
   for (const Projection *q : {&p, gate})
     if (q)
       for (const QuantizedSegment &s : q->blocks().segments)
-        if (!(column ? kern::column_tile_format(s.formatId) : sq_tile_format(s.formatId)))
-          throw std::invalid_argument(std::string(column ? "the decode tile" : "this tile") + " does not run " +
-                                      s.name() + " weights" + (column ? "" : " (decode rows of at most four do)"));
+        if (!(column ? kern::column_tile_format(s.formatId)
+                     : staged ? kern::row_tile_format(s.formatId) : sq_tile_format(s.formatId)))
+          throw std::invalid_argument(std::string(staged ? "the decode tile" : "the prefill tile") + " does not run " +
+                                      s.name() + " weights" + (staged ? "" : " (decode rows of at most 32 do)"));
   const uint32_t groupUnit = planScaleGroups(&p, gate);
   if (config.tile == LinearTile::GgufStaged) {
     if ((k / 32) % (config.splits * groupUnit))

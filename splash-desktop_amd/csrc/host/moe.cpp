@@ -28,7 +28,7 @@ void requireExperts(const QuantizedSegment &s, uint32_t slots, uint32_t n, uint3
                     const char *name) {
   if (s.formatId != format || s.outputSize != uint64_t{slots} * n || s.inputSize != k)
     throw std::invalid_argument(std::string("MoE expert ") + name + " does not match the plan");
-  if (!sq_tile_format(format))
+  if (!kern::row_tile_format(format))
     throw std::invalid_argument(std::string("the MoE expert passes do not run ") + s.name() + " weights");
   requireSegmentPlanes(s, std::string("MoE expert ") + name);
 }
@@ -159,10 +159,14 @@ void MoE::addRouted(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w,
   a.meta[0] = w.gate.meta.as<const uint8_t>();
   a.plane0[1] = w.up.plane0.as<const uint8_t>();
   a.meta[1] = w.up.meta.as<const uint8_t>();
+  a.plane1[0] = w.gate.plane1.as<const uint8_t>();
+  a.plane1[1] = w.up.plane1.as<const uint8_t>();
   a.shared_plane0[0] = w.sharedGate.plane0.as<const uint8_t>();
   a.shared_meta[0] = w.sharedGate.meta.as<const uint8_t>();
   a.shared_plane0[1] = w.sharedUp.plane0.as<const uint8_t>();
   a.shared_meta[1] = w.sharedUp.meta.as<const uint8_t>();
+  a.shared_plane1[0] = w.sharedGate.plane1.as<const uint8_t>();
+  a.shared_plane1[1] = w.sharedUp.plane1.as<const uint8_t>();
   a.output = sc.expertIntermediate.as<uint16_t>();
   a.K = s.hiddenSize;
   a.output_size = s.expertIntermediateSize;
@@ -174,9 +178,13 @@ void MoE::addRouted(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w,
   a.plane0[0] = w.down.plane0.as<const uint8_t>();
   a.meta[0] = w.down.meta.as<const uint8_t>();
   a.plane0[1] = a.meta[1] = nullptr;
+  a.plane1[0] = w.down.plane1.as<const uint8_t>();
+  a.plane1[1] = nullptr;
   a.shared_plane0[0] = w.sharedDown.plane0.as<const uint8_t>();
   a.shared_meta[0] = w.sharedDown.meta.as<const uint8_t>();
   a.shared_plane0[1] = a.shared_meta[1] = nullptr;
+  a.shared_plane1[0] = w.sharedDown.plane1.as<const uint8_t>();
+  a.shared_plane1[1] = nullptr;
   a.output = sc.expertOutput.as<uint16_t>();
   a.K = s.expertIntermediateSize;
   a.output_size = s.hiddenSize;

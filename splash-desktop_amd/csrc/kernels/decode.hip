@@ -33,14 +33,18 @@ __global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeA
   const uint32_t G = a.K >> 5, units = G / F::UNIT, gs = G / a.splits;
   const uint32_t gb = split * gs + slice * GW, live = min((uint32_t)GW, gs - min(gs, slice * GW));
 
-  const uint8_t *plane[NT], *meta[NT];
+  const uint8_t *plane[NT], *high[NT], *meta[NT];
   {
-    const size_t pbase = ((size_t)tile * G * 64 + lane) * 16 + (size_t)gb * 1024;
+    const size_t pbase = ((size_t)tile * G * 64 + lane) * F::P0 + (size_t)gb * 64 * F::P0;
+    const size_t hbase = ((size_t)tile * G * 64 + lane) * F::P1 + (size_t)gb * 64 * F::P1;
     const size_t mbase = ((size_t)tile * units * 64 + j) * F::META + (size_t)(gb / F::UNIT) * 64 * F::META;
-    plane[0] = (NT == 2 ? a.gate.plane0 : seg.plane0) + pbase;
-    meta[0] = (NT == 2 ? a.gate.meta : seg.meta) + mbase;
+    const Segment &first = NT == 2 ? a.gate : seg;
+    plane[0] = first.plane0 + pbase;
+    high[0] = F::P1 ? first.plane1 + hbase : nullptr;
+    meta[0] = first.meta + mbase;
     if constexpr (NT == 2) {
       plane[1] = seg.plane0 + pbase;
+      high[1] = F::P1 ? seg.plane1 + hbase : nullptr;
       meta[1] = seg.meta + mbase;
     }
   }
@@ -54,7 +58,7 @@ __global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeA
   }
   float acc[NT][4][MB][4];
   clear(acc);
-  row_slice<FMT, MB, GW, NT>(plane, meta, xrow, live, acc);
+  row_slice<FMT, MB, GW, NT>(plane, high, meta, xrow, live, acc);
 
   __shared__ float red[row_max_waves(MB, NT) * A * 64];
   float sum[A];
@@ -136,7 +140,7 @@ hipError_t launch_format(uint32_t epilogue, bool f32_output, bool pair, const De
 
 DecodeLayout decode_layout(uint32_t fmt, uint32_t blocks, uint32_t K, uint32_t splits, bool pair, uint32_t rows) {
   const uint32_t sg = sq_format(fmt).meta_groups;   // groups of 32 per meta unit
-  const bool runs = rows <= kColumnTileRows ? column_tile_format(fmt) : sq_tile_format(fmt);
+  const bool runs = rows <= kColumnTileRows ? column_tile_format(fmt) : row_tile_format(fmt);
   if (!runs || !splits || !rows || rows > SQ_MAXIMUM_DECODE_ROWS || blocks % 4) return {0, 0};
   const uint32_t units = K / 32 / sg;
   if (units % splits || !(units / splits)) return {0, 0};
@@ -162,6 +166,10 @@ hipError_t launch_decode(uint32_t fmt, uint32_t epilogue, bool f32_output, const
     case SQ_FMT_AF4G64: return launch_format<SQ_FMT_AF4G64>(epilogue, f32_output, pair, args, tiles, layout, stream);
     case SQ_FMT_AF4G128: return launch_format<SQ_FMT_AF4G128>(epilogue, f32_output, pair, args, tiles, layout, stream);
     case SQ_FMT_Q4K: return launch_format<SQ_FMT_Q4K>(epilogue, f32_output, pair, args, tiles, layout, stream);
+    case SQ_FMT_Q5K: return launch_format<SQ_FMT_Q5K>(epilogue, f32_output, pair, args, tiles, layout, stream);
+    case SQ_FMT_Q6K: return launch_format<SQ_FMT_Q6K>(epilogue, f32_output, pair, args, tiles, layout, stream);
+    case SQ_FMT_Q80: return launch_format<SQ_FMT_Q80>(epilogue, f32_output, pair, args, tiles, layout, stream);
+    case SQ_FMT_AF8G64: return launch_format<SQ_FMT_AF8G64>(epilogue, f32_output, pair, args, tiles, layout, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -21,6 +21,12 @@ __device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
                                                   0, 0);
 }
+// D = A B + C on a 16x16x16 bf16 tile: lane l holds A[l % 16][4 (l / 16) + i], B[4 (l / 16) + i][l % 16] (i = 0..3)
+// and D as mfma_bf16 does.
+__device__ __forceinline__ f32x4 mfma_bf16_k16(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0,
+                                                    0, 0);
+}
 __device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
                                                  0);
@@ -176,18 +182,21 @@ __device__ __forceinline__ float q6k_scale(const MetaWords &m, uint32_t sg, uint
 // and 3), `high` the chunk's plane1 bits (Q5_K: byte c, bit 2p + i for element i of pair p; Q6_K: halfword c, bits
 // 4p + 2i). Codes of at most 7 bits make one operand 128 + q each, in `lo`; 8-bit codes u (Q8_0's signed byte
 // + 128) make two, 128 + (u & 15) in `lo` and 128 + (u >> 4) in `hi`, so sum x u = C_lo + 16 C_hi - 2176 sum x.
-template <uint32_t FMT>
+// With HI16 the `hi` operands are 16 (128 + (u >> 4)) = 2048 + 16 (u >> 4) instead (bf16 exponent byte 0x45, still
+// exact), so that both sets can add into one accumulator: sum x u = C - 2176 sum x.
+template <uint32_t FMT, bool HI16 = false>
 __device__ __forceinline__ void chunk_operands(uint32_t w0, uint32_t w1, uint32_t high, CodeConstants cc, u32x4 &lo,
                                                u32x4 &hi) {
   if constexpr (Fmt<FMT>::P0 == 32) {
     const uint32_t flip = FMT == SQ_FMT_Q80 ? 0x80808080u : 0u;   // the signed byte v as u = v + 128
     const uint32_t a = w0 ^ flip, b = w1 ^ flip, nib = 0x0F0F0F0Fu, e = 0x43434343u;
+    const uint32_t eh = HI16 ? 0x45454545u : e;
     const uint32_t al = a & nib, bl = b & nib, ah = (a >> 4) & nib, bh = (b >> 4) & nib;
     // Byte pair (2p', 2p' + 1) of a word into the two halves of an operand, exponent byte 0x43 above each.
     lo = u32x4{__builtin_amdgcn_perm(e, al, 0x04010400u), __builtin_amdgcn_perm(e, al, 0x04030402u),
                __builtin_amdgcn_perm(e, bl, 0x04010400u), __builtin_amdgcn_perm(e, bl, 0x04030402u)};
-    hi = u32x4{__builtin_amdgcn_perm(e, ah, 0x04010400u), __builtin_amdgcn_perm(e, ah, 0x04030402u),
-               __builtin_amdgcn_perm(e, bh, 0x04010400u), __builtin_amdgcn_perm(e, bh, 0x04030402u)};
+    hi = u32x4{__builtin_amdgcn_perm(eh, ah, 0x04010400u), __builtin_amdgcn_perm(eh, ah, 0x04030402u),
+               __builtin_amdgcn_perm(eh, bh, 0x04010400u), __builtin_amdgcn_perm(eh, bh, 0x04030402u)};
   } else {
     lo = code_pairs(w0, cc);
     if constexpr (Fmt<FMT>::P1 == 4) {

@@ -30,9 +30,10 @@ struct Segment {
 //  - The row tile (more rows): grid (64-column tiles, splits) of up to 16 waves (fewer for more than 16 rows or a
 //    gate/up pair), rows on the MFMA's 16-row side.
 constexpr uint32_t kColumnTileRows = 4;
-// The formats each tile runs: the column tile every format this build takes; the row tile, the prefill tile and the
-// MoE expert passes the 4-bit ones (sq_tile_format).
+// The formats each tile runs: the decode column and row tiles and the MoE expert passes every format this build
+// takes; the prefill tile the 4-bit ones (sq_tile_format).
 SQ_HD inline bool column_tile_format(uint32_t f) { return sq_format_supported(f); }
+SQ_HD inline bool row_tile_format(uint32_t f) { return sq_format_supported(f); }
 // The column tile's most waves (K slices) per workgroup, and the most groups of 32 inputs one wave streams.
 constexpr uint32_t kColumnMaxWaves = 16, kColumnMaxGroups = 32;
 struct DecodeArgs {
@@ -116,8 +117,10 @@ struct MoeExpertArgs {
   const SqMoeTileCount *tile_count;
   const uint8_t *plane0[2];     // gate (or the single pass's weights), up
   const uint8_t *meta[2];
+  const uint8_t *plane1[2];     // Q5_K and Q6_K high bits (null otherwise)
   const uint8_t *shared_plane0[2];
   const uint8_t *shared_meta[2];
+  const uint8_t *shared_plane1[2];
   const uint32_t *slots;
   uint16_t *output;             // [tiles * tile_rows][output_size]
   uint32_t K, output_size, tile_rows, max_tiles, fmt, gate_up, routes_per_row, experts, mode;

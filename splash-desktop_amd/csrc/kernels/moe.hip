@@ -193,10 +193,11 @@ __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDes
   // shared segment on.
   const bool shared = d.expert >= a.experts;
   const uint32_t ptile = (shared ? d.expert - a.experts : a.slots[d.expert]) * column_tiles + ct;
-  const uint8_t *plane[NT], *meta[NT];
+  const uint8_t *plane[NT], *high[NT], *meta[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
-    plane[n] = (shared ? a.shared_plane0[n] : a.plane0[n]) + ((size_t)ptile * G * 64 + lane) * 16;
+    plane[n] = (shared ? a.shared_plane0[n] : a.plane0[n]) + ((size_t)ptile * G * 64 + lane) * F::P0;
+    high[n] = F::P1 ? (shared ? a.shared_plane1[n] : a.plane1[n]) + ((size_t)ptile * G * 64 + lane) * F::P1 : nullptr;
     meta[n] = (shared ? a.shared_meta[n] : a.meta[n]) + ((size_t)ptile * (G / F::UNIT) * 64 + j) * F::META;
   }
   // Lane (j, q) of row block b reads row 16 b + j (row 0 past the tile's rows: nothing stores those results).
@@ -209,10 +210,10 @@ __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDes
   }
   float acc[NT][4][MB][4];
   clear(acc);
-  // A gate/up pair runs one wave a SIMD anyway: it takes a third register set to look further ahead (Q4_K's
-  // headers leave no room for it).
-  constexpr int kSets = NT == 2 && FMT != SQ_FMT_Q4K ? 3 : 2;
-  row_stream<FMT, MB, NT, kSets>(plane, meta, xrow, G, acc);
+  // A gate/up pair runs one wave a SIMD anyway: it takes a third register set to look further ahead (the K-quant
+  // headers and 8-bit codes leave no room for it).
+  constexpr int kSets = NT == 2 && F::UNIT < 8 && F::P0 == 16 ? 3 : 2;
+  row_stream<FMT, MB, NT, kSets>(plane, high, meta, xrow, G, acc);
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -312,6 +313,10 @@ hipError_t launch_moe_expert(const MoeExpertArgs &a, hipStream_t stream) {
     case SQ_FMT_AF4G64: return launch_expert_format<SQ_FMT_AF4G64>(a, stream);
     case SQ_FMT_AF4G128: return launch_expert_format<SQ_FMT_AF4G128>(a, stream);
     case SQ_FMT_Q4K: return launch_expert_format<SQ_FMT_Q4K>(a, stream);
+    case SQ_FMT_Q5K: return launch_expert_format<SQ_FMT_Q5K>(a, stream);
+    case SQ_FMT_Q6K: return launch_expert_format<SQ_FMT_Q6K>(a, stream);
+    case SQ_FMT_Q80: return launch_expert_format<SQ_FMT_Q80>(a, stream);
+    case SQ_FMT_AF8G64: return launch_expert_format<SQ_FMT_AF8G64>(a, stream);
     default: return hipErrorInvalidValue;
   }
 }

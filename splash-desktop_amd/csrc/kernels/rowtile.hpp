@@ -31,22 +31,173 @@ __device__ __forceinline__ void transpose4(uint32_t (&r)[4]) {
   r[3] = d[1];
 }
 
-// Adds GW groups (the first `live` of them) of NT tensors' plane tiles to acc[n][t][b][i] (tensor n, column
-// block t, row block b, row 4q + i of the block). plane[n] and meta[n] point at the slice's first group for
-// the lane (plane: + 16 lane; meta: + META j); xrow[b] at the lane's row 16 b + j, inputs 4q of the slice's first
-// group.
-template <uint32_t FMT, int MB, int GW, int NT>
-__device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], const uint8_t *const (&meta)[NT],
-                                          const uint16_t *const (&xrow)[MB], uint32_t live,
-                                          float (&acc)[NT][4][MB][4]) {
+// One group of 32 inputs of the lane's column: plane0 (16 bytes; 8-bit codes 32, `lo` then `hi`) and plane1 (Q5_K 4
+// bytes, Q6_K 8). Members a format does not have are never read.
+template <uint32_t FMT>
+struct RowGroup {
+  u32x4 lo, hi;
+  u32x2 high;
+};
+// plane and high point at group 0 of the lane's column (plane + P0 lane, high + P1 lane).
+template <uint32_t FMT>
+__device__ __forceinline__ RowGroup<FMT> load_row_group(const uint8_t *plane, const uint8_t *high, uint32_t g) {
   using F = Fmt<FMT>;
-  constexpr int SG = F::SG, UNIT = F::UNIT, P = GW < kRowPipe ? GW : kRowPipe;
+  RowGroup<FMT> r;
+  const uint8_t *p = plane + (size_t)g * 64 * F::P0;
+  r.lo = __builtin_nontemporal_load((const u32x4 *)p);
+  if constexpr (F::P0 == 32) r.hi = __builtin_nontemporal_load((const u32x4 *)(p + 16));
+  if constexpr (F::P1 == 4) r.high[0] = __builtin_nontemporal_load((const uint32_t *)(high + (size_t)g * 64 * 4));
+  if constexpr (F::P1 == 8) r.high = __builtin_nontemporal_load((const u32x2 *)(high + (size_t)g * 64 * 8));
+  return r;
+}
+
+// The lane's shift of its chunk's plane1 bits after the transpose (lane (j, q) holds chunk q): Q5_K byte q, Q6_K
+// halfword q % 2 of the word the transpose brings.
+template <uint32_t FMT>
+__device__ __forceinline__ uint32_t row_high_shift(int lane) {
+  const uint32_t q = (uint32_t)lane >> 4;
+  return Fmt<FMT>::P1 == 4 ? 8 * q : Fmt<FMT>::P1 == 8 ? 16 * (q & 1) : 0;
+}
+
+// The exact bf16 B operands of a group: lane (j, q) gets chunk q of column 16 t + j in lo[t] (chunk_operands); 8-bit
+// codes also get hi[t], the high nibbles as 16 (128 + q_hi), so that both add into one accumulator.
+//  - 4-bit codes: one 4x4 transpose of the four plane words;
+//  - 8-bit codes: chunk q is words 2q and 2q + 1 of the 32 bytes, one transpose of the even words and one of the odd;
+//  - plane1 bits follow the plane words: Q5_K's word transposed (lane (j, q) gets column 16 t + j's word in every
+//    register t, then byte q), Q6_K's two words as (w0, w0, w1, w1) (the word that holds halfword q).
+template <uint32_t FMT>
+__device__ __forceinline__ void row_operands(const RowGroup<FMT> &grp, uint32_t hshift, CodeConstants cc,
+                                             u32x4 (&lo)[4], u32x4 (&hi)[4]) {
+  using F = Fmt<FMT>;
+  if constexpr (F::P0 == 32) {
+    uint32_t e[4] = {grp.lo[0], grp.lo[2], grp.hi[0], grp.hi[2]}, o[4] = {grp.lo[1], grp.lo[3], grp.hi[1], grp.hi[3]};
+    transpose4(e);
+    transpose4(o);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) chunk_operands<FMT, true>(e[t], o[t], 0u, cc, lo[t], hi[t]);
+  } else {
+    uint32_t r[4] = {grp.lo[0], grp.lo[1], grp.lo[2], grp.lo[3]};
+    transpose4(r);
+    uint32_t h[4] = {0u, 0u, 0u, 0u};
+    if constexpr (F::P1 == 4) {
+      h[0] = h[1] = h[2] = h[3] = grp.high[0];
+      transpose4(h);
+    } else if constexpr (F::P1 == 8) {
+      h[0] = h[1] = grp.high[0];
+      h[2] = h[3] = grp.high[1];
+      transpose4(h);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) chunk_operands<FMT>(r[t], 0u, h[t] >> hshift, cc, lo[t], hi[t]);
+  }
+}
+
+// One group's MFMAs. C[n][t][b] takes sum x (operand) over the group (Q6_K: over its first half, C2 the second) and
+// S[b] the rows' input sums the same way, from zero when `first`. Q6_K's halves (one scale per 16 elements) run on
+// the 16x16x16 MFMA: operand words 0..1 of every lane are a chunk's first-half elements, words 2..3 its second.
+template <uint32_t FMT, int MB, int NT>
+__device__ __forceinline__ void row_group_mfma(const u32x4 (&x)[MB], const u32x4 (&lo)[NT][4],
+                                               const u32x4 (&hi)[NT][4], bool first, f32x4 (&C)[NT][4][MB],
+                                               f32x4 (&C2)[NT][4][MB], f32x4 (&S)[MB], f32x4 (&S2)[MB]) {
+  using F = Fmt<FMT>;
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (F::HALVES) {
+    const u32x2 one = {0x3F803F80u, 0x3F803F80u};
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+      S[b] = mfma_bf16_k16(u32x2{x[b][0], x[b][1]}, one, first ? zero : S[b]);
+      S2[b] = mfma_bf16_k16(u32x2{x[b][2], x[b][3]}, one, first ? zero : S2[b]);
+    }
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+          C[n][t][b] = mfma_bf16_k16(u32x2{x[b][0], x[b][1]}, u32x2{lo[n][t][0], lo[n][t][1]}, first ? zero : C[n][t][b]);
+          C2[n][t][b] = mfma_bf16_k16(u32x2{x[b][2], x[b][3]}, u32x2{lo[n][t][2], lo[n][t][3]}, first ? zero : C2[n][t][b]);
+        }
+  } else {
+#pragma unroll
+    for (int b = 0; b < MB; ++b) S[b] = mfma_bf16(x[b], ones_operand(), first ? zero : S[b]);
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int b = 0; b < MB; ++b) C[n][t][b] = mfma_bf16(x[b], lo[n][t], first ? zero : C[n][t][b]);
+    if constexpr (F::P0 == 32) {
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int b = 0; b < MB; ++b) C[n][t][b] = mfma_bf16(x[b], hi[n][t], C[n][t][b]);
+    }
+  }
+}
+
+// A scale group's close in fp32, every product exact: acc += s C + zc S with zc = z - 128 s (4-bit and 5-bit codes
+// 128 + q), z - 2176 s (8-bit codes, C = sum x u + 2176 sum x; Q8_0's value d (u - 128): z = -128 d), and Q6_K's
+// s_h (q - 32) = s_h (128 + q) - 160 s_h per half. `g` is the group's index in its meta unit's numbering (its
+// super-block position).
+template <uint32_t FMT, int MB, int NT>
+__device__ __forceinline__ void row_group_close(const MetaWords (&mw)[NT][4], uint32_t g, const f32x4 (&C)[NT][4][MB],
+                                                const f32x4 (&C2)[NT][4][MB], const f32x4 (&S)[MB],
+                                                const f32x4 (&S2)[MB], float (&acc)[NT][4][MB][4]) {
+  using F = Fmt<FMT>;
+#pragma unroll
+  for (int n = 0; n < NT; ++n)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if constexpr (F::HALVES) {
+        const float s0 = q6k_scale(mw[n][t], g, 0), s1 = q6k_scale(mw[n][t], g, 1);
+        const float z0 = -160.0f * s0, z1 = -160.0f * s1;
+#pragma unroll
+        for (int b = 0; b < MB; ++b)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            acc[n][t][b][i] = fmaf(s0, C[n][t][b][i], acc[n][t][b][i]);
+            acc[n][t][b][i] = fmaf(s1, C2[n][t][b][i], acc[n][t][b][i]);
+            acc[n][t][b][i] = fmaf(z0, S[b][i], acc[n][t][b][i]);
+            acc[n][t][b][i] = fmaf(z1, S2[b][i], acc[n][t][b][i]);
+          }
+      } else {
+        const Coef k = coef<FMT>(mw[n][t], g);
+        const float zc = F::P0 == 32 ? fmaf(-2176.0f, k.s, FMT == SQ_FMT_Q80 ? -128.0f * k.s : k.z)
+                                     : fmaf(-128.0f, k.s, k.z);
+#pragma unroll
+        for (int b = 0; b < MB; ++b)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            acc[n][t][b][i] = fmaf(k.s, C[n][t][b][i], acc[n][t][b][i]);
+            acc[n][t][b][i] = fmaf(zc, S[b][i], acc[n][t][b][i]);
+          }
+      }
+    }
+}
+
+// Adds GW groups (the first `live` of them) of NT tensors' plane tiles to acc[n][t][b][i] (tensor n, column
+// block t, row block b, row 4q + i of the block). plane[n] and high[n] point at the slice's first group for the
+// lane's column (load_row_group), meta[n] at its first meta unit for the lane (+ META j); xrow[b] at the lane's row
+// 16 b + j, inputs 4q of the slice's first group.
+template <uint32_t FMT, int MB, int GW, int NT>
+__device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], const uint8_t *const (&high)[NT],
+                                          const uint8_t *const (&meta)[NT], const uint16_t *const (&xrow)[MB],
+                                          uint32_t live, float (&acc)[NT][4][MB][4]) {
+  using F = Fmt<FMT>;
+  // 8-bit codes (twice the bytes a group) keep fewer groups in flight, and so do the K-quants with plane1 bits in the
+  // longest slices of one tensor's 16 rows (whose workgroups hold the most waves, 128 registers each).
+  constexpr bool kTight = F::P1 && MB == 1 && NT == 1 && GW == 32;
+  constexpr int kDepth = F::P0 == 32 || kTight ? kRowPipe / 2 : kRowPipe;
+  constexpr int SG = F::SG, UNIT = F::UNIT, P = GW < kDepth ? GW : kDepth;
   static_assert(GW % UNIT == 0 && GW % SG == 0, "a slice holds whole meta units");
   const uint32_t last = live ? live - 1 : 0;
   const CodeConstants cc = make_code_constants();
+  const uint32_t hshift = row_high_shift<FMT>(threadIdx.x & 63);
 
   u32x4 xv[MB][GW];
-  u32x4 codes[NT][GW];
+  RowGroup<FMT> codes[NT][GW];
   MetaWords mw[NT][4][GW / UNIT];
   const auto issue = [&](int u) __attribute__((always_inline)) {
     const uint32_t g = min((uint32_t)u, last);
@@ -64,47 +215,30 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
           mw[n][t][u / UNIT] = load_meta<FMT>(meta[n] + ((size_t)v * 64 + 16 * t) * F::META);
     }
 #pragma unroll
-    for (int n = 0; n < NT; ++n) codes[n][u] = __builtin_nontemporal_load((const u32x4 *)(plane[n] + (size_t)g * 1024));
+    for (int n = 0; n < NT; ++n) codes[n][u] = load_row_group<FMT>(plane[n], high[n], g);
   };
 #pragma unroll
   for (int u = 0; u < P; ++u) issue(u);
 
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4 C[NT][4][MB], S[MB];
+  f32x4 C[NT][4][MB], C2[NT][4][MB], S[MB], S2[MB];
 #pragma unroll
   for (int u = 0; u < GW; ++u) {
     if (u + P < GW) issue(u + P);
     __builtin_amdgcn_sched_barrier(0);
     if ((uint32_t)u < live) {
-      const bool first = u % SG == 0;
+      u32x4 x[MB], lo[NT][4], hi[NT][4];
 #pragma unroll
-      for (int b = 0; b < MB; ++b) S[b] = mfma_bf16(xv[b][u], ones_operand(), first ? zero : S[b]);
+      for (int b = 0; b < MB; ++b) x[b] = xv[b][u];
 #pragma unroll
-      for (int n = 0; n < NT; ++n) {
-        uint32_t r[4] = {codes[n][u][0], codes[n][u][1], codes[n][u][2], codes[n][u][3]};
-        transpose4(r);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const u32x4 w = code_pairs(r[t], cc);
-#pragma unroll
-          for (int b = 0; b < MB; ++b) C[n][t][b] = mfma_bf16(xv[b][u], w, first ? zero : C[n][t][b]);
-        }
-      }
+      for (int n = 0; n < NT; ++n) row_operands<FMT>(codes[n][u], hshift, cc, lo[n], hi[n]);
+      row_group_mfma<FMT, MB, NT>(x, lo, hi, u % SG == 0, C, C2, S, S2);
       if ((u + 1) % SG == 0) {
+        MetaWords m[NT][4];
 #pragma unroll
         for (int n = 0; n < NT; ++n)
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const Coef k = coef<FMT>(mw[n][t][u / UNIT], u);
-            const float zc = fmaf(-128.0f, k.s, k.z);
-#pragma unroll
-            for (int b = 0; b < MB; ++b)
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                acc[n][t][b][i] = fmaf(k.s, C[n][t][b][i], acc[n][t][b][i]);
-                acc[n][t][b][i] = fmaf(zc, S[b][i], acc[n][t][b][i]);
-              }
-          }
+          for (int t = 0; t < 4; ++t) m[n][t] = mw[n][t][u / UNIT];
+        row_group_close<FMT, MB, NT>(m, u, C, C2, S, S2, acc);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -113,17 +247,19 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
 
 // Adds all G groups of NT tensors' plane tiles to acc, as row_slice does, in one continuous stream: chunks of four
 // groups, each chunk's loads (clamped to the last group, so every chunk issues as many) issued SETS - 1 chunks
-// ahead into a ring of SETS register sets. plane[n], meta[n] and xrow[b] point at group 0 for the lane.
+// ahead into a ring of SETS register sets. plane[n], high[n], meta[n] and xrow[b] point at group 0 for the lane.
 template <uint32_t FMT, int MB, int NT, int SETS = 2>
-__device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], const uint8_t *const (&meta)[NT],
-                                           const uint16_t *const (&xrow)[MB], uint32_t G,
-                                           float (&acc)[NT][4][MB][4]) {
+__device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], const uint8_t *const (&high)[NT],
+                                           const uint8_t *const (&meta)[NT], const uint16_t *const (&xrow)[MB],
+                                           uint32_t G, float (&acc)[NT][4][MB][4]) {
   using F = Fmt<FMT>;
   constexpr int SG = F::SG, UNIT = F::UNIT, CH = 4, MU = UNIT < CH ? CH / UNIT : 1;
   static_assert(CH % SG == 0, "a chunk holds whole scale groups");
   const uint32_t last = G - 1, chunks = (G + CH - 1) / CH;
   const CodeConstants cc = make_code_constants();
-  u32x4 xv[SETS][MB][CH], codes[SETS][NT][CH];
+  const uint32_t hshift = row_high_shift<FMT>(threadIdx.x & 63);
+  u32x4 xv[SETS][MB][CH];
+  RowGroup<FMT> codes[SETS][NT][CH];
   MetaWords mw[SETS][NT][4][MU];
   const auto issue = [&](uint32_t c, int set) __attribute__((always_inline)) {
 #pragma unroll
@@ -136,8 +272,7 @@ __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], co
         xv[set][b][u] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
 #pragma unroll
-      for (int n = 0; n < NT; ++n)
-        codes[set][n][u] = __builtin_nontemporal_load((const u32x4 *)(plane[n] + (size_t)g * 1024));
+      for (int n = 0; n < NT; ++n) codes[set][n][u] = load_row_group<FMT>(plane[n], high[n], g);
     }
 #pragma unroll
     for (int m = 0; m < MU; ++m) {
@@ -148,53 +283,39 @@ __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], co
         for (int t = 0; t < 4; ++t) mw[set][n][t][m] = load_meta<FMT>(meta[n] + ((size_t)unit * 64 + 16 * t) * F::META);
     }
   };
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4 C[NT][4][MB], S[MB];
-  // Each group's exact operands (transposed words as bf16 128 + q) are built one group ahead, into the other of
-  // two operand sets, so that building them interleaves with the previous group's MFMAs.
-  u32x4 wop[2][NT][4];
+  f32x4 C[NT][4][MB], C2[NT][4][MB], S[MB], S2[MB];
+  // Each group's exact operands are built one group ahead, into the other of two operand sets, so that building
+  // them interleaves with the previous group's MFMAs; 8-bit codes (two operand sets a group) build them just before
+  // their MFMAs, to fit the registers.
+  constexpr bool kAhead = F::P0 != 32;
+  u32x4 lo[2][NT][4], hi[2][NT][4];
   const auto prepare = [&](int set, int u, int os) __attribute__((always_inline)) {
 #pragma unroll
-    for (int n = 0; n < NT; ++n) {
-      uint32_t r[4] = {codes[set][n][u][0], codes[set][n][u][1], codes[set][n][u][2], codes[set][n][u][3]};
-      transpose4(r);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) wop[os][n][t] = code_pairs(r[t], cc);
-    }
+    for (int n = 0; n < NT; ++n) row_operands<FMT>(codes[set][n][u], hshift, cc, lo[os][n], hi[os][n]);
   };
   const auto compute = [&](uint32_t c, int set, int next_set) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const uint32_t g = c * CH + u;
-      const int os = u & 1;   // CH is even: group g's operands sit in set g % 2
+      const int os = kAhead ? u & 1 : 0;   // CH is even: group g's operands sit in set g % 2
       if (g < G) {
-        const bool first = u % SG == 0;
+        u32x4 x[MB];
 #pragma unroll
-        for (int b = 0; b < MB; ++b) S[b] = mfma_bf16(xv[set][b][u], ones_operand(), first ? zero : S[b]);
-#pragma unroll
-        for (int n = 0; n < NT; ++n)
-#pragma unroll
-          for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int b = 0; b < MB; ++b) C[n][t][b] = mfma_bf16(xv[set][b][u], wop[os][n][t], first ? zero : C[n][t][b]);
+        for (int b = 0; b < MB; ++b) x[b] = xv[set][b][u];
+        if constexpr (!kAhead) prepare(set, u, 0);
+        row_group_mfma<FMT, MB, NT>(x, lo[os], hi[os], u % SG == 0, C, C2, S, S2);
         // The next group's operands (the last group of a chunk takes the next chunk's first).
-        if (u + 1 < CH) prepare(set, u + 1, os ^ 1);
-        else prepare(next_set, 0, os ^ 1);
+        if constexpr (kAhead) {
+          if (u + 1 < CH) prepare(set, u + 1, os ^ 1);
+          else prepare(next_set, 0, os ^ 1);
+        }
         if ((u + 1) % SG == 0) {
+          MetaWords m[NT][4];
 #pragma unroll
           for (int n = 0; n < NT; ++n)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              const Coef k = coef<FMT>(mw[set][n][t][UNIT < CH ? u / UNIT : 0], g);
-              const float zc = fmaf(-128.0f, k.s, k.z);
-#pragma unroll
-              for (int b = 0; b < MB; ++b)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                  acc[n][t][b][i] = fmaf(k.s, C[n][t][b][i], acc[n][t][b][i]);
-                  acc[n][t][b][i] = fmaf(zc, S[b][i], acc[n][t][b][i]);
-                }
-            }
+            for (int t = 0; t < 4; ++t) m[n][t] = mw[set][n][t][UNIT < CH ? u / UNIT : 0];
+          row_group_close<FMT, MB, NT>(m, g, C, C2, S, S2, acc);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -202,7 +323,7 @@ __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], co
   };
 #pragma unroll
   for (int c = 0; c < SETS - 1; ++c) issue(c, c);
-  prepare(0, 0, 0);
+  if constexpr (kAhead) prepare(0, 0, 0);
   for (uint32_t c = 0; c < chunks; c += SETS) {
 #pragma unroll
     for (int k = 0; k < SETS; ++k) {

@@ -212,11 +212,11 @@ NEW_FORMATS = [oracle.FMT_Q5K, oracle.FMT_Q6K, oracle.FMT_Q80, oracle.FMT_AF8G64
 
 
 @pytest.mark.parametrize("fmt", NEW_FORMATS)
-@pytest.mark.parametrize("rows", [1, 2, 4])
+@pytest.mark.parametrize("rows", [1, 2, 4, 5, 16, 17, 32])
 @pytest.mark.parametrize("splits", [1, 4])
 def test_decode_new_formats(fmt, rows, splits):
-    """Q5_K, Q6_K, Q8_0 and af8g64 through the decode column tile (rows <= 4): every output inside its fp64
-    interval, the BASELINE tolerances, and no worse than the reference's staged numerics."""
+    """Q5_K, Q6_K, Q8_0 and af8g64 through the decode column tile (rows <= 4) and row tile (5 to 32 rows): every
+    output inside its fp64 interval, the BASELINE tolerances, and no worse than the reference's staged numerics."""
     rng = np.random.default_rng(2000 * fmt + 10 * rows + splits)
     n, k = 256, 2048
     w = make_weights(rng, fmt, n, k)
@@ -230,31 +230,49 @@ def test_decode_new_formats(fmt, rows, splits):
 
 
 @pytest.mark.parametrize("fmt", NEW_FORMATS)
-def test_decode_new_formats_fixture_and_pairs(fmt):
-    """The reference's fixture weights (every byte random, finite half scales) through the column tile, sparse
-    +-1e5 inputs, and a one-pass gate/up pair bitwise equal to two passes."""
-    rng = np.random.default_rng(77 + fmt)
+@pytest.mark.parametrize("rows", [3, 9])
+def test_decode_new_formats_fixture_and_pairs(fmt, rows):
+    """The reference's fixture weights (every byte random, finite half scales) through the column and row tiles,
+    sparse +-1e5 inputs, and one-pass gate/up pairs (column tile, both row-tile register budgets) bitwise equal to
+    two passes."""
+    rng = np.random.default_rng(77 + fmt + rows)
     n, k = 128, 1024
     native = oracle.fixture(fmt, n, k, 9)
     if fmt == oracle.FMT_AF8G64:
         native = make_weights(rng, fmt, n, k).native
     w = Weights(fmt, n, k, native)
     if np.isfinite(w.values).all() and np.abs(w.values).max() < 1e30:
-        x = sparse_inputs(3, k, 1.0)
-        got = run_plan(staged(n, k, 3, 1), sq.projection(w.segment()), x, n)
-        check_projection(got, x, w, f"fixture fmt {fmt}")
+        x = sparse_inputs(rows, k, 1.0)
+        got = run_plan(staged(n, k, rows, 1), sq.projection(w.segment()), x, n)
+        check_projection(got, x, w, f"fixture fmt {fmt} rows {rows}")
     wg, wu = make_weights(rng, fmt, 256, 2048), make_weights(rng, fmt, 256, 2048)
-    x = dense_inputs(rng, 2, 2048)
     gate, up = sq.projection(wg.segment()), sq.projection(wu.segment())
-    two = run_plan(staged(256, 2048, 2, 2, sq.EPILOGUE_GATE_UP), up, x, 256, gate=gate)
-    one = run_plan(staged(256, 2048, 2, 2, sq.EPILOGUE_GATE_UP, one_pass=1), up, x, 256, gate=gate)
-    assert np.array_equal(one, two)
+    for pair_rows in ([2] if rows < 5 else [rows, 32]):
+        x = dense_inputs(rng, pair_rows, 2048)
+        two = run_plan(staged(256, 2048, pair_rows, 2, sq.EPILOGUE_GATE_UP), up, x, 256, gate=gate)
+        one = run_plan(staged(256, 2048, pair_rows, 2, sq.EPILOGUE_GATE_UP, one_pass=1), up, x, 256, gate=gate)
+        assert np.array_equal(one, two), pair_rows
 
 
 @pytest.mark.parametrize("fmt", NEW_FORMATS)
-def test_new_formats_refused_past_the_column_tile(fmt):
-    """The row tile (more than four rows) does not run these formats yet: refused before any launch."""
+@pytest.mark.parametrize("rows", [8, 24])
+def test_decode_new_formats_longest_slices(fmt, rows):
+    """One K partition of the row tile's longest slices (32 groups a wave: sixteen waves, 512 groups, at up to 16
+    rows, where the K-quants keep fewer groups in flight; eight waves, 256 groups, past 16)."""
+    rng = np.random.default_rng(300 + fmt + rows)
+    n, k = 64, 16384 if rows <= 16 else 8192
+    w = make_weights(rng, fmt, n, k)
+    x = dense_inputs(rng, rows, k)
+    got = run_plan(staged(n, k, rows, 1), sq.projection(w.segment()), x, n)
+    check_projection(got, x, w, f"fmt {fmt} rows {rows} k {k}")
+
+
+@pytest.mark.parametrize("fmt", NEW_FORMATS)
+def test_new_formats_refused_by_the_prefill_tile(fmt):
+    """The prefill tile (more than 32 rows) does not run these formats yet: refused before any launch."""
     rng = np.random.default_rng(5)
     w = make_weights(rng, fmt, 128, 1024)
+    proj = sq.projection(w.segment())
+    plan = sq.plan_for(sq.prefill_workload(128, 1024, 64), proj)
     with pytest.raises(sq.InvalidArgument, match="does not run"):
-        run_plan(staged(128, 1024, 8, 1), sq.projection(w.segment()), dense_inputs(rng, 8, 1024), 128)
+        run_plan(plan, proj, dense_inputs(rng, 64, 1024), 128)

@@ -8,16 +8,10 @@ import pytest
 
 import splash_q4 as sq
 import sq_oracle as oracle
-from helpers import affine_native, to_device, to_host, torch
+from helpers import make_weights, to_device, to_host, torch
 from splash_q4 import synthetic
 
 pytestmark = pytest.mark.gpu
-
-
-def native_rows(rng, fmt, n, k):
-    if fmt == oracle.FMT_Q4K:
-        return synthetic.q4k_native(rng, n, k).ravel()
-    return affine_native(rng, fmt, n, k)
 
 
 class Block:
@@ -37,16 +31,14 @@ class Block:
             plan += [("shared_gate", shared * intermediate, hidden, sf), ("shared_up", shared * intermediate, hidden, sf),
                      ("shared_down", shared * hidden, intermediate, df)]
         for name, n, k, f in plan:
-            p0, meta, values = oracle.repack(f, native_rows(rng, f, n, k), n, k)
-            self.parts[name] = (to_device(p0), to_device(meta), values, n, k, f)
+            self.parts[name] = make_weights(rng, f, n, k)
         self.slots = to_device(np.arange(experts, dtype=np.uint32))
         self.scalar_gate = rng.normal(0, 0.05, hidden).astype(np.float32) if gated else None
 
     def segment(self, name):
         if name not in self.parts:
             return sq.Segment()
-        p0, meta, _, n, k, f = self.parts[name]
-        return sq.segment(f, n, k, p0, meta)
+        return self.parts[name].segment()
 
     def weights(self):
         self._gate = to_device(self.scalar_gate) if self.gated else None
@@ -63,7 +55,7 @@ class Block:
         """Expert `expert`'s rows of projection `name`; ids from the expert count on are the shared slices."""
         if expert >= self.e:
             name, expert = "shared_" + name, expert - self.e
-        v = self.parts[name][2]
+        v = self.parts[name].values
         rows = self.i if name.endswith("gate") or name.endswith("up") else self.h
         return v[expert * rows:(expert + 1) * rows]
 
@@ -151,13 +143,26 @@ def check_block(block, x, scores, top_k, residual, phase="prefill", weight_rtol=
     return sel_gpu
 
 
-@pytest.mark.parametrize("fmt", [oracle.FMT_Q4K, oracle.FMT_AF4G32])
-def test_moe_routed_formats(fmt):
-    rng = np.random.default_rng(900 + fmt)
+@pytest.mark.parametrize("fmt", [oracle.FMT_Q4K, oracle.FMT_AF4G32, oracle.FMT_Q5K, oracle.FMT_Q6K, oracle.FMT_Q80,
+                                 oracle.FMT_AF8G64])
+@pytest.mark.parametrize("rows", [40, 6])
+def test_moe_routed_formats(fmt, rows):
+    """Every format through both expert-pass register budgets (tiles of 32 and of 16 rows)."""
+    rng = np.random.default_rng(900 + fmt + rows)
     block = Block(rng, 16, 512, 256, fmt=fmt)
-    x = synthetic.activations(rng, 40, 512)
-    scores = synthetic.router_logits(rng, 40, 16)
-    check_block(block, x, scores, 4, None)
+    x = synthetic.activations(rng, rows, 512)
+    scores = synthetic.router_logits(rng, rows, 16)
+    check_block(block, x, scores, 4, None, "prefill" if rows > 32 else "decode")
+
+
+def test_moe_k_quant_experts_with_q8_0_shared_slice():
+    """The mix the 4-bit MoE checkpoints ship: Q5_K routed experts with a gated Q8_0 shared slice (its own launches)."""
+    rng = np.random.default_rng(950)
+    block = Block(rng, 16, 512, 256, fmt=oracle.FMT_Q5K, shared=1, gated=True, shared_fmt=oracle.FMT_Q80)
+    x = synthetic.activations(rng, 48, 512)
+    scores = synthetic.router_logits(rng, 48, 16)
+    residual = synthetic.bf16_bits(rng.uniform(-2, 2, (48, 512)).astype(np.float32))
+    check_block(block, x, scores, 4, residual)
 
 
 @pytest.mark.parametrize("rows,phase", [(48, "prefill"), (5, "decode")])
