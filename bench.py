@@ -62,6 +62,12 @@ def gemv_bytes(m: int, n: int, k: int) -> float:
     return n * k * 0.5625 + 2 * m * k + 2 * m * n
 
 
+def weight_bytes(sq, fmt: int, n: int, k: int) -> int:
+    """Plane bytes of an n x k tensor: plane0, meta and plane1 (the format's native bits per weight)."""
+    p0, meta = sq.plane_bytes(fmt, n, k)
+    return p0 + meta + n * (k // 32) * sq.FORMATS[fmt][5]
+
+
 class Projection:
     """An n x k weight tensor in `copies` ring slots on the device, prepared through the library's repack."""
 
@@ -69,19 +75,26 @@ class Projection:
         rng = np.random.default_rng(seed)
         self.fmt, self.n, self.k = fmt, n, k
         p0_bytes, meta_bytes = sq.plane_bytes(fmt, n, k)
+        p1_bytes = n * (k // 32) * sq.FORMATS[fmt][5]
         self.plane0 = [torch.empty(p0_bytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
         self.meta = [torch.empty(meta_bytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
-        if fmt == sq.FMT_Q4K:
-            native = synthetic.q4k_native(rng, n, k)
+        self.plane1 = [torch.empty(p1_bytes, dtype=torch.uint8, device="cuda") if p1_bytes else None
+                       for _ in range(copies)]
+        if fmt in (sq.FMT_Q4K, sq.FMT_Q5K, sq.FMT_Q6K, sq.FMT_Q80):
+            native = synthetic.q4k_native(rng, n, k) if fmt == sq.FMT_Q4K else synthetic.gguf_native(rng, fmt, n, k)
             src = torch.from_numpy(native.reshape(-1)).cuda()
-            dst = torch.empty(p0_bytes + meta_bytes, dtype=torch.uint8, device="cuda")
-            sq.gguf_repack(src, dst, n, k, fmt, native.shape[1], p0_bytes)
+            dst = torch.empty(p0_bytes + meta_bytes + p1_bytes, dtype=torch.uint8, device="cuda")
+            sq.gguf_repack(src, dst, n, k, fmt, native.shape[1], p0_bytes, dst_plane1=p0_bytes + meta_bytes)
             for c in range(copies):
                 self.plane0[c].copy_(dst[:p0_bytes])
-                self.meta[c].copy_(dst[p0_bytes:])
+                self.meta[c].copy_(dst[p0_bytes:p0_bytes + meta_bytes])
+                if p1_bytes:
+                    self.plane1[c].copy_(dst[p0_bytes + meta_bytes:])
+            del src, dst
         else:
-            group = {sq.FMT_AF4G32: 32, sq.FMT_AF4G64: 64, sq.FMT_AF4G128: 128}[fmt]
-            _, weight, scales, biases = synthetic.mlx_affine(rng, n, k, group)
+            group, bits = {sq.FMT_AF4G32: (32, 4), sq.FMT_AF4G64: (64, 4), sq.FMT_AF4G128: (128, 4),
+                           sq.FMT_AF8G64: (64, 8)}[fmt]
+            _, weight, scales, biases = synthetic.mlx_affine(rng, n, k, group, bits=bits)
             w = torch.from_numpy(weight.view(np.int32)).cuda()
             s = torch.from_numpy(scales.view(np.int16)).cuda()
             b = torch.from_numpy(biases.view(np.int16)).cuda()
@@ -90,10 +103,11 @@ class Projection:
         torch.cuda.synchronize()
 
     def projection(self, sq, copy: int = 0):
-        return sq.projection(sq.segment(self.fmt, self.n, self.k, self.plane0[copy], self.meta[copy]))
+        return sq.projection(sq.segment(self.fmt, self.n, self.k, self.plane0[copy], self.meta[copy],
+                                        plane1=self.plane1[copy]))
 
     def bytes(self) -> int:
-        return self.plane0[0].numel() + self.meta[0].numel()
+        return self.plane0[0].numel() + self.meta[0].numel() + (self.plane1[0].numel() if self.plane1[0] is not None else 0)
 
 
 def time_steps(torch, fn, steps: int, warmup: int) -> float:
@@ -159,7 +173,7 @@ class Gemv:
     """A decode projection over a weight ring; launch(i, stream) dispatches step i on ring copy i % copies."""
 
     def __init__(self, torch, sq, synthetic, fmt, m, n, k, seed=1):
-        one = int(gemv_bytes(0, n, k))
+        one = weight_bytes(sq, fmt, n, k)
         self.copies = max(1, -(-RING_BYTES // one))
         self.weights = Projection(torch, sq, synthetic, fmt, n, k, seed, self.copies)
         self.projs = [self.weights.projection(sq, c) for c in range(self.copies)]
@@ -232,8 +246,8 @@ def bench_moe(torch, sq, synthetic, steps, warmup, rows=512, experts=128, top_k=
         sq.call("sq_moe_add", handle, sq.byref(buffers), sq.byref(weights), sq.byref(plan))
 
     sec = time_steps(torch, step, steps, warmup)
-    weight_bytes = sum(p.bytes() for p in parts.values())
-    return sec, weight_bytes + 2 * rows * hidden * 2, 2 * rows * top_k * 3 * inter * hidden
+    planes = sum(p.bytes() for p in parts.values())
+    return sec, planes + 2 * rows * hidden * 2, 2 * rows * top_k * 3 * inter * hidden
 
 
 def cpu_baseline(sq, synthetic, m, n, k, budget_s: float):
@@ -336,6 +350,18 @@ def main() -> int:
         q4k["M512_K5120xN27648"] = {"us": round(s * 1e6, 1), "TFLOPS": round(tf, 1), "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 3)}
         log(f"  q4k M512: {s * 1e6:.0f} us, {tf:.0f} TFLOPS")
         extra["c3_q4k"] = q4k
+        # The adjacent formats on the BASELINE config-1 shape, in GB/s of their own plane bytes plus activations
+        # and outputs.
+        formats = {}
+        for fmt, name in ((sq.FMT_Q5K, "q5_k"), (sq.FMT_Q6K, "q6_k"), (sq.FMT_Q80, "q8_0"), (sq.FMT_AF8G64, "af8g64")):
+            for mm in (1, 16):
+                s, p = bench_gemv(torch, sq, synthetic, fmt, mm, 14336, 4096, max(50, args.steps // 2), 10)
+                g = (weight_bytes(sq, fmt, 14336, 4096) + 2 * mm * (4096 + 14336)) / s / 1e9
+                formats[f"{name}_M{mm}_K4096xN14336"] = {"us": round(s * 1e6, 2), "GB/s": round(g, 1),
+                                                          "hbm_frac": round(g / HBM_PEAK_GBS, 3),
+                                                          "splits": p.config.splits}
+                log(f"  {name} M{mm}: {s * 1e6:.2f} us, {g:.0f} GB/s")
+        extra["c5_formats_decode"] = formats
         s, moe_bytes, moe_flops = bench_moe(torch, sq, synthetic, 50, 5)
         g = moe_bytes / s / 1e9
         extra["c4_moe_af4g64"] = {"us": round(s * 1e6, 1), "GB/s": round(g, 1), "hbm_frac": round(g / HBM_PEAK_GBS, 3),

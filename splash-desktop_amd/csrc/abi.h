@@ -54,11 +54,6 @@ SQ_HD inline bool sq_format_supported(uint32_t f) {
   return f == SQ_FMT_Q4K || f == SQ_FMT_Q5K || f == SQ_FMT_Q6K || f == SQ_FMT_Q80 || f == SQ_FMT_AF4G32 ||
          f == SQ_FMT_AF4G64 || f == SQ_FMT_AF4G128 || f == SQ_FMT_AF8G64;
 }
-// The formats the decode, prefill and MoE tiles run (the load-time repack and the dequantisation take every
-// supported one).
-SQ_HD inline bool sq_tile_format(uint32_t f) {
-  return f == SQ_FMT_Q4K || f == SQ_FMT_AF4G32 || f == SQ_FMT_AF4G64 || f == SQ_FMT_AF4G128;
-}
 SQ_HD inline SqQuantFormat sq_format(uint32_t f) {
   switch (f) {
     case SQ_FMT_Q4K: return {12u, 256u, 144u, 16u, 0u, 16u, 8u};

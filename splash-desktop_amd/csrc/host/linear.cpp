@@ -320,17 +320,17 @@ PreparedInput Linear::add(hipStream_t graph, LinearBuffers b, const Projection &
   if (selected.destination() == FloatOutput::Float32 && segments.size() > 1)
     throw std::invalid_argument("an fp32 destination takes a single-tensor block projection");
   const LinearConfig config = selected.configuration();
-  // The decode tiles (the column tile to four rows, the row tile past it) run every format; the prefill tile the
-  // 4-bit ones.
+  // Each tile states the formats it runs (the decode column tile to four rows, the row tile past it, the prefill
+  // tile).
   const bool staged = config.tile == LinearTile::GgufStaged;
   const bool column = staged && w.rows <= kern::kColumnTileRows;
   for (const Projection *q : {&p, gate})
     if (q)
       for (const QuantizedSegment &s : q->blocks().segments)
         if (!(column ? kern::column_tile_format(s.formatId)
-                     : staged ? kern::row_tile_format(s.formatId) : sq_tile_format(s.formatId)))
+                     : staged ? kern::row_tile_format(s.formatId) : kern::prefill_tile_format(s.formatId)))
           throw std::invalid_argument(std::string(staged ? "the decode tile" : "the prefill tile") + " does not run " +
-                                      s.name() + " weights" + (staged ? "" : " (decode rows of at most 32 do)"));
+                                      s.name() + " weights");
   const uint32_t groupUnit = planScaleGroups(&p, gate);
   if (config.tile == LinearTile::GgufStaged) {
     if ((k / 32) % (config.splits * groupUnit))

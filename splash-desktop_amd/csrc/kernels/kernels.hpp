@@ -30,10 +30,11 @@ struct Segment {
 //  - The row tile (more rows): grid (64-column tiles, splits) of up to 16 waves (fewer for more than 16 rows or a
 //    gate/up pair), rows on the MFMA's 16-row side.
 constexpr uint32_t kColumnTileRows = 4;
-// The formats each tile runs: the decode column and row tiles and the MoE expert passes every format this build
-// takes; the prefill tile the 4-bit ones (sq_tile_format).
+// The formats each tile runs: the decode column and row tiles, the prefill tile and the MoE expert passes, every
+// format this build takes.
 SQ_HD inline bool column_tile_format(uint32_t f) { return sq_format_supported(f); }
 SQ_HD inline bool row_tile_format(uint32_t f) { return sq_format_supported(f); }
+SQ_HD inline bool prefill_tile_format(uint32_t f) { return sq_format_supported(f); }
 // The column tile's most waves (K slices) per workgroup, and the most groups of 32 inputs one wave streams.
 constexpr uint32_t kColumnMaxWaves = 16, kColumnMaxGroups = 32;
 struct DecodeArgs {

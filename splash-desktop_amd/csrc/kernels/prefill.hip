@@ -35,11 +35,23 @@ namespace {
 
 constexpr int BK = 64, kWaves = 4, kThreads = 64 * kWaves, kStages = 3, kSlots = 4;
 constexpr int kRowBytes = BK * 2;                  // one LDS activation row: 64 fp16
-constexpr int kWaveSlotBytes = 2048 + 1024;        // a wave's codes of one step (2 groups x 64 columns x 16 B) + meta
-constexpr int kSlotBytes = kWaves * kWaveSlotBytes;
+constexpr int kLdsLimit = 160 * 1024;              // LDS a workgroup may hold
+// A wave's LDS slot for one step of its plane tile: the step's two groups of codes (64 columns x P0 bytes each), their
+// plane1 bits (64 x P1 each), then the meta the step reads (its meta unit, or both groups' units of a format with a
+// unit a group). Each part lies in the planes as in the slot, so it arrives by whole 16-byte or dword copies. The
+// 4-bit formats without plane1 keep 1 KiB for the meta.
+template <uint32_t FMT>
+struct StepSlot {
+  using F = Fmt<FMT>;
+  static constexpr int code = 2 * 64 * F::P0, high = 2 * 64 * F::P1;
+  static constexpr int meta = (F::UNIT == 1 ? 2 : 1) * 64 * F::META;
+  static constexpr int high_at = code, meta_at = code + high;
+  static constexpr int wave = meta_at + (F::P0 == 16 && F::P1 == 0 ? 1024 : (meta + 15) / 16 * 16);
+  static constexpr int all = kWaves * wave;       // the slot of every wave
+};
 template <int BM> constexpr int stage_bytes() { return BM * kRowBytes; }
 template <int BM> constexpr int code_base() { return kStages * stage_bytes<BM>(); }
-template <int BM> constexpr int lds_bytes() { return code_base<BM>() + kSlots * kSlotBytes; }
+template <uint32_t FMT, int BM> constexpr int lds_bytes() { return code_base<BM>() + kSlots * StepSlot<FMT>::all; }
 
 // global -> LDS copy of SIZE bytes per lane (global_load_lds): lane l's bytes land at lds + SIZE l.
 // (The size is spelled as a literal: the host pass of hipcc does not take a template argument there.)
@@ -135,35 +147,64 @@ __device__ __forceinline__ uint32_t column_of(uint32_t j, int t) {
 }
 
 // The meta of column c for group h of one step out of the wave's LDS slot: af4g32 the words of its two groups,
-// af4g64 and af4g128 the one word covering the step, Q4_K the fp32 (s, z) of group h that q4k_coefficients left
-// in place of the column's header.
+// af4g64, af4g128 and af8g64 the one word covering the step, Q8_0 the group's half d, Q4_K and Q5_K the fp32 (s, z)
+// and Q6_K the fp32 scales of its two halves that step_coefficients left in place of the column's meta.
 template <uint32_t FMT>
 __device__ __forceinline__ MetaWords slot_meta(const uint8_t *meta, uint32_t c, int h) {
-  if constexpr (FMT == SQ_FMT_Q4K) {
+  if constexpr (FMT == SQ_FMT_Q4K || FMT == SQ_FMT_Q5K) {
     const u32x2 v = *(const u32x2 *)(meta + c * 16 + h * 8);
-    return MetaWords{{v[0], v[1], 0u, 0u}};
+    return MetaWords{{v[0], v[1], 0u, 0u, 0u}};
+  } else if constexpr (FMT == SQ_FMT_Q6K) {
+    const uint32_t *w = (const uint32_t *)(meta + c * 20 + h * 8);   // 4-byte aligned
+    return MetaWords{{w[0], w[1], 0u, 0u, 0u}};
+  } else if constexpr (FMT == SQ_FMT_Q80) {
+    return MetaWords{{*(const uint16_t *)(meta + h * 128 + c * 2), 0u, 0u, 0u, 0u}};
   } else if constexpr (FMT == SQ_FMT_AF4G32) {
-    return MetaWords{{*(const uint32_t *)(meta + c * 4), *(const uint32_t *)(meta + 256 + c * 4), 0u, 0u}};
+    return MetaWords{{*(const uint32_t *)(meta + c * 4), *(const uint32_t *)(meta + 256 + c * 4), 0u, 0u, 0u}};
   } else {
-    return MetaWords{{*(const uint32_t *)(meta + c * 4), 0u, 0u, 0u}};
+    return MetaWords{{*(const uint32_t *)(meta + c * 4), 0u, 0u, 0u, 0u}};
   }
 }
-// The coefficients of group h (0, 1) of the step, the step's group `group` of the tile.
+// The coefficients of group h (0, 1) of the step, the step's group `group` of the tile, for the first and second
+// half of its elements (the same unless the format scales halves, Q6_K). value = fma(q, s, z) with Q6_K's
+// s (q - 32) as fma(q, s, -32 s) and Q8_0's d v as fma(v + 128, d, -128 d): both exact, the same values.
 template <uint32_t FMT>
-__device__ __forceinline__ Coef group_coef(const MetaWords &m, uint32_t group, int h) {
-  if constexpr (FMT == SQ_FMT_Q4K) return Coef{__uint_as_float(m.w[0]), __uint_as_float(m.w[1])};
-  else if constexpr (FMT == SQ_FMT_AF4G32) return coef<FMT>(MetaWords{{m.w[h], 0u, 0u, 0u}}, group);
-  else return coef<FMT>(m, group);
+__device__ __forceinline__ void group_coef(const MetaWords &m, uint32_t group, int h, Coef &first, Coef &second) {
+  if constexpr (FMT == SQ_FMT_Q4K || FMT == SQ_FMT_Q5K) {
+    first = Coef{__uint_as_float(m.w[0]), __uint_as_float(m.w[1])};
+  } else if constexpr (FMT == SQ_FMT_Q6K) {
+    const float s0 = __uint_as_float(m.w[0]), s1 = __uint_as_float(m.w[1]);
+    first = Coef{s0, -32.0f * s0};
+    second = Coef{s1, -32.0f * s1};
+  } else if constexpr (FMT == SQ_FMT_Q80) {
+    const float d = f16_to_f32(m.w[0]);
+    first = Coef{d, -128.0f * d};
+  } else if constexpr (FMT == SQ_FMT_AF4G32) {
+    first = coef<FMT>(MetaWords{{m.w[h], 0u, 0u, 0u, 0u}}, group);
+  } else {
+    first = coef<FMT>(m, group);
+  }
+  if constexpr (!Fmt<FMT>::HALVES) second = first;
 }
-// Q4_K: lane l turns column l's 16-byte header in the slot into the fp32 (s, z) of the step's two groups, in place,
-// so each lane derives one column's coefficients instead of four (the wave's reads precede its writes).
+// Q4_K and Q5_K: lane l turns column l's 16-byte header in the slot into the fp32 (s, z) of the step's two groups,
+// Q6_K its 20 bytes into the fp32 scales of the two groups' halves, in place, so each lane derives one column's
+// coefficients instead of four (the wave's reads precede its writes).
 template <uint32_t FMT>
-__device__ __forceinline__ void q4k_coefficients(uint8_t *meta, uint32_t step, int lane) {
-  if constexpr (FMT == SQ_FMT_Q4K) {
+__device__ __forceinline__ void step_coefficients(uint8_t *meta, uint32_t step, int lane) {
+  if constexpr (FMT == SQ_FMT_Q4K || FMT == SQ_FMT_Q5K) {
     const u32x4 v = *(const u32x4 *)(meta + lane * 16);
-    const MetaWords m{{v[0], v[1], v[2], v[3]}};
+    const MetaWords m{{v[0], v[1], v[2], v[3], 0u}};
     const Coef c0 = coef<FMT>(m, 2 * step), c1 = coef<FMT>(m, 2 * step + 1);
     *(f32x4 *)(meta + lane * 16) = f32x4{c0.s, c0.z, c1.s, c1.z};
+  } else if constexpr (FMT == SQ_FMT_Q6K) {
+    uint32_t *w = (uint32_t *)(meta + lane * 20);   // 4-byte aligned
+    const MetaWords m{{w[0], w[1], w[2], w[3], w[4]}};
+    const float a = q6k_scale(m, 2 * step, 0), b = q6k_scale(m, 2 * step, 1);
+    const float c = q6k_scale(m, 2 * step + 1, 0), d = q6k_scale(m, 2 * step + 1, 1);
+    w[0] = __float_as_uint(a);
+    w[1] = __float_as_uint(b);
+    w[2] = __float_as_uint(c);
+    w[3] = __float_as_uint(d);
   }
 }
 
@@ -194,13 +235,19 @@ static_assert(kMicroTable.op[kMicro - 1].kind == 3 && kMicroTable.op[kMicro - 1]
 template <uint32_t FMT, uint32_t EP, int BM>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_kernel(PrefillArgs a) {
   using F = Fmt<FMT>;
+  using S = StepSlot<FMT>;
   constexpr int MI = BM / 16;                         // 16-row blocks of the wave
   static_assert(MI == 8 || MI == 16, "128- or 256-row tiles");
-  constexpr int kStage = stage_bytes<BM>(), kCodeBase = code_base<BM>();
-  constexpr int kMetaCopies = FMT == SQ_FMT_AF4G32 ? 2 : 1;
-  constexpr int kCopies = BM / 32 + 2 + kMetaCopies;  // copy instructions a wave issues per step
+  constexpr int kStage = stage_bytes<BM>(), kCodeBase = code_base<BM>(), kSlotBytes = S::all;
+  // The step's plane copies: the codes, plane1 and meta parts by 16-byte copies of 1 KiB and dword copies of 256 B.
+  constexpr int kCode16 = S::code / 1024, kHigh16 = S::high / 1024, kHigh4 = S::high % 1024 / 256;
+  constexpr int kMeta16 = S::meta / 1024, kMeta4 = S::meta % 1024 / 256;
+  static_assert(S::high % 256 == 0 && S::meta % 256 == 0, "whole dword copies");
+  constexpr int kBCopies = kCode16 + kHigh16 + kHigh4 + kMeta16 + kMeta4;
+  constexpr int kCopies = BM / 32 + kBCopies;        // copy instructions a wave issues per step
   static_assert(kCopies < 64, "vmcnt counts to 63");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes<BM>()];
+  static_assert(lds_bytes<FMT, BM>() <= kLdsLimit, "the tile's LDS fits a workgroup");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes<FMT, BM>()];
   const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, q = lane >> 4;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t row0 = blockIdx.x * BM;
@@ -212,9 +259,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   while (s + 1 < a.segments && ptile >= a.seg[s].tiles) ptile -= a.seg[s++].tiles;
   const bool live = ptile < a.seg[s].tiles;
   const Segment seg = a.seg[s];
-  const uint8_t *bplane = seg.plane0 + ((size_t)(live ? ptile : 0) * G * 64 + lane) * 16;
-  const uint8_t *bmeta = seg.meta + (size_t)(live ? ptile : 0) * units * 64 * F::META + lane * F::META;
-  uint8_t *const wave_slot = lds + kCodeBase + wave * kWaveSlotBytes;
+  // The lane's copy sources in the plane tile: 16-byte copies read 16 lane bytes on, dword copies 4 lane.
+  const size_t tile = live ? ptile : 0;
+  const uint8_t *bplane = seg.plane0 + (tile * G * 64 * F::P0 + 16 * lane);
+  const uint8_t *bhigh16 = F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + 16 * lane) : nullptr;
+  const uint8_t *bhigh4 = F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + 4 * lane) : nullptr;
+  const uint8_t *bmeta16 = seg.meta + (tile * units * 64 * F::META + 16 * lane);
+  const uint8_t *bmeta4 = seg.meta + (tile * units * 64 * F::META + 4 * lane);
+  uint8_t *const wave_slot = lds + kCodeBase + wave * S::wave;
   uint32_t mask = 0x0F0F0F0Fu;
   asm volatile("" : "+s"(mask));
 
@@ -236,22 +288,34 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     for (int i = 0; i < BM / 32; ++i)
       copy_to_lds<16>(from + aoff[i], lds + stage * kStage + (kRowsPerWave * wave + 8 * i) * kRowBytes);
   };
-  // Step `step`'s codes (two 1 KiB groups) and meta into slot `slot` of this wave.
-  const auto copy_b = [&](uint32_t step, uint32_t slot) __attribute__((always_inline)) {
-    const uint32_t from = min(step, steps - 1);
-    uint8_t *dst = wave_slot + slot * kSlotBytes;
-    copy_to_lds<16>(bplane + (size_t)(2 * from) * 1024, dst);
-    copy_to_lds<16>(bplane + (size_t)(2 * from + 1) * 1024, dst + 1024);
-    if constexpr (FMT == SQ_FMT_AF4G32) {
-      copy_to_lds<4>(bmeta + (size_t)(2 * from) * 256, dst + 2048);
-      copy_to_lds<4>(bmeta + (size_t)(2 * from + 1) * 256, dst + 2048 + 256);
+  // Plane copy k of step `from` (clamped) into the wave's slot at dst: the codes' 1 KiB pieces, then plane1's and the
+  // meta's 1 KiB and 256-byte pieces.
+  const auto copy_b_one = [&](uint32_t from, int k, uint8_t *dst) __attribute__((always_inline)) {
+    const size_t meta = (size_t)(F::UNIT == 1 ? 2 * from : 2 * from / F::UNIT) * 64 * F::META;
+    if (k < kCode16) {
+      copy_to_lds<16>(bplane + (size_t)from * S::code + 1024 * k, dst + 1024 * k);
+    } else if (k < kCode16 + kHigh16) {
+      const int i = k - kCode16;
+      copy_to_lds<16>(bhigh16 + (size_t)from * S::high + 1024 * i, dst + S::high_at + 1024 * i);
+    } else if (k < kCode16 + kHigh16 + kHigh4) {
+      const int i = k - kCode16 - kHigh16;
+      copy_to_lds<4>(bhigh4 + (size_t)from * S::high + 1024 * kHigh16 + 256 * i,
+                     dst + S::high_at + 1024 * kHigh16 + 256 * i);
+    } else if (k < kCode16 + kHigh16 + kHigh4 + kMeta16) {
+      const int i = k - kCode16 - kHigh16 - kHigh4;
+      copy_to_lds<16>(bmeta16 + meta + 1024 * i, dst + S::meta_at + 1024 * i);
     } else {
-      copy_to_lds<F::META>(bmeta + (size_t)(2 * from / F::UNIT) * 64 * F::META, dst + 2048);
+      const int i = k - kCode16 - kHigh16 - kHigh4 - kMeta16;
+      copy_to_lds<4>(bmeta4 + meta + 1024 * kMeta16 + 256 * i, dst + S::meta_at + 1024 * kMeta16 + 256 * i);
     }
   };
+  // Step `step`'s codes, plane1 and meta into slot `slot` of this wave.
+  const auto copy_b = [&](uint32_t step, uint32_t slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < kBCopies; ++k) copy_b_one(min(step, steps - 1), k, wave_slot + slot * kSlotBytes);
+  };
 
-  // Copy c of step `step`'s copies: c < BM / 32 the activation rows of step + 2, then step + 3's two code groups
-  // and its meta.
+  // Copy c of step `step`'s copies: c < BM / 32 the activation rows of step + 2, then step + 3's plane copies.
   const auto copy_one = [&](uint32_t step, int c) __attribute__((always_inline)) {
     if (c < BM / 32) {
       const uint8_t *from = (const uint8_t *)a.half_input + (size_t)min(step + 2, steps - 1) * BK * 2;
@@ -259,13 +323,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       copy_to_lds<16>(from + aoff[c], stage + (kRowsPerWave * wave + 8 * c) * kRowBytes);
       return;
     }
-    const uint32_t from = min(step + 3, steps - 1), k = c - BM / 32;
-    uint8_t *dst = wave_slot + ((step + 3) % kSlots) * kSlotBytes;
-    if (k < 2) copy_to_lds<16>(bplane + (size_t)(2 * from + k) * 1024, dst + k * 1024);
-    else if constexpr (FMT == SQ_FMT_AF4G32)
-      copy_to_lds<4>(bmeta + (size_t)(2 * from + k - 2) * 256, dst + 2048 + (k - 2) * 256);
-    else
-      copy_to_lds<F::META>(bmeta + (size_t)(2 * from / F::UNIT) * 64 * F::META, dst + 2048);
+    copy_b_one(min(step + 3, steps - 1), c - BM / 32, wave_slot + ((step + 3) % kSlots) * kSlotBytes);
   };
 
   f32x4 acc[MI][4];
@@ -278,41 +336,77 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   // next step's group 0 is dequantised into wq[0]; each register set has one role, so the step loop needs no
   // unrolling.
   u32x4 wq[2][4];
-  // The plane words and meta of group h of a step for the lane's four columns, out of the step's slot.
-  uint32_t cw[2][4];
+  // The plane words (8-bit codes: two words, cw and cw1), plane1 bits and meta of group h of a step for the lane's
+  // four columns, out of the step's slot: chunk q of the column (its codes of inputs 4q..4q+3 and 16+4q..19+4q).
+  uint32_t cw[2][4], cw1[2][4], hb[2][4];
   MetaWords mw[2][4];
   const auto read_b = [&](uint32_t slot, int h) __attribute__((always_inline)) {
     const uint8_t *src = wave_slot + slot * kSlotBytes;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const uint32_t c = column_of(j, t);
-      cw[h][t] = *(const uint32_t *)(src + h * 1024 + c * 16 + q * 4);
-      mw[h][t] = slot_meta<FMT>(src + 2048, c, h);
+      if constexpr (F::P0 == 32) {
+        const u32x2 v = *(const u32x2 *)(src + h * 2048 + c * 32 + q * 8);
+        cw[h][t] = v[0];
+        cw1[h][t] = v[1];
+      } else {
+        cw[h][t] = *(const uint32_t *)(src + h * 1024 + c * 16 + q * 4);
+      }
+      if constexpr (F::P1 == 4) hb[h][t] = src[S::high_at + h * 256 + c * 4 + q];
+      if constexpr (F::P1 == 8) hb[h][t] = *(const uint16_t *)(src + S::high_at + h * 512 + c * 8 + 2 * q);
+      mw[h][t] = slot_meta<FMT>(src + S::meta_at, c, h);
     }
   };
   // The dequantisation of one group's four words runs as 52 micro-operations (see micro_op) spread one or two
   // after each MFMA: prep(t) masks word t and derives its coefficients, then every pair of weights p (word p / 4,
   // fragment register p % 4) is converted (C), multiplied and added (F) and packed to fp16 (P), software
   // pipelined so that no micro-operation waits on the one just before it.
+  // 4-bit codes: lo holds the word's slots 0, 4, 1, 5 and hi its slots 2, 6, 3, 7, one a byte, so pair r (slots 2r,
+  // 2r + 1) is bytes r / 2 and r / 2 + 2 of hi (r odd) or lo; plane1 bits go to bits 4 (and 5) of those bytes.
+  // 8-bit codes: lo and hi are the two words, pair r bytes 2 (r % 2) and 2 (r % 2) + 1 of word r / 2.
   uint32_t lo[4], hi[4];
-  Coef kw[4];
+  Coef kw[4], kw2[4];
   float cf[4][2], vf[4][2];
   const auto micro = [&](int u, uint32_t step, int h) __attribute__((always_inline)) {
     const Micro m = kMicroTable.op[u];
     if (m.kind == 0) {
       const int t = m.arg;
-      lo[t] = cw[h][t] & mask;
-      hi[t] = (cw[h][t] >> 4) & mask;
-      kw[t] = group_coef<FMT>(mw[h][t], 2 * step + h, h);
+      if constexpr (F::P0 == 32) {
+        const uint32_t flip = FMT == SQ_FMT_Q80 ? 0x80808080u : 0u;   // the signed byte v as v + 128
+        lo[t] = cw[h][t] ^ flip;
+        hi[t] = cw1[h][t] ^ flip;
+      } else {
+        lo[t] = cw[h][t] & mask;
+        hi[t] = (cw[h][t] >> 4) & mask;
+        if constexpr (F::P1 == 4) {
+          // Fifth bits (bit i of the byte: slot i): the product (24-bit operands, one v_mul_u32_u24) puts bits 0, 4,
+          // 1, 5 at 4, 12, 20, 28, and carries between its partial products stay clear of those.
+          lo[t] |= ((hb[h][t] & 0x33u) * 0x880110u) & 0x10101010u;
+          hi[t] |= (((hb[h][t] >> 2) & 0x33u) * 0x880110u) & 0x10101010u;
+        } else if constexpr (F::P1 == 8) {
+          // High two bits (bits 2i, 2i + 1: slot i).
+          lo[t] |= ((hb[h][t] & 0x0303u) << 4) | ((hb[h][t] & 0x0C0Cu) << 18);
+          hi[t] |= (hb[h][t] & 0x3030u) | ((hb[h][t] & 0xC0C0u) << 14);
+        }
+      }
+      group_coef<FMT>(mw[h][t], 2 * step + h, h, kw[t], kw2[t]);
     } else {
       const int p = m.arg, t = p >> 2, r = p & 3, slot = p & 3;
       if (m.kind == 1) {
-        const uint32_t src = (r & 1) ? hi[t] : lo[t];
-        cf[slot][0] = byte_float(src, r >> 1);
-        cf[slot][1] = byte_float(src, (r >> 1) + 2);
+        if constexpr (F::P0 == 32) {
+          const uint32_t src = (r >> 1) ? hi[t] : lo[t];
+          cf[slot][0] = byte_float(src, 2 * (r & 1));
+          cf[slot][1] = byte_float(src, 2 * (r & 1) + 1);
+        } else {
+          const uint32_t src = (r & 1) ? hi[t] : lo[t];
+          cf[slot][0] = byte_float(src, r >> 1);
+          cf[slot][1] = byte_float(src, (r >> 1) + 2);
+        }
       } else if (m.kind == 2) {
-        vf[slot][0] = fmaf(cf[slot][0], kw[t].s, kw[t].z);
-        vf[slot][1] = fmaf(cf[slot][1], kw[t].s, kw[t].z);
+        // Pairs 0, 1 are the chunk's first-half elements, 2, 3 its second half.
+        const Coef k = F::HALVES && r >= 2 ? kw2[t] : kw[t];
+        vf[slot][0] = fmaf(cf[slot][0], k.s, k.z);
+        vf[slot][1] = fmaf(cf[slot][1], k.s, k.z);
       } else {
         // fp32 by the fma, then fp16: the empty asm keeps the two roundings apart (no fused mixed-precision fma).
         asm volatile("" : "+v"(vf[slot][0]), "+v"(vf[slot][1]));
@@ -333,7 +427,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   copy_a(1, 1);
   __builtin_amdgcn_s_waitcnt(wait_vm(0));
   lds_barrier();
-  q4k_coefficients<FMT>(wave_slot + 2048, 0, lane);
+  step_coefficients<FMT>(wave_slot + S::meta_at, 0, lane);
   read_b(0, 0);
   read_b(0, 1);
   dequant_group(0, 0);
@@ -387,7 +481,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       __builtin_amdgcn_s_waitcnt(kWaitLds);
       if (b + 1 < kBatches) read_batch(step, b + 1);
       if (b == 0) {
-        q4k_coefficients<FMT>(wave_slot + ((step + 1) % kSlots) * kSlotBytes + 2048, step + 1, lane);
+        step_coefficients<FMT>(wave_slot + ((step + 1) % kSlots) * kSlotBytes + S::meta_at, step + 1, lane);
         read_b((step + 1) % kSlots, 0);
       }
       if (b == kBatches / 2) read_b((step + 1) % kSlots, 1);
@@ -446,8 +540,12 @@ hipError_t launch_format(uint32_t epilogue, const PrefillArgs &a, hipStream_t st
   const uint32_t columns = (tiles + 3) / 4, units = a.compute_units ? a.compute_units : 256;
   const uint32_t rounds256 = ((a.rows + 255) / 256 * columns + units - 1) / units;
   const uint32_t rounds128 = ((a.rows + 127) / 128 * columns + units - 1) / units;
-  if (7 * rounds128 < 10 * rounds256) return launch_tile<FMT, 128>(epilogue, a, tiles, stream);
-  return launch_tile<FMT, 256>(epilogue, a, tiles, stream);
+  // Formats whose step slots need more LDS than a 256-row tile leaves (Q6_K, Q8_0, af8g64) run 128-row tiles.
+  if constexpr (lds_bytes<FMT, 256>() > kLdsLimit) return launch_tile<FMT, 128>(epilogue, a, tiles, stream);
+  else {
+    if (7 * rounds128 < 10 * rounds256) return launch_tile<FMT, 128>(epilogue, a, tiles, stream);
+    return launch_tile<FMT, 256>(epilogue, a, tiles, stream);
+  }
 }
 
 }  // namespace
@@ -470,6 +568,10 @@ hipError_t launch_prefill(uint32_t fmt, uint32_t epilogue, const PrefillArgs &a,
     case SQ_FMT_AF4G64: return launch_format<SQ_FMT_AF4G64>(epilogue, a, stream);
     case SQ_FMT_AF4G128: return launch_format<SQ_FMT_AF4G128>(epilogue, a, stream);
     case SQ_FMT_Q4K: return launch_format<SQ_FMT_Q4K>(epilogue, a, stream);
+    case SQ_FMT_Q5K: return launch_format<SQ_FMT_Q5K>(epilogue, a, stream);
+    case SQ_FMT_Q6K: return launch_format<SQ_FMT_Q6K>(epilogue, a, stream);
+    case SQ_FMT_Q80: return launch_format<SQ_FMT_Q80>(epilogue, a, stream);
+    case SQ_FMT_AF8G64: return launch_format<SQ_FMT_AF8G64>(epilogue, a, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -42,7 +42,10 @@ def run_prefill(w_list, x, epilogue=sq.EPILOGUE_NONE, residual=None, gate_scratc
     return out[:rows]
 
 
-@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K, oracle.FMT_AF4G128, oracle.FMT_AF4G32])
+NEW_FORMATS = [oracle.FMT_Q5K, oracle.FMT_Q6K, oracle.FMT_Q80, oracle.FMT_AF8G64]
+
+
+@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K, oracle.FMT_AF4G128, oracle.FMT_AF4G32] + NEW_FORMATS)
 @pytest.mark.parametrize("rows", [33, 128, 300])
 def test_prefill_dense(fmt, rows):
     rng = np.random.default_rng(rows + fmt)
@@ -63,6 +66,31 @@ def test_prefill_sparse_inputs_past_half_range():
     xm[:, ::300] = 1e5
     xb = synthetic.bf16_bits(xm)
     check_projection(run_prefill([w], xb), xb, w, "prefill mixed")
+
+
+@pytest.mark.parametrize("fmt", NEW_FORMATS)
+def test_prefill_new_formats_sparse_and_mixed(fmt):
+    """Sparse +-1e5 inputs (past half's range: the row scale) through the format's prefill tile, and the format beside
+    a Q4_K segment in one fused projection (one dispatch per format, each writing its own columns)."""
+    rng = np.random.default_rng(40 + fmt)
+    k = 2048
+    w = make_weights(rng, fmt, 256, k)
+    x = sparse_inputs(64, k)
+    check_projection(run_prefill([w], x), x, w, f"prefill sparse fmt {fmt}")
+    parts = [make_weights(rng, oracle.FMT_Q4K, 128, k), make_weights(rng, fmt, 192, k)]
+    x = dense_inputs(rng, 100, k)
+    check_projection(run_prefill(parts, x), x, parts, f"prefill mixed fmt {fmt}")
+
+
+@pytest.mark.parametrize("fmt", [oracle.FMT_Q4K, oracle.FMT_Q5K])
+def test_prefill_tall_tiles(fmt):
+    """Enough rows and columns that the launcher takes 256-row tiles (fewer rounds over the compute units), ragged in
+    the last tile: the formats whose step slots leave room for them."""
+    rng = np.random.default_rng(60 + fmt)
+    n, k, rows = 32768, 1024, 520
+    w = make_weights(rng, fmt, n, k)
+    x = dense_inputs(rng, rows, k)
+    check_projection(run_prefill([w], x), x, w, f"prefill tall fmt {fmt}")
 
 
 def test_prefill_fused_segments():
