@@ -217,18 +217,34 @@ def bench_prefill(torch, sq, synthetic, m, n, k, steps, warmup, fmt=None):
     return sec
 
 
-def bench_moe(torch, sq, synthetic, steps, warmup, rows=512, experts=128, top_k=8, hidden=2048, inter=768):
-    fmt = sq.FMT_AF4G64
-    parts = {name: Projection(torch, sq, synthetic, fmt, n, kk, 20 + i)
-             for i, (name, n, kk) in enumerate((("gate", experts * inter, hidden), ("up", experts * inter, hidden),
-                                                ("down", experts * hidden, inter)))}
-    seg = lambda p: sq.segment(fmt, p.n, p.k, p.plane0[0], p.meta[0])
+def bench_moe(torch, sq, synthetic, steps, warmup, rows=512, experts=128, top_k=8, hidden=2048, inter=768,
+              fmt=None, formats=None, shared=0, gated=False, router=False):
+    """One MoE layer (sq_moe_add) per step: routing from the caller's scores, or with `router` the block's F32 router
+    rows projected first; routed experts in `fmt` unless `formats` names a projection's own ("gate", "up", "down",
+    "shared_gate", ...). Returns (seconds, bytes of planes + router + activations in and out, flops)."""
+    fmt = sq.FMT_AF4G64 if fmt is None else fmt
+    formats = formats or {}
+    plan_parts = [("gate", experts * inter, hidden), ("up", experts * inter, hidden), ("down", experts * hidden, inter)]
+    if shared:
+        plan_parts += [("shared_gate", shared * inter, hidden), ("shared_up", shared * inter, hidden),
+                       ("shared_down", shared * hidden, inter)]
+    parts = {name: Projection(torch, sq, synthetic, formats.get(name, fmt), n, kk, 20 + i)
+             for i, (name, n, kk) in enumerate(plan_parts)}
+    seg = lambda name: (sq.segment(parts[name].fmt, parts[name].n, parts[name].k, parts[name].plane0[0],
+                                   parts[name].meta[0], plane1=parts[name].plane1[0]) if name in parts else sq.Segment())
     slots = torch.arange(experts, dtype=torch.int32, device="cuda")
-    weights = sq.MoeWeights(seg(parts["gate"]), seg(parts["up"]), seg(parts["down"]), sq.view(slots), experts)
-    shape = sq.MoeShape(hidden, experts, top_k, inter, fmt)
+    rng = np.random.default_rng(30)
+    scalar_gate = torch.from_numpy(rng.normal(0, 0.05, hidden).astype(np.float32)).cuda() if gated else None
+    router_rows, router_seg = None, sq.Segment()
+    if router:
+        router_rows = torch.from_numpy(rng.normal(0, 0.05, (experts, hidden)).astype(np.float32)).cuda()
+        router_seg = sq.Segment(sq.view(router_rows), sq.view(None), sq.view(None), experts, hidden, 0,
+                                sq.FLOAT32_ROWS)
+    weights = sq.MoeWeights(seg("gate"), seg("up"), seg("down"), sq.view(slots), experts, seg("shared_gate"),
+                            seg("shared_up"), seg("shared_down"), sq.view(scalar_gate), router_seg)
+    shape = sq.MoeShape(hidden, experts, top_k, inter, formats.get("gate", fmt), 0, shared, int(gated))
     plan = sq.MoePlan()
     sq.call("sq_moe_prefill_plan", sq.byref(shape), rows, sq.byref(plan))
-    rng = np.random.default_rng(30)
     x = torch.from_numpy(synthetic.activations(rng, rows, hidden).view(np.int16)).cuda()
     scores = torch.from_numpy(synthetic.router_logits(rng, rows, experts)).cuda()
     out = torch.empty((rows, hidden), dtype=torch.int16, device="cuda")
@@ -246,8 +262,9 @@ def bench_moe(torch, sq, synthetic, steps, warmup, rows=512, experts=128, top_k=
         sq.call("sq_moe_add", handle, sq.byref(buffers), sq.byref(weights), sq.byref(plan))
 
     sec = time_steps(torch, step, steps, warmup)
-    planes = sum(p.bytes() for p in parts.values())
-    return sec, planes + 2 * rows * hidden * 2, 2 * rows * top_k * 3 * inter * hidden
+    planes = sum(p.bytes() for p in parts.values()) + (experts * hidden * 4 if router else 0)
+    flops = 2 * rows * (top_k + shared) * 3 * inter * hidden + (2 * rows * experts * hidden if router else 0)
+    return sec, planes + 2 * rows * hidden * 2, flops
 
 
 def cpu_baseline(sq, synthetic, m, n, k, budget_s: float):
@@ -349,6 +366,14 @@ def main() -> int:
         tf = 2 * 512 * 27648 * 5120 / s / 1e12
         q4k["M512_K5120xN27648"] = {"us": round(s * 1e6, 1), "TFLOPS": round(tf, 1), "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 3)}
         log(f"  q4k M512: {s * 1e6:.0f} us, {tf:.0f} TFLOPS")
+        # The reference's gguf-projection-benchmark: one Q4_K 17408x5120 projection on 2048 rows
+        # (dev/benchmarks/prefill-m3max.md:38-41: 30.68 ms on a 40-core M3 Max).
+        s = bench_prefill(torch, sq, synthetic, 2048, 17408, 5120, 10, 3, fmt=sq.FMT_Q4K)
+        tf = 2 * 2048 * 17408 * 5120 / s / 1e12
+        q4k["M2048_K5120xN17408"] = {"us": round(s * 1e6, 1), "TFLOPS": round(tf, 1),
+                                     "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 3), "reference_ms": 30.68,
+                                     "speedup_vs_reference": round(30.68e-3 / s, 1)}
+        log(f"  q4k M2048 17408x5120: {s * 1e6:.0f} us, {tf:.0f} TFLOPS (reference 30.68 ms on M3 Max)")
         extra["c3_q4k"] = q4k
         # The adjacent formats on the BASELINE config-1 shape, in GB/s of their own plane bytes plus activations
         # and outputs.
@@ -361,12 +386,30 @@ def main() -> int:
                                                           "hbm_frac": round(g / HBM_PEAK_GBS, 3),
                                                           "splits": p.config.splits}
                 log(f"  {name} M{mm}: {s * 1e6:.2f} us, {g:.0f} GB/s")
-        extra["c5_formats_decode"] = formats
+            s = bench_prefill(torch, sq, synthetic, 2048, 14336, 4096, 10, 3, fmt=fmt)
+            tf = 2 * 2048 * 14336 * 4096 / s / 1e12
+            formats[f"{name}_M2048_K4096xN14336"] = {"us": round(s * 1e6, 1), "TFLOPS": round(tf, 1),
+                                                       "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 3)}
+            log(f"  {name} prefill M2048: {s * 1e6:.0f} us, {tf:.0f} TFLOPS")
+        extra["c5_formats"] = formats
         s, moe_bytes, moe_flops = bench_moe(torch, sq, synthetic, 50, 5)
         g = moe_bytes / s / 1e9
         extra["c4_moe_af4g64"] = {"us": round(s * 1e6, 1), "GB/s": round(g, 1), "hbm_frac": round(g / HBM_PEAK_GBS, 3),
                                   "TFLOPS": round(moe_flops / s / 1e12, 2)}
         log(f"  moe: {s * 1e6:.0f} us, {g:.0f} GB/s")
+        # The reference's own MoE benchmark layer (gguf_moe_benchmark.mm, 35B shape: hidden 2048, 256 experts, top 8,
+        # intermediate 512, Q4_K gate/up and Q5_K down experts, a gated Q8_0 shared expert, an F32 router) on a
+        # 2048-row prefill chunk, the whole layer: router projection, routing, expert passes and combine.
+        s, moe_bytes, moe_flops = bench_moe(torch, sq, synthetic, 20, 3, rows=2048, experts=256, top_k=8, hidden=2048,
+                                            inter=512, fmt=sq.FMT_Q4K,
+                                            formats={"down": sq.FMT_Q5K, "shared_gate": sq.FMT_Q80,
+                                                     "shared_up": sq.FMT_Q80, "shared_down": sq.FMT_Q80},
+                                            shared=1, gated=True, router=True)
+        extra["c6_moe_35b_gguf_2048_rows"] = {
+            "ms": round(s * 1e3, 3), "TFLOPS": round(moe_flops / s / 1e12, 2), "GB/s": round(moe_bytes / s / 1e9, 1),
+            "reference_ms": 11.7, "reference_device": "40-core M3 Max (dev/benchmarks/prefill-m3max.md:44-50)",
+            "speedup_vs_reference": round(11.7e-3 / s, 1)}
+        log(f"  moe 35b gguf 2048 rows: {s * 1e3:.3f} ms (reference 11.7 ms on M3 Max)")
     result = {
         "metric": "4-bit GEMV GB/s (% HBM peak) at M=1; prefill q-GEMM TFLOPS at M=2048",
         "value": round(gbs, 1),

@@ -233,7 +233,7 @@ int sq_diag_stream_read(void *graph, sq_buffer src, sq_buffer sink, uint32_t wor
  * scalar gate g, else 1. */
 typedef struct sq_moe_shape {
   uint32_t hidden_size, experts, experts_per_token, expert_intermediate_size;
-  uint32_t expert_format; /* the routed experts' format id */
+  uint32_t expert_format; /* the format of most routed expert weights (each projection runs in its own) */
   uint32_t router;        /* SQ_MOE_ROUTER_* */
   uint32_t shared_slices; /* 0, 1 or 2 */
   uint32_t shared_gated;  /* 1: slice weights sigmoid(x . g); 0: 1 */
@@ -249,9 +249,11 @@ typedef struct sq_moe_plan {
 } sq_moe_plan;
 /* BlockExpertProjection (MoE.hpp:111-148). routed: `slots` experts' planes in one segment of slots * N rows.
  * shared: the shared slices' planes in their order, slice s's rows s * N on (a shared down of shared_slices * I
- * inputs laid out as shared_slices column windows of I inputs, window s rows s * H on); their format may differ
- * from the routed one, gate and up alike. shared_scalar_gate: the block's fp32 gate [hidden] for a gated shared
- * expert. The shared views are ignored without shared slices. */
+ * inputs laid out as shared_slices column windows of I inputs, window s rows s * H on). Each of the six segments
+ * has a format of its own (MoE.cpp:27-62): a gate and up of different formats run as a gate pass and an up pass
+ * whose epilogue reads the gate's bf16 output from expert_output (MoE.cpp:154-173), the same bits as one pass.
+ * shared_scalar_gate: the block's fp32 gate [hidden] for a gated shared expert. The shared views are ignored
+ * without shared slices. */
 typedef struct sq_moe_weights {
   sq_segment gate, up, down;
   sq_buffer slot_table; /* uint32 per expert: its slot */

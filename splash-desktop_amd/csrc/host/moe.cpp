@@ -23,12 +23,12 @@ MoeWorkspace workspaceFor(const MoeShape &shape, uint32_t rows, uint32_t tileRow
           groupedRows * 4, routes * 4, 0, groupedRows * shape.expertIntermediateSize * 2, groupedRows * widest * 2};
 }
 
-// A routed projection: `slots` experts of n rows of k inputs in the segment's format (MoE.cpp:27-62).
-void requireExperts(const QuantizedSegment &s, uint32_t slots, uint32_t n, uint32_t k, uint32_t format,
-                    const char *name) {
-  if (s.formatId != format || s.outputSize != uint64_t{slots} * n || s.inputSize != k)
+// A routed or shared projection: `slots` experts (slices) of n rows of k inputs, each projection in a format of its
+// own (MoE.cpp:27-62).
+void requireExperts(const QuantizedSegment &s, uint32_t slots, uint32_t n, uint32_t k, const char *name) {
+  if (s.outputSize != uint64_t{slots} * n || s.inputSize != k)
     throw std::invalid_argument(std::string("MoE expert ") + name + " does not match the plan");
-  if (!kern::row_tile_format(format))
+  if (!kern::row_tile_format(s.formatId))
     throw std::invalid_argument(std::string("the MoE expert passes do not run ") + s.name() + " weights");
   requireSegmentPlanes(s, std::string("MoE expert ") + name);
 }
@@ -38,16 +38,14 @@ void validate(const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
   const uint32_t h = s.hiddenSize, in = s.expertIntermediateSize;
   if (!w.slots) throw std::invalid_argument("MoE routed experts have no slots");
   requireBytes(w.slotTable, uint64_t{s.experts} * 4, "MoE slot table");
-  requireExperts(w.gate, w.slots, in, h, s.expertFormat, "gate");
-  requireExperts(w.up, w.slots, in, h, s.expertFormat, "up");
-  requireExperts(w.down, w.slots, h, in, s.expertFormat, "down");
+  requireExperts(w.gate, w.slots, in, h, "gate");
+  requireExperts(w.up, w.slots, in, h, "up");
+  requireExperts(w.down, w.slots, h, in, "down");
   if (s.sharedSlices) {
-    // The shared slices (MoE.cpp:40-60). The gate/up pass runs gate and up in one format.
-    if (!sq_format_supported(w.sharedGate.formatId) || !sq_format_supported(w.sharedDown.formatId))
-      throw std::invalid_argument("MoE shared expert format is not supported");
-    requireExperts(w.sharedGate, s.sharedSlices, in, h, w.sharedGate.formatId, "shared gate");
-    requireExperts(w.sharedUp, s.sharedSlices, in, h, w.sharedGate.formatId, "shared up");
-    requireExperts(w.sharedDown, s.sharedSlices, h, in, w.sharedDown.formatId, "shared down");
+    // The shared slices (MoE.cpp:40-60).
+    requireExperts(w.sharedGate, s.sharedSlices, in, h, "shared gate");
+    requireExperts(w.sharedUp, s.sharedSlices, in, h, "shared up");
+    requireExperts(w.sharedDown, s.sharedSlices, h, in, "shared down");
     if (s.sharedGate) requireBytes(w.sharedScalarGate, uint64_t{h} * 4, "MoE shared scalar gate weight");
   }
   if (w.router.plane0 && (!w.router.isFloat() || w.router.outputSize != s.experts || w.router.inputSize != h))
@@ -138,58 +136,79 @@ void MoE::addRouted(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w,
   a.routes = sc.groupedRoutes.as<const uint32_t>();
   a.routes_per_row = s.routesPerToken();
   a.experts = s.experts;
-  // A pass runs the routed and the shared tiles in one launch when their formats agree, else one launch each.
-  const auto pass = [&](uint32_t routedFormat, uint32_t sharedFormat, const char *what) {
-    if (!s.sharedSlices || routedFormat == sharedFormat) {
-      a.fmt = routedFormat;
-      a.mode = s.sharedSlices ? 2 : 0;
-      launched(kern::launch_moe_expert(a, graph), what);
-      return;
-    }
-    a.fmt = routedFormat;
-    a.mode = 0;
-    launched(kern::launch_moe_expert(a, graph), what);
-    a.fmt = sharedFormat;
-    a.mode = 1;
-    launched(kern::launch_moe_expert(a, graph), what);
+  // Plane views of tensor slot n: the routed projection's and the shared one's.
+  const auto bind = [&](int n, const QuantizedSegment &routed, const QuantizedSegment &shared) {
+    a.plane0[n] = routed.plane0.as<const uint8_t>();
+    a.meta[n] = routed.meta.as<const uint8_t>();
+    a.plane1[n] = routed.plane1.as<const uint8_t>();
+    a.shared_plane0[n] = shared.plane0.as<const uint8_t>();
+    a.shared_meta[n] = shared.meta.as<const uint8_t>();
+    a.shared_plane1[n] = shared.plane1.as<const uint8_t>();
   };
-  // Gate and up in one pass over the input rows of the routes: intermediate = bf16(bf16(up) silu(bf16(gate))).
+  const QuantizedSegment none{};
+  // The tiles of one format run in one launch: the routed and shared tiles together when their formats agree
+  // (mode 2), else each on its own (modes 0 and 1). `formats(mode)` gives a launch's (first, second) formats.
+  const auto launches = [&](auto &&formats, auto &&launch) {
+    const auto [r0, r1] = formats(0);
+    if (!s.sharedSlices) return launch(0, r0, r1);
+    const auto [s0, s1] = formats(1);
+    if (r0 == s0 && r1 == s1) return launch(2, r0, r1);
+    launch(0, r0, r1);
+    launch(1, s0, s1);
+  };
+  // Gate and up over the input rows of the routes: intermediate = bf16(bf16(up) silu(bf16(gate))), in one pass when
+  // the two share a format, else the gate into the output scratch and up with the gate epilogue (MoE.cpp:154-173).
+  const auto gateUpFormats = [&](uint32_t mode) {
+    return mode == 0 ? std::pair{w.gate.formatId, w.up.formatId} : std::pair{w.sharedGate.formatId, w.sharedUp.formatId};
+  };
   a.input = b.input.as<const uint16_t>();
-  a.plane0[0] = w.gate.plane0.as<const uint8_t>();
-  a.meta[0] = w.gate.meta.as<const uint8_t>();
-  a.plane0[1] = w.up.plane0.as<const uint8_t>();
-  a.meta[1] = w.up.meta.as<const uint8_t>();
-  a.plane1[0] = w.gate.plane1.as<const uint8_t>();
-  a.plane1[1] = w.up.plane1.as<const uint8_t>();
-  a.shared_plane0[0] = w.sharedGate.plane0.as<const uint8_t>();
-  a.shared_meta[0] = w.sharedGate.meta.as<const uint8_t>();
-  a.shared_plane0[1] = w.sharedUp.plane0.as<const uint8_t>();
-  a.shared_meta[1] = w.sharedUp.meta.as<const uint8_t>();
-  a.shared_plane1[0] = w.sharedGate.plane1.as<const uint8_t>();
-  a.shared_plane1[1] = w.sharedUp.plane1.as<const uint8_t>();
-  a.output = sc.expertIntermediate.as<uint16_t>();
   a.K = s.hiddenSize;
   a.output_size = s.expertIntermediateSize;
-  a.gate_up = 1;
-  pass(s.expertFormat, w.sharedGate.formatId, "MoE gate/up pass");
+  a.gather = 1;
+  launches(gateUpFormats, [&](uint32_t mode, uint32_t gateFormat, uint32_t upFormat) {
+    a.mode = mode;
+    if (gateFormat == upFormat) {
+      bind(0, w.gate, w.sharedGate);
+      bind(1, w.up, w.sharedUp);
+      a.fmt = gateFormat;
+      a.gate_up = 1;
+      a.gate = nullptr;
+      a.output = sc.expertIntermediate.as<uint16_t>();
+      launched(kern::launch_moe_expert(a, graph), "MoE gate/up pass");
+      return;
+    }
+    a.gate_up = 0;
+    bind(0, w.gate, w.sharedGate);
+    bind(1, none, none);
+    a.fmt = gateFormat;
+    a.gate = nullptr;
+    a.output = sc.expertOutput.as<uint16_t>();
+    launched(kern::launch_moe_expert(a, graph), "MoE gate pass");
+    bind(0, w.up, w.sharedUp);
+    a.fmt = upFormat;
+    a.gate = sc.expertOutput.as<const uint16_t>();
+    a.output = sc.expertIntermediate.as<uint16_t>();
+    launched(kern::launch_moe_expert(a, graph), "MoE up pass");
+  });
   // Down over the grouped intermediate rows.
   a.input = sc.expertIntermediate.as<const uint16_t>();
   a.routes = nullptr;
-  a.plane0[0] = w.down.plane0.as<const uint8_t>();
-  a.meta[0] = w.down.meta.as<const uint8_t>();
-  a.plane0[1] = a.meta[1] = nullptr;
-  a.plane1[0] = w.down.plane1.as<const uint8_t>();
-  a.plane1[1] = nullptr;
-  a.shared_plane0[0] = w.sharedDown.plane0.as<const uint8_t>();
-  a.shared_meta[0] = w.sharedDown.meta.as<const uint8_t>();
-  a.shared_plane0[1] = a.shared_meta[1] = nullptr;
-  a.shared_plane1[0] = w.sharedDown.plane1.as<const uint8_t>();
-  a.shared_plane1[1] = nullptr;
+  a.gather = 0;
+  a.gate_up = 0;
+  a.gate = nullptr;
+  bind(0, w.down, w.sharedDown);
+  bind(1, none, none);
   a.output = sc.expertOutput.as<uint16_t>();
   a.K = s.expertIntermediateSize;
   a.output_size = s.hiddenSize;
-  a.gate_up = 0;
-  pass(s.expertFormat, w.sharedDown.formatId, "MoE down pass");
+  const auto downFormats = [&](uint32_t mode) {
+    return std::pair{mode == 0 ? w.down.formatId : w.sharedDown.formatId, 0u};
+  };
+  launches(downFormats, [&](uint32_t mode, uint32_t format, uint32_t) {
+    a.mode = mode;
+    a.fmt = format;
+    launched(kern::launch_moe_expert(a, graph), "MoE down pass");
+  });
   const SqMoeCombineParams combine{plan.rows(), s.hiddenSize, s.routesPerToken()};
   launched(kern::launch_moe_combine(sc.expertOutput.as<const uint16_t>(), sc.routeRows.as<const uint32_t>(),
                                     sc.routingWeights.as<const float>(), b.residual.as<const uint16_t>(),

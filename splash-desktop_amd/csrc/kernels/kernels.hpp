@@ -107,10 +107,12 @@ hipError_t launch_moe_group(const uint32_t *selected, SqMoeTileDescriptor *tiles
                             uint32_t *grouped_routes, uint32_t *route_rows, const SqMoeGroupParams &params,
                             uint32_t shared, hipStream_t stream);
 // An expert pass over the grouped rows, tile by tile: gate_up: gate and up of each tile's expert in one pass over
-// input rows routes[row] / routes_per_row, out = bf16(bf16(up) silu(bf16(gate))); else one tensor over the grouped
-// input rows. Routed tiles (expert < experts) read the routed planes, expert e's rows from slots[e] * output_size
-// on; shared tiles (expert experts + s) the shared planes, slice s's rows s * output_size on. `mode` picks the
-// tiles a launch runs: 0 routed, 1 shared, 2 both (one format).
+// input rows routes[row] / routes_per_row, out = bf16(bf16(up) silu(bf16(gate))); else one tensor, over those input
+// rows when `gather` (a gate or up of its own format) and over the grouped input rows otherwise, out = bf16(y), or
+// with `gate` set (the gate pass's bf16 output, [tiles * tile_rows][output_size]) bf16(bf16(y) silu(gate)), the
+// one-pass result bit for bit. Routed tiles (expert < experts) read the routed planes, expert e's rows from
+// slots[e] * output_size on; shared tiles (expert experts + s) the shared planes, slice s's rows s * output_size on.
+// `mode` picks the tiles a launch runs: 0 routed, 1 shared, 2 both (one format).
 struct MoeExpertArgs {
   const uint16_t *input;        // gate/up: the step's rows [rows][K]; down: grouped rows [tiles * tile_rows][K]
   const uint32_t *routes;       // gate/up: the route of each grouped row (~0u padding)
@@ -124,7 +126,8 @@ struct MoeExpertArgs {
   const uint8_t *shared_plane1[2];
   const uint32_t *slots;
   uint16_t *output;             // [tiles * tile_rows][output_size]
-  uint32_t K, output_size, tile_rows, max_tiles, fmt, gate_up, routes_per_row, experts, mode;
+  const uint16_t *gate;         // a single tensor's up-with-gate operand (null otherwise)
+  uint32_t K, output_size, tile_rows, max_tiles, fmt, gate_up, routes_per_row, experts, mode, gather;
 };
 hipError_t launch_moe_expert(const MoeExpertArgs &args, hipStream_t stream);
 hipError_t launch_moe_combine(const uint16_t *expert_output, const uint32_t *route_rows,

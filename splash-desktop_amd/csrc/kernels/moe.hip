@@ -179,7 +179,8 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
 // over all of K against the tile's rows (at most 32: the expert's grouped rows from tile * tile_rows), so each
 // wave owns its outputs and no wave waits on another. The gate/up pass reads its rows through the grouped routes
 // (row r of the tile is input row routes[r] / top_k: the reference's gather copy folds into these loads) and
-// writes bf16(bf16(up) silu(bf16(gate))); the down pass reads the grouped intermediate rows
+// writes bf16(bf16(up) silu(bf16(gate))); a gate and up of different formats run as two such gathering passes, the
+// gate's output feeding the up pass's epilogue; the down pass reads the grouped intermediate rows
 // (moe_gguf.metal:121-206, moe_expert_slab.h:13-99).
 template <uint32_t FMT, int MB, int NT>
 __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDescriptor d, uint32_t tile,
@@ -205,7 +206,7 @@ __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDes
 #pragma unroll
   for (int b = 0; b < MB; ++b) {
     const uint32_t r = 16u * b + j < rows ? 16u * b + j : 0u;
-    const uint32_t source = NT == 2 ? a.routes[first_row + r] / a.routes_per_row : first_row + r;
+    const uint32_t source = NT == 2 || a.gather ? a.routes[first_row + r] / a.routes_per_row : first_row + r;
     xrow[b] = a.input + (size_t)source * a.K + 4 * q;
   }
   float acc[NT][4][MB][4];
@@ -226,6 +227,9 @@ __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDes
         if constexpr (NT == 2) {
           const float g = bf16_to_f32(f32_to_bf16(acc[0][t][b][i])), u = bf16_to_f32(f32_to_bf16(acc[1][t][b][i]));
           a.output[at] = f32_to_bf16(u * silu(g));
+        } else if (a.gate) {
+          const float u = bf16_to_f32(f32_to_bf16(acc[0][t][b][i]));
+          a.output[at] = f32_to_bf16(u * silu(bf16_to_f32(a.gate[at])));
         } else {
           a.output[at] = f32_to_bf16(acc[0][t][b][i]);
         }

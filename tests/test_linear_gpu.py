@@ -266,13 +266,3 @@ def test_decode_new_formats_longest_slices(fmt, rows):
     got = run_plan(staged(n, k, rows, 1), sq.projection(w.segment()), x, n)
     check_projection(got, x, w, f"fmt {fmt} rows {rows} k {k}")
 
-
-@pytest.mark.parametrize("fmt", NEW_FORMATS)
-def test_new_formats_refused_by_the_prefill_tile(fmt):
-    """The prefill tile (more than 32 rows) does not run these formats yet: refused before any launch."""
-    rng = np.random.default_rng(5)
-    w = make_weights(rng, fmt, 128, 1024)
-    proj = sq.projection(w.segment())
-    plan = sq.plan_for(sq.prefill_workload(128, 1024, 64), proj)
-    with pytest.raises(sq.InvalidArgument, match="does not run"):
-        run_plan(plan, proj, dense_inputs(rng, 64, 1024), 128)

@@ -16,13 +16,15 @@ pytestmark = pytest.mark.gpu
 
 class Block:
     """Routed experts in `fmt`; `shared` shared slices with gate and up in shared_fmt and down in down_fmt, laid out
-    as the reference's BlockExpertProjection (slice s's rows s * N on); a scalar gate when `gated`."""
+    as the reference's BlockExpertProjection (slice s's rows s * N on); a scalar gate when `gated`. `formats` names
+    any projection's own format ("gate", "up", "down", "shared_gate", ...), as the reference's blocks carry them."""
 
     def __init__(self, rng, experts, hidden, intermediate, fmt=oracle.FMT_AF4G64, shared=0, gated=False,
-                 router=oracle.ROUTER_SOFTMAX, shared_fmt=None, down_fmt=None):
+                 router=oracle.ROUTER_SOFTMAX, shared_fmt=None, down_fmt=None, formats=None):
         self.e, self.h, self.i, self.fmt = experts, hidden, intermediate, fmt
         self.shared, self.gated, self.router = shared, gated, router
         self.parts = {}
+        formats = formats or {}
         plan = [("gate", experts * intermediate, hidden, fmt), ("up", experts * intermediate, hidden, fmt),
                 ("down", experts * hidden, intermediate, fmt)]
         if shared:
@@ -30,6 +32,7 @@ class Block:
             df = sf if down_fmt is None else down_fmt
             plan += [("shared_gate", shared * intermediate, hidden, sf), ("shared_up", shared * intermediate, hidden, sf),
                      ("shared_down", shared * hidden, intermediate, df)]
+        plan = [(name, n, k, formats.get(name, f)) for name, n, k, f in plan]
         for name, n, k, f in plan:
             self.parts[name] = make_weights(rng, f, n, k)
         self.slots = to_device(np.arange(experts, dtype=np.uint32))
@@ -153,6 +156,31 @@ def test_moe_routed_formats(fmt, rows):
     x = synthetic.activations(rng, rows, 512)
     scores = synthetic.router_logits(rng, rows, 16)
     check_block(block, x, scores, 4, None, "prefill" if rows > 32 else "decode")
+
+
+@pytest.mark.parametrize("rows,phase", [(48, "prefill"), (5, "decode")])
+def test_moe_projections_in_formats_of_their_own(rows, phase):
+    """Every projection in its own format (MoE.cpp:27-62): a routed gate and up of different formats (a gate pass and
+    an up pass whose epilogue reads the gate), a shared pair likewise, and downs in others."""
+    rng = np.random.default_rng(970 + rows)
+    formats = {"gate": oracle.FMT_Q4K, "up": oracle.FMT_Q5K, "down": oracle.FMT_Q6K,
+               "shared_gate": oracle.FMT_Q80, "shared_up": oracle.FMT_AF8G64, "shared_down": oracle.FMT_AF4G64}
+    block = Block(rng, 16, 512, 256, fmt=oracle.FMT_Q4K, shared=1, gated=True, formats=formats)
+    x = synthetic.activations(rng, rows, 512)
+    scores = synthetic.router_logits(rng, rows, 16)
+    residual = synthetic.bf16_bits(rng.uniform(-2, 2, (rows, 512)).astype(np.float32))
+    check_block(block, x, scores, 4, residual, phase)
+
+
+def test_moe_35b_formats():
+    """The reference benchmark's 35B mix at a small width: Q4_K gate/up and Q5_K down experts, a gated Q8_0 shared
+    expert, top 8 (gguf_moe_benchmark.mm:1-6; its F32 router is test_moe_router_projection's)."""
+    rng = np.random.default_rng(990)
+    block = Block(rng, 32, 512, 256, fmt=oracle.FMT_Q4K, shared=1, gated=True, shared_fmt=oracle.FMT_Q80,
+                  formats={"down": oracle.FMT_Q5K})
+    x = synthetic.activations(rng, 70, 512)
+    scores = synthetic.router_logits(rng, 70, 32)
+    check_block(block, x, scores, 8, None)
 
 
 def test_moe_k_quant_experts_with_q8_0_shared_slice():
