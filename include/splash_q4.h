@@ -1,6 +1,7 @@
 /*
- * splash_q4 — MI355X (gfx950) quantized matmul path: bf16 activations x 4-bit group-quantized weights, fp32
- * accumulation. C ABI over the reference's splash::ops::Linear / splash::ops::MoE call surface.
+ * splash_q4 — MI355X (gfx950) quantized matmul path: bf16 activations x 4-bit group-quantized weights (and the
+ * adjacent 5-, 6- and 8-bit formats), fp32 accumulation. C ABI over the reference's splash::ops::Linear /
+ * splash::ops::MoE call surface.
  *
  * Conventions
  *  - Buffers are device-pointer views {ptr, bytes} (the reference's MetalBuffer views). The caller owns every
@@ -10,7 +11,8 @@
  *  - Every function returns SQ_OK or an error code; nothing is launched when it fails. sq_last_error() holds the
  *    thread's message for the last failure (the text of the reference's std::invalid_argument where it has one).
  *  - Format ids, plane layouts and parameter blocks are the reference's (runtime/metal/abi/QuantFormat.h, Gguf.h,
- *    MoE.h): Q4_K (0) and MLX affine 4-bit in groups of 32, 64 and 128 (25, 26, 27).
+ *    MoE.h): Q4_K (0), Q5_K (3), Q6_K (4), Q8_0 (6), MLX affine 4-bit in groups of 32, 64 and 128 (25, 26, 27)
+ *    and MLX affine 8-bit in groups of 64 (35), in every entry point.
  *  - Split scratch (partials, counters) is reused serially on one stream: counters are zero at allocation and every
  *    split dispatch returns them to zero; two streams never share one scratch.
  * Reference interfaces each entry point replaces are named in its comment (paths under the reference checkout).
@@ -198,18 +200,19 @@ int sq_linear_add_prefill_swiglu(const sq_device *device, void *graph, const sq_
 /* ---- weight preparation (load time) ---- */
 
 /* The gguf_repack dispatch (kernels/shared/gguf_repack.metal:232-238; GgufRepack.h:10-18): native rows in src
- * (src_row_bytes apart) into dst: plane0 at 0, meta at dst_meta (plane1 unused by these formats).
+ * (src_row_bytes apart) into dst: plane0 at 0, meta at dst_meta, and Q5_K's and Q6_K's high bits at dst_plane1
+ * (unused by the other formats).
  * params points at the reference's 24-byte GgufRepackParams {rows, input_size, fmt, src_row_bytes, dst_plane1,
  * dst_meta}. */
 int sq_gguf_repack(void *graph, sq_buffer src, sq_buffer dst, const void *params);
-/* MLX tensors (mlx.core.quantize affine, bits 4: uint32 codes [rows][K/8], bf16 scales and biases
+/* MLX tensors (mlx.core.quantize affine, bits 4 or 8: uint32 codes [rows][K * bits / 32], bf16 scales and biases
  * [rows][K/group]) straight into planes: the loader's native-block build (model/GgufPreparation.cpp:141-193) and
  * the repack in one dispatch. */
 int sq_mlx_repack(void *graph, uint32_t format_id, uint32_t rows, uint32_t input_size, sq_buffer weight,
                   sq_buffer scales, sq_buffer biases, sq_buffer plane0, sq_buffer meta);
-/* Every weight of a segment dequantised: fp32 fma(q, s, z) and its fp16 rounding (the staged tiles' weight), [N][K]
- * each; either output may have a NULL ptr (reference test kernel gguf_test_dequant_<fmt>,
- * dev/tests/engine/gguf_dequant_test.metal:5-21). */
+/* Every weight of a segment dequantised: fp32 fma(q, s, z) (Q6_K s (q - 32), Q8_0 d v) and its fp16 rounding (the
+ * staged tiles' weight), [N][K] each; either output may have a NULL ptr (reference test kernel
+ * gguf_test_dequant_<fmt>, dev/tests/engine/gguf_dequant_test.metal:5-21). */
 int sq_dequant(void *graph, const sq_segment *segment, sq_buffer values_f32, sq_buffer values_f16);
 
 /* ---- measurement ---- */

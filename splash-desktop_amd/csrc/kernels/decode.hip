@@ -1,5 +1,5 @@
 // The row tile of the decode GEMV: y[r][c] = sum_k x[r][k] w[c][k] for 5 to 32 rows of bf16 activations against
-// 4-bit plane weights, fp32 accumulation (reference: gguf_decode / gguf_decode_tile and gguf_decode_gate_up,
+// plane weights of any format this build takes, fp32 accumulation (reference: gguf_decode / gguf_decode_tile and gguf_decode_gate_up,
 // kernels/shared/gguf_linear.metal:71-192, and the exact-operand register tile of
 // kernels/decode/linear_gguf_sgmatrix.metal), and the decode tiles' layout and dispatch.
 //

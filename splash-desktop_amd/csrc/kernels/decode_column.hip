@@ -1,5 +1,5 @@
 // The column tile of the decode GEMV: y[r][c] = sum_k x[r][k] w[c][k] for one to four rows of bf16 activations
-// against 4-bit plane weights, fp32 accumulation (reference: gguf_decode / gguf_decode_tile,
+// against plane weights of any format this build takes, fp32 accumulation (reference: gguf_decode / gguf_decode_tile,
 // kernels/shared/gguf_linear.metal:71-192, with its K-split reduction, kernels/shared/split_reduce.h:14-45).
 //
 // CDNA4 mapping. The GEMV is HBM-bound at 0.5625 bytes per weight, so every lane owns one output column of a

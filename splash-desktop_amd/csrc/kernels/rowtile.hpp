@@ -3,8 +3,9 @@
 // (reference: the exact-operand register tile, kernels/decode/linear_gguf_sgmatrix.metal:37-328), and the waves of
 // a workgroup meet in LDS.
 //
-// CDNA4 mapping. Per group of 32 inputs one 16-byte load per lane (lane l: column l's 32 codes), 1 KiB per wave,
-// kRowPipe groups in flight, every load unconditional. The rows go on the 16-row side of the 16x16x32 bf16 MFMA:
+// CDNA4 mapping. Per group of 32 inputs one 16-byte load per lane (lane l: column l's 32 codes; 8-bit codes two,
+// and Q5_K and Q6_K a plane1 word beside), 1 KiB per wave, kRowPipe groups in flight, every load unconditional. The
+// rows go on the 16-row side of the 16x16x32 bf16 MFMA (the other formats' operands: row_operands):
 //  - a 4x4 transpose of the four code dwords across the wave's four 16-lane rows (v_permlane32_swap, then
 //    v_permlane16_swap) gives lane (j, q) word q of column 16t + j in register t, the MFMA's B layout for column
 //    block t; each word becomes eight exact bf16 operands 128 + q (code_pairs);
