@@ -33,7 +33,7 @@
 namespace sq::kern {
 namespace {
 
-constexpr int BK = 64, kWaves = 4, kThreads = 64 * kWaves, kStages = 3, kSlots = 4;
+constexpr int BK = 64, kWaves = 4, kThreads = 64 * kWaves, kStages = 3;
 constexpr int kRowBytes = BK * 2;                  // one LDS activation row: 64 fp16
 constexpr int kLdsLimit = 160 * 1024;              // LDS a workgroup may hold
 // A wave's LDS slot for one step of its plane tile: the step's two groups of codes (64 columns x P0 bytes each), their
@@ -51,7 +51,14 @@ struct StepSlot {
 };
 template <int BM> constexpr int stage_bytes() { return BM * kRowBytes; }
 template <int BM> constexpr int code_base() { return kStages * stage_bytes<BM>(); }
-template <uint32_t FMT, int BM> constexpr int lds_bytes() { return code_base<BM>() + kSlots * StepSlot<FMT>::all; }
+// Step slots per wave: four (a step's copies run three steps ahead, into the slot two behind the one being read),
+// or three where four do not fit beside a 256-row tile's stages. Then step s's copies of step s + 3 go to step s's
+// own slot, which the wave finished reading (into registers, its LDS reads waited for) and rewriting in place
+// (step_coefficients) during step s - 1; nothing reads it during step s.
+template <uint32_t FMT, int BM>
+constexpr int step_slots() { return code_base<BM>() + 4 * StepSlot<FMT>::all <= kLdsLimit ? 4 : 3; }
+template <uint32_t FMT, int BM>
+constexpr int lds_bytes() { return code_base<BM>() + step_slots<FMT, BM>() * StepSlot<FMT>::all; }
 
 // global -> LDS copy of SIZE bytes per lane (global_load_lds): lane l's bytes land at lds + SIZE l.
 // (The size is spelled as a literal: the host pass of hipcc does not take a template argument there.)
@@ -239,6 +246,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   constexpr int MI = BM / 16;                         // 16-row blocks of the wave
   static_assert(MI == 8 || MI == 16, "128- or 256-row tiles");
   constexpr int kStage = stage_bytes<BM>(), kCodeBase = code_base<BM>(), kSlotBytes = S::all;
+  constexpr int kSlots = step_slots<FMT, BM>();
   // The step's plane copies: the codes, plane1 and meta parts by 16-byte copies of 1 KiB and dword copies of 256 B.
   constexpr int kCode16 = S::code / 1024, kHigh16 = S::high / 1024, kHigh4 = S::high % 1024 / 256;
   constexpr int kMeta16 = S::meta / 1024, kMeta4 = S::meta % 1024 / 256;
@@ -540,7 +548,7 @@ hipError_t launch_format(uint32_t epilogue, const PrefillArgs &a, hipStream_t st
   const uint32_t columns = (tiles + 3) / 4, units = a.compute_units ? a.compute_units : 256;
   const uint32_t rounds256 = ((a.rows + 255) / 256 * columns + units - 1) / units;
   const uint32_t rounds128 = ((a.rows + 127) / 128 * columns + units - 1) / units;
-  // Formats whose step slots need more LDS than a 256-row tile leaves (Q6_K, Q8_0, af8g64) run 128-row tiles.
+  // (Every format's 256-row tile fits the LDS, with three step slots where four do not fit.)
   if constexpr (lds_bytes<FMT, 256>() > kLdsLimit) return launch_tile<FMT, 128>(epilogue, a, tiles, stream);
   else {
     if (7 * rounds128 < 10 * rounds256) return launch_tile<FMT, 128>(epilogue, a, tiles, stream);

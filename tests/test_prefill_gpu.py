@@ -82,10 +82,11 @@ def test_prefill_new_formats_sparse_and_mixed(fmt):
     check_projection(run_prefill(parts, x), x, parts, f"prefill mixed fmt {fmt}")
 
 
-@pytest.mark.parametrize("fmt", [oracle.FMT_Q4K, oracle.FMT_Q5K])
+@pytest.mark.parametrize("fmt", [oracle.FMT_Q4K] + NEW_FORMATS)
 def test_prefill_tall_tiles(fmt):
     """Enough rows and columns that the launcher takes 256-row tiles (fewer rounds over the compute units), ragged in
-    the last tile: the formats whose step slots leave room for them."""
+    the last tile: four step slots a wave, or three for the formats whose slots leave room for no more (Q6_K, Q8_0,
+    af8g64)."""
     rng = np.random.default_rng(60 + fmt)
     n, k, rows = 32768, 1024, 520
     w = make_weights(rng, fmt, n, k)
