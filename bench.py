@@ -20,7 +20,9 @@ Also reported on the same line: the config-1 sweep (M in 1..16 over the four 8B 
 prefill GEMM at M = 2048 (TFLOPS), the config-3 Q4_K shapes, the config-4 MoE block and the CPU baseline (the
 oracle's threaded C implementation of the same quantized matmul on this host's cores, over a bounded sample).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--calibrate-copy]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--sections LIST] [--calibrate-copy]
+(--sections: a comma list of sweep, prefill, q4k, formats, moe, cpu; the headline always runs, and every section runs
+by default. It picks which benchmarks run, for profiling one of them; it changes nothing inside any timed region.)
 """
 from __future__ import annotations
 
@@ -306,7 +308,14 @@ def main() -> int:
     ap.add_argument("--quick", action="store_true", help="headline only (no sweep, prefill, MoE or CPU baseline)")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", action="store_true", help="also run a plain copy of known size (counters)")
+    ap.add_argument("--sections", default="sweep,prefill,q4k,formats,moe,cpu",
+                    help="benchmarks beside the headline: sweep, prefill, q4k, formats, moe, cpu")
     args = ap.parse_args()
+    sections = set() if args.quick else {v.strip() for v in args.sections.split(",") if v.strip()}
+    unknown = sections - {"sweep", "prefill", "q4k", "formats", "moe", "cpu"}
+    if unknown:
+        print(f"bench.py: unknown sections {sorted(unknown)}", file=sys.stderr)
+        return 2
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
@@ -338,7 +347,7 @@ def main() -> int:
         log(f"  calibration copy: 5 x {COPY_BYTES} bytes")
         del src, dst
     extra = {}
-    if not args.quick:
+    if "sweep" in sections:
         sweep = {}
         for (kk, nn) in ((4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)):
             for mm in (1, 2, 4, 8, 16):
@@ -348,6 +357,7 @@ def main() -> int:
                                                "hbm_frac": round(g / HBM_PEAK_GBS, 3), "splits": p.config.splits}
                 log(f"  sweep K{kk} N{nn} M{mm}: {s * 1e6:.2f} us, {g:.0f} GB/s")
         extra["c1_decode_sweep_af4g64"] = sweep
+    if "prefill" in sections:
         prefill = {}
         for (kk, nn) in ((4096, 14336), (14336, 4096), (5120, 27648)):
             s = bench_prefill(torch, sq, synthetic, 2048, nn, kk, 10, 3)
@@ -356,6 +366,7 @@ def main() -> int:
                                              "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 3)}
             log(f"  prefill K{kk} N{nn}: {s * 1e6:.0f} us, {tf:.0f} TFLOPS")
         extra["c2_prefill_af4g64"] = prefill
+    if "q4k" in sections:
         q4k = {}
         for mm in (1, 16):
             s, p = bench_gemv(torch, sq, synthetic, sq.FMT_Q4K, mm, 27648, 5120, max(50, args.steps // 2), 10)
@@ -375,6 +386,7 @@ def main() -> int:
                                      "speedup_vs_reference": round(30.68e-3 / s, 1)}
         log(f"  q4k M2048 17408x5120: {s * 1e6:.0f} us, {tf:.0f} TFLOPS (reference 30.68 ms on M3 Max)")
         extra["c3_q4k"] = q4k
+    if "formats" in sections:
         # The adjacent formats on the BASELINE config-1 shape, in GB/s of their own plane bytes plus activations
         # and outputs.
         formats = {}
@@ -392,6 +404,7 @@ def main() -> int:
                                                        "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 3)}
             log(f"  {name} prefill M2048: {s * 1e6:.0f} us, {tf:.0f} TFLOPS")
         extra["c5_formats"] = formats
+    if "moe" in sections:
         s, moe_bytes, moe_flops = bench_moe(torch, sq, synthetic, 50, 5)
         g = moe_bytes / s / 1e9
         extra["c4_moe_af4g64"] = {"us": round(s * 1e6, 1), "GB/s": round(g, 1), "hbm_frac": round(g / HBM_PEAK_GBS, 3),
@@ -433,7 +446,7 @@ def main() -> int:
         "stream_floor": dict(floor, frac_of_floor=round(gbs / floor["GB/s"], 3)),
     }
     result.update(extra)
-    if not args.quick:
+    if "cpu" in sections:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(sq, synthetic, m, n, k, args.cpu_budget)
     print(json.dumps(result), flush=True)

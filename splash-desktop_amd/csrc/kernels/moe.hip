@@ -236,11 +236,57 @@ __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDes
       }
 }
 
+// The tile workgroup row y runs, longest first: the tiles of more than 16 rows (two row blocks, about twice the work)
+// in tile order, then the others in tile order, so that the cheap tiles fill the compute units' last round instead of
+// a few expensive ones trailing it. The workgroup ranks the live tiles itself (each thread counts a run of them, then
+// a scan of the counts); past kOrderedTiles live tiles it keeps the tile order.
+constexpr uint32_t kOrderedTiles = 2048;
+__device__ uint32_t longest_first_tile(const SqMoeTileDescriptor *tiles, uint32_t n, uint32_t y) {
+  constexpr uint32_t kThreads = 256, kWaves = kThreads / 64;
+  __shared__ uint32_t wave_total[kWaves], picked;
+  if (n > kOrderedTiles) return y;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t run = (n + kThreads - 1) / kThreads, begin = min(n, tid * run), end = min(n, begin + run);
+  uint32_t big = 0;
+  for (uint32_t t = begin; t < end; ++t) big += tiles[t].rows > 16;
+  // Inclusive scan of the threads' counts of big tiles.
+  uint32_t inclusive = big;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t up = (uint32_t)__shfl_up((int)inclusive, d);
+    if (lane >= (uint32_t)d) inclusive += up;
+  }
+  if (lane == 63) wave_total[wave] = inclusive;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+#pragma unroll
+  for (uint32_t w = 0; w < kWaves; ++w) {
+    before += w < wave ? wave_total[w] : 0u;
+    all += wave_total[w];
+  }
+  const uint32_t big_before = before + inclusive - big;   // big tiles before this thread's run
+  // Row y takes big tile y (y < all), else small tile y - all; the thread whose run holds it writes its index.
+  const bool want_big = y < all;
+  const uint32_t rank = want_big ? y : y - all;
+  const uint32_t mine_before = want_big ? big_before : begin - big_before, mine = want_big ? big : end - begin - big;
+  if (rank >= mine_before && rank < mine_before + mine) {
+    uint32_t seen = mine_before;
+    for (uint32_t t = begin; t < end; ++t)
+      if ((tiles[t].rows > 16) == want_big && seen++ == rank) {
+        picked = t;
+        break;
+      }
+  }
+  __syncthreads();
+  return picked;
+}
+
 // Tiles of at most 16 rows (most of an expert's last tiles) take the one-block path.
 template <uint32_t FMT, int MB, int NT>
 __global__ __launch_bounds__(256) void expert_kernel(MoeExpertArgs a) {
-  const uint32_t tile = blockIdx.y;
-  if (tile >= a.tile_count->tiles) return;
+  const uint32_t n = a.tile_count->tiles;
+  if (blockIdx.y >= n) return;
+  const uint32_t tile = longest_first_tile(a.tiles, n, blockIdx.y);
   const uint32_t ct = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (ct >= a.output_size / 64) return;
   const SqMoeTileDescriptor d = a.tiles[tile];
