@@ -1,17 +1,17 @@
 // The row tile of the decode GEMV: y[r][c] = sum_k x[r][k] w[c][k] for 5 to 32 rows of bf16 activations against
-// plane weights of any format this build takes, fp32 accumulation (reference: gguf_decode / gguf_decode_tile and gguf_decode_gate_up,
-// kernels/shared/gguf_linear.metal:71-192, and the exact-operand register tile of
+// plane weights of any format this build takes, fp32 accumulation (reference: gguf_decode / gguf_decode_tile and
+// gguf_decode_gate_up, kernels/shared/gguf_linear.metal:71-192, and the exact-operand register tile of
 // kernels/decode/linear_gguf_sgmatrix.metal), and the decode tiles' layout and dispatch.
 //
 // CDNA4 mapping. A workgroup of W waves takes a 64-column plane tile and W K slices; each wave streams its slice
 // with the row tile's inner loop (rowtile.hpp: exact bf16 operands on the 16x16x32 MFMA, rows on its 16-row side,
-// per-group closes in fp32); the slices meet in LDS in slice order, every wave adding a share of the accumulators,
-// and K partitions across workgroups reduce through split_reduce. A row's result depends only on its own
-// activations and the layout, never on the other rows.
+// per-group closes in fp32); the slices meet in LDS in slice order, every wave adding and storing only the outputs
+// it owns, and K partitions across workgroups reduce as the column tile's do (the last workgroup to arrive adds the
+// splits in split order). A row's result depends only on its own activations and the layout, never on the other
+// rows.
 #include "device.hpp"
 #include "kernels.hpp"
 #include "rowtile.hpp"
-#include "split.hpp"
 
 namespace sq::kern {
 namespace {
@@ -60,14 +60,13 @@ __global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeA
   clear(acc);
   row_slice<FMT, MB, GW, NT>(plane, high, meta, xrow, live, acc);
 
+  // The slices meet in LDS: red[slice][n FO + f][lane], f = (t MB + b) 4 + i the accumulator of column block t, row
+  // block b, row 4q + i of the block. Output f (of both tensors) belongs to wave f % waves, which adds it over the
+  // slices in slice order and stores it; a wave decodes and indexes only the outputs it owns. A K partition across
+  // workgroups stores the sums as fp32 partials, and the last workgroup to arrive adds every split's in split order
+  // and returns the counter to zero (split_reduce.h:14-45).
+  constexpr uint32_t FO = 4 * MB * 4;   // outputs per tensor
   __shared__ float red[row_max_waves(MB, NT) * A * 64];
-  float sum[A];
-  bool owned[A];
-  row_reduce<MB, NT>(acc, red, slice, waves, lane, sum, owned);
-  const uint32_t cstride = NT == 2 ? 2 * a.out_stride : a.out_stride;
-  float total[A][1];
-  bool rlive[A][1];
-  size_t index[A][1];
 #pragma unroll
   for (int n = 0; n < NT; ++n)
 #pragma unroll
@@ -75,34 +74,76 @@ __global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeA
 #pragma unroll
       for (int b = 0; b < MB; ++b)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int e = ((n * 4 + t) * MB + b) * 4 + i;
-          const uint32_t row = 16u * b + 4u * q + i;
-          total[e][0] = sum[e];
-          rlive[e][0] = owned[e] && row < a.rows;
-          index[e][0] = (size_t)row * cstride + n * a.out_stride + seg.out_offset + tile * 64 + 16 * t + j;
-        }
-  if (a.splits > 1 && !split_reduce<A, 1>(total, rlive, index, a.partials, (size_t)a.rows * cstride, split, a.splits,
-                                          a.counters + blockIdx.x, true))
-    return;
+        for (int i = 0; i < 4; ++i) red[(slice * A + n * FO + (t * MB + b) * 4 + i) * 64 + lane] = acc[n][t][b][i];
+  __syncthreads();
+  const uint32_t cstride = NT == 2 ? 2 * a.out_stride : a.out_stride, column0 = seg.out_offset + tile * 64 + j;
+  const size_t split_elements = (size_t)a.rows * cstride;
+  // Output f's row and column.
+  const auto place = [&](uint32_t f, uint32_t &row, uint32_t &col) __attribute__((always_inline)) {
+    row = 16u * ((f >> 2) % MB) + 4u * q + (f & 3);
+    col = column0 + 16u * ((f >> 2) / MB);
+  };
+  const auto store = [&](const float (&v)[NT], uint32_t row, uint32_t col) __attribute__((always_inline)) {
+    const size_t o = (size_t)row * a.out_stride + col;
+    if constexpr (NT == 2) {
+      const float g = bf16_to_f32(f32_to_bf16(v[0])), up = bf16_to_f32(f32_to_bf16(v[1]));
+      ((uint16_t *)a.output)[o] = f32_to_bf16(up * silu(g));
+    } else {
+      const float y = epilogue<EP>(v[0], a.aux, o);
+      if constexpr (F32OUT) ((float *)a.output)[o] = y;
+      else ((uint16_t *)a.output)[o] = f32_to_bf16(y);
+    }
+  };
+  const bool splitting = a.splits > 1;
+#pragma unroll 1
+  for (uint32_t f = slice; f < FO; f += waves) {
+    uint32_t row, col;
+    place(f, row, col);
+    float v[NT];
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+    for (int n = 0; n < NT; ++n) {
+      float sum = 0.0f;
+      for (uint32_t w = 0; w < waves; ++w) sum += red[(w * A + n * FO + f) * 64 + lane];
+      v[n] = sum;
+    }
+    if (row >= a.rows) continue;
+    if (!splitting) {
+      store(v, row, col);
+      continue;
+    }
 #pragma unroll
-    for (int b = 0; b < MB; ++b)
+    for (int n = 0; n < NT; ++n)
+      __hip_atomic_store(&a.partials[split * split_elements + (size_t)row * cstride + n * a.out_stride + col], v[n],
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (!splitting) return;
+  // Every access to the partials and the counter is a device-scope atomic, performed past the per-XCD L2s; each wave
+  // waits for its partial stores to complete before thread 0 arrives at the counter.
+  __shared__ uint32_t arrival;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  uint32_t *counter = a.counters + blockIdx.x;
+  if (threadIdx.x == 0) arrival = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (arrival != a.splits - 1) return;
+#pragma unroll 1
+  for (uint32_t f = slice; f < FO; f += waves) {
+    uint32_t row, col;
+    place(f, row, col);
+    if (row >= a.rows) continue;
+    float v[NT];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int e = (t * MB + b) * 4 + i;
-        if (!rlive[e][0]) continue;
-        const size_t o = (size_t)(16u * b + 4u * q + i) * a.out_stride + seg.out_offset + tile * 64 + 16 * t + j;
-        if constexpr (NT == 2) {
-          const float g = bf16_to_f32(f32_to_bf16(total[e][0])), up = bf16_to_f32(f32_to_bf16(total[4 * MB * 4 + e][0]));
-          ((uint16_t *)a.output)[o] = f32_to_bf16(up * silu(g));
-        } else {
-          const float v = epilogue<EP>(total[e][0], a.aux, o);
-          if constexpr (F32OUT) ((float *)a.output)[o] = v;
-          else ((uint16_t *)a.output)[o] = f32_to_bf16(v);
-        }
-      }
+    for (int n = 0; n < NT; ++n) {
+      float sum = 0.0f;
+      for (uint32_t p = 0; p < a.splits; ++p)
+        sum += __hip_atomic_load(&a.partials[p * split_elements + (size_t)row * cstride + n * a.out_stride + col],
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      v[n] = sum;
+    }
+    store(v, row, col);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <uint32_t FMT, int MB, int NT, uint32_t EP, bool F32OUT>

@@ -1,7 +1,6 @@
 // The row tile's inner loop, shared by the decode row tile (decode.hip) and the MoE expert passes (moe.hip): one
 // wave streams one K slice of a 64-column plane tile against 16 or 32 rows of bf16 activations with exact operands
-// (reference: the exact-operand register tile, kernels/decode/linear_gguf_sgmatrix.metal:37-328), and the waves of
-// a workgroup meet in LDS.
+// (reference: the exact-operand register tile, kernels/decode/linear_gguf_sgmatrix.metal:37-328).
 //
 // CDNA4 mapping. Per group of 32 inputs one 16-byte load per lane (lane l: column l's 32 codes; 8-bit codes two,
 // and Q5_K and Q6_K a plane1 word beside), 1 KiB per wave, kRowPipe groups in flight, every load unconditional. The
@@ -188,8 +187,9 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
                                           uint32_t live, float (&acc)[NT][4][MB][4]) {
   using F = Fmt<FMT>;
   // 8-bit codes (twice the bytes a group) keep fewer groups in flight, and so do the K-quants with plane1 bits in the
-  // longest slices of one tensor's 16 rows (whose workgroups hold the most waves, 128 registers each).
-  constexpr bool kTight = F::P1 && MB == 1 && NT == 1 && GW == 32;
+  // longest slices of one tensor's 16 rows (whose workgroups hold the most waves, 128 registers each), and Q6_K (two
+  // scales a group) in every slice of 16 rows.
+  constexpr bool kTight = F::P1 && MB == 1 && ((NT == 1 && GW == 32) || F::HALVES);
   constexpr int kDepth = F::P0 == 32 || kTight ? kRowPipe / 2 : kRowPipe;
   constexpr int SG = F::SG, UNIT = F::UNIT, P = GW < kDepth ? GW : kDepth;
   static_assert(GW % UNIT == 0 && GW % SG == 0, "a slice holds whole meta units");
@@ -345,34 +345,6 @@ __device__ __forceinline__ void clear(float (&acc)[NT][4][MB][4]) {
       for (int b = 0; b < MB; ++b)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[n][t][b][i] = 0.0f;
-}
-
-// The workgroup's slices meet in LDS (red: waves x A x 64 floats, A = NT * 4 * MB * 4): accumulator e of every
-// tensor is added, in slice order, by wave owner(e) = (e % (4 MB 4)) % waves, which gets total[e]; owned[e] says
-// whether this wave holds it.
-template <int MB, int NT>
-__device__ __forceinline__ void row_reduce(const float (&acc)[NT][4][MB][4], float *red, uint32_t slice,
-                                           uint32_t waves, int lane, float (&total)[NT * 4 * MB * 4],
-                                           bool (&owned)[NT * 4 * MB * 4]) {
-  constexpr int A = NT * 4 * MB * 4;
-#pragma unroll
-  for (int n = 0; n < NT; ++n)
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int b = 0; b < MB; ++b)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) red[((slice * A) + ((n * 4 + t) * MB + b) * 4 + i) * 64 + lane] = acc[n][t][b][i];
-  __syncthreads();
-#pragma unroll
-  for (int e = 0; e < A; ++e) {
-    const uint32_t own = (uint32_t)(e % (4 * MB * 4)) % waves;
-    float v = 0.0f;
-    if (own == slice)
-      for (uint32_t w = 0; w < waves; ++w) v += red[(w * A + e) * 64 + lane];
-    total[e] = v;
-    owned[e] = own == slice;
-  }
 }
 
 }  // namespace sq::kern
