@@ -211,10 +211,9 @@ __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDes
   }
   float acc[NT][4][MB][4];
   clear(acc);
-  // A gate/up pair runs one wave a SIMD anyway: it takes a third register set to look further ahead (the K-quant
-  // headers and 8-bit codes leave no room for it).
-  constexpr int kSets = NT == 2 && F::UNIT < 8 && F::P0 == 16 ? 3 : 2;
-  row_stream<FMT, MB, NT, kSets>(plane, high, meta, xrow, G, acc);
+  // Two register sets (one chunk of loads ahead): the passes are bound by instruction issue, and a third set for a
+  // gate/up pair only moves more of its MFMA results through the accumulation registers.
+  row_stream<FMT, MB, NT, 2>(plane, high, meta, xrow, G, acc);
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
