@@ -16,7 +16,8 @@
 //    shorter; slices start on meta units). Each wave streams its slice with P groups in flight: codes, meta and
 //    activations are issued in the order they are consumed, every load unconditional (addresses past the slice
 //    repeat its last group and are not computed on), so the wait counts stay exact and every wave draws bandwidth
-//    for the whole dispatch instead of in one burst. The slices meet in LDS in slice order.
+//    for the whole dispatch instead of in one burst. The slices meet in LDS in slice order, each row's outputs
+//    summed and stored by a wave of their own.
 //  - One workgroup covers a tile's whole K unless the launcher's layout splits it: a split across workgroups adds
 //    three device-scope round trips at the end of the dispatch (split_reduce), which only pays when the tiles alone
 //    leave most compute units idle.
@@ -202,14 +203,14 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  // Slices meet in LDS; the slice-0 wave adds them in slice order.
+  // Slices meet in LDS; row r's outputs (of both tensors) belong to wave r % waves, which adds them in slice order
+  // and stores them (or stages them for the split reduce).
   __shared__ float red[kColumnMaxWaves][NT][MR][64];
 #pragma unroll
   for (int n = 0; n < NT; ++n)
 #pragma unroll
     for (int r = 0; r < MR; ++r) red[slice][n][r][lane] = acc[n][r];
   __syncthreads();
-  const bool owner = slice == 0;
   const uint32_t col = seg.out_offset + tile * 64 + lane;
   const uint32_t cstride = NT == 2 ? 2 * a.out_stride : a.out_stride;
   float total[NT][MR];
@@ -219,20 +220,20 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
   for (int n = 0; n < NT; ++n)
 #pragma unroll
     for (int r = 0; r < MR; ++r) {
+      const bool mine = (uint32_t)r % waves == slice;
       float v = 0.0f;
-      if (owner)
+      if (mine)
         for (uint32_t w = 0; w < waves; ++w) v += red[w][n][r][lane];
       total[n][r] = v;
-      rlive[n][r] = (uint32_t)r < a.rows;
+      rlive[n][r] = mine && (uint32_t)r < a.rows;
       index[n][r] = (size_t)r * cstride + n * a.out_stride + col;
     }
   if (a.splits > 1 && !split_reduce<NT, MR>(total, rlive, index, a.partials, (size_t)a.rows * cstride, split,
-                                            a.splits, a.counters + blockIdx.x, owner))
+                                            a.splits, a.counters + blockIdx.x, true))
     return;
-  if (!owner) return;
 #pragma unroll
   for (int r = 0; r < MR; ++r) {
-    if ((uint32_t)r >= a.rows) continue;
+    if (!rlive[0][r]) continue;
     const size_t o = (size_t)r * a.out_stride + col;
     if constexpr (NT == 2) {
       const float g = bf16_to_f32(f32_to_bf16(total[0][r])), up = bf16_to_f32(f32_to_bf16(total[1][r]));
