@@ -182,6 +182,11 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
 // writes bf16(bf16(up) silu(bf16(gate))); a gate and up of different formats run as two such gathering passes, the
 // gate's output feeding the up pass's epilogue; the down pass reads the grouped intermediate rows
 // (moe_gguf.metal:121-206, moe_expert_slab.h:13-99).
+// The gate/up pairs whose registers fit two waves a SIMD (the others, with K-quant headers, plane1 bits, 8-bit codes
+// or 128-input scale groups, run one).
+template <uint32_t FMT>
+constexpr bool pair_two_waves() { return FMT == SQ_FMT_AF4G32 || FMT == SQ_FMT_AF4G64; }
+
 template <uint32_t FMT, int MB, int NT>
 __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDescriptor d, uint32_t tile,
                                             uint32_t ct) {
@@ -212,8 +217,11 @@ __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDes
   float acc[NT][4][MB][4];
   clear(acc);
   // Two register sets (one chunk of loads ahead): the passes are bound by instruction issue, and a third set for a
-  // gate/up pair only moves more of its MFMA results through the accumulation registers.
-  row_stream<FMT, MB, NT, 2>(plane, high, meta, xrow, G, acc);
+  // gate/up pair only moves more of its MFMA results through the accumulation registers. A pair of 4-bit affine
+  // codes in groups of 32 or 64 streams chunks of two groups with operands built just before their MFMAs, which fits
+  // two waves a SIMD (expert_kernel); a second resident wave covers more of the first one's dependency stalls.
+  constexpr bool kTwoWaves = NT == 2 && pair_two_waves<FMT>();
+  row_stream<FMT, MB, NT, 2, kTwoWaves ? 2 : 4, !kTwoWaves>(plane, high, meta, xrow, G, acc);
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -282,7 +290,8 @@ __device__ uint32_t longest_first_tile(const SqMoeTileDescriptor *tiles, uint32_
 
 // Tiles of at most 16 rows (most of an expert's last tiles) take the one-block path.
 template <uint32_t FMT, int MB, int NT>
-__global__ __launch_bounds__(256) void expert_kernel(MoeExpertArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 2 && pair_two_waves<FMT>() ? 2 : 1)))
+void expert_kernel(MoeExpertArgs a) {
   const uint32_t n = a.tile_count->tiles;
   if (blockIdx.y >= n) return;
   const uint32_t tile = longest_first_tile(a.tiles, n, blockIdx.y);

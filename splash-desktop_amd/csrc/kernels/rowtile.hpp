@@ -246,15 +246,16 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
   }
 }
 
-// Adds all G groups of NT tensors' plane tiles to acc, as row_slice does, in one continuous stream: chunks of four
+// Adds all G groups of NT tensors' plane tiles to acc, as row_slice does, in one continuous stream: chunks of CH
 // groups, each chunk's loads (clamped to the last group, so every chunk issues as many) issued SETS - 1 chunks
-// ahead into a ring of SETS register sets. plane[n], high[n], meta[n] and xrow[b] point at group 0 for the lane.
-template <uint32_t FMT, int MB, int NT, int SETS = 2>
+// ahead into a ring of SETS register sets; AHEAD builds each group's operands a group ahead (else just before its
+// MFMAs). plane[n], high[n], meta[n] and xrow[b] point at group 0 for the lane.
+template <uint32_t FMT, int MB, int NT, int SETS = 2, int CH = 4, bool AHEAD = true>
 __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], const uint8_t *const (&high)[NT],
                                            const uint8_t *const (&meta)[NT], const uint16_t *const (&xrow)[MB],
                                            uint32_t G, float (&acc)[NT][4][MB][4]) {
   using F = Fmt<FMT>;
-  constexpr int SG = F::SG, UNIT = F::UNIT, CH = 4, MU = UNIT < CH ? CH / UNIT : 1;
+  constexpr int SG = F::SG, UNIT = F::UNIT, MU = UNIT < CH ? CH / UNIT : 1;
   static_assert(CH % SG == 0, "a chunk holds whole scale groups");
   const uint32_t last = G - 1, chunks = (G + CH - 1) / CH;
   const CodeConstants cc = make_code_constants();
@@ -286,9 +287,9 @@ __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], co
   };
   f32x4 C[NT][4][MB], C2[NT][4][MB], S[MB], S2[MB];
   // Each group's exact operands are built one group ahead, into the other of two operand sets, so that building
-  // them interleaves with the previous group's MFMAs; 8-bit codes (two operand sets a group) build them just before
-  // their MFMAs, to fit the registers.
-  constexpr bool kAhead = F::P0 != 32;
+  // them interleaves with the previous group's MFMAs; 8-bit codes (two operand sets a group), and callers that ask
+  // for it to fit the registers, build them just before their MFMAs.
+  constexpr bool kAhead = F::P0 != 32 && AHEAD;
   u32x4 lo[2][NT][4], hi[2][NT][4];
   const auto prepare = [&](int set, int u, int os) __attribute__((always_inline)) {
 #pragma unroll
