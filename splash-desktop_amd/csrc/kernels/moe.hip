@@ -182,10 +182,14 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
 // writes bf16(bf16(up) silu(bf16(gate))); a gate and up of different formats run as two such gathering passes, the
 // gate's output feeding the up pass's epilogue; the down pass reads the grouped intermediate rows
 // (moe_gguf.metal:121-206, moe_expert_slab.h:13-99).
-// The gate/up pairs whose registers fit two waves a SIMD (the others, with K-quant headers, plane1 bits, 8-bit codes
-// or 128-input scale groups, run one).
+// The formats whose passes stream chunks of two groups with operands built just before their MFMAs: 4-bit affine
+// codes in groups of 32 or 64, whose gate/up pair then fits two waves a SIMD and single tensor three. The others
+// (K-quant headers, plane1 bits, 8-bit codes, 128-input scale groups) would spill there and keep four-group chunks
+// with operands a group ahead. Chunks hold whole scale groups either way, so the sums are the same bits.
 template <uint32_t FMT>
-constexpr bool pair_two_waves() { return FMT == SQ_FMT_AF4G32 || FMT == SQ_FMT_AF4G64; }
+constexpr bool short_chunks() { return FMT == SQ_FMT_AF4G32 || FMT == SQ_FMT_AF4G64; }
+template <uint32_t FMT, int NT>
+constexpr int expert_waves() { return short_chunks<FMT>() ? (NT == 2 ? 2 : 3) : 1; }
 
 template <uint32_t FMT, int MB, int NT>
 __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDescriptor d, uint32_t tile,
@@ -217,11 +221,10 @@ __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDes
   float acc[NT][4][MB][4];
   clear(acc);
   // Two register sets (one chunk of loads ahead): the passes are bound by instruction issue, and a third set for a
-  // gate/up pair only moves more of its MFMA results through the accumulation registers. A pair of 4-bit affine
-  // codes in groups of 32 or 64 streams chunks of two groups with operands built just before their MFMAs, which fits
-  // two waves a SIMD (expert_kernel); a second resident wave covers more of the first one's dependency stalls.
-  constexpr bool kTwoWaves = NT == 2 && pair_two_waves<FMT>();
-  row_stream<FMT, MB, NT, 2, kTwoWaves ? 2 : 4, !kTwoWaves>(plane, high, meta, xrow, G, acc);
+  // gate/up pair only moves more of its MFMA results through the accumulation registers. Short chunks fit more
+  // waves a SIMD (expert_kernel), and each resident wave covers more of the others' dependency stalls.
+  constexpr bool kShort = short_chunks<FMT>();
+  row_stream<FMT, MB, NT, 2, kShort ? 2 : 4, !kShort>(plane, high, meta, xrow, G, acc);
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -290,7 +293,7 @@ __device__ uint32_t longest_first_tile(const SqMoeTileDescriptor *tiles, uint32_
 
 // Tiles of at most 16 rows (most of an expert's last tiles) take the one-block path.
 template <uint32_t FMT, int MB, int NT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 2 && pair_two_waves<FMT>() ? 2 : 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(expert_waves<FMT, NT>())))
 void expert_kernel(MoeExpertArgs a) {
   const uint32_t n = a.tile_count->tiles;
   if (blockIdx.y >= n) return;
