@@ -182,14 +182,18 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
 // writes bf16(bf16(up) silu(bf16(gate))); a gate and up of different formats run as two such gathering passes, the
 // gate's output feeding the up pass's epilogue; the down pass reads the grouped intermediate rows
 // (moe_gguf.metal:121-206, moe_expert_slab.h:13-99).
-// The formats whose passes stream chunks of two groups with operands built just before their MFMAs: 4-bit affine
-// codes in groups of 32 or 64, whose gate/up pair then fits two waves a SIMD and single tensor three. The others
-// (K-quant headers, plane1 bits, 8-bit codes, 128-input scale groups) would spill there and keep four-group chunks
-// with operands a group ahead. Chunks hold whole scale groups either way, so the sums are the same bits.
+// The passes that stream chunks of two groups with operands built just before their MFMAs: those of 4-bit affine
+// codes in groups of 32 or 64 (a gate/up pair then fits two waves a SIMD, a single tensor three), and every
+// single-tensor pass whose scale groups fit a two-group chunk (the K-quants and 8-bit codes then fit two waves a SIMD
+// instead of one). The other gate/up pairs (K-quant headers, plane1 bits, 8-bit codes) would spill there and keep
+// four-group chunks with operands a group ahead, one wave a SIMD. Chunks hold whole scale groups either way, so the
+// sums are the same bits.
 template <uint32_t FMT>
-constexpr bool short_chunks() { return FMT == SQ_FMT_AF4G32 || FMT == SQ_FMT_AF4G64; }
+constexpr bool affine4_short() { return FMT == SQ_FMT_AF4G32 || FMT == SQ_FMT_AF4G64; }
 template <uint32_t FMT, int NT>
-constexpr int expert_waves() { return short_chunks<FMT>() ? (NT == 2 ? 2 : 3) : 1; }
+constexpr bool short_chunks() { return affine4_short<FMT>() || (NT == 1 && Fmt<FMT>::SG <= 2); }
+template <uint32_t FMT, int NT>
+constexpr int expert_waves() { return affine4_short<FMT>() ? (NT == 2 ? 2 : 3) : short_chunks<FMT, NT>() ? 2 : 1; }
 
 template <uint32_t FMT, int MB, int NT>
 __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDescriptor d, uint32_t tile,
@@ -223,7 +227,7 @@ __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDes
   // Two register sets (one chunk of loads ahead): the passes are bound by instruction issue, and a third set for a
   // gate/up pair only moves more of its MFMA results through the accumulation registers. Short chunks fit more
   // waves a SIMD (expert_kernel), and each resident wave covers more of the others' dependency stalls.
-  constexpr bool kShort = short_chunks<FMT>();
+  constexpr bool kShort = short_chunks<FMT, NT>();
   row_stream<FMT, MB, NT, 2, kShort ? 2 : 4, !kShort>(plane, high, meta, xrow, G, acc);
 #pragma unroll
   for (int t = 0; t < 4; ++t)
