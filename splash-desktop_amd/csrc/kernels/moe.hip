@@ -11,6 +11,25 @@
 namespace sq::kern {
 namespace {
 
+// A 64-lane reduction by DPP row operations (dpp_ctrl quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror, then row_bcast15 into rows 1 and 3 and row_bcast31 into rows 2 and 3): after the six steps lane 63
+// holds op over all 64 lanes, which readlane gives every lane. op must be associative, commutative and idempotent
+// (a row the mask leaves out combines a value with itself).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_row(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROWS, 0xF, false);
+}
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_reduce(uint32_t v, Op op) {
+  v = op(v, dpp_row<0xB1, 0xF>(v));
+  v = op(v, dpp_row<0x4E, 0xF>(v));
+  v = op(v, dpp_row<0x141, 0xF>(v));
+  v = op(v, dpp_row<0x140, 0xF>(v));
+  v = op(v, dpp_row<0x142, 0xA>(v));
+  v = op(v, dpp_row<0x143, 0xC>(v));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 // One wave per row (moe.metal:23-112). Rank by rank, the highest remaining score wins, the lowest expert id among
 // equal scores; the router then weights the top_k routes in rank order: Softmax weight_r =
 // 2^((s_r - s_0) log2 e) / sum_o 2^((s_o - s_0) log2 e), SigmoidNormalized weight_r = sigmoid(s_r) /
@@ -51,13 +70,11 @@ __global__ __launch_bounds__(64) void route_select_kernel(const float *scores, u
 #pragma unroll
     for (int i = 0; i < kPer; ++i)
       if (lane + 64u * i < p.experts && !((taken >> i) & 1u) && (at < 0 || v[i] > best)) best = v[i], at = i;
-    float top = best;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) top = fmaxf(top, __shfl_xor(top, m));
+    const float top = __uint_as_float(wave_reduce(__float_as_uint(best), [](uint32_t a, uint32_t b) {
+      return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+    }));
     const uint32_t candidate = at >= 0 && best == top ? lane + 64u * at : 0xFFFFFFFFu;
-    uint32_t winner = candidate;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) winner = min(winner, (uint32_t)__shfl_xor((int)winner, m));
+    const uint32_t winner = wave_reduce(candidate, [](uint32_t a, uint32_t b) { return min(a, b); });
     if (candidate == winner && at >= 0) taken |= 1u << at;
     if (lane == 0) {
       selected[base + rank] = winner;
