@@ -221,8 +221,8 @@ def bench_prefill(torch, sq, synthetic, m, n, k, steps, warmup, fmt=None):
 
 def bench_moe(torch, sq, synthetic, steps, warmup, rows=512, experts=128, top_k=8, hidden=2048, inter=768,
               fmt=None, formats=None, shared=0, gated=False, router=False):
-    """One MoE layer (sq_moe_add) per step: routing from the caller's scores, or with `router` the block's F32 router
-    rows projected first; routed experts in `fmt` unless `formats` names a projection's own ("gate", "up", "down",
+    """One MoE layer (sq_moe_add) per step: routing from the caller's scores (written once into the grouped-input
+    scratch, where the router's scores live), or with `router` the block's F32 router rows projected first; routed experts in `fmt` unless `formats` names a projection's own ("gate", "up", "down",
     "shared_gate", ...). Returns (seconds, bytes of planes + router + activations in and out, flops)."""
     fmt = sq.FMT_AF4G64 if fmt is None else fmt
     formats = formats or {}
@@ -246,18 +246,21 @@ def bench_moe(torch, sq, synthetic, steps, warmup, rows=512, experts=128, top_k=
                             seg("shared_up"), seg("shared_down"), sq.view(scalar_gate), router_seg)
     shape = sq.MoeShape(hidden, experts, top_k, inter, formats.get("gate", fmt), 0, shared, int(gated))
     plan = sq.MoePlan()
-    sq.call("sq_moe_prefill_plan", sq.byref(shape), rows, sq.byref(plan))
+    sq.call("sq_moe_prefill_plan", sq.byref(shape), rows, None, sq.byref(plan))
     x = torch.from_numpy(synthetic.activations(rng, rows, hidden).view(np.int16)).cuda()
-    scores = torch.from_numpy(synthetic.router_logits(rng, rows, experts)).cuda()
+    width = sq.lib().sq_moe_router_width(sq.byref(shape))
+    scores = np.zeros((rows, width), np.float32)
+    scores[:, :experts] = synthetic.router_logits(rng, rows, experts)
     out = torch.empty((rows, hidden), dtype=torch.int16, device="cuda")
     held = []
     fields = []
     for name in sq._MOE_WORKSPACE:
         nbytes = getattr(plan.workspace, name)
-        t = torch.zeros(max(nbytes, 4) // 4 + 1, dtype=torch.int32, device="cuda") if nbytes else None
+        t = (torch.from_numpy(scores).cuda() if name == "grouped_input" else
+             torch.zeros(max(nbytes, 4) // 4 + 1, dtype=torch.int32, device="cuda") if nbytes else None)
         held.append(t)
         fields.append(sq.view(t))
-    buffers = sq.MoeBuffers(sq.view(x), sq.view(scores), sq.view(None), sq.view(out), 0, sq.MoeScratch(*fields))
+    buffers = sq.MoeBuffers(sq.view(x), sq.view(None), sq.view(out), sq.MoeScratch(*fields), sq.view(None))
     handle = sq.stream_handle()
 
     def step(i):

@@ -245,9 +245,30 @@ typedef struct sq_moe_workspace {
   uint64_t selected_experts, routing_weights, tile_descriptors, tile_count, grouped_routes, route_rows,
       grouped_input, expert_intermediate, expert_output;
 } sq_moe_workspace;
+/* MoeExpertTile (MoE.hpp:284): the rows of an expert tile. */
+#define SQ_MOE_EXPERT_TILE_M8 8u
+#define SQ_MOE_EXPERT_TILE_M32 32u
+/* MoeGgufTile (MoE.hpp:297): Staged runs here; Register is the reference's Apple9 tile, which a plan refuses. */
+#define SQ_MOE_GGUF_TILE_STAGED 0u
+#define SQ_MOE_GGUF_TILE_REGISTER 1u
+/* FloatTile (Linear.hpp:33): the router projection's tile. Both values run this build's one float tile (the results
+ * lie within the same fp32 bound); NEURAL_ACCELERATOR names an Apple unit and is accepted as the reference's callers
+ * may pass it. */
+#define SQ_FLOAT_TILE_SIMDGROUP 0u
+#define SQ_FLOAT_TILE_NEURAL_ACCELERATOR 1u
+/* MoeConfig (MoE.hpp:333-346): the device's policy for a MoE plan. cpu_bf16_experts opts the reference's streamed
+ * CPU experts in; its experts here are never streamed, so the flag selects nothing, as the reference's MoE::add
+ * takes the GPU route for weights that are not streamed (MoE.cpp:225-245). */
+typedef struct sq_moe_config {
+  uint32_t expert_tile; /* SQ_MOE_EXPERT_TILE_* */
+  uint32_t gguf_tile;   /* SQ_MOE_GGUF_TILE_* */
+  uint32_t router_tile; /* SQ_FLOAT_TILE_* */
+  uint32_t cpu_bf16_experts;
+} sq_moe_config;
 typedef struct sq_moe_plan {
   sq_moe_shape shape;
   uint32_t rows, phase, tile_rows, maximum_tiles;
+  sq_moe_config config;
   sq_moe_workspace workspace;
 } sq_moe_plan;
 /* BlockExpertProjection (MoE.hpp:111-148). routed: `slots` experts' planes in one segment of slots * N rows.
@@ -263,27 +284,42 @@ typedef struct sq_moe_weights {
   uint32_t slots;
   sq_segment shared_gate, shared_up, shared_down;
   sq_buffer shared_scalar_gate;
-  /* BlockMoeWeights::router (MoE.hpp:133): F32 (SQ_FLOAT32_ROWS) or BF16 rows [experts][hidden] in plane0. With
-   * plane0 set the routing first projects the input onto it into buffers->scores (MoE::addRoutes,
-   * MoE.cpp:527-543); with plane0 NULL the scores are the caller's. */
+  /* BlockMoeWeights::router (MoE.hpp:133): F32 (SQ_FLOAT32_ROWS) or BF16 rows [experts][hidden] in plane0. The
+   * routing projects the input onto it into the router scores (MoE::addRoutes, MoE.cpp:527-543). With plane0 NULL
+   * the routing reads scores the caller wrote (below). */
   sq_segment router;
 } sq_moe_weights;
+/* MoeScratch (MoE.hpp:225-245), sized by the plan's workspace. As in the reference, the router's fp32 scores live in
+ * grouped_input, a row of the shape's router width (256 expert slots, or 512 past 256 experts:
+ * sq_moe_router_width) per row; a block without router rows takes the caller's scores from there. The expert passes
+ * read the input rows through the grouped routes, so grouped_input holds nothing else. */
 typedef struct sq_moe_scratch {
   sq_buffer selected_experts, routing_weights, tile_descriptors, tile_count, grouped_routes, route_rows,
       grouped_input, expert_intermediate, expert_output;
 } sq_moe_scratch;
-/* scores: the router's fp32 [rows][score_stride] logits (the router projection is the caller's). residual may be a
- * NULL view (zeros). */
+/* MoeBuffers (MoE.hpp:375-385). residual may be a NULL view (zeros). verify_rows: a verify step's live rows per lane
+ * of 8 rows, a uint32 per lane (ceil(rows / 8) of them); routed routes of rows past their lane's count are grouped
+ * into no tile, their route_rows are ~0u and the combine adds nothing for them, so such a row's output is its
+ * residual plus its shared slices' routes (moe_group_routes_verified, moe.metal:164-173,196-236, 496). A NULL view:
+ * every row routes. Decode plans only. */
 typedef struct sq_moe_buffers {
-  sq_buffer input, scores, residual, output;
-  uint32_t score_stride;
+  sq_buffer input, residual, output;
   sq_moe_scratch scratch;
+  sq_buffer verify_rows;
 } sq_moe_buffers;
 
-/* MoE::prefillPlan / decodePlan (MoE.cpp:204-223; MoePlan, MoE.hpp:349-373). A decode plan
- * takes any 1..32 rows (the reference's lanes * 8 among them); a prefill plan up to 2048. */
-int sq_moe_prefill_plan(const sq_moe_shape *shape, uint32_t rows, sq_moe_plan *out);
-int sq_moe_decode_plan(const sq_moe_shape *shape, uint32_t rows, sq_moe_plan *out);
+/* The policy a plan takes when its config is NULL (ExecutionPlans::moeConfig, ExecutionPlans.cpp:56-65): Staged tiles,
+ * 8-row tiles in decode and, in prefill, 8-row tiles while rows * top_k <= experts, else 32 (moeGgufPrefillTile,
+ * MoE.hpp:321-330). phase is SQ_PHASE_*. */
+int sq_moe_config_for(const sq_moe_shape *shape, uint32_t rows, uint32_t phase, sq_moe_config *out);
+/* MoE::prefillPlan(shape, rows, config) (MoE.cpp:561-565): rows 1..2048. config NULL takes sq_moe_config_for's. */
+int sq_moe_prefill_plan(const sq_moe_shape *shape, uint32_t rows, const sq_moe_config *config, sq_moe_plan *out);
+/* MoE::decodePlan(shape, lanes, config) (MoE.cpp:567-571): lanes 1..4 of 8 rows each, 8-row tiles. */
+int sq_moe_decode_plan(const sq_moe_shape *shape, uint32_t lanes, const sq_moe_config *config, sq_moe_plan *out);
+/* No counterpart in the reference: a decode plan of any 1..32 rows (the reference's decode rows are lanes * 8). */
+int sq_moe_decode_rows_plan(const sq_moe_shape *shape, uint32_t rows, sq_moe_plan *out);
+/* MoeShape::routerWidth (MoE.hpp:94-96): the fp32 scores a row of the router scores holds. */
+uint32_t sq_moe_router_width(const sq_moe_shape *shape);
 /* MoE::add = addRouting then addRouted (MoE.cpp:225-525). */
 int sq_moe_add(void *graph, const sq_moe_buffers *buffers, const sq_moe_weights *weights, const sq_moe_plan *plan);
 int sq_moe_add_routing(void *graph, const sq_moe_buffers *buffers, const sq_moe_weights *weights,

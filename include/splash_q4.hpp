@@ -23,6 +23,7 @@ using LinearScratchSize = sq_linear_scratch_size;
 using LinearBuffers = sq_linear_buffers;
 using MoeShape = sq_moe_shape;
 using MoePlan = sq_moe_plan;
+using MoeConfig = sq_moe_config;
 using MoeWeights = sq_moe_weights;
 using MoeBuffers = sq_moe_buffers;
 using PreparedInput = sq_prepared_input;
@@ -165,16 +166,23 @@ inline void addGgufFloat(Graph graph, Buffer input, const QuantizedSegment &weig
   check(sq_float_add(graph, input, &weights, output, rows, outStride, outOffset, destination));
 }
 
+// MoE (MoE.hpp:387-423). The config the reference's execution plans derive (ExecutionPlans::moeConfig) is
+// MoE::config's here.
 class MoE final {
  public:
-  [[nodiscard]] static MoePlan prefillPlan(const MoeShape &shape, uint32_t rows) {
-    MoePlan out{};
-    check(sq_moe_prefill_plan(&shape, rows, &out));
+  [[nodiscard]] static MoeConfig config(const MoeShape &shape, uint32_t rows, uint32_t phase) {
+    MoeConfig out{};
+    check(sq_moe_config_for(&shape, rows, phase, &out));
     return out;
   }
-  [[nodiscard]] static MoePlan decodePlan(const MoeShape &shape, uint32_t rows) {
+  [[nodiscard]] static MoePlan prefillPlan(const MoeShape &shape, uint32_t rows, const MoeConfig &config) {
     MoePlan out{};
-    check(sq_moe_decode_plan(&shape, rows, &out));
+    check(sq_moe_prefill_plan(&shape, rows, &config, &out));
+    return out;
+  }
+  [[nodiscard]] static MoePlan decodePlan(const MoeShape &shape, uint32_t lanes, const MoeConfig &config) {
+    MoePlan out{};
+    check(sq_moe_decode_plan(&shape, lanes, &config, &out));
     return out;
   }
   void add(Graph graph, const MoeBuffers &buffers, const MoeWeights &weights, const MoePlan &plan) const {

@@ -625,47 +625,57 @@ double sqo_cpu_matmul(uint32_t fmt, uint32_t M, uint32_t N, uint32_t K, const ui
 
 static double sqo_sigmoid(double x) { return 1.0 / (1.0 + exp(-x)); }
 
-/* moe_route_select (moe.metal:23-104): ranks by descending score, the lower expert id among equal scores. Softmax
- * (router 0): weight of rank r = exp(s_r - s_0) / sum_j exp(s_j - s_0) over the selected k; SigmoidNormalized
- * (router 1): sigmoid(s_r) / (sum_j sigmoid(s_j) + 1e-20). In fp64. Rows of `per_row` routes, the routed top_k
- * first (the caller fills the shared slices' routes after them). */
+/* moe_route_select (moe.metal:23-104): rank by rank, the highest remaining score wins and the lower expert id among
+ * equal scores. A selected expert's score becomes -inf. Scores compare as the kernel's strict `score > best` from a
+ * best of -inf does: a NaN never wins, and when no score above -inf is left expert 0 wins (moe.metal:77-93, where
+ * every lane then offers its first slot and the lowest lane is expert 0), so an all-NaN row selects expert 0 k
+ * times. Softmax (router 0): weight of rank r = exp(s_r - s_0) / sum_j exp(s_j - s_0) over the selected k, the s the
+ * ranks' winning scores; SigmoidNormalized (router 1): sigmoid(s_r) / (sum_j sigmoid(s_j) + 1e-20). In fp64. Rows
+ * of `per_row` routes, the routed top_k first (the caller fills the shared slices' routes after them). */
 void sqo_route_select(uint32_t rows, uint32_t experts, uint32_t top_k, uint32_t router, uint32_t per_row,
                       const float *scores, uint32_t *selected, double *weights) {
-  unsigned char *taken = (unsigned char *)malloc(experts);
+  float *left = (float *)malloc(sizeof(float) * experts);
+  double *ordered = (double *)malloc(sizeof(double) * (top_k ? top_k : 1));
   for (uint32_t r = 0; r < rows; ++r) {
-    const float *s = scores + (size_t)r * experts;
     uint32_t *sel = selected + (size_t)r * per_row;
     double *w = weights + (size_t)r * per_row;
-    memset(taken, 0, experts);
+    memcpy(left, scores + (size_t)r * experts, sizeof(float) * experts);
     for (uint32_t rank = 0; rank < top_k; ++rank) {
-      uint32_t best = experts;
+      float top = -INFINITY;
+      uint32_t best = 0;
       for (uint32_t e = 0; e < experts; ++e)
-        if (!taken[e] && (best == experts || s[e] > s[best])) best = e;
-      taken[best] = 1;
+        if (left[e] > top) top = left[e], best = e;   /* strict: the first (lowest) id of the top score */
+      left[best] = -INFINITY;
       sel[rank] = best;
+      ordered[rank] = top;
     }
-    const double top = s[sel[0]];
     double denominator = 0;
     for (uint32_t rank = 0; rank < top_k; ++rank)
-      denominator += router ? sqo_sigmoid(s[sel[rank]]) : exp((double)s[sel[rank]] - top);
+      denominator += router ? sqo_sigmoid(ordered[rank]) : exp(ordered[rank] - ordered[0]);
     if (router) denominator += 1e-20;
     for (uint32_t rank = 0; rank < top_k; ++rank)
-      w[rank] = (router ? sqo_sigmoid(s[sel[rank]]) : exp((double)s[sel[rank]] - top)) / denominator;
+      w[rank] = (router ? sqo_sigmoid(ordered[rank]) : exp(ordered[rank] - ordered[0])) / denominator;
   }
-  free(taken);
+  free(ordered);
+  free(left);
 }
 
 /* moe_group_routes_phase (moe.metal:184-278): count per expert, exclusive prefix of the experts' tiles in expert
  * order, then each expert's routes in route order over its tiles; the `shared` slices' tiles follow, slice after
- * slice, each holding every row in order. Rows hold top_k + shared routes, the routed ones first. */
+ * slice, each holding every row in order. Rows hold top_k + shared routes, the routed ones first. With verify_rows
+ * (the verified grouping, moe.metal:164-173 moe_unverified_route): a routed route of row r is left out when
+ * r % lane_rows >= verify_rows[r / lane_rows]; it takes no grouped row and its route row is ~0u. The shared slices
+ * route every row either way. */
 uint32_t sqo_group_routes(uint32_t rows, uint32_t top_k, uint32_t shared, uint32_t experts, uint32_t tile_rows,
-                          const uint32_t *selected, uint32_t *tiles, uint32_t *grouped_routes, uint32_t *route_rows) {
+                          const uint32_t *selected, const uint32_t *verify_rows, uint32_t lane_rows, uint32_t *tiles,
+                          uint32_t *grouped_routes, uint32_t *route_rows) {
   const uint32_t per_row = top_k + shared, routes = rows * per_row;
   uint32_t *count = (uint32_t *)calloc(experts, sizeof(uint32_t));
   uint32_t *offset = (uint32_t *)calloc(experts, sizeof(uint32_t));
   uint32_t *cursor = (uint32_t *)calloc(experts, sizeof(uint32_t));
+#define SQO_UNVERIFIED(r) (verify_rows && ((r) / per_row) % lane_rows >= verify_rows[((r) / per_row) / lane_rows])
   for (uint32_t r = 0; r < routes; ++r)
-    if (r % per_row < top_k) ++count[selected[r]];
+    if (r % per_row < top_k && !SQO_UNVERIFIED(r)) ++count[selected[r]];
   uint32_t total = 0;
   for (uint32_t e = 0; e < experts; ++e) {
     offset[e] = total;
@@ -680,6 +690,10 @@ uint32_t sqo_group_routes(uint32_t rows, uint32_t top_k, uint32_t shared, uint32
   for (uint32_t i = 0; i < (total + shared * shared_tiles) * tile_rows; ++i) grouped_routes[i] = ~0u;
   for (uint32_t r = 0; r < routes; ++r) {
     if (r % per_row >= top_k) continue;
+    if (SQO_UNVERIFIED(r)) {
+      route_rows[r] = ~0u;
+      continue;
+    }
     const uint32_t e = selected[r], row = offset[e] * tile_rows + cursor[e]++;
     grouped_routes[row] = r;
     route_rows[r] = row;
@@ -696,6 +710,7 @@ uint32_t sqo_group_routes(uint32_t rows, uint32_t top_k, uint32_t shared, uint32
       route_rows[r] = g;
     }
   }
+#undef SQO_UNVERIFIED
   total += shared * shared_tiles;
   free(count);
   free(offset);

@@ -89,7 +89,8 @@ void sqo_route_select(uint32_t rows, uint32_t experts, uint32_t top_k, uint32_t 
  * tiles of every row; returns the tile count. tiles: 2 uint32 per tile (expert, live rows); grouped_routes
  * [tiles * tile_rows] (~0u padding); route_rows [rows * (top_k + shared)]. */
 uint32_t sqo_group_routes(uint32_t rows, uint32_t top_k, uint32_t shared, uint32_t experts, uint32_t tile_rows,
-                          const uint32_t *selected, uint32_t *tiles, uint32_t *grouped_routes, uint32_t *route_rows);
+                          const uint32_t *selected, const uint32_t *verify_rows, uint32_t lane_rows, uint32_t *tiles,
+                          uint32_t *grouped_routes, uint32_t *route_rows);
 
 #ifdef __cplusplus
 }

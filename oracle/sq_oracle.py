@@ -191,8 +191,13 @@ def route_select(scores: np.ndarray, top_k: int, router: int = ROUTER_SOFTMAX, s
     return selected, weights
 
 
-def group_routes(selected: np.ndarray, experts: int, tile_rows: int, shared: int = 0):
-    """moe_group_routes_phase (moe.metal:184-278) over rows of top_k routed then `shared` shared routes."""
+LANE_ROWS = 8
+
+
+def group_routes(selected: np.ndarray, experts: int, tile_rows: int, shared: int = 0, verify_rows=None):
+    """moe_group_routes_phase (moe.metal:184-278) over rows of top_k routed then `shared` shared routes; with
+    verify_rows (a live-row count per lane of LANE_ROWS rows) the verified grouping, which leaves the routed routes of
+    rows past their lane's count out (route row ~0u)."""
     rows, per_row = selected.shape
     top_k = per_row - shared
     routed = rows * top_k
@@ -200,8 +205,10 @@ def group_routes(selected: np.ndarray, experts: int, tile_rows: int, shared: int
     tiles = np.zeros((max_tiles, 2), np.uint32)
     grouped = np.zeros(max_tiles * tile_rows, np.uint32)
     route_rows = np.zeros(rows * per_row, np.uint32)
+    verify = None if verify_rows is None else np.ascontiguousarray(verify_rows, np.uint32)
     count = lib().sqo_group_routes(rows, top_k, shared, experts, tile_rows,
                                    _ptr(np.ascontiguousarray(selected), c_uint32),
+                                   None if verify is None else _ptr(verify, c_uint32), LANE_ROWS,
                                    _ptr(tiles, c_uint32), _ptr(grouped, c_uint32), _ptr(route_rows, c_uint32))
     return tiles[:count], grouped[:count * tile_rows], route_rows
 

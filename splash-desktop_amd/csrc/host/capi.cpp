@@ -39,6 +39,10 @@ template <class T> const T &need(const T *p, const char *what) {
   if (!p) throw std::invalid_argument(std::string(what) + " is null");
   return *p;
 }
+template <class T> T *need(T *p, const char *what) {
+  if (!p) throw std::invalid_argument(std::string(what) + " is null");
+  return p;
+}
 
 QuantizedSegment segment(const sq_segment &s) {
   QuantizedSegment q = QuantizedSegment::planes(s.format_id, s.output_size, s.input_size, buf(s.plane0), buf(s.plane1),
@@ -88,7 +92,7 @@ LinearPlan plan(const sq_linear_plan &p) {
   return Linear::plan(workload(p.workload), config(p.config), FloatOutput(p.destination));
 }
 Linear linear(const sq_device *d) { return Linear(DeviceCapabilities{d ? d->compute_units : 0}); }
-LinearScratch scratch(const sq_linear_scratch *s) {
+LinearScratch linearScratch(const sq_linear_scratch *s) {
   if (!s) return {};
   return {buf(s->input), buf(s->sums), buf(s->partials), buf(s->counters), buf(s->rotated)};
 }
@@ -181,7 +185,7 @@ int sq_linear_add_prepared(void *graph, const sq_linear_buffers *b, const sq_pro
                            const sq_projection *gate, sq_prepared_input *result) {
   return guarded([&] {
     const sq_linear_buffers &bb = need(b, "buffers");
-    LinearBuffers buffers{buf(bb.input), buf(bb.output), buf(bb.residual), buf(bb.gate_scratch), scratch(&bb.scratch),
+    LinearBuffers buffers{buf(bb.input), buf(bb.output), buf(bb.residual), buf(bb.gate_scratch), linearScratch(&bb.scratch),
                           prepared(bb.prepared)};
     const Projection proj = projection(need(p, "projection"));
     const LinearPlan selected = plan(need(lp, "plan"));
@@ -213,7 +217,7 @@ int sq_norm_add_rms(void *graph, sq_buffer input, const sq_norm_weights *weight,
     if (layout > SQ_LINEAR_INPUT_HALF_ROWS) throw std::invalid_argument("unknown linear input layout");
     const sq_norm_weights &w = need(weight, "norm weights");
     const PreparedInput after = Normalization::addRms(stream(graph), buf(input), NormWeights{buf(w.buffer), w.float32 != 0},
-                                                      buf(output), width, rows, scratch(s), LinearInput(layout));
+                                                      buf(output), width, rows, linearScratch(s), LinearInput(layout));
     if (result) *result = cprepared(after);
   });
 }
@@ -231,14 +235,14 @@ int sq_float_add(void *graph, sq_buffer input, const sq_segment *weights, sq_buf
 int sq_linear_add_prefill(const sq_device *device, void *graph, sq_buffer input, const sq_projection *p,
                           sq_buffer output, uint32_t rows, const sq_linear_scratch *s) {
   return guarded([&] {
-    linear(device).addPrefill(stream(graph), buf(input), projection(need(p, "projection")), buf(output), rows, scratch(s));
+    linear(device).addPrefill(stream(graph), buf(input), projection(need(p, "projection")), buf(output), rows, linearScratch(s));
   });
 }
 int sq_linear_add_prefill_residual(const sq_device *device, void *graph, sq_buffer input, const sq_projection *p,
                                    sq_buffer residual, sq_buffer output, uint32_t rows, const sq_linear_scratch *s) {
   return guarded([&] {
     linear(device).addPrefillResidual(stream(graph), buf(input), projection(need(p, "projection")), buf(residual),
-                                      buf(output), rows, scratch(s));
+                                      buf(output), rows, linearScratch(s));
   });
 }
 int sq_linear_add_prefill_up_with_gate(const sq_device *device, void *graph, sq_buffer input, const sq_projection *up,
@@ -246,7 +250,7 @@ int sq_linear_add_prefill_up_with_gate(const sq_device *device, void *graph, sq_
                                        const sq_linear_scratch *s) {
   return guarded([&] {
     linear(device).addPrefillUpWithGate(stream(graph), buf(input), projection(need(up, "projection")),
-                                        buf(gate_scratch), buf(output), rows, scratch(s));
+                                        buf(gate_scratch), buf(output), rows, linearScratch(s));
   });
 }
 int sq_linear_add_prefill_swiglu(const sq_device *device, void *graph, const sq_projection *gate,
@@ -255,7 +259,7 @@ int sq_linear_add_prefill_swiglu(const sq_device *device, void *graph, const sq_
                                  sq_buffer residual, sq_buffer output, uint32_t rows) {
   return guarded([&] {
     const Projection g = projection(need(gate, "gate")), u = projection(need(up, "up")), d = projection(need(down, "down"));
-    const PrefillFfnBuffers b{buf(normalized), buf(gate_scratch), buf(intermediate), scratch(s)};
+    const PrefillFfnBuffers b{buf(normalized), buf(gate_scratch), buf(intermediate), linearScratch(s)};
     linear(device).addPrefillSwiGlu(stream(graph), {&g, &u, &d}, b, buf(residual), buf(output), rows);
   });
 }
@@ -344,6 +348,16 @@ MoeShape moeShape(const sq_moe_shape &s) {
   return {s.hidden_size, s.experts, s.experts_per_token, s.expert_intermediate_size, s.expert_format,
           MoeRouter(s.router), s.shared_slices, s.shared_gated != 0};
 }
+sq_moe_config cconfig(const MoeConfig &c) {
+  return {uint32_t(c.expertTile), uint32_t(c.ggufTile), uint32_t(c.ggufRouterTile), uint32_t(c.cpuBf16Experts)};
+}
+MoeConfig moeConfig(const sq_moe_config &c) {
+  if (c.expert_tile != SQ_MOE_EXPERT_TILE_M8 && c.expert_tile != SQ_MOE_EXPERT_TILE_M32)
+    throw std::invalid_argument("invalid MoE expert tile configuration");
+  if (c.gguf_tile > SQ_MOE_GGUF_TILE_REGISTER) throw std::invalid_argument("invalid MoE GGUF tile");
+  if (c.router_tile > SQ_FLOAT_TILE_NEURAL_ACCELERATOR) throw std::invalid_argument("invalid MoE router tile");
+  return {MoeExpertTile(c.expert_tile), MoeGgufTile(c.gguf_tile), FloatTile(c.router_tile), c.cpu_bf16_experts != 0};
+}
 sq_moe_plan cmoe(const MoePlan &p) {
   sq_moe_plan out{};
   const MoeShape s = p.shape();
@@ -353,14 +367,20 @@ sq_moe_plan cmoe(const MoePlan &p) {
   out.phase = uint32_t(p.phase());
   out.tile_rows = p.tileRows();
   out.maximum_tiles = p.maximumTiles();
+  out.config = cconfig(p.configuration());
   const MoeWorkspace &w = p.workspace();
   out.workspace = {w.selectedExperts, w.routingWeights, w.tileDescriptors, w.tileCount, w.groupedRoutes,
                    w.routeRows, w.groupedInput, w.expertIntermediate, w.expertOutput};
   return out;
 }
+// The plan a caller holds, rebuilt and checked: the same shape, rows, phase and config give the same plan.
 MoePlan moePlan(const sq_moe_plan &p) {
   if (p.phase > SQ_PHASE_DECODE) throw std::invalid_argument("invalid MoE phase");
-  return p.phase == SQ_PHASE_DECODE ? MoE::decodeRows(moeShape(p.shape), p.rows) : MoE::prefillPlan(moeShape(p.shape), p.rows);
+  const MoePlan plan(moeShape(p.shape), p.rows, moeConfig(p.config),
+                     p.phase == SQ_PHASE_DECODE ? MoePhase::Decode : MoePhase::Prefill);
+  if (plan.tileRows() != p.tile_rows || plan.maximumTiles() != p.maximum_tiles)
+    throw std::invalid_argument("MoE plan fields do not match its shape, rows and config");
+  return plan;
 }
 // The shared views are read only when the plan has shared slices.
 MoeWeights moeWeights(const sq_moe_weights &w, const sq_moe_plan &p) {
@@ -378,29 +398,64 @@ MoeWeights moeWeights(const sq_moe_weights &w, const sq_moe_plan &p) {
 }
 MoeBuffers moeBuffers(const sq_moe_buffers &b) {
   const sq_moe_scratch &s = b.scratch;
-  return {buf(b.input), buf(b.scores), buf(b.residual), buf(b.output), b.score_stride,
+  return {buf(b.input), buf(b.residual), buf(b.output),
           MoeScratch{buf(s.selected_experts), buf(s.routing_weights), buf(s.tile_descriptors), buf(s.tile_count),
                      buf(s.grouped_routes), buf(s.route_rows), buf(s.grouped_input), buf(s.expert_intermediate),
-                     buf(s.expert_output)}};
+                     buf(s.expert_output)},
+          buf(b.verify_rows)};
 }
 }  // namespace
 
 extern "C" {
 
-int sq_moe_prefill_plan(const sq_moe_shape *shape, uint32_t rows, sq_moe_plan *out) {
-  return guarded([&] { *out = cmoe(MoE::prefillPlan(moeShape(need(shape, "shape")), rows)); });
+int sq_moe_config_for(const sq_moe_shape *shape, uint32_t rows, uint32_t phase, sq_moe_config *out) {
+  return guarded([&] {
+    if (phase > SQ_PHASE_DECODE) throw std::invalid_argument("invalid MoE phase");
+    *need(out, "config") = cconfig(MoE::config(moeShape(need(shape, "shape")), rows,
+                                               phase == SQ_PHASE_DECODE ? MoePhase::Decode : MoePhase::Prefill));
+  });
 }
-int sq_moe_decode_plan(const sq_moe_shape *shape, uint32_t rows, sq_moe_plan *out) {
-  return guarded([&] { *out = cmoe(MoE::decodeRows(moeShape(need(shape, "shape")), rows)); });
+int sq_moe_prefill_plan(const sq_moe_shape *shape, uint32_t rows, const sq_moe_config *config, sq_moe_plan *out) {
+  return guarded([&] {
+    const MoeShape s = moeShape(need(shape, "shape"));
+    *need(out, "plan") =
+        cmoe(MoE::prefillPlan(s, rows, config ? moeConfig(*config) : MoE::config(s, rows, MoePhase::Prefill)));
+  });
 }
+int sq_moe_decode_plan(const sq_moe_shape *shape, uint32_t lanes, const sq_moe_config *config, sq_moe_plan *out) {
+  return guarded([&] {
+    const MoeShape s = moeShape(need(shape, "shape"));
+    const MoeConfig c = config ? moeConfig(*config) : MoE::config(s, lanes * SQ_TARGET_VERIFY_ROWS, MoePhase::Decode);
+    *need(out, "plan") = cmoe(MoE::decodePlan(s, lanes, c));
+  });
+}
+int sq_moe_decode_rows_plan(const sq_moe_shape *shape, uint32_t rows, sq_moe_plan *out) {
+  return guarded([&] { *need(out, "plan") = cmoe(MoE::decodeRows(moeShape(need(shape, "shape")), rows)); });
+}
+uint32_t sq_moe_router_width(const sq_moe_shape *shape) {
+  if (!shape) return 0;
+  MoeShape s;
+  s.experts = shape->experts;
+  return s.routerWidth();
+}
+// Each MoE call rebuilds and checks the plan before it reads the buffers or weights.
 int sq_moe_add(void *graph, const sq_moe_buffers *b, const sq_moe_weights *w, const sq_moe_plan *p) {
-  return guarded([&] { MoE::add(stream(graph), moeBuffers(need(b, "buffers")), moeWeights(need(w, "weights"), need(p, "plan")), moePlan(need(p, "plan"))); });
+  return guarded([&] {
+    const MoePlan plan = moePlan(need(p, "plan"));
+    MoE::add(stream(graph), moeBuffers(need(b, "buffers")), moeWeights(need(w, "weights"), *p), plan);
+  });
 }
 int sq_moe_add_routing(void *graph, const sq_moe_buffers *b, const sq_moe_weights *w, const sq_moe_plan *p) {
-  return guarded([&] { MoE::addRouting(stream(graph), moeBuffers(need(b, "buffers")), moeWeights(need(w, "weights"), need(p, "plan")), moePlan(need(p, "plan"))); });
+  return guarded([&] {
+    const MoePlan plan = moePlan(need(p, "plan"));
+    MoE::addRouting(stream(graph), moeBuffers(need(b, "buffers")), moeWeights(need(w, "weights"), *p), plan);
+  });
 }
 int sq_moe_add_routed(void *graph, const sq_moe_buffers *b, const sq_moe_weights *w, const sq_moe_plan *p) {
-  return guarded([&] { MoE::addRouted(stream(graph), moeBuffers(need(b, "buffers")), moeWeights(need(w, "weights"), need(p, "plan")), moePlan(need(p, "plan"))); });
+  return guarded([&] {
+    const MoePlan plan = moePlan(need(p, "plan"));
+    MoE::addRouted(stream(graph), moeBuffers(need(b, "buffers")), moeWeights(need(w, "weights"), *p), plan);
+  });
 }
 
 }  // extern "C"

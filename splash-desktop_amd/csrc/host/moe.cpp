@@ -11,16 +11,19 @@ void launched(hipError_t e, const char *what) {
   if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
 
-// MoE.cpp:64-84: the grouped rows' intermediates and outputs; the gather reads the input rows
-// straight from the routes, so the grouped input holds nothing.
+// MoE.cpp:64-84: the grouped rows' intermediates and outputs. The expert passes read the input rows straight through
+// the routes, so the grouped input holds only the router's fp32 scores, a row of routerWidth() per row, as the
+// reference parks them there until its gather overwrites them.
 MoeWorkspace workspaceFor(const MoeShape &shape, uint32_t rows, uint32_t tileRows) {
   if (!shape.valid()) throw std::invalid_argument("invalid MoE workspace shape");
   const uint64_t routes = uint64_t{rows} * shape.routesPerToken();
   const uint32_t tiles = moeMaximumTiles(rows, shape, tileRows);
   const uint64_t groupedRows = uint64_t{tiles} * tileRows;
   const uint32_t widest = std::max(shape.hiddenSize, shape.expertIntermediateSize);
+  const uint64_t scoreBytes = uint64_t{rows} * shape.routerWidth() * 4;
   return {routes * 4, routes * 4, uint64_t{tiles} * sizeof(SqMoeTileDescriptor), sizeof(SqMoeTileCount),
-          groupedRows * 4, routes * 4, 0, groupedRows * shape.expertIntermediateSize * 2, groupedRows * widest * 2};
+          groupedRows * 4, routes * 4, scoreBytes, groupedRows * shape.expertIntermediateSize * 2,
+          groupedRows * widest * 2};
 }
 
 // A routed or shared projection: `slots` experts (slices) of n rows of k inputs, each projection in a format of its
@@ -54,9 +57,6 @@ void validate(const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
   requireBytes(b.input, hiddenRows, "MoE input");
   if (b.residual) requireBytes(b.residual, hiddenRows, "MoE residual");
   requireBytes(b.output, hiddenRows, "MoE output");
-  const uint32_t stride = b.scoreStride ? b.scoreStride : s.experts;
-  if (stride < s.experts) throw std::invalid_argument("MoE score rows are narrower than the experts");
-  requireBytes(b.scores, rowBytes(plan.rows(), stride, s.experts, 4), "MoE scores");
   const MoeWorkspace &need = plan.workspace();
   const MoeScratch &sc = b.scratch;
   requireBytes(sc.selectedExperts, need.selectedExperts, "MoE selected experts");
@@ -65,33 +65,58 @@ void validate(const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
   requireBytes(sc.tileCount, need.tileCount, "MoE tile count");
   requireBytes(sc.groupedRoutes, need.groupedRoutes, "MoE grouped routes");
   requireBytes(sc.routeRows, need.routeRows, "MoE route rows");
+  requireBytes(sc.groupedInput, need.groupedInput, "MoE grouped input");
   requireBytes(sc.expertIntermediate, need.expertIntermediate, "MoE expert intermediate");
   requireBytes(sc.expertOutput, need.expertOutput, "MoE expert output");
   // The combine moves eight bf16 a lane.
   const auto aligned = [](const Buffer &buffer) { return (reinterpret_cast<uintptr_t>(buffer.ptr) & 15u) == 0; };
   if (!aligned(b.residual) || !aligned(b.output) || !aligned(sc.expertOutput))
     throw std::invalid_argument("MoE output, residual and expert output buffers are 16-byte aligned");
+  if (b.verifyRows) {
+    // A verify step's rows are its lanes' blocks (MoE.cpp:467-475).
+    if (plan.phase() != MoePhase::Decode) throw std::invalid_argument("only a verify step's MoE routes its verify rows");
+    const uint32_t lanes = (plan.rows() + SQ_TARGET_VERIFY_ROWS - 1) / SQ_TARGET_VERIFY_ROWS;
+    requireBytes(b.verifyRows, uint64_t{lanes} * 4, "MoE verify rows");
+  }
 }
 
 }  // namespace
 
-MoePlan::MoePlan(MoeShape shape, uint32_t rows, uint32_t tileRows, MoePhase phase)
-    : shape_(shape), rows_(rows), tileRows_(tileRows), phase_(phase) {
+MoePlan::MoePlan(MoeShape shape, uint32_t rows, MoeConfig config, MoePhase phase)
+    : shape_(shape), rows_(rows), config_(config), phase_(phase) {
   if (!rows || rows > SQ_PREFILL_TOKEN_BUDGET || (phase == MoePhase::Decode && rows > SQ_MAXIMUM_DECODE_ROWS))
     throw std::invalid_argument("invalid MoE rows");
-  workspace_ = workspaceFor(shape, rows, tileRows);
-  maximumTiles_ = moeMaximumTiles(rows, shape, tileRows);
+  if (config.expertTile != MoeExpertTile::M8 && config.expertTile != MoeExpertTile::M32)
+    throw std::invalid_argument("invalid MoE expert tile configuration");
+  if (phase == MoePhase::Decode && config.expertTile != MoeExpertTile::M8)
+    throw std::invalid_argument("invalid MoE expert tile configuration");
+  if (config.ggufTile == MoeGgufTile::Register)
+    throw std::invalid_argument(
+        "the register expert tile is the reference's Apple9 tile; MI355X plans run the staged expert tiles");
+  if (config.ggufTile != MoeGgufTile::Staged) throw std::invalid_argument("invalid MoE GGUF tile");
+  if (config.ggufRouterTile != FloatTile::Simdgroup && config.ggufRouterTile != FloatTile::NeuralAccelerator)
+    throw std::invalid_argument("invalid MoE router tile");
+  workspace_ = workspaceFor(shape, rows, tileRows());
+  maximumTiles_ = moeMaximumTiles(rows, shape, tileRows());
 }
 
-MoePlan MoE::prefillPlan(MoeShape shape, uint32_t rows) {
-  const uint32_t tile = uint64_t{rows} * shape.expertsPerToken <= shape.experts ? 8 : 32;
-  return MoePlan(shape, rows, tile, MoePhase::Prefill);
+MoeConfig MoE::config(MoeShape shape, uint32_t rows, MoePhase phase) {
+  MoeConfig c;
+  if (phase == MoePhase::Prefill)
+    c.expertTile = uint64_t{rows} * shape.expertsPerToken <= shape.experts ? MoeExpertTile::M8 : MoeExpertTile::M32;
+  return c;
 }
-MoePlan MoE::decodePlan(MoeShape shape, uint32_t lanes) {
+MoePlan MoE::prefillPlan(MoeShape shape, uint32_t rows, MoeConfig config) {
+  if (!rows || rows > SQ_PREFILL_TOKEN_BUDGET) throw std::invalid_argument("invalid MoE prefill rows");
+  return MoePlan(shape, rows, config, MoePhase::Prefill);
+}
+MoePlan MoE::decodePlan(MoeShape shape, uint32_t lanes, MoeConfig config) {
   if (!lanes || lanes > SQ_MAXIMUM_BATCH_WIDTH) throw std::invalid_argument("invalid MoE decode batch width");
-  return MoePlan(shape, lanes * SQ_TARGET_VERIFY_ROWS, 8, MoePhase::Decode);
+  return MoePlan(shape, lanes * SQ_TARGET_VERIFY_ROWS, config, MoePhase::Decode);
 }
-MoePlan MoE::decodeRows(MoeShape shape, uint32_t rows) { return MoePlan(shape, rows, 8, MoePhase::Decode); }
+MoePlan MoE::decodeRows(MoeShape shape, uint32_t rows) {
+  return MoePlan(shape, rows, config(shape, rows, MoePhase::Decode), MoePhase::Decode);
+}
 
 void MoE::add(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
   validate(b, w, plan);
@@ -103,12 +128,13 @@ void MoE::addRouting(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w
   validate(b, w, plan);
   const MoeShape s = plan.shape();
   const MoeScratch &sc = b.scratch;
-  const uint32_t stride = b.scoreStride ? b.scoreStride : s.experts;
-  // The router's fp32 scores (MoE.cpp:527-543), when the block carries its rows.
+  // The router's fp32 scores in the grouped input, rows of routerWidth() (MoE.cpp:527-543), when the block carries
+  // its rows; else the caller wrote them there.
+  const uint32_t stride = s.routerWidth();
   if (w.router.plane0)
-    addGgufFloat(graph, b.input, w.router, b.scores, plan.rows(), stride, 0, FloatOutput::Float32);
+    addGgufFloat(graph, b.input, w.router, sc.groupedInput, plan.rows(), stride, 0, FloatOutput::Float32);
   const SqMoeRouteParams route{plan.rows(), s.hiddenSize, s.experts, s.expertsPerToken};
-  launched(kern::launch_moe_route_select(b.scores.as<const float>(), stride,
+  launched(kern::launch_moe_route_select(sc.groupedInput.as<const float>(), stride,
                                          sc.selectedExperts.as<uint32_t>(), sc.routingWeights.as<float>(), route,
                                          b.input.as<const uint16_t>(),
                                          s.sharedGate ? w.sharedScalarGate.as<const float>() : nullptr,
@@ -119,7 +145,8 @@ void MoE::addRouting(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w
                                SQ_TARGET_VERIFY_ROWS, 0};
   launched(kern::launch_moe_group(sc.selectedExperts.as<const uint32_t>(), sc.tileDescriptors.as<SqMoeTileDescriptor>(),
                                   sc.tileCount.as<SqMoeTileCount>(), sc.groupedRoutes.as<uint32_t>(),
-                                  sc.routeRows.as<uint32_t>(), group, s.sharedSlices, graph),
+                                  sc.routeRows.as<uint32_t>(), b.verifyRows.as<const uint32_t>(), group,
+                                  s.sharedSlices, graph),
            "MoE grouping");
 }
 

@@ -1,6 +1,6 @@
 // ops::MoE over HIP: the routed and shared experts' grouped gather-GEMM (reference: runtime/ops/MoE.hpp:19-423 and
-// runtime/ops/MoE.cpp:27-543). A step starts from fp32 router scores: the block's router rows projected by the
-// routing itself (MoeWeights::router), or the caller's.
+// runtime/ops/MoE.cpp:27-543). A step starts from fp32 router scores in the grouped-input scratch: the block's router
+// rows projected by the routing itself (MoeWeights::router), or the caller's.
 #pragma once
 #include "ops.hpp"
 
@@ -30,9 +30,24 @@ struct MoeShape {
            expertIntermediateSize % 64 == 0 && sq_format_supported(expertFormat) && compiledRouting();
   }
   [[nodiscard]] uint32_t routesPerToken() const noexcept { return expertsPerToken + sharedSlices; }
+  // routerWidth (MoE.hpp:94-96): the fp32 scores of a row of the router's output.
+  [[nodiscard]] uint32_t routerWidth() const noexcept {
+    return experts > SQ_MOE_EXPERT_SLOTS ? SQ_MOE_WIDE_EXPERT_SLOTS : SQ_MOE_EXPERT_SLOTS;
+  }
 };
 
 enum class MoePhase : uint8_t { Prefill, Decode };
+
+// MoeExpertTile, MoeGgufTile (MoE.hpp:284,297), FloatTile (Linear.hpp:33) and MoeConfig (MoE.hpp:333-346).
+enum class MoeExpertTile : uint8_t { M8 = 8, M32 = 32 };
+enum class MoeGgufTile : uint8_t { Staged, Register };
+enum class FloatTile : uint8_t { Simdgroup, NeuralAccelerator };
+struct MoeConfig {
+  MoeExpertTile expertTile = MoeExpertTile::M8;
+  MoeGgufTile ggufTile = MoeGgufTile::Staged;
+  FloatTile ggufRouterTile = FloatTile::Simdgroup;
+  bool cpuBf16Experts = false;
+};
 
 // moeMaximumTiles (MoE.hpp:200-205): every routed expert may leave one partial tile and no tile is empty; each shared
 // slice fills one tile per tileRows rows.
@@ -59,14 +74,17 @@ struct MoeWeights {
   QuantizedSegment sharedGate, sharedUp, sharedDown;
   Buffer sharedScalarGate;
   // The router (BlockMoeWeights::router, MoE.hpp:133): F32 or BF16 rows [experts][hidden]. With it the routing
-  // projects the input onto it into the scores buffer first (MoE::addRoutes, MoE.cpp:527-543); without it the
-  // scores are the caller's.
+  // projects the input onto it into the scores first (MoE::addRoutes, MoE.cpp:527-543); without it the scores are
+  // the caller's.
   QuantizedSegment router;
 };
+// MoeBuffers (MoE.hpp:375-385). The router's fp32 scores live in scratch.groupedInput, rows of routerWidth() (the
+// caller's when the block has no router rows). verifyRows: a verify step's live rows per lane of
+// SQ_TARGET_VERIFY_ROWS rows; routed routes of the rows past them go to no tile and add nothing.
 struct MoeBuffers {
-  Buffer input, scores, residual, output;
-  uint32_t scoreStride = 0;   // floats per row of scores; 0 takes the expert count
+  Buffer input, residual, output;
   MoeScratch scratch;
+  Buffer verifyRows;
 };
 
 class MoePlan {
@@ -74,25 +92,30 @@ public:
   [[nodiscard]] MoeShape shape() const noexcept { return shape_; }
   [[nodiscard]] uint32_t rows() const noexcept { return rows_; }
   [[nodiscard]] MoePhase phase() const noexcept { return phase_; }
-  [[nodiscard]] uint32_t tileRows() const noexcept { return tileRows_; }
+  [[nodiscard]] MoeConfig configuration() const noexcept { return config_; }
+  [[nodiscard]] uint32_t tileRows() const noexcept { return uint32_t(config_.expertTile); }
   [[nodiscard]] uint32_t maximumTiles() const noexcept { return maximumTiles_; }
   [[nodiscard]] const MoeWorkspace &workspace() const noexcept { return workspace_; }
-  MoePlan(MoeShape shape, uint32_t rows, uint32_t tileRows, MoePhase phase);
+  // MoePlan::MoePlan (MoE.cpp:196-206): decode plans take 8-row tiles, and the register tile is refused.
+  MoePlan(MoeShape shape, uint32_t rows, MoeConfig config, MoePhase phase);
 
 private:
   MoeShape shape_;
-  uint32_t rows_, tileRows_;
+  uint32_t rows_;
+  MoeConfig config_;
   MoePhase phase_;
   uint32_t maximumTiles_;
   MoeWorkspace workspace_;
 };
 
 struct MoE {
-  // Tiles of 8 rows while a chunk's routes average at most one row per expert, else 32 (moeGgufPrefillTile,
-  // MoE.hpp:321-330).
-  [[nodiscard]] static MoePlan prefillPlan(MoeShape shape, uint32_t rows);
-  // Decode steps of `lanes` lanes of 8 rows (MoE.cpp decodePlan) and, here, of any rows up to 32.
-  [[nodiscard]] static MoePlan decodePlan(MoeShape shape, uint32_t lanes);
+  // The device's policy (ExecutionPlans::moeConfig, ExecutionPlans.cpp:56-65): Staged tiles; in prefill 8-row tiles
+  // while a chunk's routes average at most one row per expert, else 32 (moeGgufPrefillTile, MoE.hpp:321-330); in
+  // decode 8-row tiles.
+  [[nodiscard]] static MoeConfig config(MoeShape shape, uint32_t rows, MoePhase phase);
+  [[nodiscard]] static MoePlan prefillPlan(MoeShape shape, uint32_t rows, MoeConfig config);
+  // Decode steps of `lanes` lanes of 8 rows (MoE.cpp:567-571) and, here, of any rows up to 32 on 8-row tiles.
+  [[nodiscard]] static MoePlan decodePlan(MoeShape shape, uint32_t lanes, MoeConfig config);
   [[nodiscard]] static MoePlan decodeRows(MoeShape shape, uint32_t rows);
   static void add(hipStream_t graph, const MoeBuffers &buffers, const MoeWeights &weights, const MoePlan &plan);
   static void addRouting(hipStream_t graph, const MoeBuffers &buffers, const MoeWeights &weights, const MoePlan &plan);

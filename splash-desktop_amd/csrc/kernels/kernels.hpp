@@ -104,8 +104,8 @@ hipError_t launch_moe_route_select(const float *scores, uint32_t score_stride, u
                                    float *routing_weights, const SqMoeRouteParams &params, const uint16_t *input,
                                    const float *shared_gate, uint32_t router, uint32_t shared, hipStream_t stream);
 hipError_t launch_moe_group(const uint32_t *selected, SqMoeTileDescriptor *tiles, SqMoeTileCount *tile_count,
-                            uint32_t *grouped_routes, uint32_t *route_rows, const SqMoeGroupParams &params,
-                            uint32_t shared, hipStream_t stream);
+                            uint32_t *grouped_routes, uint32_t *route_rows, const uint32_t *verify_rows,
+                            const SqMoeGroupParams &params, uint32_t shared, hipStream_t stream);
 // An expert pass over the grouped rows, tile by tile: gate_up: gate and up of each tile's expert in one pass over
 // input rows routes[row] / routes_per_row, out = bf16(bf16(up) silu(bf16(gate))); else one tensor, over those input
 // rows when `gather` (a gate or up of its own format) and over the grouped input rows otherwise, out = bf16(y), or

@@ -63,19 +63,24 @@ __global__ __launch_bounds__(64) void route_select_kernel(const float *scores, u
     v[i] = e < p.experts ? scores[(size_t)row * stride + e] : -INFINITY;
   }
   __shared__ float ordered[64];
-  uint32_t taken = 0;   // bit i: expert lane + 64 i already selected
+  // A lane's best starts at -inf in its first slot and moves only to a strictly greater score, so a NaN score never
+  // becomes a lane's best and the wave maximum sees no NaN; a taken expert's score becomes -inf (moe.metal:77-93).
+  // Every lane offers at least its first slot, so the winner is always an expert id below `experts`: when no finite
+  // score is left, every lane's best is -inf and lane 0's expert 0 wins (the reference's choice too).
   for (uint32_t rank = 0; rank < p.top_k; ++rank) {
     float best = -INFINITY;
-    int at = -1;
+    int at = 0;
 #pragma unroll
     for (int i = 0; i < kPer; ++i)
-      if (lane + 64u * i < p.experts && !((taken >> i) & 1u) && (at < 0 || v[i] > best)) best = v[i], at = i;
+      if (v[i] > best) best = v[i], at = i;
     const float top = __uint_as_float(wave_reduce(__float_as_uint(best), [](uint32_t a, uint32_t b) {
       return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
     }));
-    const uint32_t candidate = at >= 0 && best == top ? lane + 64u * at : 0xFFFFFFFFu;
+    const uint32_t candidate = best == top ? lane + 64u * at : 0xFFFFFFFFu;
     const uint32_t winner = wave_reduce(candidate, [](uint32_t a, uint32_t b) { return min(a, b); });
-    if (candidate == winner && at >= 0) taken |= 1u << at;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+      if (candidate == winner && i == at) v[i] = -INFINITY;
     if (lane == 0) {
       selected[base + rank] = winner;
       ordered[rank] = top;
@@ -99,9 +104,13 @@ __global__ __launch_bounds__(64) void route_select_kernel(const float *scores, u
 // order (a bitmap of the rows that route to each expert, 512 rows at a time, gives a route's rank), so the
 // grouping, and every expert pass after it, is deterministic. The `shared` slices' tiles follow the routed tiles,
 // slice after slice, each slice's holding every row in order (route row * (top_k + shared) + top_k + slice).
+// With verify_rows (a verify step: a live-row count per lane of lane_rows rows) the routed routes of a row past its
+// lane's count are grouped into no tile and their route_rows are ~0u (moe_group_routes_verified,
+// moe.metal:164-173); the shared slices still hold every row.
 __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, SqMoeTileDescriptor *tiles,
                                                     SqMoeTileCount *tile_count, uint32_t *grouped_routes,
-                                                    uint32_t *route_rows, SqMoeGroupParams p, uint32_t shared) {
+                                                    uint32_t *route_rows, const uint32_t *verify_rows,
+                                                    SqMoeGroupParams p, uint32_t shared) {
   constexpr uint32_t kChunk = 512, kWords = kChunk / 32;
   __shared__ uint32_t counts[SQ_MOE_WIDE_EXPERT_SLOTS], offsets[SQ_MOE_WIDE_EXPERT_SLOTS],
       running[SQ_MOE_WIDE_EXPERT_SLOTS];
@@ -110,10 +119,18 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
   const uint32_t tid = threadIdx.x, per_row = p.top_k + shared, tr = p.tile_rows;
   // Routed route k of row r: selected[r * per_row + k].
   const auto route_of = [&](uint32_t i) { return i / p.top_k * per_row + i % p.top_k; };
+  // The route select writes expert ids below `experts` only; the clamp keeps a corrupted selection inside the
+  // tables below.
+  const auto expert_of = [&](uint32_t i) { return min(selected[route_of(i)], p.experts - 1u); };
+  const auto dead = [&](uint32_t i) {
+    const uint32_t row = i / p.top_k;
+    return verify_rows != nullptr && row % p.lane_rows >= verify_rows[row / p.lane_rows];
+  };
   counts[tid] = 0;
   running[tid] = 0;
   __syncthreads();
-  for (uint32_t i = tid; i < p.rows * p.top_k; i += 512) atomicAdd(&counts[selected[route_of(i)]], 1u);
+  for (uint32_t i = tid; i < p.rows * p.top_k; i += 512)
+    if (!dead(i)) atomicAdd(&counts[expert_of(i)], 1u);
   __syncthreads();
   {
     // Exclusive prefix of the experts' tile counts: a scan within each wave, then over the eight wave totals.
@@ -138,36 +155,55 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
     for (uint32_t t = 0; t < n; ++t) tiles[first + t] = SqMoeTileDescriptor{tid, min(tr, c - t * tr)};
     for (uint32_t row = first * tr + c; row < (first + n) * tr; ++row) grouped_routes[row] = ~0u;
   }
+  __shared__ uint32_t duplicated;
   for (uint32_t chunk = 0; chunk < p.rows; chunk += kChunk) {
     for (uint32_t i = tid; i < p.experts * kWords; i += 512) bits[i] = 0;
+    if (tid == 0) duplicated = 0;
     __syncthreads();
     const uint32_t i0 = chunk * p.top_k, i1 = min(p.rows, chunk + kChunk) * p.top_k;
     for (uint32_t i = i0 + tid; i < i1; i += 512) {
-      const uint32_t local = i / p.top_k - chunk;
-      atomicOr(&bits[selected[route_of(i)] * kWords + local / 32], 1u << (local % 32));
+      if (dead(i)) {
+        route_rows[route_of(i)] = ~0u;
+        continue;
+      }
+      const uint32_t local = i / p.top_k - chunk, bit = 1u << (local % 32);
+      // A bit already set names another route of the same row to the same expert: a row with fewer scores above
+      // -inf than top_k routes (an all-NaN row selects expert 0 at every rank). Such a chunk is ranked serially.
+      if (atomicOr(&bits[expert_of(i) * kWords + local / 32], bit) & bit) duplicated = 1;
     }
     __syncthreads();
-    // Rows of the chunk before word w that route to expert e: one pass per expert, then each route's rank is a
-    // table read and one population count.
-    if (tid < p.experts) {
-      uint32_t before = 0;
-      for (uint32_t w = 0; w < kWords; ++w) {
-        prefix[tid * kWords + w] = before;
-        before += __popc(bits[tid * kWords + w]);
+    if (!duplicated) {
+      // Rows of the chunk before word w that route to expert e: one pass per expert, then each route's rank is a
+      // table read and one population count.
+      if (tid < p.experts) {
+        uint32_t before = 0;
+        for (uint32_t w = 0; w < kWords; ++w) {
+          prefix[tid * kWords + w] = before;
+          before += __popc(bits[tid * kWords + w]);
+        }
+      }
+      __syncthreads();
+      for (uint32_t i = i0 + tid; i < i1; i += 512) {
+        if (dead(i)) continue;
+        const uint32_t r = route_of(i), e = expert_of(i), local = i / p.top_k - chunk;
+        uint32_t rank = running[e] + prefix[e * kWords + local / 32];
+        rank += __popc(bits[e * kWords + local / 32] & ((1u << (local % 32)) - 1u));
+        const uint32_t row = offsets[e] * tr + rank;
+        grouped_routes[row] = r;
+        route_rows[r] = row;
+      }
+      __syncthreads();
+      if (tid < p.experts)
+        for (uint32_t w = 0; w < kWords; ++w) running[tid] += __popc(bits[tid * kWords + w]);
+    } else if (tid < p.experts) {
+      // Thread e takes its expert's routes of the chunk in route order.
+      for (uint32_t i = i0; i < i1; ++i) {
+        if (dead(i) || expert_of(i) != tid) continue;
+        const uint32_t r = route_of(i), row = offsets[tid] * tr + running[tid]++;
+        grouped_routes[row] = r;
+        route_rows[r] = row;
       }
     }
-    __syncthreads();
-    for (uint32_t i = i0 + tid; i < i1; i += 512) {
-      const uint32_t r = route_of(i), e = selected[r], local = i / p.top_k - chunk;
-      uint32_t rank = running[e] + prefix[e * kWords + local / 32];
-      rank += __popc(bits[e * kWords + local / 32] & ((1u << (local % 32)) - 1u));
-      const uint32_t row = offsets[e] * tr + rank;
-      grouped_routes[row] = r;
-      route_rows[r] = row;
-    }
-    __syncthreads();
-    if (tid < p.experts)
-      for (uint32_t w = 0; w < kWords; ++w) running[tid] += __popc(bits[tid * kWords + w]);
     __syncthreads();
   }
   // Shared slices (moe.metal:245-270): slice s's tiles after slice s - 1's, each of every row in order.
@@ -382,10 +418,10 @@ hipError_t launch_moe_route_select(const float *scores, uint32_t stride, uint32_
 }
 
 hipError_t launch_moe_group(const uint32_t *selected, SqMoeTileDescriptor *tiles, SqMoeTileCount *tile_count,
-                            uint32_t *grouped_routes, uint32_t *route_rows, const SqMoeGroupParams &p,
-                            uint32_t shared, hipStream_t stream) {
+                            uint32_t *grouped_routes, uint32_t *route_rows, const uint32_t *verify_rows,
+                            const SqMoeGroupParams &p, uint32_t shared, hipStream_t stream) {
   hipLaunchKernelGGL(group_kernel, dim3(1), dim3(512), 0, stream, selected, tiles, tile_count, grouped_routes,
-                     route_rows, p, shared);
+                     route_rows, verify_rows, p, shared);
   return hipGetLastError();
 }
 

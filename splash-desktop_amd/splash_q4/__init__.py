@@ -108,9 +108,18 @@ class MoeWorkspace(Structure):
     _fields_ = [(n, c_uint64) for n in _MOE_WORKSPACE]
 
 
+MOE_EXPERT_TILE_M8, MOE_EXPERT_TILE_M32 = 8, 32
+MOE_GGUF_TILE_STAGED, MOE_GGUF_TILE_REGISTER = 0, 1
+FLOAT_TILE_SIMDGROUP, FLOAT_TILE_NEURAL_ACCELERATOR = 0, 1
+
+
+class MoeConfig(Structure):
+    _fields_ = [(n, c_uint32) for n in ("expert_tile", "gguf_tile", "router_tile", "cpu_bf16_experts")]
+
+
 class MoePlan(Structure):
     _fields_ = [("shape", MoeShape), ("rows", c_uint32), ("phase", c_uint32), ("tile_rows", c_uint32),
-                ("maximum_tiles", c_uint32), ("workspace", MoeWorkspace)]
+                ("maximum_tiles", c_uint32), ("config", MoeConfig), ("workspace", MoeWorkspace)]
 
 
 class MoeWeights(Structure):
@@ -124,8 +133,8 @@ class MoeScratch(Structure):
 
 
 class MoeBuffers(Structure):
-    _fields_ = [("input", Buffer), ("scores", Buffer), ("residual", Buffer), ("output", Buffer),
-                ("score_stride", c_uint32), ("scratch", MoeScratch)]
+    _fields_ = [("input", Buffer), ("residual", Buffer), ("output", Buffer), ("scratch", MoeScratch),
+                ("verify_rows", Buffer)]
 
 
 class SqError(RuntimeError):
@@ -174,8 +183,11 @@ _SIGNATURES = {
     "sq_mlx_repack": [c_void_p, c_uint32, c_uint32, c_uint32, Buffer, Buffer, Buffer, Buffer, Buffer],
     "sq_dequant": [c_void_p, POINTER(Segment), Buffer, Buffer],
     "sq_diag_stream_read": [c_void_p, Buffer, Buffer, c_uint32, c_uint32],
-    "sq_moe_prefill_plan": [POINTER(MoeShape), c_uint32, POINTER(MoePlan)],
-    "sq_moe_decode_plan": [POINTER(MoeShape), c_uint32, POINTER(MoePlan)],
+    "sq_moe_config_for": [POINTER(MoeShape), c_uint32, c_uint32, POINTER(MoeConfig)],
+    "sq_moe_prefill_plan": [POINTER(MoeShape), c_uint32, POINTER(MoeConfig), POINTER(MoePlan)],
+    "sq_moe_decode_plan": [POINTER(MoeShape), c_uint32, POINTER(MoeConfig), POINTER(MoePlan)],
+    "sq_moe_decode_rows_plan": [POINTER(MoeShape), c_uint32, POINTER(MoePlan)],
+    "sq_moe_router_width": [POINTER(MoeShape)],
     "sq_moe_add": [c_void_p, POINTER(MoeBuffers), POINTER(MoeWeights), POINTER(MoePlan)],
     "sq_moe_add_routing": [c_void_p, POINTER(MoeBuffers), POINTER(MoeWeights), POINTER(MoePlan)],
     "sq_moe_add_routed": [c_void_p, POINTER(MoeBuffers), POINTER(MoeWeights), POINTER(MoePlan)],
@@ -192,7 +204,8 @@ def lib() -> ctypes.CDLL:
         for name, args in _SIGNATURES.items():
             fn = getattr(handle, name)
             fn.argtypes = args
-            fn.restype = c_char_p if name in ("sq_last_error", "sq_version") else c_int
+            fn.restype = (c_char_p if name in ("sq_last_error", "sq_version") else
+                          c_uint32 if name == "sq_moe_router_width" else c_int)
         _lib = handle
     return _lib
 

@@ -24,6 +24,10 @@ int main() {
   const LinearScratchSize s = linear.decodeScratchSize({14336, 4096});
   std::printf("decode rows %u tile %u splits %u; prefill tile %u; decode partials %llu\n", decode.storage_rows,
               decode.config.tile, decode.config.splits, prefill.config.tile, (unsigned long long)s.partials);
+  const MoeShape shape{2048, 128, 8, 768, SQ_FMT_AF4G64, SQ_MOE_ROUTER_SOFTMAX, 0, 0};
+  const MoePlan moe = MoE::decodePlan(shape, 2, MoE::config(shape, 16, SQ_PHASE_DECODE));
+  const MoePlan moePrefill = MoE::prefillPlan(shape, 512, MoE::config(shape, 512, SQ_PHASE_PREFILL));
+  std::printf("moe decode rows %u tile %u; moe prefill tile %u\n", moe.rows, moe.tile_rows, moePrefill.tile_rows);
   try {
     (void)linear.decodePlan(p, 0);
     std::printf("no exception\n");

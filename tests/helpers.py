@@ -44,6 +44,32 @@ class Weights:
         return sq.segment(self.fmt, self.n, self.k, self.plane0, self.meta, column_offset, self.plane1)
 
 
+class DeviceAffine:
+    """An n x k MLX affine 4-bit tensor (z = -8 s, the benchmark's) repacked into planes on the device by the
+    library's own load path (sq_mlx_repack, bit-exact against the oracle in test_quant_gpu), with its fp32 values
+    fma(q, s, z) and their fp16 bits computed in numpy: s q and s (q - 8) have at most 12 significant bits, so the
+    fp32 products and sums are exact and equal the fma. For tensors too large for the CPU repack in a test's time
+    (the MoE block's 100 M-weight projections)."""
+
+    def __init__(self, rng: np.random.Generator, n: int, k: int, group: int = 64):
+        self.fmt = {32: oracle.FMT_AF4G32, 64: oracle.FMT_AF4G64, 128: oracle.FMT_AF4G128}[group]
+        self.n, self.k = n, k
+        codes, weight, scales, biases = synthetic.mlx_affine(rng, n, k, group, scale_sigma=0.02)
+        s, z = synthetic.bf16_to_f32(scales)[:, :, None], synthetic.bf16_to_f32(biases)[:, :, None]
+        self.values = (codes.reshape(n, k // group, group).astype(np.float32) * s + z).reshape(n, k)
+        self.halves = self.values.astype(np.float16).view(np.uint16)
+        t = torch()
+        p0_bytes, meta_bytes = sq.plane_bytes(self.fmt, n, k)
+        self.plane0 = t.zeros(p0_bytes, dtype=t.uint8, device="cuda")
+        self.meta = t.zeros(meta_bytes, dtype=t.uint8, device="cuda")
+        self.plane1 = None
+        sq.mlx_repack(self.fmt, n, k, to_device(weight), to_device(scales), to_device(biases), self.plane0, self.meta)
+        t.cuda.synchronize()
+
+    def segment(self, column_offset: int = 0) -> sq.Segment:
+        return sq.segment(self.fmt, self.n, self.k, self.plane0, self.meta, column_offset, self.plane1)
+
+
 def affine_native(rng: np.random.Generator, fmt: int, n: int, k: int, centred: bool = False) -> np.ndarray:
     """Native rows of an af4 format: z = -8 s (the benchmark's), or z centring the codes at a random point
     (the reference's makeAffineNative)."""
@@ -83,15 +109,20 @@ def bf16(values) -> np.ndarray:
     return synthetic.bf16_to_f32(synthetic.bf16_bits(np.asarray(values, np.float32)))
 
 
-def check_projection(got_bf16: np.ndarray, x: np.ndarray, weights: list[Weights] | Weights, what: str,
-                     residual: np.ndarray | None = None) -> dict:
-    """Every output inside [bf16(v - e), bf16(v + e)] of its fp64 value v and projectionBound e (staged), and the
-    BASELINE tolerances: rel-L2 <= 1e-2 and max-abs <= 2^-6 max|row| against fp64. Returns error statistics."""
-    if isinstance(weights, Weights):
+def check_projection(got_bf16: np.ndarray, x: np.ndarray, weights, what: str,
+                     residual: np.ndarray | None = None, staged: bool = True, columns=None) -> dict:
+    """Every output inside [bf16(v - e), bf16(v + e)] of its fp64 value v and projectionBound e, and the BASELINE
+    tolerances: rel-L2 <= 1e-2 and max-abs <= 2^-6 max|row| against fp64. staged: the bound of the reference's staged
+    tile (fp16 weights: the prefill tile); else the register tile's, accumulation alone (GgufFormatReference.hpp:
+    787-797), which the decode tiles' exact operands meet. columns: the output columns `got_bf16` holds (all by
+    default). Returns error statistics."""
+    if not isinstance(weights, (list, tuple)):
         weights = [weights]
     w = np.concatenate([wt.values for wt in weights], axis=0)
+    if columns is not None:
+        w = w[columns]
     value, magnitude, inputs, largest = oracle.project_f64(x, w)
-    bound = oracle.projection_bound(magnitude, inputs, largest, True)
+    bound = oracle.projection_bound(magnitude, inputs, largest, staged)
     lo, hi = value - bound, value + bound
     if residual is not None:
         res = synthetic.bf16_to_f32(residual).astype(np.float64)

@@ -13,7 +13,7 @@ ROOT = pathlib.Path(__file__).resolve().parent.parent
 
 def declared_functions():
     text = sq.HEADER.read_text()
-    return sorted(set(re.findall(r"^(?:int|const char \*)\s*(sq_\w+)\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^(?:int|uint32_t|const char \*)\s*(sq_\w+)\(", text, flags=re.M)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -186,11 +186,20 @@ def test_scratch_bounds_cover_every_plan():
     assert out.input == 2048 * 4096 * 2
 
 
+def moe_plan(kind, shape, count, config=None):
+    plan = sq.MoePlan()
+    if kind == "rows":
+        sq.call("sq_moe_decode_rows_plan", sq.byref(shape), count, sq.byref(plan))
+    else:
+        sq.call(f"sq_moe_{kind}_plan", sq.byref(shape), count, sq.byref(config) if config is not None else None,
+                sq.byref(plan))
+    return plan
+
+
 def test_moe_plans_and_workspace():
     shape = sq.MoeShape(2048, 128, 8, 768, sq.FMT_AF4G64)
-    plan = sq.MoePlan()
-    sq.call("sq_moe_prefill_plan", sq.byref(shape), 512, sq.byref(plan))
-    assert plan.tile_rows == 32
+    plan = moe_plan("prefill", shape, 512)
+    assert plan.tile_rows == 32 and plan.config.expert_tile == 32
     routes = 512 * 8
     assert plan.maximum_tiles == min(routes // 32 + 128, routes)
     w = plan.workspace
@@ -198,34 +207,98 @@ def test_moe_plans_and_workspace():
     assert w.tile_descriptors == plan.maximum_tiles * 8 and w.tile_count == 40
     assert w.expert_intermediate == plan.maximum_tiles * 32 * 768 * 2
     assert w.expert_output == plan.maximum_tiles * 32 * 2048 * 2
-    sq.call("sq_moe_prefill_plan", sq.byref(shape), 8, sq.byref(plan))
+    # The router's scores live in the grouped input: a row of 256 expert slots per row (MoE.cpp:64-84).
+    assert w.grouped_input == 512 * 256 * 4 and sq.lib().sq_moe_router_width(sq.byref(shape)) == 256
+    wide = sq.MoeShape(2048, 300, 8, 768, sq.FMT_AF4G64)
+    assert sq.lib().sq_moe_router_width(sq.byref(wide)) == 512
+    assert moe_plan("prefill", wide, 10).workspace.grouped_input == 10 * 512 * 4
+    plan = moe_plan("prefill", shape, 8)
     assert plan.tile_rows == 8   # 8 rows x 8 routes <= 128 experts
     with pytest.raises(sq.InvalidArgument, match="invalid MoE workspace shape"):
-        sq.call("sq_moe_prefill_plan", sq.byref(sq.MoeShape(2000, 128, 8, 768, sq.FMT_AF4G64)), 8, sq.byref(plan))
+        moe_plan("prefill", sq.MoeShape(2000, 128, 8, 768, sq.FMT_AF4G64), 8)
     with pytest.raises(sq.InvalidArgument, match="invalid MoE rows"):
-        sq.call("sq_moe_decode_plan", sq.byref(shape), 33, sq.byref(plan))
+        moe_plan("rows", shape, 33)
+    with pytest.raises(sq.InvalidArgument, match="invalid MoE prefill rows"):
+        moe_plan("prefill", shape, 2049)
+
+
+def test_moe_decode_plan_takes_lanes():
+    """MoE::decodePlan(shape, lanes, config) (MoE.cpp:567-571): a lane is 8 rows, at most 4 lanes; the policy's
+    config is 8-row staged tiles in decode, and a 32-row tile or the register tile is refused (MoE.cpp:196-206)."""
+    shape = sq.MoeShape(2048, 128, 8, 768, sq.FMT_AF4G64)
+    for lanes in (1, 2, 4):
+        plan = moe_plan("decode", shape, lanes)
+        assert plan.rows == 8 * lanes and plan.tile_rows == 8 and plan.phase == sq.PHASE_DECODE
+        assert plan.workspace.selected_experts == 8 * lanes * 8 * 4
+        assert plan.maximum_tiles == min(8 * lanes * 8 // 8 + 128, 8 * lanes * 8)
+    for lanes in (0, 5):
+        with pytest.raises(sq.InvalidArgument, match="invalid MoE decode batch width"):
+            moe_plan("decode", shape, lanes)
+    config = sq.MoeConfig()
+    sq.call("sq_moe_config_for", sq.byref(shape), 16, sq.PHASE_DECODE, sq.byref(config))
+    assert (config.expert_tile, config.gguf_tile, config.router_tile, config.cpu_bf16_experts) == (8, 0, 0, 0)
+    assert moe_plan("decode", shape, 2, config).rows == 16
+    with pytest.raises(sq.InvalidArgument, match="invalid MoE expert tile configuration"):
+        moe_plan("decode", shape, 2, sq.MoeConfig(32, 0, 0, 0))
+    with pytest.raises(sq.InvalidArgument, match="register expert tile"):
+        moe_plan("decode", shape, 2, sq.MoeConfig(8, sq.MOE_GGUF_TILE_REGISTER, 0, 0))
+    with pytest.raises(sq.InvalidArgument, match="invalid MoE expert tile configuration"):
+        moe_plan("prefill", shape, 64, sq.MoeConfig(16, 0, 0, 0))
+    # A prefill caller's config is taken as given: 8-row tiles on a chunk the policy would give 32.
+    assert moe_plan("prefill", shape, 512, sq.MoeConfig(8, 0, sq.FLOAT_TILE_NEURAL_ACCELERATOR, 1)).tile_rows == 8
+    sq.call("sq_moe_config_for", sq.byref(shape), 512, sq.PHASE_PREFILL, sq.byref(config))
+    assert config.expert_tile == 32
+    # The rows entry (no counterpart in the reference) takes any 1..32 rows.
+    assert moe_plan("rows", shape, 3).rows == 3
+
+
+def test_moe_plan_fields_must_match():
+    """A plan whose fields were changed after planning is refused rather than run with another workspace."""
+    shape = sq.MoeShape(512, 16, 4, 256, sq.FMT_AF4G64)
+    plan = moe_plan("prefill", shape, 100)
+    plan.tile_rows = 8
+    buffers = sq.MoeBuffers()
+    weights = sq.MoeWeights()
+    with pytest.raises(sq.InvalidArgument, match="do not match"):
+        sq.call("sq_moe_add", None, sq.byref(buffers), sq.byref(weights), sq.byref(plan))
+
+
+def test_moe_verify_rows_refusals():
+    """Verify rows are a decode step's, one uint32 per lane of 8 rows (MoE.cpp:467-475)."""
+    shape = sq.MoeShape(512, 16, 4, 256, sq.FMT_AF4G64)
+    n_i, n_h = 16 * 256, 16 * 512
+    seg = lambda n, k: sq.Segment(_fake(n * k // 2, 1 << 28), sq.Buffer(), _fake(n * k // 16, 1 << 29), n, k, 0,
+                                  sq.FMT_AF4G64)
+    weights = sq.MoeWeights(seg(n_i, 512), seg(n_i, 512), seg(n_h, 256), _fake(64, 1 << 27), 16)
+    for kind, count, verify_bytes, message in (("prefill", 16, 8, "only a verify step"),
+                                               ("decode", 2, 4, "MoE verify rows")):
+        plan = moe_plan(kind, shape, count)
+        w = plan.workspace
+        scratch = sq.MoeScratch(*[_fake(max(getattr(w, n), 16), (1 << 30) + (i << 24))
+                                  for i, n in enumerate(sq._MOE_WORKSPACE)])
+        io = _fake(plan.rows * 512 * 2, 1 << 26)
+        buffers = sq.MoeBuffers(io, sq.Buffer(), io, scratch, _fake(verify_bytes, 1 << 25))
+        with pytest.raises(sq.InvalidArgument, match=message):
+            sq.call("sq_moe_add", None, sq.byref(buffers), sq.byref(weights), sq.byref(plan))
 
 
 def test_moe_shared_slice_plans():
     """Shared slices add their routes to every row and one tile per tile_rows rows each (MoE.hpp:200-205); only the
     compiled routings plan (kCompiledMoeRoutings, MoE.hpp:34-46)."""
-    plan = sq.MoePlan()
     gated = sq.MoeShape(2048, 128, 8, 768, sq.FMT_AF4G64, sq.ROUTER_SOFTMAX, 1, 1)
-    sq.call("sq_moe_prefill_plan", sq.byref(gated), 500, sq.byref(plan))
+    plan = moe_plan("prefill", gated, 500)
     assert plan.maximum_tiles == min(500 * 8 // 32 + 128, 500 * 8) + 16
     assert plan.workspace.selected_experts == 500 * 9 * 4 and plan.workspace.route_rows == 500 * 9 * 4
     assert plan.workspace.expert_output == plan.maximum_tiles * 32 * 2048 * 2
     two = sq.MoeShape(2048, 64, 6, 512, sq.FMT_AF4G64, sq.ROUTER_SIGMOID_NORMALIZED, 2, 0)
-    sq.call("sq_moe_decode_plan", sq.byref(two), 3, sq.byref(plan))
+    plan = moe_plan("rows", two, 3)
     assert plan.tile_rows == 8 and plan.maximum_tiles == min(3 * 6 // 8 + 64, 18) + 2
     for router, slices, gate in ((sq.ROUTER_SOFTMAX, 2, 0), (sq.ROUTER_SOFTMAX, 1, 0),
                                  (sq.ROUTER_SIGMOID_NORMALIZED, 2, 1), (sq.ROUTER_SIGMOID_NORMALIZED, 0, 0)):
         with pytest.raises(sq.InvalidArgument, match="invalid MoE workspace shape"):
-            sq.call("sq_moe_prefill_plan", sq.byref(sq.MoeShape(2048, 64, 6, 512, sq.FMT_AF4G64, router, slices, gate)),
-                    8, sq.byref(plan))
+            moe_plan("prefill", sq.MoeShape(2048, 64, 6, 512, sq.FMT_AF4G64, router, slices, gate), 8)
     with pytest.raises(sq.InvalidArgument, match="unknown MoE router"):
-        sq.call("sq_moe_prefill_plan", sq.byref(sq.MoeShape(2048, 64, 6, 512, sq.FMT_AF4G64, 2, 0, 0)), 8,
-                sq.byref(plan))
+        moe_plan("prefill", sq.MoeShape(2048, 64, 6, 512, sq.FMT_AF4G64, 2, 0, 0), 8)
 
 
 def test_cxx_face_plans_and_throws(tmp_path):
@@ -241,6 +314,7 @@ def test_cxx_face_plans_and_throws(tmp_path):
                     "-L", str(lib_dir), "-lsplash_q4", f"-Wl,-rpath,{lib_dir}", "-o", str(exe)], check=True)
     out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
     assert "decode rows 8 tile 0" in out and "prefill tile 1" in out
+    assert "moe decode rows 16 tile 8; moe prefill tile 32" in out
     assert "invalid_argument:" in out
 
 
@@ -297,3 +371,4 @@ def test_norm_and_float_rows_refusals():
     f32 = sq.Segment(_fake(64 * 2048 * 4), sq.Buffer(), sq.Buffer(), 64, 2048, 0, sq.FLOAT32_ROWS)
     with pytest.raises(sq.InvalidArgument, match="outside its destination"):
         sq.call("sq_float_add", None, io, sq.byref(f32), _fake(rows * 64 * 4), rows, 64, 8, sq.OUTPUT_F32)
+

@@ -1,5 +1,7 @@
 """Decode tile (rows <= 32) through the C ABI against the fp64 oracle, with the reference's projection-test
-properties (dev/tests/engine/gguf_projection_test.mm): every output inside its fp64 interval (projectionBound),
+properties (dev/tests/engine/gguf_projection_test.mm): every output inside its fp64 interval (projectionBound of the
+register tile, the accumulation term alone: the decode tiles multiply exact code operands, GgufFormatReference.hpp:
+787-797),
 BASELINE's rel-L2 <= 1e-2 and max-abs <= 2^-6 max|row|, sparse inputs past half's range, a row's output bitwise
 independent of the other rows of its tile kind (the column tile runs 1..4 rows, the row tile more), K-split
 determinism with counters returned to zero, the epilogues (residual, gate/up in one pass bitwise equal to two
@@ -10,11 +12,16 @@ import pytest
 
 import splash_q4 as sq
 import sq_oracle as oracle
-from helpers import (Run, Weights, bf16, check_projection, dense_inputs, make_weights, sparse_inputs, staged_reference,
-                     to_device, to_host, torch)
+from helpers import (DeviceAffine, Run, Weights, bf16, check_projection, dense_inputs, make_weights, sparse_inputs,
+                     staged_reference, to_device, to_host, torch)
 from splash_q4 import synthetic
 
 pytestmark = pytest.mark.gpu
+
+
+def check_decode(*args, **kwargs):
+    """check_projection with the register tile's bound (no fp16 weight rounding term)."""
+    return check_projection(*args, staged=False, **kwargs)
 
 FORMATS = [oracle.FMT_AF4G64, oracle.FMT_Q4K, oracle.FMT_AF4G32, oracle.FMT_AF4G128]
 
@@ -50,7 +57,7 @@ def test_decode_dense(fmt, rows, splits):
     w = make_weights(rng, fmt, n, k, centred=rows % 2 == 1)
     x = dense_inputs(rng, rows, k)
     got = run_plan(staged(n, k, rows, splits), sq.projection(w.segment()), x, n)
-    stats = check_projection(got, x, w, f"fmt {fmt} rows {rows} splits {splits}")
+    stats = check_decode(got, x, w, f"fmt {fmt} rows {rows} splits {splits}")
     # no worse than the reference's staged numerics (fp16 weights, fp32 sums), beyond rounding-boundary noise
     ref = staged_reference(x, w)
     value, *_ = oracle.project_f64(x, w.values)
@@ -66,7 +73,7 @@ def test_decode_sparse_inputs(fmt, splits):
     w = make_weights(rng, fmt, n, k)
     x = sparse_inputs(8, k)
     got = run_plan(staged(n, k, 8, splits), sq.projection(w.segment()), x, n)
-    check_projection(got, x, w, "sparse")
+    check_decode(got, x, w, "sparse")
 
 
 @pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K])
@@ -87,8 +94,8 @@ def test_rows_are_independent(fmt, splits):
     for r in range(4):
         alone = run_plan(staged(n, k, 1, splits), proj, x[r:r + 1], n)
         assert np.array_equal(alone[0], four[r]), f"row {r}"
-    check_projection(four, x[:4], w, "column tile")
-    check_projection(all32, x, w, "row tile")
+    check_decode(four, x[:4], w, "column tile")
+    check_decode(all32, x, w, "row tile")
 
 
 def test_split_determinism_and_poisoned_partials():
@@ -108,7 +115,7 @@ def test_split_determinism_and_poisoned_partials():
         assert int(run.scratch.counters.abs().sum().item()) == 0
         outs.append(run.output().copy())
     assert np.array_equal(outs[0], outs[1])
-    check_projection(outs[0][:4], x, w, "poisoned partials")
+    check_decode(outs[0][:4], x, w, "poisoned partials")
 
 
 @pytest.mark.parametrize("rows", [2, 8])
@@ -121,7 +128,7 @@ def test_residual_epilogue(rows):
     for splits in (2, 4):
         got = run_plan(staged(n, k, rows, splits, sq.EPILOGUE_RESIDUAL), sq.projection(w.segment()), x, n,
                        residual=residual)
-        check_projection(got, x, w, "residual", residual=residual)
+        check_decode(got, x, w, "residual", residual=residual)
 
 
 @pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K])
@@ -157,7 +164,7 @@ def test_fp32_destination_rounds_to_the_bf16_output(rows):
         b16 = run_plan(staged(n, k, rows, splits), sq.projection(w.segment()), x, n)
         assert np.array_equal(synthetic.bf16_bits(f32), b16)
         value, magnitude, inputs, largest = oracle.project_f64(x, w.values)
-        bound = oracle.projection_bound(magnitude, inputs, largest, True)
+        bound = oracle.projection_bound(magnitude, inputs, largest, False)
         assert np.all(np.abs(f32.astype(np.float64) - value) <= bound)
         # no worse than the reference's staged fp32 sums on these rows (plus accumulation-order slack)
         ref = oracle.project_staged_f32(x, w.halves).astype(np.float64)
@@ -181,7 +188,7 @@ def test_fused_segments_equal_segments_alone(rows):
         alone = run_plan(staged(p.n, k, rows, 2), sq.projection(p.segment()), x, p.n)
         assert np.array_equal(fused[:, offset:offset + p.n], alone)
         offset += p.n
-    check_projection(fused, x, parts, "fused")
+    check_decode(fused, x, parts, "fused")
 
 
 def test_padding_columns_untouched():
@@ -192,20 +199,57 @@ def test_padding_columns_untouched():
     proj = sq.projection(w.segment(), output_size=n + pad)
     got = run_plan(staged(n + pad, k, 4, 4), proj, x, n + pad)
     assert np.all(got[:, n:] == 0xFFFF)
-    check_projection(got[:, :n], x, w, "padded")
+    check_decode(got[:, :n], x, w, "padded")
+
+
+_SHAPE_CACHE = {}
+
+
+def shape_weights(fmt, n, k, seed):
+    """Weights of a BASELINE shape, built once per module (the largest take seconds on the CPU)."""
+    key = (fmt, n, k, seed)
+    if key not in _SHAPE_CACHE:
+        _SHAPE_CACHE.clear()
+        rng = np.random.default_rng(seed)
+        _SHAPE_CACHE[key] = DeviceAffine(rng, n, k) if fmt == oracle.FMT_AF4G64 else make_weights(rng, fmt, n, k)
+    return _SHAPE_CACHE[key]
 
 
 @pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
-@pytest.mark.parametrize("rows", [1, 4, 16])
-def test_baseline_shapes_policy_plans(n, k, rows):
-    """The BASELINE decode sweep's shapes at M = 1 and 16 under the library's own plan."""
+@pytest.mark.parametrize("rows", [1, 2, 4, 8, 16])
+def test_config1_sweep_policy_plans(n, k, rows):
+    """BASELINE config 1's decode sweep (and config 0, the 4096 x 4096 shape at M = 1): every shape at every M under
+    the library's own plan, every output against fp64 with the register tile's bound, and no worse than the
+    reference's staged numerics."""
+    w = shape_weights(oracle.FMT_AF4G64, n, k, n + k)
     rng = np.random.default_rng(n + k + rows)
-    w = make_weights(rng, oracle.FMT_AF4G64, n, k)
     x = dense_inputs(rng, rows, k)
     proj = sq.projection(w.segment())
     plan = sq.plan_for(sq.decode_workload(n, k, rows), proj)
     got = run_plan(plan, proj, x, n)
-    check_projection(got, x, w, f"{n}x{k} rows {rows}")
+    stats = check_decode(got, x, w, f"{n}x{k} rows {rows}")
+    value, *_ = oracle.project_f64(x, w.values)
+    ref = synthetic.bf16_to_f32(synthetic.bf16_bits(oracle.project_staged_f32(x, w.halves)))
+    ref_l2 = np.linalg.norm(ref - value) / np.linalg.norm(value)
+    assert stats["rel_l2"] <= ref_l2 * 1.10 + 1e-6
+
+
+@pytest.mark.parametrize("rows", [1, 16])
+def test_config3_q4k_decode(rows):
+    """BASELINE config 3's decode points: Q4_K, K = 5120, N = 27648, M = 1 and 16 under the library's plan, every
+    output against fp64 (register tile bound) and no worse than the reference's staged numerics."""
+    n, k = 27648, 5120
+    w = shape_weights(oracle.FMT_Q4K, n, k, 3)
+    rng = np.random.default_rng(300 + rows)
+    x = dense_inputs(rng, rows, k)
+    proj = sq.projection(w.segment())
+    plan = sq.plan_for(sq.decode_workload(n, k, rows), proj)
+    got = run_plan(plan, proj, x, n)
+    stats = check_decode(got, x, w, f"Q4_K {n}x{k} rows {rows}")
+    value, *_ = oracle.project_f64(x, w.values)
+    ref = synthetic.bf16_to_f32(staged_reference(x, w))
+    ref_l2 = np.linalg.norm(ref - value) / np.linalg.norm(value)
+    assert stats["rel_l2"] <= ref_l2 * 1.10 + 1e-6
 
 
 NEW_FORMATS = [oracle.FMT_Q5K, oracle.FMT_Q6K, oracle.FMT_Q80, oracle.FMT_AF8G64]
@@ -222,7 +266,7 @@ def test_decode_new_formats(fmt, rows, splits):
     w = make_weights(rng, fmt, n, k)
     x = dense_inputs(rng, rows, k)
     got = run_plan(staged(n, k, rows, splits), sq.projection(w.segment()), x, n)
-    stats = check_projection(got, x, w, f"fmt {fmt} rows {rows} splits {splits}")
+    stats = check_decode(got, x, w, f"fmt {fmt} rows {rows} splits {splits}")
     ref = staged_reference(x, w)
     value, *_ = oracle.project_f64(x, w.values)
     ref_l2 = np.linalg.norm(synthetic.bf16_to_f32(ref) - value) / np.linalg.norm(value)
@@ -244,7 +288,7 @@ def test_decode_new_formats_fixture_and_pairs(fmt, rows):
     if np.isfinite(w.values).all() and np.abs(w.values).max() < 1e30:
         x = sparse_inputs(rows, k, 1.0)
         got = run_plan(staged(n, k, rows, 1), sq.projection(w.segment()), x, n)
-        check_projection(got, x, w, f"fixture fmt {fmt} rows {rows}")
+        check_decode(got, x, w, f"fixture fmt {fmt} rows {rows}")
     wg, wu = make_weights(rng, fmt, 256, 2048), make_weights(rng, fmt, 256, 2048)
     gate, up = sq.projection(wg.segment()), sq.projection(wu.segment())
     for pair_rows in ([2] if rows < 5 else [rows, 32]):
@@ -264,5 +308,5 @@ def test_decode_new_formats_longest_slices(fmt, rows):
     w = make_weights(rng, fmt, n, k)
     x = dense_inputs(rng, rows, k)
     got = run_plan(staged(n, k, rows, 1), sq.projection(w.segment()), x, n)
-    check_projection(got, x, w, f"fmt {fmt} rows {rows} k {k}")
+    check_decode(got, x, w, f"fmt {fmt} rows {rows} k {k}")
 

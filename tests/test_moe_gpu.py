@@ -8,7 +8,7 @@ import pytest
 
 import splash_q4 as sq
 import sq_oracle as oracle
-from helpers import make_weights, to_device, to_host, torch
+from helpers import DeviceAffine, make_weights, to_device, to_host, torch
 from splash_q4 import synthetic
 
 pytestmark = pytest.mark.gpu
@@ -20,7 +20,7 @@ class Block:
     any projection's own format ("gate", "up", "down", "shared_gate", ...), as the reference's blocks carry them."""
 
     def __init__(self, rng, experts, hidden, intermediate, fmt=oracle.FMT_AF4G64, shared=0, gated=False,
-                 router=oracle.ROUTER_SOFTMAX, shared_fmt=None, down_fmt=None, formats=None):
+                 router=oracle.ROUTER_SOFTMAX, shared_fmt=None, down_fmt=None, formats=None, device_repack=False):
         self.e, self.h, self.i, self.fmt = experts, hidden, intermediate, fmt
         self.shared, self.gated, self.router = shared, gated, router
         self.parts = {}
@@ -34,7 +34,9 @@ class Block:
                      ("shared_down", shared * hidden, intermediate, df)]
         plan = [(name, n, k, formats.get(name, f)) for name, n, k, f in plan]
         for name, n, k, f in plan:
-            self.parts[name] = make_weights(rng, f, n, k)
+            # device_repack: af4g64 planes from the library's MLX repack, values from numpy (helpers.DeviceAffine)
+            self.parts[name] = (DeviceAffine(rng, n, k) if device_repack and f == oracle.FMT_AF4G64
+                                else make_weights(rng, f, n, k))
         self.slots = to_device(np.arange(experts, dtype=np.uint32))
         self.scalar_gate = rng.normal(0, 0.05, hidden).astype(np.float32) if gated else None
 
@@ -54,13 +56,16 @@ class Block:
                              self.segment("shared_gate"), self.segment("shared_up"), self.segment("shared_down"),
                              sq.view(self._gate), router)
 
-    def values(self, name, expert):
-        """Expert `expert`'s rows of projection `name`; ids from the expert count on are the shared slices."""
+    def weights_of(self, name, expert, halves=False):
+        """Expert `expert`'s rows of projection `name` as fp32 values (or, halves, their fp16 rounding); ids from the
+        expert count on are the shared slices."""
         if expert >= self.e:
             name, expert = "shared_" + name, expert - self.e
-        v = self.parts[name].values
+        part = self.parts[name]
         rows = self.i if name.endswith("gate") or name.endswith("up") else self.h
-        return v[expert * rows:(expert + 1) * rows]
+        if halves:
+            return part.halves[expert * rows:(expert + 1) * rows].view(np.float16).astype(np.float32)
+        return part.values[expert * rows:(expert + 1) * rows]
 
     def shape(self, top_k):
         return sq.MoeShape(self.h, self.e, top_k, self.i, self.fmt, self.router, self.shared, int(self.gated))
@@ -69,43 +74,86 @@ class Block:
         return oracle.route_select(scores, top_k, self.router, self.shared, x, self.scalar_gate)
 
 
-def run_moe(block, x, scores, top_k, residual=None, phase="prefill"):
+def make_plan(shape, rows, phase):
+    """prefill: MoE::prefillPlan with the policy's config; lanes: MoE::decodePlan(shape, rows / 8 lanes); decode: the
+    rows entry (any 1..32 rows)."""
+    plan = sq.MoePlan()
+    if phase == "prefill":
+        sq.call("sq_moe_prefill_plan", sq.byref(shape), rows, None, sq.byref(plan))
+    elif phase == "lanes":
+        assert rows % 8 == 0
+        sq.call("sq_moe_decode_plan", sq.byref(shape), rows // 8, None, sq.byref(plan))
+    else:
+        sq.call("sq_moe_decode_rows_plan", sq.byref(shape), rows, sq.byref(plan))
+    return plan
+
+
+def run_moe(block, x, scores, top_k, residual=None, phase="prefill", verify=None):
+    """One sq_moe_add. The caller's router scores go where the reference's router writes them: the grouped-input
+    scratch, a row of the shape's router width per row (a block with router rows overwrites them). Returns the plan,
+    the scratch tensors and the bf16 output."""
     t = torch()
     rows = x.shape[0]
     shape = block.shape(top_k)
-    plan = sq.MoePlan()
-    sq.call("sq_moe_prefill_plan" if phase == "prefill" else "sq_moe_decode_plan", sq.byref(shape), rows, sq.byref(plan))
+    plan = make_plan(shape, rows, phase)
     scratch = {}
     for name in sq._MOE_WORKSPACE:
         nbytes = getattr(plan.workspace, name)
         scratch[name] = t.zeros(max(nbytes, 4) // 4 + 1, dtype=t.int32, device="cuda")
-    ms = sq.MoeScratch(*[sq.view(scratch[n]) if getattr(plan.workspace, n) else sq.Buffer(None, 0)
-                         for n in sq._MOE_WORKSPACE])
-    xin, sc = to_device(x), t.from_numpy(np.ascontiguousarray(scores)).cuda()
-    scratch["scores"] = sc
+    width = sq.lib().sq_moe_router_width(sq.byref(shape))
+    assert plan.workspace.grouped_input == rows * width * 4
+    padded = np.full((rows, width), np.nan, np.float32)   # slots past the experts: no kernel reads them
+    padded[:, :block.e] = scores
+    scratch["grouped_input"] = t.from_numpy(padded).cuda()
+    ms = sq.MoeScratch(*[sq.view(scratch[n]) for n in sq._MOE_WORKSPACE])
+    xin = to_device(x)
     res = to_device(residual) if residual is not None else None
     out = t.full((rows, block.h), -1, dtype=t.int16, device="cuda")
-    buffers = sq.MoeBuffers(sq.view(xin), sq.view(sc), sq.view(res), sq.view(out), 0, ms)
+    vr = to_device(np.asarray(verify, np.uint32)) if verify is not None else None
+    buffers = sq.MoeBuffers(sq.view(xin), sq.view(res), sq.view(out), ms, sq.view(vr))
     sq.call("sq_moe_add", sq.stream_handle(), sq.byref(buffers), sq.byref(block.weights()), sq.byref(plan))
     t.cuda.synchronize()
+    scratch["scores"] = scratch["grouped_input"].cpu().numpy().view(np.float32).reshape(rows, width)[:, :block.e]
     return plan, scratch, to_host(out, np.uint16)
 
 
-def expected(block, x, selected, weights, residual):
-    xf = synthetic.bf16_to_f32(x).astype(np.float64)
-    rows = x.shape[0]
+def live_routes(rows, per_row, top_k, verify):
+    """[rows][per_row] bool: the routes the grouping keeps (a verify step leaves the routed routes of rows past their
+    lane's count out; the shared slices' routes always stay)."""
+    live = np.ones((rows, per_row), bool)
+    if verify is not None:
+        dead = np.array([r % 8 >= verify[r // 8] for r in range(rows)])
+        live[dead, :top_k] = False
+    return live
+
+
+def expected(block, x, selected, weights, residual, top_k=None, verify=None, staged=False):
+    """The block's output from the routes' expert FFNs, expert by expert: fp64 products and sums (or, staged, the
+    reference's staged numerics emulated: fp16 weights, fp32 products and sums) with the kernels' bf16 rounding
+    points (gate and up, the SwiGLU intermediate, the expert output), then the residual plus the routing-weighted
+    sum of the live routes."""
+    dtype = np.float32 if staged else np.float64
+    xf = synthetic.bf16_to_f32(x).astype(dtype)
+    rows, per_row = selected.shape
+    live = live_routes(rows, per_row, top_k if top_k is not None else per_row - block.shared, verify)
     out = np.zeros((rows, block.h))
     if residual is not None:
         out += synthetic.bf16_to_f32(residual)
-    for r in range(rows):
-        for s, e in enumerate(selected[r]):
-            g = block.values("gate", e).astype(np.float64) @ xf[r]
-            u = block.values("up", e).astype(np.float64) @ xf[r]
-            gb, ub = synthetic.bf16_to_f32(synthetic.bf16_bits(g)), synthetic.bf16_to_f32(synthetic.bf16_bits(u))
-            h = synthetic.bf16_to_f32(synthetic.bf16_bits(ub * (gb / (1 + np.exp(-gb.astype(np.float64))))))
-            y = block.values("down", e).astype(np.float64) @ h.astype(np.float64)
-            out[r] += weights[r, s] * synthetic.bf16_to_f32(synthetic.bf16_bits(y))
+    rb = lambda v: synthetic.bf16_to_f32(synthetic.bf16_bits(v.astype(np.float32))).astype(dtype)
+    for e in np.unique(selected[live]):
+        r_idx, s_idx = np.nonzero((selected == e) & live)
+        w = lambda name: block.weights_of(name, e, staged).astype(dtype)
+        g, u = rb(xf[r_idx] @ w("gate").T), rb(xf[r_idx] @ w("up").T)
+        h = rb(u * (g / (1 + np.exp(-g.astype(np.float64))).astype(dtype)))
+        y = rb(h @ w("down").T).astype(np.float64)
+        np.add.at(out, r_idx, weights[r_idx, s_idx].astype(np.float64)[:, None] * y)
     return out
+
+
+def errors(got, want):
+    gotf = synthetic.bf16_to_f32(got).astype(np.float64)
+    err = gotf - want
+    return np.linalg.norm(err) / np.linalg.norm(want), err
 
 
 @pytest.mark.parametrize("rows,experts,top_k", [(64, 32, 4), (6, 32, 4), (300, 16, 2)])
@@ -117,33 +165,44 @@ def test_moe_routed_experts(rows, experts, top_k):
     scores = synthetic.router_logits(rng, rows, experts)
     scores[0, 3] = scores[0, 5] = scores[0].max() + 1   # a tie: the lower id ranks first
     residual = synthetic.bf16_bits(rng.uniform(-4, 4, (rows, hidden)).astype(np.float32))
-    selected = check_block(block, x, scores, top_k, residual)
+    selected, _, _ = check_block(block, x, scores, top_k, residual)
     assert selected[0, 0] == 3 and selected[0, 1] == 5
 
 
-def check_block(block, x, scores, top_k, residual, phase="prefill", weight_rtol=2e-6):
-    """Runs the block and checks selection, weights, grouping and output against the oracle; returns the selection."""
+def check_block(block, x, scores, top_k, residual, phase="prefill", weight_rtol=2e-6, verify=None, staged_check=False):
+    """Runs the block and checks selection, weights, grouping and output against the oracle; returns the selection
+    and the tile descriptors."""
     rows = x.shape[0]
-    plan, scratch, got = run_moe(block, x, scores, top_k, residual, phase)
+    plan, scratch, got = run_moe(block, x, scores, top_k, residual, phase, verify)
     per_row = top_k + block.shared
     routes = rows * per_row
     sel_gpu = to_host(scratch["selected_experts"], np.uint32)[:routes].reshape(rows, per_row)
     w_gpu = scratch["routing_weights"].cpu().numpy().view(np.float32)[:routes].reshape(rows, per_row)
     selected, weights = block.route(x, scores, top_k)
     assert np.array_equal(sel_gpu, selected)
-    assert np.allclose(w_gpu, weights, rtol=weight_rtol, atol=1e-7)
-    tiles, grouped, route_rows = oracle.group_routes(selected, block.e, plan.tile_rows, block.shared)
+    finite = np.isfinite(weights)
+    assert np.array_equal(np.isfinite(w_gpu), finite)
+    assert np.allclose(w_gpu[finite], weights[finite], rtol=weight_rtol, atol=1e-7)
+    tiles, grouped, route_rows = oracle.group_routes(selected, block.e, plan.tile_rows, block.shared, verify)
     count = to_host(scratch["tile_count"], np.uint32)
     assert count[0] == tiles.shape[0] <= plan.maximum_tiles
-    assert np.array_equal(to_host(scratch["tile_descriptors"], np.uint32)[: 2 * count[0]].reshape(-1, 2), tiles)
+    gpu_tiles = to_host(scratch["tile_descriptors"], np.uint32)[: 2 * count[0]].reshape(-1, 2)
+    assert np.array_equal(gpu_tiles, tiles)
     assert np.array_equal(to_host(scratch["grouped_routes"], np.uint32)[: grouped.size], grouped)
     assert np.array_equal(to_host(scratch["route_rows"], np.uint32)[:routes], route_rows)
-    want = expected(block, x, selected, weights, residual)
-    gotf = synthetic.bf16_to_f32(got).astype(np.float64)
-    err = gotf - want
-    assert np.linalg.norm(err) / np.linalg.norm(want) <= 1e-2
+    # rows whose routing weights are all finite (an all-NaN score row has none)
+    ok = finite.all(axis=1)
+    want = expected(block, x, selected, weights, residual, top_k, verify)[ok]
+    rel, err = errors(got[ok], want)
+    assert rel <= 1e-2, rel
     assert np.all(np.abs(err) <= np.ldexp(np.abs(want).max(axis=1, keepdims=True), -6))
-    return sel_gpu
+    if staged_check:
+        # no worse than the reference's staged expert tile (fp16 weights, fp32 sums), emulated on the CPU
+        ref = expected(block, x, selected, weights, residual, top_k, verify, staged=True)[ok]
+        ref_rel = np.linalg.norm(synthetic.bf16_to_f32(synthetic.bf16_bits(ref.astype(np.float32))) - want) / \
+            np.linalg.norm(want)
+        assert rel <= 1.10 * ref_rel + 1e-6, (rel, ref_rel)
+    return sel_gpu, gpu_tiles, got
 
 
 @pytest.mark.parametrize("fmt", [oracle.FMT_Q4K, oracle.FMT_AF4G32, oracle.FMT_Q5K, oracle.FMT_Q6K, oracle.FMT_Q80,
@@ -223,13 +282,14 @@ def test_moe_shared_slices_in_their_own_formats(shared_fmt, down_fmt):
     check_block(block, x, scores, 2, None)
 
 
-def test_moe_decode_rows():
+def test_moe_decode_lane():
+    """One decode lane through MoE::decodePlan(shape, 1 lane): 8 rows on 8-row tiles."""
     rng = np.random.default_rng(77)
     block = Block(rng, 64, 512, 128)
     x = synthetic.activations(rng, 8, 512)
     scores = synthetic.router_logits(rng, 8, 64)
-    plan, _, got = run_moe(block, x, scores, 8, None, phase="decode")
-    assert plan.tile_rows == 8
+    plan, _, got = run_moe(block, x, scores, 8, None, phase="lanes")
+    assert plan.tile_rows == 8 and plan.rows == 8
     selected, weights = oracle.route_select(scores, 8)
     want = expected(block, x, selected, weights, None)
     err = synthetic.bf16_to_f32(got) - want
@@ -246,7 +306,7 @@ def test_moe_router_projection():
     rows = 44
     x = synthetic.activations(rng, rows, 512)
     plan, scratch, got = run_moe(block, x, np.zeros((rows, 32), np.float32), 4)
-    scores = scratch["scores"].cpu().numpy()
+    scores = scratch["scores"].copy()
     exact, magnitude = oracle.float_rows_f64(x, block.router_rows)
     assert np.all(np.abs(scores - exact) <= (512 / 64 + 8) * 2.0 ** -24 * magnitude)
     per_row = 4 + 1
@@ -259,3 +319,74 @@ def test_moe_router_projection():
     want = expected(block, x, selected, weights, None)
     err = synthetic.bf16_to_f32(got).astype(np.float64) - want
     assert np.linalg.norm(err) / np.linalg.norm(want) <= 1e-2
+
+
+def test_moe_nan_score_rows():
+    """Rows of NaN router scores (an upstream NaN through the router projection): a NaN never wins, an all-NaN row
+    selects expert 0 at every rank as the reference's kernel does, every selected id stays a valid expert, and the
+    grouping and the other rows' outputs are the oracle's."""
+    rng = np.random.default_rng(4242)
+    block = Block(rng, 32, 512, 128)
+    rows = 40
+    x = synthetic.activations(rng, rows, 512)
+    scores = synthetic.router_logits(rng, rows, 32)
+    scores[3] = np.nan
+    scores[7, ::2] = np.nan
+    scores[11, :20] = -np.inf
+    selected, _, got = check_block(block, x, scores, 4, None)
+    assert selected[3].tolist() == [0, 0, 0, 0]
+    assert np.all(selected < 32)
+    assert np.all(selected[7] % 2 == 1)
+
+
+@pytest.mark.parametrize("shared", [0, 1])
+def test_moe_verify_rows(shared):
+    """A verify step (MoeBuffers::verifyRows, MoE.cpp:467-475): two lanes of 8 rows with 3 and 8 live rows. The
+    grouping is the oracle's verified grouping bit for bit (the dead rows' routed routes in no tile, their route rows
+    ~0u), and a dead row's output is its residual plus its shared slices' routes only: without a shared expert,
+    exactly its residual."""
+    rng = np.random.default_rng(31 + shared)
+    block = Block(rng, 16, 512, 256, shared=shared, gated=bool(shared))
+    rows = 16
+    x = synthetic.activations(rng, rows, 512)
+    scores = synthetic.router_logits(rng, rows, 16)
+    residual = synthetic.bf16_bits(rng.uniform(-2, 2, (rows, 512)).astype(np.float32))
+    verify = [3, 8]
+    _, tiles, got = check_block(block, x, scores, 4, residual, "lanes", verify=verify)
+    assert tiles[:, 1].sum() == (3 + 8) * 4 + shared * rows
+    dead = got[3:8]
+    if not shared:
+        assert np.array_equal(dead, residual[3:8])
+    else:
+        assert not np.array_equal(dead, residual[3:8])
+    # every row live: the plain grouping
+    check_block(block, x, scores, 4, residual, "lanes", verify=[8, 8])
+
+
+@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_AF4G32, oracle.FMT_AF4G128, oracle.FMT_Q4K,
+                                 oracle.FMT_Q5K, oracle.FMT_Q6K, oracle.FMT_Q80, oracle.FMT_AF8G64])
+def test_moe_tall_tiles_every_format(fmt):
+    """Router scores skewed towards four experts give them tiles of more than 16 rows (the two-row-block body of the
+    expert passes), in every format, in the one-pass gate/up pair (two tensors a wave) and the down pass (one)."""
+    rng = np.random.default_rng(1300 + fmt)
+    block = Block(rng, 16, 512, 256, fmt=fmt)
+    rows = 64
+    x = synthetic.activations(rng, rows, 512)
+    scores = synthetic.router_logits(rng, rows, 16)
+    scores[:, :4] += 4.0
+    _, tiles, _ = check_block(block, x, scores, 4, None)
+    assert tiles[:, 1].max() > 16 and np.count_nonzero(tiles[:, 1] > 16) >= 4
+
+
+def test_moe_config4_block():
+    """BASELINE config 4 at full size: 128 experts, top 8 of softmax(N(0,1) logits), hidden 2048, intermediate 768,
+    512 tokens, MLX affine 4-bit group 64, on the prefill plan (32-row tiles, about 250 of them, dispatched longest
+    first). Every row of the output against fp64 within BASELINE's tolerances, and no worse than the reference's
+    staged expert numerics emulated on the CPU."""
+    rng = np.random.default_rng(4096)
+    block = Block(rng, 128, 2048, 768, device_repack=True)
+    rows = 512
+    x = synthetic.activations(rng, rows, 2048)
+    scores = synthetic.router_logits(rng, rows, 128)
+    _, tiles, _ = check_block(block, x, scores, 8, None, staged_check=True)
+    assert tiles.shape[0] > 128 and tiles[:, 1].max() > 16

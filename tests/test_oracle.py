@@ -63,16 +63,47 @@ def test_q4k_golden_hash():
     assert hashlib.sha256(values.tobytes()).hexdigest() == golden["q4k"]
 
 
+def _q4k_values_numpy(native: np.ndarray, min_sign: float = -1.0, swap_scale_min: bool = False,
+                      high_nibble_first: bool = False) -> np.ndarray:
+    """GGML's dequantize_row_q4_K restated in numpy, block by block from the native bytes (d, dmin, the 12 packed
+    6-bit scale/min bytes of get_scale_min_k4, then 4 chunks of 64 values: 32 low nibbles, 32 high nibbles), value =
+    d sc q - dmin mn. The arguments plant the mistakes the golden hash must catch."""
+    blocks = native.reshape(-1, 144)
+    d = blocks[:, 0:2].copy().view(np.float16).astype(np.float32).ravel()
+    dmin = blocks[:, 2:4].copy().view(np.float16).astype(np.float32).ravel()
+    sc, qs = blocks[:, 4:16].astype(np.int32), blocks[:, 16:].astype(np.int32)
+
+    def scale_min(j):
+        if j < 4:
+            return sc[:, j] & 63, sc[:, j + 4] & 63
+        return (sc[:, j + 4] & 15) | ((sc[:, j - 4] >> 6) << 4), (sc[:, j + 4] >> 4) | ((sc[:, j] >> 6) << 4)
+
+    out = np.zeros((blocks.shape[0], 256), np.float32)
+    for chunk in range(4):
+        q = qs[:, 32 * chunk:32 * chunk + 32]
+        for half in range(2):
+            s, m = scale_min(2 * chunk + half)
+            if swap_scale_min:
+                s, m = m, s
+            d1, m1 = d * s.astype(np.float32), dmin * m.astype(np.float32)
+            nibble = (q >> 4) if (half == 1) != high_nibble_first else (q & 15)
+            out[:, 64 * chunk + 32 * half:][:, :32] = d1[:, None] * nibble.astype(np.float32) + np.float32(min_sign) * m1[:, None]
+    return out
+
+
 def test_q4k_planted_error_fails_golden():
-    """A plausible mistake in the Q4_K value formula (the min term added rather than subtracted) fails the hash."""
+    """A second, independent restatement of the Q4_K values (numpy, from the native bytes) reproduces the golden
+    hash; the same restatement with a plausible mistake planted (the min term added rather than subtracted, the
+    6-bit scale and min swapped, the two nibbles of a byte swapped) does not, so the hash pins each of them."""
     golden = json.loads((GOLDEN / "weight_goldens.json").read_text())
-    native = oracle.fixture(oracle.FMT_Q4K, 256, 1024, 7)
-    _, _, values = oracle.repack(oracle.FMT_Q4K, native, 256, 1024)
-    # recompute with the sign of dmin * mn flipped: value' = value + 2 m
-    _, meta, _ = oracle.repack(oracle.FMT_Q4K, native, 256, 1024)
-    changed = values.copy()
-    changed[0, 0] = np.nextafter(changed[0, 0], np.float32(np.inf))
-    assert hashlib.sha256(changed.tobytes()).hexdigest() != golden["q4k"]
+    fx = golden["fixture"]
+    native = oracle.fixture(oracle.FMT_Q4K, fx["rows"], fx["columns"], fx["seed"])
+    digest = lambda v: hashlib.sha256(v.reshape(fx["rows"], fx["columns"]).tobytes()).hexdigest()
+    assert digest(_q4k_values_numpy(native)) == golden["q4k"]
+    _, _, values = oracle.repack(oracle.FMT_Q4K, native, fx["rows"], fx["columns"])
+    assert np.array_equal(values.ravel().view(np.uint32), _q4k_values_numpy(native).ravel().view(np.uint32))
+    for planted in ({"min_sign": 1.0}, {"swap_scale_min": True}, {"high_nibble_first": True}):
+        assert digest(_q4k_values_numpy(native, **planted)) != golden["q4k"], planted
 
 
 @pytest.mark.parametrize("fmt", [oracle.FMT_Q4K, oracle.FMT_AF4G32, oracle.FMT_AF4G64, oracle.FMT_AF4G128])
@@ -203,6 +234,88 @@ def test_route_select_ties_and_weights():
     assert selected.tolist() == [[1, 2, 5], [0, 1, 2]]
     assert np.allclose(weights.sum(axis=1), 1.0)
     assert np.allclose(weights[1], 1 / 3)
+
+
+def _route_select_lanes(scores: np.ndarray, top_k: int, lanes: int = 32) -> np.ndarray:
+    """The reference kernel's selection simulated lane by lane (moe.metal:77-93): lane l holds experts l, l + lanes,
+    ...; each rank every lane takes its best by strict `>` from -inf (its first slot when none beats -inf), the
+    wave maximum of those, and the lowest expert id among the lanes whose best equals it; the winner's score
+    becomes -inf. A different formulation from the oracle's flat scan, and run at two lane counts."""
+    rows, experts = scores.shape
+    slots = -(-experts // lanes)
+    out = np.zeros((rows, top_k), np.uint32)
+    for r in range(rows):
+        table = np.full((lanes, slots), -np.inf, np.float32)
+        for e in range(experts):
+            table[e % lanes, e // lanes] = scores[r, e]
+        for rank in range(top_k):
+            best = np.full(lanes, -np.inf, np.float32)
+            slot = np.zeros(lanes, np.int64)
+            for lane in range(lanes):
+                for i in range(slots):
+                    if table[lane, i] > best[lane]:
+                        best[lane], slot[lane] = table[lane, i], i
+            top = best.max()
+            candidates = [lane + lanes * slot[lane] for lane in range(lanes) if best[lane] == top]
+            winner = min(candidates)
+            table[winner % lanes, winner // lanes] = -np.inf
+            out[r, rank] = winner
+    return out
+
+
+def test_route_select_nan_and_exhausted_scores():
+    """NaN scores never win; with no score above -inf left expert 0 wins (so an all-NaN row selects expert 0 every
+    rank), matching the reference's lane algorithm, simulated at 32 and 64 lanes over rows with NaNs, -inf, ties and
+    fewer finite scores than top_k."""
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    scores = np.array([[nan, 1.0, nan, 2.0, 0.5],
+                       [nan, nan, nan, nan, nan],
+                       [nan, 5.0, 4.0, -inf, -inf],
+                       [-inf, -inf, -inf, 3.0, 3.0],
+                       [1.0, 1.0, 1.0, 1.0, 1.0]], np.float32)
+    selected, weights = oracle.route_select(scores, 3)
+    assert selected.tolist() == [[3, 1, 4], [0, 0, 0], [1, 2, 0], [3, 4, 0], [0, 1, 2]]
+    assert np.allclose(weights[0].sum(), 1.0) and np.allclose(weights[4], 1 / 3)
+    rng = np.random.default_rng(12)
+    for experts, top_k in ((40, 8), (70, 6), (8, 8)):
+        s = rng.choice(np.array([0.0, 1.0, 2.0, -1.0, nan, -inf, inf], np.float32), size=(24, experts))
+        s[::3] = rng.standard_normal((8, experts)).astype(np.float32)
+        s[5] = nan
+        want, _ = oracle.route_select(s, top_k)
+        for lanes in (32, 64):
+            assert np.array_equal(_route_select_lanes(s, top_k, lanes), want), (experts, lanes)
+
+
+def test_group_routes_verified():
+    """The verified grouping (moe.metal:164-173): routed routes of rows past their lane's verify count take no grouped
+    row and their route row is ~0u; the live ones are grouped as if the dead ones were absent; the shared slices hold
+    every row; a full count per lane is the plain grouping."""
+    rng = np.random.default_rng(21)
+    rows, experts, top_k, shared, tile_rows = 24, 16, 4, 1, 8
+    scores = rng.standard_normal((rows, experts)).astype(np.float32)
+    selected, _ = oracle.route_select(scores, top_k, oracle.ROUTER_SOFTMAX, shared)
+    plain = oracle.group_routes(selected, experts, tile_rows, shared)
+    full = oracle.group_routes(selected, experts, tile_rows, shared, verify_rows=[8, 8, 8])
+    for a, b in zip(plain, full):
+        assert np.array_equal(a, b)
+    verify = np.array([3, 0, 8], np.uint32)
+    tiles, grouped, route_rows = oracle.group_routes(selected, experts, tile_rows, shared, verify_rows=verify)
+    per_row = top_k + shared
+    live_row = np.array([r % 8 < verify[r // 8] for r in range(rows)])
+    for r in range(rows):
+        for k in range(per_row):
+            route = r * per_row + k
+            if k < top_k and not live_row[r]:
+                assert route_rows[route] == 0xFFFFFFFF
+            else:
+                assert grouped[route_rows[route]] == route
+                assert tiles[route_rows[route] // tile_rows, 0] == selected[r, k]
+    # the live routes alone, grouped plainly, give the same routed tiles
+    live = selected[live_row][:, :top_k]
+    counts = np.bincount(live.ravel(), minlength=experts)
+    routed_tiles = sum((c + tile_rows - 1) // tile_rows for c in counts)
+    assert tiles.shape[0] == routed_tiles + shared * 3
+    assert tiles[:routed_tiles, 1].sum() == live.size
 
 
 def test_group_routes_invariants():

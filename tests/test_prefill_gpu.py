@@ -7,10 +7,20 @@ import pytest
 
 import splash_q4 as sq
 import sq_oracle as oracle
-from helpers import Run, check_projection, dense_inputs, make_weights, sparse_inputs, to_device, torch
+from helpers import (DeviceAffine, Run, check_projection, dense_inputs, make_weights, sparse_inputs, staged_reference,
+                     to_device, torch)
 from splash_q4 import synthetic
 
 pytestmark = pytest.mark.gpu
+
+
+def no_worse_than_staged(got, x, w, stats, what):
+    """rel-L2 against fp64 no worse than the reference's staged numerics (fp16 weights, exact products, fp32 sums),
+    emulated on the CPU, beyond rounding-boundary noise."""
+    value, *_ = oracle.project_f64(x, w.values)
+    ref = synthetic.bf16_to_f32(staged_reference(x, w))
+    ref_l2 = np.linalg.norm(ref - value) / np.linalg.norm(value)
+    assert stats["rel_l2"] <= ref_l2 * 1.10 + 1e-6, f"{what}: {stats['rel_l2']} against the staged {ref_l2}"
 
 
 def run_prefill(w_list, x, epilogue=sq.EPILOGUE_NONE, residual=None, gate_scratch=None, n=None):
@@ -52,7 +62,8 @@ def test_prefill_dense(fmt, rows):
     n, k = 320, 1024   # five 64-column tiles: the last workgroup's second half lies past the projection
     w = make_weights(rng, fmt, n, k)
     x = dense_inputs(rng, rows, k)
-    check_projection(run_prefill([w], x), x, w, f"prefill fmt {fmt} rows {rows}")
+    stats = check_projection(run_prefill([w], x), x, w, f"prefill fmt {fmt} rows {rows}")
+    no_worse_than_staged(None, x, w, stats, f"prefill fmt {fmt} rows {rows}")
 
 
 def test_prefill_sparse_inputs_past_half_range():
@@ -91,7 +102,8 @@ def test_prefill_tall_tiles(fmt):
     n, k, rows = 32768, 1024, 520
     w = make_weights(rng, fmt, n, k)
     x = dense_inputs(rng, rows, k)
-    check_projection(run_prefill([w], x), x, w, f"prefill tall fmt {fmt}")
+    stats = check_projection(run_prefill([w], x), x, w, f"prefill tall fmt {fmt}")
+    no_worse_than_staged(None, x, w, stats, f"prefill tall fmt {fmt}")
 
 
 def test_prefill_fused_segments():
@@ -129,3 +141,55 @@ def test_short_prefill_runs_decode_tile():
     for rows in (1, 17, 32):
         x = dense_inputs(rng, rows, k)
         check_projection(run_prefill([w], x), x, w, f"short prefill {rows}")
+
+
+_SHAPE_CACHE = {}
+
+
+def shape_weights(fmt, n, k, seed):
+    """Weights of a BASELINE shape, built once per module: af4g64 through the library's MLX repack (DeviceAffine),
+    Q4_K through the oracle."""
+    key = (fmt, n, k, seed)
+    if key not in _SHAPE_CACHE:
+        _SHAPE_CACHE.clear()
+        rng = np.random.default_rng(seed)
+        _SHAPE_CACHE[key] = DeviceAffine(rng, n, k) if fmt == oracle.FMT_AF4G64 else make_weights(rng, fmt, n, k)
+    return _SHAPE_CACHE[key]
+
+
+def sampled_rows(rows, count, rng):
+    """The first and last rows, the last row of each 256-row tile and random others: every row tile kind is seen."""
+    pick = {0, rows - 1} | {min(rows - 1, t * 256 + 255) for t in range((rows + 255) // 256)}
+    pick |= set(rng.choice(rows, size=max(0, count - len(pick)), replace=False).tolist())
+    return np.array(sorted(pick))
+
+
+def check_sampled(out, x, w, what, rng, count=48):
+    """Every column of a sample of rows against fp64: the staged interval, BASELINE's tolerances and no worse than
+    the staged emulation."""
+    pick = sampled_rows(x.shape[0], count, rng)
+    stats = check_projection(out[pick], x[pick], w, what)
+    no_worse_than_staged(None, x[pick], w, stats, what)
+    return stats
+
+
+@pytest.mark.parametrize("n,k,rows", [(14336, 4096, 2048), (4096, 14336, 2048), (27648, 5120, 2048),
+                                      (14336, 4096, 2047)])
+def test_config2_prefill_shapes(n, k, rows):
+    """BASELINE config 2 at full size through the library's plan (its 256- and 128-row tiles as the launcher picks
+    them per shape), af4g64 with z = -8 s; 2047 rows leave the last row tile ragged."""
+    w = shape_weights(oracle.FMT_AF4G64, n, k, n + k)
+    rng = np.random.default_rng(n + rows)
+    x = dense_inputs(rng, rows, k)
+    out = run_prefill([w], x)
+    check_sampled(out, x, w, f"config 2 {k}x{n} rows {rows}", rng)
+
+
+def test_config3_q4k_prefill():
+    """BASELINE config 3's prefill point: Q4_K, K = 5120, N = 27648, M = 512."""
+    n, k, rows = 27648, 5120, 512
+    w = shape_weights(oracle.FMT_Q4K, n, k, 3)
+    rng = np.random.default_rng(512)
+    x = dense_inputs(rng, rows, k)
+    out = run_prefill([w], x)
+    check_sampled(out, x, w, "config 3 Q4_K rows 512", rng)
