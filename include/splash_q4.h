@@ -159,6 +159,17 @@ int sq_linear_add(void *graph, const sq_linear_buffers *buffers, const sq_projec
  * dispatch (the PreparedInput Linear::add returns, Linear.cpp:222-231). */
 int sq_linear_add_prepared(void *graph, const sq_linear_buffers *buffers, const sq_projection *projection,
                            const sq_linear_plan *plan, const sq_projection *gate, sq_prepared_input *prepared);
+/* No counterpart in the reference: Linear::add for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation). The same plans and kernels as sq_linear_add, but
+ * the split partials and counters, the prefill table and its row scales and the gate scratch come from a static
+ * array of SQ_STATIC_SCRATCH_BYTES per GPU inside the library (held from its first use on that GPU to the end of the
+ * process); buffers->scratch and buffers->gate_scratch are ignored and buffers->prepared must be empty. A plan whose
+ * scratch exceeds the array is refused (SQ_INVALID_ARGUMENT). Nothing is allocated: it launches a counter-clearing
+ * kernel, then the plan's dispatches. Every call on one GPU shares that GPU's array, so calls that overlap on one GPU
+ * (two streams, two threads) race; calls in one stream's order do not. */
+#define SQ_STATIC_SCRATCH_BYTES (16u << 20)
+int sq_linear_add_static(void *graph, const sq_linear_buffers *buffers, const sq_projection *projection,
+                         const sq_linear_plan *plan, const sq_projection *gate);
 /* LinearPlan::input (Linear.hpp:199-202): the layout the producer of the plan's input may write (SQ_LINEAR_INPUT_*):
  * HALF_ROWS for a prefill plan, PLAIN otherwise. */
 int sq_linear_plan_input(const sq_linear_plan *plan, uint32_t *layout);

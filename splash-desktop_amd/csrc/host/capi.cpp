@@ -3,6 +3,7 @@
 #include "../../../include/splash_q4.h"
 
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../kernels/kernels.hpp"
@@ -204,6 +205,97 @@ int sq_linear_add(void *graph, const sq_linear_buffers *b, const sq_projection *
                   const sq_projection *gate) {
   return sq_linear_add_prepared(graph, b, p, lp, gate, nullptr);
 }
+}  // extern "C"
+
+// ---- The entry point that allocates nothing (sq_linear_add_static)
+
+namespace {
+
+// The scratch of sq_linear_add_static: one array per GPU, held from the library's first use on that GPU to the end
+// of the process. In host code `scratch` names a host-side stand-in; kernels get the device address that
+// hipGetSymbolAddress gives, once per device (staticScratch).
+constexpr uint64_t kStaticScratchBytes = SQ_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+constexpr int kMaximumDevices = 64;
+std::mutex staticScratchMutex;
+void *staticScratchBase[kMaximumDevices] = {};
+
+void *staticScratch() {
+  int device = 0;
+  launched(hipGetDevice(&device), "static scratch device");
+  if (device < 0 || device >= kMaximumDevices) throw std::runtime_error("static scratch: device index out of range");
+  const std::lock_guard<std::mutex> lock(staticScratchMutex);
+  if (!staticScratchBase[device]) {
+    void *ptr = nullptr;
+    launched(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "static scratch address");
+    if (!ptr) throw std::runtime_error("static scratch address: null");
+    staticScratchBase[device] = ptr;
+  }
+  return staticScratchBase[device];
+}
+
+// Clears `words` counters before a dispatch: a fill kernel rather than a memset, so that a captured graph replays it
+// as a kernel node.
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t *words, uint32_t count) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i < count) words[i] = 0;
+}
+
+// The plan's scratch regions (counters, partials, the prefill table and its row scales, the gate scratch) at
+// 256-byte aligned offsets of the static array.
+struct StaticLayout {
+  uint64_t counters = 0, partials = 0, input = 0, sums = 0, gate = 0, end = 0;
+};
+StaticLayout staticLayout(const LinearScratchSize &s, uint64_t gateBytes) {
+  const auto round = [](uint64_t v) { return (v + 255) & ~uint64_t{255}; };
+  StaticLayout l;
+  l.partials = round(l.counters + s.counters);
+  l.input = round(l.partials + s.partials);
+  l.sums = round(l.input + s.input);
+  l.gate = round(l.sums + s.sums);
+  l.end = l.gate + gateBytes;
+  return l;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sq_linear_add_static(void *graph, const sq_linear_buffers *b, const sq_projection *p, const sq_linear_plan *lp,
+                         const sq_projection *gate) {
+  return guarded([&] {
+    const sq_linear_buffers &bb = need(b, "buffers");
+    const Projection proj = projection(need(p, "projection"));
+    const LinearPlan selected = plan(need(lp, "plan"));
+    if (bb.prepared.source.ptr || bb.prepared.source.bytes || bb.prepared.layout)
+      throw std::invalid_argument("the static-scratch entry point prepares its own table: buffers->prepared must be empty");
+    const LinearScratchSize sizes = selected.scratchSize();
+    const uint64_t gateBytes = selected.gateScratchBytes();
+    const StaticLayout l = staticLayout(sizes, gateBytes);
+    if (l.end > kStaticScratchBytes)
+      throw std::invalid_argument("the plan needs " + std::to_string(l.end) + " bytes of scratch; the static scratch holds " +
+                                  std::to_string(kStaticScratchBytes));
+    uint8_t *base = static_cast<uint8_t *>(staticScratch());
+    const auto region = [&](uint64_t offset, uint64_t bytes) { return bytes ? Buffer{base + offset, bytes} : Buffer{}; };
+    if (sizes.counters) {
+      const uint32_t words = uint32_t(sizes.counters / 4);
+      hipLaunchKernelGGL(zero_words_kernel, dim3((words + 255) / 256), dim3(256), 0, stream(graph),
+                         reinterpret_cast<uint32_t *>(base + l.counters), words);
+      launched(hipGetLastError(), "static scratch counters");
+    }
+    const LinearScratch sc{region(l.input, sizes.input), region(l.sums, sizes.sums),
+                           region(l.partials, sizes.partials), region(l.counters, sizes.counters), {}};
+    const LinearBuffers buffers{buf(bb.input), buf(bb.output), buf(bb.residual), region(l.gate, gateBytes), sc, {}};
+    const Linear linearOp(DeviceCapabilities{});
+    if (gate) {
+      const Projection g = projection(*gate);
+      linearOp.add(stream(graph), buffers, proj, selected, &g);
+    } else {
+      linearOp.add(stream(graph), buffers, proj, selected);
+    }
+  });
+}
+
 int sq_linear_plan_input(const sq_linear_plan *lp, uint32_t *layout) {
   return guarded([&] {
     if (!layout) throw std::invalid_argument("layout is null");

@@ -167,6 +167,8 @@ _SIGNATURES = {
     "sq_linear_add_prepared": [c_void_p, POINTER(LinearBuffers), POINTER(Projection), POINTER(LinearPlan),
                                POINTER(Projection), POINTER(PreparedInput)],
     "sq_linear_plan_input": [POINTER(LinearPlan), POINTER(c_uint32)],
+    "sq_linear_add_static": [c_void_p, POINTER(LinearBuffers), POINTER(Projection), POINTER(LinearPlan),
+                             POINTER(Projection)],
     "sq_norm_add_rms": [c_void_p, Buffer, POINTER(NormWeights), Buffer, c_uint32, c_uint32, POINTER(LinearScratch),
                         c_uint32, POINTER(PreparedInput)],
     "sq_float_add": [c_void_p, Buffer, POINTER(Segment), Buffer, c_uint32, c_uint32, c_uint32, c_uint32],

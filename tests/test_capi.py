@@ -372,3 +372,16 @@ def test_norm_and_float_rows_refusals():
     with pytest.raises(sq.InvalidArgument, match="outside its destination"):
         sq.call("sq_float_add", None, io, sq.byref(f32), _fake(rows * 64 * 4), rows, 64, 8, sq.OUTPUT_F32)
 
+
+def test_static_scratch_entry_point_refusals():
+    """sq_linear_add_static refuses, on the host and before touching any device, a plan whose scratch exceeds its
+    static array, and a prepared-input handoff (its table is its own)."""
+    proj = sq.projection(seg(14336, 4096))
+    plan = sq.plan_for(sq.prefill_workload(14336, 4096, 2048), proj)   # a 16 MiB fp16 table plus row scales
+    buffers = sq.LinearBuffers(_fake(2048 * 4096 * 2), _fake(2048 * 14336 * 2, 1 << 34), sq.Buffer(), sq.Buffer(),
+                               sq.LinearScratch())
+    with pytest.raises(sq.InvalidArgument, match="the static scratch holds 16777216"):
+        sq.call("sq_linear_add_static", None, sq.byref(buffers), sq.byref(proj), sq.byref(plan), None)
+    buffers.prepared = sq.PreparedInput(_fake(16), sq.LINEAR_INPUT_HALF_ROWS)
+    with pytest.raises(sq.InvalidArgument, match="prepared must be empty"):
+        sq.call("sq_linear_add_static", None, sq.byref(buffers), sq.byref(proj), sq.byref(plan), None)
