@@ -10,8 +10,11 @@
 //    activations (A) of the MFMA's sixteen blocks are broadcast from one block (cbsz 4, abid): lane (b, i) holds row
 //    i's inputs 4b..4b+3 of a pair of groups, so one 8-byte load per lane covers 64 inputs of up to four rows, and D
 //    gives each lane its own column for the four rows.
-//  - Each scale group closes in fp32: acc += s * sum x (128 + q) + (z - 128 s) * sum x, every product exact; the
-//    rows' input sums come from a wave butterfly over the same activation registers, read out into scalars.
+//  - Each scale group closes in fp32: acc += s * sum x (128 + q) + (z - 128 s) * sum x, every product exact. The
+//    rows' input sums of every group of the slice (of each half, for Q6_K) are summed once, before the slice's
+//    stream, by eight lanes a group in a fixed DPP tree, and parked in the wave's own LDS; a close reads them with one
+//    broadcast LDS read, so the stream's instructions are the operands, the MFMAs and the closes alone (the VALU
+//    issue of the operands is what bounds this tile: a wave64 VALU instruction holds its SIMD four cycles).
 //  - A workgroup of W waves takes one tile and W K slices of GW groups each (the split's last slice may be
 //    shorter; slices start on meta units). Each wave streams its slice with P groups in flight: codes, meta and
 //    activations are issued in the order they are consumed, every load unconditional (addresses past the slice
@@ -37,8 +40,11 @@ __device__ __forceinline__ float quad_sum(u32x2 v) {
   const float x2 = __uint_as_float(v[1] << 16), x3 = __uint_as_float(v[1] & 0xFFFF0000u);
   return (x0 + x1) + (x2 + x3);
 }
-__device__ __forceinline__ float lane_value(float v, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+// v combined with the lane that DPP control CTRL names (quad_perm [1,0,3,2]: lane ^ 1; [2,3,0,1]: lane ^ 2;
+// row_half_mirror: lane 7 - i within eight lanes).
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
 template <uint32_t FMT, int MR, int GW, int NT, uint32_t EP, bool F32OUT>
@@ -109,46 +115,46 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
       if constexpr (F::P1 == 8) highs[n][u] = __builtin_nontemporal_load((const u32x2 *)(high[n] + (size_t)g * 64 * F::P1));
     }
   };
+  // The rows' input sums of the slice's groups (of each half for Q6_K): lanes 8j..8j+7 take one (row, group), each
+  // lane four inputs, then a fixed tree over the eight lanes (quads first: the halves). Rows past the live ones and
+  // groups past the slice's sum to zero, which no close reads. Their inputs are loaded before the stream's first
+  // groups, so waiting for them waits for nothing else.
+  constexpr int NH = F::HALVES ? 2 : 1, kItems = MR * GW * 8, kIt = (kItems + 63) / 64;
+  __shared__ float xsum[kColumnMaxWaves][GW][NH][4];
+  u32x2 xq[kIt];
+#pragma unroll
+  for (int it = 0; it < kIt; ++it) {
+    const int item = it * 64 + lane, e = item & 7, g = (item >> 3) % GW, r = (item >> 3) / GW;
+    const bool use = item < kItems && (uint32_t)r < a.rows && (uint32_t)g < live;
+    xq[it] = use ? *(const u32x2 *)(a.input + (size_t)r * a.K + (size_t)(gb + g) * 32 + 4 * e) : u32x2{0u, 0u};
+  }
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int u = 0; u < P; ++u) issue(u);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int it = 0; it < kIt; ++it) {
+    const int item = it * 64 + lane, e = item & 7, g = (item >> 3) % GW, r = (item >> 3) / GW;
+    float v = quad_sum(xq[it]);
+    v = dpp_add<0xB1>(v);
+    v = dpp_add<0x4E>(v);
+    if (F::HALVES && item < kItems && e % 4 == 0) xsum[slice][g][e / 4][r] = v;
+    v = dpp_add<0x141>(v);
+    if (!F::HALVES && item < kItems && e == 0) xsum[slice][g][0][r] = v;
+  }
+  // The wave reads back what its own lanes wrote.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   f32x4 C0[NT], C1[NT], H0[NT], H1[NT];   // H: the high nibbles' chains of 8-bit codes
-  float pair_sum = 0.0f;   // lane's butterfly value of the current pair
-  float half_sum = 0.0f;   // the same over 16 inputs (Q6_K's scales cover halves of a group)
-  float sx[MR];            // the rows' input sums over the current scale group
-  float sh[2][MR];         // Q6_K: the rows' input sums over each half of the group
 #pragma unroll
   for (int u = 0; u < GW; ++u) {
     if (u + P < GW) issue(u + P);
     __builtin_amdgcn_sched_barrier(0);
     if ((uint32_t)u < live) {
       const int p = u >> 1, h = u & 1;
-      if (h == 0) {
-        float t = quad_sum(xp[p]);
-        t += __shfl_xor(t, 4);
-        t += __shfl_xor(t, 8);
-        half_sum = t;             // lanes b % 8 < 4: the first half's sum; b % 8 >= 4: the second's
-        t += __shfl_xor(t, 16);   // lanes b < 8: group 2p's sum; b >= 8: group 2p + 1's
-        if constexpr (SG > 1) t += __shfl_xor(t, 32);
-        pair_sum = t;
-      }
-      if constexpr (F::HALVES) {
-#pragma unroll
-        for (int r = 0; r < MR; ++r) {
-          sh[0][r] = lane_value(half_sum, 32 * h + r);
-          sh[1][r] = lane_value(half_sum, 32 * h + 16 + r);
-        }
-      } else if constexpr (SG == 1) {
-#pragma unroll
-        for (int r = 0; r < MR; ++r) sx[r] = lane_value(pair_sum, 32 * h + r);
-      } else if (h == 0) {
-#pragma unroll
-        for (int r = 0; r < MR; ++r) {
-          const float v = lane_value(pair_sum, r);
-          sx[r] = u % SG == 0 ? v : sx[r] + v;
-        }
-      }
       const bool first = u % SG == 0;
 #pragma unroll
       for (int n = 0; n < NT; ++n)
@@ -172,6 +178,19 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
           }
         }
       if ((u + 1) % SG == 0) {
+        // The rows' input sums of the scale group (of the group's halves for Q6_K), in group order.
+        float sx[MR], sh[2][MR];
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+          if constexpr (F::HALVES) {
+            sh[0][r] = xsum[slice][u][0][r];
+            sh[1][r] = xsum[slice][u][NH - 1][r];
+          } else {
+            sx[r] = xsum[slice][u + 1 - SG][0][r];
+#pragma unroll
+            for (int k = 1; k < SG; ++k) sx[r] += xsum[slice][u + 1 - SG + k][0][r];
+          }
+        }
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
           if constexpr (F::HALVES) {
