@@ -153,22 +153,47 @@ def time_graph(torch, launch, steps: int, warmup: int) -> float:
 
 def stream_floor(torch, sq, nbytes: int, steps: int, warmup: int) -> dict:
     """The read-only streaming kernel (sq_diag_stream_read) over `nbytes` from a ring of copies larger than the
-    Infinity Cache, timed like the headline GEMV: the HBM read rate one dispatch of that size reaches here."""
+    Infinity Cache, timed like the headline GEMV: the HBM read rate one dispatch of that size reaches here, best of
+    several launch shapes. Beside it, the dispatch floor: the same kernel over one 16-byte vector on the GEMV's grid
+    (224 x 1024), graph-replayed: the time a dispatch costs with nothing to read."""
     span = (nbytes + 4095) // 4096 * 4096
     copies = max(2, -(-RING_BYTES // span))
     ring = torch.empty(copies * span, dtype=torch.uint8, device="cuda").fill_(1)
-    sink = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    sink = torch.zeros(8192, dtype=torch.int32, device="cuda")
     results = {}
-    for workgroups, threads in ((224, 1024), (256, 1024), (512, 512), (1024, 256), (2048, 256)):
+    for workgroups, threads in ((224, 1024), (512, 256), (1024, 256), (2048, 256), (2048, 512), (4096, 512)):
         def launch(i, stream, workgroups=workgroups, threads=threads):
             copy = ring[(i % copies) * span:]
             sq.stream_read(copy, sink, workgroups, threads, nbytes=nbytes, stream=sq.c_void_p(stream))
         sec = time_graph(torch, launch, steps, warmup)
         results[f"{workgroups}x{threads}"] = round(nbytes / sec / 1e9, 1)
     best = max(results, key=results.get)
+
+    def empty(i, stream):
+        sq.stream_read(ring, sink, 224, 1024, nbytes=16, stream=sq.c_void_p(stream))
+    dispatch_us = time_graph(torch, empty, steps, warmup) * 1e6
     del ring, sink
     torch.cuda.empty_cache()
-    return {"GB/s": results[best], "launch": best, "bytes": nbytes, "by_launch": results}
+    return {"GB/s": results[best], "launch": best, "bytes": nbytes, "by_launch": results,
+            "dispatch_floor_us": round(dispatch_us, 3),
+            "bound_us": round(dispatch_us + nbytes / (HBM_PEAK_GBS * 1e3), 3)}
+
+
+def mfma_ceiling(torch, sq, steps: int, warmup: int) -> dict:
+    """The sustained f16 MFMA rate of this device (sq_diag_mfma_peak): one and two waves a SIMD on every compute
+    unit, eight independent 16x16x32 chains a wave, graph-replayed like the GEMM; in TFLOP/s."""
+    sink = torch.zeros(1024, dtype=torch.float32, device="cuda")
+    iterations, out = 4096, {}
+    for waves in (1, 2):
+        workgroups = 256 * waves
+
+        def launch(i, stream, workgroups=workgroups, waves=waves):
+            sq.call("sq_diag_mfma_peak", sq.c_void_p(stream), sq.view(sink), workgroups, waves, iterations)
+        sec = time_graph(torch, launch, max(4, steps // 4), max(1, warmup // 4))
+        flops = workgroups * 4 * iterations * 8 * 16384
+        out[f"{waves}_wave_per_simd"] = round(flops / sec / 1e12, 1)
+    out["best"] = max(out.values())
+    return out
 
 
 class Gemv:
@@ -361,12 +386,16 @@ def main() -> int:
                 log(f"  sweep K{kk} N{nn} M{mm}: {s * 1e6:.2f} us, {g:.0f} GB/s")
         extra["c1_decode_sweep_af4g64"] = sweep
     if "prefill" in sections:
+        ceiling = mfma_ceiling(torch, sq, args.steps, args.warmup)
+        log(f"  MFMA ceiling: {ceiling}")
+        extra["mfma_ceiling_tflops"] = ceiling
         prefill = {}
         for (kk, nn) in ((4096, 14336), (14336, 4096), (5120, 27648)):
             s = bench_prefill(torch, sq, synthetic, 2048, nn, kk, 10, 3)
             tf = 2 * 2048 * nn * kk / s / 1e12
             prefill[f"M2048_K{kk}xN{nn}"] = {"us": round(s * 1e6, 1), "TFLOPS": round(tf, 1),
-                                             "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 3)}
+                                             "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 3),
+                                             "frac_of_measured_ceiling": round(tf / ceiling["best"], 3)}
             log(f"  prefill K{kk} N{nn}: {s * 1e6:.0f} us, {tf:.0f} TFLOPS")
         extra["c2_prefill_af4g64"] = prefill
     if "q4k" in sections:

@@ -233,6 +233,11 @@ int sq_dequant(void *graph, const sq_segment *segment, sq_buffer values_f32, sq_
  * (bench.py). */
 int sq_diag_stream_read(void *graph, sq_buffer src, sq_buffer sink, uint32_t workgroups, uint32_t threads);
 
+/* No counterpart in the reference: `workgroups` workgroups of four waves (at most waves_per_simd, 1 or 2, resident a
+ * SIMD), each wave running `iterations` x 8 independent 16x16x32 f16 MFMAs (16384 flops each) on operands held in
+ * registers. The sustained MFMA ceiling the prefill GEMM is measured against (bench.py). */
+int sq_diag_mfma_peak(void *graph, sq_buffer sink, uint32_t workgroups, uint32_t waves_per_simd, uint32_t iterations);
+
 /* ---- MoE (runtime/ops/MoE.hpp:387-423) ---- */
 
 /* MoeRouter (MoE.hpp:22-28): Softmax weights the top_k routes by the softmax of their scores, SigmoidNormalized by

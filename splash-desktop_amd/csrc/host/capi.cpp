@@ -415,6 +415,18 @@ int sq_diag_stream_read(void *graph, sq_buffer src, sq_buffer sink, uint32_t wor
   });
 }
 
+int sq_diag_mfma_peak(void *graph, sq_buffer sink, uint32_t workgroups, uint32_t waves_per_simd,
+                      uint32_t iterations) {
+  return guarded([&] {
+    if (!workgroups || !iterations) throw std::invalid_argument("MFMA loop takes workgroups and iterations");
+    if (waves_per_simd != 1 && waves_per_simd != 2) throw std::invalid_argument("MFMA loop runs 1 or 2 waves a SIMD");
+    requireBytes(buf(sink), uint64_t{workgroups} * 4, "MFMA loop sink");
+    launched(sq::kern::launch_mfma_peak(workgroups, waves_per_simd, iterations, static_cast<float *>(sink.ptr),
+                                        stream(graph)),
+             "MFMA loop");
+  });
+}
+
 int sq_dequant(void *graph, const sq_segment *s, sq_buffer values, sq_buffer halves) {
   return guarded([&] {
     const QuantizedSegment q = segment(need(s, "segment"));

@@ -96,6 +96,8 @@ hipError_t launch_float_rows(const uint16_t *input, const void *weights, bool f3
                              uint32_t out_offset, hipStream_t stream);
 hipError_t launch_stream_read(const void *src, uint64_t bytes, uint32_t *sink, uint32_t workgroups, uint32_t threads,
                               hipStream_t stream);
+hipError_t launch_mfma_peak(uint32_t workgroups, uint32_t waves_per_simd, uint32_t iterations, float *sink,
+                            hipStream_t stream);
 hipError_t launch_mlx_repack(uint32_t fmt, const uint32_t *weight, const uint16_t *scales, const uint16_t *biases,
                              uint32_t rows, uint32_t K, uint8_t *plane0, uint8_t *meta, hipStream_t stream);
 

@@ -185,6 +185,7 @@ _SIGNATURES = {
     "sq_mlx_repack": [c_void_p, c_uint32, c_uint32, c_uint32, Buffer, Buffer, Buffer, Buffer, Buffer],
     "sq_dequant": [c_void_p, POINTER(Segment), Buffer, Buffer],
     "sq_diag_stream_read": [c_void_p, Buffer, Buffer, c_uint32, c_uint32],
+    "sq_diag_mfma_peak": [c_void_p, Buffer, c_uint32, c_uint32, c_uint32],
     "sq_moe_config_for": [POINTER(MoeShape), c_uint32, c_uint32, POINTER(MoeConfig)],
     "sq_moe_prefill_plan": [POINTER(MoeShape), c_uint32, POINTER(MoeConfig), POINTER(MoePlan)],
     "sq_moe_decode_plan": [POINTER(MoeShape), c_uint32, POINTER(MoeConfig), POINTER(MoePlan)],
