@@ -165,6 +165,51 @@ def cpu_matmul(fmt: int, x_bf16: np.ndarray, plane0: np.ndarray, meta: np.ndarra
     return out, secs
 
 
+class CpuPool:
+    """The CPU baseline's persistent thread pool (sq_cpu.c): started once, then matmul() runs y = x W^T on it and
+    returns the call's wall seconds. Buffers are reserved outside any timed call (reserve)."""
+
+    def __init__(self, threads: int):
+        L = lib()
+        L.sqo_pool_create.restype = ctypes.c_void_p
+        L.sqo_pool_create.argtypes = [ctypes.c_int]
+        L.sqo_pool_destroy.argtypes = [ctypes.c_void_p]
+        L.sqo_pool_threads.argtypes = [ctypes.c_void_p]
+        L.sqo_pool_isa.restype = ctypes.c_char_p
+        L.sqo_pool_isa.argtypes = [ctypes.c_void_p]
+        L.sqo_pool_reserve.argtypes = [ctypes.c_void_p, c_uint32, c_uint32]
+        L.sqo_pool_matmul.restype = ctypes.c_double
+        L.sqo_pool_matmul.argtypes = [ctypes.c_void_p, c_uint32, c_uint32, c_uint32, c_uint32, POINTER(c_uint16),
+                                      POINTER(c_uint8), POINTER(c_uint8), POINTER(c_uint16)]
+        self._lib = L
+        self._pool = L.sqo_pool_create(threads)
+        self.threads = L.sqo_pool_threads(self._pool)
+        self.isa = L.sqo_pool_isa(self._pool).decode()
+
+    def reserve(self, m: int, k: int) -> None:
+        if self._lib.sqo_pool_reserve(self._pool, m, k) != 0:
+            raise MemoryError("CPU baseline buffer")
+
+    def matmul(self, fmt: int, x_bf16: np.ndarray, plane0: np.ndarray, meta: np.ndarray, n: int, out=None):
+        """(bf16 bits [M][N], seconds); x must be reserved for (see reserve)."""
+        m, k = x_bf16.shape
+        out = np.zeros((m, n), np.uint16) if out is None else out
+        secs = self._lib.sqo_pool_matmul(self._pool, fmt, m, n, k,
+                                         _ptr(np.ascontiguousarray(x_bf16, np.uint16), c_uint16),
+                                         _ptr(plane0, c_uint8), _ptr(meta, c_uint8), _ptr(out, c_uint16))
+        if secs < 0:
+            raise ValueError("the CPU baseline does not take this format or shape")
+        return out, secs
+
+    def close(self) -> None:
+        if self._pool:
+            self._lib.sqo_pool_destroy(self._pool)
+            self._pool = None
+
+    def __del__(self):
+        self.close()
+
+
 ROUTER_SOFTMAX, ROUTER_SIGMOID_NORMALIZED = 0, 1
 
 

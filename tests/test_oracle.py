@@ -548,3 +548,36 @@ def test_mlx_fixture_values_bit_exact_8bit(group):
         for b in range(k // group):
             blk = native[(r * (k // group) + b) * f["block_bytes"]:][: f["block_bytes"]]
             assert np.array_equal(blk[4:], codes[r, b * group:(b + 1) * group])
+
+
+@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K, oracle.FMT_AF4G32, oracle.FMT_AF4G128])
+@pytest.mark.parametrize("m", [1, 3, 19])
+def test_cpu_pool_matches_fp64(fmt, m):
+    """The vectorised CPU baseline (thread pool, AVX-512 or AVX2 kernels) agrees with the fp64 projection within the
+    accumulation bound plus one bf16 rounding of the output, for row counts around its eight-row blocks."""
+    rng = np.random.default_rng(50 + fmt + m)
+    n, k = 192, 1024
+    if fmt == oracle.FMT_Q4K:
+        native = oracle.fixture(fmt, n, k, 23)
+    else:
+        group = {oracle.FMT_AF4G32: 32, oracle.FMT_AF4G64: 64, oracle.FMT_AF4G128: 128}[fmt]
+        codes = rng.integers(0, 16, (n, k), dtype=np.uint8)
+        w = np.bitwise_or.reduce(codes.reshape(n, k // 8, 8).astype(np.uint32)
+                                 << (np.arange(8, dtype=np.uint32) * 4), axis=2).astype(np.uint32)
+        s = (np.abs(rng.standard_normal((n, k // group))).astype(np.float32) * np.float32(0.02)).view(np.uint32) >> 16
+        z = ((np.float32(-8) * (s << 16).view(np.float32)).view(np.uint32) >> 16).astype(np.uint16)
+        native = oracle.mlx_native(fmt, w, s.astype(np.uint16), z, n, k)
+    plane0, meta, values = oracle.repack(fmt, native, n, k)
+    x = (rng.standard_normal((m, k)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    pool = oracle.CpuPool(3)
+    pool.reserve(m, k)
+    out, secs = pool.matmul(fmt, x, plane0, meta, n)
+    pool.close()
+    assert secs > 0
+    got = (out.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    value, magnitude, inputs, largest = oracle.project_f64(x, values)
+    bound = oracle.projection_bound(magnitude, inputs, largest, False)
+    lo, hi = value - bound, value + bound
+    rb = lambda v: ((v.astype(np.float32).view(np.uint32) + 0x7FFF + ((v.astype(np.float32).view(np.uint32) >> 16) & 1))
+                    >> 16 << 16).view(np.float32)
+    assert np.all(got >= np.nextafter(rb(lo), -np.inf)) and np.all(got <= np.nextafter(rb(hi), np.inf))
