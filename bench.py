@@ -246,9 +246,10 @@ def bench_prefill(torch, sq, synthetic, m, n, k, steps, warmup, fmt=None):
 
 def bench_moe(torch, sq, synthetic, steps, warmup, rows=512, experts=128, top_k=8, hidden=2048, inter=768,
               fmt=None, formats=None, shared=0, gated=False, router=False):
-    """One MoE layer (sq_moe_add) per step: routing from the caller's scores (written once into the grouped-input
-    scratch, where the router's scores live), or with `router` the block's F32 router rows projected first; routed experts in `fmt` unless `formats` names a projection's own ("gate", "up", "down",
-    "shared_gate", ...). Returns (seconds, bytes of planes + router + activations in and out, flops)."""
+    """One MoE layer (sq_moe_add) per step: routing from the caller's scores (copied each step into the
+    grouped-input scratch, where the router's scores live), or with `router` the block's F32 router rows projected
+    first; routed experts in `fmt` unless `formats` names a projection's own ("gate", "up", "down", "shared_gate",
+    ...). Returns (seconds, bytes of planes + router + activations in and out, flops)."""
     fmt = sq.FMT_AF4G64 if fmt is None else fmt
     formats = formats or {}
     plan_parts = [("gate", experts * inter, hidden), ("up", experts * inter, hidden), ("down", experts * hidden, inter)]
@@ -277,18 +278,22 @@ def bench_moe(torch, sq, synthetic, steps, warmup, rows=512, experts=128, top_k=
     scores = np.zeros((rows, width), np.float32)
     scores[:, :experts] = synthetic.router_logits(rng, rows, experts)
     out = torch.empty((rows, hidden), dtype=torch.int16, device="cuda")
-    held = []
-    fields = []
+    held = {}
     for name in sq._MOE_WORKSPACE:
         nbytes = getattr(plan.workspace, name)
-        t = (torch.from_numpy(scores).cuda() if name == "grouped_input" else
-             torch.zeros(max(nbytes, 4) // 4 + 1, dtype=torch.int32, device="cuda") if nbytes else None)
-        held.append(t)
-        fields.append(sq.view(t))
-    buffers = sq.MoeBuffers(sq.view(x), sq.view(None), sq.view(out), sq.MoeScratch(*fields), sq.view(None))
+        held[name] = torch.zeros(max(nbytes, 4) // 4 + 1, dtype=torch.int32, device="cuda") if nbytes else None
+    # The routed work overwrites the grouped input (the scores' home) with the input rows, so a step without router
+    # rows starts with the caller writing its scores there, as a router projection would: a 16-byte-vector copy of
+    # rows x router width fp32 on the same stream, inside the timed step.
+    score_dev = torch.from_numpy(scores.reshape(-1)).cuda()
+    score_dst = held["grouped_input"].view(torch.float32)[:score_dev.numel()]
+    buffers = sq.MoeBuffers(sq.view(x), sq.view(None), sq.view(out),
+                            sq.MoeScratch(*[sq.view(held[n]) for n in sq._MOE_WORKSPACE]), sq.view(None))
     handle = sq.stream_handle()
 
     def step(i):
+        if not router:
+            score_dst.copy_(score_dev)
         sq.call("sq_moe_add", handle, sq.byref(buffers), sq.byref(weights), sq.byref(plan))
 
     sec = time_steps(torch, step, steps, warmup)

@@ -307,8 +307,10 @@ typedef struct sq_moe_weights {
 } sq_moe_weights;
 /* MoeScratch (MoE.hpp:225-245), sized by the plan's workspace. As in the reference, the router's fp32 scores live in
  * grouped_input, a row of the shape's router width (256 expert slots, or 512 past 256 experts:
- * sq_moe_router_width) per row; a block without router rows takes the caller's scores from there. The expert passes
- * read the input rows through the grouped routes, so grouped_input holds nothing else. */
+ * sq_moe_router_width) per row; a block without router rows takes the caller's scores from there. As the reference's
+ * gather does, the routed work (sq_moe_add_routed) then overwrites them, with the block's input rows in the expert
+ * tiles' read order; the gate/up pass reads those through the grouped routes. Every buffer here, and the block's
+ * input, output and residual, is 16-byte aligned. */
 typedef struct sq_moe_scratch {
   sq_buffer selected_experts, routing_weights, tile_descriptors, tile_count, grouped_routes, route_rows,
       grouped_input, expert_intermediate, expert_output;

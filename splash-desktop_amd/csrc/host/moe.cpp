@@ -11,9 +11,10 @@ void launched(hipError_t e, const char *what) {
   if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
 
-// MoE.cpp:64-84: the grouped rows' intermediates and outputs. The expert passes read the input rows straight through
-// the routes, so the grouped input holds only the router's fp32 scores, a row of routerWidth() per row, as the
-// reference parks them there until its gather overwrites them.
+// MoE.cpp:64-84: the grouped rows' intermediates and outputs. The grouped input holds the router's fp32 scores, a
+// row of routerWidth() per row, until the routed work overwrites them, as the reference's gather does, with the
+// block's input rows in the expert tiles' read order (the gate/up pass gathers through the routes as it reads, so
+// the rows are the block's, not the routes').
 MoeWorkspace workspaceFor(const MoeShape &shape, uint32_t rows, uint32_t tileRows) {
   if (!shape.valid()) throw std::invalid_argument("invalid MoE workspace shape");
   const uint64_t routes = uint64_t{rows} * shape.routesPerToken();
@@ -21,9 +22,10 @@ MoeWorkspace workspaceFor(const MoeShape &shape, uint32_t rows, uint32_t tileRow
   const uint64_t groupedRows = uint64_t{tiles} * tileRows;
   const uint32_t widest = std::max(shape.hiddenSize, shape.expertIntermediateSize);
   const uint64_t scoreBytes = uint64_t{rows} * shape.routerWidth() * 4;
+  const uint64_t inputBytes = uint64_t{rows} * shape.hiddenSize * 2;
   return {routes * 4, routes * 4, uint64_t{tiles} * sizeof(SqMoeTileDescriptor), sizeof(SqMoeTileCount),
-          groupedRows * 4, routes * 4, scoreBytes, groupedRows * shape.expertIntermediateSize * 2,
-          groupedRows * widest * 2};
+          groupedRows * 4, routes * 4, std::max(scoreBytes, inputBytes),
+          groupedRows * shape.expertIntermediateSize * 2, groupedRows * widest * 2};
 }
 
 // A routed or shared projection: `slots` experts (slices) of n rows of k inputs, each projection in a format of its
@@ -68,10 +70,13 @@ void validate(const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
   requireBytes(sc.groupedInput, need.groupedInput, "MoE grouped input");
   requireBytes(sc.expertIntermediate, need.expertIntermediate, "MoE expert intermediate");
   requireBytes(sc.expertOutput, need.expertOutput, "MoE expert output");
-  // The combine moves eight bf16 a lane.
+  // The combine and the input rows' reordering move eight bf16 a lane, the expert passes read 16-byte chunks of
+  // their input rows.
   const auto aligned = [](const Buffer &buffer) { return (reinterpret_cast<uintptr_t>(buffer.ptr) & 15u) == 0; };
-  if (!aligned(b.residual) || !aligned(b.output) || !aligned(sc.expertOutput))
-    throw std::invalid_argument("MoE output, residual and expert output buffers are 16-byte aligned");
+  if (!aligned(b.input) || !aligned(b.residual) || !aligned(b.output) || !aligned(sc.groupedInput) ||
+      !aligned(sc.expertIntermediate) || !aligned(sc.expertOutput))
+    throw std::invalid_argument(
+        "MoE input, output, residual, grouped input, expert intermediate and expert output buffers are 16-byte aligned");
   if (b.verifyRows) {
     // A verify step's rows are its lanes' blocks (MoE.cpp:467-475).
     if (plan.phase() != MoePhase::Decode) throw std::invalid_argument("only a verify step's MoE routes its verify rows");
@@ -188,7 +193,12 @@ void MoE::addRouted(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w,
   const auto gateUpFormats = [&](uint32_t mode) {
     return mode == 0 ? std::pair{w.gate.formatId, w.up.formatId} : std::pair{w.sharedGate.formatId, w.sharedUp.formatId};
   };
-  a.input = b.input.as<const uint16_t>();
+  // The block's input rows in the tiles' read order, over the router's scores (MoE.cpp:480-517 opens the same way
+  // with its gather).
+  launched(kern::launch_moe_input_rows(b.input.as<const uint16_t>(), plan.rows(), s.hiddenSize,
+                                       sc.groupedInput.as<uint16_t>(), graph),
+           "MoE input rows");
+  a.input = sc.groupedInput.as<const uint16_t>();
   a.K = s.hiddenSize;
   a.output_size = s.expertIntermediateSize;
   a.gather = 1;

@@ -108,13 +108,19 @@ hipError_t launch_moe_route_select(const float *scores, uint32_t score_stride, u
 hipError_t launch_moe_group(const uint32_t *selected, SqMoeTileDescriptor *tiles, SqMoeTileCount *tile_count,
                             uint32_t *grouped_routes, uint32_t *route_rows, const uint32_t *verify_rows,
                             const SqMoeGroupParams &params, uint32_t shared, hipStream_t stream);
+// The block's input rows [rows][K] in the expert tiles' read order (the table the expert passes read): 16-byte
+// chunk 4 g + c of a row holds inputs 32 g + 4 c .. +3 then 32 g + 16 + 4 c .. +3.
+hipError_t launch_moe_input_rows(const uint16_t *input, uint32_t rows, uint32_t K, uint16_t *table,
+                                 hipStream_t stream);
 // An expert pass over the grouped rows, tile by tile: gate_up: gate and up of each tile's expert in one pass over
 // input rows routes[row] / routes_per_row, out = bf16(bf16(up) silu(bf16(gate))); else one tensor, over those input
 // rows when `gather` (a gate or up of its own format) and over the grouped input rows otherwise, out = bf16(y), or
 // with `gate` set (the gate pass's bf16 output, [tiles * tile_rows][output_size]) bf16(bf16(y) silu(gate)), the
-// one-pass result bit for bit. Routed tiles (expert < experts) read the routed planes, expert e's rows from
-// slots[e] * output_size on; shared tiles (expert experts + s) the shared planes, slice s's rows s * output_size on.
-// `mode` picks the tiles a launch runs: 0 routed, 1 shared, 2 both (one format).
+// one-pass result bit for bit. Every pass reads its input rows in the read order of launch_moe_input_rows, and the
+// gathering passes (gate/up) write their rows in that order too, for the down pass; the down pass writes in column
+// order. Routed tiles (expert < experts) read the routed planes, expert e's rows from slots[e] * output_size on;
+// shared tiles (expert experts + s) the shared planes, slice s's rows s * output_size on. `mode` picks the tiles a
+// launch runs: 0 routed, 1 shared, 2 both (one format).
 struct MoeExpertArgs {
   const uint16_t *input;        // gate/up: the step's rows [rows][K]; down: grouped rows [tiles * tile_rows][K]
   const uint32_t *routes;       // gate/up: the route of each grouped row (~0u padding)

@@ -4,7 +4,9 @@
 //
 // CDNA4 mapping. Each expert pass is the decode row tile's exact-operand inner loop (rowtile.hpp) per expert tile:
 // a wave streams one 64-column plane tile of its expert over all of K against the tile's (at most 32) grouped
-// rows; an expert's other tiles read the same weights while they are still in L2.
+// rows; an expert's other tiles read the same weights while they are still in L2. The passes read their input rows
+// in the tile's read order (one 16-byte load per row block and group): the routed work opens by writing the block's
+// input rows in that order, and the gate/up pass writes the intermediate rows in it.
 #include "kernels.hpp"
 #include "rowtile.hpp"
 
@@ -265,15 +267,16 @@ __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDes
   for (int n = 0; n < NT; ++n) {
     plane[n] = (shared ? a.shared_plane0[n] : a.plane0[n]) + ((size_t)ptile * G * 64 + lane) * F::P0;
     high[n] = F::P1 ? (shared ? a.shared_plane1[n] : a.plane1[n]) + ((size_t)ptile * G * 64 + lane) * F::P1 : nullptr;
-    meta[n] = (shared ? a.shared_meta[n] : a.meta[n]) + ((size_t)ptile * (G / F::UNIT) * 64 + j) * F::META;
+    meta[n] = (shared ? a.shared_meta[n] : a.meta[n]) + ((size_t)ptile * (G / F::UNIT) * 64 + lane) * F::META;
   }
-  // Lane (j, q) of row block b reads row 16 b + j (row 0 past the tile's rows: nothing stores those results).
+  // Lane (j, q) of row block b reads row 16 b + j (row 0 past the tile's rows: nothing stores those results), its
+  // 16-byte chunk q of each group in the read order.
   const uint16_t *xrow[MB];
 #pragma unroll
   for (int b = 0; b < MB; ++b) {
     const uint32_t r = 16u * b + j < rows ? 16u * b + j : 0u;
     const uint32_t source = NT == 2 || a.gather ? a.routes[first_row + r] / a.routes_per_row : first_row + r;
-    xrow[b] = a.input + (size_t)source * a.K + 4 * q;
+    xrow[b] = a.input + (size_t)source * a.K + 8 * q;
   }
   float acc[NT][4][MB][4];
   clear(acc);
@@ -282,6 +285,9 @@ __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDes
   // waves a SIMD (expert_kernel), and each resident wave covers more of the others' dependency stalls.
   constexpr bool kShort = short_chunks<FMT, NT>();
   row_stream<FMT, MB, NT, 2, kShort ? 2 : 4, !kShort>(plane, high, meta, xrow, G, acc);
+  // Column 16 t + j of the tile: the gathering passes store it at its place in the read order (chunk 4 g + j / 4 of
+  // group g = 2 ct + t / 2, then position 4 (t % 2) + j % 4), for the down pass; the down pass in column order.
+  const uint32_t column = a.gather ? 8 * (j >> 2) + (j & 3) : j;
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -290,7 +296,8 @@ __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDes
       for (int i = 0; i < 4; ++i) {
         const uint32_t r = 16u * b + 4u * q + i;
         if (r >= rows) continue;
-        const size_t at = (size_t)(first_row + r) * a.output_size + ct * 64 + 16 * t + j;
+        const uint32_t c = a.gather ? 32 * (t >> 1) + 4 * (t & 1) + column : 16 * t + column;
+        const size_t at = (size_t)(first_row + r) * a.output_size + ct * 64 + c;
         if constexpr (NT == 2) {
           const float g = bf16_to_f32(f32_to_bf16(acc[0][t][b][i])), u = bf16_to_f32(f32_to_bf16(acc[1][t][b][i]));
           a.output[at] = f32_to_bf16(u * silu(g));
@@ -363,6 +370,22 @@ void expert_kernel(MoeExpertArgs a) {
   else expert_tile<FMT, MB, NT>(a, d, tile, ct);
 }
 
+// Thread: one group of 32 inputs, its four 16-byte chunks of the table (chunk c: 4-input units c and c + 4 of the
+// group, the prefill's half rows order, half_rows.hpp) from the group's four 16-byte vectors in input order (the
+// reference's routed pass opens with its gather of the input rows into the grouped input, MoE.cpp:480-517; here the
+// rows keep their order and the gate/up pass gathers through the routes as it reads).
+__global__ __launch_bounds__(256) void input_rows_kernel(const uint16_t *input, uint64_t groups, uint16_t *table) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;   // group i of 32 inputs, rows back to back
+  if (i >= groups) return;
+  const u32x4 *in = (const u32x4 *)(input + 32 * i);
+  u32x4 *out = (u32x4 *)(table + 32 * i);
+  const u32x4 a = in[0], b = in[1], c = in[2], d = in[3];   // inputs 0..7, 8..15, 16..23, 24..31
+  out[0] = u32x4{a[0], a[1], c[0], c[1]};                    // chunk c: units c and c + 4
+  out[1] = u32x4{a[2], a[3], c[2], c[3]};
+  out[2] = u32x4{b[0], b[1], d[0], d[1]};
+  out[3] = u32x4{b[2], b[3], d[2], d[3]};
+}
+
 // out[r][d] = bf16(residual + sum_slot w_slot * expert_out[route_rows[slot]][d]) in slot order (moe.metal:480-505).
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *expert_output, const uint32_t *route_rows,
                                                       const float *weights, const uint16_t *residual,
@@ -422,6 +445,15 @@ hipError_t launch_moe_group(const uint32_t *selected, SqMoeTileDescriptor *tiles
                             const SqMoeGroupParams &p, uint32_t shared, hipStream_t stream) {
   hipLaunchKernelGGL(group_kernel, dim3(1), dim3(512), 0, stream, selected, tiles, tile_count, grouped_routes,
                      route_rows, verify_rows, p, shared);
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_input_rows(const uint16_t *input, uint32_t rows, uint32_t K, uint16_t *table,
+                                 hipStream_t stream) {
+  if (K % 32) return hipErrorInvalidValue;
+  const uint64_t groups = (uint64_t)rows * (K / 32);
+  hipLaunchKernelGGL(input_rows_kernel, dim3((uint32_t)((groups + 255) / 256)), dim3(256), 0, stream, input, groups,
+                     table);
   return hipGetLastError();
 }
 

@@ -246,10 +246,27 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
   }
 }
 
+// Column 16 t + j's meta at lane (j, q), from the lanes that loaded their own column's (lane l holds column l's):
+// ds_bpermute through the LDS crossbar (no LDS memory, not the VALU), one per word of the format's meta.
+template <uint32_t FMT>
+__device__ __forceinline__ MetaWords spread_meta(const MetaWords &own, int t, int j) {
+  constexpr int W = (Fmt<FMT>::META + 3) / 4;
+  MetaWords m{};
+  const int from = (16 * t + j) * 4;
+#pragma unroll
+  for (int w = 0; w < W; ++w) m.w[w] = (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)own.w[w]);
+  return m;
+}
+
 // Adds all G groups of NT tensors' plane tiles to acc, as row_slice does, in one continuous stream: chunks of CH
 // groups, each chunk's loads (clamped to the last group, so every chunk issues as many) issued SETS - 1 chunks
 // ahead into a ring of SETS register sets; AHEAD builds each group's operands a group ahead (else just before its
-// MFMAs). plane[n], high[n], meta[n] and xrow[b] point at group 0 for the lane.
+// MFMAs). plane[n] and high[n] point at group 0 for the lane, meta[n] at unit 0 of the lane's own column l (one
+// load per unit and tensor, spread_meta hands each lane the columns its MFMA blocks hold). The input rows come in the
+// tile's read order
+// (16-byte chunk 4 g + c of a row: inputs 32 g + 4 c .. +3 then 32 g + 16 + 4 c .. +3), so each group of a row block
+// is one 16-byte load a lane, half the vector memory instructions of two 8-byte loads from a row in input order:
+// xrow[b] points at chunk q of group 0 of the lane's row 16 b + j.
 template <uint32_t FMT, int MB, int NT, int SETS = 2, int CH = 4, bool AHEAD = true>
 __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], const uint8_t *const (&high)[NT],
                                            const uint8_t *const (&meta)[NT], const uint16_t *const (&xrow)[MB],
@@ -262,17 +279,13 @@ __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], co
   const uint32_t hshift = row_high_shift<FMT>(threadIdx.x & 63);
   u32x4 xv[SETS][MB][CH];
   RowGroup<FMT> codes[SETS][NT][CH];
-  MetaWords mw[SETS][NT][4][MU];
+  MetaWords own[SETS][NT][MU];
   const auto issue = [&](uint32_t c, int set) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const uint32_t g = min(c * CH + u, last);
 #pragma unroll
-      for (int b = 0; b < MB; ++b) {
-        const u32x2 lo = *(const u32x2 *)(xrow[b] + (size_t)g * 32);
-        const u32x2 hi = *(const u32x2 *)(xrow[b] + (size_t)g * 32 + 16);
-        xv[set][b][u] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-      }
+      for (int b = 0; b < MB; ++b) xv[set][b][u] = *(const u32x4 *)(xrow[b] + (size_t)g * 32);
 #pragma unroll
       for (int n = 0; n < NT; ++n) codes[set][n][u] = load_row_group<FMT>(plane[n], high[n], g);
     }
@@ -280,9 +293,7 @@ __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], co
     for (int m = 0; m < MU; ++m) {
       const uint32_t unit = min((c * CH) / UNIT + m, last / UNIT);
 #pragma unroll
-      for (int n = 0; n < NT; ++n)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) mw[set][n][t][m] = load_meta<FMT>(meta[n] + ((size_t)unit * 64 + 16 * t) * F::META);
+      for (int n = 0; n < NT; ++n) own[set][n][m] = load_meta<FMT>(meta[n] + (size_t)unit * 64 * F::META);
     }
   };
   f32x4 C[NT][4][MB], C2[NT][4][MB], S[MB], S2[MB];
@@ -295,7 +306,15 @@ __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], co
 #pragma unroll
     for (int n = 0; n < NT; ++n) row_operands<FMT>(codes[set][n][u], hshift, cc, lo[os][n], hi[os][n]);
   };
+  const int j = threadIdx.x & 15;
   const auto compute = [&](uint32_t c, int set, int next_set) __attribute__((always_inline)) {
+    MetaWords mw[NT][4][MU];
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int m = 0; m < MU; ++m) mw[n][t][m] = spread_meta<FMT>(own[set][n][m], t, j);
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const uint32_t g = c * CH + u;
@@ -316,7 +335,7 @@ __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], co
 #pragma unroll
           for (int n = 0; n < NT; ++n)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) m[n][t] = mw[set][n][t][UNIT < CH ? u / UNIT : 0];
+            for (int t = 0; t < 4; ++t) m[n][t] = mw[n][t][UNIT < CH ? u / UNIT : 0];
           row_group_close<FMT, MB, NT>(m, g, C, C2, S, S2, acc);
         }
       }

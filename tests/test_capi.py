@@ -207,11 +207,15 @@ def test_moe_plans_and_workspace():
     assert w.tile_descriptors == plan.maximum_tiles * 8 and w.tile_count == 40
     assert w.expert_intermediate == plan.maximum_tiles * 32 * 768 * 2
     assert w.expert_output == plan.maximum_tiles * 32 * 2048 * 2
-    # The router's scores live in the grouped input: a row of 256 expert slots per row (MoE.cpp:64-84).
-    assert w.grouped_input == 512 * 256 * 4 and sq.lib().sq_moe_router_width(sq.byref(shape)) == 256
+    # The grouped input holds the router's scores (a row of 256 expert slots per row) until the routed work
+    # overwrites them with the block's input rows in the tiles' read order (MoE.cpp:64-84).
+    assert w.grouped_input == max(512 * 256 * 4, 512 * 2048 * 2)
+    assert sq.lib().sq_moe_router_width(sq.byref(shape)) == 256
     wide = sq.MoeShape(2048, 300, 8, 768, sq.FMT_AF4G64)
     assert sq.lib().sq_moe_router_width(sq.byref(wide)) == 512
-    assert moe_plan("prefill", wide, 10).workspace.grouped_input == 10 * 512 * 4
+    assert moe_plan("prefill", wide, 10).workspace.grouped_input == max(10 * 512 * 4, 10 * 2048 * 2)
+    narrow = sq.MoeShape(256, 300, 8, 128, sq.FMT_AF4G64)   # the scores outweigh the input rows
+    assert moe_plan("prefill", narrow, 10).workspace.grouped_input == 10 * 512 * 4
     plan = moe_plan("prefill", shape, 8)
     assert plan.tile_rows == 8   # 8 rows x 8 routes <= 128 experts
     with pytest.raises(sq.InvalidArgument, match="invalid MoE workspace shape"):

@@ -89,9 +89,11 @@ def make_plan(shape, rows, phase):
 
 
 def run_moe(block, x, scores, top_k, residual=None, phase="prefill", verify=None):
-    """One sq_moe_add. The caller's router scores go where the reference's router writes them: the grouped-input
-    scratch, a row of the shape's router width per row (a block with router rows overwrites them). Returns the plan,
-    the scratch tensors and the bf16 output."""
+    """One MoE layer as sq_moe_add_routing then sq_moe_add_routed (sq_moe_add's two halves). The caller's router
+    scores go where the reference's router writes them: the grouped-input scratch, a row of the shape's router width
+    per row (a block with router rows overwrites them); they are read back between the halves, before the routed
+    work overwrites the grouped input with the input rows. Returns the plan, the scratch tensors and the bf16
+    output."""
     t = torch()
     rows = x.shape[0]
     shape = block.shape(top_k)
@@ -101,9 +103,9 @@ def run_moe(block, x, scores, top_k, residual=None, phase="prefill", verify=None
         nbytes = getattr(plan.workspace, name)
         scratch[name] = t.zeros(max(nbytes, 4) // 4 + 1, dtype=t.int32, device="cuda")
     width = sq.lib().sq_moe_router_width(sq.byref(shape))
-    assert plan.workspace.grouped_input == rows * width * 4
-    padded = np.full((rows, width), np.nan, np.float32)   # slots past the experts: no kernel reads them
-    padded[:, :block.e] = scores
+    assert plan.workspace.grouped_input == max(rows * width * 4, rows * block.h * 2)
+    padded = np.full(plan.workspace.grouped_input // 4, np.nan, np.float32)   # slots past the experts: unread
+    padded[:rows * width].reshape(rows, width)[:, :block.e] = scores
     scratch["grouped_input"] = t.from_numpy(padded).cuda()
     ms = sq.MoeScratch(*[sq.view(scratch[n]) for n in sq._MOE_WORKSPACE])
     xin = to_device(x)
@@ -111,9 +113,16 @@ def run_moe(block, x, scores, top_k, residual=None, phase="prefill", verify=None
     out = t.full((rows, block.h), -1, dtype=t.int16, device="cuda")
     vr = to_device(np.asarray(verify, np.uint32)) if verify is not None else None
     buffers = sq.MoeBuffers(sq.view(xin), sq.view(res), sq.view(out), ms, sq.view(vr))
-    sq.call("sq_moe_add", sq.stream_handle(), sq.byref(buffers), sq.byref(block.weights()), sq.byref(plan))
+    weights = block.weights()
+    sq.call("sq_moe_add_routing", sq.stream_handle(), sq.byref(buffers), sq.byref(weights), sq.byref(plan))
     t.cuda.synchronize()
-    scratch["scores"] = scratch["grouped_input"].cpu().numpy().view(np.float32).reshape(rows, width)[:, :block.e]
+    scratch["scores"] = scratch["grouped_input"].cpu().numpy().view(np.float32)[:rows * width].reshape(
+        rows, width)[:, :block.e].copy()
+    sq.call("sq_moe_add_routed", sq.stream_handle(), sq.byref(buffers), sq.byref(weights), sq.byref(plan))
+    t.cuda.synchronize()
+    # The routed work leaves the input rows in the tiles' read order in the grouped input.
+    table = to_host(scratch["grouped_input"], np.uint16)[:rows * block.h].reshape(rows, block.h // 32, 4, 2, 4)
+    assert np.array_equal(table.transpose(0, 1, 3, 2, 4).reshape(rows, block.h), np.asarray(x, np.uint16))
     return plan, scratch, to_host(out, np.uint16)
 
 
