@@ -37,7 +37,7 @@ __global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeA
   {
     const size_t pbase = ((size_t)tile * G * 64 + lane) * F::P0 + (size_t)gb * 64 * F::P0;
     const size_t hbase = ((size_t)tile * G * 64 + lane) * F::P1 + (size_t)gb * 64 * F::P1;
-    const size_t mbase = ((size_t)tile * units * 64 + j) * F::META + (size_t)(gb / F::UNIT) * 64 * F::META;
+    const size_t mbase = ((size_t)tile * units * 64 + lane) * F::META + (size_t)(gb / F::UNIT) * 64 * F::META;
     const Segment &first = NT == 2 ? a.gate : seg;
     plane[0] = first.plane0 + pbase;
     high[0] = F::P1 ? first.plane1 + hbase : nullptr;

@@ -177,10 +177,23 @@ __device__ __forceinline__ void row_group_close(const MetaWords (&mw)[NT][4], ui
     }
 }
 
+// Column 16 t + j's meta at lane (j, q), from the lanes that loaded their own column's (lane l holds column l's):
+// ds_bpermute through the LDS crossbar (no LDS memory, not the VALU), one per word of the format's meta.
+template <uint32_t FMT>
+__device__ __forceinline__ MetaWords spread_meta(const MetaWords &own, int t, int j) {
+  constexpr int W = (Fmt<FMT>::META + 3) / 4;
+  MetaWords m{};
+  const int from = (16 * t + j) * 4;
+#pragma unroll
+  for (int w = 0; w < W; ++w) m.w[w] = (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)own.w[w]);
+  return m;
+}
+
 // Adds GW groups (the first `live` of them) of NT tensors' plane tiles to acc[n][t][b][i] (tensor n, column
 // block t, row block b, row 4q + i of the block). plane[n] and high[n] point at the slice's first group for the
-// lane's column (load_row_group), meta[n] at its first meta unit for the lane (+ META j); xrow[b] at the lane's row
-// 16 b + j, inputs 4q of the slice's first group.
+// lane's column (load_row_group), meta[n] at its first meta unit for the lane's own column l (+ META l: one load per
+// unit and tensor, which spread_meta hands to the lanes whose MFMA blocks hold the column); xrow[b] at the lane's
+// row 16 b + j, inputs 4q of the slice's first group.
 template <uint32_t FMT, int MB, int GW, int NT>
 __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], const uint8_t *const (&high)[NT],
                                           const uint8_t *const (&meta)[NT], const uint16_t *const (&xrow)[MB],
@@ -199,7 +212,7 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
 
   u32x4 xv[MB][GW];
   RowGroup<FMT> codes[NT][GW];
-  MetaWords mw[NT][4][GW / UNIT];
+  MetaWords own[NT][GW / UNIT];
   const auto issue = [&](int u) __attribute__((always_inline)) {
     const uint32_t g = min((uint32_t)u, last);
 #pragma unroll
@@ -210,10 +223,7 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
     if (u % UNIT == 0) {
       const uint32_t v = min((uint32_t)(u / UNIT), last / UNIT);
 #pragma unroll
-      for (int n = 0; n < NT; ++n)
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          mw[n][t][u / UNIT] = load_meta<FMT>(meta[n] + ((size_t)v * 64 + 16 * t) * F::META);
+      for (int n = 0; n < NT; ++n) own[n][u / UNIT] = load_meta<FMT>(meta[n] + (size_t)v * 64 * F::META);
     }
 #pragma unroll
     for (int n = 0; n < NT; ++n) codes[n][u] = load_row_group<FMT>(plane[n], high[n], g);
@@ -222,40 +232,29 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
   for (int u = 0; u < P; ++u) issue(u);
 
   f32x4 C[NT][4][MB], C2[NT][4][MB], S[MB], S2[MB];
+  MetaWords mw[NT][4];   // the current unit's meta of column 16 t + j
+  const int j = threadIdx.x & 15;
 #pragma unroll
   for (int u = 0; u < GW; ++u) {
     if (u + P < GW) issue(u + P);
     __builtin_amdgcn_sched_barrier(0);
     if ((uint32_t)u < live) {
+      if (u % UNIT == 0) {
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) mw[n][t] = spread_meta<FMT>(own[n][u / UNIT], t, j);
+      }
       u32x4 x[MB], lo[NT][4], hi[NT][4];
 #pragma unroll
       for (int b = 0; b < MB; ++b) x[b] = xv[b][u];
 #pragma unroll
       for (int n = 0; n < NT; ++n) row_operands<FMT>(codes[n][u], hshift, cc, lo[n], hi[n]);
       row_group_mfma<FMT, MB, NT>(x, lo, hi, u % SG == 0, C, C2, S, S2);
-      if ((u + 1) % SG == 0) {
-        MetaWords m[NT][4];
-#pragma unroll
-        for (int n = 0; n < NT; ++n)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) m[n][t] = mw[n][t][u / UNIT];
-        row_group_close<FMT, MB, NT>(m, u, C, C2, S, S2, acc);
-      }
+      if ((u + 1) % SG == 0) row_group_close<FMT, MB, NT>(mw, u, C, C2, S, S2, acc);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
-}
-
-// Column 16 t + j's meta at lane (j, q), from the lanes that loaded their own column's (lane l holds column l's):
-// ds_bpermute through the LDS crossbar (no LDS memory, not the VALU), one per word of the format's meta.
-template <uint32_t FMT>
-__device__ __forceinline__ MetaWords spread_meta(const MetaWords &own, int t, int j) {
-  constexpr int W = (Fmt<FMT>::META + 3) / 4;
-  MetaWords m{};
-  const int from = (16 * t + j) * 4;
-#pragma unroll
-  for (int w = 0; w < W; ++w) m.w[w] = (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)own.w[w]);
-  return m;
 }
 
 // Adds all G groups of NT tensors' plane tiles to acc, as row_slice does, in one continuous stream: chunks of CH
