@@ -229,8 +229,9 @@ int sq_dequant(void *graph, const sq_segment *segment, sq_buffer values_f32, sq_
 /* ---- measurement ---- */
 
 /* No counterpart in the reference: a read-only stream of src (whole 16-byte vectors) by `workgroups` workgroups of
- * `threads` threads, each folding what it reads into its word of sink. The HBM floor the GEMV is measured against
- * (bench.py). */
+ * `threads` threads, thread g folding vectors g, g + S, g + 2S, ... (S = workgroups * threads). A workgroup's word of
+ * sink is written only when one of its threads' folds equals the marker word 0x9E3779B9 (the thread's index + 1), so
+ * no store is timed. The HBM floor the GEMV is measured against (bench.py). */
 int sq_diag_stream_read(void *graph, sq_buffer src, sq_buffer sink, uint32_t workgroups, uint32_t threads);
 
 /* No counterpart in the reference: `workgroups` workgroups of four waves (at most waves_per_simd, 1 or 2, resident a

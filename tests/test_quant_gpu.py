@@ -82,19 +82,30 @@ def test_repack_rejects_bad_chunks():
 
 
 def test_stream_read_folds_every_word():
-    """The measurement stream reads every 16-byte vector of its source: each workgroup's word is the xor of its
-    share (4 workgroups, a share not a multiple of the launch width)."""
+    """The measurement stream reads every 16-byte vector of its share: thread g of the grid folds vectors g, g + S,
+    g + 2S, ... (S the launch width; pairs, then a last single), and records itself in its workgroup's sink word only
+    when they fold to the marker word. Chosen threads get vectors that fold to it only if every one is read, the
+    others zeros (4 workgroups of 256 threads over 5000 vectors, not a multiple of the width; thread 5 ends on a
+    single, thread 1023 on a pair)."""
     t = torch()
     rng = np.random.default_rng(21)
-    words = rng.integers(0, 2**32, size=4 * 5000, dtype=np.uint32)
-    src = to_device(words.view(np.uint8))
-    sink = t.zeros(4, dtype=t.int32, device="cuda")
-    sq.stream_read(src, sink, 4, 256)
-    got = to_host(sink, np.int32).view(np.uint32)
-    vectors = words.reshape(-1, 4)
-    share = -(-len(vectors) // 4)
-    want = [np.bitwise_xor.reduce(vectors[w * share:(w + 1) * share].ravel()) for w in range(4)]
-    assert got.tolist() == [int(v) for v in want]
+    grid, threads, n, marker = 4, 256, 5000, 0x9E3779B9
+    stride = grid * threads
+    words = np.zeros((n, 4), np.uint32)
+    picks = [5, 256 + 200, 1023]
+    for g in picks:
+        share = np.arange(g, n, stride)
+        words[share] = rng.integers(0, 2**32, size=(len(share), 4), dtype=np.uint32)
+        words[share[-1], 0] ^= np.bitwise_xor.reduce(words[share].ravel()) ^ np.uint32(marker)
+        assert np.bitwise_xor.reduce(words[share].ravel()) == marker
+        assert np.bitwise_xor.reduce(words[share[:-1]].ravel()) != marker
+    src = to_device(words.reshape(-1).view(np.uint8))
+    sink = t.zeros(grid, dtype=t.int32, device="cuda")
+    sq.stream_read(src, sink, grid, threads)
+    want = [0] * grid
+    for g in picks:
+        want[g // threads] = g % threads + 1
+    assert to_host(sink, np.int32).tolist() == want
 
 
 NEW_FORMATS = [oracle.FMT_Q5K, oracle.FMT_Q6K, oracle.FMT_Q80, oracle.FMT_AF8G64]
