@@ -261,13 +261,18 @@ __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDes
   // The plane tile: routed expert e's from tile slots[e] of its projection on, shared slice s's from tile s of the
   // shared segment on.
   const bool shared = d.expert >= a.experts;
+  // A down pass of two tensor slots (pair) streams column tiles ct and ct + 1 of its one tensor, both against the
+  // same input loads.
+  const bool pair = NT == 2 && !a.gate_up;
   const uint32_t ptile = (shared ? d.expert - a.experts : a.slots[d.expert]) * column_tiles + ct;
   const uint8_t *plane[NT], *high[NT], *meta[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
-    plane[n] = (shared ? a.shared_plane0[n] : a.plane0[n]) + ((size_t)ptile * G * 64 + lane) * F::P0;
-    high[n] = F::P1 ? (shared ? a.shared_plane1[n] : a.plane1[n]) + ((size_t)ptile * G * 64 + lane) * F::P1 : nullptr;
-    meta[n] = (shared ? a.shared_meta[n] : a.meta[n]) + ((size_t)ptile * (G / F::UNIT) * 64 + lane) * F::META;
+    const int slot = pair ? 0 : n;
+    const size_t pt = ptile + (pair ? n : 0);
+    plane[n] = (shared ? a.shared_plane0[slot] : a.plane0[slot]) + (pt * G * 64 + lane) * F::P0;
+    high[n] = F::P1 ? (shared ? a.shared_plane1[slot] : a.plane1[slot]) + (pt * G * 64 + lane) * F::P1 : nullptr;
+    meta[n] = (shared ? a.shared_meta[slot] : a.meta[slot]) + (pt * (G / F::UNIT) * 64 + lane) * F::META;
   }
   // Lane (j, q) of row block b reads row 16 b + j (row 0 past the tile's rows: nothing stores those results), its
   // 16-byte chunk q of each group in the read order.
@@ -275,7 +280,7 @@ __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDes
 #pragma unroll
   for (int b = 0; b < MB; ++b) {
     const uint32_t r = 16u * b + j < rows ? 16u * b + j : 0u;
-    const uint32_t source = NT == 2 || a.gather ? a.routes[first_row + r] / a.routes_per_row : first_row + r;
+    const uint32_t source = a.gather ? a.routes[first_row + r] / a.routes_per_row : first_row + r;
     xrow[b] = a.input + (size_t)source * a.K + 8 * q;
   }
   float acc[NT][4][MB][4];
@@ -298,7 +303,10 @@ __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDes
         if (r >= rows) continue;
         const uint32_t c = a.gather ? 32 * (t >> 1) + 4 * (t & 1) + column : 16 * t + column;
         const size_t at = (size_t)(first_row + r) * a.output_size + ct * 64 + c;
-        if constexpr (NT == 2) {
+        if (pair) {
+          a.output[at] = f32_to_bf16(acc[0][t][b][i]);
+          a.output[at + 64] = f32_to_bf16(acc[NT - 1][t][b][i]);
+        } else if constexpr (NT == 2) {
           const float g = bf16_to_f32(f32_to_bf16(acc[0][t][b][i])), u = bf16_to_f32(f32_to_bf16(acc[1][t][b][i]));
           a.output[at] = f32_to_bf16(u * silu(g));
         } else if (a.gate) {
@@ -362,7 +370,7 @@ void expert_kernel(MoeExpertArgs a) {
   const uint32_t n = a.tile_count->tiles;
   if (blockIdx.y >= n) return;
   const uint32_t tile = longest_first_tile(a.tiles, n, blockIdx.y);
-  const uint32_t ct = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const uint32_t ct = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (NT == 2 && !a.gate_up ? 2 : 1);
   if (ct >= a.output_size / 64) return;
   const SqMoeTileDescriptor d = a.tiles[tile];
   if (a.mode != 2 && (d.expert >= a.experts) != (a.mode == 1)) return;
@@ -418,16 +426,21 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *expert_out
 
 template <uint32_t FMT, int MB, int NT>
 hipError_t launch_expert_rows(const MoeExpertArgs &a, hipStream_t stream) {
-  const dim3 grid((a.output_size / 64 + 3) / 4, a.max_tiles), block(256);
+  const uint32_t per = NT == 2 && !a.gate_up ? 8 : 4;   // column tiles a workgroup
+  const dim3 grid((a.output_size / 64 + per - 1) / per, a.max_tiles), block(256);
   hipLaunchKernelGGL((expert_kernel<FMT, MB, NT>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 
+// The down pass over 4-bit affine codes in groups of 32 or 64 streams column tiles in pairs (an even count of them):
+// each input load then serves two tiles, for the same registers as a gate/up pair (two waves a SIMD instead of three;
+// the pass is bound by its vector memory instructions more than by its waves: c4 174 -> 168 us).
 template <uint32_t FMT>
 hipError_t launch_expert_format(const MoeExpertArgs &a, hipStream_t stream) {
+  const bool pairs = affine4_short<FMT>() && !a.gate_up && !a.gather && (a.output_size / 64) % 2 == 0;
   if (a.tile_rows <= 16)
-    return a.gate_up ? launch_expert_rows<FMT, 1, 2>(a, stream) : launch_expert_rows<FMT, 1, 1>(a, stream);
-  return a.gate_up ? launch_expert_rows<FMT, 2, 2>(a, stream) : launch_expert_rows<FMT, 2, 1>(a, stream);
+    return a.gate_up || pairs ? launch_expert_rows<FMT, 1, 2>(a, stream) : launch_expert_rows<FMT, 1, 1>(a, stream);
+  return a.gate_up || pairs ? launch_expert_rows<FMT, 2, 2>(a, stream) : launch_expert_rows<FMT, 2, 1>(a, stream);
 }
 
 }  // namespace
