@@ -443,6 +443,16 @@ def main() -> int:
                 sweep[f"K{kk}xN{nn}_M{mm}"] = {"us": round(s * 1e6, 2), "GB/s": round(g, 1),
                                                "hbm_frac": round(g / HBM_PEAK_GBS, 3), "splits": p.config.splits}
                 log(f"  sweep K{kk} N{nn} M{mm}: {s * 1e6:.2f} us, {g:.0f} GB/s")
+        # The small shapes' floors: the streaming kernel over each M=1 point's own bytes (best launch shape) and the
+        # empty dispatch, timed alike. Below ~10 MB a dispatch's fixed cost is most of its time.
+        for (kk, nn) in ((4096, 4096), (4096, 1024)):
+            point = sweep[f"K{kk}xN{nn}_M1"]
+            f = stream_floor(torch, sq, int(gemv_bytes(1, nn, kk)), max(50, args.steps // 2), 10)
+            point["stream_floor_us"] = round(gemv_bytes(1, nn, kk) / f["GB/s"] / 1e3, 2)
+            point["dispatch_floor_us"] = f["dispatch_floor_us"]
+            point["frac_of_floor"] = round(point["stream_floor_us"] / point["us"], 3)
+            log(f"  stream floor K{kk} N{nn}: {point['stream_floor_us']} us ({f['launch']}), "
+                f"dispatch {f['dispatch_floor_us']} us")
         extra["c1_decode_sweep_af4g64"] = sweep
     if "prefill" in sections:
         ceiling = mfma_ceiling(torch, sq, args.steps, args.warmup)
