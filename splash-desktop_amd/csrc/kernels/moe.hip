@@ -128,11 +128,44 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
     const uint32_t row = i / p.top_k;
     return verify_rows != nullptr && row % p.lane_rows >= verify_rows[row / p.lane_rows];
   };
+  // When one chunk takes every row and a row has at most kHeld routes, each thread loads its routes' expert ids once
+  // (route tid + 512 k, k < top_k), counts them and sets their row bits in one pass, and ranks them from registers:
+  // one read of the selection instead of three. Otherwise the passes below each read it again.
+  constexpr uint32_t kHeld = 8;
+  const uint32_t routes = p.rows * p.top_k;
+  const bool one = p.rows <= kChunk && p.top_k <= kHeld;
+  uint32_t held[kHeld];
+#pragma unroll
+  for (uint32_t k = 0; k < kHeld; ++k) {
+    const uint32_t i = tid + 512 * k;
+    held[k] = one && i < routes && !dead(i) ? expert_of(i) : ~0u;   // ~0u: no live route
+  }
+  __shared__ uint32_t duplicated;
   counts[tid] = 0;
   running[tid] = 0;
+  if (one) {
+    for (uint32_t i = tid; i < p.experts * kWords; i += 512) bits[i] = 0;
+    if (tid == 0) duplicated = 0;
+  }
   __syncthreads();
-  for (uint32_t i = tid; i < p.rows * p.top_k; i += 512)
-    if (!dead(i)) atomicAdd(&counts[expert_of(i)], 1u);
+  if (one) {
+#pragma unroll
+    for (uint32_t k = 0; k < kHeld; ++k) {
+      const uint32_t i = tid + 512 * k;
+      if (i >= routes) continue;
+      if (held[k] == ~0u) {
+        route_rows[route_of(i)] = ~0u;
+        continue;
+      }
+      const uint32_t local = i / p.top_k, bit = 1u << (local % 32);
+      atomicAdd(&counts[held[k]], 1u);
+      // A bit already set names another route of the same row to the same expert (see below).
+      if (atomicOr(&bits[held[k] * kWords + local / 32], bit) & bit) duplicated = 1;
+    }
+  } else {
+    for (uint32_t i = tid; i < routes; i += 512)
+      if (!dead(i)) atomicAdd(&counts[expert_of(i)], 1u);
+  }
   __syncthreads();
   {
     // Exclusive prefix of the experts' tile counts: a scan within each wave, then over the eight wave totals.
@@ -157,13 +190,14 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
     for (uint32_t t = 0; t < n; ++t) tiles[first + t] = SqMoeTileDescriptor{tid, min(tr, c - t * tr)};
     for (uint32_t row = first * tr + c; row < (first + n) * tr; ++row) grouped_routes[row] = ~0u;
   }
-  __shared__ uint32_t duplicated;
   for (uint32_t chunk = 0; chunk < p.rows; chunk += kChunk) {
-    for (uint32_t i = tid; i < p.experts * kWords; i += 512) bits[i] = 0;
-    if (tid == 0) duplicated = 0;
-    __syncthreads();
     const uint32_t i0 = chunk * p.top_k, i1 = min(p.rows, chunk + kChunk) * p.top_k;
-    for (uint32_t i = i0 + tid; i < i1; i += 512) {
+    if (!one) {
+      for (uint32_t i = tid; i < p.experts * kWords; i += 512) bits[i] = 0;
+      if (tid == 0) duplicated = 0;
+      __syncthreads();
+    }
+    for (uint32_t i = i0 + tid; !one && i < i1; i += 512) {
       if (dead(i)) {
         route_rows[route_of(i)] = ~0u;
         continue;
@@ -185,14 +219,21 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
         }
       }
       __syncthreads();
-      for (uint32_t i = i0 + tid; i < i1; i += 512) {
-        if (dead(i)) continue;
-        const uint32_t r = route_of(i), e = expert_of(i), local = i / p.top_k - chunk;
+      const auto place = [&](uint32_t i, uint32_t e) __attribute__((always_inline)) {
+        const uint32_t r = route_of(i), local = i / p.top_k - chunk;
         uint32_t rank = running[e] + prefix[e * kWords + local / 32];
         rank += __popc(bits[e * kWords + local / 32] & ((1u << (local % 32)) - 1u));
         const uint32_t row = offsets[e] * tr + rank;
         grouped_routes[row] = r;
         route_rows[r] = row;
+      };
+      if (one) {
+#pragma unroll
+        for (uint32_t k = 0; k < kHeld; ++k)
+          if (tid + 512 * k < routes && held[k] != ~0u) place(tid + 512 * k, held[k]);
+      } else {
+        for (uint32_t i = i0 + tid; i < i1; i += 512)
+          if (!dead(i)) place(i, expert_of(i));
       }
       __syncthreads();
       if (tid < p.experts)
