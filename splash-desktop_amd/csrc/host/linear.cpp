@@ -1,5 +1,6 @@
 // ops::Linear over HIP: plan policy, validation and dispatch of the decode and prefill tiles.
 // Reference: runtime/ops/Linear.cpp:19-258 and runtime/ops/LinearGguf.cpp:396-923.
+#include <algorithm>
 #include <cmath>
 
 #include "../kernels/kernels.hpp"
@@ -67,7 +68,7 @@ char epilogueOf(LinearEpilogue e) { return e == LinearEpilogue::Residual ? 1 : e
 
 kern::Segment kernelSegment(const QuantizedSegment &s) {
   return {s.plane0.as<const uint8_t>(), s.meta.as<const uint8_t>(), s.outputSize / SQ_TILE_COLUMNS, s.columnOffset,
-          s.plane1.as<const uint8_t>()};
+          s.plane1.as<const uint8_t>(), s.formatId};
 }
 
 }  // namespace
@@ -395,7 +396,11 @@ PreparedInput Linear::add(hipStream_t graph, LinearBuffers b, const Projection &
     a.rows = w.rows;
     a.splits = config.splits;
     a.out_stride = n;
-    requireLaunch(kern::launch_decode(group.front()->formatId, epilogue, f32, a, graph), "decode tile");
+    // Segments of different formats run in one dispatch, each workgroup in its own segment's format.
+    uint32_t fmt = group.front()->formatId;
+    for (const QuantizedSegment *s : group)
+      if (s->formatId != fmt) fmt = kern::kSegmentFormats;
+    requireLaunch(kern::launch_decode(fmt, epilogue, f32, a, graph), "decode tile");
   };
   if (w.epilogue == LinearEpilogue::GateUp && config.oneGateUpPass) {
     const QuantizedSegment &g = gate->blocks().segments.front(), &u = segments.front();
@@ -424,6 +429,21 @@ PreparedInput Linear::add(hipStream_t graph, LinearBuffers b, const Projection &
     return b.prepared;
   }
   const Buffer aux = w.epilogue == LinearEpilogue::Residual ? b.residual : b.gateScratch;
+  if (segments.size() > 1 && segments.size() <= 3) {
+    // A fused projection's segments in one dispatch whatever their formats (LinearGguf.cpp:655-667), those with the
+    // most bytes per weight first so that their workgroups do not form the tail. Each tile computes what it does
+    // alone: the split and slices take whole meta units of every segment's format.
+    std::vector<const QuantizedSegment *> order;
+    for (const QuantizedSegment &s : segments) order.push_back(&s);
+    const auto bitsPerWeight = [](const QuantizedSegment *s) {
+      const SqQuantFormat f = s->format();
+      return (f.plane0_bytes + f.plane1_bytes) * 8.0 / 32.0 + f.meta_bytes * 8.0 / (32.0 * f.meta_groups);
+    };
+    std::stable_sort(order.begin(), order.end(),
+                     [&](const QuantizedSegment *x, const QuantizedSegment *y) { return bitsPerWeight(x) > bitsPerWeight(y); });
+    decode(order, kern::EpNone, b.output, {}, false);
+    return b.prepared;
+  }
   for (const auto &group : byFormat)
     decode(group, epilogueOf(w.epilogue), b.output, aux, selected.destination() == FloatOutput::Float32);
   return b.prepared;

@@ -20,19 +20,14 @@ namespace {
 // one tensor of 16 rows, 4 (512) for a gate/up pair of 32 rows, else 8 (256).
 constexpr uint32_t row_max_waves(int mb, int nt) { return mb == 1 && nt == 1 ? 16 : mb == 2 && nt == 2 ? 4 : 8; }
 
-template <uint32_t FMT, int MB, int GW, int NT, uint32_t EP, bool F32OUT>
-__global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeArgs a) {
+// Wave `slice`'s K slice (groups gb.. of which `live` are in the slice) of plane tile `tile` of segment `seg`, in
+// format FMT, into acc.
+template <uint32_t FMT, int MB, int GW, int NT>
+__device__ __forceinline__ void row_walk(const DecodeArgs &a, const Segment &seg, uint32_t tile, uint32_t gb,
+                                         uint32_t live, float (&acc)[NT][4][MB][4]) {
   using F = Fmt<FMT>;
-  constexpr int A = NT * 4 * MB * 4;   // accumulators per lane: tensor n, column block t, row block b, row i
   const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
-  const uint32_t slice = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), waves = blockDim.x >> 6;
-  const uint32_t split = blockIdx.y;
-  uint32_t tile = blockIdx.x, s = 0;
-  while (s + 1 < a.segments && tile >= a.seg[s].tiles) tile -= a.seg[s++].tiles;
-  const Segment seg = a.seg[s];
-  const uint32_t G = a.K >> 5, units = G / F::UNIT, gs = G / a.splits;
-  const uint32_t gb = split * gs + slice * GW, live = min((uint32_t)GW, gs - min(gs, slice * GW));
-
+  const uint32_t G = a.K >> 5, units = G / F::UNIT;
   const uint8_t *plane[NT], *high[NT], *meta[NT];
   {
     const size_t pbase = ((size_t)tile * G * 64 + lane) * F::P0 + (size_t)gb * 64 * F::P0;
@@ -56,9 +51,28 @@ __global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeA
     const uint32_t r = 16u * b + j;
     xrow[b] = a.input + (size_t)(r < a.rows ? r : 0) * a.K + 4 * q + (size_t)gb * 32;
   }
+  row_slice<FMT, MB, GW, NT>(plane, high, meta, xrow, live, acc);
+}
+
+// FMT kSegmentFormats: each workgroup runs its segment's format.
+template <uint32_t FMT, int MB, int GW, int NT, uint32_t EP, bool F32OUT>
+__global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeArgs a) {
+  constexpr int A = NT * 4 * MB * 4;   // accumulators per lane: tensor n, column block t, row block b, row i
+  const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
+  const uint32_t slice = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), waves = blockDim.x >> 6;
+  const uint32_t split = blockIdx.y;
+  uint32_t tile = blockIdx.x, s = 0;
+  while (s + 1 < a.segments && tile >= a.seg[s].tiles) tile -= a.seg[s++].tiles;
+  const Segment seg = a.seg[s];
+  const uint32_t G = a.K >> 5, gs = G / a.splits;
+  const uint32_t gb = split * gs + slice * GW, live = min((uint32_t)GW, gs - min(gs, slice * GW));
+
   float acc[NT][4][MB][4];
   clear(acc);
-  row_slice<FMT, MB, GW, NT>(plane, high, meta, xrow, live, acc);
+  if constexpr (FMT == kSegmentFormats)
+    with_format(seg.fmt, [&](auto f) { row_walk<decltype(f)::value, MB, GW, NT>(a, seg, tile, gb, live, acc); });
+  else
+    row_walk<FMT, MB, GW, NT>(a, seg, tile, gb, live, acc);
 
   // The slices meet in LDS: red[slice][n FO + f][lane], f = (t MB + b) 4 + i the accumulator of column block t, row
   // block b, row 4q + i of the block. Output f (of both tensors) belongs to wave f % waves, which adds it over the
@@ -194,13 +208,23 @@ DecodeLayout decode_layout(uint32_t fmt, uint32_t blocks, uint32_t K, uint32_t s
   return {0, 0};
 }
 
+uint32_t layout_format(uint32_t fmt, const DecodeArgs &args) {
+  if (fmt != kSegmentFormats) return fmt;
+  // Slices and splits that take whole meta units of the longest unit take whole units of every shorter one (units
+  // of 1, 2, 4 or 8 groups), so that format's layout is every segment's.
+  uint32_t widest = args.seg[0].fmt;
+  for (uint32_t s = 1; s < args.segments; ++s)
+    if (sq_format(args.seg[s].fmt).meta_groups > sq_format(widest).meta_groups) widest = args.seg[s].fmt;
+  return widest;
+}
+
 hipError_t launch_decode(uint32_t fmt, uint32_t epilogue, bool f32_output, const DecodeArgs &args,
                          hipStream_t stream) {
   if (args.rows <= kColumnTileRows) return launch_decode_column(fmt, epilogue, f32_output, args, stream);
   uint32_t tiles = 0;
   for (uint32_t s = 0; s < args.segments; ++s) tiles += args.seg[s].tiles;
   const bool pair = args.gate.plane0 != nullptr;
-  const DecodeLayout layout = decode_layout(fmt, tiles * 4, args.K, args.splits, pair, args.rows);
+  const DecodeLayout layout = decode_layout(layout_format(fmt, args), tiles * 4, args.K, args.splits, pair, args.rows);
   if (!layout.nb) return hipErrorInvalidValue;
   switch (fmt) {
     case SQ_FMT_AF4G32: return launch_format<SQ_FMT_AF4G32>(epilogue, f32_output, pair, args, tiles, layout, stream);
@@ -211,6 +235,9 @@ hipError_t launch_decode(uint32_t fmt, uint32_t epilogue, bool f32_output, const
     case SQ_FMT_Q6K: return launch_format<SQ_FMT_Q6K>(epilogue, f32_output, pair, args, tiles, layout, stream);
     case SQ_FMT_Q80: return launch_format<SQ_FMT_Q80>(epilogue, f32_output, pair, args, tiles, layout, stream);
     case SQ_FMT_AF8G64: return launch_format<SQ_FMT_AF8G64>(epilogue, f32_output, pair, args, tiles, layout, stream);
+    case kSegmentFormats:
+      if (epilogue != EpNone || f32_output || pair) return hipErrorInvalidValue;
+      return launch_rows<kSegmentFormats, 1, EpNone, false>(args, tiles, layout, stream);
     default: return hipErrorInvalidValue;
   }
 }

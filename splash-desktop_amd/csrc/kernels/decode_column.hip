@@ -47,8 +47,12 @@ __device__ __forceinline__ float dpp_add(float v) {
   return v + __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-template <uint32_t FMT, int MR, int GW, int NT, uint32_t EP, bool F32OUT>
-__global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs a) {
+// Wave `slice`'s K slice of plane tile `tile` of segment `seg` (K partition `split`), in format FMT, into acc; the
+// slice's input sums go through the wave's own xsum[slice] (NHS slots a group, at least the format's halves).
+template <uint32_t FMT, int MR, int GW, int NT, int NHS>
+__device__ __forceinline__ void column_walk(const DecodeArgs &a, const Segment &seg, uint32_t tile, uint32_t split,
+                                            uint32_t slice, float (&xsum)[kColumnMaxWaves][GW][NHS][4],
+                                            float (&acc)[NT][MR]) {
   using F = Fmt<FMT>;
   // Groups in flight: 8-bit codes of a gate/up pair (four 16-byte loads a group) keep two, to fit the registers of
   // a full workgroup.
@@ -56,11 +60,6 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
   constexpr int SG = F::SG, UNIT = F::UNIT, P = GW < kDepth ? GW : kDepth;
   static_assert(GW % UNIT == 0 && GW % 2 == 0 && GW % SG == 0, "a slice holds whole meta units and group pairs");
   const int lane = threadIdx.x & 63, b = lane >> 2, i = lane & 3;
-  const uint32_t slice = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), waves = blockDim.x >> 6;
-  const uint32_t split = blockIdx.y;
-  uint32_t tile = blockIdx.x, s = 0;
-  while (s + 1 < a.segments && tile >= a.seg[s].tiles) tile -= a.seg[s++].tiles;
-  const Segment seg = a.seg[s];
   const uint32_t G = a.K >> 5, units = G / UNIT, gs = G / a.splits;
   const uint32_t gb = split * gs + slice * GW, live = min((uint32_t)GW, gs - min(gs, slice * GW));
   const uint32_t last = live ? live - 1 : 0;
@@ -85,7 +84,6 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
   const uint16_t *xrow = a.input + (size_t)(i < MR && (uint32_t)i < a.rows ? i : 0) * a.K + 4 * (b & 7) + (size_t)gb * 32;
   const CodeConstants cc = make_code_constants();
 
-  float acc[NT][MR];
 #pragma unroll
   for (int n = 0; n < NT; ++n)
 #pragma unroll
@@ -120,7 +118,7 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
   // groups past the slice's sum to zero, which no close reads. Their inputs are loaded before the stream's first
   // groups, so waiting for them waits for nothing else.
   constexpr int NH = F::HALVES ? 2 : 1, kItems = MR * GW * 8, kIt = (kItems + 63) / 64;
-  __shared__ float xsum[kColumnMaxWaves][GW][NH][4];
+  static_assert(NH <= NHS, "the kernel's input-sum slots hold the format's halves");
   u32x2 xq[kIt];
 #pragma unroll
   for (int it = 0; it < kIt; ++it) {
@@ -221,6 +219,32 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
     }
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+template <uint32_t FMT>
+constexpr int xsum_halves() {
+  if constexpr (FMT == kSegmentFormats) return 2;
+  else return Fmt<FMT>::HALVES ? 2 : 1;
+}
+
+// FMT kSegmentFormats: each workgroup runs its segment's format.
+template <uint32_t FMT, int MR, int GW, int NT, uint32_t EP, bool F32OUT>
+__global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t slice = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), waves = blockDim.x >> 6;
+  const uint32_t split = blockIdx.y;
+  uint32_t tile = blockIdx.x, s = 0;
+  while (s + 1 < a.segments && tile >= a.seg[s].tiles) tile -= a.seg[s++].tiles;
+  const Segment seg = a.seg[s];
+  constexpr int NHS = xsum_halves<FMT>();
+  __shared__ float xsum[kColumnMaxWaves][GW][NHS][4];
+  float acc[NT][MR];
+  if constexpr (FMT == kSegmentFormats)
+    with_format(seg.fmt, [&](auto f) {
+      column_walk<decltype(f)::value, MR, GW, NT, NHS>(a, seg, tile, split, slice, xsum, acc);
+    });
+  else
+    column_walk<FMT, MR, GW, NT, NHS>(a, seg, tile, split, slice, xsum, acc);
 
   // Slices meet in LDS; row r's outputs (of both tensors) belong to wave r % waves, which adds them in slice order
   // and stores them (or stages them for the split reduce).
@@ -304,7 +328,7 @@ hipError_t launch_decode_column(uint32_t fmt, uint32_t epilogue, bool f32_output
   for (uint32_t s = 0; s < a.segments; ++s) tiles += a.seg[s].tiles;
   const bool pair = a.gate.plane0 != nullptr;
   // nb: the workgroup's waves (K slices), ks: a slice's groups of 32 inputs.
-  const DecodeLayout layout = decode_layout(fmt, tiles * 4, a.K, a.splits, pair, a.rows);
+  const DecodeLayout layout = decode_layout(layout_format(fmt, a), tiles * 4, a.K, a.splits, pair, a.rows);
   if (!a.rows || a.rows > kColumnTileRows || !layout.nb) return hipErrorInvalidValue;
   switch (fmt) {
     case SQ_FMT_AF4G32: return launch_format<SQ_FMT_AF4G32>(epilogue, f32_output, pair, a, tiles, layout, stream);
@@ -315,6 +339,9 @@ hipError_t launch_decode_column(uint32_t fmt, uint32_t epilogue, bool f32_output
     case SQ_FMT_Q6K: return launch_format<SQ_FMT_Q6K>(epilogue, f32_output, pair, a, tiles, layout, stream);
     case SQ_FMT_Q80: return launch_format<SQ_FMT_Q80>(epilogue, f32_output, pair, a, tiles, layout, stream);
     case SQ_FMT_AF8G64: return launch_format<SQ_FMT_AF8G64>(epilogue, f32_output, pair, a, tiles, layout, stream);
+    case kSegmentFormats:
+      if (epilogue != EpNone || f32_output || pair) return hipErrorInvalidValue;
+      return launch_rows<kSegmentFormats, 1, EpNone, false>(a, tiles, layout, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../abi.h"
 
 namespace sq::kern {
@@ -115,6 +117,23 @@ template <> struct Fmt<SQ_FMT_Q4K> { static constexpr int SG = 1, UNIT = 8, META
 template <> struct Fmt<SQ_FMT_Q5K> { static constexpr int SG = 1, UNIT = 8, META = 16, P0 = 16, P1 = 4, ZERO = 0, HALVES = 0; };
 template <> struct Fmt<SQ_FMT_Q6K> { static constexpr int SG = 1, UNIT = 8, META = 20, P0 = 16, P1 = 8, ZERO = 32, HALVES = 1; };
 template <> struct Fmt<SQ_FMT_Q80> { static constexpr int SG = 1, UNIT = 1, META = 2, P0 = 32, P1 = 0, ZERO = 0, HALVES = 0; };
+
+// fn(std::integral_constant<uint32_t, f>{}) for a format id f this build takes (a wave-uniform branch): how a
+// dispatch of segments in different formats runs each workgroup's own.
+template <class Fn>
+__device__ __forceinline__ void with_format(uint32_t f, Fn &&fn) {
+  switch (f) {
+    case SQ_FMT_AF4G32: fn(std::integral_constant<uint32_t, SQ_FMT_AF4G32>{}); break;
+    case SQ_FMT_AF4G64: fn(std::integral_constant<uint32_t, SQ_FMT_AF4G64>{}); break;
+    case SQ_FMT_AF4G128: fn(std::integral_constant<uint32_t, SQ_FMT_AF4G128>{}); break;
+    case SQ_FMT_AF8G64: fn(std::integral_constant<uint32_t, SQ_FMT_AF8G64>{}); break;
+    case SQ_FMT_Q4K: fn(std::integral_constant<uint32_t, SQ_FMT_Q4K>{}); break;
+    case SQ_FMT_Q5K: fn(std::integral_constant<uint32_t, SQ_FMT_Q5K>{}); break;
+    case SQ_FMT_Q6K: fn(std::integral_constant<uint32_t, SQ_FMT_Q6K>{}); break;
+    case SQ_FMT_Q80: fn(std::integral_constant<uint32_t, SQ_FMT_Q80>{}); break;
+    default: break;   // the host passes only the formats above
+  }
+}
 
 // The meta words one column needs for scale group `sg` (the meta unit that holds it): affine the (s, z) word,
 // Q4_K and Q5_K the 16-byte super-block header, Q6_K its 16 int8 scales and d, Q8_0 its half d.

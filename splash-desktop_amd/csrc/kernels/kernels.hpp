@@ -18,9 +18,12 @@ struct Segment {
   uint32_t tiles;
   uint32_t out_offset;
   const uint8_t *plane1;   // the high bits of Q5_K and Q6_K (null for the other formats)
+  uint32_t fmt;            // SQ_FMT_*: read by a decode dispatch of kSegmentFormats
 };
 
-// The decode tiles: y[r][c] = sum_k x[r][k] w[c][k] over up to three segments of one format. With gate.plane0 set,
+// The decode tiles: y[r][c] = sum_k x[r][k] w[c][k] over up to three segments of one format, or of any formats when
+// launch_decode is given kSegmentFormats (each workgroup then runs its own segment's format; no epilogue, bf16
+// output, the layout of the segments' longest meta unit, so each tile computes what it does alone). With gate.plane0 set,
 // gate (gate) and up (seg[0]) run in one pass and the output is bf16(bf16(up) silu(bf16(gate))). Split partials
 // are fp32 [split][rows][out_stride] (a gate/up pair's [split][rows][2 out_stride], gate's columns then up's);
 // counters one per workgroup column (grid.x, at most one per 16 destination columns), zero before and after each
@@ -30,6 +33,7 @@ struct Segment {
 //  - The row tile (more rows): grid (64-column tiles, splits) of up to 16 waves (fewer for more than 16 rows or a
 //    gate/up pair), rows on the MFMA's 16-row side.
 constexpr uint32_t kColumnTileRows = 4;
+constexpr uint32_t kSegmentFormats = 0xFFFFFFFFu;
 // The formats each tile runs: the decode column and row tiles, the prefill tile and the MoE expert passes, every
 // format this build takes.
 SQ_HD inline bool column_tile_format(uint32_t f) { return sq_format_supported(f); }
@@ -55,6 +59,8 @@ struct DecodeLayout {
   uint32_t nb, ks;
 };
 DecodeLayout decode_layout(uint32_t fmt, uint32_t blocks, uint32_t K, uint32_t splits, bool pair, uint32_t rows);
+// The format whose layout a dispatch takes: fmt, or for kSegmentFormats the segment format of the longest meta unit.
+uint32_t layout_format(uint32_t fmt, const DecodeArgs &args);
 hipError_t launch_decode(uint32_t fmt, uint32_t epilogue, bool f32_output, const DecodeArgs &args,
                          hipStream_t stream);
 hipError_t launch_decode_column(uint32_t fmt, uint32_t epilogue, bool f32_output, const DecodeArgs &args,

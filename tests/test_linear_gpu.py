@@ -191,6 +191,35 @@ def test_fused_segments_equal_segments_alone(rows):
     check_decode(fused, x, parts, "fused")
 
 
+MIXED = [(oracle.FMT_Q4K, oracle.FMT_Q4K, oracle.FMT_Q6K), (oracle.FMT_Q80, oracle.FMT_Q5K, oracle.FMT_AF4G32),
+         (oracle.FMT_AF8G64, oracle.FMT_AF4G128, oracle.FMT_AF4G64)]
+
+
+@pytest.mark.parametrize("formats", MIXED)
+@pytest.mark.parametrize("rows", [1, 3, 8, 20])
+@pytest.mark.parametrize("splits", [1, 4])
+def test_mixed_format_segments_in_one_dispatch(formats, rows, splits):
+    """Up to three segments of any formats run in one dispatch (the reference's fused decode takes a format per
+    segment: GgufDecodeFusedParams.fmt[3], Gguf.h:97-106), a Q4_K q|k with a Q6_K v among them. Each tile computes
+    what it does alone: the fused columns equal each segment run by itself at the same split."""
+    rng = np.random.default_rng(37 + 100 * rows + splits + formats[0])
+    k = 2048
+    parts = [make_weights(rng, f, n, k) for f, n in zip(formats, (128, 64, 192))]
+    x = dense_inputs(rng, rows, k)
+    total = sum(p.n for p in parts)
+    segs, offset = [], 0
+    for p in parts:
+        segs.append(p.segment(offset))
+        offset += p.n
+    fused = run_plan(staged(total, k, rows, splits), sq.projection(segs), x, total)
+    offset = 0
+    for p in parts:
+        alone = run_plan(staged(p.n, k, rows, splits), sq.projection(p.segment()), x, p.n)
+        assert np.array_equal(fused[:, offset:offset + p.n], alone), f"segment at {offset} ({p.fmt})"
+        offset += p.n
+    check_decode(fused, x, parts, f"mixed {formats} rows {rows} splits {splits}")
+
+
 def test_padding_columns_untouched():
     rng = np.random.default_rng(29)
     n, k, pad = 256, 1024, 256
