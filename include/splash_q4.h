@@ -89,7 +89,9 @@ typedef struct sq_linear_plan {
   uint32_t storage_rows;
 } sq_linear_plan;
 
-/* LinearScratch / LinearScratchSize / LinearBuffers (runtime/ops/Linear.hpp:125-162,216-226). */
+/* LinearScratch / LinearScratchSize / LinearBuffers (runtime/ops/Linear.hpp:125-162,216-226). A decode plan's
+ * partials hold its K splits' fp32 sums; a prefill plan's, where its tiles' K is halved (projections of 64 to 128
+ * tiles of 256 rows by 256 columns, K a multiple of 512), the two halves' fp32 sums [2][rows][N]. */
 typedef struct sq_linear_scratch_size {
   uint64_t input, sums, partials, counters, rotated;
 } sq_linear_scratch_size;
@@ -116,7 +118,8 @@ typedef struct sq_linear_buffers {
   sq_prepared_input prepared;
 } sq_linear_buffers;
 
-/* DeviceCapabilities, as far as the MI355X policy reads it; compute_units 0 takes 256. */
+/* DeviceCapabilities, as far as the MI355X policy reads it (the decode split law); compute_units 0 takes 256. The
+ * prefill tile's schedule is a function of the shape alone, for the MI355X's 256 compute units. */
 typedef struct sq_device {
   uint32_t compute_units;
 } sq_device;

@@ -181,12 +181,14 @@ uint32_t LinearPlan::storageRows() const noexcept {
 }
 
 // Decode tile: [split][row][column] fp32 partials and a counter per 64 destination columns (LinearGguf.cpp:432-453).
-// Prefill tile: the activations in fp16 and one fp32 scale per row, which its prepare dispatch writes.
+// Prefill tile: the activations in fp16 and one fp32 scale per row, which its prepare dispatch writes, and where the
+// projection halves its tiles' K the fp32 sums of both halves (kern::prefill_split).
 LinearScratchSize LinearPlan::scratchSize() const noexcept {
   const auto [n, k] = workload_.matrix;
   if (config_.tile == LinearTile::GgufPrefill) {
     const uint64_t rows = storageRows();
-    return {uint64_t{workload_.rows} * k * 2, rows * 4, 0, 0, 0};
+    const kern::PrefillScratch halves = kern::prefill_scratch_bytes(workload_.rows, n / SQ_TILE_COLUMNS, k);
+    return {uint64_t{workload_.rows} * k * 2, rows * 4, halves.partials, halves.counters, 0};
   }
   // Counters: one per workgroup column of the decode tile, at most one per 16 destination columns.
   const uint64_t columns = config_.oneGateUpPass ? 2 * uint64_t{n} : n;
@@ -377,7 +379,7 @@ PreparedInput Linear::add(hipStream_t graph, LinearBuffers b, const Projection &
       a.K = k;
       a.rows = w.rows;
       a.out_stride = n;
-      a.compute_units = computeUnits_;
+      a.partials = b.scratch.partials.as<float>();
       requireLaunch(kern::launch_prefill(group.front()->formatId, epilogueOf(w.epilogue), a, graph), "prefill tile");
     }
     return {b.input, LinearInput::HalfRows};

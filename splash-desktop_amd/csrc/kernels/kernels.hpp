@@ -78,9 +78,24 @@ struct PrefillArgs {
   uint16_t *output;            // bf16 [rows][out_stride]
   const uint16_t *aux;
   uint32_t K, rows, out_stride;
-  uint32_t compute_units;      // the device's, for the tile choice
+  float *partials;             // a split dispatch's fp32 halves (prefill_scratch_bytes)
 };
 hipError_t launch_prefill(uint32_t fmt, uint32_t epilogue, const PrefillArgs &args, hipStream_t stream);
+// The prefill dispatch's shape: tiles of bm rows (128 or 256) by four plane tiles, row_blocks x column_groups of
+// them, 64 inputs a step, one workgroup each; with `split` (prefill_split of the projection's rows, whole width and
+// K), two workgroups each, one per half of K, which store fp32 sums [2][rows][out_stride] to the partials for a close
+// dispatch that adds the halves in K order and applies the epilogue.
+constexpr uint32_t kPrefillUnits = 256, kPrefillSplitTiles = 64;   // an MI355X's compute units
+struct PrefillSchedule {
+  uint32_t bm, split, row_blocks, column_groups;
+};
+bool prefill_split(uint32_t rows, uint32_t plane_tiles, uint32_t K);
+PrefillSchedule prefill_schedule(uint32_t rows, uint32_t plane_tiles, uint32_t K, bool split);
+// The partials (and counters: none) a prefill of `rows` over a projection of `plane_tiles` plane tiles uses.
+struct PrefillScratch {
+  uint64_t partials, counters;
+};
+PrefillScratch prefill_scratch_bytes(uint32_t rows, uint32_t plane_tiles, uint32_t K);
 
 // Dequantisation of every weight of a segment's planes: fp32 fma(q, s, z) and the staged tile's fp16 rounding of
 // it, [N][K] each (either may be null).

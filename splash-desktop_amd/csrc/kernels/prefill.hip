@@ -24,6 +24,7 @@
 //    second half, in pieces of four weights between MFMAs.
 // LDS rows are 128 bytes whose 16-byte chunk c sits in slot c ^ (row % 8), so fragment reads (16 rows x one chunk
 // per 16 lanes) and the copies spread over all banks. One barrier a step.
+#include <algorithm>
 #include <type_traits>
 
 #include "device.hpp"
@@ -239,7 +240,8 @@ constexpr MicroTable make_micro_table() {
 constexpr MicroTable kMicroTable = make_micro_table();
 static_assert(kMicroTable.op[kMicro - 1].kind == 3 && kMicroTable.op[kMicro - 1].arg == 15, "52 micro-operations");
 
-template <uint32_t FMT, uint32_t EP, int BM>
+// SPLIT: the tile's K is halved between the two workgroups of blockIdx.z (prefill_schedule), which meet in fp32.
+template <uint32_t FMT, uint32_t EP, int BM, bool SPLIT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_kernel(PrefillArgs a) {
   using F = Fmt<FMT>;
   using S = StepSlot<FMT>;
@@ -260,6 +262,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t row0 = blockIdx.x * BM;
   const uint32_t G = a.K >> 5, units = G / F::UNIT, steps = a.K / BK;
+  // The workgroup's steps of the tile: all of them, or half z of them (a multiple of four steps, whole meta units of
+  // every format), run with their own numbers from 0 from plane and input pointers moved on by `first` steps.
+  const uint32_t first = SPLIT ? blockIdx.z * (steps / 2) : 0, n = SPLIT ? steps / 2 : steps;
 
   // The wave's plane tile. A grid whose tile count is not a multiple of 4 ends short: a spare wave runs tile 0 of
   // its segment and stores nothing.
@@ -269,11 +274,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const Segment seg = a.seg[s];
   // The lane's copy sources in the plane tile: 16-byte copies read 16 lane bytes on, dword copies 4 lane.
   const size_t tile = live ? ptile : 0;
-  const uint8_t *bplane = seg.plane0 + (tile * G * 64 * F::P0 + 16 * lane);
-  const uint8_t *bhigh16 = F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + 16 * lane) : nullptr;
-  const uint8_t *bhigh4 = F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + 4 * lane) : nullptr;
-  const uint8_t *bmeta16 = seg.meta + (tile * units * 64 * F::META + 16 * lane);
-  const uint8_t *bmeta4 = seg.meta + (tile * units * 64 * F::META + 4 * lane);
+  const size_t unit0 = F::UNIT == 1 ? 2 * first : 2 * first / F::UNIT;
+  const uint8_t *bplane = seg.plane0 + (tile * G * 64 * F::P0 + (size_t)first * S::code + 16 * lane);
+  const uint8_t *bhigh16 = F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + (size_t)first * S::high + 16 * lane) : nullptr;
+  const uint8_t *bhigh4 = F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + (size_t)first * S::high + 4 * lane) : nullptr;
+  const uint8_t *bmeta16 = seg.meta + ((tile * units + unit0) * 64 * F::META + 16 * lane);
+  const uint8_t *bmeta4 = seg.meta + ((tile * units + unit0) * 64 * F::META + 4 * lane);
+  const uint8_t *xin = (const uint8_t *)a.half_input + (size_t)first * BK * 2;
   uint8_t *const wave_slot = lds + kCodeBase + wave * S::wave;
   uint32_t mask = 0x0F0F0F0Fu;
   asm volatile("" : "+s"(mask));
@@ -291,7 +298,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   // Step `step`'s activations into stage `stage` (sources clamped to the last step: every step issues as many
   // copies, which the vmcnt waits count on).
   const auto copy_a = [&](uint32_t step, uint32_t stage) __attribute__((always_inline)) {
-    const uint8_t *from = (const uint8_t *)a.half_input + (size_t)min(step, steps - 1) * BK * 2;
+    const uint8_t *from = xin + (size_t)min(step, n - 1) * BK * 2;
 #pragma unroll
     for (int i = 0; i < BM / 32; ++i)
       copy_to_lds<16>(from + aoff[i], lds + stage * kStage + (kRowsPerWave * wave + 8 * i) * kRowBytes);
@@ -320,18 +327,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   // Step `step`'s codes, plane1 and meta into slot `slot` of this wave.
   const auto copy_b = [&](uint32_t step, uint32_t slot) __attribute__((always_inline)) {
 #pragma unroll
-    for (int k = 0; k < kBCopies; ++k) copy_b_one(min(step, steps - 1), k, wave_slot + slot * kSlotBytes);
+    for (int k = 0; k < kBCopies; ++k) copy_b_one(min(step, n - 1), k, wave_slot + slot * kSlotBytes);
   };
 
   // Copy c of step `step`'s copies: c < BM / 32 the activation rows of step + 2, then step + 3's plane copies.
   const auto copy_one = [&](uint32_t step, int c) __attribute__((always_inline)) {
     if (c < BM / 32) {
-      const uint8_t *from = (const uint8_t *)a.half_input + (size_t)min(step + 2, steps - 1) * BK * 2;
+      const uint8_t *from = xin + (size_t)min(step + 2, n - 1) * BK * 2;
       uint8_t *stage = lds + ((step + 2) % kStages) * kStage;
       copy_to_lds<16>(from + aoff[c], stage + (kRowsPerWave * wave + 8 * c) * kRowBytes);
       return;
     }
-    copy_b_one(min(step + 3, steps - 1), c - BM / 32, wave_slot + ((step + 3) % kSlots) * kSlotBytes);
+    copy_b_one(min(step + 3, n - 1), c - BM / 32, wave_slot + ((step + 3) % kSlots) * kSlotBytes);
   };
 
   f32x4 acc[MI][4];
@@ -479,7 +486,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     }
   };
   read_batch(0, 0);
-  for (uint32_t step = 0; step < steps; ++step) {
+  for (uint32_t step = 0; step < n; ++step) {
     if (step > 0) mfma_batch(step - 1, kBatches - 1);
 #pragma unroll
     for (int b = 0; b < kBatches; ++b) {
@@ -497,10 +504,39 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     }
     __builtin_amdgcn_s_waitcnt(wait_vm(kCopies));
     lds_barrier();
-    if (step + 1 < steps) read_batch(step + 1, 0);
+    if (step + 1 < n) read_batch(step + 1, 0);
   }
-  mfma_batch(steps - 1, kBatches - 1);
+  mfma_batch(n - 1, kBatches - 1);
 
+  if constexpr (SPLIT) {
+    // Half z of K: the fp32 sums, exactly, as two 16-bit planes of [rows][out_stride] (the high halves of the bits,
+    // then the low), stored as the bf16 epilogue stores (eight consecutive columns of a row twice over);
+    // split_close_kernel adds the halves and applies the epilogue.
+    if (!live) return;
+    uint16_t *const high = (uint16_t *)a.partials + (size_t)blockIdx.z * 2 * a.rows * a.out_stride;
+    uint16_t *const low = high + (size_t)a.rows * a.out_stride;
+    const uint32_t col0 = seg.out_offset + ptile * 64 + 8 * q;
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) {
+      const uint32_t r = row0 + mi * 16 + j;
+      if (r >= a.rows) continue;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const size_t at = (size_t)r * a.out_stride + col0 + 32 * half;
+        u32x4 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const f32x4 &v = acc[mi][2 * half + (e >> 1)];
+          const uint32_t b0 = __float_as_uint(v[2 * (e & 1)]), b1 = __float_as_uint(v[2 * (e & 1) + 1]);
+          hi[e] = __builtin_amdgcn_perm(b1, b0, 0x07060302u);
+          lo[e] = __builtin_amdgcn_perm(b1, b0, 0x05040100u);
+        }
+        *(u32x4 *)(high + at) = hi;
+        *(u32x4 *)(low + at) = lo;
+      }
+    }
+    return;
+  }
   // Epilogue: lane (j, q) holds row 16 mi + j of each row block at columns 8q..8q+7 (blocks 0, 1) and
   // 32+8q..32+8q+7 (blocks 2, 3) of the plane tile: two 16-byte stores a row block.
   if (!live) return;
@@ -528,35 +564,106 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   }
 }
 
-template <uint32_t FMT, int BM>
-hipError_t launch_tile(uint32_t epilogue, const PrefillArgs &a, uint32_t tiles, hipStream_t stream) {
-  const dim3 grid((a.rows + BM - 1) / BM, (tiles + 3) / 4), block(kThreads);
+// The close of a K-halved dispatch: y = epilogue((half 0 + half 1) * 2^e) in bf16, eight columns a thread, the halves
+// fp32 sums rebuilt from their two 16-bit planes and added in K order.
+template <uint32_t EP>
+__global__ __launch_bounds__(256) void split_close_kernel(const uint16_t *partials, const float *row_scale,
+                                                          const uint16_t *aux, uint16_t *output, uint32_t rows,
+                                                          uint32_t out_stride, uint32_t columns, uint32_t col0) {
+  const uint32_t groups = columns / 8, r = blockIdx.y;
+  const uint32_t g = blockIdx.x * 256 + threadIdx.x;
+  if (g >= groups) return;
+  const size_t at = (size_t)r * out_stride + col0 + 8 * g, plane = (size_t)rows * out_stride;
+  const u32x4 h0 = *(const u32x4 *)(partials + at), l0 = *(const u32x4 *)(partials + plane + at);
+  const u32x4 h1 = *(const u32x4 *)(partials + 2 * plane + at), l1 = *(const u32x4 *)(partials + 3 * plane + at);
+  const float scale = row_scale[r];
+  u32x4 x = {0u, 0u, 0u, 0u};
+  if constexpr (EP != EpNone) x = *(const u32x4 *)(aux + at);
+  u32x4 out;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    // Columns 2e, 2e + 1: bits (high << 16) | low of each half.
+    const float a0 = __uint_as_float(__builtin_amdgcn_perm(h0[e], l0[e], 0x05040100u));
+    const float a1 = __uint_as_float(__builtin_amdgcn_perm(h0[e], l0[e], 0x07060302u));
+    const float b0 = __uint_as_float(__builtin_amdgcn_perm(h1[e], l1[e], 0x05040100u));
+    const float b1 = __uint_as_float(__builtin_amdgcn_perm(h1[e], l1[e], 0x07060302u));
+    const float lo = epilogue_bits<EP>((a0 + b0) * scale, x[e] & 0xFFFFu);
+    const float hi = epilogue_bits<EP>((a1 + b1) * scale, x[e] >> 16);
+    out[e] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+  }
+  *(u32x4 *)(output + at) = out;
+}
+
+template <uint32_t FMT, int BM, bool SPLIT>
+hipError_t launch_tile(uint32_t epilogue, const PrefillArgs &a, dim3 grid, hipStream_t stream) {
+  const dim3 block(kThreads);
   switch (epilogue) {
-    case EpNone: hipLaunchKernelGGL((prefill_kernel<FMT, EpNone, BM>), grid, block, 0, stream, a); break;
-    case EpResidual: hipLaunchKernelGGL((prefill_kernel<FMT, EpResidual, BM>), grid, block, 0, stream, a); break;
-    default: hipLaunchKernelGGL((prefill_kernel<FMT, EpUpWithGate, BM>), grid, block, 0, stream, a); break;
+    case EpNone: hipLaunchKernelGGL((prefill_kernel<FMT, EpNone, BM, SPLIT>), grid, block, 0, stream, a); break;
+    case EpResidual: hipLaunchKernelGGL((prefill_kernel<FMT, EpResidual, BM, SPLIT>), grid, block, 0, stream, a); break;
+    default: hipLaunchKernelGGL((prefill_kernel<FMT, EpUpWithGate, BM, SPLIT>), grid, block, 0, stream, a); break;
   }
   return hipGetLastError();
 }
 
-// The tile height with fewer rounds of workgroups over the compute units (one workgroup a unit), a 128-row tile
-// costing 0.7 of a 256-row one (measured: the dequantisation and the step's fixed work are shared by half the rows).
 template <uint32_t FMT>
 hipError_t launch_format(uint32_t epilogue, const PrefillArgs &a, hipStream_t stream) {
+  static_assert(lds_bytes<FMT, 256>() <= kLdsLimit, "every format's 256-row tile fits the LDS");
   uint32_t tiles = 0;
   for (uint32_t s = 0; s < a.segments; ++s) tiles += a.seg[s].tiles;
-  const uint32_t columns = (tiles + 3) / 4, units = a.compute_units ? a.compute_units : 256;
-  const uint32_t rounds256 = ((a.rows + 255) / 256 * columns + units - 1) / units;
-  const uint32_t rounds128 = ((a.rows + 127) / 128 * columns + units - 1) / units;
-  // (Every format's 256-row tile fits the LDS, with three step slots where four do not fit.)
-  if constexpr (lds_bytes<FMT, 256>() > kLdsLimit) return launch_tile<FMT, 128>(epilogue, a, tiles, stream);
-  else {
-    if (7 * rounds128 < 10 * rounds256) return launch_tile<FMT, 128>(epilogue, a, tiles, stream);
-    return launch_tile<FMT, 256>(epilogue, a, tiles, stream);
+  // The projection's whole width decides the halving, so every dispatch of it (one per format) halves alike.
+  const PrefillSchedule sc = prefill_schedule(a.rows, tiles, a.K, prefill_split(a.rows, a.out_stride / 64, a.K));
+  if (sc.split) {
+    if (!a.partials) return hipErrorInvalidValue;
+    const hipError_t e = launch_tile<FMT, 256, true>(epilogue, a, dim3(sc.row_blocks, sc.column_groups, 2), stream);
+    if (e != hipSuccess) return e;
+    // Every segment's columns: one close over their span (segments of one dispatch lie side by side in the output).
+    uint32_t lo = a.seg[0].out_offset, hi = 0;
+    for (uint32_t s = 0; s < a.segments; ++s) {
+      lo = std::min(lo, a.seg[s].out_offset);
+      hi = std::max(hi, a.seg[s].out_offset + 64 * a.seg[s].tiles);
+    }
+    const dim3 grid(((hi - lo) / 8 + 255) / 256, a.rows), block(256);
+    switch (epilogue) {
+      case EpNone: hipLaunchKernelGGL(split_close_kernel<EpNone>, grid, block, 0, stream, (const uint16_t *)a.partials, a.row_scale, a.aux, a.output, a.rows, a.out_stride, hi - lo, lo); break;
+      case EpResidual: hipLaunchKernelGGL(split_close_kernel<EpResidual>, grid, block, 0, stream, (const uint16_t *)a.partials, a.row_scale, a.aux, a.output, a.rows, a.out_stride, hi - lo, lo); break;
+      default: hipLaunchKernelGGL(split_close_kernel<EpUpWithGate>, grid, block, 0, stream, (const uint16_t *)a.partials, a.row_scale, a.aux, a.output, a.rows, a.out_stride, hi - lo, lo); break;
+    }
+    return hipGetLastError();
   }
+  const dim3 grid(sc.row_blocks, sc.column_groups);
+  if (sc.bm == 128) return launch_tile<FMT, 128, false>(epilogue, a, grid, stream);
+  return launch_tile<FMT, 256, false>(epilogue, a, grid, stream);
 }
 
 }  // namespace
+
+// Whether a projection of `rows` x `plane_tiles` plane tiles halves its tiles' K: when its 256-row tiles are
+// kPrefillSplitTiles to kPrefillUnits / 2 (one round of halves over the compute units, where whole tiles would leave
+// half of them idle or take 128-row tiles at 0.7 of the cost each), and each half starts on whole meta units (K a
+// multiple of 512). A halved step costs what a 256-row step costs; the fp32 halves and their close about six more.
+bool prefill_split(uint32_t rows, uint32_t plane_tiles, uint32_t K) {
+  const uint32_t columns = (plane_tiles + 3) / 4, steps = K / BK;
+  const uint64_t tiles256 = (uint64_t)((rows + 255) / 256) * columns, tiles128 = (uint64_t)((rows + 127) / 128) * columns;
+  if (tiles256 < kPrefillSplitTiles || 2 * tiles256 > kPrefillUnits || steps % 8) return false;
+  const double cost128 = 0.7 * steps * (double)((tiles128 + kPrefillUnits - 1) / kPrefillUnits);
+  return steps / 2.0 + 6.0 < std::min(cost128, (double)steps);
+}
+// The tile height with fewer rounds of workgroups over the compute units (one workgroup a unit), a 128-row tile
+// costing 0.7 of a 256-row one; 256 rows for a halved projection.
+PrefillSchedule prefill_schedule(uint32_t rows, uint32_t plane_tiles, uint32_t K, bool split) {
+  const uint32_t columns = (plane_tiles + 3) / 4, units = kPrefillUnits;
+  const uint32_t blocks128 = (rows + 127) / 128, blocks256 = (rows + 255) / 256;
+  if (split) return {256, 1, blocks256, columns};
+  const uint64_t rounds128 = ((uint64_t)blocks128 * columns + units - 1) / units;
+  const uint64_t rounds256 = ((uint64_t)blocks256 * columns + units - 1) / units;
+  (void)K;
+  if (7 * rounds128 < 10 * rounds256) return {128, 0, blocks128, columns};
+  return {256, 0, blocks256, columns};
+}
+PrefillScratch prefill_scratch_bytes(uint32_t rows, uint32_t plane_tiles, uint32_t K) {
+  if (!prefill_split(rows, plane_tiles, K)) return {0, 0};
+  return {(uint64_t)2 * rows * plane_tiles * 64 * 4, 0};
+}
 
 hipError_t launch_prefill_prepare(const uint16_t *input, uint32_t rows, uint32_t K, uint16_t *half_input,
                                   float *row_scale, hipStream_t stream) {

@@ -94,6 +94,17 @@ def test_prefill_plans():
     assert ragged.storage_rows == 384
     short = sq.plan_for(sq.prefill_workload(14336, 4096, 32), proj)
     assert short.config.tile == sq.TILE_STAGED
+    # 448 tiles of 256 rows fill the compute units: no halves. 128 (N 4096 by K 14336) halve their K, whose fp32
+    # halves [2][rows][N] the plan's partials hold; K not a multiple of 512 does not halve.
+    assert size.partials == 0 and size.counters == 0
+    down = sq.projection(seg(4096, 14336))
+    size, _ = sq.scratch_size(sq.plan_for(sq.prefill_workload(4096, 14336, 2048), down))
+    assert size.partials == 2 * 2048 * 4096 * 4 and size.counters == 0
+    size, _ = sq.scratch_size(sq.plan_for(sq.prefill_workload(4096, 14336, 300), down))
+    assert size.partials == 0
+    dev, bound = sq.device(), sq.LinearScratchSize()
+    sq.call("sq_linear_prefill_scratch_size", sq.byref(dev), 4096, 14336, sq.byref(bound))
+    assert bound.partials >= 2 * 2048 * 4096 * 4
 
 
 def test_gate_up_plans():

@@ -185,6 +185,42 @@ def test_config2_prefill_shapes(n, k, rows):
     check_sampled(out, x, w, f"config 2 {k}x{n} rows {rows}", rng)
 
 
+@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K, oracle.FMT_Q6K, oracle.FMT_AF8G64])
+def test_prefill_halved_k(fmt):
+    """A projection whose 256-row tiles would fill at most half the compute units runs each tile as two halves of K
+    (two workgroups, fp32 halves added in K order by a close dispatch): 1800 rows (the last row tile ragged) of
+    4096 x 4096, each half starting on whole meta units of the format."""
+    n, k, rows = 4096, 4096, 1800
+    w = make_weights(np.random.default_rng(70 + fmt), fmt, n, k)
+    size, _ = sq.scratch_size(sq.plan_for(sq.prefill_workload(n, k, rows), sq.projection(w.segment())))
+    assert size.partials == 2 * rows * n * 4, "the plan halves K"
+    rng = np.random.default_rng(71 + fmt)
+    x = dense_inputs(rng, rows, k)
+    out = run_prefill([w], x)
+    check_sampled(out, x, w, f"halved K fmt {fmt}", rng)
+
+
+def test_prefill_halved_k_epilogues():
+    """The close dispatch of a halved projection applies the residual and the up-with-gate epilogues."""
+    rng = np.random.default_rng(72)
+    n, k, rows = 4096, 4096, 2048
+    w = make_weights(rng, oracle.FMT_AF4G64, n, k)
+    x = dense_inputs(rng, rows, k)
+    pick = sampled_rows(rows, 24, rng)
+    plain = run_prefill([w], x)
+    residual = synthetic.bf16_bits(rng.uniform(-64, 64, (rows, n)).astype(np.float32))
+    out = run_prefill([w], x, sq.EPILOGUE_RESIDUAL, residual=residual)
+    check_projection(out[pick], x[pick], w, "halved residual", residual=residual[pick])
+    gate = synthetic.bf16_bits(rng.uniform(-4, 4, (rows, n)).astype(np.float32))
+    up_gated = run_prefill([w], x, sq.EPILOGUE_UP_WITH_GATE, gate_scratch=gate)
+    gf = synthetic.bf16_to_f32(gate[pick]).astype(np.float64)
+    uf = synthetic.bf16_to_f32(plain[pick]).astype(np.float64)
+    want = uf * gf / (1 + np.exp(-gf))
+    got = synthetic.bf16_to_f32(up_gated[pick]).astype(np.float64)
+    ulp = np.ldexp(1.0, np.floor(np.log2(np.maximum(np.abs(want), 1e-30))).astype(int) - 7)
+    assert np.all(np.abs(got - want) <= ulp + 1e-30)
+
+
 def test_config3_q4k_prefill():
     """BASELINE config 3's prefill point: Q4_K, K = 5120, N = 27648, M = 512."""
     n, k, rows = 27648, 5120, 512
