@@ -78,16 +78,19 @@ struct PrefillArgs {
   uint16_t *output;            // bf16 [rows][out_stride]
   const uint16_t *aux;
   uint32_t K, rows, out_stride;
-  float *partials;             // a split dispatch's fp32 halves (prefill_scratch_bytes)
+  float *partials;             // a split dispatch's fp32 pieces (prefill_scratch_bytes)
+  uint32_t column_group0;      // set by launch_prefill: the dispatch's first column group,
+  uint32_t split_at, split_columns;   // the step its pieces are cut at, the partial planes' row length
 };
 hipError_t launch_prefill(uint32_t fmt, uint32_t epilogue, const PrefillArgs &args, hipStream_t stream);
 // The prefill dispatch's shape: tiles of bm rows (128 or 256) by four plane tiles, row_blocks x column_groups of
-// them, 64 inputs a step, one workgroup each; with `split` (prefill_split of the projection's rows, whole width and
-// K), two workgroups each, one per half of K, which store fp32 sums [2][rows][out_stride] to the partials for a close
-// dispatch that adds the halves in K order and applies the epilogue.
+// them, 64 inputs a step, one workgroup each. With `split` (prefill_split of the projection's rows, whole width and
+// K), the tiles from column group whole_groups on are cut at step split_at between two workgroups, which store their
+// fp32 sums [2][rows][split columns] to the partials for a close dispatch that adds the pieces in K order and
+// applies the epilogue (the schedule cuts every tile in halves: whole_groups 0, split_at half the steps).
 constexpr uint32_t kPrefillUnits = 256, kPrefillSplitTiles = 64;   // an MI355X's compute units
 struct PrefillSchedule {
-  uint32_t bm, split, row_blocks, column_groups;
+  uint32_t bm, split, row_blocks, column_groups, whole_groups, split_at;
 };
 bool prefill_split(uint32_t rows, uint32_t plane_tiles, uint32_t K);
 PrefillSchedule prefill_schedule(uint32_t rows, uint32_t plane_tiles, uint32_t K, bool split);

@@ -240,7 +240,8 @@ constexpr MicroTable make_micro_table() {
 constexpr MicroTable kMicroTable = make_micro_table();
 static_assert(kMicroTable.op[kMicro - 1].kind == 3 && kMicroTable.op[kMicro - 1].arg == 15, "52 micro-operations");
 
-// SPLIT: the tile's K is halved between the two workgroups of blockIdx.z (prefill_schedule), which meet in fp32.
+// SPLIT: the tile's K is cut between the two workgroups of blockIdx.z (steps [0, split_at) and [split_at, K / 64)),
+// whose fp32 sums a close dispatch adds (prefill_schedule).
 template <uint32_t FMT, uint32_t EP, int BM, bool SPLIT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_kernel(PrefillArgs a) {
   using F = Fmt<FMT>;
@@ -262,13 +263,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t row0 = blockIdx.x * BM;
   const uint32_t G = a.K >> 5, units = G / F::UNIT, steps = a.K / BK;
-  // The workgroup's steps of the tile: all of them, or half z of them (a multiple of four steps, whole meta units of
-  // every format), run with their own numbers from 0 from plane and input pointers moved on by `first` steps.
-  const uint32_t first = SPLIT ? blockIdx.z * (steps / 2) : 0, n = SPLIT ? steps / 2 : steps;
+  // The workgroup's steps of the tile: all of them, or piece z of them (cut at a multiple of four steps, whole meta
+  // units of every format), run with their own numbers from 0 from plane and input pointers moved on by `first`.
+  const uint32_t first = SPLIT && blockIdx.z ? a.split_at : 0;
+  const uint32_t n = SPLIT ? (blockIdx.z ? steps - a.split_at : a.split_at) : steps;
 
-  // The wave's plane tile. A grid whose tile count is not a multiple of 4 ends short: a spare wave runs tile 0 of
-  // its segment and stores nothing.
-  uint32_t ptile = blockIdx.y * 4 + wave, s = 0;
+  // The wave's plane tile (the dispatch's column groups start at column_group0). A grid whose tile count is not a
+  // multiple of 4 ends short: a spare wave runs tile 0 of its segment and stores nothing.
+  uint32_t ptile = (a.column_group0 + blockIdx.y) * 4 + wave, s = 0;
   while (s + 1 < a.segments && ptile >= a.seg[s].tiles) ptile -= a.seg[s++].tiles;
   const bool live = ptile < a.seg[s].tiles;
   const Segment seg = a.seg[s];
@@ -509,20 +511,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   mfma_batch(n - 1, kBatches - 1);
 
   if constexpr (SPLIT) {
-    // Half z of K: the fp32 sums, exactly, as two 16-bit planes of [rows][out_stride] (the high halves of the bits,
-    // then the low), stored as the bf16 epilogue stores (eight consecutive columns of a row twice over);
-    // split_close_kernel adds the halves and applies the epilogue.
+    // Piece z of K: the fp32 sums, exactly, as two 16-bit planes of [rows][split_columns] (the high halves of the
+    // bits, then the low; column 64 t + c of the dispatch's plane tile t), stored as the bf16 epilogue stores (eight
+    // consecutive columns of a row twice over); split_close_kernel adds the pieces and applies the epilogue.
     if (!live) return;
-    uint16_t *const high = (uint16_t *)a.partials + (size_t)blockIdx.z * 2 * a.rows * a.out_stride;
-    uint16_t *const low = high + (size_t)a.rows * a.out_stride;
-    const uint32_t col0 = seg.out_offset + ptile * 64 + 8 * q;
+    const size_t plane = (size_t)a.rows * a.split_columns;
+    uint16_t *const high = (uint16_t *)a.partials + blockIdx.z * 2 * plane;
+    uint16_t *const low = high + plane;
+    const uint32_t col0 = (blockIdx.y * 4 + wave) * 64 + 8 * q;
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
       const uint32_t r = row0 + mi * 16 + j;
       if (r >= a.rows) continue;
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const size_t at = (size_t)r * a.out_stride + col0 + 32 * half;
+        const size_t at = (size_t)r * a.split_columns + col0 + 32 * half;
         u32x4 hi, lo;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -564,25 +567,27 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   }
 }
 
-// The close of a K-halved dispatch: y = epilogue((half 0 + half 1) * 2^e) in bf16, eight columns a thread, the halves
-// fp32 sums rebuilt from their two 16-bit planes and added in K order.
+// The close of a split dispatch: y = epilogue((piece 0 + piece 1) * 2^e) in bf16, eight columns of one of its plane
+// tiles a thread, the pieces' fp32 sums rebuilt from their two 16-bit planes and added in K order.
 template <uint32_t EP>
-__global__ __launch_bounds__(256) void split_close_kernel(const uint16_t *partials, const float *row_scale,
-                                                          const uint16_t *aux, uint16_t *output, uint32_t rows,
-                                                          uint32_t out_stride, uint32_t columns, uint32_t col0) {
-  const uint32_t groups = columns / 8, r = blockIdx.y;
-  const uint32_t g = blockIdx.x * 256 + threadIdx.x;
-  if (g >= groups) return;
-  const size_t at = (size_t)r * out_stride + col0 + 8 * g, plane = (size_t)rows * out_stride;
-  const u32x4 h0 = *(const u32x4 *)(partials + at), l0 = *(const u32x4 *)(partials + plane + at);
-  const u32x4 h1 = *(const u32x4 *)(partials + 2 * plane + at), l1 = *(const u32x4 *)(partials + 3 * plane + at);
-  const float scale = row_scale[r];
+__global__ __launch_bounds__(256) void split_close_kernel(PrefillArgs a, uint32_t tiles) {
+  const uint32_t r = blockIdx.y, g = blockIdx.x * 256 + threadIdx.x;
+  if (g >= tiles * 8) return;
+  uint32_t ptile = a.column_group0 * 4 + g / 8, s = 0;
+  while (s + 1 < a.segments && ptile >= a.seg[s].tiles) ptile -= a.seg[s++].tiles;
+  if (ptile >= a.seg[s].tiles) return;
+  const size_t plane = (size_t)a.rows * a.split_columns, from = (size_t)r * a.split_columns + 8 * g;
+  const uint16_t *partials = (const uint16_t *)a.partials;
+  const u32x4 h0 = *(const u32x4 *)(partials + from), l0 = *(const u32x4 *)(partials + plane + from);
+  const u32x4 h1 = *(const u32x4 *)(partials + 2 * plane + from), l1 = *(const u32x4 *)(partials + 3 * plane + from);
+  const size_t at = (size_t)r * a.out_stride + a.seg[s].out_offset + ptile * 64 + 8 * (g % 8);
+  const float scale = a.row_scale[r];
   u32x4 x = {0u, 0u, 0u, 0u};
-  if constexpr (EP != EpNone) x = *(const u32x4 *)(aux + at);
+  if constexpr (EP != EpNone) x = *(const u32x4 *)(a.aux + at);
   u32x4 out;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    // Columns 2e, 2e + 1: bits (high << 16) | low of each half.
+    // Columns 2e, 2e + 1: bits (high << 16) | low of each piece.
     const float a0 = __uint_as_float(__builtin_amdgcn_perm(h0[e], l0[e], 0x05040100u));
     const float a1 = __uint_as_float(__builtin_amdgcn_perm(h0[e], l0[e], 0x07060302u));
     const float b0 = __uint_as_float(__builtin_amdgcn_perm(h1[e], l1[e], 0x05040100u));
@@ -591,7 +596,7 @@ __global__ __launch_bounds__(256) void split_close_kernel(const uint16_t *partia
     const float hi = epilogue_bits<EP>((a1 + b1) * scale, x[e] >> 16);
     out[e] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
   }
-  *(u32x4 *)(output + at) = out;
+  *(u32x4 *)(a.output + at) = out;
 }
 
 template <uint32_t FMT, int BM, bool SPLIT>
@@ -606,63 +611,66 @@ hipError_t launch_tile(uint32_t epilogue, const PrefillArgs &a, dim3 grid, hipSt
 }
 
 template <uint32_t FMT>
-hipError_t launch_format(uint32_t epilogue, const PrefillArgs &a, hipStream_t stream) {
+hipError_t launch_format(uint32_t epilogue, const PrefillArgs &args, hipStream_t stream) {
   static_assert(lds_bytes<FMT, 256>() <= kLdsLimit, "every format's 256-row tile fits the LDS");
   uint32_t tiles = 0;
-  for (uint32_t s = 0; s < a.segments; ++s) tiles += a.seg[s].tiles;
+  for (uint32_t s = 0; s < args.segments; ++s) tiles += args.seg[s].tiles;
   // The projection's whole width decides the halving, so every dispatch of it (one per format) halves alike.
-  const PrefillSchedule sc = prefill_schedule(a.rows, tiles, a.K, prefill_split(a.rows, a.out_stride / 64, a.K));
-  if (sc.split) {
-    if (!a.partials) return hipErrorInvalidValue;
-    const hipError_t e = launch_tile<FMT, 256, true>(epilogue, a, dim3(sc.row_blocks, sc.column_groups, 2), stream);
-    if (e != hipSuccess) return e;
-    // Every segment's columns: one close over their span (segments of one dispatch lie side by side in the output).
-    uint32_t lo = a.seg[0].out_offset, hi = 0;
-    for (uint32_t s = 0; s < a.segments; ++s) {
-      lo = std::min(lo, a.seg[s].out_offset);
-      hi = std::max(hi, a.seg[s].out_offset + 64 * a.seg[s].tiles);
-    }
-    const dim3 grid(((hi - lo) / 8 + 255) / 256, a.rows), block(256);
-    switch (epilogue) {
-      case EpNone: hipLaunchKernelGGL(split_close_kernel<EpNone>, grid, block, 0, stream, (const uint16_t *)a.partials, a.row_scale, a.aux, a.output, a.rows, a.out_stride, hi - lo, lo); break;
-      case EpResidual: hipLaunchKernelGGL(split_close_kernel<EpResidual>, grid, block, 0, stream, (const uint16_t *)a.partials, a.row_scale, a.aux, a.output, a.rows, a.out_stride, hi - lo, lo); break;
-      default: hipLaunchKernelGGL(split_close_kernel<EpUpWithGate>, grid, block, 0, stream, (const uint16_t *)a.partials, a.row_scale, a.aux, a.output, a.rows, a.out_stride, hi - lo, lo); break;
-    }
-    return hipGetLastError();
+  const PrefillSchedule sc = prefill_schedule(args.rows, tiles, args.K, prefill_split(args.rows, args.out_stride / 64, args.K));
+  PrefillArgs a = args;
+  a.column_group0 = 0;
+  if (!sc.split) {
+    const dim3 grid(sc.row_blocks, sc.column_groups);
+    if (sc.bm == 128) return launch_tile<FMT, 128, false>(epilogue, a, grid, stream);
+    return launch_tile<FMT, 256, false>(epilogue, a, grid, stream);
   }
-  const dim3 grid(sc.row_blocks, sc.column_groups);
-  if (sc.bm == 128) return launch_tile<FMT, 128, false>(epilogue, a, grid, stream);
-  return launch_tile<FMT, 256, false>(epilogue, a, grid, stream);
+  if (!a.partials) return hipErrorInvalidValue;
+  a.column_group0 = sc.whole_groups;
+  a.split_at = sc.split_at;
+  a.split_columns = (sc.column_groups - sc.whole_groups) * 256;
+  hipError_t e = launch_tile<FMT, 256, true>(epilogue, a, dim3(sc.row_blocks, sc.column_groups - sc.whole_groups, 2),
+                                             stream);
+  if (e != hipSuccess) return e;
+  const uint32_t split_tiles = tiles - 4 * sc.whole_groups;
+  const dim3 grid((split_tiles * 8 + 255) / 256, a.rows), block(256);
+  switch (epilogue) {
+    case EpNone: hipLaunchKernelGGL(split_close_kernel<EpNone>, grid, block, 0, stream, a, split_tiles); break;
+    case EpResidual: hipLaunchKernelGGL(split_close_kernel<EpResidual>, grid, block, 0, stream, a, split_tiles); break;
+    default: hipLaunchKernelGGL(split_close_kernel<EpUpWithGate>, grid, block, 0, stream, a, split_tiles); break;
+  }
+  return hipGetLastError();
 }
 
 }  // namespace
 
-// Whether a projection of `rows` x `plane_tiles` plane tiles halves its tiles' K: when its 256-row tiles are
+// Whether a projection of `rows` x `plane_tiles` plane tiles halves its tiles' K: when its 256-row tiles number
 // kPrefillSplitTiles to kPrefillUnits / 2 (one round of halves over the compute units, where whole tiles would leave
-// half of them idle or take 128-row tiles at 0.7 of the cost each), and each half starts on whole meta units (K a
-// multiple of 512). A halved step costs what a 256-row step costs; the fp32 halves and their close about six more.
+// half of them idle or take 128-row tiles at 0.7 of the cost each, measured: the dequantisation and the step's fixed
+// work are shared by half the rows), and each half starts on whole meta units (K a multiple of 512). Costs in 256-row
+// steps a compute unit: a half costs its steps, about two for its prologue and stores, and about six for the close.
+// (Whole rounds of tiles followed by cut ones were measured too: 4096 x 14336 at M 2048 ran 309 us against 266 whole,
+// and 5120 x 27648 gained nothing.)
 bool prefill_split(uint32_t rows, uint32_t plane_tiles, uint32_t K) {
-  const uint32_t columns = (plane_tiles + 3) / 4, steps = K / BK;
+  const uint32_t columns = (plane_tiles + 3) / 4, steps = K / BK, units = kPrefillUnits;
   const uint64_t tiles256 = (uint64_t)((rows + 255) / 256) * columns, tiles128 = (uint64_t)((rows + 127) / 128) * columns;
-  if (tiles256 < kPrefillSplitTiles || 2 * tiles256 > kPrefillUnits || steps % 8) return false;
-  const double cost128 = 0.7 * steps * (double)((tiles128 + kPrefillUnits - 1) / kPrefillUnits);
-  return steps / 2.0 + 6.0 < std::min(cost128, (double)steps);
+  if (tiles256 < kPrefillSplitTiles || 2 * tiles256 > units || steps % 8) return false;
+  const double cost128 = 0.7 * steps * (double)((tiles128 + units - 1) / units);
+  return steps / 2.0 + 8.0 < std::min(cost128, (double)steps);
 }
 // The tile height with fewer rounds of workgroups over the compute units (one workgroup a unit), a 128-row tile
-// costing 0.7 of a 256-row one; 256 rows for a halved projection.
+// costing 0.7 of a 256-row one; 256 rows cut in halves for a halved projection.
 PrefillSchedule prefill_schedule(uint32_t rows, uint32_t plane_tiles, uint32_t K, bool split) {
   const uint32_t columns = (plane_tiles + 3) / 4, units = kPrefillUnits;
   const uint32_t blocks128 = (rows + 127) / 128, blocks256 = (rows + 255) / 256;
-  if (split) return {256, 1, blocks256, columns};
+  if (split) return {256, 1, blocks256, columns, 0, K / BK / 2};
   const uint64_t rounds128 = ((uint64_t)blocks128 * columns + units - 1) / units;
   const uint64_t rounds256 = ((uint64_t)blocks256 * columns + units - 1) / units;
-  (void)K;
-  if (7 * rounds128 < 10 * rounds256) return {128, 0, blocks128, columns};
-  return {256, 0, blocks256, columns};
+  if (7 * rounds128 < 10 * rounds256) return {128, 0, blocks128, columns, 0, 0};
+  return {256, 0, blocks256, columns, 0, 0};
 }
 PrefillScratch prefill_scratch_bytes(uint32_t rows, uint32_t plane_tiles, uint32_t K) {
   if (!prefill_split(rows, plane_tiles, K)) return {0, 0};
-  return {(uint64_t)2 * rows * plane_tiles * 64 * 4, 0};
+  return {(uint64_t)2 * rows * ((plane_tiles + 3) / 4) * 256 * 4, 0};
 }
 
 hipError_t launch_prefill_prepare(const uint16_t *input, uint32_t rows, uint32_t K, uint16_t *half_input,

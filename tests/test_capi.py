@@ -95,7 +95,7 @@ def test_prefill_plans():
     short = sq.plan_for(sq.prefill_workload(14336, 4096, 32), proj)
     assert short.config.tile == sq.TILE_STAGED
     # 448 tiles of 256 rows fill the compute units: no halves. 128 (N 4096 by K 14336) halve their K, whose fp32
-    # halves [2][rows][N] the plan's partials hold; K not a multiple of 512 does not halve.
+    # halves [2][rows][N] the plan's partials hold; 32 tiles do not halve.
     assert size.partials == 0 and size.counters == 0
     down = sq.projection(seg(4096, 14336))
     size, _ = sq.scratch_size(sq.plan_for(sq.prefill_workload(4096, 14336, 2048), down))

@@ -200,6 +200,25 @@ def test_prefill_halved_k(fmt):
     check_sampled(out, x, w, f"halved K fmt {fmt}", rng)
 
 
+def test_prefill_halved_k_across_segments():
+    """A fused projection whose halved tiles span segment boundaries: 1024 rows (4 row blocks) by 32 column groups of
+    segments of 4096, 1536 and 2560 columns; the close maps each plane tile back to its segment's columns."""
+    rng = np.random.default_rng(73)
+    k, rows = 4096, 1024
+    parts = [make_weights(rng, oracle.FMT_AF4G64, n, k) for n in (4096, 1536, 2560)]
+    n = sum(p.n for p in parts)
+    segs, offset = [], 0
+    for p in parts:
+        segs.append(p.segment(offset))
+        offset += p.n
+    size, _ = sq.scratch_size(sq.plan_for(sq.prefill_workload(n, k, rows), sq.projection(segs)))
+    assert size.partials == 2 * rows * n * 4, "the plan halves K"
+    x = dense_inputs(rng, rows, k)
+    out = run_prefill(parts, x)
+    pick = sampled_rows(rows, 24, rng)
+    check_projection(out[pick], x[pick], parts, "halved K across segments")
+
+
 def test_prefill_halved_k_epilogues():
     """The close dispatch of a halved projection applies the residual and the up-with-gate epilogues."""
     rng = np.random.default_rng(72)
