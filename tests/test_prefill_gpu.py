@@ -219,6 +219,21 @@ def test_prefill_halved_k_across_segments():
     check_projection(out[pick], x[pick], parts, "halved K across segments")
 
 
+def test_prefill_halved_k_mixed_formats():
+    """A projection of two formats halves by its whole width: each format's dispatch cuts its own tiles' K and closes
+    its own columns, one after the other through the same partials."""
+    rng = np.random.default_rng(74)
+    k, rows = 4096, 1024
+    parts = [make_weights(rng, oracle.FMT_AF4G64, 4096, k), make_weights(rng, oracle.FMT_Q4K, 4096, k)]
+    segs = [parts[0].segment(0), parts[1].segment(4096)]
+    size, _ = sq.scratch_size(sq.plan_for(sq.prefill_workload(8192, k, rows), sq.projection(segs)))
+    assert size.partials == 2 * rows * 8192 * 4, "the plan halves K"
+    x = dense_inputs(rng, rows, k)
+    out = run_prefill(parts, x)
+    pick = sampled_rows(rows, 24, rng)
+    check_projection(out[pick], x[pick], parts, "halved K, two formats")
+
+
 def test_prefill_halved_k_epilogues():
     """The close dispatch of a halved projection applies the residual and the up-with-gate epilogues."""
     rng = np.random.default_rng(72)
