@@ -23,11 +23,11 @@ struct Segment {
 
 // The decode tiles: y[r][c] = sum_k x[r][k] w[c][k] over up to three segments of one format, or of any formats when
 // launch_decode is given kSegmentFormats (each workgroup then runs its own segment's format; no epilogue, bf16
-// output, the layout of the segments' longest meta unit, so each tile computes what it does alone). With gate.plane0 set,
-// gate (gate) and up (seg[0]) run in one pass and the output is bf16(bf16(up) silu(bf16(gate))). Split partials
-// are fp32 [split][rows][out_stride] (a gate/up pair's [split][rows][2 out_stride], gate's columns then up's);
-// counters one per workgroup column (grid.x, at most one per 16 destination columns), zero before and after each
-// dispatch.
+// output, the layout of the segments' longest meta unit, so each tile computes what it does alone). With
+// gate.plane0 set, gate (gate) and up (seg[0]) run in one pass and the output is bf16(bf16(up) silu(bf16(gate))).
+// Split partials are fp32 [split][rows][out_stride] (a gate/up pair's [split][rows][2 out_stride], gate's columns
+// then up's); counters one per workgroup column (grid.x, at most one per 16 destination columns), zero before and
+// after each dispatch.
 //  - The column tile (rows <= kColumnTileRows): grid (64-column tiles, splits) of up to kColumnMaxWaves waves, each
 //    lane one destination column.
 //  - The row tile (more rows): grid (64-column tiles, splits) of up to 16 waves (fewer for more than 16 rows or a

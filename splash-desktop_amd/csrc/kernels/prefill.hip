@@ -624,7 +624,8 @@ hipError_t launch_format(uint32_t epilogue, const PrefillArgs &args, hipStream_t
   uint32_t tiles = 0;
   for (uint32_t s = 0; s < args.segments; ++s) tiles += args.seg[s].tiles;
   // The projection's whole width decides the halving, so every dispatch of it (one per format) halves alike.
-  const PrefillSchedule sc = prefill_schedule(args.rows, tiles, args.K, prefill_split(args.rows, args.out_stride / 64, args.K));
+  const bool split = prefill_split(args.rows, args.out_stride / 64, args.K);
+  const PrefillSchedule sc = prefill_schedule(args.rows, tiles, args.K, split);
   PrefillArgs a = args;
   a.column_group0 = 0;
   if (!sc.split) {
@@ -660,7 +661,8 @@ hipError_t launch_format(uint32_t epilogue, const PrefillArgs &args, hipStream_t
 // and 5120 x 27648 gained nothing.)
 bool prefill_split(uint32_t rows, uint32_t plane_tiles, uint32_t K) {
   const uint32_t columns = (plane_tiles + 3) / 4, steps = K / BK, units = kPrefillUnits;
-  const uint64_t tiles256 = (uint64_t)((rows + 255) / 256) * columns, tiles128 = (uint64_t)((rows + 127) / 128) * columns;
+  const uint64_t tiles256 = (uint64_t)((rows + 255) / 256) * columns;
+  const uint64_t tiles128 = (uint64_t)((rows + 127) / 128) * columns;
   if (tiles256 < kPrefillSplitTiles || 2 * tiles256 > units || steps % 8) return false;
   const double cost128 = 0.7 * steps * (double)((tiles128 + units - 1) / units);
   return steps / 2.0 + 8.0 < std::min(cost128, (double)steps);
