@@ -192,8 +192,10 @@ __device__ __forceinline__ Coef coef(const MetaWords &m, uint32_t sg) {
 }
 // Q6_K's scale of half h (elements 16 h .. 16 h + 15) of group sg: d * int8 scale 2 (sg % 8) + h, exact in fp32.
 __device__ __forceinline__ float q6k_scale(const MetaWords &m, uint32_t sg, uint32_t h) {
-  const uint32_t i = 2 * (sg & 7u) + h;
-  return f16_to_f32(m.w[4] & 0xFFFFu) * (float)(int8_t)(m.w[i >> 2] >> (8 * (i & 3)));
+  const uint32_t i = 2 * (sg & 7u) + h, k = i >> 2;
+  // The word by selects, not by index: a run-time index into the words puts them in scratch memory.
+  const uint32_t word = k == 0 ? m.w[0] : k == 1 ? m.w[1] : k == 2 ? m.w[2] : m.w[3];
+  return f16_to_f32(m.w[4] & 0xFFFFu) * (float)(int8_t)(word >> (8 * (i & 3)));
 }
 
 // The exact bf16 operands of chunk c of a group (elements 4c..4c+3 and 16+4c..19+4c, pairs 0..3), for every
