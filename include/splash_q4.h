@@ -155,7 +155,9 @@ int sq_require_segment_planes(const sq_segment *segment, const char *what, uint3
 
 /* ---- dispatch ---- */
 
-/* Linear::add (Linear.cpp:203-232; LinearGguf.cpp:579-802): the plan's projection of buffers->input. */
+/* Linear::add (Linear.cpp:203-232; LinearGguf.cpp:579-802): the plan's projection of buffers->input. A decode of a
+ * projection of up to SQ_MAX_SEGMENTS segments runs them in one dispatch whatever their formats (gguf_decode_fused);
+ * a prefill runs one dispatch per format. */
 int sq_linear_add(void *graph, const sq_linear_buffers *buffers, const sq_projection *projection,
                   const sq_linear_plan *plan, const sq_projection *gate);
 /* Linear::add with its result: *prepared (may be NULL) receives what the scratch table describes after the
