@@ -279,15 +279,18 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
 // gate's output feeding the up pass's epilogue; the down pass reads the grouped intermediate rows
 // (moe_gguf.metal:121-206, moe_expert_slab.h:13-99).
 // The passes that stream chunks of two groups with operands built just before their MFMAs: those of 4-bit affine
-// codes in groups of 32 or 64 (a gate/up pair then fits two waves a SIMD, a single tensor three), and every
+// codes in groups of 32 or 64 (a gate/up pair then fits two waves a SIMD, a single tensor three), every
 // single-tensor pass whose scale groups fit a two-group chunk (the K-quants and 8-bit codes then fit two waves a SIMD
-// instead of one). The other gate/up pairs (K-quant headers, plane1 bits, 8-bit codes) would spill there and keep
-// four-group chunks with operands a group ahead, one wave a SIMD. Chunks hold whole scale groups either way, so the
-// sums are the same bits.
+// instead of one), and the Q4_K and Q5_K gate/up pairs, whose coefficients each lane derives for its own column only
+// (rowtile.hpp: 239 and 250 registers, two waves a SIMD). The other gate/up pairs (Q6_K's halves, 8-bit codes, groups
+// of 128) would spill there and keep four-group chunks with operands a group ahead, one wave a SIMD. Chunks hold
+// whole scale groups either way, so the sums are the same bits.
 template <uint32_t FMT>
 constexpr bool affine4_short() { return FMT == SQ_FMT_AF4G32 || FMT == SQ_FMT_AF4G64; }
 template <uint32_t FMT, int NT>
-constexpr bool short_chunks() { return affine4_short<FMT>() || (NT == 1 && Fmt<FMT>::SG <= 2); }
+constexpr bool short_chunks() {
+  return affine4_short<FMT>() || (NT == 1 && Fmt<FMT>::SG <= 2) || FMT == SQ_FMT_Q4K || FMT == SQ_FMT_Q5K;
+}
 template <uint32_t FMT, int NT>
 constexpr int expert_waves() { return affine4_short<FMT>() ? (NT == 2 ? 2 : 3) : short_chunks<FMT, NT>() ? 2 : 1; }
 

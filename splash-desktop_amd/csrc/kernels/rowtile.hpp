@@ -189,6 +189,46 @@ __device__ __forceinline__ MetaWords spread_meta(const MetaWords &own, int t, in
   return m;
 }
 
+// Q4_K and Q5_K: a group's coefficients cost ~9 VALU from the 16-byte header (6-bit scale and min of the group's
+// sub-block), so each lane derives them once, for its own column l, and hands (s, zc = z - 128 s) to the lanes whose
+// MFMA blocks hold the column (two ds_bpermute a column block) instead of every lane deriving them for its four
+// columns from spread header words.
+template <uint32_t FMT>
+constexpr bool owner_coefs() { return FMT == SQ_FMT_Q4K || FMT == SQ_FMT_Q5K; }
+struct CloseCoef {
+  float s, zc;
+};
+template <uint32_t FMT, int NT>
+__device__ __forceinline__ void spread_coefs(const MetaWords (&own)[NT], uint32_t g, int j, CloseCoef (&k)[NT][4]) {
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const Coef mine = coef<FMT>(own[n], g);
+    const float zc = fmaf(-128.0f, mine.s, mine.z);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int from = (16 * t + j) * 4;
+      k[n][t].s = __int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(mine.s)));
+      k[n][t].zc = __int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(zc)));
+    }
+  }
+}
+// row_group_close's fp32 close from handed coefficients: acc += s C + zc S, in the same order.
+template <int MB, int NT>
+__device__ __forceinline__ void row_group_close_coefs(const CloseCoef (&k)[NT][4], const f32x4 (&C)[NT][4][MB],
+                                                      const f32x4 (&S)[MB], float (&acc)[NT][4][MB][4]) {
+#pragma unroll
+  for (int n = 0; n < NT; ++n)
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[n][t][b][i] = fmaf(k[n][t].s, C[n][t][b][i], acc[n][t][b][i]);
+          acc[n][t][b][i] = fmaf(k[n][t].zc, S[b][i], acc[n][t][b][i]);
+        }
+}
+
 // Adds GW groups (the first `live` of them) of NT tensors' plane tiles to acc[n][t][b][i] (tensor n, column
 // block t, row block b, row 4q + i of the block). plane[n] and high[n] point at the slice's first group for the
 // lane's column (load_row_group), meta[n] at its first meta unit for the lane's own column l (+ META l: one load per
@@ -239,7 +279,7 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
     if (u + P < GW) issue(u + P);
     __builtin_amdgcn_sched_barrier(0);
     if ((uint32_t)u < live) {
-      if (u % UNIT == 0) {
+      if (u % UNIT == 0 && !owner_coefs<FMT>()) {
 #pragma unroll
         for (int n = 0; n < NT; ++n)
 #pragma unroll
@@ -251,7 +291,18 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
 #pragma unroll
       for (int n = 0; n < NT; ++n) row_operands<FMT>(codes[n][u], hshift, cc, lo[n], hi[n]);
       row_group_mfma<FMT, MB, NT>(x, lo, hi, u % SG == 0, C, C2, S, S2);
-      if ((u + 1) % SG == 0) row_group_close<FMT, MB, NT>(mw, u, C, C2, S, S2, acc);
+      if ((u + 1) % SG == 0) {
+        if constexpr (owner_coefs<FMT>()) {
+          MetaWords unit[NT];
+#pragma unroll
+          for (int n = 0; n < NT; ++n) unit[n] = own[n][u / UNIT];
+          CloseCoef k[NT][4];
+          spread_coefs<FMT, NT>(unit, u, j, k);
+          row_group_close_coefs<MB, NT>(k, C, S, acc);
+        } else {
+          row_group_close<FMT, MB, NT>(mw, u, C, C2, S, S2, acc);
+        }
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -308,12 +359,14 @@ __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], co
   const int j = threadIdx.x & 15;
   const auto compute = [&](uint32_t c, int set, int next_set) __attribute__((always_inline)) {
     MetaWords mw[NT][4][MU];
+    if constexpr (!owner_coefs<FMT>()) {
 #pragma unroll
-    for (int n = 0; n < NT; ++n)
+      for (int n = 0; n < NT; ++n)
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int m = 0; m < MU; ++m) mw[n][t][m] = spread_meta<FMT>(own[set][n][m], t, j);
+          for (int m = 0; m < MU; ++m) mw[n][t][m] = spread_meta<FMT>(own[set][n][m], t, j);
+    }
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const uint32_t g = c * CH + u;
@@ -330,12 +383,21 @@ __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], co
           else prepare(next_set, 0, os ^ 1);
         }
         if ((u + 1) % SG == 0) {
-          MetaWords m[NT][4];
+          if constexpr (owner_coefs<FMT>()) {
+            MetaWords unit[NT];
 #pragma unroll
-          for (int n = 0; n < NT; ++n)
+            for (int n = 0; n < NT; ++n) unit[n] = own[set][n][UNIT < CH ? u / UNIT : 0];
+            CloseCoef k[NT][4];
+            spread_coefs<FMT, NT>(unit, g, j, k);
+            row_group_close_coefs<MB, NT>(k, C, S, acc);
+          } else {
+            MetaWords m[NT][4];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) m[n][t] = mw[n][t][UNIT < CH ? u / UNIT : 0];
-          row_group_close<FMT, MB, NT>(m, g, C, C2, S, S2, acc);
+            for (int n = 0; n < NT; ++n)
+#pragma unroll
+              for (int t = 0; t < 4; ++t) m[n][t] = mw[n][t][UNIT < CH ? u / UNIT : 0];
+            row_group_close<FMT, MB, NT>(m, g, C, C2, S, S2, acc);
+          }
         }
       }
       __builtin_amdgcn_sched_barrier(0);
