@@ -190,43 +190,60 @@ __device__ __forceinline__ MetaWords spread_meta(const MetaWords &own, int t, in
 }
 
 // Q4_K and Q5_K: a group's coefficients cost ~9 VALU from the 16-byte header (6-bit scale and min of the group's
-// sub-block), so each lane derives them once, for its own column l, and hands (s, zc = z - 128 s) to the lanes whose
-// MFMA blocks hold the column (two ds_bpermute a column block) instead of every lane deriving them for its four
-// columns from spread header words.
+// sub-block), and Q6_K's two half scales ~14 from its 20 bytes, so each lane derives them once, for its own column l,
+// and hands them to the lanes whose MFMA blocks hold the column (two ds_bpermute a column block) instead of every lane
+// deriving them for its four columns from spread meta words. The values are the same, so the sums are the same bits.
 template <uint32_t FMT>
-constexpr bool owner_coefs() { return FMT == SQ_FMT_Q4K || FMT == SQ_FMT_Q5K; }
+constexpr bool owner_coefs() { return FMT == SQ_FMT_Q4K || FMT == SQ_FMT_Q5K || FMT == SQ_FMT_Q6K; }
+// A column's close coefficients for one group: (s, zc = z - 128 s), or Q6_K's half scales (s0, s1).
 struct CloseCoef {
-  float s, zc;
+  float a, b;
 };
 template <uint32_t FMT, int NT>
 __device__ __forceinline__ void spread_coefs(const MetaWords (&own)[NT], uint32_t g, int j, CloseCoef (&k)[NT][4]) {
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
-    const Coef mine = coef<FMT>(own[n], g);
-    const float zc = fmaf(-128.0f, mine.s, mine.z);
+    CloseCoef mine;
+    if constexpr (Fmt<FMT>::HALVES) {
+      mine = {q6k_scale(own[n], g, 0), q6k_scale(own[n], g, 1)};
+    } else {
+      const Coef c = coef<FMT>(own[n], g);
+      mine = {c.s, fmaf(-128.0f, c.s, c.z)};
+    }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int from = (16 * t + j) * 4;
-      k[n][t].s = __int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(mine.s)));
-      k[n][t].zc = __int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(zc)));
+      k[n][t].a = __int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(mine.a)));
+      k[n][t].b = __int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(mine.b)));
     }
   }
 }
-// row_group_close's fp32 close from handed coefficients: acc += s C + zc S, in the same order.
-template <int MB, int NT>
+// row_group_close's fp32 close from handed coefficients, in the same order: acc += s C + zc S, or Q6_K's
+// s0 C + s1 C2 - 160 s0 S - 160 s1 S2.
+template <uint32_t FMT, int MB, int NT>
 __device__ __forceinline__ void row_group_close_coefs(const CloseCoef (&k)[NT][4], const f32x4 (&C)[NT][4][MB],
-                                                      const f32x4 (&S)[MB], float (&acc)[NT][4][MB][4]) {
+                                                      const f32x4 (&C2)[NT][4][MB], const f32x4 (&S)[MB],
+                                                      const f32x4 (&S2)[MB], float (&acc)[NT][4][MB][4]) {
 #pragma unroll
   for (int n = 0; n < NT; ++n)
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < 4; ++t) {
+      const float s0 = k[n][t].a, s1 = k[n][t].b;
 #pragma unroll
       for (int b = 0; b < MB; ++b)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          acc[n][t][b][i] = fmaf(k[n][t].s, C[n][t][b][i], acc[n][t][b][i]);
-          acc[n][t][b][i] = fmaf(k[n][t].zc, S[b][i], acc[n][t][b][i]);
+          if constexpr (Fmt<FMT>::HALVES) {
+            acc[n][t][b][i] = fmaf(s0, C[n][t][b][i], acc[n][t][b][i]);
+            acc[n][t][b][i] = fmaf(s1, C2[n][t][b][i], acc[n][t][b][i]);
+            acc[n][t][b][i] = fmaf(-160.0f * s0, S[b][i], acc[n][t][b][i]);
+            acc[n][t][b][i] = fmaf(-160.0f * s1, S2[b][i], acc[n][t][b][i]);
+          } else {
+            acc[n][t][b][i] = fmaf(s0, C[n][t][b][i], acc[n][t][b][i]);
+            acc[n][t][b][i] = fmaf(s1, S[b][i], acc[n][t][b][i]);
+          }
         }
+    }
 }
 
 // Adds GW groups (the first `live` of them) of NT tensors' plane tiles to acc[n][t][b][i] (tensor n, column
@@ -298,7 +315,7 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
           for (int n = 0; n < NT; ++n) unit[n] = own[n][u / UNIT];
           CloseCoef k[NT][4];
           spread_coefs<FMT, NT>(unit, u, j, k);
-          row_group_close_coefs<MB, NT>(k, C, S, acc);
+          row_group_close_coefs<FMT, MB, NT>(k, C, C2, S, S2, acc);
         } else {
           row_group_close<FMT, MB, NT>(mw, u, C, C2, S, S2, acc);
         }
@@ -389,7 +406,7 @@ __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], co
             for (int n = 0; n < NT; ++n) unit[n] = own[set][n][UNIT < CH ? u / UNIT : 0];
             CloseCoef k[NT][4];
             spread_coefs<FMT, NT>(unit, g, j, k);
-            row_group_close_coefs<MB, NT>(k, C, S, acc);
+            row_group_close_coefs<FMT, MB, NT>(k, C, C2, S, S2, acc);
           } else {
             MetaWords m[NT][4];
 #pragma unroll
