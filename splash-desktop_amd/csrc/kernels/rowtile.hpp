@@ -139,62 +139,11 @@ __device__ __forceinline__ void row_group_mfma(const u32x4 (&x)[MB], const u32x4
 
 // A scale group's close in fp32, every product exact: acc += s C + zc S with zc = z - 128 s (4-bit and 5-bit codes
 // 128 + q), z - 2176 s (8-bit codes, C = sum x u + 2176 sum x; Q8_0's value d (u - 128): z = -128 d), and Q6_K's
-// s_h (q - 32) = s_h (128 + q) - 160 s_h per half. `g` is the group's index in its meta unit's numbering (its
+// s_h (q - 32) = s_h (128 + q) - 160 s_h per half. A lane holds four columns (16 t + j), so each lane derives the
+// coefficients once, for its own column l (a Q4_K or Q5_K group's from its 16-byte header costs ~9 VALU, Q6_K's half
+// scales ~14), and hands them to the lanes whose MFMA blocks hold the column: two ds_bpermute a column block, through
+// the LDS crossbar (no LDS memory, not the VALU). `g` is the group's index in its meta unit's numbering (its
 // super-block position).
-template <uint32_t FMT, int MB, int NT>
-__device__ __forceinline__ void row_group_close(const MetaWords (&mw)[NT][4], uint32_t g, const f32x4 (&C)[NT][4][MB],
-                                                const f32x4 (&C2)[NT][4][MB], const f32x4 (&S)[MB],
-                                                const f32x4 (&S2)[MB], float (&acc)[NT][4][MB][4]) {
-  using F = Fmt<FMT>;
-#pragma unroll
-  for (int n = 0; n < NT; ++n)
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      if constexpr (F::HALVES) {
-        const float s0 = q6k_scale(mw[n][t], g, 0), s1 = q6k_scale(mw[n][t], g, 1);
-        const float z0 = -160.0f * s0, z1 = -160.0f * s1;
-#pragma unroll
-        for (int b = 0; b < MB; ++b)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            acc[n][t][b][i] = fmaf(s0, C[n][t][b][i], acc[n][t][b][i]);
-            acc[n][t][b][i] = fmaf(s1, C2[n][t][b][i], acc[n][t][b][i]);
-            acc[n][t][b][i] = fmaf(z0, S[b][i], acc[n][t][b][i]);
-            acc[n][t][b][i] = fmaf(z1, S2[b][i], acc[n][t][b][i]);
-          }
-      } else {
-        const Coef k = coef<FMT>(mw[n][t], g);
-        const float zc = F::P0 == 32 ? fmaf(-2176.0f, k.s, FMT == SQ_FMT_Q80 ? -128.0f * k.s : k.z)
-                                     : fmaf(-128.0f, k.s, k.z);
-#pragma unroll
-        for (int b = 0; b < MB; ++b)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            acc[n][t][b][i] = fmaf(k.s, C[n][t][b][i], acc[n][t][b][i]);
-            acc[n][t][b][i] = fmaf(zc, S[b][i], acc[n][t][b][i]);
-          }
-      }
-    }
-}
-
-// Column 16 t + j's meta at lane (j, q), from the lanes that loaded their own column's (lane l holds column l's):
-// ds_bpermute through the LDS crossbar (no LDS memory, not the VALU), one per word of the format's meta.
-template <uint32_t FMT>
-__device__ __forceinline__ MetaWords spread_meta(const MetaWords &own, int t, int j) {
-  constexpr int W = (Fmt<FMT>::META + 3) / 4;
-  MetaWords m{};
-  const int from = (16 * t + j) * 4;
-#pragma unroll
-  for (int w = 0; w < W; ++w) m.w[w] = (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)own.w[w]);
-  return m;
-}
-
-// Q4_K and Q5_K: a group's coefficients cost ~9 VALU from the 16-byte header (6-bit scale and min of the group's
-// sub-block), and Q6_K's two half scales ~14 from its 20 bytes, so each lane derives them once, for its own column l,
-// and hands them to the lanes whose MFMA blocks hold the column (two ds_bpermute a column block) instead of every lane
-// deriving them for its four columns from spread meta words. The values are the same, so the sums are the same bits.
-template <uint32_t FMT>
-constexpr bool owner_coefs() { return FMT == SQ_FMT_Q4K || FMT == SQ_FMT_Q5K || FMT == SQ_FMT_Q6K; }
 // A column's close coefficients for one group: (s, zc = z - 128 s), or Q6_K's half scales (s0, s1).
 struct CloseCoef {
   float a, b;
@@ -208,7 +157,10 @@ __device__ __forceinline__ void spread_coefs(const MetaWords (&own)[NT], uint32_
       mine = {q6k_scale(own[n], g, 0), q6k_scale(own[n], g, 1)};
     } else {
       const Coef c = coef<FMT>(own[n], g);
-      mine = {c.s, fmaf(-128.0f, c.s, c.z)};
+      // row_group_close's zc: 8-bit codes' z - 2176 s (Q8_0: -128 d - 2176 d), else z - 128 s.
+      const float zc = Fmt<FMT>::P0 == 32 ? fmaf(-2176.0f, c.s, FMT == SQ_FMT_Q80 ? -128.0f * c.s : c.z)
+                                          : fmaf(-128.0f, c.s, c.z);
+      mine = {c.s, zc};
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -218,12 +170,11 @@ __device__ __forceinline__ void spread_coefs(const MetaWords (&own)[NT], uint32_
     }
   }
 }
-// row_group_close's fp32 close from handed coefficients, in the same order: acc += s C + zc S, or Q6_K's
-// s0 C + s1 C2 - 160 s0 S - 160 s1 S2.
+// The close from the handed coefficients: acc += s C + zc S, or Q6_K's s0 C + s1 C2 - 160 s0 S - 160 s1 S2.
 template <uint32_t FMT, int MB, int NT>
-__device__ __forceinline__ void row_group_close_coefs(const CloseCoef (&k)[NT][4], const f32x4 (&C)[NT][4][MB],
-                                                      const f32x4 (&C2)[NT][4][MB], const f32x4 (&S)[MB],
-                                                      const f32x4 (&S2)[MB], float (&acc)[NT][4][MB][4]) {
+__device__ __forceinline__ void row_group_close(const CloseCoef (&k)[NT][4], const f32x4 (&C)[NT][4][MB],
+                                                const f32x4 (&C2)[NT][4][MB], const f32x4 (&S)[MB],
+                                                const f32x4 (&S2)[MB], float (&acc)[NT][4][MB][4]) {
 #pragma unroll
   for (int n = 0; n < NT; ++n)
 #pragma unroll
@@ -249,8 +200,8 @@ __device__ __forceinline__ void row_group_close_coefs(const CloseCoef (&k)[NT][4
 // Adds GW groups (the first `live` of them) of NT tensors' plane tiles to acc[n][t][b][i] (tensor n, column
 // block t, row block b, row 4q + i of the block). plane[n] and high[n] point at the slice's first group for the
 // lane's column (load_row_group), meta[n] at its first meta unit for the lane's own column l (+ META l: one load per
-// unit and tensor, which spread_meta hands to the lanes whose MFMA blocks hold the column); xrow[b] at the lane's
-// row 16 b + j, inputs 4q of the slice's first group.
+// unit and tensor, whose coefficients spread_coefs hands to the lanes whose MFMA blocks hold the column); xrow[b] at
+// the lane's row 16 b + j, inputs 4q of the slice's first group.
 template <uint32_t FMT, int MB, int GW, int NT>
 __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], const uint8_t *const (&high)[NT],
                                           const uint8_t *const (&meta)[NT], const uint16_t *const (&xrow)[MB],
@@ -289,19 +240,12 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
   for (int u = 0; u < P; ++u) issue(u);
 
   f32x4 C[NT][4][MB], C2[NT][4][MB], S[MB], S2[MB];
-  MetaWords mw[NT][4];   // the current unit's meta of column 16 t + j
   const int j = threadIdx.x & 15;
 #pragma unroll
   for (int u = 0; u < GW; ++u) {
     if (u + P < GW) issue(u + P);
     __builtin_amdgcn_sched_barrier(0);
     if ((uint32_t)u < live) {
-      if (u % UNIT == 0 && !owner_coefs<FMT>()) {
-#pragma unroll
-        for (int n = 0; n < NT; ++n)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) mw[n][t] = spread_meta<FMT>(own[n][u / UNIT], t, j);
-      }
       u32x4 x[MB], lo[NT][4], hi[NT][4];
 #pragma unroll
       for (int b = 0; b < MB; ++b) x[b] = xv[b][u];
@@ -309,16 +253,12 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
       for (int n = 0; n < NT; ++n) row_operands<FMT>(codes[n][u], hshift, cc, lo[n], hi[n]);
       row_group_mfma<FMT, MB, NT>(x, lo, hi, u % SG == 0, C, C2, S, S2);
       if ((u + 1) % SG == 0) {
-        if constexpr (owner_coefs<FMT>()) {
-          MetaWords unit[NT];
+        MetaWords unit[NT];
 #pragma unroll
-          for (int n = 0; n < NT; ++n) unit[n] = own[n][u / UNIT];
-          CloseCoef k[NT][4];
-          spread_coefs<FMT, NT>(unit, u, j, k);
-          row_group_close_coefs<FMT, MB, NT>(k, C, C2, S, S2, acc);
-        } else {
-          row_group_close<FMT, MB, NT>(mw, u, C, C2, S, S2, acc);
-        }
+        for (int n = 0; n < NT; ++n) unit[n] = own[n][u / UNIT];
+        CloseCoef k[NT][4];
+        spread_coefs<FMT, NT>(unit, u, j, k);
+        row_group_close<FMT, MB, NT>(k, C, C2, S, S2, acc);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -329,7 +269,7 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
 // groups, each chunk's loads (clamped to the last group, so every chunk issues as many) issued SETS - 1 chunks
 // ahead into a ring of SETS register sets; AHEAD builds each group's operands a group ahead (else just before its
 // MFMAs). plane[n] and high[n] point at group 0 for the lane, meta[n] at unit 0 of the lane's own column l (one
-// load per unit and tensor, spread_meta hands each lane the columns its MFMA blocks hold). The input rows come in the
+// load per unit and tensor, spread_coefs hands each lane the columns its MFMA blocks hold). The input rows come in the
 // tile's read order
 // (16-byte chunk 4 g + c of a row: inputs 32 g + 4 c .. +3 then 32 g + 16 + 4 c .. +3), so each group of a row block
 // is one 16-byte load a lane, half the vector memory instructions of two 8-byte loads from a row in input order:
@@ -375,15 +315,6 @@ __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], co
   };
   const int j = threadIdx.x & 15;
   const auto compute = [&](uint32_t c, int set, int next_set) __attribute__((always_inline)) {
-    MetaWords mw[NT][4][MU];
-    if constexpr (!owner_coefs<FMT>()) {
-#pragma unroll
-      for (int n = 0; n < NT; ++n)
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int m = 0; m < MU; ++m) mw[n][t][m] = spread_meta<FMT>(own[set][n][m], t, j);
-    }
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const uint32_t g = c * CH + u;
@@ -400,21 +331,12 @@ __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], co
           else prepare(next_set, 0, os ^ 1);
         }
         if ((u + 1) % SG == 0) {
-          if constexpr (owner_coefs<FMT>()) {
-            MetaWords unit[NT];
+          MetaWords unit[NT];
 #pragma unroll
-            for (int n = 0; n < NT; ++n) unit[n] = own[set][n][UNIT < CH ? u / UNIT : 0];
-            CloseCoef k[NT][4];
-            spread_coefs<FMT, NT>(unit, g, j, k);
-            row_group_close_coefs<FMT, MB, NT>(k, C, C2, S, S2, acc);
-          } else {
-            MetaWords m[NT][4];
-#pragma unroll
-            for (int n = 0; n < NT; ++n)
-#pragma unroll
-              for (int t = 0; t < 4; ++t) m[n][t] = mw[n][t][UNIT < CH ? u / UNIT : 0];
-            row_group_close<FMT, MB, NT>(m, g, C, C2, S, S2, acc);
-          }
+          for (int n = 0; n < NT; ++n) unit[n] = own[set][n][UNIT < CH ? u / UNIT : 0];
+          CloseCoef k[NT][4];
+          spread_coefs<FMT, NT>(unit, g, j, k);
+          row_group_close<FMT, MB, NT>(k, C, C2, S, S2, acc);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
