@@ -422,20 +422,17 @@ void expert_kernel(MoeExpertArgs a) {
   else expert_tile<FMT, MB, NT>(a, d, tile, ct);
 }
 
-// Thread: one group of 32 inputs, its four 16-byte chunks of the table (chunk c: 4-input units c and c + 4 of the
-// group, the prefill's half rows order, half_rows.hpp) from the group's four 16-byte vectors in input order (the
-// reference's routed pass opens with its gather of the input rows into the grouped input, MoE.cpp:480-517; here the
-// rows keep their order and the gate/up pass gathers through the routes as it reads).
-__global__ __launch_bounds__(256) void input_rows_kernel(const uint16_t *input, uint64_t groups, uint16_t *table) {
-  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;   // group i of 32 inputs, rows back to back
-  if (i >= groups) return;
-  const u32x4 *in = (const u32x4 *)(input + 32 * i);
-  u32x4 *out = (u32x4 *)(table + 32 * i);
-  const u32x4 a = in[0], b = in[1], c = in[2], d = in[3];   // inputs 0..7, 8..15, 16..23, 24..31
-  out[0] = u32x4{a[0], a[1], c[0], c[1]};                    // chunk c: units c and c + 4
-  out[1] = u32x4{a[2], a[3], c[2], c[3]};
-  out[2] = u32x4{b[0], b[1], d[0], d[1]};
-  out[3] = u32x4{b[2], b[3], d[2], d[3]};
+// Thread: one 16-byte chunk of the table, chunk c of a group of 32 inputs: its 4-input units c and c + 4 (inputs
+// 4c..4c+3 and 16+4c..19+4c, the group's dwords 2c, 2c + 1 and 8 + 2c, 9 + 2c), the prefill's half rows order
+// (half_rows.hpp). The reference's routed pass opens with its gather of the input rows into the grouped input
+// (MoE.cpp:480-517); here the rows keep their order and the gate/up pass gathers through the routes as it reads.
+// Four threads a group, so each wave reads and writes 1 KiB contiguous.
+__global__ __launch_bounds__(256) void input_rows_kernel(const uint16_t *input, uint64_t chunks, uint16_t *table) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;   // chunk i % 4 of group i / 4, rows back to back
+  if (i >= chunks) return;
+  const uint32_t *in = (const uint32_t *)(input + 32 * (i / 4)) + 2 * (i % 4);
+  const u32x2 lo = *(const u32x2 *)in, hi = *(const u32x2 *)(in + 8);
+  *(u32x4 *)(table + 8 * i) = u32x4{lo[0], lo[1], hi[0], hi[1]};
 }
 
 // out[r][d] = bf16(residual + sum_slot w_slot * expert_out[route_rows[slot]][d]) in slot order (moe.metal:480-505).
@@ -451,15 +448,32 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *expert_out
 #pragma unroll
   for (int e = 0; e < 4; ++e) v[2 * e] = bf16_to_f32(res[e] & 0xFFFFu), v[2 * e + 1] = bf16_to_f32(res[e] >> 16);
   const size_t route = (size_t)r * p.routes_per_row;
-  for (uint32_t slot = 0; slot < p.routes_per_row; ++slot) {
-    const uint32_t grouped = route_rows[route + slot];
-    if (grouped == ~0u) continue;
-    const float w = weights[route + slot];
-    const u32x4 x = *(const u32x4 *)(expert_output + (size_t)grouped * p.hidden_size + d);
+  // Eight slots at a time: their route rows (one scalar load each: the row is the workgroup's), then every live
+  // slot's 16 bytes in flight together, then the sums in slot order. A route row of ~0u (a dead verify row) adds
+  // nothing, not even a zero.
+  constexpr uint32_t kBatch = 8;
+  for (uint32_t s0 = 0; s0 < p.routes_per_row; s0 += kBatch) {
+    uint32_t grouped[kBatch];
+    u32x4 x[kBatch];
+    float w[kBatch];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[2 * e] = fmaf(w, bf16_to_f32(x[e] & 0xFFFFu), v[2 * e]);
-      v[2 * e + 1] = fmaf(w, bf16_to_f32(x[e] >> 16), v[2 * e + 1]);
+    for (uint32_t k = 0; k < kBatch; ++k) {
+      grouped[k] = s0 + k < p.routes_per_row ? route_rows[route + s0 + k] : ~0u;
+      w[k] = 0.0f;
+      x[k] = u32x4{0u, 0u, 0u, 0u};
+      if (grouped[k] != ~0u) {
+        w[k] = weights[route + s0 + k];
+        x[k] = *(const u32x4 *)(expert_output + (size_t)grouped[k] * p.hidden_size + d);
+      }
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kBatch; ++k) {
+      if (grouped[k] == ~0u) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[2 * e] = fmaf(w[k], bf16_to_f32(x[k][e] & 0xFFFFu), v[2 * e]);
+        v[2 * e + 1] = fmaf(w[k], bf16_to_f32(x[k][e] >> 16), v[2 * e + 1]);
+      }
     }
   }
   u32x4 out;
@@ -508,8 +522,8 @@ hipError_t launch_moe_group(const uint32_t *selected, SqMoeTileDescriptor *tiles
 hipError_t launch_moe_input_rows(const uint16_t *input, uint32_t rows, uint32_t K, uint16_t *table,
                                  hipStream_t stream) {
   if (K % 32) return hipErrorInvalidValue;
-  const uint64_t groups = (uint64_t)rows * (K / 32);
-  hipLaunchKernelGGL(input_rows_kernel, dim3((uint32_t)((groups + 255) / 256)), dim3(256), 0, stream, input, groups,
+  const uint64_t chunks = (uint64_t)rows * (K / 32) * 4;
+  hipLaunchKernelGGL(input_rows_kernel, dim3((uint32_t)((chunks + 255) / 256)), dim3(256), 0, stream, input, chunks,
                      table);
   return hipGetLastError();
 }
