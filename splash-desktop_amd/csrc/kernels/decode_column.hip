@@ -49,9 +49,13 @@ __device__ __forceinline__ float dpp_add(float v) {
 
 // Wave `slice`'s K slice of plane tile `tile` of segment `seg` (K partition `split`), in format FMT, into acc; the
 // slice's input sums go through the wave's own xsum[slice] (NHS slots a group, at least the format's halves).
-template <uint32_t FMT, int MR, int GW, int NT, int NHS>
+// NARROW: the wave takes columns 16 cs..16 cs + 15 of the tile and four K slices, 4 slice + q for its quarter q (lanes
+// 16q..16q + 15, lane 16q + c column 16 cs + c), every slice whole; each lane computes exactly what the wide walk's
+// lane of that column computes for that slice (the same activations, operands, MFMA blocks, input-sum tree and
+// closes, in the same order), so the two layouts give the same bits.
+template <uint32_t FMT, int MR, int GW, int NT, int NHS, bool NARROW>
 __device__ __forceinline__ void column_walk(const DecodeArgs &a, const Segment &seg, uint32_t tile, uint32_t split,
-                                            uint32_t slice, float (&xsum)[kColumnMaxWaves][GW][NHS][4],
+                                            uint32_t slice, uint32_t cs, float (&xsum)[kColumnMaxWaves][GW][NHS][4],
                                             float (&acc)[NT][MR]) {
   using F = Fmt<FMT>;
   // Groups in flight: 8-bit codes of a gate/up pair (four 16-byte loads a group) keep two, to fit the registers of
@@ -59,16 +63,20 @@ __device__ __forceinline__ void column_walk(const DecodeArgs &a, const Segment &
   constexpr int kDepth = F::P0 == 32 && NT == 2 ? 2 : kPipe;
   constexpr int SG = F::SG, UNIT = F::UNIT, P = GW < kDepth ? GW : kDepth;
   static_assert(GW % UNIT == 0 && GW % 2 == 0 && GW % SG == 0, "a slice holds whole meta units and group pairs");
-  const int lane = threadIdx.x & 63, b = lane >> 2, i = lane & 3;
-  const uint32_t G = a.K >> 5, units = G / UNIT, gs = G / a.splits;
-  const uint32_t gb = split * gs + slice * GW, live = min((uint32_t)GW, gs - min(gs, slice * GW));
+  const int lane = threadIdx.x & 63, b = lane >> 2, i = lane & 3, c16 = lane & 15, xa = c16 >> 2;
+  const uint32_t G = a.K >> 5, units = G / UNIT, gs = G / a.splits, slices = gs / GW;
+  // The lane's column and slice; a narrow quarter past the split's slices streams its first slice again (nothing
+  // reads its sums).
+  const uint32_t col = NARROW ? 16 * cs + c16 : lane, mine = NARROW ? 4 * slice + (lane >> 4) : slice;
+  const uint32_t gb = split * gs + (NARROW && mine >= slices ? 0 : mine) * GW;
+  const uint32_t live = NARROW ? GW : min((uint32_t)GW, gs - min(gs, slice * GW));
   const uint32_t last = live ? live - 1 : 0;
 
   const uint8_t *plane[NT], *meta[NT], *high[NT];
   {
-    const size_t pbase = ((size_t)tile * G * 64 + lane) * F::P0 + (size_t)gb * 64 * F::P0;
-    const size_t hbase = ((size_t)tile * G * 64 + lane) * F::P1 + (size_t)gb * 64 * F::P1;
-    const size_t mbase = ((size_t)tile * units * 64 + lane) * F::META + (size_t)(gb / UNIT) * 64 * F::META;
+    const size_t pbase = ((size_t)tile * G * 64 + col) * F::P0 + (size_t)gb * 64 * F::P0;
+    const size_t hbase = ((size_t)tile * G * 64 + col) * F::P1 + (size_t)gb * 64 * F::P1;
+    const size_t mbase = ((size_t)tile * units * 64 + col) * F::META + (size_t)(gb / UNIT) * 64 * F::META;
     const Segment &first = NT == 2 ? a.gate : seg;
     plane[0] = first.plane0 + pbase;
     meta[0] = first.meta + mbase;
@@ -79,9 +87,12 @@ __device__ __forceinline__ void column_walk(const DecodeArgs &a, const Segment &
       high[1] = F::P1 ? seg.plane1 + hbase : nullptr;
     }
   }
-  // Lane (b, i) reads row i's inputs 4 (b % 8)..+3 of the pair's group b / 8; rows past the live ones read row 0,
-  // whose MFMA rows nothing reads.
-  const uint16_t *xrow = a.input + (size_t)(i < MR && (uint32_t)i < a.rows ? i : 0) * a.K + 4 * (b & 7) + (size_t)gb * 32;
+  // Wide: lane (b, i) reads row i's inputs 4 (b % 8)..+3 of the pair's group b / 8. Narrow: lane (q, a, i) =
+  // 16q + 4a + i reads row i's inputs 8a..8a + 7 of each group of its quarter's slice, so block 4q + a holds the
+  // group's input quads 2a (low half) and 2a + 1 (high half). Rows past the live ones read row 0, whose MFMA rows
+  // nothing reads.
+  const uint16_t *xrow = a.input + (size_t)(i < MR && (uint32_t)i < a.rows ? i : 0) * a.K +
+                         (NARROW ? 8 * xa : 4 * (b & 7)) + (size_t)gb * 32;
   const CodeConstants cc = make_code_constants();
 
 #pragma unroll
@@ -90,13 +101,15 @@ __device__ __forceinline__ void column_walk(const DecodeArgs &a, const Segment &
     for (int r = 0; r < MR; ++r) acc[n][r] = 0.0f;
 
   constexpr bool kWide = F::P0 == 32;   // 8-bit codes: two 16-byte loads and two operand sets a group
-  u32x2 xp[GW / 2];
+  u32x2 xp[NARROW ? 1 : GW / 2];
+  u32x4 xn[NARROW ? GW : 1];
   u32x4 codes[NT][GW];
   u32x4 codes_hi[NT][kWide ? GW : 1];
   u32x2 highs[NT][F::P1 ? GW : 1];
   MetaWords mw[NT][GW / UNIT];
   const auto issue = [&](int u) __attribute__((always_inline)) {
-    if (u % 2 == 0) xp[u / 2] = *(const u32x2 *)(xrow + (size_t)min((uint32_t)(u + (b >> 3)), last) * 32);
+    if constexpr (NARROW) xn[u] = *(const u32x4 *)(xrow + (size_t)min((uint32_t)u, last) * 32);
+    else if (u % 2 == 0) xp[u / 2] = *(const u32x2 *)(xrow + (size_t)min((uint32_t)(u + (b >> 3)), last) * 32);
     if (u % UNIT == 0) {
       const uint32_t v = min((uint32_t)(u / UNIT), last / UNIT);
 #pragma unroll
@@ -116,15 +129,28 @@ __device__ __forceinline__ void column_walk(const DecodeArgs &a, const Segment &
   // The rows' input sums of the slice's groups (of each half for Q6_K): lanes 8j..8j+7 take one (row, group), each
   // lane four inputs, then a fixed tree over the eight lanes (quads first: the halves). Rows past the live ones and
   // groups past the slice's sum to zero, which no close reads. Their inputs are loaded before the stream's first
-  // groups, so waiting for them waits for nothing else.
-  constexpr int NH = F::HALVES ? 2 : 1, kItems = MR * GW * 8, kIt = (kItems + 63) / 64;
+  // groups, so waiting for them waits for nothing else. A narrow wave sums its four slices' (item quarter q: slice
+  // 4 slice + q; a slice past the split's sums nothing).
+  constexpr int NH = F::HALVES ? 2 : 1, kItems = (NARROW ? 4 : 1) * MR * GW * 8, kIt = (kItems + 63) / 64;
   static_assert(NH <= NHS, "the kernel's input-sum slots hold the format's halves");
+  static_assert(kIt <= 16, "the input sums' loads fit the registers of a full workgroup");
+  const auto item_of = [&](int it, int &e, int &g, int &r, uint32_t &sl) __attribute__((always_inline)) {
+    const int item = it * 64 + lane, rest = item >> 3;
+    e = item & 7;
+    g = rest % GW;
+    r = (rest / GW) % MR;
+    sl = NARROW ? 4 * slice + (uint32_t)(rest / (GW * MR)) : slice;
+    return item < kItems;
+  };
   u32x2 xq[kIt];
 #pragma unroll
   for (int it = 0; it < kIt; ++it) {
-    const int item = it * 64 + lane, e = item & 7, g = (item >> 3) % GW, r = (item >> 3) / GW;
-    const bool use = item < kItems && (uint32_t)r < a.rows && (uint32_t)g < live;
-    xq[it] = use ? *(const u32x2 *)(a.input + (size_t)r * a.K + (size_t)(gb + g) * 32 + 4 * e) : u32x2{0u, 0u};
+    int e, g, r;
+    uint32_t sl;
+    const bool in = item_of(it, e, g, r, sl);
+    const bool use = in && (uint32_t)r < a.rows && (uint32_t)g < live && (!NARROW || sl < slices);
+    const size_t at = (size_t)r * a.K + (size_t)(split * gs + sl * GW + g) * 32 + 4 * e;
+    xq[it] = use ? *(const u32x2 *)(a.input + at) : u32x2{0u, 0u};
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -132,13 +158,15 @@ __device__ __forceinline__ void column_walk(const DecodeArgs &a, const Segment &
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int it = 0; it < kIt; ++it) {
-    const int item = it * 64 + lane, e = item & 7, g = (item >> 3) % GW, r = (item >> 3) / GW;
+    int e, g, r;
+    uint32_t sl;
+    const bool in = item_of(it, e, g, r, sl);
     float v = quad_sum(xq[it]);
     v = dpp_add<0xB1>(v);
     v = dpp_add<0x4E>(v);
-    if (F::HALVES && item < kItems && e % 4 == 0) xsum[slice][g][e / 4][r] = v;
+    if (F::HALVES && in && e % 4 == 0) xsum[sl][g][e / 4][r] = v;
     v = dpp_add<0x141>(v);
-    if (!F::HALVES && item < kItems && e == 0) xsum[slice][g][0][r] = v;
+    if (!F::HALVES && in && e == 0) xsum[sl][g][0][r] = v;
   }
   // The wave reads back what its own lanes wrote.
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -147,12 +175,20 @@ __device__ __forceinline__ void column_walk(const DecodeArgs &a, const Segment &
 
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   f32x4 C0[NT], C1[NT], H0[NT], H1[NT];   // H: the high nibbles' chains of 8-bit codes
+  // Input quad Q (inputs 4Q..4Q + 3) of group u against the lane's four operands: wide, block 8 (u % 2) + Q of the
+  // pair's register broadcast to the wave; narrow, block Q / 2 of the quarter (half Q % 2 of its register) broadcast
+  // to the quarter.
+  const auto quad_mfma = [&](int u, int Q, u32x2 operands, f32x4 c) __attribute__((always_inline)) {
+    if constexpr (NARROW)
+      return mfma_bcast_quarter(Q >> 1, Q & 1 ? u32x2{xn[u][2], xn[u][3]} : u32x2{xn[u][0], xn[u][1]}, operands, c);
+    else
+      return mfma_bcast(8 * (u & 1) + Q, xp[u >> 1], operands, c);
+  };
 #pragma unroll
   for (int u = 0; u < GW; ++u) {
     if (u + P < GW) issue(u + P);
     __builtin_amdgcn_sched_barrier(0);
     if ((uint32_t)u < live) {
-      const int p = u >> 1, h = u & 1;
       const bool first = u % SG == 0;
 #pragma unroll
       for (int n = 0; n < NT; ++n)
@@ -168,11 +204,11 @@ __device__ __forceinline__ void column_walk(const DecodeArgs &a, const Segment &
           if constexpr (F::P1 == 8) hb = (highs[n][u][d >> 1] >> (16 * (d & 1))) & 0xFFFFu;
           u32x4 lo, hi;
           chunk_operands<FMT>(w0, w1, hb, cc, lo, hi);
-          C0[n] = mfma_bcast(8 * h + d, xp[p], u32x2{lo[0], lo[1]}, first && d == 0 ? zero : C0[n]);
-          C1[n] = mfma_bcast(8 * h + 4 + d, xp[p], u32x2{lo[2], lo[3]}, first && d == 0 ? zero : C1[n]);
+          C0[n] = quad_mfma(u, d, u32x2{lo[0], lo[1]}, first && d == 0 ? zero : C0[n]);
+          C1[n] = quad_mfma(u, 4 + d, u32x2{lo[2], lo[3]}, first && d == 0 ? zero : C1[n]);
           if constexpr (kWide) {
-            H0[n] = mfma_bcast(8 * h + d, xp[p], u32x2{hi[0], hi[1]}, first && d == 0 ? zero : H0[n]);
-            H1[n] = mfma_bcast(8 * h + 4 + d, xp[p], u32x2{hi[2], hi[3]}, first && d == 0 ? zero : H1[n]);
+            H0[n] = quad_mfma(u, d, u32x2{hi[0], hi[1]}, first && d == 0 ? zero : H0[n]);
+            H1[n] = quad_mfma(u, 4 + d, u32x2{hi[2], hi[3]}, first && d == 0 ? zero : H1[n]);
           }
         }
       if ((u + 1) % SG == 0) {
@@ -181,12 +217,12 @@ __device__ __forceinline__ void column_walk(const DecodeArgs &a, const Segment &
 #pragma unroll
         for (int r = 0; r < MR; ++r) {
           if constexpr (F::HALVES) {
-            sh[0][r] = xsum[slice][u][0][r];
-            sh[1][r] = xsum[slice][u][NH - 1][r];
+            sh[0][r] = xsum[mine][u][0][r];
+            sh[1][r] = xsum[mine][u][NH - 1][r];
           } else {
-            sx[r] = xsum[slice][u + 1 - SG][0][r];
+            sx[r] = xsum[mine][u + 1 - SG][0][r];
 #pragma unroll
-            for (int k = 1; k < SG; ++k) sx[r] += xsum[slice][u + 1 - SG + k][0][r];
+            for (int k = 1; k < SG; ++k) sx[r] += xsum[mine][u + 1 - SG + k][0][r];
           }
         }
 #pragma unroll
@@ -228,12 +264,14 @@ constexpr int xsum_halves() {
 }
 
 // FMT kSegmentFormats: each workgroup runs its segment's format.
-template <uint32_t FMT, int MR, int GW, int NT, uint32_t EP, bool F32OUT>
+// NARROW: workgroup x takes columns 16 (x % 4)..+15 of tile x / 4 over the whole K (one split, whole slices), its
+// waves four slices each; the slices then meet in LDS as the wide workgroup's do.
+template <uint32_t FMT, int MR, int GW, int NT, uint32_t EP, bool F32OUT, bool NARROW>
 __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs a) {
   const int lane = threadIdx.x & 63;
   const uint32_t slice = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), waves = blockDim.x >> 6;
-  const uint32_t split = blockIdx.y;
-  uint32_t tile = blockIdx.x, s = 0;
+  const uint32_t split = blockIdx.y, cs = NARROW ? blockIdx.x & 3 : 0;
+  uint32_t tile = NARROW ? blockIdx.x >> 2 : blockIdx.x, s = 0;
   while (s + 1 < a.segments && tile >= a.seg[s].tiles) tile -= a.seg[s++].tiles;
   const Segment seg = a.seg[s];
   constexpr int NHS = xsum_halves<FMT>();
@@ -241,20 +279,22 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
   float acc[NT][MR];
   if constexpr (FMT == kSegmentFormats)
     with_format(seg.fmt, [&](auto f) {
-      column_walk<decltype(f)::value, MR, GW, NT, NHS>(a, seg, tile, split, slice, xsum, acc);
+      column_walk<decltype(f)::value, MR, GW, NT, NHS, NARROW>(a, seg, tile, split, slice, cs, xsum, acc);
     });
   else
-    column_walk<FMT, MR, GW, NT, NHS>(a, seg, tile, split, slice, xsum, acc);
+    column_walk<FMT, MR, GW, NT, NHS, NARROW>(a, seg, tile, split, slice, cs, xsum, acc);
 
   // Slices meet in LDS; row r's outputs (of both tensors) belong to wave r % waves, which adds them in slice order
-  // and stores them (or stages them for the split reduce).
+  // and stores them (or stages them for the split reduce). Narrow: lane 16q + c holds slice 4 wave + q of column
+  // 16 cs + c, and lanes 0..15 of the row's wave add the slices.
   __shared__ float red[kColumnMaxWaves][NT][MR][64];
+  const uint32_t slices = NARROW ? (a.K >> 5) / a.splits / GW : waves, c = NARROW ? lane & 15 : lane;
 #pragma unroll
   for (int n = 0; n < NT; ++n)
 #pragma unroll
-    for (int r = 0; r < MR; ++r) red[slice][n][r][lane] = acc[n][r];
+    for (int r = 0; r < MR; ++r) red[NARROW ? 4 * slice + (lane >> 4) : slice][n][r][c] = acc[n][r];
   __syncthreads();
-  const uint32_t col = seg.out_offset + tile * 64 + lane;
+  const uint32_t col = seg.out_offset + tile * 64 + 16 * cs + c;
   const uint32_t cstride = NT == 2 ? 2 * a.out_stride : a.out_stride;
   float total[NT][MR];
   bool rlive[NT][MR];
@@ -263,14 +303,15 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
   for (int n = 0; n < NT; ++n)
 #pragma unroll
     for (int r = 0; r < MR; ++r) {
-      const bool mine = (uint32_t)r % waves == slice;
+      const bool mine = (uint32_t)r % waves == slice && (!NARROW || lane < 16);
       float v = 0.0f;
       if (mine)
-        for (uint32_t w = 0; w < waves; ++w) v += red[w][n][r][lane];
+        for (uint32_t w = 0; w < slices; ++w) v += red[w][n][r][c];
       total[n][r] = v;
       rlive[n][r] = mine && (uint32_t)r < a.rows;
       index[n][r] = (size_t)r * cstride + n * a.out_stride + col;
     }
+  // Counters: one per workgroup column, a 16-column workgroup's among them (the plan holds one per 16 columns).
   if (a.splits > 1 && !split_reduce<NT, MR>(total, rlive, index, a.partials, (size_t)a.rows * cstride, split,
                                             a.splits, a.counters + blockIdx.x, true))
     return;
@@ -289,14 +330,38 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
   }
 }
 
+// The narrow layout (16-column workgroups, each wave four K slices) runs when the caller asks for it
+// (column_slices 4), the split's slices are whole, and the input sums of a wave's four slices fit its registers
+// (rows x groups a slice at most 32); otherwise the wide one. Both give the same bits. Q6_K gate/up pairs keep the
+// wide layout (their narrow walk of 16-group slices spills).
+template <uint32_t FMT, int MR, int GW, int NT>
+constexpr bool narrow_fits() {
+  if constexpr (FMT != kSegmentFormats && NT == 2) {
+    if (Fmt<FMT>::HALVES) return false;
+  }
+  return MR * GW <= 32;
+}
+
+template <uint32_t FMT, int MR, int GW, int NT, uint32_t EP, bool F32OUT>
+void launch_gw(const DecodeArgs &a, uint32_t tiles, DecodeLayout layout, hipStream_t stream) {
+  if constexpr (narrow_fits<FMT, MR, GW, NT>()) {
+    if (a.column_slices == 4 && layout.nb * layout.ks == (a.K >> 5) / a.splits) {
+      const dim3 grid(tiles * 4, a.splits), block(64 * ((layout.nb + 3) / 4));
+      hipLaunchKernelGGL((column_kernel<FMT, MR, GW, NT, EP, F32OUT, true>), grid, block, 0, stream, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((column_kernel<FMT, MR, GW, NT, EP, F32OUT, false>), dim3(tiles, a.splits),
+                     dim3(64 * layout.nb), 0, stream, a);
+}
+
 template <uint32_t FMT, int MR, int NT, uint32_t EP, bool F32OUT>
 hipError_t launch_mr(const DecodeArgs &a, uint32_t tiles, DecodeLayout layout, hipStream_t stream) {
-  const dim3 grid(tiles, a.splits), block(64 * layout.nb);
   switch (layout.ks) {
-    case 8: hipLaunchKernelGGL((column_kernel<FMT, MR, 8, NT, EP, F32OUT>), grid, block, 0, stream, a); break;
-    case 16: hipLaunchKernelGGL((column_kernel<FMT, MR, 16, NT, EP, F32OUT>), grid, block, 0, stream, a); break;
+    case 8: launch_gw<FMT, MR, 8, NT, EP, F32OUT>(a, tiles, layout, stream); break;
+    case 16: launch_gw<FMT, MR, 16, NT, EP, F32OUT>(a, tiles, layout, stream); break;
     default:
-      if constexpr (NT == 1) hipLaunchKernelGGL((column_kernel<FMT, MR, 32, NT, EP, F32OUT>), grid, block, 0, stream, a);
+      if constexpr (NT == 1) launch_gw<FMT, MR, 32, NT, EP, F32OUT>(a, tiles, layout, stream);
       break;
   }
   return hipGetLastError();

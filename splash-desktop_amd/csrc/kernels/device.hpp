@@ -51,6 +51,17 @@ __device__ __forceinline__ f32x4 mfma_bcast(int abid, u32x2 a, u32x2 b, f32x4 c)
   return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(av, bv, c, 4, 15, 0);
 #undef SQ_MFMA_BCAST
 }
+// The same blocks with the A of block `abid` of each quarter broadcast within its quarter (cbsz 2: blocks 4q..4q + 3,
+// lanes 16q..16q + 15, take block 4q + abid's A): each 16-lane quarter multiplies its own activations.
+__device__ __forceinline__ f32x4 mfma_bcast_quarter(int abid, u32x2 a, u32x2 b, f32x4 c) {
+  const i16x4 av = __builtin_bit_cast(i16x4, a), bv = __builtin_bit_cast(i16x4, b);
+  switch (abid) {
+    case 0: return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(av, bv, c, 2, 0, 0);
+    case 1: return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(av, bv, c, 2, 1, 0);
+    case 2: return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(av, bv, c, 2, 2, 0);
+    default: return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(av, bv, c, 2, 3, 0);
+  }
+}
 
 // The eight codes of plane word w as exact bf16 operands 128 + q, in chunk-element order: pair p (bits 4p and
 // 16 + 4p) gives operands 2p and 2p + 1. bf16 0x4300 is 128 with unit spacing, so or-ing a code into its mantissa

@@ -51,6 +51,9 @@ struct DecodeArgs {
   float *partials;
   uint32_t *counters;
   uint32_t K, rows, splits, out_stride;
+  // Column tile: 4 asks for 16-column workgroups (each wave four K slices; the same bits as 64-column ones), which
+  // spread a projection of few tiles over more compute units; 0 or 1 for 64-column workgroups.
+  uint32_t column_slices;
 };
 // A decode dispatch's layout: nb waves per workgroup, each a K slice of ks groups of 32 inputs (8, 16 or 32) of the
 // split. {0, 0} when the split is not one the tile runs (a K partition takes whole meta units, and the split's

@@ -231,6 +231,82 @@ def test_padding_columns_untouched():
     check_decode(got[:, :n], x, w, "padded")
 
 
+def widened(w, extra):
+    """w's planes followed by `extra` zero columns (whole tiles): the planes are tile-major, so the first w.n columns
+    of the wider tensor are w's bytes. Returns the segment and the device buffers it points at."""
+    t = torch()
+    groups, p1 = w.k // 32, sq.FORMATS[w.fmt][5]
+    p0_bytes, meta_bytes = sq.plane_bytes(w.fmt, extra, w.k)
+    zeros = lambda b: t.zeros(b, dtype=t.uint8, device="cuda")
+    plane0 = t.cat([w.plane0, zeros(p0_bytes)])
+    meta = t.cat([w.meta, zeros(meta_bytes)])
+    plane1 = t.cat([w.plane1, zeros(extra * groups * p1)]) if p1 else None
+    keep = (plane0, meta, plane1)
+    return sq.segment(w.fmt, w.n + extra, w.k, plane0, meta, 0, plane1), keep
+
+
+# The column tile runs 16-column workgroups (each wave four K slices) while four for each of a dispatch's 64-column
+# tiles times its splits fit one a compute unit (256 for the default device), 64-column ones past that: zero columns
+# past a projection's own widen its dispatch to 64-column workgroups.
+NARROW = [(oracle.FMT_AF4G64, 1, 1, 2048), (oracle.FMT_AF4G64, 4, 2, 4096), (oracle.FMT_AF4G64, 1, 1, 14336),
+          (oracle.FMT_Q4K, 1, 4, 4096), (oracle.FMT_Q4K, 3, 1, 2048), (oracle.FMT_Q4K, 1, 1, 8192),
+          (oracle.FMT_Q5K, 2, 1, 2048), (oracle.FMT_Q6K, 1, 2, 4096), (oracle.FMT_Q6K, 4, 1, 2048),
+          (oracle.FMT_Q80, 1, 1, 4096), (oracle.FMT_AF8G64, 4, 4, 4096), (oracle.FMT_AF4G32, 2, 1, 2048),
+          (oracle.FMT_AF4G128, 1, 2, 8192)]
+
+
+@pytest.mark.parametrize("fmt,rows,splits,k", NARROW)
+def test_column_slices_equal_whole_tile_workgroups(fmt, rows, splits, k):
+    """A projection of few tiles runs 16-column workgroups; the same weights widened past the compute units run one
+    64-column workgroup per tile (and split). Both compute the same bits for the shared columns, and those are
+    inside the oracle's interval with the register tile's bound (K 14336: 14 slices of 32 groups, two quarters of
+    the last wave idle)."""
+    rng = np.random.default_rng(41 + fmt + 10 * rows + 100 * splits + k)
+    n = 128
+    w = make_weights(rng, fmt, n, k)
+    x = dense_inputs(rng, rows, k)
+    narrow = run_plan(staged(n, k, rows, splits), sq.projection(w.segment()), x, n)
+    seg, keep = widened(w, 64 * (256 // splits))
+    total = seg.output_size
+    wide = run_plan(staged(total, k, rows, splits), sq.projection(seg), x, total)
+    assert np.array_equal(wide[:, :n], narrow)
+    assert np.all(wide[:, n:] == 0)
+    check_decode(narrow, x, w, f"16-column workgroups fmt {fmt} rows {rows} splits {splits} k {k}")
+
+
+@pytest.mark.parametrize("fmt,rows,splits", [(oracle.FMT_AF4G64, 1, 1), (oracle.FMT_Q4K, 4, 2),
+                                             (oracle.FMT_Q80, 1, 1), (oracle.FMT_AF8G64, 2, 4)])
+def test_column_slices_gate_up_pairs(fmt, rows, splits):
+    """One-pass gate/up pairs: 16-column workgroups (few tiles) and 64-column ones (widened) give the same bits."""
+    rng = np.random.default_rng(43 + fmt + rows + splits)
+    n, k = 128, 2048
+    wg, wu = make_weights(rng, fmt, n, k), make_weights(rng, fmt, n, k)
+    x = dense_inputs(rng, rows, k)
+    narrow = run_plan(staged(n, k, rows, splits, sq.EPILOGUE_GATE_UP, one_pass=1), sq.projection(wu.segment()), x,
+                      n, gate=sq.projection(wg.segment()))
+    (g, keep_g), (u, keep_u) = widened(wg, 64 * (256 // splits)), widened(wu, 64 * (256 // splits))
+    total = g.output_size
+    wide = run_plan(staged(total, k, rows, splits, sq.EPILOGUE_GATE_UP, one_pass=1), sq.projection(u), x, total,
+                    gate=sq.projection(g))
+    assert np.array_equal(wide[:, :n], narrow)
+
+
+@pytest.mark.parametrize("rows", [1, 4])
+def test_column_slices_mixed_formats(rows):
+    """Mixed-format segments in one dispatch: 16-column workgroups alone, 64-column ones with a wide third segment."""
+    rng = np.random.default_rng(47 + rows)
+    k = 2048
+    a, b = make_weights(rng, oracle.FMT_Q4K, 128, k), make_weights(rng, oracle.FMT_Q6K, 64, k)
+    c = make_weights(rng, oracle.FMT_AF4G64, 64, k)
+    x = dense_inputs(rng, rows, k)
+    narrow = run_plan(staged(256, k, rows, 1), sq.projection([a.segment(), b.segment(128), c.segment(192)]), x, 256)
+    wide_c, keep = widened(c, 64 * 256)
+    total = 192 + wide_c.output_size
+    wide_c.column_offset = 192
+    wide = run_plan(staged(total, k, rows, 1), sq.projection([a.segment(), b.segment(128), wide_c]), x, total)
+    assert np.array_equal(wide[:, :256], narrow)
+
+
 _SHAPE_CACHE = {}
 
 
