@@ -118,8 +118,9 @@ typedef struct sq_linear_buffers {
   sq_prepared_input prepared;
 } sq_linear_buffers;
 
-/* DeviceCapabilities, as far as the MI355X policy reads it (the decode split law); compute_units 0 takes 256. The
- * prefill tile's schedule is a function of the shape alone, for the MI355X's 256 compute units. */
+/* DeviceCapabilities, as far as the MI355X policy reads it (the decode split law, and the column tile's 16-column
+ * workgroups for dispatches of few tiles, which compute the same bits as 64-column ones); compute_units 0 takes 256.
+ * The prefill tile's schedule is a function of the shape alone, for the MI355X's 256 compute units. */
 typedef struct sq_device {
   uint32_t compute_units;
 } sq_device;
