@@ -217,6 +217,10 @@ uint64_t LinearPlan::gateScratchBytes() const noexcept {
 // shape and the tile kind, never on the rows themselves, so a row's result is the same in any batch of its kind.
 namespace {
 constexpr double kColumnBytes = 160e3, kRowBytes = 80e3;
+// The row tile's 16-column workgroups (one MFMA column block a wave: a quarter of the MFMAs and operands, the same
+// activation loads and input sums) pay while four a tile times the splits fit one a compute unit: K 4096 x N 1024
+// at M = 8 / 16 8.6 / 9.5 -> 7.8 / 9.1 us; allowed two a unit, N 4096 went 8.8 / 9.7 -> 11.0 / 13.5 us.
+constexpr uint64_t kRowSliceUnits = 1;
 }  // namespace
 
 uint32_t Linear::decodeSplits(uint32_t n, uint32_t k, uint32_t rows, uint32_t groupUnit, bool pair) const noexcept {
@@ -384,12 +388,13 @@ PreparedInput Linear::add(hipStream_t graph, LinearBuffers b, const Projection &
     }
     return {b.input, LinearInput::HalfRows};
   }
-  // The column tile's 64-column workgroups (a tile's K slices in one workgroup) leave most compute units idle when
+  // The decode tiles' 64-column workgroups (a tile's K slices in one workgroup) leave most compute units idle when
   // a dispatch has few tiles times splits; while four times as many still fit one a compute unit it takes 16-column
-  // workgroups, four for each, which compute the same bits (measured on MI355X, K 4096: N 4096 at M = 1 5.8 ->
-  // 4.5 us, N 1024 5.5 -> 3.9 us; N 14336, 224 tiles, was slower: 7.8 -> 9.1 us).
+  // workgroups, four for each, which compute the same bits (measured on MI355X, column tile, K 4096: N 4096 at M = 1
+  // 5.8 -> 4.5 us, N 1024 5.5 -> 3.9 us; N 14336, 224 tiles, was slower: 7.8 -> 9.1 us).
   const auto columnSlices = [&](uint32_t tiles) -> uint32_t {
-    return w.rows <= kern::kColumnTileRows && uint64_t{tiles} * config.splits * 4 <= computeUnits_ ? 4 : 1;
+    const uint64_t units = w.rows <= kern::kColumnTileRows ? computeUnits_ : kRowSliceUnits * computeUnits_;
+    return uint64_t{tiles} * config.splits * 4 <= units ? 4 : 1;
   };
   const auto decode = [&](const std::vector<const QuantizedSegment *> &group, uint32_t epilogue, Buffer output,
                           Buffer aux, bool f32) {

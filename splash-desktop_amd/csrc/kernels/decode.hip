@@ -21,18 +21,20 @@ namespace {
 constexpr uint32_t row_max_waves(int mb, int nt) { return mb == 1 && nt == 1 ? 16 : mb == 2 && nt == 2 ? 4 : 8; }
 
 // Wave `slice`'s K slice (groups gb.. of which `live` are in the slice) of plane tile `tile` of segment `seg`, in
-// format FMT, into acc.
-template <uint32_t FMT, int MB, int GW, int NT>
-__device__ __forceinline__ void row_walk(const DecodeArgs &a, const Segment &seg, uint32_t tile, uint32_t gb,
-                                         uint32_t live, float (&acc)[NT][4][MB][4]) {
+// format FMT, into acc. TB 1: column block cs of the tile only, lane (j, q) loading chunk q of column 16 cs + j and
+// that column's meta itself.
+template <uint32_t FMT, int MB, int GW, int NT, int TB>
+__device__ __forceinline__ void row_walk(const DecodeArgs &a, const Segment &seg, uint32_t tile, uint32_t cs,
+                                         uint32_t gb, uint32_t live, float (&acc)[NT][TB][MB][4]) {
   using F = Fmt<FMT>;
   const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
-  const uint32_t G = a.K >> 5, units = G / F::UNIT;
+  const uint32_t G = a.K >> 5, units = G / F::UNIT, col = TB == 1 ? 16 * cs + j : lane;
   const uint8_t *plane[NT], *high[NT], *meta[NT];
   {
-    const size_t pbase = ((size_t)tile * G * 64 + lane) * F::P0 + (size_t)gb * 64 * F::P0;
-    const size_t hbase = ((size_t)tile * G * 64 + lane) * F::P1 + (size_t)gb * 64 * F::P1;
-    const size_t mbase = ((size_t)tile * units * 64 + lane) * F::META + (size_t)(gb / F::UNIT) * 64 * F::META;
+    const size_t chunk = TB == 1 ? (size_t)q * (F::P0 / 4) : 0, word = TB == 1 && F::P1 == 8 ? 4 * (q >> 1) : 0;
+    const size_t pbase = ((size_t)tile * G * 64 + col) * F::P0 + chunk + (size_t)gb * 64 * F::P0;
+    const size_t hbase = ((size_t)tile * G * 64 + col) * F::P1 + word + (size_t)gb * 64 * F::P1;
+    const size_t mbase = ((size_t)tile * units * 64 + col) * F::META + (size_t)(gb / F::UNIT) * 64 * F::META;
     const Segment &first = NT == 2 ? a.gate : seg;
     plane[0] = first.plane0 + pbase;
     high[0] = F::P1 ? first.plane1 + hbase : nullptr;
@@ -51,46 +53,48 @@ __device__ __forceinline__ void row_walk(const DecodeArgs &a, const Segment &seg
     const uint32_t r = 16u * b + j;
     xrow[b] = a.input + (size_t)(r < a.rows ? r : 0) * a.K + 4 * q + (size_t)gb * 32;
   }
-  row_slice<FMT, MB, GW, NT>(plane, high, meta, xrow, live, acc);
+  row_slice<FMT, MB, GW, NT, TB>(plane, high, meta, xrow, live, acc);
 }
 
-// FMT kSegmentFormats: each workgroup runs its segment's format.
-template <uint32_t FMT, int MB, int GW, int NT, uint32_t EP, bool F32OUT>
+// FMT kSegmentFormats: each workgroup runs its segment's format. TB 1: workgroup x takes column block x % 4 of tile
+// x / 4 (16-column workgroups, each wave the same K slice as in the 64-column layout; the same bits).
+template <uint32_t FMT, int MB, int GW, int NT, uint32_t EP, bool F32OUT, int TB>
 __global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeArgs a) {
-  constexpr int A = NT * 4 * MB * 4;   // accumulators per lane: tensor n, column block t, row block b, row i
+  constexpr int A = NT * TB * MB * 4;   // accumulators per lane: tensor n, column block t, row block b, row i
   const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
   const uint32_t slice = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), waves = blockDim.x >> 6;
-  const uint32_t split = blockIdx.y;
-  uint32_t tile = blockIdx.x, s = 0;
+  const uint32_t split = blockIdx.y, cs = TB == 1 ? blockIdx.x & 3 : 0;
+  uint32_t tile = TB == 1 ? blockIdx.x >> 2 : blockIdx.x, s = 0;
   while (s + 1 < a.segments && tile >= a.seg[s].tiles) tile -= a.seg[s++].tiles;
   const Segment seg = a.seg[s];
   const uint32_t G = a.K >> 5, gs = G / a.splits;
   const uint32_t gb = split * gs + slice * GW, live = min((uint32_t)GW, gs - min(gs, slice * GW));
 
-  float acc[NT][4][MB][4];
+  float acc[NT][TB][MB][4];
   clear(acc);
   if constexpr (FMT == kSegmentFormats)
-    with_format(seg.fmt, [&](auto f) { row_walk<decltype(f)::value, MB, GW, NT>(a, seg, tile, gb, live, acc); });
+    with_format(seg.fmt, [&](auto f) { row_walk<decltype(f)::value, MB, GW, NT, TB>(a, seg, tile, cs, gb, live, acc); });
   else
-    row_walk<FMT, MB, GW, NT>(a, seg, tile, gb, live, acc);
+    row_walk<FMT, MB, GW, NT, TB>(a, seg, tile, cs, gb, live, acc);
 
   // The slices meet in LDS: red[slice][n FO + f][lane], f = (t MB + b) 4 + i the accumulator of column block t, row
   // block b, row 4q + i of the block. Output f (of both tensors) belongs to wave f % waves, which adds it over the
   // slices in slice order and stores it; a wave decodes and indexes only the outputs it owns. A K partition across
   // workgroups stores the sums as fp32 partials, and the last workgroup to arrive adds every split's in split order
   // and returns the counter to zero (split_reduce.h:14-45).
-  constexpr uint32_t FO = 4 * MB * 4;   // outputs per tensor
+  constexpr uint32_t FO = TB * MB * 4;   // outputs per tensor
   __shared__ float red[row_max_waves(MB, NT) * A * 64];
 #pragma unroll
   for (int n = 0; n < NT; ++n)
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < TB; ++t)
 #pragma unroll
       for (int b = 0; b < MB; ++b)
 #pragma unroll
         for (int i = 0; i < 4; ++i) red[(slice * A + n * FO + (t * MB + b) * 4 + i) * 64 + lane] = acc[n][t][b][i];
   __syncthreads();
-  const uint32_t cstride = NT == 2 ? 2 * a.out_stride : a.out_stride, column0 = seg.out_offset + tile * 64 + j;
+  const uint32_t cstride = NT == 2 ? 2 * a.out_stride : a.out_stride;
+  const uint32_t column0 = seg.out_offset + tile * 64 + 16 * cs + j;
   const size_t split_elements = (size_t)a.rows * cstride;
   // Output f's row and column.
   const auto place = [&](uint32_t f, uint32_t &row, uint32_t &col) __attribute__((always_inline)) {
@@ -160,14 +164,23 @@ __global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeA
   if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// column_slices 4: 16-column workgroups, four a tile (the same bits as the 64-column ones).
+template <uint32_t FMT, int MB, int GW, int NT, uint32_t EP, bool F32OUT>
+void launch_gw(const DecodeArgs &a, uint32_t tiles, DecodeLayout layout, hipStream_t stream) {
+  const dim3 block(64 * layout.nb);
+  if (a.column_slices == 4)
+    hipLaunchKernelGGL((row_kernel<FMT, MB, GW, NT, EP, F32OUT, 1>), dim3(tiles * 4, a.splits), block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((row_kernel<FMT, MB, GW, NT, EP, F32OUT, 4>), dim3(tiles, a.splits), block, 0, stream, a);
+}
+
 template <uint32_t FMT, int MB, int NT, uint32_t EP, bool F32OUT>
 hipError_t launch_mb(const DecodeArgs &a, uint32_t tiles, DecodeLayout layout, hipStream_t stream) {
-  const dim3 grid(tiles, a.splits), block(64 * layout.nb);
   switch (layout.ks) {
-    case 8: hipLaunchKernelGGL((row_kernel<FMT, MB, 8, NT, EP, F32OUT>), grid, block, 0, stream, a); break;
-    case 16: hipLaunchKernelGGL((row_kernel<FMT, MB, 16, NT, EP, F32OUT>), grid, block, 0, stream, a); break;
+    case 8: launch_gw<FMT, MB, 8, NT, EP, F32OUT>(a, tiles, layout, stream); break;
+    case 16: launch_gw<FMT, MB, 16, NT, EP, F32OUT>(a, tiles, layout, stream); break;
     default:
-      if constexpr (NT == 1) hipLaunchKernelGGL((row_kernel<FMT, MB, 32, NT, EP, F32OUT>), grid, block, 0, stream, a);
+      if constexpr (NT == 1) launch_gw<FMT, MB, 32, NT, EP, F32OUT>(a, tiles, layout, stream);
       break;
   }
   return hipGetLastError();

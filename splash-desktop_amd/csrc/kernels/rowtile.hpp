@@ -51,6 +51,26 @@ __device__ __forceinline__ RowGroup<FMT> load_row_group(const uint8_t *plane, co
   return r;
 }
 
+// One column block (16-column workgroups): lane (j, q) loads chunk q of its own column's group directly, the words
+// the transpose would bring it: plane word q (8-bit codes: words 2q, 2q + 1, into lo[0..1]), and the plane1 word
+// that holds chunk q's bits (Q5_K the column's word, Q6_K its word q / 2) into high[0]. plane points at chunk q of
+// group 0 of the column (plane + P0 column + (P0 / 4) q), high at the word (high + P1 column (+ 4 (q / 2) for Q6_K)).
+template <uint32_t FMT>
+__device__ __forceinline__ RowGroup<FMT> load_row_chunk(const uint8_t *plane, const uint8_t *high, uint32_t g) {
+  using F = Fmt<FMT>;
+  RowGroup<FMT> r;
+  const uint8_t *p = plane + (size_t)g * 64 * F::P0;
+  if constexpr (F::P0 == 32) {
+    const u32x2 w = __builtin_nontemporal_load((const u32x2 *)p);
+    r.lo[0] = w[0];
+    r.lo[1] = w[1];
+  } else {
+    r.lo[0] = __builtin_nontemporal_load((const uint32_t *)p);
+  }
+  if constexpr (F::P1) r.high[0] = __builtin_nontemporal_load((const uint32_t *)(high + (size_t)g * 64 * F::P1));
+  return r;
+}
+
 // The lane's shift of its chunk's plane1 bits after the transpose (lane (j, q) holds chunk q): Q5_K byte q, Q6_K
 // halfword q % 2 of the word the transpose brings.
 template <uint32_t FMT>
@@ -92,13 +112,23 @@ __device__ __forceinline__ void row_operands(const RowGroup<FMT> &grp, uint32_t 
   }
 }
 
+// The exact operands of one column block from load_row_chunk's words: what row_operands leaves in lo[t], hi[t] for
+// the block's column.
+template <uint32_t FMT>
+__device__ __forceinline__ void row_operands_one(const RowGroup<FMT> &grp, uint32_t hshift, CodeConstants cc,
+                                                 u32x4 (&lo)[1], u32x4 (&hi)[1]) {
+  using F = Fmt<FMT>;
+  if constexpr (F::P0 == 32) chunk_operands<FMT, true>(grp.lo[0], grp.lo[1], 0u, cc, lo[0], hi[0]);
+  else chunk_operands<FMT>(grp.lo[0], 0u, F::P1 ? grp.high[0] >> hshift : 0u, cc, lo[0], hi[0]);
+}
+
 // One group's MFMAs. C[n][t][b] takes sum x (operand) over the group (Q6_K: over its first half, C2 the second) and
 // S[b] the rows' input sums the same way, from zero when `first`. Q6_K's halves (one scale per 16 elements) run on
 // the 16x16x16 MFMA: operand words 0..1 of every lane are a chunk's first-half elements, words 2..3 its second.
-template <uint32_t FMT, int MB, int NT>
-__device__ __forceinline__ void row_group_mfma(const u32x4 (&x)[MB], const u32x4 (&lo)[NT][4],
-                                               const u32x4 (&hi)[NT][4], bool first, f32x4 (&C)[NT][4][MB],
-                                               f32x4 (&C2)[NT][4][MB], f32x4 (&S)[MB], f32x4 (&S2)[MB]) {
+template <uint32_t FMT, int MB, int NT, int TB = 4>
+__device__ __forceinline__ void row_group_mfma(const u32x4 (&x)[MB], const u32x4 (&lo)[NT][TB],
+                                               const u32x4 (&hi)[NT][TB], bool first, f32x4 (&C)[NT][TB][MB],
+                                               f32x4 (&C2)[NT][TB][MB], f32x4 (&S)[MB], f32x4 (&S2)[MB]) {
   using F = Fmt<FMT>;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   if constexpr (F::HALVES) {
@@ -111,7 +141,7 @@ __device__ __forceinline__ void row_group_mfma(const u32x4 (&x)[MB], const u32x4
 #pragma unroll
     for (int n = 0; n < NT; ++n)
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < TB; ++t)
 #pragma unroll
         for (int b = 0; b < MB; ++b) {
           C[n][t][b] = mfma_bf16_k16(u32x2{x[b][0], x[b][1]}, u32x2{lo[n][t][0], lo[n][t][1]}, first ? zero : C[n][t][b]);
@@ -123,14 +153,14 @@ __device__ __forceinline__ void row_group_mfma(const u32x4 (&x)[MB], const u32x4
 #pragma unroll
     for (int n = 0; n < NT; ++n)
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < TB; ++t)
 #pragma unroll
         for (int b = 0; b < MB; ++b) C[n][t][b] = mfma_bf16(x[b], lo[n][t], first ? zero : C[n][t][b]);
     if constexpr (F::P0 == 32) {
 #pragma unroll
       for (int n = 0; n < NT; ++n)
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < TB; ++t)
 #pragma unroll
           for (int b = 0; b < MB; ++b) C[n][t][b] = mfma_bf16(x[b], hi[n][t], C[n][t][b]);
     }
@@ -148,8 +178,9 @@ __device__ __forceinline__ void row_group_mfma(const u32x4 (&x)[MB], const u32x4
 struct CloseCoef {
   float a, b;
 };
-template <uint32_t FMT, int NT>
-__device__ __forceinline__ void spread_coefs(const MetaWords (&own)[NT], uint32_t g, int j, CloseCoef (&k)[NT][4]) {
+// TB 1 (16-column workgroups): each lane's meta is its own block column's, so its coefficients are its own.
+template <uint32_t FMT, int NT, int TB = 4>
+__device__ __forceinline__ void spread_coefs(const MetaWords (&own)[NT], uint32_t g, int j, CloseCoef (&k)[NT][TB]) {
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     CloseCoef mine;
@@ -162,23 +193,27 @@ __device__ __forceinline__ void spread_coefs(const MetaWords (&own)[NT], uint32_
                                           : fmaf(-128.0f, c.s, c.z);
       mine = {c.s, zc};
     }
+    if constexpr (TB == 1) {
+      k[n][0] = mine;
+    } else {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int from = (16 * t + j) * 4;
-      k[n][t].a = __int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(mine.a)));
-      k[n][t].b = __int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(mine.b)));
+      for (int t = 0; t < TB; ++t) {
+        const int from = (16 * t + j) * 4;
+        k[n][t].a = __int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(mine.a)));
+        k[n][t].b = __int_as_float(__builtin_amdgcn_ds_bpermute(from, __float_as_int(mine.b)));
+      }
     }
   }
 }
 // The close from the handed coefficients: acc += s C + zc S, or Q6_K's s0 C + s1 C2 - 160 s0 S - 160 s1 S2.
-template <uint32_t FMT, int MB, int NT>
-__device__ __forceinline__ void row_group_close(const CloseCoef (&k)[NT][4], const f32x4 (&C)[NT][4][MB],
-                                                const f32x4 (&C2)[NT][4][MB], const f32x4 (&S)[MB],
-                                                const f32x4 (&S2)[MB], float (&acc)[NT][4][MB][4]) {
+template <uint32_t FMT, int MB, int NT, int TB = 4>
+__device__ __forceinline__ void row_group_close(const CloseCoef (&k)[NT][TB], const f32x4 (&C)[NT][TB][MB],
+                                                const f32x4 (&C2)[NT][TB][MB], const f32x4 (&S)[MB],
+                                                const f32x4 (&S2)[MB], float (&acc)[NT][TB][MB][4]) {
 #pragma unroll
   for (int n = 0; n < NT; ++n)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < TB; ++t) {
       const float s0 = k[n][t].a, s1 = k[n][t].b;
 #pragma unroll
       for (int b = 0; b < MB; ++b)
@@ -201,11 +236,13 @@ __device__ __forceinline__ void row_group_close(const CloseCoef (&k)[NT][4], con
 // block t, row block b, row 4q + i of the block). plane[n] and high[n] point at the slice's first group for the
 // lane's column (load_row_group), meta[n] at its first meta unit for the lane's own column l (+ META l: one load per
 // unit and tensor, whose coefficients spread_coefs hands to the lanes whose MFMA blocks hold the column); xrow[b] at
-// the lane's row 16 b + j, inputs 4q of the slice's first group.
-template <uint32_t FMT, int MB, int GW, int NT>
+// the lane's row 16 b + j, inputs 4q of the slice's first group. TB 1: one column block, the lane's column j of it,
+// its chunk q and meta loaded directly (load_row_chunk); the same operands, MFMAs and closes as that block's in the
+// four-block walk.
+template <uint32_t FMT, int MB, int GW, int NT, int TB = 4>
 __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], const uint8_t *const (&high)[NT],
                                           const uint8_t *const (&meta)[NT], const uint16_t *const (&xrow)[MB],
-                                          uint32_t live, float (&acc)[NT][4][MB][4]) {
+                                          uint32_t live, float (&acc)[NT][TB][MB][4]) {
   using F = Fmt<FMT>;
   // 8-bit codes (twice the bytes a group) keep fewer groups in flight, and so do the K-quants with plane1 bits in the
   // longest slices of one tensor's 16 rows (whose workgroups hold the most waves, 128 registers each), and Q6_K (two
@@ -234,31 +271,35 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
       for (int n = 0; n < NT; ++n) own[n][u / UNIT] = load_meta<FMT>(meta[n] + (size_t)v * 64 * F::META);
     }
 #pragma unroll
-    for (int n = 0; n < NT; ++n) codes[n][u] = load_row_group<FMT>(plane[n], high[n], g);
+    for (int n = 0; n < NT; ++n)
+      codes[n][u] = TB == 1 ? load_row_chunk<FMT>(plane[n], high[n], g) : load_row_group<FMT>(plane[n], high[n], g);
   };
 #pragma unroll
   for (int u = 0; u < P; ++u) issue(u);
 
-  f32x4 C[NT][4][MB], C2[NT][4][MB], S[MB], S2[MB];
+  f32x4 C[NT][TB][MB], C2[NT][TB][MB], S[MB], S2[MB];
   const int j = threadIdx.x & 15;
 #pragma unroll
   for (int u = 0; u < GW; ++u) {
     if (u + P < GW) issue(u + P);
     __builtin_amdgcn_sched_barrier(0);
     if ((uint32_t)u < live) {
-      u32x4 x[MB], lo[NT][4], hi[NT][4];
+      u32x4 x[MB], lo[NT][TB], hi[NT][TB];
 #pragma unroll
       for (int b = 0; b < MB; ++b) x[b] = xv[b][u];
 #pragma unroll
-      for (int n = 0; n < NT; ++n) row_operands<FMT>(codes[n][u], hshift, cc, lo[n], hi[n]);
-      row_group_mfma<FMT, MB, NT>(x, lo, hi, u % SG == 0, C, C2, S, S2);
+      for (int n = 0; n < NT; ++n) {
+        if constexpr (TB == 1) row_operands_one<FMT>(codes[n][u], hshift, cc, lo[n], hi[n]);
+        else row_operands<FMT>(codes[n][u], hshift, cc, lo[n], hi[n]);
+      }
+      row_group_mfma<FMT, MB, NT, TB>(x, lo, hi, u % SG == 0, C, C2, S, S2);
       if ((u + 1) % SG == 0) {
         MetaWords unit[NT];
 #pragma unroll
         for (int n = 0; n < NT; ++n) unit[n] = own[n][u / UNIT];
-        CloseCoef k[NT][4];
-        spread_coefs<FMT, NT>(unit, u, j, k);
-        row_group_close<FMT, MB, NT>(k, C, C2, S, S2, acc);
+        CloseCoef k[NT][TB];
+        spread_coefs<FMT, NT, TB>(unit, u, j, k);
+        row_group_close<FMT, MB, NT, TB>(k, C, C2, S, S2, acc);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -355,12 +396,12 @@ __device__ __forceinline__ void row_stream(const uint8_t *const (&plane)[NT], co
   }
 }
 
-template <int MB, int NT>
-__device__ __forceinline__ void clear(float (&acc)[NT][4][MB][4]) {
+template <int MB, int NT, int TB>
+__device__ __forceinline__ void clear(float (&acc)[NT][TB][MB][4]) {
 #pragma unroll
   for (int n = 0; n < NT; ++n)
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < TB; ++t)
 #pragma unroll
       for (int b = 0; b < MB; ++b)
 #pragma unroll

@@ -246,13 +246,19 @@ def widened(w, extra):
 
 
 # The column tile runs 16-column workgroups (each wave four K slices) while four for each of a dispatch's 64-column
-# tiles times its splits fit one a compute unit (256 for the default device), 64-column ones past that: zero columns
-# past a projection's own widen its dispatch to 64-column workgroups.
+# tiles times its splits fit one a compute unit (256 for the default device), the row tile (one MFMA column block a
+# wave) while they fit a few a compute unit, 64-column ones past that: zero columns past a projection's own (more
+# than 256 tiles times splits) widen its dispatch to 64-column workgroups.
 NARROW = [(oracle.FMT_AF4G64, 1, 1, 2048), (oracle.FMT_AF4G64, 4, 2, 4096), (oracle.FMT_AF4G64, 1, 1, 14336),
           (oracle.FMT_Q4K, 1, 4, 4096), (oracle.FMT_Q4K, 3, 1, 2048), (oracle.FMT_Q4K, 1, 1, 8192),
           (oracle.FMT_Q5K, 2, 1, 2048), (oracle.FMT_Q6K, 1, 2, 4096), (oracle.FMT_Q6K, 4, 1, 2048),
           (oracle.FMT_Q80, 1, 1, 4096), (oracle.FMT_AF8G64, 4, 4, 4096), (oracle.FMT_AF4G32, 2, 1, 2048),
-          (oracle.FMT_AF4G128, 1, 2, 8192)]
+          (oracle.FMT_AF4G128, 1, 2, 8192),
+          # the row tile (5..32 rows): one MFMA column block a workgroup
+          (oracle.FMT_AF4G64, 8, 1, 4096), (oracle.FMT_AF4G64, 16, 2, 4096), (oracle.FMT_AF4G64, 32, 1, 2048),
+          (oracle.FMT_Q4K, 12, 4, 4096), (oracle.FMT_Q5K, 24, 1, 2048), (oracle.FMT_Q6K, 8, 2, 2048),
+          (oracle.FMT_Q6K, 20, 1, 4096), (oracle.FMT_Q80, 16, 1, 2048), (oracle.FMT_AF8G64, 9, 2, 2048),
+          (oracle.FMT_AF4G32, 32, 4, 2048), (oracle.FMT_AF4G128, 16, 1, 8192)]
 
 
 @pytest.mark.parametrize("fmt,rows,splits,k", NARROW)
@@ -260,7 +266,7 @@ def test_column_slices_equal_whole_tile_workgroups(fmt, rows, splits, k):
     """A projection of few tiles runs 16-column workgroups; the same weights widened past the compute units run one
     64-column workgroup per tile (and split). Both compute the same bits for the shared columns, and those are
     inside the oracle's interval with the register tile's bound (K 14336: 14 slices of 32 groups, two quarters of
-    the last wave idle)."""
+    the last wave idle). Rows past 4 run the row tile's one-block workgroups."""
     rng = np.random.default_rng(41 + fmt + 10 * rows + 100 * splits + k)
     n = 128
     w = make_weights(rng, fmt, n, k)
@@ -275,7 +281,9 @@ def test_column_slices_equal_whole_tile_workgroups(fmt, rows, splits, k):
 
 
 @pytest.mark.parametrize("fmt,rows,splits", [(oracle.FMT_AF4G64, 1, 1), (oracle.FMT_Q4K, 4, 2),
-                                             (oracle.FMT_Q80, 1, 1), (oracle.FMT_AF8G64, 2, 4)])
+                                             (oracle.FMT_Q80, 1, 1), (oracle.FMT_AF8G64, 2, 4),
+                                             (oracle.FMT_AF4G64, 8, 1), (oracle.FMT_Q4K, 24, 2),
+                                             (oracle.FMT_Q6K, 16, 1), (oracle.FMT_AF8G64, 32, 1)])
 def test_column_slices_gate_up_pairs(fmt, rows, splits):
     """One-pass gate/up pairs: 16-column workgroups (few tiles) and 64-column ones (widened) give the same bits."""
     rng = np.random.default_rng(43 + fmt + rows + splits)
@@ -291,7 +299,7 @@ def test_column_slices_gate_up_pairs(fmt, rows, splits):
     assert np.array_equal(wide[:, :n], narrow)
 
 
-@pytest.mark.parametrize("rows", [1, 4])
+@pytest.mark.parametrize("rows", [1, 4, 8, 20])
 def test_column_slices_mixed_formats(rows):
     """Mixed-format segments in one dispatch: 16-column workgroups alone, 64-column ones with a wide third segment."""
     rng = np.random.default_rng(47 + rows)
