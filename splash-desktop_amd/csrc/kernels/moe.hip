@@ -113,10 +113,12 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
                                                     SqMoeTileCount *tile_count, uint32_t *grouped_routes,
                                                     uint32_t *route_rows, const uint32_t *verify_rows,
                                                     SqMoeGroupParams p, uint32_t shared) {
-  constexpr uint32_t kChunk = 512, kWords = kChunk / 32;
+  // The row bitmaps and their prefixes: an expert's kWords words at a stride of kStride, so that the threads that
+  // walk their experts' words together (thread e, word w) take different LDS banks.
+  constexpr uint32_t kChunk = 512, kWords = kChunk / 32, kStride = kWords + 1;
   __shared__ uint32_t counts[SQ_MOE_WIDE_EXPERT_SLOTS], offsets[SQ_MOE_WIDE_EXPERT_SLOTS],
       running[SQ_MOE_WIDE_EXPERT_SLOTS];
-  __shared__ uint32_t bits[SQ_MOE_WIDE_EXPERT_SLOTS * kWords], prefix[SQ_MOE_WIDE_EXPERT_SLOTS * kWords];
+  __shared__ uint32_t bits[SQ_MOE_WIDE_EXPERT_SLOTS * kStride], prefix[SQ_MOE_WIDE_EXPERT_SLOTS * kStride];
   __shared__ uint32_t total;
   const uint32_t tid = threadIdx.x, per_row = p.top_k + shared, tr = p.tile_rows;
   // Routed route k of row r: selected[r * per_row + k].
@@ -144,7 +146,7 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
   counts[tid] = 0;
   running[tid] = 0;
   if (one) {
-    for (uint32_t i = tid; i < p.experts * kWords; i += 512) bits[i] = 0;
+    for (uint32_t i = tid; i < p.experts * kStride; i += 512) bits[i] = 0;
     if (tid == 0) duplicated = 0;
   }
   __syncthreads();
@@ -160,7 +162,7 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
       const uint32_t local = i / p.top_k, bit = 1u << (local % 32);
       atomicAdd(&counts[held[k]], 1u);
       // A bit already set names another route of the same row to the same expert (see below).
-      if (atomicOr(&bits[held[k] * kWords + local / 32], bit) & bit) duplicated = 1;
+      if (atomicOr(&bits[held[k] * kStride + local / 32], bit) & bit) duplicated = 1;
     }
   } else {
     for (uint32_t i = tid; i < routes; i += 512)
@@ -193,7 +195,7 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
   for (uint32_t chunk = 0; chunk < p.rows; chunk += kChunk) {
     const uint32_t i0 = chunk * p.top_k, i1 = min(p.rows, chunk + kChunk) * p.top_k;
     if (!one) {
-      for (uint32_t i = tid; i < p.experts * kWords; i += 512) bits[i] = 0;
+      for (uint32_t i = tid; i < p.experts * kStride; i += 512) bits[i] = 0;
       if (tid == 0) duplicated = 0;
       __syncthreads();
     }
@@ -205,7 +207,7 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
       const uint32_t local = i / p.top_k - chunk, bit = 1u << (local % 32);
       // A bit already set names another route of the same row to the same expert: a row with fewer scores above
       // -inf than top_k routes (an all-NaN row selects expert 0 at every rank). Such a chunk is ranked serially.
-      if (atomicOr(&bits[expert_of(i) * kWords + local / 32], bit) & bit) duplicated = 1;
+      if (atomicOr(&bits[expert_of(i) * kStride + local / 32], bit) & bit) duplicated = 1;
     }
     __syncthreads();
     if (!duplicated) {
@@ -214,15 +216,15 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
       if (tid < p.experts) {
         uint32_t before = 0;
         for (uint32_t w = 0; w < kWords; ++w) {
-          prefix[tid * kWords + w] = before;
-          before += __popc(bits[tid * kWords + w]);
+          prefix[tid * kStride + w] = before;
+          before += __popc(bits[tid * kStride + w]);
         }
       }
       __syncthreads();
       const auto place = [&](uint32_t i, uint32_t e) __attribute__((always_inline)) {
         const uint32_t r = route_of(i), local = i / p.top_k - chunk;
-        uint32_t rank = running[e] + prefix[e * kWords + local / 32];
-        rank += __popc(bits[e * kWords + local / 32] & ((1u << (local % 32)) - 1u));
+        uint32_t rank = running[e] + prefix[e * kStride + local / 32];
+        rank += __popc(bits[e * kStride + local / 32] & ((1u << (local % 32)) - 1u));
         const uint32_t row = offsets[e] * tr + rank;
         grouped_routes[row] = r;
         route_rows[r] = row;
@@ -236,8 +238,11 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
           if (!dead(i)) place(i, expert_of(i));
       }
       __syncthreads();
-      if (tid < p.experts)
-        for (uint32_t w = 0; w < kWords; ++w) running[tid] += __popc(bits[tid * kWords + w]);
+      if (tid < p.experts) {
+        uint32_t ranked = running[tid];
+        for (uint32_t w = 0; w < kWords; ++w) ranked += __popc(bits[tid * kStride + w]);
+        running[tid] = ranked;
+      }
     } else if (tid < p.experts) {
       // Thread e takes its expert's routes of the chunk in route order.
       for (uint32_t i = i0; i < i1; ++i) {
@@ -449,16 +454,17 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *expert_out
   for (int e = 0; e < 4; ++e) v[2 * e] = bf16_to_f32(res[e] & 0xFFFFu), v[2 * e + 1] = bf16_to_f32(res[e] >> 16);
   const size_t route = (size_t)r * p.routes_per_row;
   // Eight slots at a time: their route rows (one scalar load each: the row is the workgroup's), then every live
-  // slot's 16 bytes in flight together, then the sums in slot order. A route row of ~0u (a dead verify row) adds
-  // nothing, not even a zero.
+  // slot's 16 bytes in flight together, then the sums in slot order; the slots past the last eight one at a time. A
+  // route row of ~0u (a dead verify row) adds nothing, not even a zero.
   constexpr uint32_t kBatch = 8;
-  for (uint32_t s0 = 0; s0 < p.routes_per_row; s0 += kBatch) {
+  uint32_t s0 = 0;
+  for (; s0 + kBatch <= p.routes_per_row; s0 += kBatch) {
     uint32_t grouped[kBatch];
     u32x4 x[kBatch];
     float w[kBatch];
 #pragma unroll
     for (uint32_t k = 0; k < kBatch; ++k) {
-      grouped[k] = s0 + k < p.routes_per_row ? route_rows[route + s0 + k] : ~0u;
+      grouped[k] = route_rows[route + s0 + k];
       w[k] = 0.0f;
       x[k] = u32x4{0u, 0u, 0u, 0u};
       if (grouped[k] != ~0u) {
@@ -474,6 +480,17 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *expert_out
         v[2 * e] = fmaf(w[k], bf16_to_f32(x[k][e] & 0xFFFFu), v[2 * e]);
         v[2 * e + 1] = fmaf(w[k], bf16_to_f32(x[k][e] >> 16), v[2 * e + 1]);
       }
+    }
+  }
+  for (; s0 < p.routes_per_row; ++s0) {
+    const uint32_t grouped = route_rows[route + s0];
+    if (grouped == ~0u) continue;
+    const float w = weights[route + s0];
+    const u32x4 x = *(const u32x4 *)(expert_output + (size_t)grouped * p.hidden_size + d);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = fmaf(w, bf16_to_f32(x[e] & 0xFFFFu), v[2 * e]);
+      v[2 * e + 1] = fmaf(w, bf16_to_f32(x[e] >> 16), v[2 * e + 1]);
     }
   }
   u32x4 out;
