@@ -255,6 +255,19 @@ def test_prefill_halved_k_epilogues():
     assert np.all(np.abs(got - want) <= ulp + 1e-30)
 
 
+def test_q4k_projection_benchmark_shape():
+    """The reference's gguf-projection-benchmark shape (Q4_K, K = 5120, N = 17408, M = 2048; 256-row tiles, the last
+    of three rounds over the compute units an eighth full): sampled rows against fp64, and a row's output bitwise
+    the same as in a 300-row prefill of the same weights (128-row tiles)."""
+    n, k, rows = 17408, 5120, 2048
+    w = shape_weights(oracle.FMT_Q4K, n, k, 4)
+    rng = np.random.default_rng(2048)
+    x = dense_inputs(rng, rows, k)
+    out = run_prefill([w], x)
+    check_sampled(out, x, w, "Q4_K projection benchmark rows 2048", rng)
+    assert np.array_equal(run_prefill([w], x[:300]), out[:300])
+
+
 def test_config3_q4k_prefill():
     """BASELINE config 3's prefill point: Q4_K, K = 5120, N = 27648, M = 512."""
     n, k, rows = 27648, 5120, 512
