@@ -208,6 +208,82 @@ __global__ __launch_bounds__(256) void float_rows_kernel(const uint16_t *input, 
   else ((uint16_t *)output)[at] = f32_to_bf16(v);
 }
 
+// The same projection for rows in the prefill's numbers, on the fp32 MFMA (16x16x4): a workgroup of kFloatSlices
+// waves computes 32 rows x 32 columns, wave s over K slice s (K / kFloatSlices inputs). Per 16 inputs lane (kq, r)
+// (l = 16 kq + r) loads inputs 4 kq..4 kq + 3 of row r of each row block and of column r of each column block, and
+// MFMA e (0..3) takes input 4 kq + e of them, into accumulator chain e: four chains of K / (16 kFloatSlices) MFMAs,
+// added ((0 + 1) + (2 + 3)), then the slices in a fixed pairwise tree through LDS. An output's longest path is at most
+// 4 K / (16 kFloatSlices) + 2 + log2 kFloatSlices + 1 roundings (an MFMA's four products summed in at most four),
+// K / 64 + 7 for sixteen slices: within the lane-chain kernel's K / 64 + 8.
+constexpr int kFloatSlices = 16;
+constexpr uint32_t kFloatMfmaRows = 64;   // fewer rows take the lane chains (a decode step's handful)
+template <bool F32W, bool F32OUT>
+__global__ __launch_bounds__(64 * kFloatSlices) void float_rows_mfma_kernel(const uint16_t *input, const void *weights,
+                                                                            void *output, uint32_t rows, uint32_t N,
+                                                                            uint32_t K, uint32_t out_stride,
+                                                                            uint32_t out_offset) {
+  const uint32_t lane = threadIdx.x & 63, slice = threadIdx.x >> 6, r = lane & 15, kq = lane >> 4;
+  const uint32_t r0 = 32 * blockIdx.y, n0 = 32 * blockIdx.x, span = K / kFloatSlices, k0 = slice * span + 4 * kq;
+  const uint16_t *xr[2];
+  const uint8_t *wr[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    xr[b] = input + (size_t)min(r0 + 16 * b + r, rows - 1) * K + k0;
+    wr[b] = (const uint8_t *)weights + ((size_t)min(n0 + 16 * b + r, N - 1) * K + k0) * (F32W ? 4 : 2);
+  }
+  const auto widen = [](u32x2 v) __attribute__((always_inline)) {
+    return f32x4{bf16_to_f32(v[0] & 0xFFFFu), bf16_to_f32(v[0] >> 16), bf16_to_f32(v[1] & 0xFFFFu),
+                 bf16_to_f32(v[1] >> 16)};
+  };
+  f32x4 acc[4][2][2];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) acc[e][a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (uint32_t k = 0; k < span; k += 16) {
+    f32x4 x[2], w[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      x[b] = widen(*(const u32x2 *)(xr[b] + k));
+      if constexpr (F32W) w[b] = *(const f32x4 *)(wr[b] + (size_t)k * 4);
+      else w[b] = widen(*(const u32x2 *)(wr[b] + (size_t)k * 2));
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          acc[e][a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[a][e], w[b][e], acc[e][a][b], 0, 0, 0);
+  }
+  // Lane (kq, c) holds rows 4 kq + i of each row block at column c of each column block.
+  __shared__ float red[kFloatSlices][2][2][4][64];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        red[slice][a][b][i][lane] = (acc[0][a][b][i] + acc[1][a][b][i]) + (acc[2][a][b][i] + acc[3][a][b][i]);
+  __syncthreads();
+  // Output o = ((a 2 + b) 4 + i) 64 + lane, 1024 of them: one a thread, the slices added pairwise in a fixed tree.
+  const uint32_t o = threadIdx.x, a = o >> 9, b = (o >> 8) & 1, i = (o >> 6) & 3, l = o & 63;
+  float v[kFloatSlices];
+#pragma unroll
+  for (int s = 0; s < kFloatSlices; ++s) v[s] = red[s][a][b][i][l];
+#pragma unroll
+  for (int w = 1; w < kFloatSlices; w <<= 1)
+#pragma unroll
+    for (int s = 0; s < kFloatSlices; s += 2 * w) v[s] += v[s + w];
+  const uint32_t row = r0 + 16 * a + 4 * (l >> 4) + i, col = n0 + 16 * b + (l & 15);
+  if (row >= rows || col >= N) return;
+  const size_t at = (size_t)row * out_stride + out_offset + col;
+  if constexpr (F32OUT) ((float *)output)[at] = v[0];
+  else ((uint16_t *)output)[at] = f32_to_bf16(v[0]);
+}
+
 }  // namespace
 
 hipError_t launch_rms_norm(const uint16_t *input, const void *weight, bool f32_weights, uint16_t *output,
@@ -226,10 +302,18 @@ hipError_t launch_float_rows(const uint16_t *input, const void *weights, bool f3
                              bool f32_output, uint32_t rows, uint32_t N, uint32_t K, uint32_t out_stride,
                              uint32_t out_offset, hipStream_t stream) {
   if (!rows || !N || K % 4) return hipErrorInvalidValue;
-  const dim3 grid((N + 15) / 16, (rows + 3) / 4), block(256);
-#define SQ_FLOAT(W, O) \
-  hipLaunchKernelGGL((float_rows_kernel<W, O>), grid, block, 0, stream, input, weights, output, rows, N, K, \
-                     out_stride, out_offset)
+  // Prefill-sized row counts take the MFMA kernel (whole 16-input steps in every slice), decode-sized ones the lane
+  // chains.
+  const bool mfma = rows >= kFloatMfmaRows && K % (16 * kFloatSlices) == 0;
+  const dim3 grid = mfma ? dim3((N + 31) / 32, (rows + 31) / 32) : dim3((N + 15) / 16, (rows + 3) / 4);
+  const dim3 block = mfma ? dim3(64 * kFloatSlices) : dim3(256);
+#define SQ_FLOAT(W, O)                                                                                                \
+  if (mfma)                                                                                                          \
+    hipLaunchKernelGGL((float_rows_mfma_kernel<W, O>), grid, block, 0, stream, input, weights, output, rows, N, K,   \
+                       out_stride, out_offset);                                                                      \
+  else                                                                                                               \
+    hipLaunchKernelGGL((float_rows_kernel<W, O>), grid, block, 0, stream, input, weights, output, rows, N, K,         \
+                       out_stride, out_offset)
   if (f32_weights) {
     if (f32_output) SQ_FLOAT(true, true);
     else SQ_FLOAT(true, false);

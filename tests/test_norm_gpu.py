@@ -107,11 +107,15 @@ def test_prefill_takes_the_norm_table():
     assert after.layout == sq.LINEAR_INPUT_HALF_ROWS and after.source.ptr == normalized2.data_ptr()
 
 
-@pytest.mark.parametrize("f32_rows,f32_out", [(True, True), (False, True), (True, False)])
-def test_float_rows(f32_rows, f32_out):
+@pytest.mark.parametrize("f32_rows,f32_out,rows,n", [(True, True, 37, 128), (False, True, 37, 128),
+                                                      (True, False, 37, 128), (True, True, 300, 128),
+                                                      (False, True, 2048, 128), (True, False, 97, 60)])
+def test_float_rows(f32_rows, f32_out, rows, n):
+    """37 rows run the lane chains, 64 and more the fp32 MFMA (32 x 32 tiles, ragged in rows and columns at 97 x 60);
+    both within the lane chains' rounding bound."""
     t = torch()
-    rng = np.random.default_rng(51 + 2 * f32_rows + f32_out)
-    rows, n, k, stride, offset = 37, 128, 2048, 136, 5
+    rng = np.random.default_rng(51 + 2 * f32_rows + f32_out + rows)
+    k, stride, offset = 2048, 136, 5
     x = synthetic.activations(rng, rows, k)
     values = rng.normal(0, 0.02, (n, k)).astype(np.float32)
     if f32_rows:
@@ -130,8 +134,9 @@ def test_float_rows(f32_rows, f32_out):
     host = out.cpu().numpy()
     got = host[:, offset:offset + n].astype(np.float64) if f32_out else \
         synthetic.bf16_to_f32(host.view(np.uint16)[:, offset:offset + n]).astype(np.float64)
-    # Each lane sums k / 64 products in a chain, then a 6-level butterfly: (k / 64 + 8) roundings of sum |x w| at
-    # most, plus half a bf16 ulp of the result for a bf16 destination.
+    # Each lane sums k / 64 products in a chain, then a 6-level butterfly; the MFMA kernel's longest path is
+    # 4 k / 256 + 2 + 4 + 1: (k / 64 + 8) roundings of sum |x w| at most, plus half a bf16 ulp of the result for a
+    # bf16 destination.
     bound = (k / 64 + 8) * 2.0 ** -24 * magnitude
     if not f32_out:
         bound = bound + 0.5 * oracle.ulp_bf16(exact)
