@@ -132,10 +132,16 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
   };
   // When one chunk takes every row and a row has at most kHeld routes, each thread loads its routes' expert ids once
   // (route tid + 512 k, k < top_k), counts them and sets their row bits in one pass, and ranks them from registers:
-  // one read of the selection instead of three. Otherwise the passes below each read it again.
-  constexpr uint32_t kHeld = 8;
+  // one read of the selection instead of three. Up to kStaged routes otherwise go through LDS once (each route's
+  // expert id, ~0u for a dead one), which the passes below read instead of the selection.
+  constexpr uint32_t kHeld = 8, kStaged = 4 * kChunk * kHeld;
   const uint32_t routes = p.rows * p.top_k;
-  const bool one = p.rows <= kChunk && p.top_k <= kHeld;
+  const bool one = p.rows <= kChunk && p.top_k <= kHeld, staged = !one && routes <= kStaged;
+  __shared__ uint32_t stage[kStaged];
+  // Route i's expert, or ~0u for a dead route.
+  const auto live_expert = [&](uint32_t i) __attribute__((always_inline)) {
+    return staged ? stage[i] : dead(i) ? ~0u : expert_of(i);
+  };
   uint32_t held[kHeld];
 #pragma unroll
   for (uint32_t k = 0; k < kHeld; ++k) {
@@ -165,8 +171,11 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
       if (atomicOr(&bits[held[k] * kStride + local / 32], bit) & bit) duplicated = 1;
     }
   } else {
-    for (uint32_t i = tid; i < routes; i += 512)
-      if (!dead(i)) atomicAdd(&counts[expert_of(i)], 1u);
+    for (uint32_t i = tid; i < routes; i += 512) {
+      const uint32_t e = dead(i) ? ~0u : expert_of(i);
+      if (staged) stage[i] = e;
+      if (e != ~0u) atomicAdd(&counts[e], 1u);
+    }
   }
   __syncthreads();
   {
@@ -200,14 +209,15 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
       __syncthreads();
     }
     for (uint32_t i = i0 + tid; !one && i < i1; i += 512) {
-      if (dead(i)) {
+      const uint32_t e = live_expert(i);
+      if (e == ~0u) {
         route_rows[route_of(i)] = ~0u;
         continue;
       }
       const uint32_t local = i / p.top_k - chunk, bit = 1u << (local % 32);
       // A bit already set names another route of the same row to the same expert: a row with fewer scores above
       // -inf than top_k routes (an all-NaN row selects expert 0 at every rank). Such a chunk is ranked serially.
-      if (atomicOr(&bits[expert_of(i) * kStride + local / 32], bit) & bit) duplicated = 1;
+      if (atomicOr(&bits[e * kStride + local / 32], bit) & bit) duplicated = 1;
     }
     __syncthreads();
     if (!duplicated) {
@@ -234,8 +244,10 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
         for (uint32_t k = 0; k < kHeld; ++k)
           if (tid + 512 * k < routes && held[k] != ~0u) place(tid + 512 * k, held[k]);
       } else {
-        for (uint32_t i = i0 + tid; i < i1; i += 512)
-          if (!dead(i)) place(i, expert_of(i));
+        for (uint32_t i = i0 + tid; i < i1; i += 512) {
+          const uint32_t e = live_expert(i);
+          if (e != ~0u) place(i, e);
+        }
       }
       __syncthreads();
       if (tid < p.experts) {
@@ -246,7 +258,7 @@ __global__ __launch_bounds__(512) void group_kernel(const uint32_t *selected, Sq
     } else if (tid < p.experts) {
       // Thread e takes its expert's routes of the chunk in route order.
       for (uint32_t i = i0; i < i1; ++i) {
-        if (dead(i) || expert_of(i) != tid) continue;
+        if (live_expert(i) != tid) continue;
         const uint32_t r = route_of(i), row = offsets[tid] * tr + running[tid]++;
         grouped_routes[row] = r;
         route_rows[r] = row;
