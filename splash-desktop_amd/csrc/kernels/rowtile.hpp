@@ -125,10 +125,13 @@ __device__ __forceinline__ void row_operands_one(const RowGroup<FMT> &grp, uint3
 // One group's MFMAs. C[n][t][b] takes sum x (operand) over the group (Q6_K: over its first half, C2 the second) and
 // S[b] the rows' input sums the same way, from zero when `first`. Q6_K's halves (one scale per 16 elements) run on
 // the 16x16x16 MFMA: operand words 0..1 of every lane are a chunk's first-half elements, words 2..3 its second.
+// `ones` is ones_operand(): the decode slices keep it in registers, the MoE streams rebuild it (their registers are
+// spent).
 template <uint32_t FMT, int MB, int NT, int TB = 4>
 __device__ __forceinline__ void row_group_mfma(const u32x4 (&x)[MB], const u32x4 (&lo)[NT][TB],
                                                const u32x4 (&hi)[NT][TB], bool first, f32x4 (&C)[NT][TB][MB],
-                                               f32x4 (&C2)[NT][TB][MB], f32x4 (&S)[MB], f32x4 (&S2)[MB]) {
+                                               f32x4 (&C2)[NT][TB][MB], f32x4 (&S)[MB], f32x4 (&S2)[MB],
+                                               const u32x4 ones = ones_operand()) {
   using F = Fmt<FMT>;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   if constexpr (F::HALVES) {
@@ -149,7 +152,7 @@ __device__ __forceinline__ void row_group_mfma(const u32x4 (&x)[MB], const u32x4
         }
   } else {
 #pragma unroll
-    for (int b = 0; b < MB; ++b) S[b] = mfma_bf16(x[b], ones_operand(), first ? zero : S[b]);
+    for (int b = 0; b < MB; ++b) S[b] = mfma_bf16(x[b], ones, first ? zero : S[b]);
 #pragma unroll
     for (int n = 0; n < NT; ++n)
 #pragma unroll
@@ -279,6 +282,9 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
 
   f32x4 C[NT][TB][MB], C2[NT][TB][MB], S[MB], S2[MB];
   const int j = threadIdx.x & 15;
+  // The input sums' bf16 ones, built once and held (the compiler otherwise rebuilds them every group).
+  u32x4 ones = ones_operand();
+  asm volatile("" : "+v"(ones));
 #pragma unroll
   for (int u = 0; u < GW; ++u) {
     if (u + P < GW) issue(u + P);
@@ -292,7 +298,7 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
         if constexpr (TB == 1) row_operands_one<FMT>(codes[n][u], hshift, cc, lo[n], hi[n]);
         else row_operands<FMT>(codes[n][u], hshift, cc, lo[n], hi[n]);
       }
-      row_group_mfma<FMT, MB, NT, TB>(x, lo, hi, u % SG == 0, C, C2, S, S2);
+      row_group_mfma<FMT, MB, NT, TB>(x, lo, hi, u % SG == 0, C, C2, S, S2, ones);
       if ((u + 1) % SG == 0) {
         MetaWords unit[NT];
 #pragma unroll
