@@ -47,8 +47,23 @@ __global__ __launch_bounds__(64) void route_select_kernel(const float *scores, u
     float gate = 1.0f;
     if (shared_gate) {
       float dot = 0.0f;
-      for (uint32_t d = lane; d < p.input_size; d += 64)
-        dot = fmaf(bf16_to_f32(input[(size_t)row * p.input_size + d]), shared_gate[d], dot);
+      const uint16_t *xr = input + (size_t)row * p.input_size;
+      if (p.input_size % 512 == 0) {
+        // Eight inputs a lane a step (one 16-byte load of the row, two of the gate), four steps' loads in flight.
+#pragma unroll 4
+        for (uint32_t d = 8 * lane; d < p.input_size; d += 512) {
+          const u32x4 x = *(const u32x4 *)(xr + d);
+          const f32x4 g0 = *(const f32x4 *)(shared_gate + d), g1 = *(const f32x4 *)(shared_gate + d + 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float ge = e < 2 ? g0[2 * e] : g1[2 * e - 4], go = e < 2 ? g0[2 * e + 1] : g1[2 * e - 3];
+            dot = fmaf(bf16_to_f32(x[e] & 0xFFFFu), ge, dot);
+            dot = fmaf(bf16_to_f32(x[e] >> 16), go, dot);
+          }
+        }
+      } else {
+        for (uint32_t d = lane; d < p.input_size; d += 64) dot = fmaf(bf16_to_f32(xr[d]), shared_gate[d], dot);
+      }
 #pragma unroll
       for (int m = 32; m >= 1; m >>= 1) dot += __shfl_xor(dot, m);
       gate = sigmoid(dot);
