@@ -202,8 +202,16 @@ void MoE::addRouted(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w,
   a.K = s.hiddenSize;
   a.output_size = s.expertIntermediateSize;
   a.gather = 1;
+  // A launch of the shared slices alone with few tiles (every tile full: the rows of a block of a few thousand rows)
+  // runs each tile's rows as two 16-row halves, a workgroup each, so that it fills twice the SIMDs; each row
+  // computes what it does in the whole tile (35B layer, Q8_0 shared gate/up over 2048 rows: 512 -> 1024 waves).
+  const auto halves = [&](uint32_t mode, uint32_t outputSize) -> uint32_t {
+    const uint64_t tiles = uint64_t{s.sharedSlices} * ((plan.rows() + plan.tileRows() - 1) / plan.tileRows());
+    return mode == 1 && plan.tileRows() > 16 && tiles * (outputSize / 64) <= 2 * kern::kPrefillUnits ? 1 : 0;
+  };
   launches(gateUpFormats, [&](uint32_t mode, uint32_t gateFormat, uint32_t upFormat) {
     a.mode = mode;
+    a.row_halves = halves(mode, s.expertIntermediateSize);
     if (gateFormat == upFormat) {
       bind(0, w.gate, w.sharedGate);
       bind(1, w.up, w.sharedUp);
@@ -243,6 +251,7 @@ void MoE::addRouted(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w,
   };
   launches(downFormats, [&](uint32_t mode, uint32_t format, uint32_t) {
     a.mode = mode;
+    a.row_halves = halves(mode, s.hiddenSize);
     a.fmt = format;
     launched(kern::launch_moe_expert(a, graph), "MoE down pass");
   });

@@ -164,6 +164,7 @@ struct MoeExpertArgs {
   uint16_t *output;             // [tiles * tile_rows][output_size]
   const uint16_t *gate;         // a single tensor's up-with-gate operand (null otherwise)
   uint32_t K, output_size, tile_rows, max_tiles, fmt, gate_up, routes_per_row, experts, mode, gather;
+  uint32_t row_halves;          // 1: each tile's rows in 16-row halves, a workgroup each (tile_rows <= 32)
 };
 hipError_t launch_moe_expert(const MoeExpertArgs &args, hipStream_t stream);
 hipError_t launch_moe_combine(const uint16_t *expert_output, const uint32_t *route_rows,

@@ -326,12 +326,13 @@ constexpr bool short_chunks() {
 template <uint32_t FMT, int NT>
 constexpr int expert_waves() { return affine4_short<FMT>() ? (NT == 2 ? 2 : 3) : short_chunks<FMT, NT>() ? 2 : 1; }
 
+// Rows row0..row0 + rows - 1 of tile `tile` (all of them, or a 16-row half of it).
 template <uint32_t FMT, int MB, int NT>
 __device__ __forceinline__ void expert_tile(const MoeExpertArgs &a, SqMoeTileDescriptor d, uint32_t tile,
-                                            uint32_t ct) {
+                                            uint32_t ct, uint32_t row0, uint32_t rows) {
   using F = Fmt<FMT>;
   const uint32_t column_tiles = a.output_size / 64;
-  const uint32_t rows = d.rows, first_row = tile * a.tile_rows;
+  const uint32_t first_row = tile * a.tile_rows + row0;
   const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
   const uint32_t G = a.K >> 5;
   // The plane tile: routed expert e's from tile slots[e] of its projection on, shared slice s's from tile s of the
@@ -439,19 +440,26 @@ __device__ uint32_t longest_first_tile(const SqMoeTileDescriptor *tiles, uint32_
   return picked;
 }
 
-// Tiles of at most 16 rows (most of an expert's last tiles) take the one-block path.
+// Tiles of at most 16 rows (most of an expert's last tiles) take the one-block path. With row_halves the grid's x
+// holds two copies of the column groups, and copy h takes rows 16 h..16 h + 15 of each tile on the one-block path
+// (a launch of few tiles then fills twice the SIMDs; each row computes what it does in the whole tile).
 template <uint32_t FMT, int MB, int NT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(expert_waves<FMT, NT>())))
 void expert_kernel(MoeExpertArgs a) {
   const uint32_t n = a.tile_count->tiles;
   if (blockIdx.y >= n) return;
   const uint32_t tile = longest_first_tile(a.tiles, n, blockIdx.y);
-  const uint32_t ct = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (NT == 2 && !a.gate_up ? 2 : 1);
+  const uint32_t groups = a.row_halves ? gridDim.x / 2 : gridDim.x, half = blockIdx.x / groups;
+  const uint32_t ct = (blockIdx.x % groups * 4 + (threadIdx.x >> 6)) * (NT == 2 && !a.gate_up ? 2 : 1);
   if (ct >= a.output_size / 64) return;
   const SqMoeTileDescriptor d = a.tiles[tile];
   if (a.mode != 2 && (d.expert >= a.experts) != (a.mode == 1)) return;
-  if (MB == 1 || d.rows <= 16) expert_tile<FMT, 1, NT>(a, d, tile, ct);
-  else expert_tile<FMT, MB, NT>(a, d, tile, ct);
+  if (a.row_halves) {
+    if (16 * half < d.rows) expert_tile<FMT, 1, NT>(a, d, tile, ct, 16 * half, min(16u, d.rows - 16 * half));
+    return;
+  }
+  if (MB == 1 || d.rows <= 16) expert_tile<FMT, 1, NT>(a, d, tile, ct, 0, d.rows);
+  else expert_tile<FMT, MB, NT>(a, d, tile, ct, 0, d.rows);
 }
 
 // Thread: one 16-byte chunk of the table, chunk c of a group of 32 inputs: its 4-input units c and c + 4 (inputs
@@ -529,7 +537,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *expert_out
 template <uint32_t FMT, int MB, int NT>
 hipError_t launch_expert_rows(const MoeExpertArgs &a, hipStream_t stream) {
   const uint32_t per = NT == 2 && !a.gate_up ? 8 : 4;   // column tiles a workgroup
-  const dim3 grid((a.output_size / 64 + per - 1) / per, a.max_tiles), block(256);
+  const dim3 grid((a.output_size / 64 + per - 1) / per * (a.row_halves ? 2 : 1), a.max_tiles), block(256);
   hipLaunchKernelGGL((expert_kernel<FMT, MB, NT>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
@@ -540,7 +548,7 @@ hipError_t launch_expert_rows(const MoeExpertArgs &a, hipStream_t stream) {
 template <uint32_t FMT>
 hipError_t launch_expert_format(const MoeExpertArgs &a, hipStream_t stream) {
   const bool pairs = affine4_short<FMT>() && !a.gate_up && !a.gather && (a.output_size / 64) % 2 == 0;
-  if (a.tile_rows <= 16)
+  if (a.tile_rows <= 16 || a.row_halves)
     return a.gate_up || pairs ? launch_expert_rows<FMT, 1, 2>(a, stream) : launch_expert_rows<FMT, 1, 1>(a, stream);
   return a.gate_up || pairs ? launch_expert_rows<FMT, 2, 2>(a, stream) : launch_expert_rows<FMT, 2, 1>(a, stream);
 }

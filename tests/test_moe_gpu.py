@@ -251,6 +251,20 @@ def test_moe_35b_formats():
     check_block(block, x, scores, 8, None)
 
 
+def test_moe_rows_independent_of_the_block():
+    """A row's output is bitwise the same in any block: the 35B mix (its gated Q8_0 shared slice in launches of its
+    own, whose few tiles run as 16-row halves) over 70 rows and over their first 24 (other expert tiles, other
+    halves)."""
+    rng = np.random.default_rng(991)
+    block = Block(rng, 32, 512, 256, fmt=oracle.FMT_Q4K, shared=1, gated=True, shared_fmt=oracle.FMT_Q80,
+                  formats={"down": oracle.FMT_Q5K})
+    x = synthetic.activations(rng, 70, 512)
+    scores = synthetic.router_logits(rng, 70, 32)
+    _, _, whole = run_moe(block, x, scores, 8)
+    _, _, first = run_moe(block, x[:24], scores[:24], 8)
+    assert np.array_equal(whole[:24], first)
+
+
 def test_moe_k_quant_experts_with_q8_0_shared_slice():
     """The mix the 4-bit MoE checkpoints ship: Q5_K routed experts with a gated Q8_0 shared slice (its own launches)."""
     rng = np.random.default_rng(950)
