@@ -280,6 +280,38 @@ def test_column_slices_equal_whole_tile_workgroups(fmt, rows, splits, k):
     check_decode(narrow, x, w, f"16-column workgroups fmt {fmt} rows {rows} splits {splits} k {k}")
 
 
+def _random_narrow_cases(count=12, seed=4242):
+    """Seeded draws of (format, columns, K, rows, splits) that the decode tiles run: K a multiple of the format's
+    meta unit times the splits, every row count of both tile kinds."""
+    rng = np.random.default_rng(seed)
+    formats = [oracle.FMT_AF4G64, oracle.FMT_AF4G32, oracle.FMT_AF4G128, oracle.FMT_Q4K, oracle.FMT_Q5K,
+               oracle.FMT_Q6K, oracle.FMT_Q80, oracle.FMT_AF8G64]
+    cases = []
+    while len(cases) < count:
+        fmt = formats[rng.integers(len(formats))]
+        unit = sq.FORMATS[fmt][4] * 32
+        splits = int(rng.choice([1, 2, 4]))
+        k = int(unit * splits * rng.integers(1, 1 + 6144 // (unit * splits)))
+        n = int(64 * rng.integers(1, 9))
+        rows = int(rng.choice([1, 2, 3, 4, 5, 9, 16, 17, 31, 32]))
+        cases.append((fmt, n, k, rows, splits))
+    return cases
+
+
+@pytest.mark.parametrize("fmt,n,k,rows,splits", _random_narrow_cases())
+def test_column_slices_random_shapes(fmt, n, k, rows, splits):
+    """Random shapes (slices of 8, 16 or 32 groups, whole or with a short last one, idle quarters, one to four
+    splits): a projection's 16-column workgroups give the bits its widened dispatch's 64-column ones give."""
+    rng = np.random.default_rng(fmt + n + k + rows + splits)
+    w = make_weights(rng, fmt, n, k)
+    x = dense_inputs(rng, rows, k)
+    narrow = run_plan(staged(n, k, rows, splits), sq.projection(w.segment()), x, n)
+    seg, keep = widened(w, 64 * (256 // splits))
+    wide = run_plan(staged(seg.output_size, k, rows, splits), sq.projection(seg), x, seg.output_size)
+    assert np.array_equal(wide[:, :n], narrow)
+    check_decode(narrow, x, w, f"random shape fmt {fmt} {n}x{k} rows {rows} splits {splits}")
+
+
 @pytest.mark.parametrize("fmt,rows,splits", [(oracle.FMT_AF4G64, 1, 1), (oracle.FMT_Q4K, 4, 2),
                                              (oracle.FMT_Q80, 1, 1), (oracle.FMT_AF8G64, 2, 4),
                                              (oracle.FMT_AF4G64, 8, 1), (oracle.FMT_Q4K, 24, 2),
