@@ -24,6 +24,9 @@
 //  - One workgroup covers a tile's whole K unless the launcher's layout splits it: a split across workgroups adds
 //    three device-scope round trips at the end of the dispatch (split_reduce), which only pays when the tiles alone
 //    leave most compute units idle.
+//  - A dispatch of few tiles (column_slices 4) runs four 16-column workgroups a tile instead, each wave four of the
+//    layout's K slices in its 16-lane quarters (the MFMA's A broadcast to a quarter's four blocks, cbsz 2): each
+//    lane computes what the 64-column lane of its column computes for its slice, so the results are the same bits.
 // A row's result depends only on its own activations and the layout (split, GW), never on the other rows.
 #include "device.hpp"
 #include "kernels.hpp"
@@ -48,7 +51,8 @@ __device__ __forceinline__ float dpp_add(float v) {
 }
 
 // Wave `slice`'s K slice of plane tile `tile` of segment `seg` (K partition `split`), in format FMT, into acc; the
-// slice's input sums go through the wave's own xsum[slice] (NHS slots a group, at least the format's halves).
+// slice's input sums go through its own xsum[slice] (NHS slots a group, at least the format's halves; narrow: each
+// quarter's xsum[4 slice + q]).
 // NARROW: the wave takes columns 16 cs..16 cs + 15 of the tile and four K slices, 4 slice + q for its quarter q (lanes
 // 16q..16q + 15, lane 16q + c column 16 cs + c), every slice whole; each lane computes exactly what the wide walk's
 // lane of that column computes for that slice (the same activations, operands, MFMA blocks, input-sum tree and
