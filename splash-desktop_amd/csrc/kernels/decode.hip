@@ -7,8 +7,10 @@
 // with the row tile's inner loop (rowtile.hpp: exact bf16 operands on the 16x16x32 MFMA, rows on its 16-row side,
 // per-group closes in fp32); the slices meet in LDS in slice order, every wave adding and storing only the outputs
 // it owns, and K partitions across workgroups reduce as the column tile's do (the last workgroup to arrive adds the
-// splits in split order). A row's result depends only on its own activations and the layout, never on the other
-// rows.
+// splits in split order). A dispatch of few tiles (column_slices 4) runs four workgroups a tile instead, each wave
+// one MFMA column block of its slice (its lanes load their column's chunks and meta directly): the same operands,
+// MFMAs and closes, so the same bits. A row's result depends only on its own activations and the layout, never on
+// the other rows.
 #include "device.hpp"
 #include "kernels.hpp"
 #include "rowtile.hpp"
