@@ -27,7 +27,7 @@ constexpr uint32_t row_max_waves(int mb, int nt) { return mb == 1 && nt == 1 ? 1
 // that column's meta itself.
 template <uint32_t FMT, int MB, int GW, int NT, int TB>
 __device__ __forceinline__ void row_walk(const DecodeArgs &a, const Segment &seg, uint32_t tile, uint32_t cs,
-                                         uint32_t gb, uint32_t live, float (&acc)[NT][TB][MB][4]) {
+                                         uint32_t gb, uint32_t live, uint8_t *xlds, float (&acc)[NT][TB][MB][4]) {
   using F = Fmt<FMT>;
   const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
   const uint32_t G = a.K >> 5, units = G / F::UNIT, col = TB == 1 ? 16 * cs + j : lane;
@@ -47,15 +47,15 @@ __device__ __forceinline__ void row_walk(const DecodeArgs &a, const Segment &seg
       meta[1] = seg.meta + mbase;
     }
   }
-  // Lane (j, q) of row block b reads row 16 b + j's inputs 4q..4q+3 and 16+4q..19+4q of each group (the MFMA's A
-  // layout); rows past the live ones read row 0, whose results nothing stores.
+  // Lane (j, q) of row block b reads row 16 b + j's inputs 8q..8q+7 of each group (row_slice puts them into the
+  // MFMA's A layout through the wave's LDS slot); rows past the live ones read row 0, whose results nothing stores.
   const uint16_t *xrow[MB];
 #pragma unroll
   for (int b = 0; b < MB; ++b) {
     const uint32_t r = 16u * b + j;
-    xrow[b] = a.input + (size_t)(r < a.rows ? r : 0) * a.K + 4 * q + (size_t)gb * 32;
+    xrow[b] = a.input + (size_t)(r < a.rows ? r : 0) * a.K + 8 * q + (size_t)gb * 32;
   }
-  row_slice<FMT, MB, GW, NT, TB>(plane, high, meta, xrow, live, acc);
+  row_slice<FMT, MB, GW, NT, TB>(plane, high, meta, xrow, xlds, live, acc);
 }
 
 // FMT kSegmentFormats: each workgroup runs its segment's format. TB 1: workgroup x takes column block x % 4 of tile
@@ -74,18 +74,23 @@ __global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeA
 
   float acc[NT][TB][MB][4];
   clear(acc);
+  // The slices' reduction buffer; during the walk each wave's own part of it (A floats a lane, at least MB KiB) is
+  // its activations' LDS slot, which the wave leaves before writing its sums there.
+  constexpr uint32_t FO = TB * MB * 4;   // outputs per tensor
+  __shared__ float red[row_max_waves(MB, NT) * A * 64];
+  static_assert(A * 64 * 4 >= MB * 1024, "a wave's reduction slot holds its activations' slot");
+  uint8_t *const xlds = (uint8_t *)(red + slice * A * 64);
   if constexpr (FMT == kSegmentFormats)
-    with_format(seg.fmt, [&](auto f) { row_walk<decltype(f)::value, MB, GW, NT, TB>(a, seg, tile, cs, gb, live, acc); });
+    with_format(seg.fmt,
+                [&](auto f) { row_walk<decltype(f)::value, MB, GW, NT, TB>(a, seg, tile, cs, gb, live, xlds, acc); });
   else
-    row_walk<FMT, MB, GW, NT, TB>(a, seg, tile, cs, gb, live, acc);
+    row_walk<FMT, MB, GW, NT, TB>(a, seg, tile, cs, gb, live, xlds, acc);
 
   // The slices meet in LDS: red[slice][n FO + f][lane], f = (t MB + b) 4 + i the accumulator of column block t, row
   // block b, row 4q + i of the block. Output f (of both tensors) belongs to wave f % waves, which adds it over the
   // slices in slice order and stores it; a wave decodes and indexes only the outputs it owns. A K partition across
   // workgroups stores the sums as fp32 partials, and the last workgroup to arrive adds every split's in split order
   // and returns the counter to zero (split_reduce.h:14-45).
-  constexpr uint32_t FO = TB * MB * 4;   // outputs per tensor
-  __shared__ float red[row_max_waves(MB, NT) * A * 64];
 #pragma unroll
   for (int n = 0; n < NT; ++n)
 #pragma unroll

@@ -239,13 +239,15 @@ __device__ __forceinline__ void row_group_close(const CloseCoef (&k)[NT][TB], co
 // block t, row block b, row 4q + i of the block). plane[n] and high[n] point at the slice's first group for the
 // lane's column (load_row_group), meta[n] at its first meta unit for the lane's own column l (+ META l: one load per
 // unit and tensor, whose coefficients spread_coefs hands to the lanes whose MFMA blocks hold the column); xrow[b] at
-// the lane's row 16 b + j, inputs 4q of the slice's first group. TB 1: one column block, the lane's column j of it,
-// its chunk q and meta loaded directly (load_row_chunk); the same operands, MFMAs and closes as that block's in the
-// four-block walk.
+// the lane's row 16 b + j, inputs 8q of the slice's first group (one 16-byte load a row block and group: the
+// wave's LDS slot xlds, MB KiB, turns the lanes' contiguous chunks into the MFMA's A layout, inputs 4q..4q+3 and
+// 16+4q..19+4q of the row, with a write and two reads instead of a second global load). TB 1: one column block, the
+// lane's column j of it, its chunk q and meta loaded directly (load_row_chunk); the same operands, MFMAs and closes
+// as that block's in the four-block walk.
 template <uint32_t FMT, int MB, int GW, int NT, int TB = 4>
 __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], const uint8_t *const (&high)[NT],
                                           const uint8_t *const (&meta)[NT], const uint16_t *const (&xrow)[MB],
-                                          uint32_t live, float (&acc)[NT][TB][MB][4]) {
+                                          uint8_t *xlds, uint32_t live, float (&acc)[NT][TB][MB][4]) {
   using F = Fmt<FMT>;
   // 8-bit codes (twice the bytes a group) keep fewer groups in flight, and so do the K-quants with plane1 bits in the
   // longest slices of one tensor's 16 rows (whose workgroups hold the most waves, 128 registers each), and Q6_K (two
@@ -264,10 +266,7 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
   const auto issue = [&](int u) __attribute__((always_inline)) {
     const uint32_t g = min((uint32_t)u, last);
 #pragma unroll
-    for (int b = 0; b < MB; ++b) {
-      const u32x2 lo = *(const u32x2 *)(xrow[b] + (size_t)g * 32), hi = *(const u32x2 *)(xrow[b] + (size_t)g * 32 + 16);
-      xv[b][u] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-    }
+    for (int b = 0; b < MB; ++b) xv[b][u] = *(const u32x4 *)(xrow[b] + (size_t)g * 32);
     if (u % UNIT == 0) {
       const uint32_t v = min((uint32_t)(u / UNIT), last / UNIT);
 #pragma unroll
@@ -281,7 +280,9 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
   for (int u = 0; u < P; ++u) issue(u);
 
   f32x4 C[NT][TB][MB], C2[NT][TB][MB], S[MB], S2[MB];
-  const int j = threadIdx.x & 15;
+  const int j = threadIdx.x & 15, lane = threadIdx.x & 63, q = lane >> 4;
+  // Lane (j, q) reads inputs 4q..4q+3 (chunk q / 2 of its row, half q % 2) and 16+4q..19+4q (chunk 2 + q / 2).
+  const uint32_t from_lo = ((q >> 1) * 16 + j) * 16 + (q & 1) * 8, from_hi = ((2 + (q >> 1)) * 16 + j) * 16 + (q & 1) * 8;
   // The input sums' bf16 ones, built once and held (the compiler otherwise rebuilds them every group).
   u32x4 ones = ones_operand();
   asm volatile("" : "+v"(ones));
@@ -292,7 +293,19 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
     if ((uint32_t)u < live) {
       u32x4 x[MB], lo[NT][TB], hi[NT][TB];
 #pragma unroll
-      for (int b = 0; b < MB; ++b) x[b] = xv[b][u];
+      for (int b = 0; b < MB; ++b) *(u32x4 *)(xlds + b * 1024 + lane * 16) = xv[b][u];
+      // The wave reads back what its own lanes wrote, and writes the next group's only after reading this one's.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int b = 0; b < MB; ++b) {
+        const u32x2 l = *(const u32x2 *)(xlds + b * 1024 + from_lo), h = *(const u32x2 *)(xlds + b * 1024 + from_hi);
+        x[b] = u32x4{l[0], l[1], h[0], h[1]};
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
         if constexpr (TB == 1) row_operands_one<FMT>(codes[n][u], hshift, cc, lo[n], hi[n]);
