@@ -221,6 +221,11 @@ constexpr double kColumnBytes = 160e3, kRowBytes = 80e3;
 // activation loads and input sums) pay while four a tile times the splits fit one a compute unit: K 4096 x N 1024
 // at M = 8 / 16 8.6 / 9.5 -> 7.8 / 9.1 us; allowed two a unit, N 4096 went 8.8 / 9.7 -> 11.0 / 13.5 us.
 constexpr uint64_t kRowSliceUnits = 1;
+// A tile whose split (above) would leave the row tile in 64-column workgroups runs unsplit in 16-column ones while
+// four a tile fit one a compute unit and each streams at most kRowNarrowBytes: K 4096 x N 4096 (36.9 KB each) at
+// M = 8 / 16 8.4 / 8.8 -> 7.1 / 8.4 us (two splits before); K 14336 x N 4096 (129 KB each) lost, 12.6 -> 18.8 us
+// at M = 8, and so did a tile already in 16-column workgroups made unsplit (N 1024 at M = 16, 7.5 -> 7.9 us).
+constexpr double kRowNarrowBytes = 40e3;
 }  // namespace
 
 uint32_t Linear::decodeSplits(uint32_t n, uint32_t k, uint32_t rows, uint32_t groupUnit, bool pair) const noexcept {
@@ -240,6 +245,10 @@ uint32_t Linear::decodeSplits(uint32_t n, uint32_t k, uint32_t rows, uint32_t gr
     best = s;
     if (tileBytes / s <= budget) break;
   }
+  const uint64_t narrowUnits = kRowSliceUnits * computeUnits_;
+  if (!column && best > 1 && uint64_t{tiles} * best * 4 > narrowUnits && uint64_t{tiles} * 4 <= narrowUnits &&
+      tileBytes / 4 <= kRowNarrowBytes && kern::decode_layout(format, blocks, k, 1, pair, kind).nb)
+    return 1;
   return best ? best : 1;
 }
 

@@ -51,9 +51,11 @@ def test_decode_plans(n, k, rows):
     assert gate == 0
 
 
-def split_law(n, k, budget, max_waves=16, pair=False):
+def split_law(n, k, budget, max_waves=16, pair=False, row=False):
     """The fewest splits whose workgroups stream at most `budget` bytes, the grid kept within 256 compute units,
-    among splits whose K slices fit one workgroup (at most `max_waves` waves of at most 32 groups)."""
+    among splits whose K slices fit one workgroup (at most `max_waves` waves of at most 32 groups). The row tile
+    (`row`) runs a tile unsplit in four 16-column workgroups instead of split 64-column ones while the four fit the
+    compute units and each streams at most 40 KB."""
     tiles, groups = n // 64, k // 32
     tile_bytes = (2 if pair else 1) * 64 * (k * 0.5 + groups * 2.0)
     best = None
@@ -65,6 +67,8 @@ def split_law(n, k, budget, max_waves=16, pair=False):
         best = s
         if tile_bytes / s <= budget:
             break
+    if row and best > 1 and tiles * best * 4 > 256 and tiles * 4 <= 256 and tile_bytes / 4 <= 40e3:
+        return 1
     return best
 
 
@@ -77,11 +81,14 @@ def test_split_law_column_tile(n, k, want):
 
 
 @pytest.mark.parametrize("rows", [8, 16])
-@pytest.mark.parametrize("n,k,want", [(14336, 4096, 1), (1024, 4096, 2), (4096, 4096, 2), (4096, 14336, 4)])
+@pytest.mark.parametrize("n,k,want", [(14336, 4096, 1), (1024, 4096, 2), (2048, 4096, 2), (4096, 4096, 1),
+                                      (3072, 4096, 1), (4096, 8192, 4), (4096, 14336, 4)])
 def test_split_law_row_tile(rows, n, k, want):
-    """5..32 rows: workgroups of at most 80 KB."""
+    """5..32 rows: workgroups of at most 80 KB; unsplit 16-column workgroups where the split would leave a few tiles
+    in 64-column ones (4096 x 4096, 3072 x 4096), not where the split already fits 16-column ones (1024, 2048) or the
+    unsplit ones would stream more than 40 KB (K 8192, 14336)."""
     s = sq.plan_for(sq.decode_workload(n, k, rows), sq.projection(seg(n, k))).config.splits
-    assert s == want == split_law(n, k, 80e3)
+    assert s == want == split_law(n, k, 80e3, row=True)
 
 
 def test_prefill_plans():
