@@ -379,6 +379,26 @@ def test_config1_sweep_policy_plans(n, k, rows):
     assert stats["rel_l2"] <= ref_l2 * 1.10 + 1e-6
 
 
+@pytest.mark.parametrize("n", [3072, 4096])
+@pytest.mark.parametrize("rows", [5, 32])
+def test_row_tile_unsplit_plans(n, rows):
+    """K 4096 at 48 or 64 tiles: the split law leaves the row tile unsplit in 16-column workgroups (a split would
+    leave it in 64-column ones). Every output against fp64 with the register tile's bound, and the same bits as the
+    unsplit 64-column workgroups of the same weights widened past the compute units."""
+    k = 4096
+    w = shape_weights(oracle.FMT_AF4G64, n, k, 7 + n)
+    rng = np.random.default_rng(n + rows)
+    x = dense_inputs(rng, rows, k)
+    proj = sq.projection(w.segment())
+    plan = sq.plan_for(sq.decode_workload(n, k, rows), proj)
+    assert plan.config.splits == 1
+    got = run_plan(plan, proj, x, n)
+    check_decode(got, x, w, f"unsplit row tile {n}x{k} rows {rows}")
+    seg, keep = widened(w, 64 * 256)
+    wide = run_plan(staged(seg.output_size, k, rows, 1), sq.projection(seg), x, seg.output_size)
+    assert np.array_equal(wide[:, :n], got)
+
+
 @pytest.mark.parametrize("rows", [1, 16])
 def test_config3_q4k_decode(rows):
     """BASELINE config 3's decode points: Q4_K, K = 5120, N = 27648, M = 1 and 16 under the library's plan, every
