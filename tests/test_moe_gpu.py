@@ -165,8 +165,11 @@ def errors(got, want):
     return np.linalg.norm(err) / np.linalg.norm(want), err
 
 
-@pytest.mark.parametrize("rows,experts,top_k", [(64, 32, 4), (6, 32, 4), (300, 16, 2)])
+@pytest.mark.parametrize("rows,experts,top_k", [(64, 32, 4), (6, 32, 4), (300, 16, 2), (1100, 32, 8), (1200, 32, 16)])
 def test_moe_routed_experts(rows, experts, top_k):
+    """Routing, grouping, expert passes and combine against the oracle: one chunk of rows, and past it the grouping's
+    512-row chunks (1100 rows at top 8: three, the last ragged, its routes staged in LDS; 1200 rows at top 16: more
+    routes than the LDS stage holds, read from the selection each chunk)."""
     rng = np.random.default_rng(rows + experts)
     hidden, intermediate = 512, 256
     block = Block(rng, experts, hidden, intermediate)
