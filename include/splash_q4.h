@@ -151,6 +151,18 @@ int sq_linear_decode_scratch_size(const sq_device *device, uint32_t output_size,
                                   sq_linear_scratch_size *out);
 int sq_linear_prefill_scratch_size(const sq_device *device, uint32_t output_size, uint32_t input_size,
                                    sq_linear_scratch_size *out);
+/* Linear::decodeStorageRows (Linear.hpp:254-257; Linear.cpp:145-149): the rows of storage a decode step of `rows`
+ * rows (1..32) binds for a projection of output_size x input_size, the storage_rows of its decode plans, which every
+ * epilogue shares. The engine sizes its decode activation and output buffers with it (QwenTarget.cpp:125,
+ * DFlashDraft.cpp:239). */
+int sq_linear_decode_storage_rows(const sq_device *device, uint32_t rows, uint32_t output_size, uint32_t input_size,
+                                  uint32_t *storage_rows);
+/* Linear::ggufFloatTile (Linear.hpp:273-276; LinearGguf.cpp:837-844): the SQ_FLOAT_TILE_* a float projection of `rows`
+ * rows into output_size columns of rows in format_id takes on this device. MI355X's policy: the matrix-core tile
+ * from 64 rows on, the lane chains below. ExecutionPlans picks the MoE router's tile with it (ExecutionPlans.cpp:62),
+ * as sq_moe_config_for does. */
+int sq_linear_float_tile(const sq_device *device, uint32_t rows, uint32_t output_size, uint32_t format_id,
+                         uint32_t *tile);
 /* requireSegmentPlanes (LinearGguf.cpp:905-923): SQ_OK when the planes hold every tile of the segment. */
 int sq_require_segment_planes(const sq_segment *segment, const char *what, uint32_t plane_inputs);
 
@@ -158,7 +170,11 @@ int sq_require_segment_planes(const sq_segment *segment, const char *what, uint3
 
 /* Linear::add (Linear.cpp:203-232; LinearGguf.cpp:579-802): the plan's projection of buffers->input. A decode of a
  * projection of up to SQ_MAX_SEGMENTS segments runs them in one dispatch whatever their formats (gguf_decode_fused);
- * a prefill runs one dispatch per format. */
+ * a prefill runs one dispatch per format. A prefill plan's input, output, residual, gate scratch, scratch table and
+ * partials are 16-byte aligned and its row scales (scratch sums) 4-byte aligned. Whether a prefill halves its tiles'
+ * K depends on the chunk's rows as well as the shape (a 4096-input, 14336-output projection halves from 257 to 512
+ * rows), so a row's output bits may differ between chunks of different row counts; each lies within the row's fp64
+ * interval. A decode row's bits depend only on the shape and the tile kind its rows run (1..4 rows, 5..16, 17..32). */
 int sq_linear_add(void *graph, const sq_linear_buffers *buffers, const sq_projection *projection,
                   const sq_linear_plan *plan, const sq_projection *gate);
 /* Linear::add with its result: *prepared (may be NULL) receives what the scratch table describes after the
@@ -167,9 +183,11 @@ int sq_linear_add_prepared(void *graph, const sq_linear_buffers *buffers, const 
                            const sq_linear_plan *plan, const sq_projection *gate, sq_prepared_input *prepared);
 /* No counterpart in the reference: Linear::add for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid allocation). The same plans and kernels as sq_linear_add, but
- * the split partials and counters, the prefill table and its row scales and the gate scratch come from a static
- * array of SQ_STATIC_SCRATCH_BYTES per GPU inside the library (held from its first use on that GPU to the end of the
- * process); buffers->scratch and buffers->gate_scratch are ignored and buffers->prepared must be empty. A plan whose
+ * the split partials and counters, the prefill table and its row scales and a two-pass gate/up pair's gate scratch
+ * come from a static array of SQ_STATIC_SCRATCH_BYTES per GPU inside the library (held from its first use on that GPU
+ * to the end of the process); buffers->scratch is ignored and buffers->prepared must be empty. buffers->gate_scratch
+ * is read only by an UP_WITH_GATE plan, as the gate operand its epilogue multiplies in (the caller's gate projection
+ * output, checked to hold the plan's rows as sq_linear_add checks it), and ignored by every other plan. A plan whose
  * scratch exceeds the array is refused (SQ_INVALID_ARGUMENT). Nothing is allocated: it launches a counter-clearing
  * kernel, then the plan's dispatches. Every call on one GPU shares that GPU's array, so calls that overlap on one GPU
  * (two streams, two threads) race; calls in one stream's order do not. */
@@ -194,11 +212,14 @@ typedef struct sq_norm_weights {
  * for PLAIN. width % 64 == 0; input, output, weights and the table 16-byte aligned. */
 int sq_norm_add_rms(void *graph, sq_buffer input, const sq_norm_weights *weight, sq_buffer output, uint32_t width,
                     uint32_t rows, const sq_linear_scratch *scratch, uint32_t layout, sq_prepared_input *prepared);
-/* addGgufFloat (Linear.hpp:29-40; LinearGguf.cpp:806-818) for a float segment (format SQ_FLOAT32_ROWS or SQ_FMT_BF16,
- * its rows in plane0): output[r][out_offset + n] = sum_k input[r][k] W[n][k] for r < rows, products and sums in
- * fp32, into an fp32 or bf16 (destination SQ_OUTPUT_*) destination of out_stride columns. input_size % 4 == 0. */
+/* addGgufFloat (Linear.hpp:34-40; LinearGguf.cpp:847-853) for a float segment (format SQ_FLOAT32_ROWS or
+ * SQ_FMT_BF16, its rows in plane0): output[r][out_offset + n] = sum_k input[r][k] W[n][k] for r < rows, products and
+ * sums in fp32, into an fp32 or bf16 (destination SQ_OUTPUT_*) destination of out_stride columns, on `tile`
+ * (SQ_FLOAT_TILE_*, sq_linear_float_tile's choice or the caller's). input_size % 4 == 0; the matrix-core tile takes
+ * input_size a multiple of 256 (the reference's neural accelerator tile: 32), else SQ_INVALID_ARGUMENT. Both tiles lie
+ * within (input_size / 64 + 8) 2^-24 sum |x w| of the exact sum. */
 int sq_float_add(void *graph, sq_buffer input, const sq_segment *weights, sq_buffer output, uint32_t rows,
-                 uint32_t out_stride, uint32_t out_offset, uint32_t destination);
+                 uint32_t out_stride, uint32_t out_offset, uint32_t destination, uint32_t tile);
 /* Linear::addPrefill / addPrefillResidual / addPrefillUpWithGate (Linear.cpp:234-256). */
 int sq_linear_add_prefill(const sq_device *device, void *graph, sq_buffer input, const sq_projection *projection,
                           sq_buffer output, uint32_t rows, const sq_linear_scratch *scratch);
@@ -274,9 +295,10 @@ typedef struct sq_moe_workspace {
 /* MoeGgufTile (MoE.hpp:297): Staged runs here; Register is the reference's Apple9 tile, which a plan refuses. */
 #define SQ_MOE_GGUF_TILE_STAGED 0u
 #define SQ_MOE_GGUF_TILE_REGISTER 1u
-/* FloatTile (Linear.hpp:33): the router projection's tile. Both values run this build's one float tile (the results
- * lie within the same fp32 bound); NEURAL_ACCELERATOR names an Apple unit and is accepted as the reference's callers
- * may pass it. */
+/* FloatTile (Linear.hpp:29-33): a float projection's tile (the MoE router's among them). On MI355X SIMDGROUP runs
+ * the lane chains (a wave of four rows by four columns, K over the lanes) and NEURAL_ACCELERATOR the matrix-core tile
+ * (fp32 16x16x4 MFMA, 32 rows by 32 columns a workgroup, K a multiple of 256); their results lie within one fp32
+ * bound. */
 #define SQ_FLOAT_TILE_SIMDGROUP 0u
 #define SQ_FLOAT_TILE_NEURAL_ACCELERATOR 1u
 /* MoeConfig (MoE.hpp:333-346): the device's policy for a MoE plan. cpu_bf16_experts opts the reference's streamed
@@ -351,6 +373,16 @@ int sq_moe_add_routing(void *graph, const sq_moe_buffers *buffers, const sq_moe_
                        const sq_moe_plan *plan);
 int sq_moe_add_routed(void *graph, const sq_moe_buffers *buffers, const sq_moe_weights *weights,
                       const sq_moe_plan *plan);
+/* MoE::addRoutes (MoE.hpp:403-411; MoE.cpp:527-543): the routing of `rows` rows (1..2048) of `input` (bf16
+ * [rows][hidden]) with no plan and no grouping, into caller buffers. With router rows (router non-NULL, plane0 set:
+ * F32 or BF16 [experts][hidden]) it first projects the input onto them into `scores` on router_tile (SQ_FLOAT_TILE_*);
+ * otherwise it reads the fp32 scores the caller wrote there. scores: rows of sq_moe_router_width(shape) fp32 slots;
+ * selected (uint32) and routing_weights (fp32): experts_per_token + shared_slices per row, the top-k experts then
+ * the shared slices, as sq_moe_add_routing writes them. shared_scalar_gate (fp32 [hidden]) is read only for a gated
+ * shared expert. input, scores and shared_scalar_gate are 16-byte aligned. */
+int sq_moe_add_routes(void *graph, sq_buffer input, const sq_segment *router, sq_buffer shared_scalar_gate,
+                      sq_buffer scores, sq_buffer selected, sq_buffer routing_weights, uint32_t rows,
+                      const sq_moe_shape *shape, uint32_t router_tile);
 
 #ifdef __cplusplus
 }

@@ -104,6 +104,18 @@ class Linear final {
     check(sq_linear_prefill_scratch_size(&device_, shape.outputSize, shape.inputSize, &out));
     return out;
   }
+  // Linear::decodeStorageRows (Linear.hpp:254-257).
+  [[nodiscard]] uint32_t decodeStorageRows(uint32_t rows, ProjectionShape shape) const {
+    uint32_t out = 0;
+    check(sq_linear_decode_storage_rows(&device_, rows, shape.outputSize, shape.inputSize, &out));
+    return out;
+  }
+  // Linear::ggufFloatTile (Linear.hpp:273-276): an SQ_FLOAT_TILE_* value.
+  [[nodiscard]] uint32_t ggufFloatTile(uint32_t rows, uint32_t outputSize, uint32_t formatId) const {
+    uint32_t out = 0;
+    check(sq_linear_float_tile(&device_, rows, outputSize, formatId, &out));
+    return out;
+  }
   // LinearPlan::scratchSize and gateScratchBytes of one plan.
   [[nodiscard]] static LinearScratchSize scratchSize(const LinearPlan &plan, uint64_t *gateScratchBytes = nullptr) {
     LinearScratchSize out{};
@@ -160,10 +172,10 @@ class Normalization final {
   }
 };
 
-// addGgufFloat (Linear.hpp:29-40) for F32 or BF16 rows.
+// addGgufFloat (Linear.hpp:34-40) for F32 or BF16 rows, on `tile` (SQ_FLOAT_TILE_*).
 inline void addGgufFloat(Graph graph, Buffer input, const QuantizedSegment &weights, Buffer output, uint32_t rows,
-                         uint32_t outStride, uint32_t outOffset, uint32_t destination = SQ_OUTPUT_F32) {
-  check(sq_float_add(graph, input, &weights, output, rows, outStride, outOffset, destination));
+                         uint32_t outStride, uint32_t outOffset, uint32_t destination, uint32_t tile) {
+  check(sq_float_add(graph, input, &weights, output, rows, outStride, outOffset, destination, tile));
 }
 
 // MoE (MoE.hpp:387-423). The config the reference's execution plans derive (ExecutionPlans::moeConfig) is
@@ -193,6 +205,13 @@ class MoE final {
   }
   void addRouted(Graph graph, const MoeBuffers &buffers, const MoeWeights &weights, const MoePlan &plan) const {
     check(sq_moe_add_routed(graph, &buffers, &weights, &plan));
+  }
+  // MoE::addRoutes (MoE.hpp:403-411): router may be null (the scores are the caller's).
+  static void addRoutes(Graph graph, Buffer input, const QuantizedSegment *router, Buffer sharedScalarGate,
+                        Buffer scores, Buffer selected, Buffer routingWeights, uint32_t rows, const MoeShape &shape,
+                        uint32_t routerTile) {
+    check(sq_moe_add_routes(graph, input, router, sharedScalarGate, scores, selected, routingWeights, rows, &shape,
+                            routerTile));
   }
 };
 

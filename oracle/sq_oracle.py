@@ -296,14 +296,15 @@ def rounded_once_to_bf16(got_bits: np.ndarray, exact: np.ndarray) -> np.ndarray:
 
 
 def half_rows(x_bf16: np.ndarray):
-    """The prefill tile's prepared input of bf16 rows [rows][K] (K % 32 == 0): each row times 2^-shift, shift the
-    smallest that brings its largest magnitude below 2^16 (0 when it already is), as fp16 bits, chunk v = 4 g + c
-    of a row holding inputs 32 g + 4 c .. +3 then 32 g + 16 + 4 c .. +3; and the fp32 scales 2^shift."""
+    """The prefill tile's prepared input of bf16 rows [rows][K] (K % 32 == 0): each row times 2^-shift, shift the one
+    that puts its largest magnitude in [2^15, 2^16), but at least -126 (zero rows and rows of bf16 subnormals take
+    -126; infinities and NaNs count as 2^128), as fp16 bits, chunk v = 4 g + c of a row holding inputs
+    32 g + 4 c .. +3 then 32 g + 16 + 4 c .. +3; and the fp32 scales 2^shift."""
     bits = np.ascontiguousarray(x_bf16, np.uint16)
     rows, k = bits.shape
     largest = (bits & 0x7FFF).max(axis=1).astype(np.int64)
     exponent = (np.minimum(largest, 0x7F80) >> 7) - 127
-    shift = np.where(exponent >= 16, exponent - 15, 0)
+    shift = np.maximum(exponent - 15, -126)
     scaled = bf16_values(bits) * np.ldexp(1.0, -shift)[:, None]
     half = scaled.astype(np.float32).astype(np.float16).view(np.uint16)   # exact in fp32; one rounding to fp16
     order = np.empty(k, np.int64)

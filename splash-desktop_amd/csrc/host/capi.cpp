@@ -270,7 +270,11 @@ int sq_linear_add_static(void *graph, const sq_linear_buffers *b, const sq_proje
     if (bb.prepared.source.ptr || bb.prepared.source.bytes || bb.prepared.layout)
       throw std::invalid_argument("the static-scratch entry point prepares its own table: buffers->prepared must be empty");
     const LinearScratchSize sizes = selected.scratchSize();
-    const uint64_t gateBytes = selected.gateScratchBytes();
+    // An up-with-gate plan's gate "scratch" is the caller's gate projection output, the operand its epilogue reads
+    // (Linear::addPrefillUpWithGate): it stays the caller's buffer. Only a two-pass gate/up pair's gate, which the
+    // plan writes and reads itself, comes from the static array.
+    const bool callerGate = selected.workload().epilogue == LinearEpilogue::UpWithGate;
+    const uint64_t gateBytes = callerGate ? 0 : selected.gateScratchBytes();
     const StaticLayout l = staticLayout(sizes, gateBytes);
     if (l.end > kStaticScratchBytes)
       throw std::invalid_argument("the plan needs " + std::to_string(l.end) + " bytes of scratch; the static scratch holds " +
@@ -285,7 +289,8 @@ int sq_linear_add_static(void *graph, const sq_linear_buffers *b, const sq_proje
     }
     const LinearScratch sc{region(l.input, sizes.input), region(l.sums, sizes.sums),
                            region(l.partials, sizes.partials), region(l.counters, sizes.counters), {}};
-    const LinearBuffers buffers{buf(bb.input), buf(bb.output), buf(bb.residual), region(l.gate, gateBytes), sc, {}};
+    const LinearBuffers buffers{buf(bb.input), buf(bb.output), buf(bb.residual),
+                                callerGate ? buf(bb.gate_scratch) : region(l.gate, gateBytes), sc, {}};
     const Linear linearOp(DeviceCapabilities{});
     if (gate) {
       const Projection g = projection(*gate);
@@ -315,12 +320,25 @@ int sq_norm_add_rms(void *graph, sq_buffer input, const sq_norm_weights *weight,
 }
 
 int sq_float_add(void *graph, sq_buffer input, const sq_segment *weights, sq_buffer output, uint32_t rows,
-                 uint32_t out_stride, uint32_t out_offset, uint32_t destination) {
+                 uint32_t out_stride, uint32_t out_offset, uint32_t destination, uint32_t tile) {
   return guarded([&] {
     if (destination > SQ_OUTPUT_F32) throw std::invalid_argument("unknown float destination");
+    if (tile > SQ_FLOAT_TILE_NEURAL_ACCELERATOR) throw std::invalid_argument("unknown float tile");
     const sq_segment &w = need(weights, "float rows");
     addGgufFloat(stream(graph), buf(input), QuantizedSegment::rows(w.format_id, w.output_size, w.input_size, buf(w.plane0)),
-                 buf(output), rows, out_stride, out_offset, FloatOutput(destination));
+                 buf(output), rows, out_stride, out_offset, FloatOutput(destination), FloatTile(tile));
+  });
+}
+
+int sq_linear_float_tile(const sq_device *device, uint32_t rows, uint32_t output_size, uint32_t format_id,
+                         uint32_t *tile) {
+  return guarded([&] { *need(tile, "tile") = uint32_t(linear(device).floatTile(rows, output_size, format_id)); });
+}
+
+int sq_linear_decode_storage_rows(const sq_device *device, uint32_t rows, uint32_t output_size, uint32_t input_size,
+                                  uint32_t *storage_rows) {
+  return guarded([&] {
+    *need(storage_rows, "storage rows") = linear(device).decodeStorageRows(rows, {output_size, input_size});
   });
 }
 
@@ -559,6 +577,19 @@ int sq_moe_add_routed(void *graph, const sq_moe_buffers *b, const sq_moe_weights
   return guarded([&] {
     const MoePlan plan = moePlan(need(p, "plan"));
     MoE::addRouted(stream(graph), moeBuffers(need(b, "buffers")), moeWeights(need(w, "weights"), *p), plan);
+  });
+}
+int sq_moe_add_routes(void *graph, sq_buffer input, const sq_segment *router, sq_buffer shared_scalar_gate,
+                      sq_buffer scores, sq_buffer selected, sq_buffer routing_weights, uint32_t rows,
+                      const sq_moe_shape *shape, uint32_t router_tile) {
+  return guarded([&] {
+    if (router_tile > SQ_FLOAT_TILE_NEURAL_ACCELERATOR) throw std::invalid_argument("invalid MoE router tile");
+    const MoeShape s = moeShape(need(shape, "shape"));
+    QuantizedSegment r;
+    if (router && router->plane0.ptr)
+      r = QuantizedSegment::rows(router->format_id, router->output_size, router->input_size, buf(router->plane0));
+    MoE::addRoutes(stream(graph), buf(input), r, buf(shared_scalar_gate), buf(scores), buf(selected),
+                   buf(routing_weights), rows, s, FloatTile(router_tile));
   });
 }
 

@@ -295,13 +295,24 @@ LinearScratchSize Linear::decodeScratchSize(ProjectionShape shape) const {
     }
   return bound;
 }
+// MI355X's float-tile policy: the matrix-core tile from kern::kFloatMfmaRows rows on, the lane chains below (a
+// decode step's handful of rows). Measured on the reference's 35B router (2048 rows x 256 experts x 2048 inputs):
+// 76 us on the lane chains, 41 us on the matrix cores. The reference's rule (LinearGguf.cpp:837-844) weighs tiles
+// per core of an Apple10 device; the row threshold here depends on neither the columns nor the format.
+FloatTile Linear::floatTile(uint32_t rows, uint32_t outputSize, uint32_t formatId) const noexcept {
+  (void)outputSize;
+  (void)formatId;
+  return rows >= kern::kFloatMfmaRows ? FloatTile::NeuralAccelerator : FloatTile::Simdgroup;
+}
+
+// Every chunk of 1..SQ_PREFILL_TOKEN_BUDGET rows: the prefill tile's halved-K partials (2 rows N fp32) exist only in
+// a band of row counts (for 4096 inputs x 14336 outputs, 257..512 rows), so no short list of row counts bounds them.
+// A plan's scratch does not depend on its epilogue; the three epilogues are taken all the same.
 LinearScratchSize Linear::prefillScratchSize(ProjectionShape shape) const {
   LinearScratchSize bound;
-  for (const uint32_t rows : {1u, 2u, 4u, 8u, 16u, 32u, SQ_PREFILL_TOKEN_BUDGET})
+  for (uint32_t rows = 1; rows <= SQ_PREFILL_TOKEN_BUDGET; ++rows)
     for (const auto e : {LinearEpilogue::None, LinearEpilogue::Residual, LinearEpilogue::UpWithGate})
       bound.include(plan({{shape.outputSize, shape.inputSize}, rows, LinearPhase::Prefill, e}).scratchSize());
-  for (uint32_t rows = 3; rows <= kMaximumStagedRows; ++rows)
-    bound.include(plan({{shape.outputSize, shape.inputSize}, rows, LinearPhase::Prefill, LinearEpilogue::None}).scratchSize());
   return bound;
 }
 
@@ -326,10 +337,12 @@ PreparedInput Linear::add(hipStream_t graph, LinearBuffers b, const Projection &
   requireSegments(p, w.matrix);
   if (gate) requireSegments(*gate, w.matrix);
   if (selected.configuration().tile == LinearTile::GgufPrefill) {
-    // The prefill tile moves activations, outputs and epilogue operands in 16-byte vectors.
+    // The prefill tile moves activations, outputs, epilogue operands, the table and a halved tile's fp32 partials in
+    // 16-byte vectors (the row scales in 4-byte words).
     const auto aligned = [](const Buffer &buffer) { return (reinterpret_cast<uintptr_t>(buffer.ptr) & 15u) == 0; };
     if (!aligned(b.input) || !aligned(b.output) || !aligned(b.residual) || !aligned(b.gateScratch) ||
-        !aligned(b.scratch.input))
+        !aligned(b.scratch.input) || !aligned(b.scratch.partials) ||
+        (reinterpret_cast<uintptr_t>(b.scratch.sums.ptr) & 3u))
       throw std::invalid_argument("prefill projection buffers are 16-byte aligned");
   }
   const std::vector<QuantizedSegment> &segments = p.blocks().segments;

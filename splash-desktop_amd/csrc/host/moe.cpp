@@ -107,6 +107,8 @@ MoePlan::MoePlan(MoeShape shape, uint32_t rows, MoeConfig config, MoePhase phase
 
 MoeConfig MoE::config(MoeShape shape, uint32_t rows, MoePhase phase) {
   MoeConfig c;
+  // ExecutionPlans.cpp:62: the router's tile by Linear's float-tile policy.
+  c.ggufRouterTile = Linear(DeviceCapabilities{}).floatTile(rows, shape.experts, SQ_FLOAT32_ROWS);
   if (phase == MoePhase::Prefill)
     c.expertTile = uint64_t{rows} * shape.expertsPerToken <= shape.experts ? MoeExpertTile::M8 : MoeExpertTile::M32;
   return c;
@@ -129,22 +131,42 @@ void MoE::add(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w, const
   addRouted(graph, b, w, plan);
 }
 
+void MoE::addRoutes(hipStream_t graph, Buffer input, const QuantizedSegment &router, Buffer sharedScalarGate,
+                    Buffer scores, Buffer selected, Buffer routingWeights, uint32_t rows, MoeShape s,
+                    FloatTile routerTile) {
+  if (!s.valid()) throw std::invalid_argument("invalid MoE routing shape");
+  if (!rows || rows > SQ_PREFILL_TOKEN_BUDGET) throw std::invalid_argument("invalid MoE routing rows");
+  if (router.plane0 && (!router.isFloat() || router.outputSize != s.experts || router.inputSize != s.hiddenSize))
+    throw std::invalid_argument("MoE router does not match the plan");
+  const uint32_t stride = s.routerWidth();
+  const uint64_t routes = uint64_t{rows} * s.routesPerToken();
+  requireBytes(input, uint64_t{rows} * s.hiddenSize * 2, "MoE input");
+  requireBytes(scores, uint64_t{rows} * stride * 4, "MoE router scores");
+  requireBytes(selected, routes * 4, "MoE selected experts");
+  requireBytes(routingWeights, routes * 4, "MoE routing weights");
+  if (s.sharedGate) requireBytes(sharedScalarGate, uint64_t{s.hiddenSize} * 4, "MoE shared scalar gate weight");
+  // The select kernel reads the scores and the shared gate's input rows in 16-byte vectors.
+  const auto aligned = [](const Buffer &buffer) { return (reinterpret_cast<uintptr_t>(buffer.ptr) & 15u) == 0; };
+  if (!aligned(input) || !aligned(scores) || !aligned(sharedScalarGate))
+    throw std::invalid_argument("MoE routing input, scores and shared scalar gate are 16-byte aligned");
+  // The router's fp32 scores, rows of routerWidth() (MoE.cpp:527-543), when the block carries its rows; else the
+  // caller wrote them there.
+  if (router.plane0) addGgufFloat(graph, input, router, scores, rows, stride, 0, FloatOutput::Float32, routerTile);
+  const SqMoeRouteParams route{rows, s.hiddenSize, s.experts, s.expertsPerToken};
+  launched(kern::launch_moe_route_select(scores.as<const float>(), stride, selected.as<uint32_t>(),
+                                         routingWeights.as<float>(), route, input.as<const uint16_t>(),
+                                         s.sharedGate ? sharedScalarGate.as<const float>() : nullptr,
+                                         uint32_t(s.router), s.sharedSlices, graph),
+           "MoE route select");
+}
+
 void MoE::addRouting(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
   validate(b, w, plan);
   const MoeShape s = plan.shape();
   const MoeScratch &sc = b.scratch;
-  // The router's fp32 scores in the grouped input, rows of routerWidth() (MoE.cpp:527-543), when the block carries
-  // its rows; else the caller wrote them there.
-  const uint32_t stride = s.routerWidth();
-  if (w.router.plane0)
-    addGgufFloat(graph, b.input, w.router, sc.groupedInput, plan.rows(), stride, 0, FloatOutput::Float32);
-  const SqMoeRouteParams route{plan.rows(), s.hiddenSize, s.experts, s.expertsPerToken};
-  launched(kern::launch_moe_route_select(sc.groupedInput.as<const float>(), stride,
-                                         sc.selectedExperts.as<uint32_t>(), sc.routingWeights.as<float>(), route,
-                                         b.input.as<const uint16_t>(),
-                                         s.sharedGate ? w.sharedScalarGate.as<const float>() : nullptr,
-                                         uint32_t(s.router), s.sharedSlices, graph),
-           "MoE route select");
+  // The scores live in the grouped input (MoE.cpp:445-459).
+  addRoutes(graph, b.input, w.router, s.sharedGate ? w.sharedScalarGate : Buffer{}, sc.groupedInput,
+            sc.selectedExperts, sc.routingWeights, plan.rows(), s, plan.configuration().ggufRouterTile);
   const SqMoeGroupParams group{plan.rows(), s.expertsPerToken, plan.tileRows(), s.experts,
                                s.expertIntermediateSize / SQ_TILE_COLUMNS, s.hiddenSize / SQ_TILE_COLUMNS,
                                SQ_TARGET_VERIFY_ROWS, 0};

@@ -38,10 +38,10 @@ struct MoeShape {
 
 enum class MoePhase : uint8_t { Prefill, Decode };
 
-// MoeExpertTile, MoeGgufTile (MoE.hpp:284,297), FloatTile (Linear.hpp:33) and MoeConfig (MoE.hpp:333-346).
+// MoeExpertTile, MoeGgufTile (MoE.hpp:284,297) and MoeConfig (MoE.hpp:333-346); FloatTile is the float
+// projection's (ops.hpp).
 enum class MoeExpertTile : uint8_t { M8 = 8, M32 = 32 };
 enum class MoeGgufTile : uint8_t { Staged, Register };
-enum class FloatTile : uint8_t { Simdgroup, NeuralAccelerator };
 struct MoeConfig {
   MoeExpertTile expertTile = MoeExpertTile::M8;
   MoeGgufTile ggufTile = MoeGgufTile::Staged;
@@ -120,6 +120,14 @@ struct MoE {
   static void add(hipStream_t graph, const MoeBuffers &buffers, const MoeWeights &weights, const MoePlan &plan);
   static void addRouting(hipStream_t graph, const MoeBuffers &buffers, const MoeWeights &weights, const MoePlan &plan);
   static void addRouted(hipStream_t graph, const MoeBuffers &buffers, const MoeWeights &weights, const MoePlan &plan);
+  // MoE::addRoutes (MoE.hpp:403-411; MoE.cpp:527-543): the routing of `rows` rows of `input` with no plan and no
+  // grouping. With router rows (F32 or BF16, [experts][hidden]) it projects the input onto them into `scores` (rows of
+  // shape.routerWidth() fp32 slots) on `routerTile`; with a null router it reads the scores already there. Then each
+  // row's top-k experts and shared slices, and their routing weights, into `selected` and `routingWeights`
+  // (shape.routesPerToken() per row). `sharedScalarGate` (fp32 [hidden]) is read only for a gated shared expert.
+  static void addRoutes(hipStream_t graph, Buffer input, const QuantizedSegment &router, Buffer sharedScalarGate,
+                        Buffer scores, Buffer selected, Buffer routingWeights, uint32_t rows, MoeShape shape,
+                        FloatTile routerTile);
 };
 
 }  // namespace sq::ops

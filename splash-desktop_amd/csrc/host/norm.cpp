@@ -36,8 +36,13 @@ PreparedInput Normalization::addRms(hipStream_t graph, Buffer input, const NormW
 }
 
 void addGgufFloat(hipStream_t graph, Buffer input, const QuantizedSegment &w, Buffer output, uint32_t rows,
-                  uint32_t outStride, uint32_t outOffset, FloatOutput type) {
+                  uint32_t outStride, uint32_t outOffset, FloatOutput type, FloatTile tile) {
   if (!w.isFloat()) throw std::invalid_argument("the float projection takes F32 or BF16 rows");
+  if (tile != FloatTile::Simdgroup && tile != FloatTile::NeuralAccelerator)
+    throw std::invalid_argument("unknown float tile");
+  const bool matrix = tile == FloatTile::NeuralAccelerator;
+  if (matrix && w.inputSize % kern::kFloatMfmaInputs)
+    throw std::invalid_argument("the matrix-core float tile takes inputs in multiples of 256");
   if (!rows || !w.outputSize || !w.inputSize || w.inputSize % 4)
     throw std::invalid_argument("the float projection takes rows of a multiple of 4 inputs");
   if (uint64_t{outOffset} + w.outputSize > outStride)
@@ -51,7 +56,7 @@ void addGgufFloat(hipStream_t graph, Buffer input, const QuantizedSegment &w, Bu
     throw std::invalid_argument("float rows are 16-byte aligned and the input 8-byte aligned");
   launched(kern::launch_float_rows(input.as<const uint16_t>(), w.plane0.ptr, f32, output.ptr,
                                    type == FloatOutput::Float32, rows, w.outputSize, w.inputSize, outStride, outOffset,
-                                   graph),
+                                   matrix, graph),
            "float projection");
 }
 

@@ -32,6 +32,11 @@ struct Buffer {
 void requireBytes(const Buffer &buffer, uint64_t bytes, std::string_view what);
 
 enum class FloatOutput : uint8_t { BFloat16, Float32 };
+// FloatTile (Linear.hpp:29-33): the tile of a float projection. On MI355X Simdgroup is the lane-chain kernel (a wave
+// of four rows by four columns, K split over the lanes) and NeuralAccelerator the matrix-core tile (the fp32
+// 16x16x4 MFMA, 32 rows by 32 columns a workgroup, K a multiple of 256); both round only in fp32 accumulation, within
+// one bound (K / 64 + 8 roundings of sum |x w|). Linear::floatTile picks one.
+enum class FloatTile : uint8_t { Simdgroup, NeuralAccelerator };
 [[nodiscard]] constexpr uint64_t elementBytes(FloatOutput type) noexcept {
   return type == FloatOutput::Float32 ? 4 : 2;
 }
@@ -192,6 +197,9 @@ public:
                                       const Projection *gate = nullptr) const;
   [[nodiscard]] LinearScratchSize decodeScratchSize(ProjectionShape shape) const;
   [[nodiscard]] LinearScratchSize prefillScratchSize(ProjectionShape shape) const;
+  // ggufFloatTile (Linear.hpp:273-276; LinearGguf.cpp:837-844): the tile of a float projection of `rows` rows into
+  // `outputSize` columns of rows in `formatId` on this device.
+  [[nodiscard]] FloatTile floatTile(uint32_t rows, uint32_t outputSize, uint32_t formatId) const noexcept;
   [[nodiscard]] static LinearPlan plan(LinearWorkload workload, LinearConfig config, FloatOutput destination);
   // Returns what the scratch table describes after the dispatch (Linear.cpp:203-231).
   PreparedInput add(hipStream_t graph, LinearBuffers buffers, const Projection &projection, const LinearPlan &plan,
@@ -230,9 +238,10 @@ struct Normalization {
                               LinearInput layout = LinearInput::Plain);
 };
 
-// addGgufFloat (Linear.hpp:29-40) for a float segment: out[r][outOffset + n] = sum_k input[r][k] W[n][k] for rows
-// r < `rows`, in fp32, into a `type` destination of `outStride` columns.
+// addGgufFloat (Linear.hpp:34-40) for a float segment: out[r][outOffset + n] = sum_k input[r][k] W[n][k] for rows
+// r < `rows`, in fp32, into a `type` destination of `outStride` columns, on `tile` (the matrix-core tile takes K a
+// multiple of 256, as the reference's neural accelerator tile takes K a multiple of 32).
 void addGgufFloat(hipStream_t graph, Buffer input, const QuantizedSegment &weights, Buffer output, uint32_t rows,
-                  uint32_t outStride, uint32_t outOffset, FloatOutput type);
+                  uint32_t outStride, uint32_t outOffset, FloatOutput type, FloatTile tile);
 
 }  // namespace sq::ops

@@ -1,8 +1,11 @@
-// The prefill tile's prepared input ("half rows"): each row of bf16 activations scaled by a power of two that
-// brings its largest magnitude below 2^16 and converted to fp16, which is exact for every bf16 value in half's
-// normal range, stored group by group in the tile's read order, with the power of two kept per row for the
-// epilogue. The prefill's own prepare dispatch and the RMS norm producer both write it, from the same bf16 values
-// and with these same helpers, so the table is the same bits whichever wrote it.
+// The prefill tile's prepared input ("half rows"): each row of bf16 activations scaled by the power of two that
+// puts its largest magnitude in [2^15, 2^16) and converted to fp16, stored group by group in the tile's read order,
+// with the power of two kept per row for the epilogue. Scaling up as well as down keeps a row of any magnitude
+// exact: every value of the row within 2^29 of its largest is a normal half after the scale (bf16's 8 significant
+// bits fit half's 11), so only values below 2^-29 of the row's largest round, by at most 2^-25 of a half unit, that
+// is 2^-40 of the largest, far below the fp32 accumulation's own error. The prefill's own prepare dispatch and the
+// RMS norm producer both write it, from the same bf16 values and with these same helpers, so the table is the same
+// bits whichever wrote it.
 #pragma once
 #include "device.hpp"
 
@@ -20,11 +23,13 @@ __device__ __forceinline__ uint32_t bf16_largest(u32x4 w) {
   return m;
 }
 
-// The row's shift: the table holds x 2^-shift, so that the largest magnitude ends below 2^16 (shift 0 when it is
-// already).
+// The row's shift: the table holds x 2^-shift, the largest magnitude in [2^15, 2^16). The shift stays at -126 or
+// above so that 2^shift and 2^-shift are both normal floats: a row whose largest magnitude is below 2^-111 (a zero
+// row, or bf16 subnormals) takes -126, where every nonzero bf16 value times 2^126 is at least 2^-7, a normal half.
+// Infinities and NaNs count as 2^128 (shift 113), as before.
 __device__ __forceinline__ int half_rows_shift(uint32_t largest) {
   const int exponent = (int)(min(largest, 0x7F80u) >> 7) - 127;
-  return exponent >= 16 ? exponent - 15 : 0;
+  return max(exponent - 15, -126);
 }
 
 // Eight bf16 values times `down` (a power of two) as fp16, in the same order.

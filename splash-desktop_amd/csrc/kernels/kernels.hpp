@@ -117,11 +117,13 @@ hipError_t launch_repack(const uint8_t *src, uint8_t *dst, const SqGgufRepackPar
 hipError_t launch_rms_norm(const uint16_t *input, const void *weight, bool f32_weights, uint16_t *output,
                            uint32_t width, uint32_t rows, uint16_t *half_input, float *row_scale, hipStream_t stream);
 // A float projection: out[r][out_offset + n] = sum_k x[r][k] W[n][k] for W's N rows of K values stored fp32 or bf16,
-// fp32 products and sums, into fp32 or bf16 [rows][out_stride]. K % 4 == 0. At least 64 rows and K a multiple of 256
-// run on the fp32 MFMA; either way an output takes at most K / 64 + 8 roundings.
+// fp32 products and sums, into fp32 or bf16 [rows][out_stride]. K % 4 == 0. `mfma` runs the fp32 MFMA tile (K a
+// multiple of kFloatMfmaInputs, any rows), else the lane chains; either way an output takes at most K / 64 + 8
+// roundings. kFloatMfmaRows: the rows from which the policy takes the MFMA tile.
+constexpr uint32_t kFloatMfmaRows = 64, kFloatMfmaInputs = 256;
 hipError_t launch_float_rows(const uint16_t *input, const void *weights, bool f32_weights, void *output,
                              bool f32_output, uint32_t rows, uint32_t N, uint32_t K, uint32_t out_stride,
-                             uint32_t out_offset, hipStream_t stream);
+                             uint32_t out_offset, bool mfma, hipStream_t stream);
 hipError_t launch_stream_read(const void *src, uint64_t bytes, uint32_t *sink, uint32_t workgroups, uint32_t threads,
                               hipStream_t stream);
 hipError_t launch_mfma_peak(uint32_t workgroups, uint32_t waves_per_simd, uint32_t iterations, float *sink,

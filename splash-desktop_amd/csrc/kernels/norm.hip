@@ -216,7 +216,7 @@ __global__ __launch_bounds__(256) void float_rows_kernel(const uint16_t *input, 
 // 4 K / (16 kFloatSlices) + 2 + log2 kFloatSlices + 1 roundings (an MFMA's four products summed in at most four),
 // K / 64 + 7 for sixteen slices: within the lane-chain kernel's K / 64 + 8.
 constexpr int kFloatSlices = 16;
-constexpr uint32_t kFloatMfmaRows = 64;   // fewer rows take the lane chains (a decode step's handful)
+static_assert(kFloatMfmaInputs == 16 * kFloatSlices, "every slice takes whole 16-input steps");
 template <bool F32W, bool F32OUT>
 __global__ __launch_bounds__(64 * kFloatSlices) void float_rows_mfma_kernel(const uint16_t *input, const void *weights,
                                                                             void *output, uint32_t rows, uint32_t N,
@@ -300,11 +300,8 @@ hipError_t launch_rms_norm(const uint16_t *input, const void *weight, bool f32_w
 
 hipError_t launch_float_rows(const uint16_t *input, const void *weights, bool f32_weights, void *output,
                              bool f32_output, uint32_t rows, uint32_t N, uint32_t K, uint32_t out_stride,
-                             uint32_t out_offset, hipStream_t stream) {
-  if (!rows || !N || K % 4) return hipErrorInvalidValue;
-  // Prefill-sized row counts take the MFMA kernel (whole 16-input steps in every slice), decode-sized ones the lane
-  // chains.
-  const bool mfma = rows >= kFloatMfmaRows && K % (16 * kFloatSlices) == 0;
+                             uint32_t out_offset, bool mfma, hipStream_t stream) {
+  if (!rows || !N || K % 4 || (mfma && K % kFloatMfmaInputs)) return hipErrorInvalidValue;
   const dim3 grid = mfma ? dim3((N + 31) / 32, (rows + 31) / 32) : dim3((N + 15) / 16, (rows + 3) / 4);
   const dim3 block = mfma ? dim3(64 * kFloatSlices) : dim3(256);
 #define SQ_FLOAT(W, O)                                                                                                \

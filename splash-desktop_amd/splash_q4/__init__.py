@@ -171,7 +171,9 @@ _SIGNATURES = {
                              POINTER(Projection)],
     "sq_norm_add_rms": [c_void_p, Buffer, POINTER(NormWeights), Buffer, c_uint32, c_uint32, POINTER(LinearScratch),
                         c_uint32, POINTER(PreparedInput)],
-    "sq_float_add": [c_void_p, Buffer, POINTER(Segment), Buffer, c_uint32, c_uint32, c_uint32, c_uint32],
+    "sq_float_add": [c_void_p, Buffer, POINTER(Segment), Buffer, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32],
+    "sq_linear_float_tile": [POINTER(Device), c_uint32, c_uint32, c_uint32, POINTER(c_uint32)],
+    "sq_linear_decode_storage_rows": [POINTER(Device), c_uint32, c_uint32, c_uint32, POINTER(c_uint32)],
     "sq_linear_add_prefill": [POINTER(Device), c_void_p, Buffer, POINTER(Projection), Buffer, c_uint32,
                               POINTER(LinearScratch)],
     "sq_linear_add_prefill_residual": [POINTER(Device), c_void_p, Buffer, POINTER(Projection), Buffer, Buffer,
@@ -194,6 +196,8 @@ _SIGNATURES = {
     "sq_moe_add": [c_void_p, POINTER(MoeBuffers), POINTER(MoeWeights), POINTER(MoePlan)],
     "sq_moe_add_routing": [c_void_p, POINTER(MoeBuffers), POINTER(MoeWeights), POINTER(MoePlan)],
     "sq_moe_add_routed": [c_void_p, POINTER(MoeBuffers), POINTER(MoeWeights), POINTER(MoePlan)],
+    "sq_moe_add_routes": [c_void_p, Buffer, POINTER(Segment), Buffer, Buffer, Buffer, Buffer, c_uint32,
+                          POINTER(MoeShape), c_uint32],
 }
 
 

@@ -24,6 +24,8 @@ int main() {
   const LinearScratchSize s = linear.decodeScratchSize({14336, 4096});
   std::printf("decode rows %u tile %u splits %u; prefill tile %u; decode partials %llu\n", decode.storage_rows,
               decode.config.tile, decode.config.splits, prefill.config.tile, (unsigned long long)s.partials);
+  std::printf("storage rows %u; float tile %u at 2048 rows, %u at 8\n", linear.decodeStorageRows(8, {14336, 4096}),
+              linear.ggufFloatTile(2048, 256, SQ_FLOAT32_ROWS), linear.ggufFloatTile(8, 256, SQ_FLOAT32_ROWS));
   const MoeShape shape{2048, 128, 8, 768, SQ_FMT_AF4G64, SQ_MOE_ROUTER_SOFTMAX, 0, 0};
   const MoePlan moe = MoE::decodePlan(shape, 2, MoE::config(shape, 16, SQ_PHASE_DECODE));
   const MoePlan moePrefill = MoE::prefillPlan(shape, 512, MoE::config(shape, 512, SQ_PHASE_PREFILL));

@@ -389,10 +389,101 @@ def test_norm_and_float_rows_refusals():
         sq.call("sq_norm_add_rms", None, io, sq.byref(weights), io, width, rows, None, 7, None)
     q4k = sq.Segment(_fake(64 * 2048), sq.Buffer(), sq.Buffer(), 64, 2048, 0, sq.FMT_Q4K)
     with pytest.raises(sq.InvalidArgument, match="F32 or BF16"):
-        sq.call("sq_float_add", None, io, sq.byref(q4k), io, rows, 64, 0, sq.OUTPUT_F32)
+        sq.call("sq_float_add", None, io, sq.byref(q4k), io, rows, 64, 0, sq.OUTPUT_F32, sq.FLOAT_TILE_SIMDGROUP)
     f32 = sq.Segment(_fake(64 * 2048 * 4), sq.Buffer(), sq.Buffer(), 64, 2048, 0, sq.FLOAT32_ROWS)
     with pytest.raises(sq.InvalidArgument, match="outside its destination"):
-        sq.call("sq_float_add", None, io, sq.byref(f32), _fake(rows * 64 * 4), rows, 64, 8, sq.OUTPUT_F32)
+        sq.call("sq_float_add", None, io, sq.byref(f32), _fake(rows * 64 * 4), rows, 64, 8, sq.OUTPUT_F32,
+                sq.FLOAT_TILE_SIMDGROUP)
+
+
+def test_float_tile_policy_and_refusals():
+    """Linear::ggufFloatTile: the matrix-core tile from 64 rows on, the lane chains below; the matrix-core tile takes
+    inputs in multiples of 256 and an unknown tile is refused."""
+    dev, tile = sq.device(), sq.c_uint32()
+    for rows, want in ((1, sq.FLOAT_TILE_SIMDGROUP), (63, sq.FLOAT_TILE_SIMDGROUP),
+                       (64, sq.FLOAT_TILE_NEURAL_ACCELERATOR), (2048, sq.FLOAT_TILE_NEURAL_ACCELERATOR)):
+        sq.call("sq_linear_float_tile", sq.byref(dev), rows, 256, sq.FLOAT32_ROWS, sq.byref(tile))
+        assert tile.value == want, rows
+    rows = 64
+    f32 = sq.Segment(_fake(64 * 2112 * 4), sq.Buffer(), sq.Buffer(), 64, 2112, 0, sq.FLOAT32_ROWS)
+    io = _fake(rows * 2112 * 4)
+    with pytest.raises(sq.InvalidArgument, match="multiples of 256"):
+        sq.call("sq_float_add", None, io, sq.byref(f32), io, rows, 64, 0, sq.OUTPUT_F32,
+                sq.FLOAT_TILE_NEURAL_ACCELERATOR)
+    with pytest.raises(sq.InvalidArgument, match="unknown float tile"):
+        sq.call("sq_float_add", None, io, sq.byref(f32), io, rows, 64, 0, sq.OUTPUT_F32, 2)
+    # the MoE policy takes its router tile from the same rule
+    shape = sq.MoeShape(2048, 128, 8, 768, sq.FMT_AF4G64, sq.ROUTER_SOFTMAX, 0, 0)
+    for rows, phase in ((512, sq.PHASE_PREFILL), (16, sq.PHASE_DECODE)):
+        config = sq.MoeConfig()
+        sq.call("sq_moe_config_for", sq.byref(shape), rows, phase, sq.byref(config))
+        sq.call("sq_linear_float_tile", sq.byref(dev), rows, 128, sq.FLOAT32_ROWS, sq.byref(tile))
+        assert config.router_tile == tile.value
+
+
+@pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (27648, 5120)])
+def test_decode_storage_rows_match_every_plan(n, k):
+    """Linear::decodeStorageRows is the storage_rows of every decode plan of its rows, whatever the epilogue, and of
+    the lane plans (lanes x 8 rows)."""
+    dev, out = sq.device(), sq.c_uint32()
+    proj = sq.projection(seg(n, k))
+    for rows in range(1, 33):
+        sq.call("sq_linear_decode_storage_rows", sq.byref(dev), rows, n, k, sq.byref(out))
+        for e in (sq.EPILOGUE_NONE, sq.EPILOGUE_RESIDUAL, sq.EPILOGUE_GATE_UP):
+            assert sq.plan_for(sq.decode_workload(n, k, rows, e)).storage_rows == out.value, (rows, e)
+        assert sq.plan_for(sq.decode_workload(n, k, rows), proj).storage_rows == out.value
+    for lanes in range(1, 5):
+        plan = sq.LinearPlan()
+        sq.call("sq_linear_decode_plan", sq.byref(dev), sq.byref(proj), lanes, sq.EPILOGUE_NONE, None, sq.byref(plan))
+        sq.call("sq_linear_decode_storage_rows", sq.byref(dev), 8 * lanes, n, k, sq.byref(out))
+        assert plan.storage_rows == out.value
+    with pytest.raises(sq.InvalidArgument, match="invalid linear decode workload"):
+        sq.call("sq_linear_decode_storage_rows", sq.byref(dev), 33, n, k, sq.byref(out))
+
+
+@pytest.mark.parametrize("n,k", [(14336, 4096), (4096, 14336), (27648, 5120), (5120, 27648), (8192, 3072)])
+def test_prefill_scratch_size_covers_every_chunk(n, k):
+    """Linear::prefillScratchSize bounds the scratch of every prefill chunk of 1..2048 rows, the halved-K partials of
+    the row bands that halve included (the reference's arenas are sized from it)."""
+    dev, bound = sq.device(), sq.LinearScratchSize()
+    sq.call("sq_linear_prefill_scratch_size", sq.byref(dev), n, k, sq.byref(bound))
+    halved = 0
+    for rows in range(1, 2049):
+        size, _ = sq.scratch_size(sq.plan_for(sq.prefill_workload(n, k, rows)))
+        for f in ("input", "sums", "partials", "counters"):
+            assert getattr(size, f) <= getattr(bound, f), (rows, f)
+        halved += size.partials > 0 and rows > 32
+    if (n, k) == (14336, 4096):
+        assert halved == 256 and bound.partials == 2 * 512 * 14336 * 4   # rows 257..512
+
+
+def test_moe_add_routes_refusals():
+    """MoE::addRoutes validates on the host before any launch: the shape, the rows, the router's rows, the buffers'
+    sizes and alignment, and the tile."""
+    shape = sq.MoeShape(2048, 128, 8, 768, sq.FMT_AF4G64, sq.ROUTER_SOFTMAX, 0, 0)
+    rows = 16
+    x, scores = _fake(rows * 2048 * 2), _fake(rows * 256 * 4, 1 << 24)
+    sel, wts = _fake(rows * 8 * 4, 1 << 25), _fake(rows * 8 * 4, 1 << 26)
+    router = sq.Segment(_fake(128 * 2048 * 4, 1 << 27), sq.Buffer(), sq.Buffer(), 128, 2048, 0, sq.FLOAT32_ROWS)
+    call = lambda **kw: sq.call("sq_moe_add_routes", None, kw.get("x", x), sq.byref(kw.get("router", router)),
+                                sq.Buffer(), kw.get("scores", scores), kw.get("sel", sel), kw.get("wts", wts),
+                                kw.get("rows", rows), sq.byref(kw.get("shape", shape)), kw.get("tile", 0))
+    with pytest.raises(sq.InvalidArgument, match="router scores"):
+        call(scores=_fake(rows * 128 * 4, 1 << 24))
+    with pytest.raises(sq.InvalidArgument, match="selected experts"):
+        call(sel=_fake(rows * 4, 1 << 25))
+    with pytest.raises(sq.InvalidArgument, match="routing weights"):
+        call(wts=_fake(rows * 4, 1 << 26))
+    with pytest.raises(sq.InvalidArgument, match="invalid MoE routing rows"):
+        call(rows=0)
+    with pytest.raises(sq.InvalidArgument, match="router does not match"):
+        call(router=sq.Segment(_fake(64 * 2048 * 4, 1 << 27), sq.Buffer(), sq.Buffer(), 64, 2048, 0, sq.FLOAT32_ROWS))
+    with pytest.raises(sq.InvalidArgument, match="invalid MoE routing shape"):
+        call(shape=sq.MoeShape(2048, 128, 8, 768, sq.FMT_AF4G64, sq.ROUTER_SOFTMAX, 1, 0))
+    with pytest.raises(sq.InvalidArgument, match="16-byte aligned"):
+        call(x=_fake(rows * 2048 * 2, (1 << 20) + 8))
+    with pytest.raises(sq.InvalidArgument, match="router tile"):
+        call(tile=2)
 
 
 def test_static_scratch_entry_point_refusals():

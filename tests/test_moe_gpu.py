@@ -347,6 +347,47 @@ def test_moe_router_projection():
     assert np.linalg.norm(err) / np.linalg.norm(want) <= 1e-2
 
 
+@pytest.mark.parametrize("router_rows,tile", [(False, sq.FLOAT_TILE_SIMDGROUP), (True, sq.FLOAT_TILE_SIMDGROUP),
+                                              (True, sq.FLOAT_TILE_NEURAL_ACCELERATOR)])
+def test_moe_add_routes(router_rows, tile):
+    """MoE::addRoutes on its own (no plan, no grouping): with router rows it projects the input into the caller's
+    scores (within the fp32 accumulation bound of fp64, on either float tile), then writes each row's top-k experts
+    and its gated shared slice into the caller's selected and weight buffers: the selection bit for bit the oracle's
+    on those scores, the weights within fp32 rounding; without router rows it routes the scores the caller wrote."""
+    t = torch()
+    rng = np.random.default_rng(909 + 2 * router_rows + tile)
+    experts, hidden, top_k, rows = 64, 512, 6, 70
+    block = Block(rng, experts, hidden, 128, shared=1, gated=True)
+    shape = block.shape(top_k)
+    width = sq.lib().sq_moe_router_width(sq.byref(shape))
+    x = synthetic.activations(rng, rows, hidden)
+    scores = np.full((rows, width), np.nan, np.float32)
+    scores[:, :experts] = synthetic.router_logits(rng, rows, experts)
+    scores_dev = to_device(scores)
+    per_row = top_k + 1
+    selected_dev = t.full((rows * per_row,), -1, dtype=t.int32, device="cuda")
+    weights_dev = t.full((rows * per_row,), float("nan"), dtype=t.float32, device="cuda")
+    gate_dev = to_device(block.scalar_gate)
+    router = sq.Segment()
+    if router_rows:
+        rr = rng.normal(0, 0.05, (experts, hidden)).astype(np.float32)
+        rr_dev = to_device(rr)
+        router = sq.Segment(sq.view(rr_dev), sq.view(None), sq.view(None), experts, hidden, 0, sq.FLOAT32_ROWS)
+    x_dev = to_device(x)
+    sq.call("sq_moe_add_routes", sq.stream_handle(), sq.view(x_dev), sq.byref(router), sq.view(gate_dev),
+            sq.view(scores_dev), sq.view(selected_dev), sq.view(weights_dev), rows, sq.byref(shape), tile)
+    t.cuda.synchronize()
+    got_scores = scores_dev.cpu().numpy()[:, :experts]
+    if router_rows:
+        exact, magnitude = oracle.float_rows_f64(x, rr)
+        assert np.all(np.abs(got_scores - exact) <= (hidden / 64 + 8) * 2.0 ** -24 * magnitude)
+    else:
+        assert np.array_equal(got_scores, scores[:, :experts])
+    selected, weights = block.route(x, got_scores, top_k)
+    assert np.array_equal(to_host(selected_dev, np.uint32).reshape(rows, per_row), selected)
+    np.testing.assert_allclose(weights_dev.cpu().numpy().reshape(rows, per_row), weights, rtol=2e-6, atol=1e-7)
+
+
 def test_moe_nan_score_rows():
     """Rows of NaN router scores (an upstream NaN through the router projection): a NaN never wins, an all-NaN row
     selects expert 0 at every rank as the reference's kernel does, every selected id stays a valid expert, and the

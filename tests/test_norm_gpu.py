@@ -74,6 +74,38 @@ def test_rms_norm_writes_prefill_table(width, rows):
     assert np.array_equal(sums.cpu().numpy(), want_scale)
 
 
+@pytest.mark.parametrize("scale", [1e-5, 1e-6, 1e-8])
+def test_norm_table_of_small_rows(scale):
+    """Norm weights of scale x U(0.25, 2) make output rows of that magnitude: the table the norm writes of them is the
+    oracle's bit for bit (scaled up into half's normal range, not left as half subnormals), and a prefill that takes
+    it keeps every output inside its fp64 interval, as good as the staged emulation."""
+    t = torch()
+    rng = np.random.default_rng(int(-np.log10(scale)))
+    rows, k, n = 96, 2048, 256
+    x = synthetic.activations(rng, rows, k)
+    w_bits = synthetic.bf16_bits(rng.uniform(0.25, 2.0, k).astype(np.float32) * np.float32(scale))
+    w = make_weights(rng, sq.FMT_AF4G64, n, k)
+    proj = sq.projection(w.segment())
+    plan = sq.plan_for(sq.prefill_workload(n, k, rows), proj)
+    normalized, table, sums, prepared = run_norm(x, to_device(w_bits), False, k, sq.LINEAR_INPUT_HALF_ROWS,
+                                                 plan.storage_rows)
+    out_bits = to_host(normalized, np.uint16)[:rows]
+    want_table, want_scale = oracle.half_rows(out_bits)
+    assert np.array_equal(to_host(table, np.uint16)[:rows], want_table)
+    assert np.array_equal(sums.cpu().numpy()[:rows], want_scale)
+    assert np.all(want_scale < 2.0 ** -10), "small rows are scaled up"
+    scratch = sq.LinearScratch(sq.view(table), sq.view(sums), sq.view(None), sq.view(None), sq.view(None))
+    got = t.zeros((plan.storage_rows, n), dtype=t.int16, device="cuda")
+    buffers = sq.LinearBuffers(sq.view(normalized), sq.view(got), sq.view(None), sq.view(None), scratch, prepared)
+    sq.call("sq_linear_add", sq.stream_handle(), ctypes.byref(buffers), ctypes.byref(proj), ctypes.byref(plan), None)
+    t.cuda.synchronize()
+    from helpers import check_projection, staged_reference
+    stats = check_projection(to_host(got, np.uint16)[:rows], out_bits, w, f"norm table x {scale}")
+    value, *_ = oracle.project_f64(out_bits, w.values)
+    ref = synthetic.bf16_to_f32(staged_reference(out_bits, w))
+    assert stats["rel_l2"] <= 1.10 * np.linalg.norm(ref - value) / np.linalg.norm(value) + 1e-6
+
+
 def test_prefill_takes_the_norm_table():
     """A prefill plan whose buffers say the scratch holds its input's table skips its own preparation: it gives the
     same bits as a prefill that prepares, even after the input rows are overwritten, and reports the table."""
@@ -107,12 +139,14 @@ def test_prefill_takes_the_norm_table():
     assert after.layout == sq.LINEAR_INPUT_HALF_ROWS and after.source.ptr == normalized2.data_ptr()
 
 
-@pytest.mark.parametrize("f32_rows,f32_out,rows,n", [(True, True, 37, 128), (False, True, 37, 128),
-                                                      (True, False, 37, 128), (True, True, 300, 128),
-                                                      (False, True, 2048, 128), (True, False, 97, 60)])
-def test_float_rows(f32_rows, f32_out, rows, n):
-    """37 rows run the lane chains, 64 and more the fp32 MFMA (32 x 32 tiles, ragged in rows and columns at 97 x 60);
-    both within the lane chains' rounding bound."""
+@pytest.mark.parametrize("f32_rows,f32_out,rows,n,tile", [
+    (True, True, 37, 128, None), (False, True, 37, 128, None), (True, False, 37, 128, None),
+    (True, True, 300, 128, None), (False, True, 2048, 128, None), (True, False, 97, 60, None),
+    (True, True, 13, 60, sq.FLOAT_TILE_NEURAL_ACCELERATOR), (False, False, 300, 128, sq.FLOAT_TILE_SIMDGROUP)])
+def test_float_rows(f32_rows, f32_out, rows, n, tile):
+    """The policy's tile (sq_linear_float_tile): 37 rows run the lane chains, 64 and more the fp32 MFMA (32 x 32 tiles,
+    ragged in rows and columns at 97 x 60); and each tile where the policy would take the other (the MFMA at 13 rows,
+    the lane chains at 300); all within the lane chains' rounding bound."""
     t = torch()
     rng = np.random.default_rng(51 + 2 * f32_rows + f32_out + rows)
     k, stride, offset = 2048, 136, 5
@@ -127,8 +161,13 @@ def test_float_rows(f32_rows, f32_out, rows, n):
         seg = sq.Segment(sq.view(w_dev), sq.view(None), sq.view(None), n, k, 0, sq.FMT_BF16)
     out = t.zeros((rows, stride), dtype=t.float32 if f32_out else t.int16, device="cuda")
     x_dev = to_device(x)
+    if tile is None:
+        chosen = ctypes.c_uint32()
+        sq.call("sq_linear_float_tile", ctypes.byref(sq.device()), rows, n, seg.format_id, ctypes.byref(chosen))
+        tile = chosen.value
+        assert tile == (sq.FLOAT_TILE_NEURAL_ACCELERATOR if rows >= 64 else sq.FLOAT_TILE_SIMDGROUP)
     sq.call("sq_float_add", sq.stream_handle(), sq.view(x_dev), ctypes.byref(seg), sq.view(out), rows, stride,
-            offset, sq.OUTPUT_F32 if f32_out else sq.OUTPUT_BF16)
+            offset, sq.OUTPUT_F32 if f32_out else sq.OUTPUT_BF16, tile)
     t.cuda.synchronize()
     exact, magnitude = oracle.float_rows_f64(x, w)
     host = out.cpu().numpy()

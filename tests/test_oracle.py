@@ -443,21 +443,41 @@ def test_rounded_once_to_bf16():
     assert not oracle.rounded_once_to_bf16(rounded + 1, exact).any()
 
 
-def test_half_rows_round_trip():
-    """The prefill table holds each row exactly: undoing the chunk order and the power of two gives the bf16 row
-    back; a row past half's range takes the smallest shift that brings it below 2^16."""
-    rng = np.random.default_rng(22)
-    x = rng.standard_normal((3, 128)).astype(np.float32)
-    x[2, 5] = 1.0e5
-    bits = _bf16(x)
-    table, scale = oracle.half_rows(bits)
-    assert scale.tolist() == [1.0, 1.0, 2.0]
-    back = np.empty((3, 128))
-    for v in range(16):
+def _undo_half_rows(table, scale):
+    rows, k = table.shape
+    back = np.empty((rows, k))
+    for v in range(k // 8):
         g, c = divmod(v, 4)
         back[:, 32 * g + 4 * c:32 * g + 4 * c + 4] = table[:, 8 * v:8 * v + 4].view(np.float16)
         back[:, 32 * g + 16 + 4 * c:32 * g + 20 + 4 * c] = table[:, 8 * v + 4:8 * v + 8].view(np.float16)
-    assert np.array_equal(back * scale[:, None], oracle.bf16_values(bits))
+    return back * scale.astype(np.float64)[:, None]
+
+
+def test_half_rows_round_trip():
+    """The prefill table holds each row exactly, at any magnitude: undoing the chunk order and the power of two gives
+    the bf16 row back, for rows of N(0,1), a 1e5 spike, N(0,1) x 1e-5, 1e-6, 1e-8 and 1e-30, bf16 subnormals and
+    zeros; each row's largest table value lies in [2^15, 2^16) (the zero and subnormal rows at the shift's floor,
+    -126). A down-only shift (rows kept as they are unless past 2^16) loses the small rows, so this pins the
+    direction."""
+    rng = np.random.default_rng(22)
+    x = rng.standard_normal((9, 128)).astype(np.float32)
+    x[2, 5] = 1.0e5
+    for r, s in ((3, 1e-5), (4, 1e-6), (5, 1e-8), (6, 1e-30)):
+        x[r] *= np.float32(s)
+    bits = _bf16(x)
+    bits[7] = rng.integers(0, 128, 128).astype(np.uint16) | (rng.integers(0, 2, 128).astype(np.uint16) << 15)
+    bits[8] = 0
+    table, scale = oracle.half_rows(bits)
+    assert np.array_equal(_undo_half_rows(table, scale), oracle.bf16_values(bits))
+    largest = np.abs(table.view(np.float16).astype(np.float64)).max(axis=1)
+    assert np.all((largest[:7] >= 2.0 ** 15) & (largest[:7] < 2.0 ** 16)), largest
+    assert np.all(scale[7:] == np.float32(2.0 ** -126))
+    assert scale[2] == np.float32(2.0 ** (16 - 15))          # 1e5 = 1.53 * 2^16
+    exponent = np.floor(np.log2(np.abs(oracle.bf16_values(bits[:2])).max(axis=1)))
+    assert np.array_equal(scale[:2], np.ldexp(1.0, (exponent - 15).astype(int)).astype(np.float32))
+    # The planted mistake: rows kept unscaled below 2^16 do not come back for the small rows.
+    values = oracle.bf16_values(bits[3:6])
+    assert not np.array_equal(values.astype(np.float16).astype(np.float64), values)
 
 
 def test_float_rows_exact_on_integers():

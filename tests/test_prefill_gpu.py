@@ -79,6 +79,39 @@ def test_prefill_sparse_inputs_past_half_range():
     check_projection(run_prefill([w], xb), xb, w, "prefill mixed")
 
 
+@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K])
+@pytest.mark.parametrize("scale", [1e-5, 1e-6, 1e-8, 1e-30])
+def test_prefill_small_rows(fmt, scale):
+    """Rows of N(0,1) x scale: the reference multiplies bf16 rows of any magnitude exactly (matmul2d takes them as
+    they are, gguf_linear.metal:36-55), so the table's row scale brings small rows up into half's normal range and
+    the outputs stay inside the fp64 interval, as good as the staged emulation's. Below ~6e-5 a row left unscaled
+    would enter the fp16 MFMA as half subnormals (1e-6: about a quarter of the outputs outside the interval)."""
+    rng = np.random.default_rng(80 + fmt)
+    n, k, rows = 512, 4096, 96
+    w = make_weights(rng, fmt, n, k)
+    x = synthetic.bf16_bits(synthetic.bf16_to_f32(dense_inputs(rng, rows, k)) * np.float32(scale))
+    what = f"prefill fmt {fmt} rows x {scale}"
+    stats = check_projection(run_prefill([w], x), x, w, what)
+    no_worse_than_staged(None, x, w, stats, what)
+
+
+def test_prefill_rows_of_every_magnitude_in_one_chunk():
+    """One chunk whose rows run from 1e-30 to 1e4 (a different row scale each, bf16 subnormals and a zero row
+    included): every row inside its interval, no worse than the staged emulation."""
+    rng = np.random.default_rng(85)
+    n, k, rows = 256, 2048, 40
+    w = make_weights(rng, oracle.FMT_AF4G64, n, k)
+    x = synthetic.bf16_to_f32(dense_inputs(rng, rows, k)).astype(np.float64)
+    x *= np.logspace(-30, 4, rows)[:, None]
+    xb = synthetic.bf16_bits(x.astype(np.float32))
+    xb[0] = rng.integers(0, 128, k).astype(np.uint16)          # bf16 subnormals
+    xb[1] = 0
+    out = run_prefill([w], xb)
+    assert not synthetic.bf16_to_f32(out[1]).any(), "a zero row projects to zeros"
+    stats = check_projection(out, xb, w, "prefill rows of every magnitude")
+    no_worse_than_staged(None, xb, w, stats, "prefill rows of every magnitude")
+
+
 @pytest.mark.parametrize("fmt", NEW_FORMATS)
 def test_prefill_new_formats_sparse_and_mixed(fmt):
     """Sparse +-1e5 inputs (past half's range: the row scale) through the format's prefill tile, and the format beside
@@ -183,6 +216,45 @@ def test_config2_prefill_shapes(n, k, rows):
     x = dense_inputs(rng, rows, k)
     out = run_prefill([w], x)
     check_sampled(out, x, w, f"config 2 {k}x{n} rows {rows}", rng)
+
+
+def test_config2_ragged_with_small_rows():
+    """Config 2's 4096 x 14336 at 2047 rows with rows scaled by 1e-5, 1e-6 and 1e-8 mixed in (the last 256-row tile
+    ragged): the sampled rows, the small ones among them, inside their fp64 intervals and no worse than staged."""
+    n, k, rows = 14336, 4096, 2047
+    w = shape_weights(oracle.FMT_AF4G64, n, k, n + k)
+    rng = np.random.default_rng(2047 + 5)
+    x = synthetic.bf16_to_f32(dense_inputs(rng, rows, k))
+    small = np.arange(3, rows, 97)
+    x[small] *= np.array([1e-5, 1e-6, 1e-8], np.float32)[np.arange(small.size) % 3][:, None]
+    xb = synthetic.bf16_bits(x)
+    out = run_prefill([w], xb)
+    pick = np.union1d(sampled_rows(rows, 24, rng), small[:12])
+    stats = check_projection(out[pick], xb[pick], w, "config 2 ragged with small rows")
+    no_worse_than_staged(None, xb[pick], w, stats, "config 2 ragged with small rows")
+
+
+def test_prefill_halving_depends_on_the_chunk_rows():
+    """Whether the prefill halves its tiles' K depends on the chunk's rows as well as the shape (4096 x 14336 halves
+    from 257 to 512 rows, not at 256), so a row's bits can differ between chunks of 256 and 257 rows; both lie
+    inside the row's fp64 interval, and their difference within two fp32 accumulation bounds of it."""
+    n, k = 14336, 4096
+    w = shape_weights(oracle.FMT_AF4G64, n, k, n + k)
+    proj = sq.projection(w.segment())
+    halved = lambda r: sq.scratch_size(sq.plan_for(sq.prefill_workload(n, k, r), proj))[0].partials > 0
+    assert not halved(256) and halved(257)
+    rng = np.random.default_rng(257)
+    x = dense_inputs(rng, 257, k)
+    whole, cut = run_prefill([w], x[:256]), run_prefill([w], x)[:256]
+    pick = np.arange(0, 256, 17)
+    check_projection(whole[pick], x[pick], w, "256 rows, whole K")
+    check_projection(cut[pick], x[pick], w, "257 rows, halved K")
+    value, magnitude, inputs, largest = oracle.project_f64(x[pick], w.values)
+    bound = 2 * oracle.projection_bound(magnitude, inputs, largest, True) + \
+        oracle.ulp_bf16(np.maximum(np.abs(value), 1e-30))
+    a = synthetic.bf16_to_f32(whole[pick]).astype(np.float64)
+    b = synthetic.bf16_to_f32(cut[pick]).astype(np.float64)
+    assert np.all(np.abs(a - b) <= bound)
 
 
 @pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K, oracle.FMT_Q6K, oracle.FMT_AF8G64])
