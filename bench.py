@@ -169,13 +169,18 @@ def stream_floor(torch, sq, nbytes: int, steps: int, warmup: int) -> dict:
         results[f"{workgroups}x{threads}"] = round(nbytes / sec / 1e9, 1)
     best = max(results, key=results.get)
 
-    def empty(i, stream):
-        sq.stream_read(ring, sink, 224, 1024, nbytes=16, stream=sq.c_void_p(stream))
-    dispatch_us = time_graph(torch, empty, steps, warmup) * 1e6
+    # The empty dispatch on several grids (the GEMV's 224 x 1024, 256 x 256 and 4096 x 512, and one wave): the
+    # kernel over one 16-byte vector, graph-replayed; the lowest is the floor the bound takes.
+    dispatch = {}
+    for workgroups, threads in ((224, 1024), (256, 256), (4096, 512), (1, 64)):
+        def empty(i, stream, workgroups=workgroups, threads=threads):
+            sq.stream_read(ring, sink, workgroups, threads, nbytes=16, stream=sq.c_void_p(stream))
+        dispatch[f"{workgroups}x{threads}"] = round(time_graph(torch, empty, steps, warmup) * 1e6, 3)
+    dispatch_us = min(dispatch.values())
     del ring, sink
     torch.cuda.empty_cache()
     return {"GB/s": results[best], "launch": best, "bytes": nbytes, "by_launch": results,
-            "dispatch_floor_us": round(dispatch_us, 3),
+            "dispatch_floor_us": dispatch_us, "dispatch_floor_by_grid_us": dispatch,
             "bound_us": round(dispatch_us + nbytes / (HBM_PEAK_GBS * 1e3), 3)}
 
 
@@ -197,25 +202,34 @@ def mfma_ceiling(torch, sq, steps: int, warmup: int) -> dict:
 
 
 class Gemv:
-    """A decode projection over a weight ring; launch(i, stream) dispatches step i on ring copy i % copies."""
+    """A decode projection over a weight ring; launch(i, stream) dispatches step i on ring copy i % copies. With
+    `gate_up`, each step is the one-pass gate/up pair of the reference's decode FFN (LinearGguf.cpp:686-694): a gate
+    and an up tensor of the shape, bf16(up) silu(bf16(gate)) out."""
 
-    def __init__(self, torch, sq, synthetic, fmt, m, n, k, seed=1):
-        one = weight_bytes(sq, fmt, n, k)
+    def __init__(self, torch, sq, synthetic, fmt, m, n, k, seed=1, gate_up=False):
+        one = weight_bytes(sq, fmt, n, k) * (2 if gate_up else 1)
         self.copies = max(1, -(-RING_BYTES // one))
         self.weights = Projection(torch, sq, synthetic, fmt, n, k, seed, self.copies)
         self.projs = [self.weights.projection(sq, c) for c in range(self.copies)]
-        self.plan = sq.plan_for(sq.decode_workload(n, k, m), self.projs[0])
+        self.gates = [None] * self.copies
+        epilogue = sq.EPILOGUE_NONE
+        if gate_up:
+            self.gate_weights = Projection(torch, sq, synthetic, fmt, n, k, seed + 100, self.copies)
+            self.gates = [self.gate_weights.projection(sq, c) for c in range(self.copies)]
+            epilogue = sq.EPILOGUE_GATE_UP
+        self.plan = sq.plan_for(sq.decode_workload(n, k, m, epilogue), self.projs[0], self.gates[0])
         self.scratch = sq.Scratch(self.plan)
         self.x = torch.from_numpy(synthetic.activations(np.random.default_rng(seed + 1), m, k).view(np.int16)).cuda()
         self.out = torch.empty((m, n), dtype=torch.int16, device="cuda")
-        self.bufs = sq.LinearBuffers(sq.view(self.x), sq.view(self.out), sq.view(None), sq.view(None),
+        self.bufs = sq.LinearBuffers(sq.view(self.x), sq.view(self.out), sq.view(None), sq.view(self.scratch.gate),
                                      self.scratch.struct())
         self.sq = sq
 
     def launch(self, i, stream):
         sq = self.sq
+        gate = self.gates[i % self.copies]
         sq.call("sq_linear_add", sq.c_void_p(stream), sq.byref(self.bufs), sq.byref(self.projs[i % self.copies]),
-                sq.byref(self.plan), None)
+                sq.byref(self.plan), sq.byref(gate) if gate is not None else None)
 
 
 def bench_gemv(torch, sq, synthetic, fmt, m, n, k, steps, warmup, seed=1):
@@ -310,7 +324,11 @@ def cpu_baseline(sq, synthetic, budget_s: float) -> dict:
     the headline figure as `value` and every config beside it."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import sq_oracle as oracle
-    threads = min(os.cpu_count() or 1, 16)   # this GPU's share of the box's cores
+    # A one-GPU box hands its GPU 16 of the host's hardware threads (its CPU share, the thread pools' limit there);
+    # the pool takes all the threads this process may use, up to that share.
+    host_threads = os.cpu_count() or 1
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else host_threads
+    threads = min(usable, 16)
     pool = oracle.CpuPool(threads)
     rng = np.random.default_rng(1)
     weights = {}
@@ -372,19 +390,29 @@ def cpu_baseline(sq, synthetic, budget_s: float) -> dict:
     out = {"value": head["GB/s"], "unit": "GB/s", "cores": pool.threads, "kind": "port",
            "sample": f"best of {head['runs']} runs of the M=1 K4096xN14336 af4g64 GEMV (BASELINE config 1) on "
                      f"{pool.threads} threads ({pool.isa}); oracle/sq_cpu.c",
-           "isa": pool.isa, "cpu": _cpu_model(), "configs": configs}
+           "isa": pool.isa, "cpu": _cpu_model(), "host_threads": host_threads, "usable_threads": usable,
+           "threads_used": pool.threads, "configs": configs}
     pool.close()
     return out
 
 
 def _cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it: model name, family/model/stepping, and whether it reports AVX-512
+    BF16."""
+    fields = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                key, value = (part.strip() for part in line.split(":", 1))
+                fields.setdefault(key, value)
+            elif fields:
+                break
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    flags = fields.get("flags", "").split()
+    return (f"{fields.get('model name', 'unknown')} (family {fields.get('cpu family', '?')}, model "
+            f"{fields.get('model', '?')}, stepping {fields.get('stepping', '?')}; "
+            f"avx512_bf16 {'yes' if 'avx512_bf16' in flags else 'no'})")
 
 
 def main() -> int:
@@ -423,7 +451,22 @@ def main() -> int:
     del headline
     torch.cuda.empty_cache()
     floor = stream_floor(torch, sq, int(gemv_bytes(m, n, k)), args.steps, args.warmup)
-    log(f"  stream floor over the same bytes: {floor['GB/s']} GB/s ({floor['launch']})")
+    log(f"  stream floor over the same bytes: {floor['GB/s']} GB/s ({floor['launch']}); empty dispatch "
+        f"{floor['dispatch_floor_by_grid_us']} us")
+    # The reference's decode form of this shape: gate and up in one pass (LinearGguf.cpp:686-694), two tensors'
+    # planes (66 MB) a launch, bf16(up) silu(bf16(gate)) out.
+    pair = Gemv(torch, sq, synthetic, sq.FMT_AF4G64, m, n, k, gate_up=True)
+    pair_sec = time_graph(torch, pair.launch, args.steps, args.warmup)
+    pair_bytes = 2 * n * k * 0.5625 + 2 * m * k + 2 * m * n
+    pair_floor = stream_floor(torch, sq, int(pair_bytes), args.steps, args.warmup)
+    gate_up_pair = {"us": round(pair_sec * 1e6, 2), "GB/s": round(pair_bytes / pair_sec / 1e9, 1),
+                    "hbm_frac": round(pair_bytes / pair_sec / 1e9 / HBM_PEAK_GBS, 4), "bytes": int(pair_bytes),
+                    "one_pass": bool(pair.plan.config.one_gate_up_pass), "splits": pair.plan.config.splits,
+                    "stream_floor_GB/s": pair_floor["GB/s"],
+                    "frac_of_floor": round(pair_bytes / pair_sec / 1e9 / pair_floor["GB/s"], 3)}
+    log(f"  gate/up pair K{k} N{n}: {pair_sec * 1e6:.2f} us, {gate_up_pair['GB/s']} GB/s")
+    del pair
+    torch.cuda.empty_cache()
     if args.calibrate_copy:
         # A plain device copy of known size for scaling the FETCH_SIZE / WRITE_SIZE counters.
         src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
@@ -446,13 +489,15 @@ def main() -> int:
         # The small shapes' floors: the streaming kernel over each M=1 point's own bytes (best launch shape) and the
         # empty dispatch, timed alike. Below ~10 MB a dispatch's fixed cost is most of its time.
         for (kk, nn) in ((4096, 4096), (4096, 1024)):
-            point = sweep[f"K{kk}xN{nn}_M1"]
             f = stream_floor(torch, sq, int(gemv_bytes(1, nn, kk)), max(50, args.steps // 2), 10)
-            point["stream_floor_us"] = round(gemv_bytes(1, nn, kk) / f["GB/s"] / 1e3, 2)
-            point["dispatch_floor_us"] = f["dispatch_floor_us"]
-            point["frac_of_floor"] = round(point["stream_floor_us"] / point["us"], 3)
-            log(f"  stream floor K{kk} N{nn}: {point['stream_floor_us']} us ({f['launch']}), "
-                f"dispatch {f['dispatch_floor_us']} us")
+            for mm in (1, 8, 16):
+                # Each point's own bytes at the rate the streaming kernel reaches over this shape's.
+                point = sweep[f"K{kk}xN{nn}_M{mm}"]
+                point["stream_floor_us"] = round(gemv_bytes(mm, nn, kk) / f["GB/s"] / 1e3, 2)
+                point["dispatch_floor_us"] = f["dispatch_floor_us"]
+                point["frac_of_floor"] = round(point["stream_floor_us"] / point["us"], 3)
+            log(f"  stream floor K{kk} N{nn}: {sweep[f'K{kk}xN{nn}_M1']['stream_floor_us']} us ({f['launch']}), "
+                f"dispatch {f['dispatch_floor_by_grid_us']} us")
         extra["c1_decode_sweep_af4g64"] = sweep
     if "prefill" in sections:
         ceiling = mfma_ceiling(torch, sq, args.steps, args.warmup)
@@ -552,6 +597,7 @@ def main() -> int:
                      "kernel": "column_kernel<af4g64, 1 row>", "launch_us": round(sec * 1e6, 3),
                      "algorithmic_bytes": int(gemv_bytes(m, n, k))},
         "stream_floor": dict(floor, frac_of_floor=round(gbs / floor["GB/s"], 3)),
+        "c1_gate_up_pair": gate_up_pair,
     }
     result.update(extra)
     if "cpu" in sections:

@@ -34,21 +34,30 @@
 namespace sq::kern {
 namespace {
 
-constexpr int BK = 64, kWaves = 4, kThreads = 64 * kWaves, kStages = 3;
+constexpr int BK = 64, kStages = 3;
 constexpr int kRowBytes = BK * 2;                  // one LDS activation row: 64 fp16
 constexpr int kLdsLimit = 160 * 1024;              // LDS a workgroup may hold
-// A wave's LDS slot for one step of its plane tile: the step's two groups of codes (64 columns x P0 bytes each), their
-// plane1 bits (64 x P1 each), then the meta the step reads (its meta unit, or both groups' units of a format with a
-// unit a group). Each part lies in the planes as in the slot, so it arrives by whole 16-byte or dword copies. The
-// 4-bit formats without plane1 keep 1 KiB for the meta.
+// A workgroup of W waves computes BM rows x 256 columns (four plane tiles): W = 4, one wave a SIMD, each owning a
+// 64-column plane tile; or W = 8, two waves a SIMD, each owning one half (32 columns) of a plane tile, so that one
+// wave's dependency and LDS stalls are covered by the other's work.
+// Formats whose codes are 16 bytes a column-group and who have no plane1 (4-bit affine and Q4_K) run W = 8.
 template <uint32_t FMT>
+constexpr int tile_waves() { return Fmt<FMT>::P0 == 16 && Fmt<FMT>::P1 == 0 ? 8 : 4; }
+// A wave's LDS slot for one step: the step's two groups of the wave's codes (its 256 / W columns x P0 bytes each),
+// their plane1 bits (P1 each), then the meta the step reads for the whole plane tile (its meta unit, or both groups'
+// units of a format with a unit a group). Each part lies in the planes as in the slot, so it arrives by whole 16-byte
+// or dword copies. With four waves the 4-bit formats without plane1 keep 1 KiB for the meta.
+template <uint32_t FMT, int W>
 struct StepSlot {
   using F = Fmt<FMT>;
-  static constexpr int code = 2 * 64 * F::P0, high = 2 * 64 * F::P1;
+  static constexpr int cols = 256 / W;            // the wave's columns of its plane tile
+  static constexpr int plane_step = 2 * 64 * F::P0, plane_high_step = 2 * 64 * F::P1;   // a tile's step in the planes
+  static constexpr int code = 2 * cols * F::P0, high = 2 * cols * F::P1;
   static constexpr int meta = (F::UNIT == 1 ? 2 : 1) * 64 * F::META;
   static constexpr int high_at = code, meta_at = code + high;
-  static constexpr int wave = meta_at + (F::P0 == 16 && F::P1 == 0 ? 1024 : (meta + 15) / 16 * 16);
-  static constexpr int all = kWaves * wave;       // the slot of every wave
+  static constexpr int wave =
+      meta_at + (W == 4 ? (F::P0 == 16 && F::P1 == 0 ? 1024 : (meta + 15) / 16 * 16) : (meta + 255) / 256 * 256);
+  static constexpr int all = W * wave;            // the slot of every wave
 };
 template <int BM> constexpr int stage_bytes() { return BM * kRowBytes; }
 template <int BM> constexpr int code_base() { return kStages * stage_bytes<BM>(); }
@@ -56,10 +65,10 @@ template <int BM> constexpr int code_base() { return kStages * stage_bytes<BM>()
 // or three where four do not fit beside a 256-row tile's stages. Then step s's copies of step s + 3 go to step s's
 // own slot, which the wave finished reading (into registers, its LDS reads waited for) and rewriting in place
 // (step_coefficients) during step s - 1; nothing reads it during step s.
-template <uint32_t FMT, int BM>
-constexpr int step_slots() { return code_base<BM>() + 4 * StepSlot<FMT>::all <= kLdsLimit ? 4 : 3; }
-template <uint32_t FMT, int BM>
-constexpr int lds_bytes() { return code_base<BM>() + step_slots<FMT, BM>() * StepSlot<FMT>::all; }
+template <uint32_t FMT, int BM, int W>
+constexpr int step_slots() { return code_base<BM>() + 4 * StepSlot<FMT, W>::all <= kLdsLimit ? 4 : 3; }
+template <uint32_t FMT, int BM, int W>
+constexpr int lds_bytes() { return code_base<BM>() + step_slots<FMT, BM, W>() * StepSlot<FMT, W>::all; }
 
 // global -> LDS copy of SIZE bytes per lane (global_load_lds): lane l's bytes land at lds + SIZE l.
 // (The size is spelled as a literal: the host pass of hipcc does not take a template argument there.)
@@ -147,10 +156,12 @@ __device__ __forceinline__ uint32_t dequant_pair(float q0, float q1, Coef k) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{v0, v1}, half2));
 }
 // The slot position of column c's 16 bytes of 4-bit codes (and of a Q4_K or Q5_K column's 16-byte header) in a
-// step's LDS slot, an involution: lane l of the copy fetches column code_slot(l). Bit 2 of the column is flipped with
-// bit 4, so the sixteen columns column_of(j, t) that one read takes over j = 0..15 lie on sixteen different 16-byte
-// slots modulo 256 bytes: with the four words q, 64 banks conflict-free (32 banks two-way, the least for 32 lanes of
-// 4-byte reads) instead of four ways. Measured: LDS bank conflicts 23% -> 9% of the tile's LDS active cycles.
+// step's LDS slot, an involution on 0..63 and on 0..31: lane l of the copy fetches column code_slot(l). Bit 2 of the
+// column is flipped with bit 4, so the sixteen columns column_of(j, t) that one read takes over j = 0..15 lie on
+// sixteen different 16-byte slots modulo 256 bytes: with the four words q, 64 banks conflict-free (32 banks two-way,
+// the least for 32 lanes of 4-byte reads) instead of four ways. Measured: LDS bank conflicts 23% -> 9% of the tile's
+// LDS active cycles. (A half tile's 32 columns, 8 a + 4 t + b, keep the property: bits 3 and 2 ^ 4 of the slot take
+// four values over a for each t.)
 __device__ __forceinline__ uint32_t code_slot(uint32_t c) { return c ^ ((c >> 2) & 4u); }
 // The plane tile column whose weights lane j of the MFMA's A operand carries in column block t. The product runs
 // weights x activations (D = W X^T), so lane (j', q) of D holds column column_of(4q + i, t) for i = 0..3: with
@@ -222,49 +233,61 @@ __device__ __forceinline__ void step_coefficients(uint8_t *meta, uint32_t step, 
   }
 }
 
-// The dequantisation of one group's four plane words as a sequence of micro-operations: kind 0 prepares word arg
-// (masks, coefficients), kinds 1, 2, 3 convert, multiply-add and pack weight pair arg (word arg / 4). Pairs are
-// software pipelined: pair i's conversion comes after pair i - 1's multiply-add and pair i - 2's pack.
+// The dequantisation of one group's NT plane words (one a column block of the wave) as a sequence of
+// micro-operations: kind 0 prepares word arg (masks, coefficients), kinds 1, 2, 3 convert, multiply-add and pack
+// weight pair arg (word arg / 4). Pairs are software pipelined: pair i's conversion comes after pair i - 1's
+// multiply-add and pair i - 2's pack.
 struct Micro {
   int kind, arg;
 };
-constexpr int kMicro = 4 + 3 * 16;
+template <int NT>
+constexpr int micro_ops() { return NT + 3 * 4 * NT; }
+template <int NT>
 struct MicroTable {
-  Micro op[kMicro];
+  Micro op[micro_ops<NT>()];
 };
-constexpr MicroTable make_micro_table() {
-  MicroTable t{};
+template <int NT>
+constexpr MicroTable<NT> make_micro_table() {
+  MicroTable<NT> t{};
   int n = 0;
-  for (int i = 0; i < 18; ++i) {
-    if (i < 16 && i % 4 == 0) t.op[n++] = {0, i / 4};
-    if (i < 16) t.op[n++] = {1, i};
-    if (i >= 1 && i <= 16) t.op[n++] = {2, i - 1};
+  for (int i = 0; i < 4 * NT + 2; ++i) {
+    if (i < 4 * NT && i % 4 == 0) t.op[n++] = {0, i / 4};
+    if (i < 4 * NT) t.op[n++] = {1, i};
+    if (i >= 1 && i <= 4 * NT) t.op[n++] = {2, i - 1};
     if (i >= 2) t.op[n++] = {3, i - 2};
   }
   return t;
 }
-constexpr MicroTable kMicroTable = make_micro_table();
-static_assert(kMicroTable.op[kMicro - 1].kind == 3 && kMicroTable.op[kMicro - 1].arg == 15, "52 micro-operations");
+template <int NT>
+constexpr MicroTable<NT> kMicroTable = make_micro_table<NT>();
+static_assert(kMicroTable<4>.op[micro_ops<4>() - 1].kind == 3 && kMicroTable<4>.op[micro_ops<4>() - 1].arg == 15,
+              "52 micro-operations for four words");
+static_assert(kMicroTable<2>.op[micro_ops<2>() - 1].kind == 3 && kMicroTable<2>.op[micro_ops<2>() - 1].arg == 7,
+              "26 micro-operations for two words");
 
 // SPLIT: the tile's K is cut between the two workgroups of blockIdx.z (steps [0, split_at) and [split_at, K / 64)),
 // whose fp32 sums a close dispatch adds (prefill_schedule).
-template <uint32_t FMT, uint32_t EP, int BM, bool SPLIT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_kernel(PrefillArgs a) {
+template <uint32_t FMT, uint32_t EP, int BM, bool SPLIT, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W / 4)))
+void prefill_kernel(PrefillArgs a) {
   using F = Fmt<FMT>;
-  using S = StepSlot<FMT>;
+  using S = StepSlot<FMT, W>;
+  static_assert(W == 4 || (W == 8 && F::P0 == 16 && F::P1 == 0), "eight waves take 16-byte codes and no plane1");
   constexpr int MI = BM / 16;                         // 16-row blocks of the wave
+  constexpr int NT = 16 / W;                          // 16-column blocks of the wave: 4 (a plane tile) or 2 (a half)
   static_assert(MI == 8 || MI == 16, "128- or 256-row tiles");
   constexpr int kStage = stage_bytes<BM>(), kCodeBase = code_base<BM>(), kSlotBytes = S::all;
-  constexpr int kSlots = step_slots<FMT, BM>();
+  constexpr int kSlots = step_slots<FMT, BM, W>();
   // The step's plane copies: the codes, plane1 and meta parts by 16-byte copies of 1 KiB and dword copies of 256 B.
   constexpr int kCode16 = S::code / 1024, kHigh16 = S::high / 1024, kHigh4 = S::high % 1024 / 256;
   constexpr int kMeta16 = S::meta / 1024, kMeta4 = S::meta % 1024 / 256;
-  static_assert(S::high % 256 == 0 && S::meta % 256 == 0, "whole dword copies");
+  static_assert(S::code % 1024 == 0 && S::high % 256 == 0 && S::meta % 256 == 0, "whole copies");
   constexpr int kBCopies = kCode16 + kHigh16 + kHigh4 + kMeta16 + kMeta4;
-  constexpr int kCopies = BM / 32 + kBCopies;        // copy instructions a wave issues per step
+  constexpr int kACopies = BM / (8 * W);              // activation copies (eight rows each) a wave issues per step
+  constexpr int kCopies = kACopies + kBCopies;        // copy instructions a wave issues per step
   static_assert(kCopies < 64, "vmcnt counts to 63");
-  static_assert(lds_bytes<FMT, BM>() <= kLdsLimit, "the tile's LDS fits a workgroup");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes<FMT, BM>()];
+  static_assert(lds_bytes<FMT, BM, W>() <= kLdsLimit, "the tile's LDS fits a workgroup");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes<FMT, BM, W>()];
   const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, q = lane >> 4;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t row0 = blockIdx.x * BM;
@@ -274,19 +297,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const uint32_t first = SPLIT && blockIdx.z ? a.split_at : 0;
   const uint32_t n = SPLIT ? (blockIdx.z ? steps - a.split_at : a.split_at) : steps;
 
-  // The wave's plane tile (the dispatch's column groups start at column_group0). A grid whose tile count is not a
-  // multiple of 4 ends short: a spare wave runs tile 0 of its segment and stores nothing.
-  uint32_t ptile = (a.column_group0 + blockIdx.y) * 4 + wave, s = 0;
+  // The wave's plane tile (the dispatch's column groups start at column_group0) and its half of it (eight waves).
+  // A grid whose tile count is not a multiple of 4 ends short: a spare wave runs tile 0 of its segment and stores
+  // nothing.
+  const uint32_t half = W == 8 ? (wave & 1u) : 0u;
+  uint32_t ptile = (a.column_group0 + blockIdx.y) * 4 + wave / (W / 4), s = 0;
   while (s + 1 < a.segments && ptile >= a.seg[s].tiles) ptile -= a.seg[s++].tiles;
   const bool live = ptile < a.seg[s].tiles;
   const Segment seg = a.seg[s];
-  // The lane's copy sources in the plane tile: 16-byte copies read 16 lane bytes on, dword copies 4 lane.
+  // The lane's copy sources in the plane tile: 16-byte copies read 16 lane bytes on, dword copies 4 lane. Four waves:
+  // code copy k is group k of the step, lane l column code_slot(l). Eight waves: one code copy a step, lane l group
+  // l / 32, column code_slot(l % 32) of the wave's half.
   const size_t tile = live ? ptile : 0;
   const size_t unit0 = F::UNIT == 1 ? 2 * first : 2 * first / F::UNIT;
-  const uint8_t *bplane =
-      seg.plane0 + (tile * G * 64 * F::P0 + (size_t)first * S::code + 16 * (F::P0 == 16 ? code_slot(lane) : lane));
-  const uint8_t *bhigh16 = F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + (size_t)first * S::high + 16 * lane) : nullptr;
-  const uint8_t *bhigh4 = F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + (size_t)first * S::high + 4 * lane) : nullptr;
+  const uint32_t code_lane = W == 8 ? (lane >> 5) * 1024 + (32 * half + code_slot(lane & 31)) * 16
+                                    : 16 * (F::P0 == 16 ? code_slot(lane) : lane);
+  const uint8_t *bplane = seg.plane0 + (tile * G * 64 * F::P0 + (size_t)first * S::plane_step + code_lane);
+  const uint8_t *bhigh16 =
+      F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + (size_t)first * S::plane_high_step + 16 * lane) : nullptr;
+  const uint8_t *bhigh4 =
+      F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + (size_t)first * S::plane_high_step + 4 * lane) : nullptr;
   const uint8_t *bmeta16 =
       seg.meta + ((tile * units + unit0) * 64 * F::META + 16 * (F::META == 16 ? code_slot(lane) : lane));
   const uint8_t *bmeta4 = seg.meta + ((tile * units + unit0) * 64 * F::META + 4 * lane);
@@ -295,13 +325,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   uint32_t mask = 0x0F0F0F0Fu;
   asm volatile("" : "+s"(mask));
 
-  // Activations: wave w copies LDS rows BM/4 w .. BM/4 (w + 1) - 1, eight per instruction: lane l fills chunk slot
+  // Activations: wave w copies LDS rows BM/W w .. BM/W (w + 1) - 1, eight per instruction: lane l fills chunk slot
   // l % 8 of row 8 i + l / 8, i.e. input chunk (l % 8) ^ (row % 8) (row % 8 = l / 8, the same for every i).
-  constexpr int kRowsPerWave = BM / kWaves;
+  constexpr int kRowsPerWave = BM / W;
   // Byte offsets of the lane's copy sources, rows clamped to the last live one (a tile past the rows reads it again).
-  uint32_t aoff[BM / 32];
+  uint32_t aoff[kACopies];
 #pragma unroll
-  for (int i = 0; i < BM / 32; ++i) {
+  for (int i = 0; i < kACopies; ++i) {
     const uint32_t r = min(row0 + kRowsPerWave * wave + 8 * i + (lane >> 3), a.rows - 1);
     aoff[i] = (r * a.K + 8 * ((lane & 7) ^ (lane >> 3))) * 2;
   }
@@ -310,7 +340,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const auto copy_a = [&](uint32_t step, uint32_t stage) __attribute__((always_inline)) {
     const uint8_t *from = xin + (size_t)min(step, n - 1) * BK * 2;
 #pragma unroll
-    for (int i = 0; i < BM / 32; ++i)
+    for (int i = 0; i < kACopies; ++i)
       copy_to_lds<16>(from + aoff[i], lds + stage * kStage + (kRowsPerWave * wave + 8 * i) * kRowBytes);
   };
   // Plane copy k of step `from` (clamped) into the wave's slot at dst: the codes' 1 KiB pieces, then plane1's and the
@@ -318,13 +348,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const auto copy_b_one = [&](uint32_t from, int k, uint8_t *dst) __attribute__((always_inline)) {
     const size_t meta = (size_t)(F::UNIT == 1 ? 2 * from : 2 * from / F::UNIT) * 64 * F::META;
     if (k < kCode16) {
-      copy_to_lds<16>(bplane + (size_t)from * S::code + 1024 * k, dst + 1024 * k);
+      copy_to_lds<16>(bplane + (size_t)from * S::plane_step + 1024 * k, dst + 1024 * k);
     } else if (k < kCode16 + kHigh16) {
       const int i = k - kCode16;
-      copy_to_lds<16>(bhigh16 + (size_t)from * S::high + 1024 * i, dst + S::high_at + 1024 * i);
+      copy_to_lds<16>(bhigh16 + (size_t)from * S::plane_high_step + 1024 * i, dst + S::high_at + 1024 * i);
     } else if (k < kCode16 + kHigh16 + kHigh4) {
       const int i = k - kCode16 - kHigh16;
-      copy_to_lds<4>(bhigh4 + (size_t)from * S::high + 1024 * kHigh16 + 256 * i,
+      copy_to_lds<4>(bhigh4 + (size_t)from * S::plane_high_step + 1024 * kHigh16 + 256 * i,
                      dst + S::high_at + 1024 * kHigh16 + 256 * i);
     } else if (k < kCode16 + kHigh16 + kHigh4 + kMeta16) {
       const int i = k - kCode16 - kHigh16 - kHigh4;
@@ -340,60 +370,62 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     for (int k = 0; k < kBCopies; ++k) copy_b_one(min(step, n - 1), k, wave_slot + slot * kSlotBytes);
   };
 
-  // Copy c of step `step`'s copies: c < BM / 32 the activation rows of step + 2, then step + 3's plane copies.
+  // Copy c of step `step`'s copies: c < kACopies the activation rows of step + 2, then step + 3's plane copies.
   const auto copy_one = [&](uint32_t step, int c) __attribute__((always_inline)) {
-    if (c < BM / 32) {
+    if (c < kACopies) {
       const uint8_t *from = xin + (size_t)min(step + 2, n - 1) * BK * 2;
       uint8_t *stage = lds + ((step + 2) % kStages) * kStage;
       copy_to_lds<16>(from + aoff[c], stage + (kRowsPerWave * wave + 8 * c) * kRowBytes);
       return;
     }
-    copy_b_one(min(step + 3, n - 1), c - BM / 32, wave_slot + ((step + 3) % kSlots) * kSlotBytes);
+    copy_b_one(min(step + 3, n - 1), c - kACopies, wave_slot + ((step + 3) % kSlots) * kSlotBytes);
   };
 
-  f32x4 acc[MI][4];
+  f32x4 acc[MI][NT];
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ni = 0; ni < NT; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
   // Weight fragments (the MFMA's A operand): wq[h][t] = group h of the step, column block t. Group 0 serves the first
   // half of a step's MFMAs while group 1 is dequantised into wq[1], then group 1 serves the second half while the
   // next step's group 0 is dequantised into wq[0]; each register set has one role, so the step loop needs no
   // unrolling.
-  u32x4 wq[2][4];
+  u32x4 wq[2][NT];
   // The plane words (8-bit codes: two words, cw and cw1), plane1 bits and meta of group h of a step for the lane's
-  // four columns, out of the step's slot: chunk q of the column (its codes of inputs 4q..4q+3 and 16+4q..19+4q).
-  uint32_t cw[2][4], cw1[2][4], hb[2][4];
-  MetaWords mw[2][4];
+  // NT columns, out of the step's slot: chunk q of the column (its codes of inputs 4q..4q+3 and 16+4q..19+4q). The
+  // meta block holds the whole plane tile, the codes the wave's columns.
+  uint32_t cw[2][NT], cw1[2][NT], hb[2][NT];
+  MetaWords mw[2][NT];
   const auto read_b = [&](uint32_t slot, int h) __attribute__((always_inline)) {
     const uint8_t *src = wave_slot + slot * kSlotBytes;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < NT; ++t) {
       const uint32_t c = column_of(j, t);
       if constexpr (F::P0 == 32) {
         const u32x2 v = *(const u32x2 *)(src + h * 2048 + c * 32 + q * 8);
         cw[h][t] = v[0];
         cw1[h][t] = v[1];
       } else {
-        cw[h][t] = *(const uint32_t *)(src + h * 1024 + code_slot(c) * 16 + q * 4);
+        cw[h][t] = *(const uint32_t *)(src + h * (S::code / 2) + code_slot(c) * 16 + q * 4);
       }
       if constexpr (F::P1 == 4) hb[h][t] = src[S::high_at + h * 256 + c * 4 + q];
       if constexpr (F::P1 == 8) hb[h][t] = *(const uint16_t *)(src + S::high_at + h * 512 + c * 8 + 2 * q);
-      mw[h][t] = slot_meta<FMT>(src + S::meta_at, c, h);
+      mw[h][t] = slot_meta<FMT>(src + S::meta_at, S::cols * half + c, h);
     }
   };
-  // The dequantisation of one group's four words runs as 52 micro-operations (see micro_op) spread one or two
+  // The dequantisation of one group's NT words runs as 13 NT micro-operations (see micro_op) spread one or two
   // after each MFMA: prep(t) masks word t and derives its coefficients, then every pair of weights p (word p / 4,
   // fragment register p % 4) is converted (C), multiplied and added (F) and packed to fp16 (P), software
   // pipelined so that no micro-operation waits on the one just before it.
   // 4-bit codes: lo holds the word's slots 0, 4, 1, 5 and hi its slots 2, 6, 3, 7, one a byte, so pair r (slots 2r,
   // 2r + 1) is bytes r / 2 and r / 2 + 2 of hi (r odd) or lo; plane1 bits go to bits 4 (and 5) of those bytes.
   // 8-bit codes: lo and hi are the two words, pair r bytes 2 (r % 2) and 2 (r % 2) + 1 of word r / 2.
-  uint32_t lo[4], hi[4];
-  Coef kw[4], kw2[4];
+  uint32_t lo[NT], hi[NT];
+  Coef kw[NT], kw2[NT];
   float cf[4][2], vf[4][2];
+  constexpr int kMicro = micro_ops<NT>();
   const auto micro = [&](int u, uint32_t step, int h) __attribute__((always_inline)) {
-    const Micro m = kMicroTable.op[u];
+    const Micro m = kMicroTable<NT>.op[u];
     if (m.kind == 0) {
       const int t = m.arg;
       if constexpr (F::P0 == 32) {
@@ -467,7 +499,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   // With copies to LDS outstanding the compiler can only wait for all LDS reads at once, so each batch waits for
   // its own reads (issued a batch earlier) before it issues the next batch's. A step's last batch runs after the
   // barrier, while the next step's first reads are in flight.
-  constexpr int kGroups = 2 * MI, kBatch = 4, kBatches = kGroups / kBatch, kSlotsHalf = 4 * MI;
+  constexpr int kGroups = 2 * MI, kBatch = 4, kBatches = kGroups / kBatch, kSlotsHalf = NT * MI;
   constexpr int kWaitLds = 0xC07F;   // s_waitcnt lgkmcnt(0), the other counters at their maximum
   u32x4 fa[2][kBatch];
   const auto read_batch = [&](uint32_t step, int b) __attribute__((always_inline)) {
@@ -483,11 +515,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     for (int i = 0; i < kBatch; ++i) {
       const int g = b * kBatch + i, kk = g / MI, mi = g % MI;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
+      for (int t = 0; t < NT; ++t) {
         acc[mi][t] = mfma_f16(wq[kk][t], fa[b & 1][i], acc[mi][t]);
         // This MFMA's share of the other group's micro-operations: slot s of the half runs micro-operations
         // [s kMicro / S, (s + 1) kMicro / S).
-        const int slot = mi * 4 + t, u0 = slot * kMicro / kSlotsHalf, u1 = (slot + 1) * kMicro / kSlotsHalf;
+        const int slot = mi * NT + t, u0 = slot * kMicro / kSlotsHalf, u1 = (slot + 1) * kMicro / kSlotsHalf;
         static_assert(kMicro <= 2 * kSlotsHalf, "at most two micro-operations a slot");
         if (u0 < u1) micro(u0, kk == 0 ? step : step + 1, kk ^ 1);
         if (u0 + 1 < u1) micro(u0 + 1, kk == 0 ? step : step + 1, kk ^ 1);
@@ -526,18 +558,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const size_t plane = (size_t)a.rows * a.split_columns;
     uint16_t *const high = (uint16_t *)a.partials + blockIdx.z * 2 * plane;
     uint16_t *const low = high + plane;
-    const uint32_t col0 = (blockIdx.y * 4 + wave) * 64 + 8 * q;
+    const uint32_t col0 = (blockIdx.y * 4 + wave / (W / 4)) * 64 + S::cols * half + 8 * q;
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
       const uint32_t r = row0 + mi * 16 + j;
       if (r >= a.rows) continue;
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const size_t at = (size_t)r * a.split_columns + col0 + 32 * half;
+      for (int hh = 0; hh < NT / 2; ++hh) {
+        const size_t at = (size_t)r * a.split_columns + col0 + 32 * hh;
         u32x4 hi, lo;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const f32x4 &v = acc[mi][2 * half + (e >> 1)];
+          const f32x4 &v = acc[mi][2 * hh + (e >> 1)];
           const uint32_t b0 = __float_as_uint(v[2 * (e & 1)]), b1 = __float_as_uint(v[2 * (e & 1) + 1]);
           hi[e] = __builtin_amdgcn_perm(b1, b0, 0x07060302u);
           lo[e] = __builtin_amdgcn_perm(b1, b0, 0x05040100u);
@@ -548,24 +580,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     }
     return;
   }
-  // Epilogue: lane (j, q) holds row 16 mi + j of each row block at columns 8q..8q+7 (blocks 0, 1) and
-  // 32+8q..32+8q+7 (blocks 2, 3) of the plane tile: two 16-byte stores a row block.
+  // Epilogue: lane (j, q) holds row 16 mi + j of each row block at columns 8q..8q+7 of the wave's columns (blocks
+  // 0, 1) and, with four column blocks, 32+8q..32+8q+7 (blocks 2, 3): one 16-byte store a row block and pair of
+  // column blocks.
   if (!live) return;
-  const uint32_t col0 = seg.out_offset + ptile * 64 + 8 * q;
+  const uint32_t col0 = seg.out_offset + ptile * 64 + S::cols * half + 8 * q;
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
     const uint32_t r = row0 + mi * 16 + j;
     if (r >= a.rows) continue;
     const float scale = a.row_scale[r];
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const size_t at = (size_t)r * a.out_stride + col0 + 32 * half;
+    for (int hh = 0; hh < NT / 2; ++hh) {
+      const size_t at = (size_t)r * a.out_stride + col0 + 32 * hh;
       u32x4 aux = {0u, 0u, 0u, 0u};
       if constexpr (EP != EpNone) aux = *(const u32x4 *)(a.aux + at);
       u32x4 out;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const f32x4 &v = acc[mi][2 * half + (e >> 1)];
+        const f32x4 &v = acc[mi][2 * hh + (e >> 1)];
         const float lo = epilogue_bits<EP>(v[2 * (e & 1)] * scale, aux[e] & 0xFFFFu);
         const float hi = epilogue_bits<EP>(v[2 * (e & 1) + 1] * scale, aux[e] >> 16);
         out[e] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
@@ -609,18 +642,21 @@ __global__ __launch_bounds__(256) void split_close_kernel(PrefillArgs a, uint32_
 
 template <uint32_t FMT, int BM, bool SPLIT>
 hipError_t launch_tile(uint32_t epilogue, const PrefillArgs &a, dim3 grid, hipStream_t stream) {
-  const dim3 block(kThreads);
+  constexpr int W = tile_waves<FMT>();
+  const dim3 block(64 * W);
   switch (epilogue) {
-    case EpNone: hipLaunchKernelGGL((prefill_kernel<FMT, EpNone, BM, SPLIT>), grid, block, 0, stream, a); break;
-    case EpResidual: hipLaunchKernelGGL((prefill_kernel<FMT, EpResidual, BM, SPLIT>), grid, block, 0, stream, a); break;
-    default: hipLaunchKernelGGL((prefill_kernel<FMT, EpUpWithGate, BM, SPLIT>), grid, block, 0, stream, a); break;
+    case EpNone: hipLaunchKernelGGL((prefill_kernel<FMT, EpNone, BM, SPLIT, W>), grid, block, 0, stream, a); break;
+    case EpResidual:
+      hipLaunchKernelGGL((prefill_kernel<FMT, EpResidual, BM, SPLIT, W>), grid, block, 0, stream, a);
+      break;
+    default: hipLaunchKernelGGL((prefill_kernel<FMT, EpUpWithGate, BM, SPLIT, W>), grid, block, 0, stream, a); break;
   }
   return hipGetLastError();
 }
 
 template <uint32_t FMT>
 hipError_t launch_format(uint32_t epilogue, const PrefillArgs &args, hipStream_t stream) {
-  static_assert(lds_bytes<FMT, 256>() <= kLdsLimit, "every format's 256-row tile fits the LDS");
+  static_assert(lds_bytes<FMT, 256, tile_waves<FMT>()>() <= kLdsLimit, "every format's 256-row tile fits the LDS");
   uint32_t tiles = 0;
   for (uint32_t s = 0; s < args.segments; ++s) tiles += args.seg[s].tiles;
   // The projection's whole width decides the halving, so every dispatch of it (one per format) halves alike.
