@@ -9,7 +9,13 @@
  * column's 16 code bytes, widens them to 32 fp32 codes (low and high nibbles), dequantises them with two vector FMAs
  * and multiply-adds them into one vector accumulator per row, against the rows' inputs permuted once per call into
  * the codes' byte order. Rows go in blocks of eight, so each dequantised group serves eight rows. AVX-512F, AVX2+FMA
- * or scalar code is chosen at run time from what the CPU reports. */
+ * or scalar code is chosen at run time from what the CPU reports.
+ *
+ * Where the CPU reports AVX512_BF16 the pool runs the bf16 dot-product kernel instead (columns_bf16): the group's 32
+ * codes become bf16 q (exact) and VDPBF16PS multiplies them with the rows' bf16 inputs (exact products, fp32 sums),
+ * one scale group at a time; the close is acc += s * sum(q x) per scale group on the vector and z * sum(x) per row in
+ * scalar. These are the exact-operand numerics of the GPU's decode tiles, within the same accumulation bound. The
+ * instruction treats bf16 subnormal inputs as zero. sqo_pool_set_isa picks another kernel the CPU has. */
 #define _GNU_SOURCE
 #include "sq_cpu.h"
 
@@ -38,6 +44,8 @@ static void init_elements(void) {
 typedef struct {
   uint32_t fmt, M, N, K, G, units, meta_groups, meta_bytes;
   const float *xp; /* [M][G][2][16]: row m's inputs of group g, low-nibble order then high-nibble order */
+  const uint16_t *xb; /* the same inputs as bf16 (the bf16 kernel) */
+  const float *sx;    /* [M][G / sg]: the sum of row m's inputs over scale group u (the bf16 kernel) */
   const uint8_t *plane0, *meta;
   uint16_t *out;
 } job_t;
@@ -50,9 +58,10 @@ struct sqo_pool {
   uint64_t generation;
   int remaining, quit;
   job_t job;
-  float *xp;
+  float *xp, *sx;
+  uint16_t *xb;
   size_t xp_floats;
-  int kind; /* 2 AVX-512F, 1 AVX2+FMA, 0 scalar */
+  int kind; /* 3 AVX512_BF16, 2 AVX-512F, 1 AVX2+FMA, 0 scalar */
 };
 
 static inline float bf16f(uint16_t b) {
@@ -153,6 +162,73 @@ __attribute__((target("avx512f"))) static void columns_avx512(const job_t *j, ui
     }
 }
 
+/* The scale group's span in groups of 32: the affine formats' meta unit, Q4_K's 32-input sub-block. */
+static inline uint32_t scale_groups(const job_t *j) { return j->fmt == SQO_FMT_Q4K ? 1u : j->meta_groups; }
+
+/* Rows r0..r0 + R - 1 of column n (R a constant at each call, so the accumulators stay in registers). */
+__attribute__((target("avx512f,avx512bw,avx512bf16"), always_inline)) static inline void column_bf16_rows(
+    const job_t *j, __m512i table, uint32_t n, uint32_t r0, const int R) {
+  const __m256i nib = _mm256_set1_epi16(15);
+  const uint32_t sg = scale_groups(j);
+  const column_t col = column_at(j, n);
+  __m512 acc[kRowBlock];
+  float zacc[kRowBlock];
+  for (int r = 0; r < R; ++r) {
+    acc[r] = _mm512_setzero_ps();
+    zacc[r] = 0.0f;
+  }
+  for (uint32_t g0 = 0; g0 < j->G; g0 += sg) {
+    float s, z;
+    group_coef(j, col, g0, &s, &z);
+    __m512 c[kRowBlock];
+    for (int r = 0; r < R; ++r) c[r] = _mm512_setzero_ps();
+    for (uint32_t g = g0; g < g0 + sg; ++g) {
+      /* Words 0..15: the low nibbles of code bytes 0..15, words 16..31 the high ones (the inputs' order). */
+      const __m256i b = _mm256_cvtepu8_epi16(_mm_loadu_si128((const __m128i *)(col.plane + (size_t)g * 1024)));
+      const __m512i q =
+          _mm512_inserti64x4(_mm512_castsi256_si512(_mm256_and_si256(b, nib)), _mm256_srli_epi16(b, 4), 1);
+      const __m512bh w = (__m512bh)_mm512_permutexvar_epi16(q, table);
+      const uint16_t *x = j->xb + ((size_t)r0 * j->G + g) * 32;
+      for (int r = 0; r < R; ++r)
+        c[r] = _mm512_dpbf16_ps(c[r], w, (__m512bh)_mm512_loadu_si512(x + (size_t)r * j->G * 32));
+    }
+    const __m512 vs = _mm512_set1_ps(s);
+    const uint32_t units = j->G / sg;
+    const float *sx = j->sx + (size_t)r0 * units + g0 / sg;
+    for (int r = 0; r < R; ++r) {
+      acc[r] = _mm512_fmadd_ps(vs, c[r], acc[r]);
+      zacc[r] = fmaf(z, sx[(size_t)r * units], zacc[r]);
+    }
+  }
+  for (int r = 0; r < R; ++r) j->out[(size_t)(r0 + r) * j->N + n] = to_bf16(hsum512(acc[r]) + zacc[r]);
+}
+
+__attribute__((target("avx512f,avx512bw,avx512bf16"))) static void columns_bf16(const job_t *j, uint32_t n0,
+                                                                                 uint32_t n1) {
+  /* bf16 of q for q = 0..15 (twice: vpermw indexes 32 words). */
+  uint16_t lut[32];
+  for (int q = 0; q < 32; ++q) {
+    const float f = (float)(q & 15);
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    lut[q] = (uint16_t)(u >> 16);
+  }
+  const __m512i table = _mm512_loadu_si512(lut);
+  for (uint32_t n = n0; n < n1; ++n)
+    for (uint32_t r0 = 0; r0 < j->M; r0 += kRowBlock) {
+      switch (j->M - r0 < kRowBlock ? j->M - r0 : kRowBlock) {
+        case 1: column_bf16_rows(j, table, n, r0, 1); break;
+        case 2: column_bf16_rows(j, table, n, r0, 2); break;
+        case 3: column_bf16_rows(j, table, n, r0, 3); break;
+        case 4: column_bf16_rows(j, table, n, r0, 4); break;
+        case 5: column_bf16_rows(j, table, n, r0, 5); break;
+        case 6: column_bf16_rows(j, table, n, r0, 6); break;
+        case 7: column_bf16_rows(j, table, n, r0, 7); break;
+        default: column_bf16_rows(j, table, n, r0, 8); break;
+      }
+    }
+}
+
 __attribute__((target("avx2,fma"))) static float hsum256(__m256 v) {
   const __m128 s = _mm_add_ps(_mm256_castps256_ps128(v), _mm256_extractf128_ps(v, 1));
   const __m128 t = _mm_add_ps(s, _mm_movehl_ps(s, s));
@@ -213,7 +289,8 @@ static void run_share(sqo_pool *p, int t) {
   const uint32_t tiles = j->N / 64, t0 = (uint32_t)((uint64_t)tiles * t / p->threads),
                  t1 = (uint32_t)((uint64_t)tiles * (t + 1) / p->threads);
   if (t0 == t1) return;
-  if (p->kind == 2) columns_avx512(j, 64 * t0, 64 * t1);
+  if (p->kind == 3) columns_bf16(j, 64 * t0, 64 * t1);
+  else if (p->kind == 2) columns_avx512(j, 64 * t0, 64 * t1);
   else if (p->kind == 1) columns_avx2(j, 64 * t0, 64 * t1);
   else columns_scalar(j, 64 * t0, 64 * t1);
 }
@@ -244,16 +321,23 @@ static void *worker(void *arg) {
   }
 }
 
-static int cpu_kind(void) {
+static const char *const kNames[] = {"scalar", "avx2+fma", "avx512f", "avx512bf16"};
+/* Whether the CPU runs kernel kind k. */
+static int cpu_has(int k) {
   __builtin_cpu_init();
-  if (__builtin_cpu_supports("avx512f")) return 2;
-  if (__builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma")) return 1;
+  switch (k) {
+    case 3: return __builtin_cpu_supports("avx512bf16") && __builtin_cpu_supports("avx512bw");
+    case 2: return __builtin_cpu_supports("avx512f");
+    case 1: return __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+    default: return k == 0;
+  }
+}
+static int cpu_kind(void) {
+  for (int k = 3; k > 0; --k)
+    if (cpu_has(k)) return k;
   return 0;
 }
-const char *sqo_cpu_isa(void) {
-  static const char *names[] = {"scalar", "avx2+fma", "avx512f"};
-  return names[cpu_kind()];
-}
+const char *sqo_cpu_isa(void) { return kNames[cpu_kind()]; }
 
 sqo_pool *sqo_pool_create(int threads) {
   if (threads < 1) threads = 1;
@@ -282,22 +366,36 @@ void sqo_pool_destroy(sqo_pool *p) {
   pthread_mutex_unlock(&p->mu);
   for (int t = 1; t < p->threads; ++t) pthread_join(p->tid[t], NULL);
   free(p->xp);
+  free(p->xb);
+  free(p->sx);
   free(p);
 }
 
 int sqo_pool_threads(const sqo_pool *p) { return p->threads; }
-const char *sqo_pool_isa(const sqo_pool *p) {
-  static const char *names[] = {"scalar", "avx2+fma", "avx512f"};
-  return names[p->kind];
+const char *sqo_pool_isa(const sqo_pool *p) { return kNames[p->kind]; }
+
+int sqo_pool_set_isa(sqo_pool *p, const char *isa) {
+  for (int k = 0; k < 4; ++k)
+    if (!strcmp(isa, kNames[k])) {
+      if (!cpu_has(k)) return -1;
+      p->kind = k;
+      return 0;
+    }
+  return -1;
 }
 
 int sqo_pool_reserve(sqo_pool *p, uint32_t M, uint32_t K) {
   const size_t need = (size_t)M * K;
   if (need <= p->xp_floats) return 0;
   free(p->xp);
+  free(p->xb);
+  free(p->sx);
   p->xp = (float *)aligned_alloc(64, (need * sizeof(float) + 63) / 64 * 64);
-  p->xp_floats = p->xp ? need : 0;
-  return p->xp ? 0 : -1;
+  p->xb = (uint16_t *)aligned_alloc(64, (need * sizeof(uint16_t) + 63) / 64 * 64);
+  p->sx = (float *)aligned_alloc(64, (need / 32 * sizeof(float) + 63) / 64 * 64);
+  const int ok = p->xp && p->xb && p->sx;
+  p->xp_floats = ok ? need : 0;
+  return ok ? 0 : -1;
 }
 
 double sqo_pool_matmul(sqo_pool *p, uint32_t fmt, uint32_t M, uint32_t N, uint32_t K, const uint16_t *x,
@@ -309,17 +407,26 @@ double sqo_pool_matmul(sqo_pool *p, uint32_t fmt, uint32_t M, uint32_t N, uint32
   struct timespec t0, t1;
   clock_gettime(CLOCK_MONOTONIC, &t0);
   const uint32_t G = K / 32;
-  /* The rows' inputs in the codes' byte order, once per call. */
+  /* The rows' inputs in the codes' byte order, once per call, and their sums per scale group. */
+  const uint32_t sg = fmt == SQO_FMT_Q4K ? 1u : f.meta_groups;
   for (uint32_t r = 0; r < M; ++r)
     for (uint32_t g = 0; g < G; ++g) {
       float *d = p->xp + ((size_t)r * G + g) * 32;
+      uint16_t *e = p->xb + ((size_t)r * G + g) * 32;
       const uint16_t *s = x + (size_t)r * K + (size_t)g * 32;
+      float sum = 0.0f;
       for (int b = 0; b < 16; ++b) {
-        d[b] = sqo_bf16_to_f32(s[g_element[b][0]]);
-        d[16 + b] = sqo_bf16_to_f32(s[g_element[b][1]]);
+        e[b] = s[g_element[b][0]];
+        e[16 + b] = s[g_element[b][1]];
+        d[b] = sqo_bf16_to_f32(e[b]);
+        d[16 + b] = sqo_bf16_to_f32(e[16 + b]);
+        sum += d[b] + d[16 + b];
       }
+      float *unit = p->sx + (size_t)r * (G / sg) + g / sg;
+      *unit = g % sg ? *unit + sum : sum;
     }
-  p->job = (job_t){fmt, M, N, K, G, G / f.meta_groups, f.meta_groups, f.meta_bytes, p->xp, plane0, meta, out};
+  p->job = (job_t){fmt, M, N, K, G, G / f.meta_groups, f.meta_groups, f.meta_bytes, p->xp, p->xb, p->sx,
+                   plane0, meta, out};
   pthread_mutex_lock(&p->mu);
   p->remaining = p->threads - 1;
   ++p->generation;

@@ -9,13 +9,15 @@ extern "C" {
 #endif
 
 typedef struct sqo_pool sqo_pool;
-/* The instruction set the kernels run: "avx512f", "avx2+fma" or "scalar" (chosen at run time). */
+/* The instruction set the kernels run: "avx512bf16", "avx512f", "avx2+fma" or "scalar" (the best the CPU has). */
 const char *sqo_cpu_isa(void);
 /* A pool of `threads` threads (the caller's thread is one of them), started once. */
 sqo_pool *sqo_pool_create(int threads);
 void sqo_pool_destroy(sqo_pool *pool);
 int sqo_pool_threads(const sqo_pool *pool);
 const char *sqo_pool_isa(const sqo_pool *pool);
+/* Runs the pool's later calls on the kernel named isa (one of sqo_cpu_isa's names); -1 when the CPU lacks it. */
+int sqo_pool_set_isa(sqo_pool *pool, const char *isa);
 /* Holds the permuted-input buffer for M x K (allocation outside any timed call); 0 on success. */
 int sqo_pool_reserve(sqo_pool *pool, uint32_t M, uint32_t K);
 /* y = x W^T for x bf16 [M][K] and W in format fmt (MLX affine 4-bit groups 32/64/128, or Q4_K) as planes

@@ -177,6 +177,7 @@ class CpuPool:
         L.sqo_pool_threads.argtypes = [ctypes.c_void_p]
         L.sqo_pool_isa.restype = ctypes.c_char_p
         L.sqo_pool_isa.argtypes = [ctypes.c_void_p]
+        L.sqo_pool_set_isa.argtypes = [ctypes.c_void_p, ctypes.c_char_p]
         L.sqo_pool_reserve.argtypes = [ctypes.c_void_p, c_uint32, c_uint32]
         L.sqo_pool_matmul.restype = ctypes.c_double
         L.sqo_pool_matmul.argtypes = [ctypes.c_void_p, c_uint32, c_uint32, c_uint32, c_uint32, POINTER(c_uint16),
@@ -185,6 +186,14 @@ class CpuPool:
         self._pool = L.sqo_pool_create(threads)
         self.threads = L.sqo_pool_threads(self._pool)
         self.isa = L.sqo_pool_isa(self._pool).decode()
+
+    def set_isa(self, isa: str) -> bool:
+        """Runs later calls on the kernel named isa ("avx512bf16", "avx512f", "avx2+fma", "scalar"); False when the CPU
+        lacks it (the pool keeps its kernel)."""
+        if self._lib.sqo_pool_set_isa(self._pool, isa.encode()) != 0:
+            return False
+        self.isa = isa
+        return True
 
     def reserve(self, m: int, k: int) -> None:
         if self._lib.sqo_pool_reserve(self._pool, m, k) != 0:

@@ -10,11 +10,10 @@ namespace sq::kern {
 // Adds this split's totals to the others' in split order when this workgroup arrives last; returns false when
 // another workgroup still has to arrive. index[b][i]: the partial's offset within a split.
 //
-// Every access to the partials and the counter is a device-scope atomic, which gfx950 performs at the device's
-// coherence point (sc1) past the per-XCD L2s, so the partials are visible to any workgroup once their stores
-// complete; each wave waits for that (s_waitcnt vmcnt(0)) before thread 0 arrives at the counter. No L2 writeback
-// or invalidate is issued: a __threadfence() in every wave writes back and invalidates the whole L2 of its XCD,
-// which serialises hundreds of workgroups per dispatch.
+// Every access to the partials and the counter is an agent-scope atomic (sc1: coherent across the XCDs' L2s). Each
+// wave waits for its partial stores to complete before thread 0 adds to the counter, and the last arriver loads the
+// partials only after its add returns. This is the memory model's agent-scope release/acquire without the L2
+// writeback and invalidate, which only ordinary (non-sc1) accesses need.
 template <int NB, int R>
 __device__ __forceinline__ bool split_reduce(float (&total)[NB][R], const bool (&live)[NB][R],
                                              const size_t (&index)[NB][R], float *partials, size_t split_elements,

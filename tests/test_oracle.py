@@ -570,11 +570,13 @@ def test_mlx_fixture_values_bit_exact_8bit(group):
             assert np.array_equal(blk[4:], codes[r, b * group:(b + 1) * group])
 
 
+@pytest.mark.parametrize("isa", ["avx512bf16", "avx512f", "avx2+fma", "scalar"])
 @pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K, oracle.FMT_AF4G32, oracle.FMT_AF4G128])
 @pytest.mark.parametrize("m", [1, 3, 19])
-def test_cpu_pool_matches_fp64(fmt, m):
-    """The vectorised CPU baseline (thread pool, AVX-512 or AVX2 kernels) agrees with the fp64 projection within the
-    accumulation bound plus one bf16 rounding of the output, for row counts around its eight-row blocks."""
+def test_cpu_pool_matches_fp64(fmt, m, isa):
+    """Every kernel of the CPU baseline this host runs (thread pool; bf16 dot products, AVX-512, AVX2 or scalar)
+    agrees with the fp64 projection within the accumulation bound plus one bf16 rounding of the output, for row
+    counts around its eight-row blocks."""
     rng = np.random.default_rng(50 + fmt + m)
     n, k = 192, 1024
     if fmt == oracle.FMT_Q4K:
@@ -590,6 +592,9 @@ def test_cpu_pool_matches_fp64(fmt, m):
     plane0, meta, values = oracle.repack(fmt, native, n, k)
     x = (rng.standard_normal((m, k)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
     pool = oracle.CpuPool(3)
+    if not pool.set_isa(isa):
+        pool.close()
+        pytest.skip(f"this CPU has no {isa}")
     pool.reserve(m, k)
     out, secs = pool.matmul(fmt, x, plane0, meta, n)
     pool.close()
