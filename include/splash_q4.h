@@ -383,6 +383,29 @@ int sq_moe_add_routed(void *graph, const sq_moe_buffers *buffers, const sq_moe_w
 int sq_moe_add_routes(void *graph, sq_buffer input, const sq_segment *router, sq_buffer shared_scalar_gate,
                       sq_buffer scores, sq_buffer selected, sq_buffer routing_weights, uint32_t rows,
                       const sq_moe_shape *shape, uint32_t router_tile);
+/* MoE::addExpertLoad (MoE.hpp:411-420, MoE.cpp:553-558; kernel moe_expert_load, gguf_repack.metal:239-257): the
+ * gate, up and down projections of up to `jobs` streamed experts repacked into their slots of `arena`. Job j's
+ * projection z takes its native rows (row_bytes apart) from staging + sources[3 j + z] (bytes) on, and writes them
+ * as sq_gguf_repack does into plane i of slot slots[j]: arena + planes[i] + slots[j] * slot_bytes[i] (plane0, plane1,
+ * meta). params is the reference's 192-byte MoeExpertLoadParams: three 64-byte MoeExpertLoadProjection
+ * {format, rows, columns, row_bytes, planes[3], slot_bytes[3]} (rows 0: no projection). slots: jobs uint32; sources:
+ * 3 jobs uint64 (8-byte aligned); grid: three uint32 workgroup counts (x, y, z) that an earlier dispatch may write,
+ * the reference's indirect grid. The launch covers (sq_moe_expert_load_groups(params), jobs, 3) workgroups of 256
+ * threads, and those past grid's counts do nothing. A job whose rows or slot planes would lie outside staging or
+ * arena writes nothing. */
+typedef struct sq_moe_expert_load_projection {
+  uint32_t format_id, rows, columns, row_bytes;
+  uint64_t planes[3];     /* plane0, plane1, meta: byte offsets in the arena */
+  uint64_t slot_bytes[3]; /* bytes a slot in each */
+} sq_moe_expert_load_projection;
+typedef struct sq_moe_expert_load_params {
+  sq_moe_expert_load_projection projections[3]; /* gate, up, down */
+} sq_moe_expert_load_params;
+int sq_moe_expert_load(void *graph, sq_buffer staging, sq_buffer arena, sq_buffer slots, sq_buffer sources,
+                       const sq_moe_expert_load_params *params, uint32_t jobs, sq_buffer grid);
+/* MoE::expertLoadGroups (MoE.cpp:545-551): the workgroups that repack one job's largest projection (0 without
+ * params). */
+uint32_t sq_moe_expert_load_groups(const sq_moe_expert_load_params *params);
 
 #ifdef __cplusplus
 }

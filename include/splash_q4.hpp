@@ -213,6 +213,14 @@ class MoE final {
     check(sq_moe_add_routes(graph, input, router, sharedScalarGate, scores, selected, routingWeights, rows, &shape,
                             routerTile));
   }
+  // MoE::addExpertLoad (MoE.hpp:411-420) and MoE::expertLoadGroups (MoE.cpp:545-551).
+  static void addExpertLoad(Graph graph, Buffer staging, Buffer arena, Buffer slots, Buffer sources,
+                            const sq_moe_expert_load_params &params, uint32_t jobs, Buffer grid) {
+    check(sq_moe_expert_load(graph, staging, arena, slots, sources, &params, jobs, grid));
+  }
+  [[nodiscard]] static uint32_t expertLoadGroups(const sq_moe_expert_load_params &params) {
+    return sq_moe_expert_load_groups(&params);
+  }
 };
 
 // Load-time weight preparation (gguf_repack.metal:232-238; GgufPreparation.cpp:141-193).

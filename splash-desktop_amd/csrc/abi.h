@@ -196,3 +196,18 @@ struct SqMoeCombineParams {
   uint32_t rows, hidden_size, routes_per_row;
 };
 static_assert(sizeof(SqMoeCombineParams) == 12, "MoeCombineParams is 12 bytes");
+// One projection (gate, up or down) of the experts a load writes into their slots (MoE.h:146-168): rows x columns
+// in `format`, job j's native rows of row_bytes each staged from its source on, and its plane0, plane1 and meta
+// planes in the arena from planes[i] on, slot_bytes[i] bytes a slot.
+struct SqMoeExpertLoadProjection {
+  uint32_t format, rows, columns, row_bytes;
+  uint64_t planes[3];
+  uint64_t slot_bytes[3];
+};
+static_assert(sizeof(SqMoeExpertLoadProjection) == 64, "MoeExpertLoadProjection is 64 bytes");
+struct SqMoeExpertLoadParams {
+  struct SqMoeExpertLoadProjection projections[3];
+};
+static_assert(sizeof(SqMoeExpertLoadParams) == 192, "MoeExpertLoadParams is 192 bytes");
+// The threads of a moe_expert_load workgroup, each of which repacks one (row, 32-wide K group) pair (MoE.h:170-172).
+#define SQ_MOE_EXPERT_LOAD_THREADS 256u

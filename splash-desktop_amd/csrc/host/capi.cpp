@@ -2,6 +2,7 @@
 // the boundary into a status code and a thread-local message, and launches on the caller's stream.
 #include "../../../include/splash_q4.h"
 
+#include <cstddef>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -590,6 +591,27 @@ int sq_moe_add_routes(void *graph, sq_buffer input, const sq_segment *router, sq
       r = QuantizedSegment::rows(router->format_id, router->output_size, router->input_size, buf(router->plane0));
     MoE::addRoutes(stream(graph), buf(input), r, buf(shared_scalar_gate), buf(scores), buf(selected),
                    buf(routing_weights), rows, s, FloatTile(router_tile));
+  });
+}
+
+static_assert(sizeof(sq_moe_expert_load_params) == sizeof(SqMoeExpertLoadParams) &&
+                  offsetof(sq_moe_expert_load_projection, planes) == offsetof(SqMoeExpertLoadProjection, planes) &&
+                  offsetof(sq_moe_expert_load_projection, slot_bytes) ==
+                      offsetof(SqMoeExpertLoadProjection, slot_bytes),
+              "sq_moe_expert_load_params is the reference's MoeExpertLoadParams");
+uint32_t sq_moe_expert_load_groups(const sq_moe_expert_load_params *params) {
+  if (!params) return 0;
+  SqMoeExpertLoadParams p;
+  std::memcpy(&p, params, sizeof p);
+  return MoE::expertLoadGroups(p);
+}
+
+int sq_moe_expert_load(void *graph, sq_buffer staging, sq_buffer arena, sq_buffer slots, sq_buffer sources,
+                       const sq_moe_expert_load_params *params, uint32_t jobs, sq_buffer grid) {
+  return guarded([&] {
+    SqMoeExpertLoadParams p;
+    std::memcpy(&p, &need(params, "params"), sizeof p);
+    MoE::addExpertLoad(stream(graph), buf(staging), buf(arena), buf(slots), buf(sources), p, jobs, buf(grid));
   });
 }
 

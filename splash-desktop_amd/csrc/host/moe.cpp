@@ -160,6 +160,51 @@ void MoE::addRoutes(hipStream_t graph, Buffer input, const QuantizedSegment &rou
            "MoE route select");
 }
 
+uint32_t MoE::expertLoadGroups(const SqMoeExpertLoadParams &params) noexcept {
+  uint64_t groups = 0;
+  for (const SqMoeExpertLoadProjection &q : params.projections)
+    groups = std::max(groups, (uint64_t{q.rows} * (q.columns / 32) + SQ_MOE_EXPERT_LOAD_THREADS - 1) /
+                                  SQ_MOE_EXPERT_LOAD_THREADS);
+  return groups > UINT32_MAX ? 0u : static_cast<uint32_t>(groups);
+}
+
+void MoE::addExpertLoad(hipStream_t graph, Buffer staging, Buffer arena, Buffer slots, Buffer sources,
+                        const SqMoeExpertLoadParams &params, uint32_t jobs, Buffer grid) {
+  const char *names[3] = {"gate", "up", "down"};
+  bool any = false;
+  for (int z = 0; z < 3; ++z) {
+    const SqMoeExpertLoadProjection &q = params.projections[z];
+    if (!q.rows) continue;
+    any = true;
+    const std::string what = std::string("MoE expert load ") + names[z];
+    if (!sq_format_supported(q.format)) throw std::invalid_argument(what + " takes a format this build runs");
+    const SqQuantFormat f = sq_format(q.format);
+    if (q.rows % SQ_TILE_ROWS || !q.columns || q.columns % f.block_elements)
+      throw std::invalid_argument(what + " takes whole plane tiles of rows and whole native blocks");
+    if (q.row_bytes < uint64_t{q.columns} / f.block_elements * f.block_bytes)
+      throw std::invalid_argument(what + " rows are shorter than their blocks");
+    const uint64_t groups = q.columns / 32;
+    const uint64_t need[3] = {q.rows * groups * f.plane0_bytes, q.rows * groups * f.plane1_bytes,
+                              q.rows * (groups / f.meta_groups) * f.meta_bytes};
+    for (int i = 0; i < 3; ++i)
+      if (q.slot_bytes[i] < need[i]) throw std::invalid_argument(what + " slots are smaller than their planes");
+  }
+  const uint32_t groups = expertLoadGroups(params);
+  if (!jobs || !any) return;
+  if (jobs > 65535 || !groups) throw std::invalid_argument("invalid MoE expert load grid");
+  requireBytes(slots, uint64_t{jobs} * 4, "MoE expert load slots");
+  requireBytes(sources, uint64_t{jobs} * 3 * 8, "MoE expert load sources");
+  requireBytes(grid, 12, "MoE expert load grid");
+  if (!staging || !arena) throw std::invalid_argument("MoE expert load needs its staging and arena buffers");
+  if ((reinterpret_cast<uintptr_t>(sources.ptr) & 7u) || (reinterpret_cast<uintptr_t>(slots.ptr) & 3u) ||
+      (reinterpret_cast<uintptr_t>(grid.ptr) & 3u))
+    throw std::invalid_argument("MoE expert load sources are 8-byte and slots and grid 4-byte aligned");
+  launched(kern::launch_expert_load(staging.as<const uint8_t>(), staging.bytes, arena.as<uint8_t>(), arena.bytes,
+                                    slots.as<const uint32_t>(), sources.as<const uint64_t>(), params, groups, jobs,
+                                    grid.as<const uint32_t>(), graph),
+           "MoE expert load");
+}
+
 void MoE::addRouting(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
   validate(b, w, plan);
   const MoeShape s = plan.shape();

@@ -128,6 +128,13 @@ struct MoE {
   static void addRoutes(hipStream_t graph, Buffer input, const QuantizedSegment &router, Buffer sharedScalarGate,
                         Buffer scores, Buffer selected, Buffer routingWeights, uint32_t rows, MoeShape shape,
                         FloatTile routerTile);
+  // MoE::addExpertLoad (MoE.hpp:411-420): up to `jobs` streamed experts' gate, up and down native rows from
+  // `staging` repacked into their slots of `arena` (moe_expert_load); `slots`, `sources` and `grid` are device
+  // buffers an earlier dispatch may write. Validates the projections and the buffers' sizes before the launch.
+  static void addExpertLoad(hipStream_t graph, Buffer staging, Buffer arena, Buffer slots, Buffer sources,
+                            const SqMoeExpertLoadParams &params, uint32_t jobs, Buffer grid);
+  // MoE::expertLoadGroups (MoE.cpp:545-551): the workgroups that repack one job's largest projection.
+  static uint32_t expertLoadGroups(const SqMoeExpertLoadParams &params) noexcept;
 };
 
 }  // namespace sq::ops

@@ -110,6 +110,11 @@ hipError_t launch_dequant(uint32_t fmt, const uint8_t *plane0, const uint8_t *pl
 // Load-time repacks: native rows (GgufRepackParams layout) into plane0 / meta, and MLX tensors (uint32 codes,
 // bf16 scales and biases) straight into plane0 / meta.
 hipError_t launch_repack(const uint8_t *src, uint8_t *dst, const SqGgufRepackParams &params, hipStream_t stream);
+// moe_expert_load: grid (groups, jobs, 3) of SQ_MOE_EXPERT_LOAD_THREADS threads, the device's grid[0..2] the live
+// part of it.
+hipError_t launch_expert_load(const uint8_t *staging, uint64_t staging_bytes, uint8_t *arena, uint64_t arena_bytes,
+                              const uint32_t *slots, const uint64_t *sources, const SqMoeExpertLoadParams &params,
+                              uint32_t groups, uint32_t jobs, const uint32_t *grid, hipStream_t stream);
 // Measurement aid (diag.hip): a read-only stream of `bytes` (a multiple of 16) over `workgroups` workgroups.
 // The RMS norm producer: out = bf16((x * rsqrt(sum x^2 / width + 1e-6)) * w) per row, w bf16 or fp32; with
 // half_input set it also writes the prefill tile's prepared input of `out` (half_input [rows][width], row_scale

@@ -38,36 +38,34 @@ __device__ __forceinline__ void store_bits(const uint8_t codes[32], uint8_t *dst
   for (uint32_t w = 0; w < BITS; ++w) ((uint32_t *)dst)[w] = word[w];
 }
 
-// One thread a (row, group of 32): the group's low codes into its plane0 unit, its high bits into its plane1 unit,
-// and the first group of each meta unit copies the unit's meta (gguf_repack_group, gguf_repack.metal:42-74, and
-// metaPack's Q6_K arrangement: its 16 int8 scales, d and two zero bytes).
-__global__ void repack_kernel(const uint8_t *src, uint8_t *dst, SqGgufRepackParams p) {
-  const uint32_t G = p.input_size / 32;
-  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= (uint64_t)p.rows * G) return;
-  const uint32_t n = (uint32_t)(t / G), g = (uint32_t)(t % G);
-  const SqQuantFormat f = sq_format(p.fmt);
+// Group g of row n (native row `row`, G groups a row) of format fmt: the group's low codes into its plane0 unit, its
+// high bits into its plane1 unit, and the first group of each meta unit copies the unit's meta (gguf_repack_group,
+// gguf_repack.metal:42-74, and metaPack's Q6_K arrangement: its 16 int8 scales, d and two zero bytes). plane0,
+// plane1 and meta point at the tensor's planes.
+__device__ void repack_group(const uint8_t *row, uint32_t fmt, uint32_t G, uint32_t n, uint32_t g, uint8_t *plane0,
+                             uint8_t *plane1, uint8_t *meta_plane) {
+  const SqQuantFormat f = sq_format(fmt);
   const uint32_t b = g / f.meta_groups, jj = g % f.meta_groups;
-  const uint8_t *blk = src + (size_t)n * p.src_row_bytes + (size_t)b * f.block_bytes;
+  const uint8_t *blk = row + (size_t)b * f.block_bytes;
   uint8_t codes[32], highs[32];
-  uint8_t *unit0 = dst + sq_tile_index(n, g, G) * f.plane0_bytes;
-  uint8_t *unit1 = dst + p.dst_plane1 + sq_tile_index(n, g, G) * f.plane1_bytes;
-  if (p.fmt == SQ_FMT_AF8G64) {
+  uint8_t *unit0 = plane0 + sq_tile_index(n, g, G) * f.plane0_bytes;
+  uint8_t *unit1 = plane1 + sq_tile_index(n, g, G) * f.plane1_bytes;
+  if (fmt == SQ_FMT_AF8G64) {
 #pragma unroll
     for (uint32_t e = 0; e < 32; ++e) codes[e] = blk[4 + 32u * jj + e];
     store_bits<8>(codes, unit0);
-  } else if (sq_affine_format(p.fmt)) {
+  } else if (sq_affine_format(fmt)) {
 #pragma unroll
     for (uint32_t e = 0; e < 32; ++e) {
       const uint32_t l = 32u * jj + e;
       codes[e] = (blk[4 + l / 2] >> (4u * (l & 1u))) & 15u;
     }
     store_pairs(codes, unit0);
-  } else if (p.fmt == SQ_FMT_Q80) {
+  } else if (fmt == SQ_FMT_Q80) {
 #pragma unroll
     for (uint32_t e = 0; e < 32; ++e) codes[e] = blk[2 + e];
     store_bits<8>(codes, unit0);
-  } else if (p.fmt == SQ_FMT_Q6K) {
+  } else if (fmt == SQ_FMT_Q6K) {
     const uint32_t h = jj / 4, r = jj % 4;
 #pragma unroll
     for (uint32_t e = 0; e < 32; ++e) {
@@ -77,19 +75,19 @@ __global__ void repack_kernel(const uint8_t *src, uint8_t *dst, SqGgufRepackPara
     store_pairs(codes, unit0);
     store_bits<2>(highs, unit1);
   } else {   // Q4_K, Q5_K
-    const uint32_t q = p.fmt == SQ_FMT_Q5K ? 48u : 16u;
+    const uint32_t q = fmt == SQ_FMT_Q5K ? 48u : 16u;
 #pragma unroll
     for (uint32_t e = 0; e < 32; ++e) codes[e] = (blk[q + (jj / 2) * 32 + e] >> (4u * (jj & 1u))) & 15u;
     store_pairs(codes, unit0);
-    if (p.fmt == SQ_FMT_Q5K) {
+    if (fmt == SQ_FMT_Q5K) {
 #pragma unroll
       for (uint32_t e = 0; e < 32; ++e) highs[e] = (blk[16 + e] >> jj) & 1u;
       store_bits<1>(highs, unit1);
     }
   }
   if (jj == 0) {
-    uint8_t *meta = dst + p.dst_meta + sq_tile_index(n, b, G / f.meta_groups) * f.meta_bytes;
-    if (p.fmt == SQ_FMT_Q6K) {
+    uint8_t *meta = meta_plane + sq_tile_index(n, b, G / f.meta_groups) * f.meta_bytes;
+    if (fmt == SQ_FMT_Q6K) {
       for (uint32_t i = 0; i < 16; ++i) meta[i] = blk[SQ_Q6K_SCALES + i];
       meta[16] = blk[SQ_Q6K_D];
       meta[17] = blk[SQ_Q6K_D + 1];
@@ -98,6 +96,45 @@ __global__ void repack_kernel(const uint8_t *src, uint8_t *dst, SqGgufRepackPara
       for (uint32_t i = 0; i < f.meta_bytes; ++i) meta[i] = blk[i];
     }
   }
+}
+
+// One thread a (row, group of 32) of one tensor (kernel gguf_repack, gguf_repack.metal:232-238).
+__global__ void repack_kernel(const uint8_t *src, uint8_t *dst, SqGgufRepackParams p) {
+  const uint32_t G = p.input_size / 32;
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (uint64_t)p.rows * G) return;
+  const uint32_t n = (uint32_t)(t / G), g = (uint32_t)(t % G);
+  repack_group(src + (size_t)n * p.src_row_bytes, p.fmt, G, n, g, dst, dst + p.dst_plane1, dst + p.dst_meta);
+}
+
+// Streamed experts into their slots (moe_expert_load, gguf_repack.metal:239-257): workgroup (x, y, z) repacks 256
+// (row, group of 32) pairs of projection z of job y from staging + sources[3 y + z] on into the planes of slot
+// slots[y] of the arena, projection z's plane i at planes[i] + slot * slot_bytes[i]. `grid` holds the three
+// workgroup counts the dispatch runs (the reference's indirect grid, written by an earlier dispatch): the launch
+// covers the largest grid and workgroups past grid's return. A job whose source rows or slot planes would fall
+// outside the staging or the arena writes nothing.
+__global__ __launch_bounds__(SQ_MOE_EXPERT_LOAD_THREADS) void expert_load_kernel(
+    const uint8_t *staging, uint64_t staging_bytes, uint8_t *arena, uint64_t arena_bytes, const uint32_t *slots,
+    const uint64_t *sources, SqMoeExpertLoadParams p, const uint32_t *grid) {
+  if (blockIdx.x >= grid[0] || blockIdx.y >= grid[1] || blockIdx.z >= grid[2]) return;
+  const SqMoeExpertLoadProjection &q = p.projections[blockIdx.z];
+  const uint32_t G = q.columns / 32;
+  const uint64_t t = (uint64_t)blockIdx.x * SQ_MOE_EXPERT_LOAD_THREADS + threadIdx.x;
+  if (!q.rows || t >= (uint64_t)q.rows * G) return;
+  const uint32_t n = (uint32_t)(t / G), g = (uint32_t)(t % G);
+  const uint64_t slot = slots[blockIdx.y], source = sources[3 * (uint64_t)blockIdx.y + blockIdx.z];
+  const SqQuantFormat f = sq_format(q.format);
+  const uint64_t row_blocks = (uint64_t)q.columns / f.block_elements * f.block_bytes;
+  const uint64_t need[3] = {(uint64_t)q.rows * G * f.plane0_bytes, (uint64_t)q.rows * G * f.plane1_bytes,
+                            (uint64_t)q.rows * (G / f.meta_groups) * f.meta_bytes};
+  if (source > staging_bytes || (uint64_t)(q.rows - 1) * q.row_bytes + row_blocks > staging_bytes - source) return;
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+    if (need[i] && (q.planes[i] > arena_bytes || slot > (arena_bytes - q.planes[i]) / max(q.slot_bytes[i], (uint64_t)1) ||
+                    q.planes[i] + slot * q.slot_bytes[i] + need[i] > arena_bytes))
+      return;
+  repack_group(staging + source + (uint64_t)n * q.row_bytes, q.format, G, n, g, arena + q.planes[0] + slot * q.slot_bytes[0],
+               arena + q.planes[1] + slot * q.slot_bytes[1], arena + q.planes[2] + slot * q.slot_bytes[2]);
 }
 
 // MLX's own tensors: row n's codes a little-endian string of BITS-bit codes (group g of 32 is BITS words of the
@@ -176,6 +213,15 @@ __global__ void dequant_kernel(const uint8_t *plane0, const uint8_t *plane1, con
 }
 
 }  // namespace
+
+hipError_t launch_expert_load(const uint8_t *staging, uint64_t staging_bytes, uint8_t *arena, uint64_t arena_bytes,
+                              const uint32_t *slots, const uint64_t *sources, const SqMoeExpertLoadParams &p,
+                              uint32_t groups, uint32_t jobs, const uint32_t *grid, hipStream_t stream) {
+  if (!groups || !jobs) return hipSuccess;
+  hipLaunchKernelGGL(expert_load_kernel, dim3(groups, jobs, 3), dim3(SQ_MOE_EXPERT_LOAD_THREADS), 0, stream, staging,
+                     staging_bytes, arena, arena_bytes, slots, sources, p, grid);
+  return hipGetLastError();
+}
 
 hipError_t launch_repack(const uint8_t *src, uint8_t *dst, const SqGgufRepackParams &p, hipStream_t stream) {
   const uint64_t threads = (uint64_t)p.rows * (p.input_size / 32);

@@ -128,6 +128,15 @@ class MoeWeights(Structure):
                 ("shared_scalar_gate", Buffer), ("router", Segment)]
 
 
+class ExpertLoadProjection(Structure):
+    _fields_ = [("format_id", c_uint32), ("rows", c_uint32), ("columns", c_uint32), ("row_bytes", c_uint32),
+                ("planes", c_uint64 * 3), ("slot_bytes", c_uint64 * 3)]
+
+
+class ExpertLoadParams(Structure):
+    _fields_ = [("projections", ExpertLoadProjection * 3)]
+
+
 class MoeScratch(Structure):
     _fields_ = [(n, Buffer) for n in _MOE_WORKSPACE]
 
@@ -198,6 +207,8 @@ _SIGNATURES = {
     "sq_moe_add_routed": [c_void_p, POINTER(MoeBuffers), POINTER(MoeWeights), POINTER(MoePlan)],
     "sq_moe_add_routes": [c_void_p, Buffer, POINTER(Segment), Buffer, Buffer, Buffer, Buffer, c_uint32,
                           POINTER(MoeShape), c_uint32],
+    "sq_moe_expert_load": [c_void_p, Buffer, Buffer, Buffer, Buffer, POINTER(ExpertLoadParams), c_uint32, Buffer],
+    "sq_moe_expert_load_groups": [POINTER(ExpertLoadParams)],
 }
 
 
@@ -212,7 +223,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.argtypes = args
             fn.restype = (c_char_p if name in ("sq_last_error", "sq_version") else
-                          c_uint32 if name == "sq_moe_router_width" else c_int)
+                          c_uint32 if name in ("sq_moe_router_width", "sq_moe_expert_load_groups") else c_int)
         _lib = handle
     return _lib
 

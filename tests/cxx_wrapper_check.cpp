@@ -30,6 +30,10 @@ int main() {
   const MoePlan moe = MoE::decodePlan(shape, 2, MoE::config(shape, 16, SQ_PHASE_DECODE));
   const MoePlan moePrefill = MoE::prefillPlan(shape, 512, MoE::config(shape, 512, SQ_PHASE_PREFILL));
   std::printf("moe decode rows %u tile %u; moe prefill tile %u\n", moe.rows, moe.tile_rows, moePrefill.tile_rows);
+  sq_moe_expert_load_params load{};
+  load.projections[0] = {SQ_FMT_Q4K, 128, 512, 288, {0, 0, 0}, {1u << 20, 0, 1u << 20}};
+  load.projections[2] = {SQ_FMT_Q6K, 256, 256, 210, {0, 0, 0}, {1u << 20, 1u << 20, 1u << 20}};
+  std::printf("expert load groups %u\n", MoE::expertLoadGroups(load));
   try {
     (void)linear.decodePlan(p, 0);
     std::printf("no exception\n");

@@ -337,6 +337,7 @@ def test_cxx_face_plans_and_throws(tmp_path):
     out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
     assert "decode rows 8 tile 0" in out and "prefill tile 1" in out
     assert "moe decode rows 16 tile 8; moe prefill tile 32" in out
+    assert "expert load groups 8" in out   # max(128 x 16, 256 x 8) pairs / 256 threads
     assert "invalid_argument:" in out
 
 
@@ -498,3 +499,54 @@ def test_static_scratch_entry_point_refusals():
     buffers.prepared = sq.PreparedInput(_fake(16), sq.LINEAR_INPUT_HALF_ROWS)
     with pytest.raises(sq.InvalidArgument, match="prepared must be empty"):
         sq.call("sq_linear_add_static", None, sq.byref(buffers), sq.byref(proj), sq.byref(plan), None)
+
+
+def test_moe_expert_load_refusals():
+    """MoE::addExpertLoad validates its projections and buffers on the host before any launch; the groups follow
+    MoE::expertLoadGroups (MoE.cpp:545-551); no jobs launch nothing."""
+    params = sq.ExpertLoadParams()
+    for z, (fmt, rows, cols) in enumerate([(sq.FMT_Q4K, 128, 512), (sq.FMT_AF4G64, 64, 2048), (sq.FMT_Q6K, 256, 256)]):
+        q = params.projections[z]
+        q.format_id, q.rows, q.columns = fmt, rows, cols
+        q.row_bytes = cols // (256 if fmt in (sq.FMT_Q4K, sq.FMT_Q6K) else 64) * (144 if fmt == sq.FMT_Q4K else
+                                                                              210 if fmt == sq.FMT_Q6K else 36)
+        q.slot_bytes[0] = q.slot_bytes[1] = q.slot_bytes[2] = 1 << 20
+    assert sq.lib().sq_moe_expert_load_groups(sq.byref(params)) == 64 * 64 // 256
+    jobs = 4
+    good = dict(staging=_fake(1 << 24), arena=_fake(1 << 26, 1 << 30), slots=_fake(jobs * 4, 1 << 24),
+                sources=_fake(jobs * 24, 1 << 25), grid=_fake(12, 1 << 26), jobs=jobs)
+
+    def call(p=params, **kw):
+        a = {**good, **kw}
+        sq.call("sq_moe_expert_load", None, a["staging"], a["arena"], a["slots"], a["sources"], sq.byref(p),
+                a["jobs"], a["grid"])
+
+    def edited(z, **fields):
+        p = sq.ExpertLoadParams.from_buffer_copy(params)
+        for k, v in fields.items():
+            if k == "slot_bytes":
+                p.projections[z].slot_bytes[v[0]] = v[1]
+            else:
+                setattr(p.projections[z], k, v)
+        return p
+    call(jobs=0)   # nothing to launch
+    with pytest.raises(sq.InvalidArgument, match="gate takes a format"):
+        call(edited(0, format_id=99))
+    with pytest.raises(sq.InvalidArgument, match="up takes whole plane tiles"):
+        call(edited(1, rows=96))
+    with pytest.raises(sq.InvalidArgument, match="down takes whole plane tiles"):
+        call(edited(2, columns=384))
+    with pytest.raises(sq.InvalidArgument, match="gate rows are shorter"):
+        call(edited(0, row_bytes=100))
+    with pytest.raises(sq.InvalidArgument, match="down slots are smaller"):
+        call(edited(2, slot_bytes=(1, 256 * 8 * 8 - 1)))
+    with pytest.raises(sq.InvalidArgument, match="expert load slots"):
+        call(slots=_fake(jobs * 4 - 4, 1 << 24))
+    with pytest.raises(sq.InvalidArgument, match="expert load sources"):
+        call(sources=_fake(jobs * 24 - 8, 1 << 25))
+    with pytest.raises(sq.InvalidArgument, match="expert load grid"):
+        call(grid=_fake(8, 1 << 26))
+    with pytest.raises(sq.InvalidArgument, match="8-byte"):
+        call(sources=_fake(jobs * 24, (1 << 25) + 4))
+    with pytest.raises(sq.InvalidArgument, match="staging and arena"):
+        call(staging=sq.Buffer())

@@ -174,3 +174,95 @@ def test_mlx_repack_8bit():
     t.cuda.synchronize()
     assert np.array_equal(p0.cpu().numpy(), plane0)
     assert np.array_equal(m.cpu().numpy(), meta)
+
+
+def _expert_load_layout(projections, slots):
+    """ExpertLoadParams for projections [(fmt, rows, columns)] with `slots` slots each: each plane of each projection
+    a run of slots in the arena, slot_bytes its plane's bytes rounded up to 256. Returns (params, arena bytes)."""
+    params, at = sq.ExpertLoadParams(), 0
+    for z, (fmt, rows, columns) in enumerate(projections):
+        q = params.projections[z]
+        q.format_id, q.rows, q.columns, q.row_bytes = fmt, rows, columns, oracle.row_bytes(fmt, columns)
+        p0, m = oracle.plane_sizes(fmt, rows, columns)
+        for i, need in enumerate((p0, oracle.plane1_size(fmt, rows, columns), m)):
+            q.slot_bytes[i] = -(-need // 256) * 256
+            q.planes[i] = at
+            at += slots * q.slot_bytes[i]
+    return params, at
+
+
+def _expert_load(staging, arena, slots, sources, params, jobs, grid):
+    sq.call("sq_moe_expert_load", sq.stream_handle(), sq.view(staging), sq.view(arena), sq.view(slots),
+            sq.view(sources), sq.byref(params), jobs, sq.view(grid))
+
+
+def test_moe_expert_load_matches_repack():
+    """MoE::addExpertLoad (moe_expert_load, gguf_repack.metal:239-257): jobs' gate (Q4_K), up (Q5_K, with plane1)
+    and down (Q6_K) native rows, staged at their sources, land in their slots' planes as the oracle's repack writes
+    them; the slots of jobs past the grid's live count, the other slots and the padding keep their bytes."""
+    projections = [(oracle.FMT_Q4K, 128, 512), (oracle.FMT_Q5K, 128, 512), (oracle.FMT_Q6K, 256, 256)]
+    params, arena_bytes = _expert_load_layout(projections, 8)
+    assert sq.lib().sq_moe_expert_load_groups(sq.byref(params)) == max(
+        -(-r * (c // 32) // 256) for _, r, c in projections)
+    jobs, live, slot_of = 4, 3, [5, 2, 7, 0]
+    natives, sources, staged = {}, [], []
+    at = 0
+    for j in range(jobs):
+        for z, (fmt, rows, columns) in enumerate(projections):
+            natives[j, z] = oracle.fixture(fmt, rows, columns, 100 + 3 * j + z)
+            at += 48   # a gap between sources
+            sources.append(at)
+            staged.append((at, natives[j, z]))
+            at += natives[j, z].size
+    staging = np.zeros(at + 64, np.uint8)
+    for off, native in staged:
+        staging[off: off + native.size] = native
+    t = torch()
+    arena = t.full((arena_bytes,), 0xAB, dtype=t.uint8, device="cuda")
+    grid = to_device(np.array([sq.lib().sq_moe_expert_load_groups(sq.byref(params)), live, 3], np.uint32))
+    _expert_load(to_device(staging), arena, to_device(np.array(slot_of, np.uint32)),
+                 t.from_numpy(np.array(sources, np.int64)).cuda(), params, jobs, grid)
+    t.cuda.synchronize()
+    got = arena.cpu().numpy()
+    want = np.full(arena_bytes, 0xAB, np.uint8)
+    for j in range(live):
+        for z, (fmt, rows, columns) in enumerate(projections):
+            plane0, plane1, meta, _ = oracle.repack_planes(fmt, natives[j, z], rows, columns)
+            q = params.projections[z]
+            for i, plane in enumerate((plane0, plane1, meta)):
+                if plane is None:
+                    continue
+                start = q.planes[i] + slot_of[j] * q.slot_bytes[i]
+                want[start: start + plane.size] = plane
+    assert np.array_equal(got, want)
+
+
+def test_moe_expert_load_skips_jobs_outside_its_buffers():
+    """A job whose staged rows would run past the staging buffer, or whose slot's planes would run past the arena,
+    writes nothing; a projection of no rows is skipped; the other jobs land as the oracle repacks them."""
+    projections = [(oracle.FMT_AF4G64, 64, 256), (oracle.FMT_AF4G64, 0, 256), (oracle.FMT_Q80, 64, 256)]
+    params, arena_bytes = _expert_load_layout(projections, 2)
+    natives = [oracle.fixture(fmt, max(rows, 64), columns, 7 + z) for z, (fmt, rows, columns) in enumerate(projections)]
+    staging = np.concatenate(natives)
+    offsets = np.cumsum([0] + [n.size for n in natives[:-1]])
+    t = torch()
+    arena = t.full((arena_bytes,), 0x5A, dtype=t.uint8, device="cuda")
+    # Job 0: slot 1, every source in range. Job 1: the gate's source past the staging, the down's in range but into
+    # slot 9, past the arena. Job 2: slot 0, the down's source one byte short of its rows.
+    sources = np.array([offsets[0], 0, offsets[2],
+                        staging.size - 16, 0, offsets[2],
+                        offsets[0], 0, staging.size - natives[2].size + 1], np.int64)
+    slot_of = np.array([1, 9, 0], np.uint32)
+    grid = to_device(np.array([sq.lib().sq_moe_expert_load_groups(sq.byref(params)), 3, 3], np.uint32))
+    _expert_load(to_device(staging), arena, to_device(slot_of), t.from_numpy(sources).cuda(), params, 3, grid)
+    t.cuda.synchronize()
+    got = arena.cpu().numpy()
+    want = np.full(arena_bytes, 0x5A, np.uint8)
+    for j, z in ((0, 0), (0, 2), (2, 0)):
+        fmt, rows, columns = projections[z]
+        plane0, _, meta, _ = oracle.repack_planes(fmt, natives[z], rows, columns)
+        q = params.projections[z]
+        for i, plane in ((0, plane0), (2, meta)):
+            start = q.planes[i] + int(slot_of[j]) * q.slot_bytes[i]
+            want[start: start + plane.size] = plane
+    assert np.array_equal(got, want)
