@@ -127,13 +127,25 @@ MoePlan MoE::decodeRows(MoeShape shape, uint32_t rows) {
 
 void MoE::add(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
   validate(b, w, plan);
+  // Where gate and up share a format (routed, and shared if any), the gate/up pass is one gathering pass and the
+  // expert-output scratch is free until the down pass writes it: the route select then writes the input rows in the
+  // tiles' read order there, and the routed work skips its own input-rows dispatch. (Gate and up of different
+  // formats park the gate's output in that scratch, so they keep the separate dispatch.)
+  const MoeShape s = plan.shape();
+  const bool onePass = w.gate.formatId == w.up.formatId &&
+                       (!s.sharedSlices || w.sharedGate.formatId == w.sharedUp.formatId);
+  if (onePass) {
+    addRouting(graph, b, w, plan, b.scratch.expertOutput);
+    addRouted(graph, b, w, plan, true);
+    return;
+  }
   addRouting(graph, b, w, plan);
   addRouted(graph, b, w, plan);
 }
 
 void MoE::addRoutes(hipStream_t graph, Buffer input, const QuantizedSegment &router, Buffer sharedScalarGate,
                     Buffer scores, Buffer selected, Buffer routingWeights, uint32_t rows, MoeShape s,
-                    FloatTile routerTile) {
+                    FloatTile routerTile, Buffer rowsTable) {
   if (!s.valid()) throw std::invalid_argument("invalid MoE routing shape");
   if (!rows || rows > SQ_PREFILL_TOKEN_BUDGET) throw std::invalid_argument("invalid MoE routing rows");
   if (router.plane0 && (!router.isFloat() || router.outputSize != s.experts || router.inputSize != s.hiddenSize))
@@ -147,8 +159,9 @@ void MoE::addRoutes(hipStream_t graph, Buffer input, const QuantizedSegment &rou
   if (s.sharedGate) requireBytes(sharedScalarGate, uint64_t{s.hiddenSize} * 4, "MoE shared scalar gate weight");
   // The select kernel reads the scores and the shared gate's input rows in 16-byte vectors.
   const auto aligned = [](const Buffer &buffer) { return (reinterpret_cast<uintptr_t>(buffer.ptr) & 15u) == 0; };
-  if (!aligned(input) || !aligned(scores) || !aligned(sharedScalarGate))
+  if (!aligned(input) || !aligned(scores) || !aligned(sharedScalarGate) || !aligned(rowsTable))
     throw std::invalid_argument("MoE routing input, scores and shared scalar gate are 16-byte aligned");
+  if (rowsTable) requireBytes(rowsTable, uint64_t{rows} * s.hiddenSize * 2, "MoE input rows table");
   // The router's fp32 scores, rows of routerWidth() (MoE.cpp:527-543), when the block carries its rows; else the
   // caller wrote them there.
   if (router.plane0) addGgufFloat(graph, input, router, scores, rows, stride, 0, FloatOutput::Float32, routerTile);
@@ -156,7 +169,7 @@ void MoE::addRoutes(hipStream_t graph, Buffer input, const QuantizedSegment &rou
   launched(kern::launch_moe_route_select(scores.as<const float>(), stride, selected.as<uint32_t>(),
                                          routingWeights.as<float>(), route, input.as<const uint16_t>(),
                                          s.sharedGate ? sharedScalarGate.as<const float>() : nullptr,
-                                         uint32_t(s.router), s.sharedSlices, graph),
+                                         uint32_t(s.router), s.sharedSlices, rowsTable.as<uint16_t>(), graph),
            "MoE route select");
 }
 
@@ -205,13 +218,14 @@ void MoE::addExpertLoad(hipStream_t graph, Buffer staging, Buffer arena, Buffer 
            "MoE expert load");
 }
 
-void MoE::addRouting(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
+void MoE::addRouting(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan,
+                     Buffer rowsTable) {
   validate(b, w, plan);
   const MoeShape s = plan.shape();
   const MoeScratch &sc = b.scratch;
   // The scores live in the grouped input (MoE.cpp:445-459).
   addRoutes(graph, b.input, w.router, s.sharedGate ? w.sharedScalarGate : Buffer{}, sc.groupedInput,
-            sc.selectedExperts, sc.routingWeights, plan.rows(), s, plan.configuration().ggufRouterTile);
+            sc.selectedExperts, sc.routingWeights, plan.rows(), s, plan.configuration().ggufRouterTile, rowsTable);
   const SqMoeGroupParams group{plan.rows(), s.expertsPerToken, plan.tileRows(), s.experts,
                                s.expertIntermediateSize / SQ_TILE_COLUMNS, s.hiddenSize / SQ_TILE_COLUMNS,
                                SQ_TARGET_VERIFY_ROWS, 0};
@@ -222,7 +236,8 @@ void MoE::addRouting(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w
            "MoE grouping");
 }
 
-void MoE::addRouted(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan) {
+void MoE::addRouted(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w, const MoePlan &plan,
+                    bool rowsReady) {
   validate(b, w, plan);
   const MoeShape s = plan.shape();
   const MoeScratch &sc = b.scratch;
@@ -262,10 +277,14 @@ void MoE::addRouted(hipStream_t graph, const MoeBuffers &b, const MoeWeights &w,
   };
   // The block's input rows in the tiles' read order, over the router's scores (MoE.cpp:480-517 opens the same way
   // with its gather).
-  launched(kern::launch_moe_input_rows(b.input.as<const uint16_t>(), plan.rows(), s.hiddenSize,
-                                       sc.groupedInput.as<uint16_t>(), graph),
-           "MoE input rows");
-  a.input = sc.groupedInput.as<const uint16_t>();
+  if (rowsReady) {
+    a.input = sc.expertOutput.as<const uint16_t>();
+  } else {
+    launched(kern::launch_moe_input_rows(b.input.as<const uint16_t>(), plan.rows(), s.hiddenSize,
+                                         sc.groupedInput.as<uint16_t>(), graph),
+             "MoE input rows");
+    a.input = sc.groupedInput.as<const uint16_t>();
+  }
   a.K = s.hiddenSize;
   a.output_size = s.expertIntermediateSize;
   a.gather = 1;

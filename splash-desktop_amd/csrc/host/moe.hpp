@@ -118,8 +118,12 @@ struct MoE {
   [[nodiscard]] static MoePlan decodePlan(MoeShape shape, uint32_t lanes, MoeConfig config);
   [[nodiscard]] static MoePlan decodeRows(MoeShape shape, uint32_t rows);
   static void add(hipStream_t graph, const MoeBuffers &buffers, const MoeWeights &weights, const MoePlan &plan);
-  static void addRouting(hipStream_t graph, const MoeBuffers &buffers, const MoeWeights &weights, const MoePlan &plan);
-  static void addRouted(hipStream_t graph, const MoeBuffers &buffers, const MoeWeights &weights, const MoePlan &plan);
+  // rowsTable (MoE::add's fusion): the route select also writes the block's input rows in the tiles' read order
+  // there, and addRouted with rowsReady reads them from the expert-output scratch instead of writing them itself.
+  static void addRouting(hipStream_t graph, const MoeBuffers &buffers, const MoeWeights &weights, const MoePlan &plan,
+                         Buffer rowsTable = {});
+  static void addRouted(hipStream_t graph, const MoeBuffers &buffers, const MoeWeights &weights, const MoePlan &plan,
+                        bool rowsReady = false);
   // MoE::addRoutes (MoE.hpp:403-411; MoE.cpp:527-543): the routing of `rows` rows of `input` with no plan and no
   // grouping. With router rows (F32 or BF16, [experts][hidden]) it projects the input onto them into `scores` (rows of
   // shape.routerWidth() fp32 slots) on `routerTile`; with a null router it reads the scores already there. Then each
@@ -127,7 +131,7 @@ struct MoE {
   // (shape.routesPerToken() per row). `sharedScalarGate` (fp32 [hidden]) is read only for a gated shared expert.
   static void addRoutes(hipStream_t graph, Buffer input, const QuantizedSegment &router, Buffer sharedScalarGate,
                         Buffer scores, Buffer selected, Buffer routingWeights, uint32_t rows, MoeShape shape,
-                        FloatTile routerTile);
+                        FloatTile routerTile, Buffer rowsTable = {});
   // MoE::addExpertLoad (MoE.hpp:411-420): up to `jobs` streamed experts' gate, up and down native rows from
   // `staging` repacked into their slots of `arena` (moe_expert_load); `slots`, `sources` and `grid` are device
   // buffers an earlier dispatch may write. Validates the projections and the buffers' sizes before the launch.

@@ -137,9 +137,12 @@ hipError_t launch_mlx_repack(uint32_t fmt, const uint32_t *weight, const uint16_
                              uint32_t rows, uint32_t K, uint8_t *plane0, uint8_t *meta, hipStream_t stream);
 
 // MoE.
+// With rows_table set, each row's wave also writes its input row in the expert tiles' read order there (what
+// launch_moe_input_rows writes), so MoE::add needs no separate dispatch for it.
 hipError_t launch_moe_route_select(const float *scores, uint32_t score_stride, uint32_t *selected,
                                    float *routing_weights, const SqMoeRouteParams &params, const uint16_t *input,
-                                   const float *shared_gate, uint32_t router, uint32_t shared, hipStream_t stream);
+                                   const float *shared_gate, uint32_t router, uint32_t shared, uint16_t *rows_table,
+                                   hipStream_t stream);
 hipError_t launch_moe_group(const uint32_t *selected, SqMoeTileDescriptor *tiles, SqMoeTileCount *tile_count,
                             uint32_t *grouped_routes, uint32_t *route_rows, const uint32_t *verify_rows,
                             const SqMoeGroupParams &params, uint32_t shared, hipStream_t stream);

@@ -37,12 +37,25 @@ __device__ __forceinline__ uint32_t wave_reduce(uint32_t v, Op op) {
 // 2^((s_r - s_0) log2 e) / sum_o 2^((s_o - s_0) log2 e), SigmoidNormalized weight_r = sigmoid(s_r) /
 // (sum_o sigmoid(s_o) + 1e-20). The row's routes top_k .. top_k + shared - 1 are the shared expert's slices (ids
 // experts on), each weighted by sigmoid(x . g) of the block's fp32 scalar gate g (gated) or by 1.
-__global__ __launch_bounds__(64) void route_select_kernel(const float *scores, uint32_t stride, uint32_t *selected,
+__global__ __launch_bounds__(128) void route_select_kernel(const float *scores, uint32_t stride, uint32_t *selected,
                                                           float *weights, SqMoeRouteParams p, const uint16_t *input,
-                                                          const float *shared_gate, uint32_t router, uint32_t shared) {
+                                                          const float *shared_gate, uint32_t router, uint32_t shared,
+                                                          uint16_t *rows_table) {
   constexpr int kPer = SQ_MOE_WIDE_EXPERT_SLOTS / 64;
-  const uint32_t row = blockIdx.x, lane = threadIdx.x, per_row = p.top_k + shared;
+  const uint32_t row = blockIdx.x, lane = threadIdx.x & 63, per_row = p.top_k + shared;
   const size_t base = (size_t)row * per_row;
+  if (threadIdx.x >= 64) {
+    // The second wave (launched with rows_table only): the row in the tiles' read order (input_rows_kernel's 16-byte
+    // chunks, lane l the row's chunks l, l + 64, ...), beside the first wave's selection.
+    const uint16_t *xr = input + (size_t)row * p.input_size;
+    uint16_t *out = rows_table + (size_t)row * p.input_size;
+    for (uint32_t i = lane; i < p.input_size / 8; i += 64) {
+      const uint32_t *in = (const uint32_t *)(xr + 32 * (i / 4)) + 2 * (i % 4);
+      const u32x2 lo = *(const u32x2 *)in, hi = *(const u32x2 *)(in + 8);
+      *(u32x4 *)(out + 8 * i) = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+    return;
+  }
   if (shared) {
     float gate = 1.0f;
     if (shared_gate) {
@@ -103,7 +116,10 @@ __global__ __launch_bounds__(64) void route_select_kernel(const float *scores, u
       ordered[rank] = top;
     }
   }
-  __syncthreads();
+  // One wave selects (a second one, if any, returned above): lane 0's LDS writes reach its other lanes.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   for (uint32_t rank = lane; rank < p.top_k; rank += 64) {
     float denominator = 0.0f;
     if (router == SQ_MOE_ROUTER_SOFTMAX) {
@@ -557,9 +573,10 @@ hipError_t launch_expert_format(const MoeExpertArgs &a, hipStream_t stream) {
 
 hipError_t launch_moe_route_select(const float *scores, uint32_t stride, uint32_t *selected, float *weights,
                                    const SqMoeRouteParams &p, const uint16_t *input, const float *shared_gate,
-                                   uint32_t router, uint32_t shared, hipStream_t stream) {
-  hipLaunchKernelGGL(route_select_kernel, dim3(p.rows), dim3(64), 0, stream, scores, stride, selected, weights, p,
-                     input, shared_gate, router, shared);
+                                   uint32_t router, uint32_t shared, uint16_t *rows_table, hipStream_t stream) {
+  if (rows_table && p.input_size % 32) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(route_select_kernel, dim3(p.rows), dim3(rows_table ? 128 : 64), 0, stream, scores, stride,
+                     selected, weights, p, input, shared_gate, router, shared, rows_table);
   return hipGetLastError();
 }
 
