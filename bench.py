@@ -20,7 +20,8 @@ Also reported on the same line: the config-1 sweep (M in 1..16 over the four 8B 
 prefill GEMM at M = 2048 (TFLOPS), the config-3 Q4_K shapes, the config-4 MoE block and the CPU baseline (the
 oracle's threaded C implementation of the same quantized matmul on this host's cores, over a bounded sample).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--sections LIST] [--calibrate-copy]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--sections LIST] [--sweep-points LIST]
+[--calibrate-copy]
 (--sections: a comma list of sweep, prefill, q4k, formats, moe, cpu; the headline always runs, and every section runs
 by default. It picks which benchmarks run, for profiling one of them; it changes nothing inside any timed region.)
 """
@@ -434,6 +435,9 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true", help="also run a plain copy of known size (counters)")
     ap.add_argument("--sections", default="sweep,prefill,q4k,formats,moe,cpu",
                     help="benchmarks beside the headline: sweep, prefill, q4k, formats, moe, cpu")
+    ap.add_argument("--sweep-points", default="",
+                    help="restrict the sweep to these points (a comma list of its keys, e.g. K4096xN1024_M8), for a "
+                         "profiler run of one shape")
     args = ap.parse_args()
     sections = set() if args.quick else {v.strip() for v in args.sections.split(",") if v.strip()}
     unknown = sections - {"sweep", "prefill", "q4k", "formats", "moe", "cpu"}
@@ -488,8 +492,11 @@ def main() -> int:
     extra = {}
     if "sweep" in sections:
         sweep = {}
+        points = {v.strip() for v in args.sweep_points.split(",") if v.strip()}
         for (kk, nn) in ((4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)):
             for mm in (1, 2, 4, 8, 16):
+                if points and f"K{kk}xN{nn}_M{mm}" not in points:
+                    continue
                 s, p = bench_gemv(torch, sq, synthetic, sq.FMT_AF4G64, mm, nn, kk, max(50, args.steps // 2), 10)
                 g = gemv_bytes(mm, nn, kk) / s / 1e9
                 sweep[f"K{kk}xN{nn}_M{mm}"] = {"us": round(s * 1e6, 2), "GB/s": round(g, 1),
@@ -498,6 +505,8 @@ def main() -> int:
         # The small shapes' floors: the streaming kernel over each M=1 point's own bytes (best launch shape) and the
         # empty dispatch, timed alike. Below ~10 MB a dispatch's fixed cost is most of its time.
         for (kk, nn) in ((4096, 4096), (4096, 1024)):
+            if any(f"K{kk}xN{nn}_M{mm}" not in sweep for mm in (1, 8, 16)):
+                continue
             f = stream_floor(torch, sq, int(gemv_bytes(1, nn, kk)), max(50, args.steps // 2), 10)
             for mm in (1, 8, 16):
                 # Each point's own bytes at the rate the streaming kernel reaches over this shape's.
