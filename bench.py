@@ -347,17 +347,29 @@ def cpu_baseline(sq, synthetic, budget_s: float) -> dict:
             weights[key] = oracle.repack(fmt, native, n, k)[:2]
         return weights[key]
 
-    def timed(fmt, m, n, k, seed=3, reps=None):
+    # The kernels this CPU runs; each config reports the fastest of them (which one wins depends on the CPU and the
+    # rows: on a Zen 5 host the fp32 kernel leads at M = 1, the bf16 dot products at more rows).
+    isas = [isa for isa in ("avx512bf16", "avx512f", "avx2+fma") if pool.set_isa(isa)] or [pool.isa]
+    fastest = {}
+
+    def timed(fmt, m, n, k, seed=3, reps=None, key=None):
         p0, meta = planes(fmt, n, k, seed)
         x = synthetic.activations(rng, m, k)
         pool.reserve(m, k)
         out = np.zeros((m, n), np.uint16)
-        pool.matmul(fmt, x, p0, meta, n, out)   # warm-up: pages and caches
-        best, total, count = float("inf"), 0.0, 0
-        while count < (reps or 50) and (total < budget_s / 10 or count < 2):
-            _, sec = pool.matmul(fmt, x, p0, meta, n, out)
-            best, total, count = min(best, sec), total + sec, count + 1
-        return best, count
+        best_all, count_all = float("inf"), 0
+        for isa in isas:
+            pool.set_isa(isa)
+            pool.matmul(fmt, x, p0, meta, n, out)   # warm-up: pages and caches
+            best, total, count = float("inf"), 0.0, 0
+            while count < (reps or 50) and (total < budget_s / 10 / len(isas) or count < 2):
+                _, sec = pool.matmul(fmt, x, p0, meta, n, out)
+                best, total, count = min(best, sec), total + sec, count + 1
+            if key is not None:
+                fastest.setdefault(key, {})[isa] = best
+            if best < best_all:
+                best_all, count_all = best, count
+        return best_all, count_all
 
     configs = {}
     af4 = oracle.FMT_AF4G64
@@ -366,16 +378,19 @@ def cpu_baseline(sq, synthetic, budget_s: float) -> dict:
                                  "c1_M16_K4096xN14336": (af4, 16, 14336, 4096),
                                  "c3_q4k_M1_K5120xN27648": (oracle.FMT_Q4K, 1, 27648, 5120),
                                  "c3_q4k_M16_K5120xN27648": (oracle.FMT_Q4K, 16, 27648, 5120)}.items():
-        sec, count = timed(fmt, m, n, k)
-        configs[name] = {"ms": round(sec * 1e3, 3), "GB/s": round(gemv_bytes(m, n, k) / sec / 1e9, 2), "runs": count}
+        sec, count = timed(fmt, m, n, k, key=name)
+        isa = min(fastest[name], key=fastest[name].get)
+        configs[name] = {"ms": round(sec * 1e3, 3), "GB/s": round(gemv_bytes(m, n, k) / sec / 1e9, 2), "runs": count,
+                         "isa": isa}
     for name, (fmt, rows, n, k) in {"c2_M2048_K4096xN14336": (af4, 2048, 14336, 4096),
                                     "c2_M2048_K14336xN4096": (af4, 2048, 4096, 14336),
                                     "c2_M2048_K5120xN27648": (af4, 2048, 27648, 5120),
                                     "c3_q4k_M512_K5120xN27648": (oracle.FMT_Q4K, 512, 27648, 5120)}.items():
-        sec, count = timed(fmt, 64, n, k, reps=2)
+        sec, count = timed(fmt, 64, n, k, reps=2, key=name)
         gflops = 2 * 64 * n * k / sec / 1e9
         configs[name] = {"sample": "64 of the chunk's rows", "GFLOPS": round(gflops, 1),
-                         "ms_for_whole_chunk": round(2 * rows * n * k / gflops / 1e6, 1), "runs": count}
+                         "ms_for_whole_chunk": round(2 * rows * n * k / gflops / 1e6, 1), "runs": count,
+                         "isa": min(fastest[name], key=fastest[name].get)}
     # c4: gate, up (768 x 2048) and down (2048 x 768) of 8 experts on 32 routed rows each.
     expert_sec = 0.0
     for e in range(8):
@@ -389,18 +404,14 @@ def cpu_baseline(sq, synthetic, budget_s: float) -> dict:
                                         "ms": round(block_sec * 1e3, 2),
                                         "GB/s": round(expert_bytes / block_sec / 1e9, 2)}
     head = configs["c1_M1_K4096xN14336"]
-    # The headline on every kernel the CPU runs (the figures above use the first, the pool's own).
-    by_isa = {pool.isa: head["GB/s"]}
-    chosen = pool.isa
-    for isa in ("avx512bf16", "avx512f", "avx2+fma"):
-        if isa != chosen and pool.set_isa(isa):
-            sec, _ = timed(af4, 1, 14336, 4096)
-            by_isa[isa] = round(gemv_bytes(1, 14336, 4096) / sec / 1e9, 2)
-    pool.set_isa(chosen)
+    # The headline on every kernel the CPU runs (value: the fastest).
+    by_isa = {isa: round(gemv_bytes(1, 14336, 4096) / sec / 1e9, 2)
+              for isa, sec in fastest["c1_M1_K4096xN14336"].items()}
+    pool.set_isa(head["isa"])
     out = {"value": head["GB/s"], "unit": "GB/s", "cores": pool.threads, "kind": "port",
            "sample": f"best of {head['runs']} runs of the M=1 K4096xN14336 af4g64 GEMV (BASELINE config 1) on "
-                     f"{pool.threads} threads ({pool.isa}); oracle/sq_cpu.c",
-           "isa": pool.isa, "headline_GB/s_by_isa": by_isa, "cpu": _cpu_model(), "host_threads": host_threads,
+                     f"{pool.threads} threads ({head['isa']}, the fastest of {', '.join(isas)}); oracle/sq_cpu.c",
+           "isa": head["isa"], "headline_GB/s_by_isa": by_isa, "cpu": _cpu_model(), "host_threads": host_threads,
            "usable_threads": usable, "threads_used": pool.threads, "configs": configs}
     pool.close()
     return out
