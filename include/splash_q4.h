@@ -14,7 +14,7 @@
  *    MoE.h): Q4_K (0), Q5_K (3), Q6_K (4), Q8_0 (6), MLX affine 4-bit in groups of 32, 64 and 128 (25, 26, 27)
  *    and MLX affine 8-bit in groups of 64 (35), in every entry point.
  *  - Split scratch (partials, counters) is reused serially on one stream: counters are zero at allocation and every
- *    split dispatch returns them to zero; two streams never share one scratch.
+ *    split or stream dispatch returns them to zero; two streams never share one scratch.
  * Reference interfaces each entry point replaces are named in its comment (paths under the reference checkout).
  */
 #ifndef SPLASH_Q4_H
@@ -91,7 +91,10 @@ typedef struct sq_linear_plan {
 
 /* LinearScratch / LinearScratchSize / LinearBuffers (runtime/ops/Linear.hpp:125-162,216-226). A decode plan's
  * partials hold its K splits' fp32 sums; a prefill plan's, where its tiles' K is halved (projections of 64 to 128
- * tiles of 256 rows by 256 columns, K a multiple of 512), the two halves' fp32 sums [2][rows][N]. */
+ * tiles of 256 rows by 256 columns, K a multiple of 512), the two halves' fp32 sums [2][rows][N], and where its
+ * tiles number more than one round over the 256 compute units (K a multiple of 256), the fp32 sums of the last
+ * round's stream pieces (128 MiB: two 256 x 256 tiles of sums for each of 256 workgroups) with a 4-byte counter
+ * a stream tile. */
 typedef struct sq_linear_scratch_size {
   uint64_t input, sums, partials, counters, rotated;
 } sq_linear_scratch_size;
@@ -174,7 +177,10 @@ int sq_require_segment_planes(const sq_segment *segment, const char *what, uint3
  * partials are 16-byte aligned and its row scales (scratch sums) 4-byte aligned. Whether a prefill halves its tiles'
  * K depends on the chunk's rows as well as the shape (a 4096-input, 14336-output projection halves from 257 to 512
  * rows), so a row's output bits may differ between chunks of different row counts; each lies within the row's fp64
- * interval. A decode row's bits depend only on the shape and the tile kind its rows run (1..4 rows, 5..16, 17..32). */
+ * interval. The same holds for the tiles past a prefill's whole rounds over the compute units, whose K runs in
+ * pieces on several workgroups (their sums add in K order whatever order the pieces finish in, so a chunk's bits
+ * repeat from run to run). A decode row's bits depend only on the shape and the tile kind its rows run (1..4 rows,
+ * 5..16, 17..32). */
 int sq_linear_add(void *graph, const sq_linear_buffers *buffers, const sq_projection *projection,
                   const sq_linear_plan *plan, const sq_projection *gate);
 /* Linear::add with its result: *prepared (may be NULL) receives what the scratch table describes after the

@@ -182,7 +182,8 @@ uint32_t LinearPlan::storageRows() const noexcept {
 
 // Decode tile: [split][row][column] fp32 partials and a counter per 64 destination columns (LinearGguf.cpp:432-453).
 // Prefill tile: the activations in fp16 and one fp32 scale per row, which its prepare dispatch writes, and where the
-// projection halves its tiles' K the fp32 sums of both halves (kern::prefill_split).
+// projection halves its tiles' K the fp32 sums of both halves (kern::prefill_split), or where its tiles may run past
+// a round as stream pieces the pieces' fp32 sums and a counter a stream tile (kern::prefill_stream).
 LinearScratchSize LinearPlan::scratchSize() const noexcept {
   const auto [n, k] = workload_.matrix;
   if (config_.tile == LinearTile::GgufPrefill) {
@@ -338,11 +339,12 @@ PreparedInput Linear::add(hipStream_t graph, LinearBuffers b, const Projection &
   if (gate) requireSegments(*gate, w.matrix);
   if (selected.configuration().tile == LinearTile::GgufPrefill) {
     // The prefill tile moves activations, outputs, epilogue operands, the table and a halved tile's fp32 partials in
-    // 16-byte vectors (the row scales in 4-byte words).
+    // 16-byte vectors (the row scales and a stream dispatch's counters in 4-byte words).
     const auto aligned = [](const Buffer &buffer) { return (reinterpret_cast<uintptr_t>(buffer.ptr) & 15u) == 0; };
     if (!aligned(b.input) || !aligned(b.output) || !aligned(b.residual) || !aligned(b.gateScratch) ||
         !aligned(b.scratch.input) || !aligned(b.scratch.partials) ||
-        (reinterpret_cast<uintptr_t>(b.scratch.sums.ptr) & 3u))
+        (reinterpret_cast<uintptr_t>(b.scratch.sums.ptr) & 3u) ||
+        (reinterpret_cast<uintptr_t>(b.scratch.counters.ptr) & 3u))
       throw std::invalid_argument("prefill projection buffers are 16-byte aligned");
   }
   const std::vector<QuantizedSegment> &segments = p.blocks().segments;
@@ -406,6 +408,7 @@ PreparedInput Linear::add(hipStream_t graph, LinearBuffers b, const Projection &
       a.rows = w.rows;
       a.out_stride = n;
       a.partials = b.scratch.partials.as<float>();
+      a.counters = b.scratch.counters.as<uint32_t>();
       requireLaunch(kern::launch_prefill(group.front()->formatId, epilogueOf(w.epilogue), a, graph), "prefill tile");
     }
     return {b.input, LinearInput::HalfRows};

@@ -81,9 +81,13 @@ struct PrefillArgs {
   uint16_t *output;            // bf16 [rows][out_stride]
   const uint16_t *aux;
   uint32_t K, rows, out_stride;
-  float *partials;             // a split dispatch's fp32 pieces (prefill_scratch_bytes)
+  float *partials;             // a split or stream dispatch's fp32 pieces (prefill_scratch_bytes)
+  uint32_t *counters;          // a stream dispatch's counter a stream tile, zero between dispatches
   uint32_t column_group0;      // set by launch_prefill: the dispatch's first column group,
   uint32_t split_at, split_columns;   // the step its pieces are cut at, the partial planes' row length
+  // Set by launch_prefill for a stream dispatch (prefill_stream): its whole tiles, its stream tiles, the steps of a
+  // range and the row blocks.
+  uint32_t stream_dp, stream_tiles, stream_range, stream_row_blocks;
 };
 hipError_t launch_prefill(uint32_t fmt, uint32_t epilogue, const PrefillArgs &args, hipStream_t stream);
 // The prefill dispatch's shape: tiles of bm rows (128 or 256) by four plane tiles, row_blocks x column_groups of
@@ -96,8 +100,15 @@ struct PrefillSchedule {
   uint32_t bm, split, row_blocks, column_groups, whole_groups, split_at;
 };
 bool prefill_split(uint32_t rows, uint32_t plane_tiles, uint32_t K);
+// A whole-K dispatch's stream schedule: its first dp_tiles tiles whole, the next stream_tiles as pieces of `range`
+// steps, `workgroups` workgroups in all (none: stream_tiles 0).
+struct PrefillStream {
+  uint32_t dp_tiles, stream_tiles, range, workgroups;
+};
+PrefillStream prefill_stream(uint32_t row_blocks, uint32_t column_groups, uint32_t K);
 PrefillSchedule prefill_schedule(uint32_t rows, uint32_t plane_tiles, uint32_t K, bool split);
-// The partials (and counters: none) a prefill of `rows` over a projection of `plane_tiles` plane tiles uses.
+// The partials and counters a prefill of `rows` over a projection of `plane_tiles` plane tiles uses (halved K:
+// partials only; a stream dispatch: both).
 struct PrefillScratch {
   uint64_t partials, counters;
 };

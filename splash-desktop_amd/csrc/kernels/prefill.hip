@@ -265,11 +265,65 @@ static_assert(kMicroTable<4>.op[micro_ops<4>() - 1].kind == 3 && kMicroTable<4>.
 static_assert(kMicroTable<2>.op[micro_ops<2>() - 1].kind == 3 && kMicroTable<2>.op[micro_ops<2>() - 1].arg == 7,
               "26 micro-operations for two words");
 
-// SPLIT: the tile's K is cut between the two workgroups of blockIdx.z (steps [0, split_at) and [split_at, K / 64)),
-// whose fp32 sums a close dispatch adds (prefill_schedule).
-template <uint32_t FMT, uint32_t EP, int BM, bool SPLIT, int W>
+// Raw buffer access (the descriptor's last dword for untyped dword access on CDNA3/4): loads past `bytes` read
+// zero and stores past it are dropped. kCoherent is the sc1 cache policy, the agent-scope coherence an agent-scope
+// atomic load or store takes, so that a piece's sums are seen by a workgroup on another XCD.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_over(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)bytes, 0x00020000);
+}
+constexpr int kCoherent = 16;
+// A stream dispatch's partials: two slots a workgroup (at most kPrefillUnits workgroups), each holding every wave's
+// fp32 sums of one piece, [wave][mi NT + ni][lane] as 16-byte vectors (32 KiB a wave).
+constexpr uint32_t kStreamSlotBytes = 256 * 256 * 4, kStreamPartialBytes = 2 * kPrefillUnits * kStreamSlotBytes;
+constexpr uint32_t kAbsent = 0x80000000u;   // an offset past the partials: reads zero
+
+// A piece of stream tile t cut in `pieces` pieces (prefill_stream: at most three) arrives at the tile's counter. It
+// stores its fp32 sums to the partials at byte offset `slot` (the wave's, acc[mi][ni] at 16 ((mi NT + ni) 64 +
+// lane)) and adds one to the counter; the last of the tile's pieces to arrive returns true, returns the counter to
+// zero and runs the epilogue, which adds the pieces' sums in K order (so the sum does not depend on the order of
+// arrival). The partials go through agent-scope coherent (sc1) accesses and the counter through agent-scope atomics,
+// ordered as the decode split reduce orders them (split.hpp): each wave waits for its stores to complete before the
+// barrier, thread 0 adds to the counter after it, and the last piece loads only after its add returns. Every wave of
+// the workgroup calls it, after its last LDS reads; the counter's value passes through the tile's first LDS word
+// (the copies have landed by then).
+template <int MI, int NT>
+__device__ __forceinline__ bool stream_arrive(const PrefillArgs &a, const f32x4 (&acc)[MI][NT], uint32_t t,
+                                              uint32_t pieces, uint32_t slot, int lane, uint8_t *lds) {
+  uint32_t &arrival = *(uint32_t *)lds;
+  const __amdgpu_buffer_rsrc_t parts = buffer_over(a.partials, kStreamPartialBytes);
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NT; ++ni)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mi][ni]), parts,
+                                             slot + ((mi * NT + ni) * 64 + lane) * 16, 0, kCoherent);
+  __builtin_amdgcn_s_waitcnt(0);   // this wave's partial stores have completed
+  __syncthreads();                 // ... and every wave's
+  if (threadIdx.x == 0) {
+    const uint32_t before = __hip_atomic_fetch_add(a.counters + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // The last arrival is the counter's last use in the dispatch.
+    if (before == pieces - 1) __hip_atomic_store(a.counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    arrival = before;
+  }
+  __syncthreads();
+  return arrival == pieces - 1;
+}
+
+// The prefill dispatch: each workgroup runs one or more pieces of tiles, a piece being steps [first, first + n) of
+// row block `row_block` of the dispatch's column group `column_group`.
+//   whole tiles: workgroup (x, y) runs row block x of column group y, all of K;
+//   SPLIT: workgroup (x, y, z) runs piece z of that tile, cut at split_at, whose fp32 sums a close dispatch adds
+//     (prefill_schedule);
+//   STREAM (prefill_stream): workgroup x runs steps [x range, (x + 1) range) of the stream tiles' steps laid end to
+//     end (tile t: row block t % stream_row_blocks of column group t / stream_row_blocks), one piece a tile it
+//     touches; a piece of every step runs the epilogue itself, a partial one meets the tile's other piece through
+//     the partials (stream_arrive).
+// The body stays in the kernel (the pieces are an outer loop) rather than in a function it calls: the same body
+// optimised as a separate function before inlining takes more registers and spills.
+template <uint32_t FMT, uint32_t EP, int BM, bool SPLIT, int W, bool STREAM>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W / 4, W / 4)))
 void prefill_kernel(PrefillArgs a) {
+  static_assert(!(SPLIT && STREAM), "a stream piece runs its own epilogue");
   using F = Fmt<FMT>;
   using S = StepSlot<FMT, W>;
   static_assert(W == 4 || (W == 8 && F::P0 == 16 && F::P1 == 0), "eight waves take 16-byte codes and no plane1");
@@ -290,321 +344,482 @@ void prefill_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes<FMT, BM, W>()];
   const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, q = lane >> 4;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t row0 = blockIdx.x * BM;
   const uint32_t G = a.K >> 5, units = G / F::UNIT, steps = a.K / BK;
-  // The workgroup's steps of the tile: all of them, or piece z of them (cut at a multiple of four steps, whole meta
-  // units of every format), run with their own numbers from 0 from plane and input pointers moved on by `first`.
-  const uint32_t first = SPLIT && blockIdx.z ? a.split_at : 0;
-  const uint32_t n = SPLIT ? (blockIdx.z ? steps - a.split_at : a.split_at) : steps;
-
-  // The wave's plane tile (the dispatch's column groups start at column_group0) and its half of it (eight waves).
-  // A grid whose tile count is not a multiple of 4 ends short: a spare wave runs tile 0 of its segment and stores
-  // nothing.
-  const uint32_t half = W == 8 ? (wave & 1u) : 0u;
-  uint32_t ptile = (a.column_group0 + blockIdx.y) * 4 + wave / (W / 4), s = 0;
-  while (s + 1 < a.segments && ptile >= a.seg[s].tiles) ptile -= a.seg[s++].tiles;
-  const bool live = ptile < a.seg[s].tiles;
-  const Segment seg = a.seg[s];
-  // The lane's copy sources in the plane tile: 16-byte copies read 16 lane bytes on, dword copies 4 lane. Four waves:
-  // code copy k is group k of the step, lane l column code_slot(l). Eight waves: one code copy a step, lane l group
-  // l / 32, column code_slot(l % 32) of the wave's half.
-  const size_t tile = live ? ptile : 0;
-  const size_t unit0 = F::UNIT == 1 ? 2 * first : 2 * first / F::UNIT;
-  const uint32_t code_lane = W == 8 ? (lane >> 5) * 1024 + (32 * half + code_slot(lane & 31)) * 16
-                                    : 16 * (F::P0 == 16 ? code_slot(lane) : lane);
-  const uint8_t *bplane = seg.plane0 + (tile * G * 64 * F::P0 + (size_t)first * S::plane_step + code_lane);
-  const uint8_t *bhigh16 =
-      F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + (size_t)first * S::plane_high_step + 16 * lane) : nullptr;
-  const uint8_t *bhigh4 =
-      F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + (size_t)first * S::plane_high_step + 4 * lane) : nullptr;
-  const uint8_t *bmeta16 =
-      seg.meta + ((tile * units + unit0) * 64 * F::META + 16 * (F::META == 16 ? code_slot(lane) : lane));
-  const uint8_t *bmeta4 = seg.meta + ((tile * units + unit0) * 64 * F::META + 4 * lane);
-  const uint8_t *xin = (const uint8_t *)a.half_input + (size_t)first * BK * 2;
-  uint8_t *const wave_slot = lds + kCodeBase + wave * S::wave;
-  uint32_t mask = 0x0F0F0F0Fu;
-  asm volatile("" : "+s"(mask));
-
-  // Activations: wave w copies LDS rows BM/W w .. BM/W (w + 1) - 1, eight per instruction: lane l fills chunk slot
-  // l % 8 of row 8 i + l / 8, i.e. input chunk (l % 8) ^ (row % 8) (row % 8 = l / 8, the same for every i).
-  constexpr int kRowsPerWave = BM / W;
-  // Byte offsets of the lane's copy sources, rows clamped to the last live one (a tile past the rows reads it again).
-  uint32_t aoff[kACopies];
-#pragma unroll
-  for (int i = 0; i < kACopies; ++i) {
-    const uint32_t r = min(row0 + kRowsPerWave * wave + 8 * i + (lane >> 3), a.rows - 1);
-    aoff[i] = (r * a.K + 8 * ((lane & 7) ^ (lane >> 3))) * 2;
+  // STREAM: workgroups below stream_dp run one whole tile each (row block b % row blocks, column group b / row
+  // blocks); the others run the steps [i range, (i + 1) range) of their row block's stream tiles laid end to end
+  // (workgroup stream_dp + i row_blocks + row block), a piece a tile it meets. A row block's workgroups then share
+  // their XCD (workgroup b runs on XCD b % 8) and its L2's copy of the row block's activations.
+  const uint32_t stream_blocks = STREAM ? a.stream_row_blocks : 1u;
+  const bool stream_whole = STREAM && blockIdx.x < a.stream_dp;
+  const uint32_t stream_b = blockIdx.x - (STREAM && !stream_whole ? a.stream_dp : 0u);
+  const uint32_t stream_rb = stream_b % stream_blocks, stream_i = stream_b / stream_blocks;
+  uint32_t stream_at = 0, stream_end = 0;
+  if constexpr (STREAM) {
+    stream_at = stream_whole ? 0u : stream_i * a.stream_range;
+    stream_end = stream_whole ? steps : min(stream_at + a.stream_range, a.stream_tiles / stream_blocks * steps);
   }
-  // Step `step`'s activations into stage `stage` (sources clamped to the last step: every step issues as many
-  // copies, which the vmcnt waits count on).
-  const auto copy_a = [&](uint32_t step, uint32_t stage) __attribute__((always_inline)) {
-    const uint8_t *from = xin + (size_t)min(step, n - 1) * BK * 2;
-#pragma unroll
-    for (int i = 0; i < kACopies; ++i)
-      copy_to_lds<16>(from + aoff[i], lds + stage * kStage + (kRowsPerWave * wave + 8 * i) * kRowBytes);
+  // Byte offset of this wave's part of slot `slot` of the workgroup that runs range ii of this row block.
+  const auto slot_at = [&](uint32_t ii, uint32_t slot) __attribute__((always_inline)) {
+    return ((2 * (ii * stream_blocks + stream_rb) + slot) * W + wave) * (kStreamSlotBytes / W);
   };
-  // Plane copy k of step `from` (clamped) into the wave's slot at dst: the codes' 1 KiB pieces, then plane1's and the
-  // meta's 1 KiB and 256-byte pieces.
-  const auto copy_b_one = [&](uint32_t from, int k, uint8_t *dst) __attribute__((always_inline)) {
-    const size_t meta = (size_t)(F::UNIT == 1 ? 2 * from : 2 * from / F::UNIT) * 64 * F::META;
-    if (k < kCode16) {
-      copy_to_lds<16>(bplane + (size_t)from * S::plane_step + 1024 * k, dst + 1024 * k);
-    } else if (k < kCode16 + kHigh16) {
-      const int i = k - kCode16;
-      copy_to_lds<16>(bhigh16 + (size_t)from * S::plane_high_step + 1024 * i, dst + S::high_at + 1024 * i);
-    } else if (k < kCode16 + kHigh16 + kHigh4) {
-      const int i = k - kCode16 - kHigh16;
-      copy_to_lds<4>(bhigh4 + (size_t)from * S::plane_high_step + 1024 * kHigh16 + 256 * i,
-                     dst + S::high_at + 1024 * kHigh16 + 256 * i);
-    } else if (k < kCode16 + kHigh16 + kHigh4 + kMeta16) {
-      const int i = k - kCode16 - kHigh16 - kHigh4;
-      copy_to_lds<16>(bmeta16 + meta + 1024 * i, dst + S::meta_at + 1024 * i);
-    } else {
-      const int i = k - kCode16 - kHigh16 - kHigh4 - kMeta16;
-      copy_to_lds<4>(bmeta4 + meta + 1024 * kMeta16 + 256 * i, dst + S::meta_at + 1024 * kMeta16 + 256 * i);
-    }
-  };
-  // Step `step`'s codes, plane1 and meta into slot `slot` of this wave.
-  const auto copy_b = [&](uint32_t step, uint32_t slot) __attribute__((always_inline)) {
-#pragma unroll
-    for (int k = 0; k < kBCopies; ++k) copy_b_one(min(step, n - 1), k, wave_slot + slot * kSlotBytes);
-  };
-
-  // Copy c of step `step`'s copies: c < kACopies the activation rows of step + 2, then step + 3's plane copies.
-  const auto copy_one = [&](uint32_t step, int c) __attribute__((always_inline)) {
-    if (c < kACopies) {
-      const uint8_t *from = xin + (size_t)min(step + 2, n - 1) * BK * 2;
-      uint8_t *stage = lds + ((step + 2) % kStages) * kStage;
-      copy_to_lds<16>(from + aoff[c], stage + (kRowsPerWave * wave + 8 * c) * kRowBytes);
-      return;
-    }
-    copy_b_one(min(step + 3, n - 1), c - kACopies, wave_slot + ((step + 3) % kSlots) * kSlotBytes);
-  };
-
-  f32x4 acc[MI][NT];
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < NT; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // Weight fragments (the MFMA's A operand): wq[h][t] = group h of the step, column block t. Group 0 serves the first
-  // half of a step's MFMAs while group 1 is dequantised into wq[1], then group 1 serves the second half while the
-  // next step's group 0 is dequantised into wq[0]; each register set has one role, so the step loop needs no
-  // unrolling.
-  u32x4 wq[2][NT];
-  // The plane words (8-bit codes: two words, cw and cw1), plane1 bits and meta of group h of a step for the lane's
-  // NT columns, out of the step's slot: chunk q of the column (its codes of inputs 4q..4q+3 and 16+4q..19+4q). The
-  // meta block holds the whole plane tile, the codes the wave's columns.
-  uint32_t cw[2][NT], cw1[2][NT], hb[2][NT];
-  MetaWords mw[2][NT];
-  const auto read_b = [&](uint32_t slot, int h) __attribute__((always_inline)) {
-    const uint8_t *src = wave_slot + slot * kSlotBytes;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const uint32_t c = column_of(j, t);
-      if constexpr (F::P0 == 32) {
-        const u32x2 v = *(const u32x2 *)(src + h * 2048 + c * 32 + q * 8);
-        cw[h][t] = v[0];
-        cw1[h][t] = v[1];
+  for (bool again = false;; again = true) {
+    uint32_t row_block = blockIdx.x, column_group = blockIdx.y;
+    // A stream piece: its tile, the tile's pieces (one a range it meets) and the piece's place among them.
+    uint32_t stream_tile = 0, stream_pieces = 1, stream_piece = 0, range0 = 0;
+    // The piece's steps of the tile (cut at a multiple of four steps, whole meta units of every format) run with their
+    // own numbers from 0, from plane and input pointers moved on by `first`.
+    uint32_t first = SPLIT && blockIdx.z ? a.split_at : 0;
+    uint32_t n = SPLIT ? (blockIdx.z ? steps - a.split_at : a.split_at) : steps;
+    if constexpr (STREAM) {
+      if (stream_at >= stream_end) return;
+      if (stream_whole) {
+        row_block = blockIdx.x % stream_blocks;
+        column_group = blockIdx.x / stream_blocks;
+        stream_at = stream_end;
       } else {
-        cw[h][t] = *(const uint32_t *)(src + h * (S::code / 2) + code_slot(c) * 16 + q * 4);
+        const uint32_t c = stream_at / steps;   // the stream column group
+        first = stream_at % steps;
+        const uint32_t last = min(steps, stream_end - c * steps);
+        n = last - first;
+        stream_at = c * steps + last;
+        row_block = stream_rb;
+        column_group = a.stream_dp / stream_blocks + c;
+        stream_tile = c * stream_blocks + stream_rb;
+        range0 = c * steps / a.stream_range;
+        stream_pieces = (c * steps + steps - 1) / a.stream_range - range0 + 1;
+        stream_piece = stream_i - range0;
       }
-      if constexpr (F::P1 == 4) hb[h][t] = src[S::high_at + h * 256 + c * 4 + q];
-      if constexpr (F::P1 == 8) hb[h][t] = *(const uint16_t *)(src + S::high_at + h * 512 + c * 8 + 2 * q);
-      mw[h][t] = slot_meta<FMT>(src + S::meta_at, S::cols * half + c, h);
-    }
-  };
-  // The dequantisation of one group's NT words runs as 13 NT micro-operations (see micro_op) spread one or two
-  // after each MFMA: prep(t) masks word t and derives its coefficients, then every pair of weights p (word p / 4,
-  // fragment register p % 4) is converted (C), multiplied and added (F) and packed to fp16 (P), software
-  // pipelined so that no micro-operation waits on the one just before it.
-  // 4-bit codes: lo holds the word's slots 0, 4, 1, 5 and hi its slots 2, 6, 3, 7, one a byte, so pair r (slots 2r,
-  // 2r + 1) is bytes r / 2 and r / 2 + 2 of hi (r odd) or lo; plane1 bits go to bits 4 (and 5) of those bytes.
-  // 8-bit codes: lo and hi are the two words, pair r bytes 2 (r % 2) and 2 (r % 2) + 1 of word r / 2.
-  uint32_t lo[NT], hi[NT];
-  Coef kw[NT], kw2[NT];
-  float cf[4][2], vf[4][2];
-  constexpr int kMicro = micro_ops<NT>();
-  const auto micro = [&](int u, uint32_t step, int h) __attribute__((always_inline)) {
-    const Micro m = kMicroTable<NT>.op[u];
-    if (m.kind == 0) {
-      const int t = m.arg;
-      if constexpr (F::P0 == 32) {
-        const uint32_t flip = FMT == SQ_FMT_Q80 ? 0x80808080u : 0u;   // the signed byte v as v + 128
-        lo[t] = cw[h][t] ^ flip;
-        hi[t] = cw1[h][t] ^ flip;
-      } else {
-        lo[t] = cw[h][t] & mask;
-        hi[t] = (cw[h][t] >> 4) & mask;
-        if constexpr (F::P1 == 4) {
-          // Fifth bits (bit i of the byte: slot i): the product (24-bit operands, one v_mul_u32_u24) puts bits 0, 4,
-          // 1, 5 at 4, 12, 20, 28, and carries between its partial products stay clear of those.
-          lo[t] |= ((hb[h][t] & 0x33u) * 0x880110u) & 0x10101010u;
-          hi[t] |= (((hb[h][t] >> 2) & 0x33u) * 0x880110u) & 0x10101010u;
-        } else if constexpr (F::P1 == 8) {
-          // High two bits (bits 2i, 2i + 1: slot i).
-          lo[t] |= ((hb[h][t] & 0x0303u) << 4) | ((hb[h][t] & 0x0C0Cu) << 18);
-          hi[t] |= (hb[h][t] & 0x3030u) | ((hb[h][t] & 0xC0C0u) << 14);
-        }
-      }
-      group_coef<FMT>(mw[h][t], 2 * step + h, h, kw[t], kw2[t]);
-    } else {
-      const int p = m.arg, t = p >> 2, r = p & 3, slot = p & 3;
-      if (m.kind == 1) {
-        if constexpr (F::P0 == 32) {
-          const uint32_t src = (r >> 1) ? hi[t] : lo[t];
-          cf[slot][0] = byte_float(src, 2 * (r & 1));
-          cf[slot][1] = byte_float(src, 2 * (r & 1) + 1);
-        } else {
-          const uint32_t src = (r & 1) ? hi[t] : lo[t];
-          cf[slot][0] = byte_float(src, r >> 1);
-          cf[slot][1] = byte_float(src, (r >> 1) + 2);
-        }
-      } else if (m.kind == 2) {
-        // Pairs 0, 1 are the chunk's first-half elements, 2, 3 its second half.
-        const Coef k = F::HALVES && r >= 2 ? kw2[t] : kw[t];
-        vf[slot][0] = fmaf(cf[slot][0], k.s, k.z);
-        vf[slot][1] = fmaf(cf[slot][1], k.s, k.z);
-      } else {
-        // fp32 by the fma, then fp16: the empty asm keeps the two roundings apart (no fused mixed-precision fma).
-        asm volatile("" : "+v"(vf[slot][0]), "+v"(vf[slot][1]));
-        wq[h][t][r] = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{vf[slot][0], vf[slot][1]}, half2));
+      if (again) {
+        // The last piece's copies have landed and every wave has done with the LDS before this piece's copies.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
       }
     }
-  };
-  const auto dequant_group = [&](uint32_t step, int h) __attribute__((always_inline)) {
-#pragma unroll
-    for (int u = 0; u < kMicro; ++u) micro(u, step, h);
-  };
+    const uint32_t row0 = row_block * BM;
 
-  // Prologue: steps 0 and 1's activations, steps 0..2's codes; step 0's group-0 fragments.
-  copy_b(0, 0);
-  copy_b(1, 1);
-  copy_b(2, 2);
-  copy_a(0, 0);
-  copy_a(1, 1);
-  __builtin_amdgcn_s_waitcnt(wait_vm(0));
-  lds_barrier();
-  step_coefficients<FMT>(wave_slot + S::meta_at, 0, lane);
-  read_b(0, 0);
-  read_b(0, 1);
-  dequant_group(0, 0);
+    // The wave's plane tile (the dispatch's column groups start at column_group0) and its half of it (eight waves).
+    // A grid whose tile count is not a multiple of 4 ends short: a spare wave runs tile 0 of its segment and stores
+    // nothing.
+    const uint32_t half = W == 8 ? (wave & 1u) : 0u;
+    uint32_t ptile = (a.column_group0 + column_group) * 4 + wave / (W / 4), s = 0;
+    while (s + 1 < a.segments && ptile >= a.seg[s].tiles) ptile -= a.seg[s++].tiles;
+    const bool live = ptile < a.seg[s].tiles;
+    const Segment seg = a.seg[s];
+    // The lane's copy sources in the plane tile: 16-byte copies read 16 lane bytes on, dword copies 4 lane. Four waves:
+    // code copy k is group k of the step, lane l column code_slot(l). Eight waves: one code copy a step, lane l group
+    // l / 32, column code_slot(l % 32) of the wave's half.
+    const size_t tile = live ? ptile : 0;
+    const size_t unit0 = F::UNIT == 1 ? 2 * first : 2 * first / F::UNIT;
+    const uint32_t code_lane = W == 8 ? (lane >> 5) * 1024 + (32 * half + code_slot(lane & 31)) * 16
+                                      : 16 * (F::P0 == 16 ? code_slot(lane) : lane);
+    const uint8_t *bplane = seg.plane0 + (tile * G * 64 * F::P0 + (size_t)first * S::plane_step + code_lane);
+    const uint8_t *bhigh16 =
+        F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + (size_t)first * S::plane_high_step + 16 * lane) : nullptr;
+    const uint8_t *bhigh4 =
+        F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + (size_t)first * S::plane_high_step + 4 * lane) : nullptr;
+    const uint8_t *bmeta16 =
+        seg.meta + ((tile * units + unit0) * 64 * F::META + 16 * (F::META == 16 ? code_slot(lane) : lane));
+    const uint8_t *bmeta4 = seg.meta + ((tile * units + unit0) * 64 * F::META + 4 * lane);
+    const uint8_t *xin = (const uint8_t *)a.half_input + (size_t)first * BK * 2;
+    uint8_t *const wave_slot = lds + kCodeBase + wave * S::wave;
+    uint32_t mask = 0x0F0F0F0Fu;
+    asm volatile("" : "+s"(mask));
 
-  // Step s copies step s + 2's activations into stage (s + 2) % 3 and step s + 3's codes into slot (s + 3) % 4,
-  // one copy instruction before each of its batches in turn (a burst of them at the top of the step stalls the wave
-  // on the address unit). It dequantises its own group 1 during its first half and step s + 1's group 0 during its
-  // second half, from words read half a step earlier (each half reads the words the next half dequantises: step
-  // s + 1's slot has been in LDS since the last barrier). Before the barrier it waits for everything but its own
-  // copies, so step s + 1's activations and step s + 2's codes are in.
-  // The activation fragments go through registers in batches of four blocks (16 MFMAs), two batches in flight.
-  // With copies to LDS outstanding the compiler can only wait for all LDS reads at once, so each batch waits for
-  // its own reads (issued a batch earlier) before it issues the next batch's. A step's last batch runs after the
-  // barrier, while the next step's first reads are in flight.
-  constexpr int kGroups = 2 * MI, kBatch = 4, kBatches = kGroups / kBatch, kSlotsHalf = NT * MI;
-  constexpr int kWaitLds = 0xC07F;   // s_waitcnt lgkmcnt(0), the other counters at their maximum
-  u32x4 fa[2][kBatch];
-  const auto read_batch = [&](uint32_t step, int b) __attribute__((always_inline)) {
-    const uint8_t *sa = lds + (step % kStages) * kStage;
+    // Activations: wave w copies LDS rows BM/W w .. BM/W (w + 1) - 1, eight per instruction: lane l fills chunk slot
+    // l % 8 of row 8 i + l / 8, i.e. input chunk (l % 8) ^ (row % 8) (row % 8 = l / 8, the same for every i).
+    constexpr int kRowsPerWave = BM / W;
+    // Byte offsets of the lane's copy sources, rows clamped to the last live one (a tile past the rows reads it again).
+    uint32_t aoff[kACopies];
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const int g = b * kBatch + i;
-      fa[b & 1][i] = *(const u32x4 *)(sa + chunk_at((g % MI) * 16 + j, 4 * (g / MI) + q));
+    for (int i = 0; i < kACopies; ++i) {
+      const uint32_t r = min(row0 + kRowsPerWave * wave + 8 * i + (lane >> 3), a.rows - 1);
+      aoff[i] = (r * a.K + 8 * ((lane & 7) ^ (lane >> 3))) * 2;
     }
-  };
-  const auto mfma_batch = [&](uint32_t step, int b) __attribute__((always_inline)) {
+    // Step `step`'s activations into stage `stage` (sources clamped to the last step: every step issues as many
+    // copies, which the vmcnt waits count on).
+    const auto copy_a = [&](uint32_t step, uint32_t stage) __attribute__((always_inline)) {
+      const uint8_t *from = xin + (size_t)min(step, n - 1) * BK * 2;
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const int g = b * kBatch + i, kk = g / MI, mi = g % MI;
+      for (int i = 0; i < kACopies; ++i)
+        copy_to_lds<16>(from + aoff[i], lds + stage * kStage + (kRowsPerWave * wave + 8 * i) * kRowBytes);
+    };
+    // Plane copy k of step `from` (clamped) into the wave's slot at dst: the codes' 1 KiB pieces, then plane1's and the
+    // meta's 1 KiB and 256-byte pieces.
+    const auto copy_b_one = [&](uint32_t from, int k, uint8_t *dst) __attribute__((always_inline)) {
+      const size_t meta = (size_t)(F::UNIT == 1 ? 2 * from : 2 * from / F::UNIT) * 64 * F::META;
+      if (k < kCode16) {
+        copy_to_lds<16>(bplane + (size_t)from * S::plane_step + 1024 * k, dst + 1024 * k);
+      } else if (k < kCode16 + kHigh16) {
+        const int i = k - kCode16;
+        copy_to_lds<16>(bhigh16 + (size_t)from * S::plane_high_step + 1024 * i, dst + S::high_at + 1024 * i);
+      } else if (k < kCode16 + kHigh16 + kHigh4) {
+        const int i = k - kCode16 - kHigh16;
+        copy_to_lds<4>(bhigh4 + (size_t)from * S::plane_high_step + 1024 * kHigh16 + 256 * i,
+                       dst + S::high_at + 1024 * kHigh16 + 256 * i);
+      } else if (k < kCode16 + kHigh16 + kHigh4 + kMeta16) {
+        const int i = k - kCode16 - kHigh16 - kHigh4;
+        copy_to_lds<16>(bmeta16 + meta + 1024 * i, dst + S::meta_at + 1024 * i);
+      } else {
+        const int i = k - kCode16 - kHigh16 - kHigh4 - kMeta16;
+        copy_to_lds<4>(bmeta4 + meta + 1024 * kMeta16 + 256 * i, dst + S::meta_at + 1024 * kMeta16 + 256 * i);
+      }
+    };
+    // Step `step`'s codes, plane1 and meta into slot `slot` of this wave.
+    const auto copy_b = [&](uint32_t step, uint32_t slot) __attribute__((always_inline)) {
+#pragma unroll
+      for (int k = 0; k < kBCopies; ++k) copy_b_one(min(step, n - 1), k, wave_slot + slot * kSlotBytes);
+    };
+
+    // Copy c of step `step`'s copies: c < kACopies the activation rows of step + 2, then step + 3's plane copies.
+    const auto copy_one = [&](uint32_t step, int c) __attribute__((always_inline)) {
+      if (c < kACopies) {
+        const uint8_t *from = xin + (size_t)min(step + 2, n - 1) * BK * 2;
+        uint8_t *stage = lds + ((step + 2) % kStages) * kStage;
+        copy_to_lds<16>(from + aoff[c], stage + (kRowsPerWave * wave + 8 * c) * kRowBytes);
+        return;
+      }
+      copy_b_one(min(step + 3, n - 1), c - kACopies, wave_slot + ((step + 3) % kSlots) * kSlotBytes);
+    };
+
+    f32x4 acc[MI][NT];
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NT; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Weight fragments (the MFMA's A operand): wq[h][t] = group h of the step, column block t. Group 0 serves the first
+    // half of a step's MFMAs while group 1 is dequantised into wq[1], then group 1 serves the second half while the
+    // next step's group 0 is dequantised into wq[0]; each register set has one role, so the step loop needs no
+    // unrolling.
+    u32x4 wq[2][NT];
+    // The plane words (8-bit codes: two words, cw and cw1), plane1 bits and meta of group h of a step for the lane's
+    // NT columns, out of the step's slot: chunk q of the column (its codes of inputs 4q..4q+3 and 16+4q..19+4q). The
+    // meta block holds the whole plane tile, the codes the wave's columns.
+    uint32_t cw[2][NT], cw1[2][NT], hb[2][NT];
+    MetaWords mw[2][NT];
+    const auto read_b = [&](uint32_t slot, int h) __attribute__((always_inline)) {
+      const uint8_t *src = wave_slot + slot * kSlotBytes;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        acc[mi][t] = mfma_f16(wq[kk][t], fa[b & 1][i], acc[mi][t]);
-        // This MFMA's share of the other group's micro-operations: slot s of the half runs micro-operations
-        // [s kMicro / S, (s + 1) kMicro / S).
-        const int slot = mi * NT + t, u0 = slot * kMicro / kSlotsHalf, u1 = (slot + 1) * kMicro / kSlotsHalf;
-        static_assert(kMicro <= 2 * kSlotsHalf, "at most two micro-operations a slot");
-        if (u0 < u1) micro(u0, kk == 0 ? step : step + 1, kk ^ 1);
-        if (u0 + 1 < u1) micro(u0 + 1, kk == 0 ? step : step + 1, kk ^ 1);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-  };
-  read_batch(0, 0);
-  for (uint32_t step = 0; step < n; ++step) {
-    if (step > 0) mfma_batch(step - 1, kBatches - 1);
-#pragma unroll
-    for (int b = 0; b < kBatches; ++b) {
-#pragma unroll
-      for (int c = 0; c < kCopies; ++c)
-        if (c * kBatches / kCopies == b) copy_one(step, c);
-      __builtin_amdgcn_s_waitcnt(kWaitLds);
-      if (b + 1 < kBatches) read_batch(step, b + 1);
-      if (b == 0) {
-        step_coefficients<FMT>(wave_slot + ((step + 1) % kSlots) * kSlotBytes + S::meta_at, step + 1, lane);
-        read_b((step + 1) % kSlots, 0);
-      }
-      if (b == kBatches / 2) read_b((step + 1) % kSlots, 1);
-      if (b + 1 < kBatches) mfma_batch(step, b);
-    }
-    __builtin_amdgcn_s_waitcnt(wait_vm(kCopies));
-    lds_barrier();
-    if (step + 1 < n) read_batch(step + 1, 0);
-  }
-  mfma_batch(n - 1, kBatches - 1);
-
-  if constexpr (SPLIT) {
-    // Piece z of K: the fp32 sums, exactly, as two 16-bit planes of [rows][split_columns] (the high halves of the
-    // bits, then the low; column 64 t + c of the dispatch's plane tile t), stored as the bf16 epilogue stores (eight
-    // consecutive columns of a row twice over); split_close_kernel adds the pieces and applies the epilogue.
-    if (!live) return;
-    const size_t plane = (size_t)a.rows * a.split_columns;
-    uint16_t *const high = (uint16_t *)a.partials + blockIdx.z * 2 * plane;
-    uint16_t *const low = high + plane;
-    const uint32_t col0 = (blockIdx.y * 4 + wave / (W / 4)) * 64 + S::cols * half + 8 * q;
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi) {
-      const uint32_t r = row0 + mi * 16 + j;
-      if (r >= a.rows) continue;
-#pragma unroll
-      for (int hh = 0; hh < NT / 2; ++hh) {
-        const size_t at = (size_t)r * a.split_columns + col0 + 32 * hh;
-        u32x4 hi, lo;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const f32x4 &v = acc[mi][2 * hh + (e >> 1)];
-          const uint32_t b0 = __float_as_uint(v[2 * (e & 1)]), b1 = __float_as_uint(v[2 * (e & 1) + 1]);
-          hi[e] = __builtin_amdgcn_perm(b1, b0, 0x07060302u);
-          lo[e] = __builtin_amdgcn_perm(b1, b0, 0x05040100u);
+        const uint32_t c = column_of(j, t);
+        if constexpr (F::P0 == 32) {
+          const u32x2 v = *(const u32x2 *)(src + h * 2048 + c * 32 + q * 8);
+          cw[h][t] = v[0];
+          cw1[h][t] = v[1];
+        } else {
+          cw[h][t] = *(const uint32_t *)(src + h * (S::code / 2) + code_slot(c) * 16 + q * 4);
         }
-        *(u32x4 *)(high + at) = hi;
-        *(u32x4 *)(low + at) = lo;
+        if constexpr (F::P1 == 4) hb[h][t] = src[S::high_at + h * 256 + c * 4 + q];
+        if constexpr (F::P1 == 8) hb[h][t] = *(const uint16_t *)(src + S::high_at + h * 512 + c * 8 + 2 * q);
+        mw[h][t] = slot_meta<FMT>(src + S::meta_at, S::cols * half + c, h);
+      }
+    };
+    // The dequantisation of one group's NT words runs as 13 NT micro-operations (see micro_op) spread one or two
+    // after each MFMA: prep(t) masks word t and derives its coefficients, then every pair of weights p (word p / 4,
+    // fragment register p % 4) is converted (C), multiplied and added (F) and packed to fp16 (P), software
+    // pipelined so that no micro-operation waits on the one just before it.
+    // 4-bit codes: lo holds the word's slots 0, 4, 1, 5 and hi its slots 2, 6, 3, 7, one a byte, so pair r (slots 2r,
+    // 2r + 1) is bytes r / 2 and r / 2 + 2 of hi (r odd) or lo; plane1 bits go to bits 4 (and 5) of those bytes.
+    // 8-bit codes: lo and hi are the two words, pair r bytes 2 (r % 2) and 2 (r % 2) + 1 of word r / 2.
+    uint32_t lo[NT], hi[NT];
+    Coef kw[NT], kw2[NT];
+    float cf[4][2], vf[4][2];
+    constexpr int kMicro = micro_ops<NT>();
+    const auto micro = [&](int u, uint32_t step, int h) __attribute__((always_inline)) {
+      const Micro m = kMicroTable<NT>.op[u];
+      if (m.kind == 0) {
+        const int t = m.arg;
+        if constexpr (F::P0 == 32) {
+          const uint32_t flip = FMT == SQ_FMT_Q80 ? 0x80808080u : 0u;   // the signed byte v as v + 128
+          lo[t] = cw[h][t] ^ flip;
+          hi[t] = cw1[h][t] ^ flip;
+        } else {
+          lo[t] = cw[h][t] & mask;
+          hi[t] = (cw[h][t] >> 4) & mask;
+          if constexpr (F::P1 == 4) {
+            // Fifth bits (bit i of the byte: slot i): the product (24-bit operands, one v_mul_u32_u24) puts bits 0, 4,
+            // 1, 5 at 4, 12, 20, 28, and carries between its partial products stay clear of those.
+            lo[t] |= ((hb[h][t] & 0x33u) * 0x880110u) & 0x10101010u;
+            hi[t] |= (((hb[h][t] >> 2) & 0x33u) * 0x880110u) & 0x10101010u;
+          } else if constexpr (F::P1 == 8) {
+            // High two bits (bits 2i, 2i + 1: slot i).
+            lo[t] |= ((hb[h][t] & 0x0303u) << 4) | ((hb[h][t] & 0x0C0Cu) << 18);
+            hi[t] |= (hb[h][t] & 0x3030u) | ((hb[h][t] & 0xC0C0u) << 14);
+          }
+        }
+        group_coef<FMT>(mw[h][t], 2 * step + h, h, kw[t], kw2[t]);
+      } else {
+        const int p = m.arg, t = p >> 2, r = p & 3, slot = p & 3;
+        if (m.kind == 1) {
+          if constexpr (F::P0 == 32) {
+            const uint32_t src = (r >> 1) ? hi[t] : lo[t];
+            cf[slot][0] = byte_float(src, 2 * (r & 1));
+            cf[slot][1] = byte_float(src, 2 * (r & 1) + 1);
+          } else {
+            const uint32_t src = (r & 1) ? hi[t] : lo[t];
+            cf[slot][0] = byte_float(src, r >> 1);
+            cf[slot][1] = byte_float(src, (r >> 1) + 2);
+          }
+        } else if (m.kind == 2) {
+          // Pairs 0, 1 are the chunk's first-half elements, 2, 3 its second half.
+          const Coef k = F::HALVES && r >= 2 ? kw2[t] : kw[t];
+          vf[slot][0] = fmaf(cf[slot][0], k.s, k.z);
+          vf[slot][1] = fmaf(cf[slot][1], k.s, k.z);
+        } else {
+          // fp32 by the fma, then fp16: the empty asm keeps the two roundings apart (no fused mixed-precision fma).
+          asm volatile("" : "+v"(vf[slot][0]), "+v"(vf[slot][1]));
+          wq[h][t][r] = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{vf[slot][0], vf[slot][1]}, half2));
+        }
+      }
+    };
+    const auto dequant_group = [&](uint32_t step, int h) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < kMicro; ++u) micro(u, step, h);
+    };
+
+    // Prologue: steps 0 and 1's activations, steps 0..2's codes; step 0's group-0 fragments.
+    copy_b(0, 0);
+    copy_b(1, 1);
+    copy_b(2, 2);
+    copy_a(0, 0);
+    copy_a(1, 1);
+    __builtin_amdgcn_s_waitcnt(wait_vm(0));
+    lds_barrier();
+    step_coefficients<FMT>(wave_slot + S::meta_at, 0, lane);
+    read_b(0, 0);
+    read_b(0, 1);
+    dequant_group(0, 0);
+
+    // Step s copies step s + 2's activations into stage (s + 2) % 3 and step s + 3's codes into slot (s + 3) % 4,
+    // one copy instruction before each of its batches in turn (a burst of them at the top of the step stalls the wave
+    // on the address unit). It dequantises its own group 1 during its first half and step s + 1's group 0 during its
+    // second half, from words read half a step earlier (each half reads the words the next half dequantises: step
+    // s + 1's slot has been in LDS since the last barrier). Before the barrier it waits for everything but its own
+    // copies, so step s + 1's activations and step s + 2's codes are in.
+    // The activation fragments go through registers in batches of four blocks (16 MFMAs), two batches in flight.
+    // With copies to LDS outstanding the compiler can only wait for all LDS reads at once, so each batch waits for
+    // its own reads (issued a batch earlier) before it issues the next batch's. A step's last batch runs after the
+    // barrier, while the next step's first reads are in flight.
+    constexpr int kGroups = 2 * MI, kBatch = 4, kBatches = kGroups / kBatch, kSlotsHalf = NT * MI;
+    constexpr int kWaitLds = 0xC07F;   // s_waitcnt lgkmcnt(0), the other counters at their maximum
+    u32x4 fa[2][kBatch];
+    const auto read_batch = [&](uint32_t step, int b) __attribute__((always_inline)) {
+      const uint8_t *sa = lds + (step % kStages) * kStage;
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int g = b * kBatch + i;
+        fa[b & 1][i] = *(const u32x4 *)(sa + chunk_at((g % MI) * 16 + j, 4 * (g / MI) + q));
+      }
+    };
+    const auto mfma_batch = [&](uint32_t step, int b) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int g = b * kBatch + i, kk = g / MI, mi = g % MI;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          acc[mi][t] = mfma_f16(wq[kk][t], fa[b & 1][i], acc[mi][t]);
+          // This MFMA's share of the other group's micro-operations: slot s of the half runs micro-operations
+          // [s kMicro / S, (s + 1) kMicro / S).
+          const int slot = mi * NT + t, u0 = slot * kMicro / kSlotsHalf, u1 = (slot + 1) * kMicro / kSlotsHalf;
+          static_assert(kMicro <= 2 * kSlotsHalf, "at most two micro-operations a slot");
+          if (u0 < u1) micro(u0, kk == 0 ? step : step + 1, kk ^ 1);
+          if (u0 + 1 < u1) micro(u0 + 1, kk == 0 ? step : step + 1, kk ^ 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    };
+    read_batch(0, 0);
+    for (uint32_t step = 0; step < n; ++step) {
+      if (step > 0) mfma_batch(step - 1, kBatches - 1);
+#pragma unroll
+      for (int b = 0; b < kBatches; ++b) {
+#pragma unroll
+        for (int c = 0; c < kCopies; ++c)
+          if (c * kBatches / kCopies == b) copy_one(step, c);
+        __builtin_amdgcn_s_waitcnt(kWaitLds);
+        if (b + 1 < kBatches) read_batch(step, b + 1);
+        if (b == 0) {
+          step_coefficients<FMT>(wave_slot + ((step + 1) % kSlots) * kSlotBytes + S::meta_at, step + 1, lane);
+          read_b((step + 1) % kSlots, 0);
+        }
+        if (b == kBatches / 2) read_b((step + 1) % kSlots, 1);
+        if (b + 1 < kBatches) mfma_batch(step, b);
+      }
+      __builtin_amdgcn_s_waitcnt(wait_vm(kCopies));
+      lds_barrier();
+      if (step + 1 < n) read_batch(step + 1, 0);
+    }
+    mfma_batch(n - 1, kBatches - 1);
+
+    if constexpr (SPLIT) {
+      // Piece z of K: the fp32 sums, exactly, as two 16-bit planes of [rows][split_columns] (the high halves of the
+      // bits, then the low; column 64 t + c of the dispatch's plane tile t), stored as the bf16 epilogue stores (eight
+      // consecutive columns of a row twice over); split_close_kernel adds the pieces and applies the epilogue.
+      if (!live) return;
+      const size_t plane = (size_t)a.rows * a.split_columns;
+      uint16_t *const high = (uint16_t *)a.partials + blockIdx.z * 2 * plane;
+      uint16_t *const low = high + plane;
+      const uint32_t col0 = (column_group * 4 + wave / (W / 4)) * 64 + S::cols * half + 8 * q;
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi) {
+        const uint32_t r = row0 + mi * 16 + j;
+        if (r >= a.rows) continue;
+#pragma unroll
+        for (int hh = 0; hh < NT / 2; ++hh) {
+          const size_t at = (size_t)r * a.split_columns + col0 + 32 * hh;
+          u32x4 hi, lo;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const f32x4 &v = acc[mi][2 * hh + (e >> 1)];
+            const uint32_t b0 = __float_as_uint(v[2 * (e & 1)]), b1 = __float_as_uint(v[2 * (e & 1) + 1]);
+            hi[e] = __builtin_amdgcn_perm(b1, b0, 0x07060302u);
+            lo[e] = __builtin_amdgcn_perm(b1, b0, 0x05040100u);
+          }
+          *(u32x4 *)(high + at) = hi;
+          *(u32x4 *)(low + at) = lo;
+        }
+      }
+      return;
+    }
+    // A tile cut in pieces: piece p's sums (stream_arrive) sit in slot 0 of its range when the range starts inside
+    // the tile (every piece but the first, and the first when a range starts with the tile), else in slot 1 (the
+    // range's last piece).
+    bool complete = true;
+    uint32_t slot0 = 0;
+    if constexpr (STREAM) {
+      if (stream_pieces > 1) {
+        slot0 = (column_group - a.stream_dp / stream_blocks) * steps % a.stream_range ? 1u : 0u;
+        complete = stream_arrive<MI, NT>(a, acc, stream_tile, stream_pieces,
+                                         slot_at(stream_i, stream_piece ? 0u : slot0), lane, lds);
       }
     }
-    return;
-  }
-  // Epilogue: lane (j, q) holds row 16 mi + j of each row block at columns 8q..8q+7 of the wave's columns (blocks
-  // 0, 1) and, with four column blocks, 32+8q..32+8q+7 (blocks 2, 3): one 16-byte store a row block and pair of
-  // column blocks.
-  if (!live) return;
-  const uint32_t col0 = seg.out_offset + ptile * 64 + S::cols * half + 8 * q;
+    // Epilogue: lane (j, q) holds row 16 mi + j of each row block at columns 8q..8q+7 of the wave's columns (blocks
+    // 0, 1) and, with four column blocks, 32+8q..32+8q+7 (blocks 2, 3): one 16-byte store a row block and pair of
+    // column blocks.
+    if (live && complete) {
+      const uint32_t col0 = seg.out_offset + ptile * 64 + S::cols * half + 8 * q;
+      bool pieces_done = false;
+      if constexpr (STREAM) {
+        if (stream_pieces > 1) {
+          // The last piece of a cut tile: the pieces' sums, the others' loaded ahead of their stores with the rows'
+          // scales. No branches within, so that the loads overlap the stores: rows past the chunk fall past the
+          // output's buffer range and are dropped.
+          const __amdgpu_buffer_rsrc_t parts = buffer_over(a.partials, kStreamPartialBytes);
+          const uint32_t out_bytes = a.rows * a.out_stride * 2;
+          const __amdgpu_buffer_rsrc_t out = buffer_over(a.output, out_bytes);
+          const __amdgpu_buffer_rsrc_t aux = buffer_over(a.aux, EP != EpNone ? out_bytes : 0u);
+          const auto row_scale = [&](int mi) __attribute__((always_inline)) {
+            return a.row_scale[min(row0 + mi * 16 + j, a.rows - 1)];
+          };
+          const auto piece = [&](uint32_t from, int mi, int ni) __attribute__((always_inline)) {
+            return __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(parts, from + (mi * NT + ni) * 1024, 0, kCoherent));
+          };
+          const auto store_block = [&](int mi, const f32x4 (&sum)[NT], float scale) __attribute__((always_inline)) {
+            const uint32_t r = row0 + mi * 16 + j;
 #pragma unroll
-  for (int mi = 0; mi < MI; ++mi) {
-    const uint32_t r = row0 + mi * 16 + j;
-    if (r >= a.rows) continue;
-    const float scale = a.row_scale[r];
+            for (int hh = 0; hh < NT / 2; ++hh) {
+              const uint32_t at = (r * a.out_stride + col0 + 32 * hh) * 2;
+              u32x4 ax = {0u, 0u, 0u, 0u};
+              if constexpr (EP != EpNone) ax = __builtin_amdgcn_raw_buffer_load_b128(aux, at, 0, 0);
+              u32x4 o;
 #pragma unroll
-    for (int hh = 0; hh < NT / 2; ++hh) {
-      const size_t at = (size_t)r * a.out_stride + col0 + 32 * hh;
-      u32x4 aux = {0u, 0u, 0u, 0u};
-      if constexpr (EP != EpNone) aux = *(const u32x4 *)(a.aux + at);
-      u32x4 out;
+              for (int e = 0; e < 4; ++e) {
+                const f32x4 &v = sum[2 * hh + (e >> 1)];
+                const float lo = epilogue_bits<EP>(v[2 * (e & 1)] * scale, ax[e] & 0xFFFFu);
+                const float hi = epilogue_bits<EP>(v[2 * (e & 1) + 1] * scale, ax[e] >> 16);
+                o[e] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+              }
+              __builtin_amdgcn_raw_buffer_store_b128(o, out, at, 0, 0);
+            }
+          };
+          if (stream_pieces == 2) {
+            // Two pieces: a + b = b + a, so the wave's own sums take the other piece's in either order. Its loads run
+            // D row blocks ahead.
+            constexpr int D = 4;
+            const uint32_t other = slot_at(range0 + (stream_piece ^ 1u), stream_piece ? slot0 : 0u) + lane * 16;
+            f32x4 ahead[D][NT];
+            float scale_ahead[D];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const f32x4 &v = acc[mi][2 * hh + (e >> 1)];
-        const float lo = epilogue_bits<EP>(v[2 * (e & 1)] * scale, aux[e] & 0xFFFFu);
-        const float hi = epilogue_bits<EP>(v[2 * (e & 1) + 1] * scale, aux[e] >> 16);
-        out[e] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+            for (int mi = 0; mi < D; ++mi) {
+              scale_ahead[mi] = row_scale(mi);
+#pragma unroll
+              for (int ni = 0; ni < NT; ++ni) ahead[mi][ni] = piece(other, mi, ni);
+            }
+#pragma unroll
+            for (int mi = 0; mi < MI; ++mi) {
+              f32x4 sum[NT];
+#pragma unroll
+              for (int ni = 0; ni < NT; ++ni) sum[ni] = acc[mi][ni] + ahead[mi % D][ni];
+              const float scale = scale_ahead[mi % D];
+              if (mi + D < MI) {
+                scale_ahead[mi % D] = row_scale(mi + D);
+#pragma unroll
+                for (int ni = 0; ni < NT; ++ni) ahead[mi % D][ni] = piece(other, mi + D, ni);
+              }
+              store_block(mi, sum, scale);
+            }
+          } else {
+            // Three pieces: (x0 + x1) + x2 in K order, a row block ahead. The wave's own piece comes from its
+            // registers (its loads take kAbsent and read zero).
+            uint32_t from[3];
+#pragma unroll
+            for (uint32_t p = 0; p < 3; ++p)
+              from[p] = p == stream_piece ? kAbsent : slot_at(range0 + p, p ? 0u : slot0) + lane * 16;
+            f32x4 next[3][NT];
+            float next_scale = row_scale(0);
+#pragma unroll
+            for (int p = 0; p < 3; ++p)
+#pragma unroll
+              for (int ni = 0; ni < NT; ++ni) next[p][ni] = piece(from[p], 0, ni);
+#pragma unroll
+            for (int mi = 0; mi < MI; ++mi) {
+              f32x4 sum[NT];
+#pragma unroll
+              for (int ni = 0; ni < NT; ++ni) {
+                const f32x4 x0 = stream_piece == 0 ? acc[mi][ni] : next[0][ni];
+                const f32x4 x1 = stream_piece == 1 ? acc[mi][ni] : next[1][ni];
+                const f32x4 x2 = stream_piece == 2 ? acc[mi][ni] : next[2][ni];
+                sum[ni] = (x0 + x1) + x2;
+              }
+              const float scale = next_scale;
+              if (mi + 1 < MI) {
+                next_scale = row_scale(mi + 1);
+#pragma unroll
+                for (int p = 0; p < 3; ++p)
+#pragma unroll
+                  for (int ni = 0; ni < NT; ++ni) next[p][ni] = piece(from[p], mi + 1, ni);
+              }
+              store_block(mi, sum, scale);
+            }
+          }
+          pieces_done = true;
+        }
       }
-      *(u32x4 *)(a.output + at) = out;
+      if (!pieces_done) {
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi) {
+          const uint32_t r = row0 + mi * 16 + j;
+          if (r >= a.rows) continue;
+          const float scale = a.row_scale[r];
+#pragma unroll
+          for (int hh = 0; hh < NT / 2; ++hh) {
+            const size_t at = (size_t)r * a.out_stride + col0 + 32 * hh;
+            u32x4 aux = {0u, 0u, 0u, 0u};
+            if constexpr (EP != EpNone) aux = *(const u32x4 *)(a.aux + at);
+            u32x4 out;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const f32x4 &v = acc[mi][2 * hh + (e >> 1)];
+              const float lo = epilogue_bits<EP>(v[2 * (e & 1)] * scale, aux[e] & 0xFFFFu);
+              const float hi = epilogue_bits<EP>(v[2 * (e & 1) + 1] * scale, aux[e] >> 16);
+              out[e] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+            }
+            *(u32x4 *)(a.output + at) = out;
+          }
+        }
+      }
     }
+    if constexpr (!STREAM) return;
   }
 }
 
@@ -640,16 +855,22 @@ __global__ __launch_bounds__(256) void split_close_kernel(PrefillArgs a, uint32_
   *(u32x4 *)(a.output + at) = out;
 }
 
-template <uint32_t FMT, int BM, bool SPLIT>
+template <uint32_t FMT, int BM, int MODE>
 hipError_t launch_tile(uint32_t epilogue, const PrefillArgs &a, dim3 grid, hipStream_t stream) {
   constexpr int W = tile_waves<FMT>();
+  constexpr bool STREAM = MODE == 2;
+  constexpr bool SPLIT = MODE == 1;
   const dim3 block(64 * W);
   switch (epilogue) {
-    case EpNone: hipLaunchKernelGGL((prefill_kernel<FMT, EpNone, BM, SPLIT, W>), grid, block, 0, stream, a); break;
-    case EpResidual:
-      hipLaunchKernelGGL((prefill_kernel<FMT, EpResidual, BM, SPLIT, W>), grid, block, 0, stream, a);
+    case EpNone:
+      hipLaunchKernelGGL((prefill_kernel<FMT, EpNone, BM, SPLIT, W, STREAM>), grid, block, 0, stream, a);
       break;
-    default: hipLaunchKernelGGL((prefill_kernel<FMT, EpUpWithGate, BM, SPLIT, W>), grid, block, 0, stream, a); break;
+    case EpResidual:
+      hipLaunchKernelGGL((prefill_kernel<FMT, EpResidual, BM, SPLIT, W, STREAM>), grid, block, 0, stream, a);
+      break;
+    default:
+      hipLaunchKernelGGL((prefill_kernel<FMT, EpUpWithGate, BM, SPLIT, W, STREAM>), grid, block, 0, stream, a);
+      break;
   }
   return hipGetLastError();
 }
@@ -665,16 +886,28 @@ hipError_t launch_format(uint32_t epilogue, const PrefillArgs &args, hipStream_t
   PrefillArgs a = args;
   a.column_group0 = 0;
   if (!sc.split) {
-    const dim3 grid(sc.row_blocks, sc.column_groups);
-    if (sc.bm == 128) return launch_tile<FMT, 128, false>(epilogue, a, grid, stream);
-    return launch_tile<FMT, 256, false>(epilogue, a, grid, stream);
+    if (sc.bm == 128) return launch_tile<FMT, 128, 0>(epilogue, a, dim3(sc.row_blocks, sc.column_groups), stream);
+    // Stream pieces run in the eight-wave tile only: the four-wave tile's 256 sums a lane leave no registers for the
+    // piece loop (its stream instance spills). Their epilogue addresses the output with 32-bit byte offsets.
+    if constexpr (tile_waves<FMT>() == 8) {
+      const PrefillStream st = prefill_stream(sc.row_blocks, sc.column_groups, args.K);
+      if (st.stream_tiles && (uint64_t)args.rows * args.out_stride * 2 < (1ull << 31)) {
+        if (!a.partials || !a.counters) return hipErrorInvalidValue;
+        a.stream_dp = st.dp_tiles;
+        a.stream_tiles = st.stream_tiles;
+        a.stream_range = st.range;
+        a.stream_row_blocks = sc.row_blocks;
+        return launch_tile<FMT, 256, 2>(epilogue, a, dim3(st.workgroups), stream);
+      }
+    }
+    return launch_tile<FMT, 256, 0>(epilogue, a, dim3(sc.row_blocks, sc.column_groups), stream);
   }
   if (!a.partials) return hipErrorInvalidValue;
   a.column_group0 = sc.whole_groups;
   a.split_at = sc.split_at;
   a.split_columns = (sc.column_groups - sc.whole_groups) * 256;
-  hipError_t e = launch_tile<FMT, 256, true>(epilogue, a, dim3(sc.row_blocks, sc.column_groups - sc.whole_groups, 2),
-                                             stream);
+  hipError_t e = launch_tile<FMT, 256, 1>(epilogue, a, dim3(sc.row_blocks, sc.column_groups - sc.whole_groups, 2),
+                                          stream);
   if (e != hipSuccess) return e;
   const uint32_t split_tiles = tiles - 4 * sc.whole_groups;
   const dim3 grid((split_tiles * 8 + 255) / 256, a.rows), block(256);
@@ -714,9 +947,40 @@ PrefillSchedule prefill_schedule(uint32_t rows, uint32_t plane_tiles, uint32_t K
   if (7 * rounds128 < 10 * rounds256) return {128, 0, blocks128, columns, 0, 0};
   return {256, 0, blocks256, columns, 0, 0};
 }
+// The stream schedule of a whole-K dispatch of 256-row tiles, row_blocks x column_groups of them, K / 64 steps each,
+// in one dispatch. Whole rounds of kPrefillUnits tiles run as whole tiles (dp_tiles: whole column groups, so that the
+// row blocks divide the units), one a workgroup; the rest (stream_tiles, between half a round and a round and a
+// half) are cut into pieces: each row block's stream tiles have their steps laid end to end and cut into ranges of
+// `range` steps (a multiple of four: whole meta units of every format), one a workgroup, kPrefillUnits / row_blocks
+// ranges at most a row block, so that the last round's work spreads over every compute unit instead of leaving some
+// idle. A tile meets at most ceil(steps / range) + 1 ranges: a range of at least half a tile cuts it in at most
+// three pieces, which stream_arrive joins. None (stream_tiles 0) where the tiles fill whole rounds or fill less than
+// one (a partial round alone runs each tile faster than a full one: measured on MI355X, a dispatch of 216 tiles
+// ran 6% slower as stream pieces), or the steps or row blocks do not allow it. A partial last round's tiles also
+// run faster than a full round's (fewer compute units share the memory system), which bounds the gain: measured, 4%
+// on 448 tiles of K 4096, 1-2% on 864 of K 5120 and 6% on 544 of K 5120 (prefill_gemm_m2048_config2.txt).
+PrefillStream prefill_stream(uint32_t row_blocks, uint32_t column_groups, uint32_t K) {
+  const uint32_t units = kPrefillUnits, steps = K / BK, tiles = row_blocks * column_groups;
+  if (K % (4 * BK) || steps < 8 || !row_blocks || units % row_blocks || tiles % units == 0 || tiles <= units)
+    return {0, 0, 0, 0};
+  const uint32_t rounds = tiles / units, rest = tiles % units;
+  const uint32_t dp = 2 * rest >= units ? rounds * units : (rounds - 1) * units;
+  const uint32_t stream = tiles - dp, ranges = units / row_blocks;   // ranges a row block
+  const uint32_t work = stream / row_blocks * steps;                  // a row block's stream steps
+  const uint32_t range = (work + 4 * ranges - 1) / (4 * ranges) * 4;
+  if (steps > 2 * range) return {0, 0, 0, 0};
+  return {dp, stream, range, dp + row_blocks * ((work + range - 1) / range)};
+}
 PrefillScratch prefill_scratch_bytes(uint32_t rows, uint32_t plane_tiles, uint32_t K) {
-  if (!prefill_split(rows, plane_tiles, K)) return {0, 0};
-  return {(uint64_t)2 * rows * ((plane_tiles + 3) / 4) * 256 * 4, 0};
+  if (prefill_split(rows, plane_tiles, K)) return {(uint64_t)2 * rows * ((plane_tiles + 3) / 4) * 256 * 4, 0};
+  // A stream dispatch (any of the projection's, one a format, whose 256-row tiles are at most all of the
+  // projection's, whether or not the whole projection's schedule takes 256-row tiles) stores the fp32 sums of at most
+  // two pieces a stream workgroup, 256 x 256 x 4 bytes each, and keeps a counter a stream tile (at most a round and
+  // a half of tiles). Reserved for every format: the plan does not know them.
+  const uint32_t row_blocks = (rows + 255) / 256, columns = (plane_tiles + 3) / 4, tiles = row_blocks * columns;
+  if (tiles <= kPrefillUnits || K % (4 * BK) || K / BK < 8 || kPrefillUnits % row_blocks) return {0, 0};
+  const uint64_t stream = std::min<uint64_t>(tiles, 3 * kPrefillUnits / 2);
+  return {(uint64_t)2 * kPrefillUnits * 256 * 256 * 4, stream * 4};
 }
 
 hipError_t launch_prefill_prepare(const uint16_t *input, uint32_t rows, uint32_t K, uint16_t *half_input,

@@ -101,9 +101,11 @@ def test_prefill_plans():
     assert ragged.storage_rows == 384
     short = sq.plan_for(sq.prefill_workload(14336, 4096, 32), proj)
     assert short.config.tile == sq.TILE_STAGED
-    # 448 tiles of 256 rows fill the compute units: no halves. 128 (N 4096 by K 14336) halve their K, whose fp32
-    # halves [2][rows][N] the plan's partials hold; 32 tiles do not halve.
-    assert size.partials == 0 and size.counters == 0
+    # 448 tiles of 256 rows: one whole round over the compute units, then 192 tiles as stream pieces, which store
+    # the fp32 sums of at most two pieces a workgroup (256 x 256 x 4 bytes each, at most 256 workgroups) and keep a
+    # counter a stream tile (at most a round and a half of tiles). 128 (N 4096 by K 14336) halve their K, whose fp32
+    # halves [2][rows][N] the plan's partials hold; 32 tiles do neither.
+    assert size.partials == 2 * 256 * 256 * 256 * 4 and size.counters == 384 * 4
     down = sq.projection(seg(4096, 14336))
     size, _ = sq.scratch_size(sq.plan_for(sq.prefill_workload(4096, 14336, 2048), down))
     assert size.partials == 2 * 2048 * 4096 * 4 and size.counters == 0
@@ -448,14 +450,21 @@ def test_prefill_scratch_size_covers_every_chunk(n, k):
     the row bands that halve included (the reference's arenas are sized from it)."""
     dev, bound = sq.device(), sq.LinearScratchSize()
     sq.call("sq_linear_prefill_scratch_size", sq.byref(dev), n, k, sq.byref(bound))
-    halved = 0
+    halved = streamed = 0
     for rows in range(1, 2049):
         size, _ = sq.scratch_size(sq.plan_for(sq.prefill_workload(n, k, rows)))
         for f in ("input", "sums", "partials", "counters"):
             assert getattr(size, f) <= getattr(bound, f), (rows, f)
-        halved += size.partials > 0 and rows > 32
+        if rows > 32 and size.partials:
+            # halved K: [2][rows][N] fp32 and no counters; stream pieces: 256 workgroups' two slots and counters
+            stream = size.counters > 0
+            assert size.partials == (2 * 256 * 256 * 256 * 4 if stream else 2 * rows * n * 4), rows
+            halved += not stream
+            streamed += stream
     if (n, k) == (14336, 4096):
-        assert halved == 256 and bound.partials == 2 * 512 * 14336 * 4   # rows 257..512
+        # rows 257..512 halve; rows 1793..2048 (448 tiles: more than one round, in row blocks that divide the 256
+        # compute units) run their last round's tiles as stream pieces
+        assert halved == 256 and streamed == 256 and bound.partials == 2 * 256 * 256 * 256 * 4
 
 
 def test_moe_add_routes_refusals():

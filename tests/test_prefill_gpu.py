@@ -327,17 +327,103 @@ def test_prefill_halved_k_epilogues():
     assert np.all(np.abs(got - want) <= ulp + 1e-30)
 
 
+def accumulation_bound(x, w, pick):
+    """Two fp32 accumulation bounds of each picked row's outputs plus a bf16 ulp: how far apart two correct results
+    of one row may lie when their fp32 sums ran in different orders (whole K against pieces of it)."""
+    value, magnitude, inputs, largest = oracle.project_f64(x[pick], w.values)
+    return 2 * oracle.projection_bound(magnitude, inputs, largest, True) + \
+        oracle.ulp_bf16(np.maximum(np.abs(value), 1e-30))
+
+
 def test_q4k_projection_benchmark_shape():
-    """The reference's gguf-projection-benchmark shape (Q4_K, K = 5120, N = 17408, M = 2048; 256-row tiles, the last
-    of three rounds over the compute units an eighth full): sampled rows against fp64, and a row's output bitwise
-    the same as in a 300-row prefill of the same weights (128-row tiles)."""
+    """The reference's gguf-projection-benchmark shape (Q4_K, K = 5120, N = 17408, M = 2048; 544 256-row tiles: one
+    whole round over the compute units, then the other 288 as stream pieces): sampled rows against fp64. Against a
+    300-row prefill of the same weights (128-row tiles, all whole): the columns of the whole round's tiles bitwise
+    the same, the stream tiles' columns within two fp32 accumulation bounds."""
     n, k, rows = 17408, 5120, 2048
     w = shape_weights(oracle.FMT_Q4K, n, k, 4)
     rng = np.random.default_rng(2048)
     x = dense_inputs(rng, rows, k)
     out = run_prefill([w], x)
     check_sampled(out, x, w, "Q4_K projection benchmark rows 2048", rng)
-    assert np.array_equal(run_prefill([w], x[:300]), out[:300])
+    short = run_prefill([w], x[:300])
+    whole = 256 // 8 * 256    # the whole rounds' 256 tiles: 8 row blocks x 32 column groups of 256 columns
+    assert np.array_equal(short[:, :whole], out[:300, :whole])
+    pick = np.arange(0, 300, 23)
+    a = synthetic.bf16_to_f32(short[pick]).astype(np.float64)
+    b = synthetic.bf16_to_f32(out[pick]).astype(np.float64)
+    assert np.all(np.abs(a - b) <= accumulation_bound(x, w, pick))
+
+
+def stream_schedule(rows, n, k):
+    """The stream schedule the library's launcher computes for a whole-K dispatch of more than one round of 256-row
+    tiles: whole rounds of 256 tiles, then each row block's remaining tiles with their K steps laid end to end and cut
+    into ranges of a multiple of four steps, 256 / row blocks ranges at most a row block, one a workgroup. Returns the
+    whole tiles, the stream tiles and how many of them are cut in two and in three pieces."""
+    steps, blocks = k // 64, (rows + 255) // 256
+    tiles = blocks * ((n // 64 + 3) // 4)
+    rounds, rest = divmod(tiles, 256)
+    assert rounds >= 1 and rest and 256 % blocks == 0
+    dp = rounds * 256 if 2 * rest >= 256 else (rounds - 1) * 256
+    per_block, ranges = (tiles - dp) // blocks, 256 // blocks
+    span = -(-per_block * steps // (4 * ranges)) * 4
+    assert steps <= 2 * span
+    cut = [(c * steps + steps - 1) // span - c * steps // span + 1 for c in range(per_block)] * blocks
+    return dp, tiles - dp, cut.count(2), cut.count(3)
+
+
+@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K])
+def test_prefill_stream_pieces(fmt):
+    """Past whole rounds of tiles, the rest run as stream pieces (ranges of K steps over every compute unit, the last
+    piece of a tile to arrive adding the pieces' fp32 sums in K order) in the same dispatch: 1024 rows of
+    1280 x 24576 run 256 whole tiles, then 128 in pieces, 84 of them cut in two and 44 in three. Sampled rows against
+    fp64, a second run bitwise the same (the sum does not depend on the order the pieces arrive in), and a 128-row
+    chunk of the rows (whole tiles) within two accumulation bounds."""
+    n, k, rows = 24576, 1280, 1024
+    assert stream_schedule(rows, n, k) == (256, 128, 84, 44)
+    w = make_weights(np.random.default_rng(80 + fmt), fmt, n, k)
+    size, _ = sq.scratch_size(sq.plan_for(sq.prefill_workload(n, k, rows), sq.projection(w.segment())))
+    assert size.partials > 0 and size.counters >= 128 * 4, "the plan reserves the stream partials and counters"
+    rng = np.random.default_rng(81 + fmt)
+    x = dense_inputs(rng, rows, k)
+    out = run_prefill([w], x)
+    check_sampled(out, x, w, f"stream pieces fmt {fmt}", rng)
+    assert np.array_equal(run_prefill([w], x), out)
+    pick = np.arange(0, 128, 9)
+    a = synthetic.bf16_to_f32(run_prefill([w], x[:128])[pick]).astype(np.float64)
+    b = synthetic.bf16_to_f32(out[pick]).astype(np.float64)
+    assert np.all(np.abs(a - b) <= accumulation_bound(x, w, pick))
+
+
+def test_prefill_stream_epilogues_and_segments():
+    """Stream pieces under the residual and up-with-gate epilogues (applied once, by the tile's last piece), across
+    a fused projection's segments (8192, 4096 and 12288 columns of af4g64), and beside a four-wave format's whole
+    tiles (24576 columns of af4g64 and 2048 of Q6_K in one projection: each format's dispatch schedules its own
+    tiles, the af4g64 ones in part as stream pieces)."""
+    rng = np.random.default_rng(82)
+    k, rows = 1280, 1024
+    parts = [make_weights(rng, oracle.FMT_AF4G64, n, k) for n in (8192, 4096, 12288)]
+    x = dense_inputs(rng, rows, k)
+    pick = sampled_rows(rows, 24, rng)
+    out = run_prefill(parts, x)
+    check_projection(out[pick], x[pick], parts, "stream pieces across segments")
+    w = make_weights(rng, oracle.FMT_AF4G64, 24576, k)
+    n = w.n
+    plain = run_prefill([w], x)
+    residual = synthetic.bf16_bits(rng.uniform(-64, 64, (rows, n)).astype(np.float32))
+    got = run_prefill([w], x, sq.EPILOGUE_RESIDUAL, residual=residual)
+    check_projection(got[pick], x[pick], w, "stream residual", residual=residual[pick])
+    gate = synthetic.bf16_bits(rng.uniform(-4, 4, (rows, n)).astype(np.float32))
+    up_gated = run_prefill([w], x, sq.EPILOGUE_UP_WITH_GATE, gate_scratch=gate)
+    gf = synthetic.bf16_to_f32(gate[pick]).astype(np.float64)
+    uf = synthetic.bf16_to_f32(plain[pick]).astype(np.float64)
+    want = uf * gf / (1 + np.exp(-gf))
+    got = synthetic.bf16_to_f32(up_gated[pick]).astype(np.float64)
+    ulp = np.ldexp(1.0, np.floor(np.log2(np.maximum(np.abs(want), 1e-30))).astype(int) - 7)
+    assert np.all(np.abs(got - want) <= ulp + 1e-30)
+    mixed = [w, make_weights(rng, oracle.FMT_Q6K, 2048, k)]
+    out = run_prefill(mixed, x)
+    check_projection(out[pick], x[pick], mixed, "stream af4g64 beside whole Q6_K tiles")
 
 
 def test_config3_q4k_prefill():
