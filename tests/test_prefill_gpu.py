@@ -395,6 +395,23 @@ def test_prefill_stream_pieces(fmt):
     assert np.all(np.abs(a - b) <= accumulation_bound(x, w, pick))
 
 
+@pytest.mark.parametrize("rows,n,k,fmt,want", [
+    (512, 49152, 1280, oracle.FMT_AF4G64, (256, 128, 86, 42)),    # two row blocks
+    (1900, 12288, 1280, oracle.FMT_Q4K, (256, 128, 88, 40)),      # eight, the last ragged
+])
+def test_prefill_stream_row_blocks(rows, n, k, fmt, want):
+    """The stream schedule over other row-block counts: each row block's ranges cover its own tiles (workgroups of a
+    row block run on the XCDs that hold its activations); the last row block's rows past the chunk are not written.
+    Sampled rows against fp64 and a second run bitwise the same."""
+    assert stream_schedule(rows, n, k) == want
+    w = make_weights(np.random.default_rng(rows + fmt), fmt, n, k)
+    rng = np.random.default_rng(rows + n)
+    x = dense_inputs(rng, rows, k)
+    out = run_prefill([w], x)
+    check_sampled(out, x, w, f"stream pieces, {rows} rows of {k} x {n}", rng, count=32)
+    assert np.array_equal(run_prefill([w], x), out)
+
+
 def test_prefill_stream_epilogues_and_segments():
     """Stream pieces under the residual and up-with-gate epilogues (applied once, by the tile's last piece), across
     a fused projection's segments (8192, 4096 and 12288 columns of af4g64), and beside a four-wave format's whole
