@@ -888,10 +888,11 @@ hipError_t launch_format(uint32_t epilogue, const PrefillArgs &args, hipStream_t
   if (!sc.split) {
     if (sc.bm == 128) return launch_tile<FMT, 128, 0>(epilogue, a, dim3(sc.row_blocks, sc.column_groups), stream);
     // Stream pieces run in the eight-wave tile only: the four-wave tile's 256 sums a lane leave no registers for the
-    // piece loop (its stream instance spills). Their epilogue addresses the output with 32-bit byte offsets.
+    // piece loop (its stream instance spills). Their epilogue addresses the output with 32-bit byte offsets, rows
+    // past the chunk included (up to the last row block's end), which must not wrap.
     if constexpr (tile_waves<FMT>() == 8) {
       const PrefillStream st = prefill_stream(sc.row_blocks, sc.column_groups, args.K);
-      if (st.stream_tiles && (uint64_t)args.rows * args.out_stride * 2 < (1ull << 31)) {
+      if (st.stream_tiles && (uint64_t)sc.row_blocks * 256 * args.out_stride * 2 < (1ull << 31)) {
         if (!a.partials || !a.counters) return hipErrorInvalidValue;
         a.stream_dp = st.dp_tiles;
         a.stream_tiles = st.stream_tiles;
