@@ -372,13 +372,14 @@ def stream_schedule(rows, n, k):
     return dp, tiles - dp, cut.count(2), cut.count(3)
 
 
-@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K])
+@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K, oracle.FMT_AF4G32, oracle.FMT_AF4G128])
 def test_prefill_stream_pieces(fmt):
     """Past whole rounds of tiles, the rest run as stream pieces (ranges of K steps over every compute unit, the last
     piece of a tile to arrive adding the pieces' fp32 sums in K order) in the same dispatch: 1024 rows of
     1280 x 24576 run 256 whole tiles, then 128 in pieces, 84 of them cut in two and 44 in three. Sampled rows against
     fp64, a second run bitwise the same (the sum does not depend on the order the pieces arrive in), and a 128-row
-    chunk of the rows (whole tiles) within two accumulation bounds."""
+    chunk of the rows (whole tiles) within two accumulation bounds. Every eight-wave format: a range is a multiple
+    of four 64-input steps, whole scale groups of 4-bit affine g32, g64 and g128 and whole Q4_K super-blocks."""
     n, k, rows = 24576, 1280, 1024
     assert stream_schedule(rows, n, k) == (256, 128, 84, 44)
     w = make_weights(np.random.default_rng(80 + fmt), fmt, n, k)
