@@ -314,10 +314,9 @@ __device__ __forceinline__ bool stream_arrive(const PrefillArgs &a, const f32x4 
 //   whole tiles: workgroup (x, y) runs row block x of column group y, all of K;
 //   SPLIT: workgroup (x, y, z) runs piece z of that tile, cut at split_at, whose fp32 sums a close dispatch adds
 //     (prefill_schedule);
-//   STREAM (prefill_stream): workgroup x runs steps [x range, (x + 1) range) of the stream tiles' steps laid end to
-//     end (tile t: row block t % stream_row_blocks of column group t / stream_row_blocks), one piece a tile it
-//     touches; a piece of every step runs the epilogue itself, a partial one meets the tile's other piece through
-//     the partials (stream_arrive).
+//   STREAM (prefill_stream): the first stream_dp workgroups run whole tiles; each of the others runs a range of
+//     steps of its row block's stream tiles laid end to end (below), one piece a tile it meets; a piece of every
+//     step runs the epilogue itself, and a tile's partial pieces meet through the partials (stream_arrive).
 // The body stays in the kernel (the pieces are an outer loop) rather than in a function it calls: the same body
 // optimised as a separate function before inlining takes more registers and spills.
 template <uint32_t FMT, uint32_t EP, int BM, bool SPLIT, int W, bool STREAM>
