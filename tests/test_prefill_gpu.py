@@ -218,6 +218,19 @@ def test_config2_prefill_shapes(n, k, rows):
     check_sampled(out, x, w, f"config 2 {k}x{n} rows {rows}", rng)
 
 
+@pytest.mark.parametrize("fmt", NEW_FORMATS)
+def test_adjacent_formats_prefill_full_size(fmt):
+    """The adjacent formats at the bench's full prefill size (M = 2048, K = 4096, N = 14336: 448 tiles of the
+    four-wave tile, two rounds over the compute units): sampled rows against fp64, the staged interval and no worse
+    than the staged emulation."""
+    n, k, rows = 14336, 4096, 2048
+    w = shape_weights(fmt, n, k, 40 + fmt)
+    rng = np.random.default_rng(4096 + fmt)
+    x = dense_inputs(rng, rows, k)
+    out = run_prefill([w], x)
+    check_sampled(out, x, w, f"fmt {fmt} at M 2048, 4096 x 14336", rng, count=24)
+
+
 def test_config2_ragged_with_small_rows():
     """Config 2's 4096 x 14336 at 2047 rows with rows scaled by 1e-5, 1e-6 and 1e-8 mixed in (the last 256-row tile
     ragged): the sampled rows, the small ones among them, inside their fp64 intervals and no worse than staged."""
