@@ -475,3 +475,23 @@ def test_decode_new_formats_longest_slices(fmt, rows):
     got = run_plan(staged(n, k, rows, 1), sq.projection(w.segment()), x, n)
     check_decode(got, x, w, f"fmt {fmt} rows {rows} k {k}")
 
+
+
+@pytest.mark.parametrize("fmt", NEW_FORMATS)
+@pytest.mark.parametrize("rows", [1, 16])
+def test_adjacent_formats_decode_full_size(fmt, rows):
+    """The adjacent formats at the bench's full decode size (K = 4096, N = 14336, M = 1 and 16) under the library's
+    own plan: every output against fp64 with the register tile's bound, and no worse than the reference's staged
+    numerics."""
+    n, k = 14336, 4096
+    w = shape_weights(fmt, n, k, 50 + fmt)
+    rng = np.random.default_rng(60 + fmt + rows)
+    x = dense_inputs(rng, rows, k)
+    proj = sq.projection(w.segment())
+    plan = sq.plan_for(sq.decode_workload(n, k, rows), proj)
+    got = run_plan(plan, proj, x, n)
+    stats = check_decode(got, x, w, f"fmt {fmt} {n}x{k} rows {rows}")
+    value, *_ = oracle.project_f64(x, w.values)
+    ref = synthetic.bf16_to_f32(staged_reference(x, w))
+    ref_l2 = np.linalg.norm(ref - value) / np.linalg.norm(value)
+    assert stats["rel_l2"] <= ref_l2 * 1.10 + 1e-6
