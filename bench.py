@@ -490,6 +490,20 @@ def main() -> int:
                     "frac_of_floor": round(pair_bytes / pair_sec / 1e9 / pair_floor["GB/s"], 3)}
     log(f"  gate/up pair K{k} N{n}: {pair_sec * 1e6:.2f} us, {gate_up_pair['GB/s']} GB/s")
     del pair
+    # The reference's published decode point: the 27B model's gate/up pair (N 17408, K 5120) for one lane of 8 rows,
+    # 245 us in two passes and 333 us in one on a 32-core M5 Max (docs/internals.md:498-500,
+    # LinearGguf.cpp:176-178); af4g64, the format of its sweeps, under this library's own plan.
+    lane = Gemv(torch, sq, synthetic, sq.FMT_AF4G64, 8, 17408, 5120, seed=27, gate_up=True)
+    lane_sec = time_graph(torch, lane.launch, args.steps, args.warmup)
+    lane_bytes = 2 * 17408 * 5120 * 0.5625 + 2 * 8 * 5120 + 2 * 8 * 17408
+    gate_up_lane = {"us": round(lane_sec * 1e6, 2), "GB/s": round(lane_bytes / lane_sec / 1e9, 1),
+                    "hbm_frac": round(lane_bytes / lane_sec / 1e9 / HBM_PEAK_GBS, 4),
+                    "one_pass": bool(lane.plan.config.one_gate_up_pass), "splits": lane.plan.config.splits,
+                    "reference_us": {"two_passes": 245.0, "one_pass": 333.0},
+                    "reference_device": "32-core M5 Max (docs/internals.md:498-500)",
+                    "speedup_vs_reference": round(245e-6 / lane_sec, 1)}
+    log(f"  27B gate/up pair, one lane (8 rows, K5120 N17408): {lane_sec * 1e6:.2f} us (reference 245 us on M5 Max)")
+    del lane
     torch.cuda.empty_cache()
     if args.calibrate_copy:
         # A plain device copy of known size for scaling the FETCH_SIZE / WRITE_SIZE counters.
@@ -627,6 +641,7 @@ def main() -> int:
                      "algorithmic_bytes": int(gemv_bytes(m, n, k))},
         "stream_floor": dict(floor, frac_of_floor=round(gbs / floor["GB/s"], 3)),
         "c1_gate_up_pair": gate_up_pair,
+        "c1_gate_up_pair_27b_lane": gate_up_lane,
     }
     result.update(extra)
     if "cpu" in sections:

@@ -260,8 +260,18 @@ LinearConfig Linear::baseline(LinearWorkload w, const Projection *p, const Proje
   const bool pair = w.phase == LinearPhase::Decode && w.epilogue == LinearEpilogue::GateUp && p && gate &&
                     p->blocks().segments.size() == 1 && gate->blocks().segments.size() == 1 &&
                     p->blocks().segments.front().formatId == gate->blocks().segments.front().formatId;
-  LinearConfig c{.tile = LinearTile::GgufStaged, .splits = decodeSplits(n, k, w.rows, planScaleGroups(p, gate), pair)};
+  const uint32_t unit = planScaleGroups(p, gate);
+  LinearConfig c{.tile = LinearTile::GgufStaged, .splits = decodeSplits(n, k, w.rows, unit, pair)};
   c.oneGateUpPass = pair;
+  // On the row tile a pair whose one pass would take K splits runs as two passes, each under the single tensor's
+  // split law (the split tail and the pair's shorter slices cost more than the second pass's activation loads).
+  // Measured (af4g64, graph-replayed): 17408 x 5120 at 5 / 8 / 16 / 32 rows 46.9 / 47.8 / 49.0 / 113.6 us in one
+  // pass (2, 2, 2, 4 splits) against 38.8 / 40.1 / 47.1 / 81.6 in two unsplit; 14336 x 4096 at 32 rows 40.1
+  // against 31.0. Unsplit pairs keep the one pass (14336 x 4096 at 5 to 16 rows: 15.3-17.0 us against 18.2-21.5).
+  if (pair && w.rows > kern::kColumnTileRows && c.splits > 1) {
+    c.oneGateUpPass = false;
+    c.splits = decodeSplits(n, k, w.rows, unit, false);
+  }
   return c;
 }
 

@@ -124,6 +124,14 @@ def test_gate_up_plans():
     assert gate_bytes == 0
     two = sq.plan_config(sq.decode_workload(14336, 4096, 8, sq.EPILOGUE_GATE_UP), sq.LinearConfig(sq.TILE_STAGED, 2, 0, 0, 0))
     assert sq.scratch_size(two)[1] == 8 * 14336 * 2
+    # On the row tile a pair whose one pass would take K splits runs as two passes under the single tensor's split
+    # law (and reports the gate scratch the first pass writes); unsplit pairs and the column tile keep one pass.
+    for (n, k), rows, want in [((14336, 4096), 4, (1, 1)), ((14336, 4096), 16, (1, 1)), ((14336, 4096), 32, (0, 1)),
+                               ((17408, 5120), 4, (1, 1)), ((17408, 5120), 8, (0, 1)), ((17408, 5120), 32, (0, 1))]:
+        up, gate = sq.projection(seg(n, k)), sq.projection(seg(n, k))
+        plan = sq.plan_for(sq.decode_workload(n, k, rows, sq.EPILOGUE_GATE_UP), up, gate)
+        assert (plan.config.one_gate_up_pass, plan.config.splits) == want, (n, k, rows)
+        assert sq.scratch_size(plan)[1] == (0 if want[0] else rows * n * 2)
 
 
 @pytest.mark.parametrize("workload,config,message", [
