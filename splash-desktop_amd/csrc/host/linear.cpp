@@ -239,10 +239,17 @@ uint32_t Linear::decodeSplits(uint32_t n, uint32_t k, uint32_t rows, uint32_t gr
   const uint32_t kind = column ? 1 : rows <= 16 ? 16 : SQ_MAXIMUM_DECODE_ROWS;
   const double tileBytes = (pair ? 2.0 : 1.0) * 64 * (k * 0.5 + G * 4.0 / groupUnit);
   const double budget = column ? kColumnBytes : kRowBytes;
+  // A column-tile pair whose tiles already outnumber the compute units takes the byte budget's split past them: its
+  // registers leave one workgroup a unit, so unsplit the tiles past a round trail in a short second one. Measured
+  // (graph-replayed, 17408 x 5120 at 1 / 2 / 4 rows, one pass unsplit against four splits): Q4_K 26.9 / 29.3 / 29.9
+  // -> 22.4 / 25.6 / 26.1 us, Q5_K 44.8 / 47.5 / 48.0 -> 36.3 / 39.5 / 40.2, Q6_K 46.7 / 49.5 / 50.5 -> 38.2 / 41.9
+  // / 42.9, Q8_0 54.2 / 56.3 / 57.3 -> 44.0 / 47.8 / 49.1, af4g64 25.5 / 27.2 / 28.4 -> 24.7 / 28.0 / 28.5; at
+  // 14336 x 4096 (224 tiles) the unsplit pair stays the faster in every format.
+  const bool pastUnits = column && pair && tiles > computeUnits_;
   uint32_t best = 0;
   for (uint32_t s = 1; s <= LinearConfig::kMaximumSplits && G % (s * groupUnit) == 0; s *= 2) {
     if (!kern::decode_layout(format, blocks, k, s, pair, kind).nb) continue;
-    if (best && uint64_t{tiles} * s > computeUnits_) break;
+    if (best && uint64_t{tiles} * s > computeUnits_ && !pastUnits) break;
     best = s;
     if (tileBytes / s <= budget) break;
   }
@@ -254,13 +261,16 @@ uint32_t Linear::decodeSplits(uint32_t n, uint32_t k, uint32_t rows, uint32_t gr
 }
 
 LinearConfig Linear::baseline(LinearWorkload w, const Projection *p, const Projection *gate) const {
-  const auto [n, k] = w.matrix;
   if (w.phase == LinearPhase::Prefill && w.rows > kMaximumStagedRows) return {.tile = LinearTile::GgufPrefill};
   // A gate/up pair of single tensors of one format runs in one dispatch: both walks share the activations' loads.
   const bool pair = w.phase == LinearPhase::Decode && w.epilogue == LinearEpilogue::GateUp && p && gate &&
                     p->blocks().segments.size() == 1 && gate->blocks().segments.size() == 1 &&
                     p->blocks().segments.front().formatId == gate->blocks().segments.front().formatId;
-  const uint32_t unit = planScaleGroups(p, gate);
+  return decodeConfig(w, planScaleGroups(p, gate), pair);
+}
+
+LinearConfig Linear::decodeConfig(LinearWorkload w, uint32_t unit, bool pair) const noexcept {
+  const auto [n, k] = w.matrix;
   LinearConfig c{.tile = LinearTile::GgufStaged, .splits = decodeSplits(n, k, w.rows, unit, pair)};
   c.oneGateUpPass = pair;
   // On the row tile a pair whose one pass would take K splits runs as two passes, each under the single tensor's
@@ -297,13 +307,19 @@ uint32_t Linear::decodeStorageRows(uint32_t rows, ProjectionShape shape) const {
   validate(w);
   return LinearPlan(w, baseline(w, nullptr, nullptr)).storageRows();
 }
+// Every decode plan a projection of this shape can take: the split law sees the format's scale-group unit (a
+// partition takes whole units: 1, 2, 4 or 8 groups of 32 inputs), and a gate/up plan may be a one-pass pair, whose
+// partials hold both tensors' columns.
 LinearScratchSize Linear::decodeScratchSize(ProjectionShape shape) const {
   LinearScratchSize bound;
   for (uint32_t rows = 1; rows <= SQ_MAXIMUM_DECODE_ROWS; ++rows)
-    for (const auto e : {LinearEpilogue::None, LinearEpilogue::Residual, LinearEpilogue::GateUp}) {
-      const LinearWorkload w{{shape.outputSize, shape.inputSize}, rows, LinearPhase::Decode, e};
-      bound.include(LinearPlan(w, baseline(w, nullptr, nullptr)).scratchSize());
-    }
+    for (const auto e : {LinearEpilogue::None, LinearEpilogue::Residual, LinearEpilogue::GateUp})
+      for (const uint32_t unit : {1u, 2u, 4u, 8u})
+        for (const bool pair : {false, true}) {
+          if (pair && e != LinearEpilogue::GateUp) continue;
+          const LinearWorkload w{{shape.outputSize, shape.inputSize}, rows, LinearPhase::Decode, e};
+          bound.include(LinearPlan(w, decodeConfig(w, unit, pair)).scratchSize());
+        }
   return bound;
 }
 // MI355X's float-tile policy: the matrix-core tile from kern::kFloatMfmaRows rows on, the lane chains below (a

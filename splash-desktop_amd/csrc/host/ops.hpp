@@ -219,6 +219,9 @@ public:
 private:
   [[nodiscard]] LinearConfig baseline(LinearWorkload workload, const Projection *projection,
                                       const Projection *gate) const;
+  // The decode plan of a projection whose formats take `unit` scale groups a meta unit; `pair` runs a gate/up pair
+  // of one format as one pass where the policy keeps it.
+  [[nodiscard]] LinearConfig decodeConfig(LinearWorkload workload, uint32_t unit, bool pair) const noexcept;
   uint32_t computeUnits_;
 };
 

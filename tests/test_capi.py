@@ -125,9 +125,11 @@ def test_gate_up_plans():
     two = sq.plan_config(sq.decode_workload(14336, 4096, 8, sq.EPILOGUE_GATE_UP), sq.LinearConfig(sq.TILE_STAGED, 2, 0, 0, 0))
     assert sq.scratch_size(two)[1] == 8 * 14336 * 2
     # On the row tile a pair whose one pass would take K splits runs as two passes under the single tensor's split
-    # law (and reports the gate scratch the first pass writes); unsplit pairs and the column tile keep one pass.
+    # law (and reports the gate scratch the first pass writes); unsplit pairs and the column tile keep one pass. A
+    # column-tile pair of more tiles than compute units (17408 columns: 272) takes the byte budget's split past them.
     for (n, k), rows, want in [((14336, 4096), 4, (1, 1)), ((14336, 4096), 16, (1, 1)), ((14336, 4096), 32, (0, 1)),
-                               ((17408, 5120), 4, (1, 1)), ((17408, 5120), 8, (0, 1)), ((17408, 5120), 32, (0, 1))]:
+                               ((17408, 5120), 1, (1, 4)), ((17408, 5120), 4, (1, 4)), ((17408, 5120), 8, (0, 1)),
+                               ((17408, 5120), 32, (0, 1))]:
         up, gate = sq.projection(seg(n, k)), sq.projection(seg(n, k))
         plan = sq.plan_for(sq.decode_workload(n, k, rows, sq.EPILOGUE_GATE_UP), up, gate)
         assert (plan.config.one_gate_up_pass, plan.config.splits) == want, (n, k, rows)
@@ -210,6 +212,20 @@ def test_scratch_bounds_cover_every_plan():
         for e in (sq.EPILOGUE_NONE, sq.EPILOGUE_RESIDUAL):
             size, _ = sq.scratch_size(sq.plan_for(sq.decode_workload(14336, 4096, rows, e)))
             assert size.partials <= out.partials and size.counters <= out.counters
+    # The bound holds the plans of projections of every format, and the one-pass gate/up pairs (whose partials
+    # hold both tensors' columns) among them.
+    for n, k in [(14336, 4096), (17408, 5120), (2048, 2048), (4096, 14336)]:
+        sq.call("sq_linear_decode_scratch_size", sq.byref(dev), n, k, sq.byref(out))
+        pairs = 0
+        for fmt in sq.FORMATS:
+            up, gate = sq.projection(seg(n, k, fmt)), sq.projection(seg(n, k, fmt))
+            for rows in range(1, 33):
+                for e in (sq.EPILOGUE_NONE, sq.EPILOGUE_RESIDUAL, sq.EPILOGUE_GATE_UP):
+                    plan = sq.plan_for(sq.decode_workload(n, k, rows, e), up, gate if e == sq.EPILOGUE_GATE_UP else None)
+                    size, _ = sq.scratch_size(plan)
+                    assert size.partials <= out.partials and size.counters <= out.counters, (n, k, fmt, rows, e)
+                    pairs += plan.config.one_gate_up_pass and plan.config.splits > 1
+        assert n != 17408 or pairs, "a split one-pass pair among the plans"
     sq.call("sq_linear_prefill_scratch_size", sq.byref(dev), 14336, 4096, sq.byref(out))
     assert out.input == 2048 * 4096 * 2
 
