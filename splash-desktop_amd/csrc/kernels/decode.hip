@@ -14,6 +14,7 @@
 #include "device.hpp"
 #include "kernels.hpp"
 #include "rowtile.hpp"
+#include "split.hpp"
 
 namespace sq::kern {
 namespace {
@@ -151,21 +152,33 @@ __global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeA
   if (threadIdx.x == 0) arrival = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   if (arrival != a.splits - 1) return;
+  // Four of the wave's outputs at a time: their splits' loads go out together (sum_splits), each output summed in
+  // split order as one at a time would be.
+  constexpr int kBatch = FO < 4 ? FO : 4;
 #pragma unroll 1
-  for (uint32_t f = slice; f < FO; f += waves) {
-    uint32_t row, col;
-    place(f, row, col);
-    if (row >= a.rows) continue;
-    float v[NT];
+  for (uint32_t f0 = slice; f0 < FO; f0 += kBatch * waves) {
+    uint32_t row[kBatch], col[kBatch];
+    float sum[kBatch * NT], *at[kBatch * NT];
+    bool on[kBatch * NT];
 #pragma unroll
-    for (int n = 0; n < NT; ++n) {
-      float sum = 0.0f;
-      for (uint32_t p = 0; p < a.splits; ++p)
-        sum += __hip_atomic_load(&a.partials[p * split_elements + (size_t)row * cstride + n * a.out_stride + col],
-                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      v[n] = sum;
+    for (int d = 0; d < kBatch; ++d) {
+      const uint32_t f = f0 + d * waves;
+      place(f < FO ? f : f0, row[d], col[d]);
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        on[d * NT + n] = f < FO && row[d] < a.rows;
+        at[d * NT + n] = a.partials + (size_t)row[d] * cstride + n * a.out_stride + col[d];
+      }
     }
-    store(v, row, col);
+    sum_splits(sum, on, at, split_elements, a.splits);
+#pragma unroll
+    for (int d = 0; d < kBatch; ++d) {
+      if (!on[d * NT]) continue;
+      float v[NT];
+#pragma unroll
+      for (int n = 0; n < NT; ++n) v[n] = sum[d * NT + n];
+      store(v, row[d], col[d]);
+    }
   }
   __syncthreads();
   if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

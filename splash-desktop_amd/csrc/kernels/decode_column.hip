@@ -22,7 +22,8 @@
 //    for the whole dispatch instead of in one burst. The slices meet in LDS in slice order, each row's outputs
 //    summed and stored by a wave of their own.
 //  - One workgroup covers a tile's whole K unless the launcher's layout splits it: a split across workgroups adds
-//    three device-scope round trips at the end of the dispatch (split_reduce), which only pays when the tiles alone
+//    device-scope round trips at the end of the dispatch (split_reduce: the partials' stores, the counter, the last
+//    arriver's loads, two splits a trip), which only pays when the tiles alone
 //    leave most compute units idle.
 //  - A dispatch of few tiles (column_slices 4) runs four 16-column workgroups a tile instead, each wave four of the
 //    layout's K slices in its 16-lane quarters (the MFMA's A broadcast to a quarter's four blocks, cbsz 2): each

@@ -7,6 +7,36 @@
 
 namespace sq::kern {
 
+// sum[i] = the live values' partials at at[i] + p * stride added in split order p = 0..splits-1 (from 0). Two splits'
+// loads of every value go out before their adds, so the sum waits for one memory round trip per two splits; the
+// loop stays a loop, so the tail's code stays short.
+template <int N>
+__device__ __forceinline__ void sum_splits(float (&sum)[N], const bool (&live)[N], float *const (&at)[N],
+                                           size_t stride, uint32_t splits) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) sum[i] = 0.0f;
+  uint32_t p = 0;
+#pragma unroll 1
+  for (; p + 2 <= splits; p += 2) {
+    float got[2][N];
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+      for (int i = 0; i < N; ++i)
+        got[d][i] = live[i] ? __hip_atomic_load(at[i] + (size_t)(p + d) * stride, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT)
+                            : 0.0f;
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+      for (int i = 0; i < N; ++i) sum[i] += got[d][i];
+  }
+  if (p < splits)
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (live[i]) sum[i] += __hip_atomic_load(at[i] + (size_t)p * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Adds this split's totals to the others' in split order when this workgroup arrives last; returns false when
 // another workgroup still has to arrive. index[b][i]: the partial's offset within a split.
 //
@@ -34,18 +64,22 @@ __device__ __forceinline__ bool split_reduce(float (&total)[NB][R], const bool (
   __syncthreads();
   if (arrival != splits - 1) return false;
   if (owner) {
+    // Every split's partials, this one's included (its stores above hold `total` bit for bit).
+    float sum[NB * R], *at[NB * R];
+    bool on[NB * R];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int i = 0; i < R; ++i) {
-        if (!live[b][i]) continue;
-        float v = 0.0f;
-        for (uint32_t p = 0; p < splits; ++p)
-          v += p == split ? total[b][i]
-                          : __hip_atomic_load(&partials[p * split_elements + index[b][i]], __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-        total[b][i] = v;
+        at[b * R + i] = partials + index[b][i];
+        on[b * R + i] = live[b][i];
       }
+    sum_splits(sum, on, at, split_elements, splits);
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int i = 0; i < R; ++i)
+        if (live[b][i]) total[b][i] = sum[b * R + i];
   }
   __syncthreads();
   if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
