@@ -128,8 +128,15 @@ __global__ __launch_bounds__(64 * row_max_waves(MB, NT)) void row_kernel(DecodeA
     float v[NT];
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
-      float sum = 0.0f;
-      for (uint32_t w = 0; w < waves; ++w) sum += red[(w * A + n * FO + f) * 64 + lane];
+      // Every wave slot's read goes out at once (slots past the workgroup's waves hold nothing the sum takes), then
+      // the adds run in slice order.
+      constexpr uint32_t kSlots = row_max_waves(MB, NT);
+      float part[kSlots], sum = 0.0f;
+#pragma unroll
+      for (uint32_t w = 0; w < kSlots; ++w) part[w] = red[(w * A + n * FO + f) * 64 + lane];
+#pragma unroll
+      for (uint32_t w = 0; w < kSlots; ++w)
+        if (w < waves) sum += part[w];
       v[n] = sum;
     }
     if (row >= a.rows) continue;

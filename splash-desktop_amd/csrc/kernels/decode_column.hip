@@ -310,8 +310,16 @@ __global__ __launch_bounds__(64 * kColumnMaxWaves) void column_kernel(DecodeArgs
     for (int r = 0; r < MR; ++r) {
       const bool mine = (uint32_t)r % waves == slice && (!NARROW || lane < 16);
       float v = 0.0f;
-      if (mine)
-        for (uint32_t w = 0; w < slices; ++w) v += red[w][n][r][c];
+      if (mine) {
+        // Every slot's read goes out at once (slots past the slices hold nothing the sum takes), then the adds run
+        // in slice order.
+        float part[kColumnMaxWaves];
+#pragma unroll
+        for (uint32_t w = 0; w < kColumnMaxWaves; ++w) part[w] = red[w][n][r][c];
+#pragma unroll
+        for (uint32_t w = 0; w < kColumnMaxWaves; ++w)
+          if (w < slices) v += part[w];
+      }
       total[n][r] = v;
       rlive[n][r] = mine && (uint32_t)r < a.rows;
       index[n][r] = (size_t)r * cstride + n * a.out_stride + col;
