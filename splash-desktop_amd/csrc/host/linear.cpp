@@ -227,6 +227,21 @@ constexpr uint64_t kRowSliceUnits = 1;
 // M = 8 / 16 8.4 / 8.8 -> 7.1 / 8.4 us (two splits before); K 14336 x N 4096 (129 KB each) lost, 12.6 -> 18.8 us
 // at M = 8, and so did a tile already in 16-column workgroups made unsplit (N 1024 at M = 16, 7.5 -> 7.9 us).
 constexpr double kRowNarrowBytes = 40e3;
+// A row tile already split whose split, doubled, would still fit 16-column workgroups on the compute units takes
+// the doubled split while each K partition still streams at least kRowFillBytes: the few tiles then spread over
+// the whole device, and the split tail, paid once, costs little more. Measured (graph-replayed, one box, M = 8 /
+// 16 / 32): K 4096 x N 1024 6.81 / 7.44 / 9.32 -> 6.70 / 6.99 / 8.10 us (four splits, not two), N 512 6.58 / 7.24
+// / 9.13 -> 6.24 / 6.60 / 7.71; an unsplit tile stays unsplit (K 2048 x N 1024 at two splits: 4.6 -> 5.7 us at
+// M = 8), and a split whose 64-column workgroups already fill a quarter of the device stays (K 4096 x N 2048 at
+// four splits: 6.88 -> 7.68 us at M = 8).
+constexpr double kRowFillBytes = 32e3;
+// A split of more than two that leaves the row tile in 64-column workgroups gives way to the largest smaller split
+// (of at least two) whose 16-column workgroups fit the compute units, while each of those streams at most
+// kRowNarrowSplitBytes. Measured (M = 8 / 16 / 32): K 5120 x N 2048 af4g64 8.32 / 8.52 / 11.98 -> 7.48 / 8.31 /
+// 11.41 us, Q4_K 8.99 / 9.16 / 12.70 -> 7.55 / 8.30 / 11.50 (two splits, 23 and 21 KB a workgroup, not four);
+// K 8192 x N 2048 (37 KB a workgroup in two splits) stays at four: 8.50 / 8.98 / 11.50 against 9.03 / 10.33 /
+// 14.30.
+constexpr double kRowNarrowSplitBytes = 30e3;
 }  // namespace
 
 uint32_t Linear::decodeSplits(uint32_t n, uint32_t k, uint32_t rows, uint32_t groupUnit, bool pair) const noexcept {
@@ -254,9 +269,23 @@ uint32_t Linear::decodeSplits(uint32_t n, uint32_t k, uint32_t rows, uint32_t gr
     if (tileBytes / s <= budget) break;
   }
   const uint64_t narrowUnits = kRowSliceUnits * computeUnits_;
-  if (!column && best > 1 && uint64_t{tiles} * best * 4 > narrowUnits && uint64_t{tiles} * 4 <= narrowUnits &&
-      tileBytes / 4 <= kRowNarrowBytes && kern::decode_layout(format, blocks, k, 1, pair, kind).nb)
+  // The unsplit 16-column rule holds for the tile of up to 16 rows; with 32 rows the split measured faster (K 4096
+  // x N 4096 at M = 32: 12.48 us unsplit, 10.88 in two splits).
+  if (!column && kind <= 16 && best > 1 && uint64_t{tiles} * best * 4 > narrowUnits &&
+      uint64_t{tiles} * 4 <= narrowUnits && tileBytes / 4 <= kRowNarrowBytes &&
+      kern::decode_layout(format, blocks, k, 1, pair, kind).nb)
     return 1;
+  if (!column && best > 2 && uint64_t{tiles} * best * 4 > narrowUnits)
+    for (uint32_t s = best / 2; s >= 2; s /= 2)
+      if (uint64_t{tiles} * s * 4 <= narrowUnits) {
+        if (tileBytes / (4.0 * s) <= kRowNarrowSplitBytes && kern::decode_layout(format, blocks, k, s, pair, kind).nb)
+          best = s;
+        break;
+      }
+  while (!column && best > 1 && best * 2 <= LinearConfig::kMaximumSplits && G % (best * 2 * groupUnit) == 0 &&
+         uint64_t{tiles} * best * 2 * 4 <= narrowUnits && tileBytes / (best * 2) >= kRowFillBytes &&
+         kern::decode_layout(format, blocks, k, best * 2, pair, kind).nb)
+    best *= 2;
   return best ? best : 1;
 }
 

@@ -47,15 +47,19 @@ def test_decode_plans(n, k, rows):
     assert size.counters == (n // 16 * 4 if s > 1 else 0)
     # the split depends on the tile kind the rows run, never on the rows: a row's result is the same in any batch
     # of its kind
-    assert s == sq.plan_for(sq.decode_workload(n, k, 1 if rows <= 4 else 32), proj).config.splits
+    kind = 1 if rows <= 4 else 16 if rows <= 16 else 32
+    assert s == sq.plan_for(sq.decode_workload(n, k, kind), proj).config.splits
     assert gate == 0
 
 
-def split_law(n, k, budget, max_waves=16, pair=False, row=False):
+def split_law(n, k, budget, max_waves=16, pair=False, row=False, rows=16):
     """The fewest splits whose workgroups stream at most `budget` bytes, the grid kept within 256 compute units,
     among splits whose K slices fit one workgroup (at most `max_waves` waves of at most 32 groups). The row tile
-    (`row`) runs a tile unsplit in four 16-column workgroups instead of split 64-column ones while the four fit the
-    compute units and each streams at most 40 KB."""
+    (`row`) of up to 16 rows runs a tile unsplit in four 16-column workgroups instead of split 64-column ones while
+    the four fit the compute units and each streams at most 40 KB; a row tile already split doubles its split while
+    the doubled split's 16-column workgroups fit the compute units and each K partition streams at least 32 KB; a
+    split of more than two in 64-column workgroups gives way to the largest smaller one (of at least two) whose
+    16-column workgroups fit the compute units and stream at most 30 KB each."""
     tiles, groups = n // 64, k // 32
     tile_bytes = (2 if pair else 1) * 64 * (k * 0.5 + groups * 2.0)
     best = None
@@ -67,8 +71,18 @@ def split_law(n, k, budget, max_waves=16, pair=False, row=False):
         best = s
         if tile_bytes / s <= budget:
             break
-    if row and best > 1 and tiles * best * 4 > 256 and tiles * 4 <= 256 and tile_bytes / 4 <= 40e3:
+    if row and rows <= 16 and best > 1 and tiles * best * 4 > 256 and tiles * 4 <= 256 and tile_bytes / 4 <= 40e3:
         return 1
+    if row and best > 2 and tiles * best * 4 > 256:
+        s = best // 2
+        while s >= 2:
+            if tiles * s * 4 <= 256:
+                if tile_bytes / (4 * s) <= 30e3:
+                    best = s
+                break
+            s //= 2
+    while row and best > 1 and groups % (4 * best) == 0 and tiles * best * 8 <= 256 and tile_bytes / (2 * best) >= 32e3:
+        best *= 2
     return best
 
 
@@ -80,15 +94,21 @@ def test_split_law_column_tile(n, k, want):
     assert s == want == split_law(n, k, 160e3)
 
 
-@pytest.mark.parametrize("rows", [8, 16])
-@pytest.mark.parametrize("n,k,want", [(14336, 4096, 1), (1024, 4096, 2), (2048, 4096, 2), (4096, 4096, 1),
-                                      (3072, 4096, 1), (4096, 8192, 4), (4096, 14336, 4)])
+@pytest.mark.parametrize("rows", [8, 16, 32])
+@pytest.mark.parametrize("n,k,want", [(14336, 4096, 1), (1024, 4096, 4), (512, 4096, 4), (2048, 4096, 2),
+                                      (4096, 4096, 1), (3072, 4096, 1), (4096, 8192, 4), (4096, 14336, 4),
+                                      (1024, 2048, 1), (1024, 8192, 4), (2048, 8192, 4), (2048, 5120, 2)])
 def test_split_law_row_tile(rows, n, k, want):
-    """5..32 rows: workgroups of at most 80 KB; unsplit 16-column workgroups where the split would leave a few tiles
-    in 64-column ones (4096 x 4096, 3072 x 4096), not where the split already fits 16-column ones (1024, 2048) or the
-    unsplit ones would stream more than 40 KB (K 8192, 14336)."""
+    """5..32 rows: workgroups of at most 80 KB; up to 16 rows, unsplit 16-column workgroups where the split would
+    leave a few tiles in 64-column ones (4096 x 4096, 3072 x 4096: two splits at 32 rows), not where the split
+    already fits 16-column ones (2048) or the unsplit ones would stream more than 40 KB (K 8192, 14336); a split of
+    few tiles doubled while its 16-column workgroups fit the device and each split streams 32 KB (1024 and 512 x
+    4096: four splits, not two); an unsplit tile stays unsplit (1024 x 2048); four splits in 64-column workgroups
+    give way to two in 16-column ones of at most 30 KB (2048 x 5120), not of 37 KB (2048 x 8192)."""
+    if rows == 32 and (n, k) in ((4096, 4096), (3072, 4096)):
+        want = 2
     s = sq.plan_for(sq.decode_workload(n, k, rows), sq.projection(seg(n, k))).config.splits
-    assert s == want == split_law(n, k, 80e3, row=True)
+    assert s == want == split_law(n, k, 80e3, row=True, rows=rows)
 
 
 def test_prefill_plans():

@@ -360,12 +360,12 @@ def shape_weights(fmt, n, k, seed):
     return _SHAPE_CACHE[key]
 
 
-@pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
-@pytest.mark.parametrize("rows", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (2048, 5120)])
+@pytest.mark.parametrize("rows", [1, 2, 4, 8, 16, 32])
 def test_config1_sweep_policy_plans(n, k, rows):
     """BASELINE config 1's decode sweep (and config 0, the 4096 x 4096 shape at M = 1): every shape at every M under
     the library's own plan, every output against fp64 with the register tile's bound, and no worse than the
-    reference's staged numerics."""
+    reference's staged numerics. 2048 x 5120 adds the split law's two splits in 16-column workgroups."""
     w = shape_weights(oracle.FMT_AF4G64, n, k, n + k)
     rng = np.random.default_rng(n + k + rows)
     x = dense_inputs(rng, rows, k)
@@ -380,11 +380,11 @@ def test_config1_sweep_policy_plans(n, k, rows):
 
 
 @pytest.mark.parametrize("n", [3072, 4096])
-@pytest.mark.parametrize("rows", [5, 32])
+@pytest.mark.parametrize("rows", [5, 16])
 def test_row_tile_unsplit_plans(n, rows):
-    """K 4096 at 48 or 64 tiles: the split law leaves the row tile unsplit in 16-column workgroups (a split would
-    leave it in 64-column ones). Every output against fp64 with the register tile's bound, and the same bits as the
-    unsplit 64-column workgroups of the same weights widened past the compute units."""
+    """K 4096 at 48 or 64 tiles: the split law leaves the row tile of up to 16 rows unsplit in 16-column workgroups
+    (a split would leave it in 64-column ones). Every output against fp64 with the register tile's bound, and the
+    same bits as the unsplit 64-column workgroups of the same weights widened past the compute units."""
     k = 4096
     w = shape_weights(oracle.FMT_AF4G64, n, k, 7 + n)
     rng = np.random.default_rng(n + rows)
