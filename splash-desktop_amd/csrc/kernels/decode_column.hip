@@ -75,29 +75,29 @@ __device__ __forceinline__ void column_walk(const DecodeArgs &a, const Segment &
   const uint32_t col = NARROW ? 16 * cs + c16 : lane, mine = NARROW ? 4 * slice + (lane >> 4) : slice;
   const uint32_t gb = split * gs + (NARROW && mine >= slices ? 0 : mine) * GW;
   const uint32_t live = NARROW ? GW : min((uint32_t)GW, gs - min(gs, slice * GW));
-  const uint32_t last = live ? live - 1 : 0;
+  // The slice's last group: wave-uniform (the scalar offsets below clamp to it).
+  const uint32_t last = __builtin_amdgcn_readfirstlane(live ? live - 1 : 0);
 
-  const uint8_t *plane[NT], *meta[NT], *high[NT];
-  {
-    const size_t pbase = ((size_t)tile * G * 64 + col) * F::P0 + (size_t)gb * 64 * F::P0;
-    const size_t hbase = ((size_t)tile * G * 64 + col) * F::P1 + (size_t)gb * 64 * F::P1;
-    const size_t mbase = ((size_t)tile * units * 64 + col) * F::META + (size_t)(gb / UNIT) * 64 * F::META;
-    const Segment &first = NT == 2 ? a.gate : seg;
-    plane[0] = first.plane0 + pbase;
-    meta[0] = first.meta + mbase;
-    high[0] = F::P1 ? first.plane1 + hbase : nullptr;
-    if constexpr (NT == 2) {
-      plane[1] = seg.plane0 + pbase;
-      meta[1] = seg.meta + mbase;
-      high[1] = F::P1 ? seg.plane1 + hbase : nullptr;
-    }
+  // Buffer resources over the tile's planes (scalar registers) and a 32-bit offset a lane: the slice's start and
+  // the lane's column. Group g's loads add g's offset as the scalar offset, so the walk's addresses cost no vector
+  // instructions; a load past the tile's planes reads zero.
+  __amdgpu_buffer_rsrc_t planes[NT], metas[NT], highs_at[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const Segment &src = NT == 2 && n == 0 ? a.gate : seg;
+    planes[n] = buffer_rsrc(src.plane0 + (size_t)tile * G * 64 * F::P0, G * 64 * F::P0);
+    metas[n] = buffer_rsrc(src.meta + (size_t)tile * units * 64 * F::META, units * 64 * F::META);
+    if constexpr (F::P1) highs_at[n] = buffer_rsrc(src.plane1 + (size_t)tile * G * 64 * F::P1, G * 64 * F::P1);
   }
+  const uint32_t pv = (gb * 64 + col) * F::P0, hv = (gb * 64 + col) * F::P1;
+  const uint32_t mv = (gb / UNIT * 64 + col) * F::META;
   // Wide: lane (b, i) reads row i's inputs 4 (b % 8)..+3 of the pair's group b / 8. Narrow: lane (q, a, i) =
   // 16q + 4a + i reads row i's inputs 8a..8a + 7 of each group of its quarter's slice, so block 4q + a holds the
   // group's input quads 2a (low half) and 2a + 1 (high half). Rows past the live ones read row 0, whose MFMA rows
   // nothing reads.
-  const uint16_t *xrow = a.input + (size_t)(i < MR && (uint32_t)i < a.rows ? i : 0) * a.K +
-                         (NARROW ? 8 * xa : 4 * (b & 7)) + (size_t)gb * 32;
+  const __amdgpu_buffer_rsrc_t inputs = buffer_rsrc(a.input, a.rows * a.K * 2);
+  const uint32_t xv = (((i < MR && (uint32_t)i < a.rows ? i : 0) * a.K + (NARROW ? 8 * xa : 4 * (b & 7)) + gb * 32) +
+                       (NARROW ? 0 : 32 * (b >> 3))) * 2;
   const CodeConstants cc = make_code_constants();
 
 #pragma unroll
@@ -112,23 +112,23 @@ __device__ __forceinline__ void column_walk(const DecodeArgs &a, const Segment &
   u32x4 codes_hi[NT][kWide ? GW : 1];
   u32x2 highs[NT][F::P1 ? GW : 1];
   MetaWords mw[NT][GW / UNIT];
+  // Groups past the slice repeat its last one (the clamp is wave-uniform, so scalar); a wide pair's high lanes read
+  // the group after it, which nothing computes on past the slice.
   const auto issue = [&](int u) __attribute__((always_inline)) {
-    if constexpr (NARROW) xn[u] = *(const u32x4 *)(xrow + (size_t)min((uint32_t)u, last) * 32);
-    else if (u % 2 == 0) xp[u / 2] = *(const u32x2 *)(xrow + (size_t)min((uint32_t)(u + (b >> 3)), last) * 32);
+    const uint32_t g = min((uint32_t)u, last);
+    if constexpr (NARROW) xn[u] = buffer_b128<0>(inputs, xv, (uint32_t)u * 64);
+    else if (u % 2 == 0) xp[u / 2] = buffer_b64<0>(inputs, xv, g * 64);
     if (u % UNIT == 0) {
       const uint32_t v = min((uint32_t)(u / UNIT), last / UNIT);
 #pragma unroll
-      for (int n = 0; n < NT; ++n) mw[n][u / UNIT] = load_meta<FMT>(meta[n] + (size_t)v * 64 * F::META);
+      for (int n = 0; n < NT; ++n) mw[n][u / UNIT] = buffer_meta<FMT>(metas[n], mv, v * 64 * F::META);
     }
-    const uint32_t g = min((uint32_t)u, last);
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
-      const uint8_t *unit = plane[n] + (size_t)g * 64 * F::P0;
-      codes[n][u] = __builtin_nontemporal_load((const u32x4 *)unit);
-      if constexpr (kWide) codes_hi[n][u] = __builtin_nontemporal_load((const u32x4 *)(unit + 16));
-      if constexpr (F::P1 == 4)
-        highs[n][u][0] = __builtin_nontemporal_load((const uint32_t *)(high[n] + (size_t)g * 64 * F::P1));
-      if constexpr (F::P1 == 8) highs[n][u] = __builtin_nontemporal_load((const u32x2 *)(high[n] + (size_t)g * 64 * F::P1));
+      codes[n][u] = buffer_b128(planes[n], pv, g * 64 * F::P0);
+      if constexpr (kWide) codes_hi[n][u] = buffer_b128(planes[n], pv, g * 64 * F::P0 + 16);
+      if constexpr (F::P1 == 4) highs[n][u][0] = buffer_b32(highs_at[n], hv, g * 64 * F::P1);
+      if constexpr (F::P1 == 8) highs[n][u] = buffer_b64(highs_at[n], hv, g * 64 * F::P1);
     }
   };
   // The rows' input sums of the slice's groups (of each half for Q6_K): lanes 8j..8j+7 take one (row, group), each

@@ -168,6 +168,43 @@ __device__ __forceinline__ MetaWords load_meta(const uint8_t *unit_row) {
   return m;
 }
 
+// Raw buffer loads: a resource (base and byte range, in scalar registers) over a wave-uniform base, a 32-bit vector
+// offset a lane and a scalar offset, so a walk's per-group addresses cost no vector instructions; a load past the
+// range reads zero. kStream marks a load as streamed once (nontemporal).
+constexpr int kStream = 2;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+}
+template <int POLICY = kStream>
+__device__ __forceinline__ u32x4 buffer_b128(__amdgpu_buffer_rsrc_t r, uint32_t voffset, uint32_t soffset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, POLICY));
+}
+template <int POLICY = kStream>
+__device__ __forceinline__ u32x2 buffer_b64(__amdgpu_buffer_rsrc_t r, uint32_t voffset, uint32_t soffset) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voffset, soffset, POLICY));
+}
+template <int POLICY = kStream>
+__device__ __forceinline__ uint32_t buffer_b32(__amdgpu_buffer_rsrc_t r, uint32_t voffset, uint32_t soffset) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voffset, soffset, POLICY);
+}
+// load_meta through a buffer resource: the meta unit at voffset + soffset.
+template <uint32_t FMT>
+__device__ __forceinline__ MetaWords buffer_meta(__amdgpu_buffer_rsrc_t r, uint32_t voffset, uint32_t soffset) {
+  MetaWords m{};
+  if constexpr (Fmt<FMT>::META == 4) {
+    m.w[0] = buffer_b32(r, voffset, soffset);
+  } else if constexpr (Fmt<FMT>::META == 2) {
+    m.w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, voffset, soffset, kStream);
+  } else if constexpr (Fmt<FMT>::META == 20) {   // 4-byte aligned only
+#pragma unroll
+    for (int i = 0; i < 5; ++i) m.w[i] = buffer_b32(r, voffset, soffset + 4 * i);
+  } else {
+    const u32x4 v = buffer_b128(r, voffset, soffset);
+    m.w[0] = v[0]; m.w[1] = v[1]; m.w[2] = v[2]; m.w[3] = v[3];
+  }
+  return m;
+}
+
 // The scale s and offset z of scale group `sg` of a column: value = fma(q, s, z). Affine: the group's bf16 s and z
 // (quant_formats.h:614-616). Q4_K: s = d * sc and z = -(dmin * mn) of sub-block sg % 8 with the 6-bit sc, mn of
 // the header's 12 scale bytes (quant_formats.h:105-118; llama.cpp's get_scale_min_k4), both products exact.
