@@ -32,31 +32,29 @@ __device__ __forceinline__ void row_walk(const DecodeArgs &a, const Segment &seg
   using F = Fmt<FMT>;
   const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
   const uint32_t G = a.K >> 5, units = G / F::UNIT, col = TB == 1 ? 16 * cs + j : lane;
-  const uint8_t *plane[NT], *high[NT], *meta[NT];
+  RowBuffers<FMT, NT, MB, TB> src;
   {
-    const size_t chunk = TB == 1 ? (size_t)q * (F::P0 / 4) : 0, word = TB == 1 && F::P1 == 8 ? 4 * (q >> 1) : 0;
-    const size_t pbase = ((size_t)tile * G * 64 + col) * F::P0 + chunk + (size_t)gb * 64 * F::P0;
-    const size_t hbase = ((size_t)tile * G * 64 + col) * F::P1 + word + (size_t)gb * 64 * F::P1;
-    const size_t mbase = ((size_t)tile * units * 64 + col) * F::META + (size_t)(gb / F::UNIT) * 64 * F::META;
-    const Segment &first = NT == 2 ? a.gate : seg;
-    plane[0] = first.plane0 + pbase;
-    high[0] = F::P1 ? first.plane1 + hbase : nullptr;
-    meta[0] = first.meta + mbase;
-    if constexpr (NT == 2) {
-      plane[1] = seg.plane0 + pbase;
-      high[1] = F::P1 ? seg.plane1 + hbase : nullptr;
-      meta[1] = seg.meta + mbase;
+    const uint32_t chunk = TB == 1 ? q * (F::P0 / 4) : 0, word = TB == 1 && F::P1 == 8 ? 4 * (q >> 1) : 0;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const Segment &from = NT == 2 && n == 0 ? a.gate : seg;
+      src.plane[n] = buffer_rsrc(from.plane0 + (size_t)tile * G * 64 * F::P0, G * 64 * F::P0);
+      if constexpr (F::P1) src.high[n] = buffer_rsrc(from.plane1 + (size_t)tile * G * 64 * F::P1, G * 64 * F::P1);
+      src.meta[n] = buffer_rsrc(from.meta + (size_t)tile * units * 64 * F::META, units * 64 * F::META);
     }
+    src.pv = (gb * 64 + col) * F::P0 + chunk;
+    src.hv = (gb * 64 + col) * F::P1 + word;
+    src.mv = (gb / F::UNIT * 64 + col) * F::META;
   }
   // Lane (j, q) of row block b reads row 16 b + j's inputs 8q..8q+7 of each group (row_slice puts them into the
   // MFMA's A layout through the wave's LDS slot); rows past the live ones read row 0, whose results nothing stores.
-  const uint16_t *xrow[MB];
+  src.input = buffer_rsrc(a.input, a.rows * a.K * 2);
 #pragma unroll
   for (int b = 0; b < MB; ++b) {
     const uint32_t r = 16u * b + j;
-    xrow[b] = a.input + (size_t)(r < a.rows ? r : 0) * a.K + 8 * q + (size_t)gb * 32;
+    src.xv[b] = ((r < a.rows ? r : 0) * a.K + 8 * q + gb * 32) * 2;
   }
-  row_slice<FMT, MB, GW, NT, TB>(plane, high, meta, xrow, xlds, live, acc);
+  row_slice<FMT, MB, GW, NT, TB>(src, xlds, live, acc);
 }
 
 // FMT kSegmentFormats: each workgroup runs its segment's format. TB 1: workgroup x takes column block x % 4 of tile

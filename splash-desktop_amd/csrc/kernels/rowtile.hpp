@@ -71,6 +71,42 @@ __device__ __forceinline__ RowGroup<FMT> load_row_chunk(const uint8_t *plane, co
   return r;
 }
 
+// The decode walk's sources as buffer resources (scalar registers) over the tile's planes and the input rows, with
+// a 32-bit offset a lane; group g's and unit v's offsets are scalar, so the walk's addresses cost no vector
+// instructions (a load past a resource's range reads zero). pv, hv and mv: the lane's offsets at the slice's first
+// group and unit, as load_row_group (TB 4) or load_row_chunk (TB 1) and load_meta expect their pointers; xv[b]: row
+// block b's lane offset at inputs 8 q of the slice's first group.
+template <uint32_t FMT, int NT, int MB, int TB>
+struct RowBuffers {
+  __amdgpu_buffer_rsrc_t plane[NT], high[NT], meta[NT], input;
+  uint32_t pv, hv, mv, xv[MB];
+  __device__ __forceinline__ u32x4 x(int b, uint32_t g) const { return buffer_b128<0>(input, xv[b], g * 64); }
+  __device__ __forceinline__ MetaWords unit(int n, uint32_t v) const {
+    return buffer_meta<FMT>(meta[n], mv, v * 64 * Fmt<FMT>::META);
+  }
+  __device__ __forceinline__ RowGroup<FMT> codes(int n, uint32_t g) const {
+    using F = Fmt<FMT>;
+    RowGroup<FMT> r;
+    const uint32_t at = g * 64 * F::P0;
+    if constexpr (TB == 1) {
+      if constexpr (F::P0 == 32) {
+        const u32x2 w = buffer_b64(plane[n], pv, at);
+        r.lo[0] = w[0];
+        r.lo[1] = w[1];
+      } else {
+        r.lo[0] = buffer_b32(plane[n], pv, at);
+      }
+      if constexpr (F::P1) r.high[0] = buffer_b32(high[n], hv, g * 64 * F::P1);
+    } else {
+      r.lo = buffer_b128(plane[n], pv, at);
+      if constexpr (F::P0 == 32) r.hi = buffer_b128(plane[n], pv, at + 16);
+      if constexpr (F::P1 == 4) r.high[0] = buffer_b32(high[n], hv, g * 64 * 4);
+      if constexpr (F::P1 == 8) r.high = buffer_b64(high[n], hv, g * 64 * 8);
+    }
+    return r;
+  }
+};
+
 // The lane's shift of its chunk's plane1 bits after the transpose (lane (j, q) holds chunk q): Q5_K byte q, Q6_K
 // halfword q % 2 of the word the transpose brings.
 template <uint32_t FMT>
@@ -236,18 +272,17 @@ __device__ __forceinline__ void row_group_close(const CloseCoef (&k)[NT][TB], co
 }
 
 // Adds GW groups (the first `live` of them) of NT tensors' plane tiles to acc[n][t][b][i] (tensor n, column
-// block t, row block b, row 4q + i of the block). plane[n] and high[n] point at the slice's first group for the
-// lane's column (load_row_group), meta[n] at its first meta unit for the lane's own column l (+ META l: one load per
-// unit and tensor, whose coefficients spread_coefs hands to the lanes whose MFMA blocks hold the column); xrow[b] at
-// the lane's row 16 b + j, inputs 8q of the slice's first group (one 16-byte load a row block and group: the
-// wave's LDS slot xlds, MB KiB, turns the lanes' contiguous chunks into the MFMA's A layout, inputs 4q..4q+3 and
-// 16+4q..19+4q of the row, with a write and two reads instead of a second global load). TB 1: one column block, the
-// lane's column j of it, its chunk q and meta loaded directly (load_row_chunk); the same operands, MFMAs and closes
-// as that block's in the four-block walk.
+// block t, row block b, row 4q + i of the block), loading through src (RowBuffers): the slice's groups for the lane's
+// column (load_row_group's words), the meta units of the lane's own column l (one load per unit and tensor, whose
+// coefficients spread_coefs hands to the lanes whose MFMA blocks hold the column), and for each row block the lane's
+// row 16 b + j, inputs 8q of each group (one 16-byte load a row block and group: the wave's LDS slot xlds, MB KiB,
+// turns the lanes' contiguous chunks into the MFMA's A layout, inputs 4q..4q+3 and 16+4q..19+4q of the row, with a
+// write and two reads instead of a second global load). TB 1: one column block, the lane's column j of it, its chunk
+// q and meta loaded directly (load_row_chunk's words); the same operands, MFMAs and closes as that block's in the
+// four-block walk.
 template <uint32_t FMT, int MB, int GW, int NT, int TB = 4>
-__device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], const uint8_t *const (&high)[NT],
-                                          const uint8_t *const (&meta)[NT], const uint16_t *const (&xrow)[MB],
-                                          uint8_t *xlds, uint32_t live, float (&acc)[NT][TB][MB][4]) {
+__device__ __forceinline__ void row_slice(const RowBuffers<FMT, NT, MB, TB> &src, uint8_t *xlds, uint32_t live,
+                                          float (&acc)[NT][TB][MB][4]) {
   using F = Fmt<FMT>;
   // 8-bit codes (twice the bytes a group) keep fewer groups in flight, and so do the K-quants with plane1 bits in the
   // longest slices of one tensor's 16 rows (whose workgroups hold the most waves, 128 registers each), and Q6_K (two
@@ -256,7 +291,8 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
   constexpr int kDepth = F::P0 == 32 || kTight ? kRowPipe / 2 : kRowPipe;
   constexpr int SG = F::SG, UNIT = F::UNIT, P = GW < kDepth ? GW : kDepth;
   static_assert(GW % UNIT == 0 && GW % SG == 0, "a slice holds whole meta units");
-  const uint32_t last = live ? live - 1 : 0;
+  // The slice's last group, wave-uniform: groups past it repeat it, with scalar offsets.
+  const uint32_t last = __builtin_amdgcn_readfirstlane(live ? live - 1 : 0);
   const CodeConstants cc = make_code_constants();
   const uint32_t hshift = row_high_shift<FMT>(threadIdx.x & 63);
 
@@ -266,15 +302,14 @@ __device__ __forceinline__ void row_slice(const uint8_t *const (&plane)[NT], con
   const auto issue = [&](int u) __attribute__((always_inline)) {
     const uint32_t g = min((uint32_t)u, last);
 #pragma unroll
-    for (int b = 0; b < MB; ++b) xv[b][u] = *(const u32x4 *)(xrow[b] + (size_t)g * 32);
+    for (int b = 0; b < MB; ++b) xv[b][u] = src.x(b, g);
     if (u % UNIT == 0) {
       const uint32_t v = min((uint32_t)(u / UNIT), last / UNIT);
 #pragma unroll
-      for (int n = 0; n < NT; ++n) own[n][u / UNIT] = load_meta<FMT>(meta[n] + (size_t)v * 64 * F::META);
+      for (int n = 0; n < NT; ++n) own[n][u / UNIT] = src.unit(n, v);
     }
 #pragma unroll
-    for (int n = 0; n < NT; ++n)
-      codes[n][u] = TB == 1 ? load_row_chunk<FMT>(plane[n], high[n], g) : load_row_group<FMT>(plane[n], high[n], g);
+    for (int n = 0; n < NT; ++n) codes[n][u] = src.codes(n, g);
   };
 #pragma unroll
   for (int u = 0; u < P; ++u) issue(u);
