@@ -238,9 +238,18 @@ DecodeLayout decode_layout(uint32_t fmt, uint32_t blocks, uint32_t K, uint32_t s
   const uint32_t units = K / 32 / sg;
   if (units % splits || !(units / splits)) return {0, 0};
   // The shortest slices (8, 16 or 32 groups; a gate/up pair streams two tensors, at most 16) whose waves fit one
-  // workgroup of the tile the rows run.
+  // workgroup of the tile the rows run. A row tile of one tensor in 16-byte codes whose 64-column workgroups
+  // outnumber the compute units takes 32-group slices instead: half the waves a workgroup, so more workgroups share
+  // a compute unit and the grid runs in fewer rounds. Measured (graph-replayed, one box, order alternated; M = 8 /
+  // 16): K 5120 x N 27648 Q4_K 23.96 / 28.02 -> 22.85 / 26.36 us, af4g64 22.21 / 25.42 -> 21.03 / 24.63, Q6_K (M =
+  // 16) 40.99 -> 38.86, N 17408 af4g64 20.12 / 23.32 -> 18.90 / 22.84; 8-bit codes lost (Q8_0 at M = 16 44.39 ->
+  // 45.97), so they keep the shortest slices.
   const uint32_t gs = units / splits * sg;
   const uint32_t most = rows <= kColumnTileRows ? kColumnMaxWaves : row_max_waves(rows <= 16 ? 1 : 2, pair ? 2 : 1);
+  const uint32_t tiles = blocks / 4;
+  if (rows > kColumnTileRows && !pair && sq_format(fmt).plane0_bytes == 16 && tiles * splits > kDecodeUnits &&
+      (gs + kColumnMaxGroups - 1) / kColumnMaxGroups <= most)
+    return {(gs + kColumnMaxGroups - 1) / kColumnMaxGroups, kColumnMaxGroups};
   for (uint32_t ks = 8; ks <= (pair ? kColumnMaxGroups / 2 : kColumnMaxGroups); ks *= 2)
     if ((gs + ks - 1) / ks <= most) return {(gs + ks - 1) / ks, ks};
   return {0, 0};

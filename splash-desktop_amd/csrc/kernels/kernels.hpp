@@ -41,6 +41,8 @@ SQ_HD inline bool row_tile_format(uint32_t f) { return sq_format_supported(f); }
 SQ_HD inline bool prefill_tile_format(uint32_t f) { return sq_format_supported(f); }
 // The column tile's most waves (K slices) per workgroup, and the most groups of 32 inputs one wave streams.
 constexpr uint32_t kColumnMaxWaves = 16, kColumnMaxGroups = 32;
+// An MI355X's compute units, past which a row tile's 64-column workgroups take the longest slices (decode_layout).
+constexpr uint32_t kDecodeUnits = 256;
 struct DecodeArgs {
   const uint16_t *input;   // bf16 [rows][K]
   Segment seg[3];

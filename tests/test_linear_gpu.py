@@ -247,8 +247,14 @@ def widened(w, extra):
 
 # The column tile runs 16-column workgroups (each wave four K slices) while four for each of a dispatch's 64-column
 # tiles times its splits fit one a compute unit (256 for the default device), the row tile (one MFMA column block a
-# wave) while they fit a few a compute unit, 64-column ones past that: zero columns past a projection's own (more
-# than 256 tiles times splits) widen its dispatch to 64-column workgroups.
+# wave) while they fit a few a compute unit, 64-column ones past that: zero columns past a projection's own widen
+# its dispatch to 64-column workgroups. The widened dispatch holds exactly 256 tiles times splits: past that the
+# row tile takes its longest slices (another summation order).
+def device_fill(n, splits=1):
+    """The zero columns that widen an n-column dispatch of `splits` K splits to 256 tiles times splits."""
+    return 64 * (256 // splits) - n
+
+
 NARROW = [(oracle.FMT_AF4G64, 1, 1, 2048), (oracle.FMT_AF4G64, 4, 2, 4096), (oracle.FMT_AF4G64, 1, 1, 14336),
           (oracle.FMT_Q4K, 1, 4, 4096), (oracle.FMT_Q4K, 3, 1, 2048), (oracle.FMT_Q4K, 1, 1, 8192),
           (oracle.FMT_Q5K, 2, 1, 2048), (oracle.FMT_Q6K, 1, 2, 4096), (oracle.FMT_Q6K, 4, 1, 2048),
@@ -272,7 +278,7 @@ def test_column_slices_equal_whole_tile_workgroups(fmt, rows, splits, k):
     w = make_weights(rng, fmt, n, k)
     x = dense_inputs(rng, rows, k)
     narrow = run_plan(staged(n, k, rows, splits), sq.projection(w.segment()), x, n)
-    seg, keep = widened(w, 64 * (256 // splits))
+    seg, keep = widened(w, device_fill(n, splits))
     total = seg.output_size
     wide = run_plan(staged(total, k, rows, splits), sq.projection(seg), x, total)
     assert np.array_equal(wide[:, :n], narrow)
@@ -306,7 +312,7 @@ def test_column_slices_random_shapes(fmt, n, k, rows, splits):
     w = make_weights(rng, fmt, n, k)
     x = dense_inputs(rng, rows, k)
     narrow = run_plan(staged(n, k, rows, splits), sq.projection(w.segment()), x, n)
-    seg, keep = widened(w, 64 * (256 // splits))
+    seg, keep = widened(w, device_fill(n, splits))
     wide = run_plan(staged(seg.output_size, k, rows, splits), sq.projection(seg), x, seg.output_size)
     assert np.array_equal(wide[:, :n], narrow)
     check_decode(narrow, x, w, f"random shape fmt {fmt} {n}x{k} rows {rows} splits {splits}")
@@ -324,7 +330,7 @@ def test_column_slices_gate_up_pairs(fmt, rows, splits):
     x = dense_inputs(rng, rows, k)
     narrow = run_plan(staged(n, k, rows, splits, sq.EPILOGUE_GATE_UP, one_pass=1), sq.projection(wu.segment()), x,
                       n, gate=sq.projection(wg.segment()))
-    (g, keep_g), (u, keep_u) = widened(wg, 64 * (256 // splits)), widened(wu, 64 * (256 // splits))
+    (g, keep_g), (u, keep_u) = widened(wg, device_fill(n, splits)), widened(wu, device_fill(n, splits))
     total = g.output_size
     wide = run_plan(staged(total, k, rows, splits, sq.EPILOGUE_GATE_UP, one_pass=1), sq.projection(u), x, total,
                     gate=sq.projection(g))
@@ -340,7 +346,7 @@ def test_column_slices_mixed_formats(rows):
     c = make_weights(rng, oracle.FMT_AF4G64, 64, k)
     x = dense_inputs(rng, rows, k)
     narrow = run_plan(staged(256, k, rows, 1), sq.projection([a.segment(), b.segment(128), c.segment(192)]), x, 256)
-    wide_c, keep = widened(c, 64 * 256)
+    wide_c, keep = widened(c, device_fill(256))
     total = 192 + wide_c.output_size
     wide_c.column_offset = 192
     wide = run_plan(staged(total, k, rows, 1), sq.projection([a.segment(), b.segment(128), wide_c]), x, total)
@@ -394,7 +400,7 @@ def test_row_tile_unsplit_plans(n, rows):
     assert plan.config.splits == 1
     got = run_plan(plan, proj, x, n)
     check_decode(got, x, w, f"unsplit row tile {n}x{k} rows {rows}")
-    seg, keep = widened(w, 64 * 256)
+    seg, keep = widened(w, device_fill(n))
     wide = run_plan(staged(seg.output_size, k, rows, 1), sq.projection(seg), x, seg.output_size)
     assert np.array_equal(wide[:, :n], got)
 
@@ -411,6 +417,28 @@ def test_config3_q4k_decode(rows):
     plan = sq.plan_for(sq.decode_workload(n, k, rows), proj)
     got = run_plan(plan, proj, x, n)
     stats = check_decode(got, x, w, f"Q4_K {n}x{k} rows {rows}")
+    value, *_ = oracle.project_f64(x, w.values)
+    ref = synthetic.bf16_to_f32(staged_reference(x, w))
+    ref_l2 = np.linalg.norm(ref - value) / np.linalg.norm(value)
+    assert stats["rel_l2"] <= ref_l2 * 1.10 + 1e-6
+
+
+@pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_AF4G32, oracle.FMT_AF4G128, oracle.FMT_Q4K,
+                                 oracle.FMT_Q5K, oracle.FMT_Q6K, oracle.FMT_Q80])
+@pytest.mark.parametrize("rows", [8, 16])
+def test_row_tile_long_slices(fmt, rows):
+    """A row tile of more 64-column workgroups than compute units (257 tiles, K 2048) takes 32-group slices in the
+    16-byte-code formats (8-bit codes keep the shortest): every output against fp64 with the register tile's bound,
+    and no worse than the reference's staged numerics."""
+    n, k = 64 * 257, 2048
+    w = shape_weights(fmt, n, k, 11 + fmt)
+    rng = np.random.default_rng(400 + rows + fmt)
+    x = dense_inputs(rng, rows, k)
+    proj = sq.projection(w.segment())
+    plan = sq.plan_for(sq.decode_workload(n, k, rows), proj)
+    assert plan.config.splits == 1
+    got = run_plan(plan, proj, x, n)
+    stats = check_decode(got, x, w, f"fmt {fmt} {n}x{k} rows {rows}")
     value, *_ = oracle.project_f64(x, w.values)
     ref = synthetic.bf16_to_f32(staged_reference(x, w))
     ref_l2 = np.linalg.norm(ref - value) / np.linalg.norm(value)
