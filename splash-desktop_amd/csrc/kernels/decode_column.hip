@@ -382,8 +382,10 @@ hipError_t launch_mr(const DecodeArgs &a, uint32_t tiles, DecodeLayout layout, h
 
 template <uint32_t FMT, int NT, uint32_t EP, bool F32OUT>
 hipError_t launch_rows(const DecodeArgs &a, uint32_t tiles, DecodeLayout layout, hipStream_t stream) {
-  return a.rows <= 1 ? launch_mr<FMT, 1, NT, EP, F32OUT>(a, tiles, layout, stream)
-                     : launch_mr<FMT, 4, NT, EP, F32OUT>(a, tiles, layout, stream);
+  // One, two or four rows' closes and input sums (a row computes the same in each instance).
+  return a.rows <= 1   ? launch_mr<FMT, 1, NT, EP, F32OUT>(a, tiles, layout, stream)
+         : a.rows == 2 ? launch_mr<FMT, 2, NT, EP, F32OUT>(a, tiles, layout, stream)
+                       : launch_mr<FMT, 4, NT, EP, F32OUT>(a, tiles, layout, stream);
 }
 
 template <uint32_t FMT>

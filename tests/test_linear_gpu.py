@@ -79,9 +79,9 @@ def test_decode_sparse_inputs(fmt, splits):
 @pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_Q4K])
 @pytest.mark.parametrize("splits", [1, 8])
 def test_rows_are_independent(fmt, splits):
-    """A row's output is bitwise the same in any batch of its tile kind: alone (the one-row instance) or among four
-    rows on the column tile, among 16 or 32 rows on the row tile; across the kinds both are inside the oracle's
-    interval (check_projection)."""
+    """A row's output is bitwise the same in any batch of its tile kind: alone (the one-row instance), in a pair (the
+    two-row instance) or among four rows on the column tile, among 16 or 32 rows on the row tile; across the kinds
+    both are inside the oracle's interval (check_projection)."""
     rng = np.random.default_rng(31 + splits)
     n, k = 128, 2048   # K partitions take whole meta units: Q4_K's 256-input super-blocks
     w = make_weights(rng, fmt, n, k)
@@ -94,6 +94,9 @@ def test_rows_are_independent(fmt, splits):
     for r in range(4):
         alone = run_plan(staged(n, k, 1, splits), proj, x[r:r + 1], n)
         assert np.array_equal(alone[0], four[r]), f"row {r}"
+    for r in (0, 2):
+        two = run_plan(staged(n, k, 2, splits), proj, x[r:r + 2], n)
+        assert np.array_equal(two, four[r:r + 2]), f"rows {r}, {r + 1}"
     check_decode(four, x[:4], w, "column tile")
     check_decode(all32, x, w, "row tile")
 
