@@ -42,7 +42,7 @@ constexpr int kLdsLimit = 160 * 1024;              // LDS a workgroup may hold
 // wave's dependency and LDS stalls are covered by the other's work.
 // Formats whose codes are 16 bytes a column-group and who have no plane1 (4-bit affine and Q4_K) run W = 8.
 template <uint32_t FMT>
-constexpr int tile_waves() { return Fmt<FMT>::P0 == 16 && Fmt<FMT>::P1 == 0 ? 8 : 4; }
+constexpr int tile_waves() { return Fmt<FMT>::P0 == 16 && Fmt<FMT>::P1 <= 4 ? 8 : 4; }
 // A wave's LDS slot for one step: the step's two groups of the wave's codes (its 256 / W columns x P0 bytes each),
 // their plane1 bits (P1 each), then the meta the step reads for the whole plane tile (its meta unit, or both groups'
 // units of a format with a unit a group). Each part lies in the planes as in the slot, so it arrives by whole 16-byte
@@ -325,7 +325,7 @@ void prefill_kernel(PrefillArgs a) {
   static_assert(!(SPLIT && STREAM), "a stream piece runs its own epilogue");
   using F = Fmt<FMT>;
   using S = StepSlot<FMT, W>;
-  static_assert(W == 4 || (W == 8 && F::P0 == 16 && F::P1 == 0), "eight waves take 16-byte codes and no plane1");
+  static_assert(W == 4 || (W == 8 && F::P0 == 16 && F::P1 <= 4), "eight waves take 16-byte codes, plane1 of 4 bytes");
   constexpr int MI = BM / 16;                         // 16-row blocks of the wave
   constexpr int NT = 16 / W;                          // 16-column blocks of the wave: 4 (a plane tile) or 2 (a half)
   static_assert(MI == 8 || MI == 16, "128- or 256-row tiles");
@@ -333,6 +333,7 @@ void prefill_kernel(PrefillArgs a) {
   constexpr int kSlots = step_slots<FMT, BM, W>();
   // The step's plane copies: the codes, plane1 and meta parts by 16-byte copies of 1 KiB and dword copies of 256 B.
   constexpr int kCode16 = S::code / 1024, kHigh16 = S::high / 1024, kHigh4 = S::high % 1024 / 256;
+  constexpr int kHighGroups = F::P1 ? 256 / (32 * (F::P1 ? F::P1 : 1)) : 1;   // eight waves: groups a dword copy
   constexpr int kMeta16 = S::meta / 1024, kMeta4 = S::meta % 1024 / 256;
   static_assert(S::code % 1024 == 0 && S::high % 256 == 0 && S::meta % 256 == 0, "whole copies");
   constexpr int kBCopies = kCode16 + kHigh16 + kHigh4 + kMeta16 + kMeta4;
@@ -414,8 +415,14 @@ void prefill_kernel(PrefillArgs a) {
     const uint8_t *bplane = seg.plane0 + (tile * G * 64 * F::P0 + (size_t)first * S::plane_step + code_lane);
     const uint8_t *bhigh16 =
         F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + (size_t)first * S::plane_high_step + 16 * lane) : nullptr;
+    // Eight waves copy their half's plane1 bytes only (32 P1 a group), the step's groups packed one after the other
+    // in the slot: a dword copy holds kHighGroups groups, lane l byte 4 (l % (64 / kHighGroups)) of group
+    // l / (64 / kHighGroups)'s half.
+    const uint32_t high_lane = W == 8 ? lane / (64 / kHighGroups) * 64 * F::P1 + 32 * half * F::P1 +
+                                            lane % (64 / kHighGroups) * 4
+                                      : 4 * lane;
     const uint8_t *bhigh4 =
-        F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + (size_t)first * S::plane_high_step + 4 * lane) : nullptr;
+        F::P1 ? seg.plane1 + (tile * G * 64 * F::P1 + (size_t)first * S::plane_high_step + high_lane) : nullptr;
     const uint8_t *bmeta16 =
         seg.meta + ((tile * units + unit0) * 64 * F::META + 16 * (F::META == 16 ? code_slot(lane) : lane));
     const uint8_t *bmeta4 = seg.meta + ((tile * units + unit0) * 64 * F::META + 4 * lane);
@@ -453,7 +460,8 @@ void prefill_kernel(PrefillArgs a) {
         copy_to_lds<16>(bhigh16 + (size_t)from * S::plane_high_step + 1024 * i, dst + S::high_at + 1024 * i);
       } else if (k < kCode16 + kHigh16 + kHigh4) {
         const int i = k - kCode16 - kHigh16;
-        copy_to_lds<4>(bhigh4 + (size_t)from * S::plane_high_step + 1024 * kHigh16 + 256 * i,
+        copy_to_lds<4>(bhigh4 + (size_t)from * S::plane_high_step + 1024 * kHigh16 +
+                           (W == 8 ? kHighGroups * 64 * F::P1 : 256) * i,
                        dst + S::high_at + 1024 * kHigh16 + 256 * i);
       } else if (k < kCode16 + kHigh16 + kHigh4 + kMeta16) {
         const int i = k - kCode16 - kHigh16 - kHigh4;
@@ -507,8 +515,8 @@ void prefill_kernel(PrefillArgs a) {
         } else {
           cw[h][t] = *(const uint32_t *)(src + h * (S::code / 2) + code_slot(c) * 16 + q * 4);
         }
-        if constexpr (F::P1 == 4) hb[h][t] = src[S::high_at + h * 256 + c * 4 + q];
-        if constexpr (F::P1 == 8) hb[h][t] = *(const uint16_t *)(src + S::high_at + h * 512 + c * 8 + 2 * q);
+        if constexpr (F::P1 == 4) hb[h][t] = src[S::high_at + h * S::cols * 4 + c * 4 + q];
+        if constexpr (F::P1 == 8) hb[h][t] = *(const uint16_t *)(src + S::high_at + h * S::cols * 8 + c * 8 + 2 * q);
         mw[h][t] = slot_meta<FMT>(src + S::meta_at, S::cols * half + c, h);
       }
     };
@@ -886,10 +894,11 @@ hipError_t launch_format(uint32_t epilogue, const PrefillArgs &args, hipStream_t
   a.column_group0 = 0;
   if (!sc.split) {
     if (sc.bm == 128) return launch_tile<FMT, 128, 0>(epilogue, a, dim3(sc.row_blocks, sc.column_groups), stream);
-    // Stream pieces run in the eight-wave tile only: the four-wave tile's 256 sums a lane leave no registers for the
-    // piece loop (its stream instance spills). Their epilogue addresses the output with 32-bit byte offsets, rows
-    // past the chunk included (up to the last row block's end), which must not wrap.
-    if constexpr (tile_waves<FMT>() == 8) {
+    // Stream pieces run in the eight-wave tile of formats without plane1 only: the four-wave tile's 256 sums a lane
+    // leave no registers for the piece loop (its stream instance spills), and so do Q5_K's plane1 bits in the
+    // eight-wave one. Their epilogue addresses the output with 32-bit byte offsets, rows past the chunk included (up
+    // to the last row block's end), which must not wrap.
+    if constexpr (tile_waves<FMT>() == 8 && Fmt<FMT>::P1 == 0) {
       const PrefillStream st = prefill_stream(sc.row_blocks, sc.column_groups, args.K);
       if (st.stream_tiles && (uint64_t)sc.row_blocks * 256 * args.out_stride * 2 < (1ull << 31)) {
         if (!a.partials || !a.counters) return hipErrorInvalidValue;
