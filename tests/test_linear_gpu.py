@@ -428,14 +428,15 @@ def test_config3_q4k_decode(rows):
 
 @pytest.mark.parametrize("fmt", [oracle.FMT_AF4G64, oracle.FMT_AF4G32, oracle.FMT_AF4G128, oracle.FMT_Q4K,
                                  oracle.FMT_Q5K, oracle.FMT_Q6K, oracle.FMT_Q80])
-@pytest.mark.parametrize("rows", [8, 16])
-def test_row_tile_long_slices(fmt, rows):
-    """A row tile of more 64-column workgroups than compute units (257 tiles, K 2048) takes 32-group slices in the
-    16-byte-code formats (8-bit codes keep the shortest): every output against fp64 with the register tile's bound,
+@pytest.mark.parametrize("rows,k", [(8, 2048), (16, 2048), (12, 2560)])
+def test_row_tile_long_slices(fmt, rows, k):
+    """A row tile of more 64-column workgroups than compute units (257 tiles) takes 32-group slices in the
+    16-byte-code formats (8-bit codes keep the shortest): K 2048 in two whole slices, K 2560 (80 groups) with a last
+    slice of 16, whose loads past it repeat its last group. Every output against fp64 with the register tile's bound,
     and no worse than the reference's staged numerics."""
-    n, k = 64 * 257, 2048
+    n = 64 * 257
     w = shape_weights(fmt, n, k, 11 + fmt)
-    rng = np.random.default_rng(400 + rows + fmt)
+    rng = np.random.default_rng(400 + rows + fmt + k)
     x = dense_inputs(rng, rows, k)
     proj = sq.projection(w.segment())
     plan = sq.plan_for(sq.decode_workload(n, k, rows), proj)
