@@ -388,6 +388,27 @@ def test_config1_sweep_policy_plans(n, k, rows):
     assert stats["rel_l2"] <= ref_l2 * 1.10 + 1e-6
 
 
+@pytest.mark.parametrize("n,k,want", [(512, 4096, 4), (1024, 4096, 4), (2048, 5120, 2), (1024, 2048, 1)])
+@pytest.mark.parametrize("rows", [8, 16, 32])
+def test_row_tile_split_law_plans(n, k, want, rows):
+    """The row tile's split law at few tiles: a split doubled while its 16-column workgroups fit the device (N 512
+    and 1024 at K 4096: four splits), four splits in 64-column workgroups narrowed to two in 16-column ones (2048 x
+    5120), an unsplit tile kept unsplit (1024 x 2048). Each plan's outputs against fp64 with the register tile's
+    bound, and no worse than the reference's staged numerics."""
+    w = shape_weights(oracle.FMT_AF4G64, n, k, 17 + n + k)
+    rng = np.random.default_rng(500 + rows + n)
+    x = dense_inputs(rng, rows, k)
+    proj = sq.projection(w.segment())
+    plan = sq.plan_for(sq.decode_workload(n, k, rows), proj)
+    assert plan.config.splits == want
+    got = run_plan(plan, proj, x, n)
+    stats = check_decode(got, x, w, f"{n}x{k} rows {rows} splits {want}")
+    value, *_ = oracle.project_f64(x, w.values)
+    ref = synthetic.bf16_to_f32(synthetic.bf16_bits(oracle.project_staged_f32(x, w.halves)))
+    ref_l2 = np.linalg.norm(ref - value) / np.linalg.norm(value)
+    assert stats["rel_l2"] <= ref_l2 * 1.10 + 1e-6
+
+
 @pytest.mark.parametrize("n", [3072, 4096])
 @pytest.mark.parametrize("rows", [5, 16])
 def test_row_tile_unsplit_plans(n, rows):
