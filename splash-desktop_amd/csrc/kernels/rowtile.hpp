@@ -285,10 +285,12 @@ __device__ __forceinline__ void row_slice(const RowBuffers<FMT, NT, MB, TB> &src
                                           float (&acc)[NT][TB][MB][4]) {
   using F = Fmt<FMT>;
   // 8-bit codes (twice the bytes a group) keep fewer groups in flight, and so do the K-quants with plane1 bits in the
-  // longest slices of one tensor's 16 rows (whose workgroups hold the most waves, 128 registers each), and Q6_K (two
-  // scales a group) in every slice of 16 rows.
+  // longest slices of one tensor's 16 rows (whose workgroups hold the most waves, 128 registers each), Q6_K (two
+  // scales a group) in every slice of 16 rows, and the 64-column workgroups of 32 rows (measured, graph-replayed, M =
+  // 32, four groups against two: K 4096 x N 14336 / 4096 and K 14336 x N 4096 and K 5120 x N 27648 15.85 / 10.90 /
+  // 18.22 / 39.70 -> 15.18 / 10.54 / 17.12 / 38.38 us; the 16-row and 16-column workgroups measured within noise).
   constexpr bool kTight = F::P1 && MB == 1 && ((NT == 1 && GW == 32) || F::HALVES);
-  constexpr int kDepth = F::P0 == 32 || kTight ? kRowPipe / 2 : kRowPipe;
+  constexpr int kDepth = F::P0 == 32 || kTight || (TB == 4 && MB == 2) ? kRowPipe / 2 : kRowPipe;
   constexpr int SG = F::SG, UNIT = F::UNIT, P = GW < kDepth ? GW : kDepth;
   static_assert(GW % UNIT == 0 && GW % SG == 0, "a slice holds whole meta units");
   // The slice's last group, wave-uniform: groups past it repeat it, with scalar offsets.
